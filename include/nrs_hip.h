@@ -1,0 +1,166 @@
+/*
+ * nrs_hip.h -- C ABI of the MI355X (gfx950) backend for NeuralRs's f32
+ * matrix-multiply family.
+ *
+ * This is the drop-in boundary: the entry points are the kernel-level seams
+ * that the reference's resident GPU ops call today through cudarc, so a `hip`
+ * cargo feature beside `cuda` (Cargo.toml:23-26) can bind them with
+ * `extern "C"` declarations and keep the operator API (`runtime::to_cuda`,
+ * `graph::matmul`, `graph::bmm`, `nn::conv2d`, `nn::Linear`) unchanged.
+ *
+ * Conventions (all entry points):
+ *   - f32 only, row-major matrices, NCHW images, sizes as int64_t.
+ *   - Device pointers are allocated by the caller (nrs_malloc or any HIP
+ *     allocation on the same device); the library owns only its internal
+ *     scratch (split-K partials, im2col columns), grown lazily and released
+ *     by nrs_shutdown().
+ *   - Every call is asynchronous on the library stream (nrs_set_stream;
+ *     default: the null stream) except the D->H copies and nrs_sync, exactly
+ *     like the reference's single default stream (src/cuda/backend.rs:30-32).
+ *   - Return 0 (NRS_OK) on success, else an NRS_ERR_* code; the message is in
+ *     nrs_last_error(). The reference panics on the same conditions
+ *     (e.g. "cuda matmul: inner dims mismatch", src/cuda/graph/matmul.rs:398);
+ *     the host wrapper turns a non-zero code into that panic/exception.
+ *   - Not thread-safe (the reference's host side is Rc<RefCell>, !Send).
+ */
+#ifndef NRS_HIP_H
+#define NRS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum nrs_status {
+    NRS_OK = 0,
+    NRS_ERR_HIP = 1,   /* a HIP runtime call or kernel launch failed      */
+    NRS_ERR_ARG = 2,   /* bad shape, null pointer or unsupported argument */
+    NRS_ERR_ALLOC = 3, /* device allocation failed                        */
+};
+
+/* GEMM operand layouts: the three kernels of src/cuda/graph/matmul.rs. */
+enum nrs_layout {
+    NRS_NN = 0, /* C[r,c] = sum_t A[r,t] B[t,c]; A [rows,inner], B [inner,cols] (matmul_nn :44-94)  */
+    NRS_NT = 1, /* C[r,c] = sum_t A[r,t] B[c,t]; A [rows,inner], B [cols,inner] (matmul_nt :96-146) */
+    NRS_TN = 2, /* C[r,c] = sum_t A[t,r] B[t,c]; A [inner,rows], B [inner,cols] (matmul_tn :148-198)*/
+};
+
+/* Epilogue flags for nrs_gemm (bit-or). Applied after the product:
+ *   v = acc (+ bias) (relu) ; C = v + beta * C_old                           */
+enum nrs_epilogue {
+    NRS_EPI_NONE = 0,
+    NRS_EPI_BIAS_COL = 1, /* + bias[c]   (Linear bias, src/cuda/graph/add.rs:25-30)   */
+    NRS_EPI_BIAS_ROW = 2, /* + bias[r]   (conv bias, src/cuda/nn/conv.rs:62-76)       */
+    NRS_EPI_RELU = 4,     /* max(v, 0)   (src/cuda/graph/relu.rs:16-28)              */
+};
+
+/* ---------------------------------------------------------------- runtime */
+/* Replaces backend::get() (src/cuda/backend.rs:19-28): select device, init. */
+int nrs_init(int device);
+/* Frees library scratch. */
+int nrs_shutdown(void);
+/* Stream all subsequent calls enqueue on (hipStream_t as void*); NULL = null stream. */
+int nrs_set_stream(void *stream);
+void *nrs_get_stream(void);
+/* Message for the last non-zero status (thread-local, valid until the next call). */
+const char *nrs_last_error(void);
+/* Device buffers: replace stream.alloc_zeros / CudaSlice drop (runtime.rs:39-51). */
+int nrs_malloc(void **ptr, size_t bytes);
+int nrs_free(void *ptr);
+/* clone_htod / clone_dtoh (runtime.rs:39-63). dtoh synchronises the stream. */
+int nrs_memcpy_htod(void *dst, const void *src, size_t bytes);
+int nrs_memcpy_dtoh(void *dst, const void *src, size_t bytes);
+int nrs_memcpy_dtod(void *dst, const void *src, size_t bytes);
+/* memset_zeros (runtime.rs:108-117 zero_grad) -- a fill kernel, graph-capture safe. */
+int nrs_memset_zero(void *ptr, size_t bytes);
+/* runtime::synchronize (runtime.rs:122-124). */
+int nrs_sync(void);
+
+/* ------------------------------------------------------------------ GEMM */
+/* mm(kernel, a, b, rows, cols, inner) (src/cuda/graph/matmul.rs:343-348) with
+ * the layout selecting matmul_nn/nt/tn. Unlike the reference, C is not
+ * freshly allocated: C = epi(A op B) + beta*C, so beta=1 fuses the
+ * accumulate_into() that follows every backward GEMM (runtime.rs:67-83).
+ * bias may be NULL unless a BIAS flag is set. rows/cols/inner may be 0.       */
+int nrs_gemm(int layout, float *C, const float *A, const float *B,
+             int64_t rows, int64_t cols, int64_t inner,
+             float beta, const float *bias, int epilogue);
+
+/* mm_nt_splitk(a, b, rows, cols, inner) (src/cuda/graph/matmul.rs:354-379):
+ * C = A[rows,inner] . B[cols,inner]^T + beta*C for skinny outputs with a huge
+ * inner dimension. The inner dimension is split across workgroups; partial
+ * tiles go to library scratch and are combined in a fixed slice order, so the
+ * result is deterministic (the reference uses float atomicAdd).               */
+int nrs_gemm_nt_splitk(float *C, const float *A, const float *B,
+                       int64_t rows, int64_t cols, int64_t inner, float beta);
+
+/* ------------------------------------------------------------------- bmm */
+/* bmm_forward / bmm_grad_a / bmm_grad_b (src/cuda/graph/bmm.rs:12-56), per
+ * batch item b with the GEMM layouts above and contiguous items:
+ *   NN : C[b] (m x n) = A[b] (m x k) . B[b] (k x n)          -- bmm_forward
+ *   NT : C[b] (m x k) = G[b] (m x n) . B[b] (k x n)^T        -- bmm_grad_a
+ *   TN : C[b] (k x n) = A[b] (m x k)^T . G[b] (m x n)        -- bmm_grad_b
+ * Arguments use GEMM naming: C[b] is rows x cols, reduced over inner.
+ * C = A op B + beta*C (beta=1 fuses accumulate_into, bmm.rs:104,118).         */
+int nrs_bmm(int layout, float *C, const float *A, const float *B,
+            int64_t batch, int64_t rows, int64_t cols, int64_t inner, float beta);
+
+/* ---------------------------------------------------------------- conv2d */
+/* The five primitive launches of src/cuda/nn/conv.rs:161-236, same index
+ * semantics (columns grouped by sample: col = ni*out_h*out_w + p).           */
+int nrs_im2col(float *cols, const float *input, int64_t N, int64_t c_in,
+               int64_t in_h, int64_t in_w, int64_t kh, int64_t kw,
+               int64_t stride, int64_t pad);                         /* :27-58   */
+int nrs_col2out(float *out, const float *mm_out, const float *bias,
+                int64_t N, int64_t c_out, int64_t out_h, int64_t out_w); /* :62-76 */
+int nrs_out2mm(float *mm_grad, const float *grad,
+               int64_t N, int64_t c_out, int64_t out_h, int64_t out_w);  /* :94-108 */
+int nrs_col2im(float *dinput, const float *dcols, int64_t N, int64_t c_in,
+               int64_t in_h, int64_t in_w, int64_t kh, int64_t kw,
+               int64_t stride, int64_t pad, float beta);             /* :113-149 */
+int nrs_conv2d_bias_grad(float *dbias, const float *grad, int64_t N, int64_t c_out,
+                         int64_t out_h, int64_t out_w, float beta);  /* :78-90   */
+
+/* Whole-op entry points for nn::conv2d (src/cuda/nn/conv.rs:244-328):
+ * forward  out[N,c_out,oh,ow] = conv(input, weight) + bias   (im2col + GEMM
+ *          whose epilogue writes NCHW + bias, replacing col2out);
+ * backward accumulates (+=) into dinput (if non-NULL; the reference skips it
+ *          when input.requires_grad is false, :304), dweight and dbias.      */
+int nrs_conv2d_forward(float *out, const float *input, const float *weight,
+                       const float *bias, int64_t N, int64_t c_in, int64_t in_h,
+                       int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
+                       int64_t stride, int64_t pad);
+int nrs_conv2d_backward(float *dinput, float *dweight, float *dbias,
+                        const float *grad, const float *input, const float *weight,
+                        int64_t N, int64_t c_in, int64_t in_h, int64_t in_w,
+                        int64_t c_out, int64_t kh, int64_t kw, int64_t stride,
+                        int64_t pad);
+
+/* ------------------------------------------------------ gradient plumbing */
+/* accumulate (src/cuda/runtime.rs:13-19): acc[i] += src[i].                  */
+int nrs_accumulate(float *acc, const float *src, int64_t n);
+/* vadd / bias_add (src/cuda/graph/add.rs:18-31).                             */
+int nrs_vadd(float *out, const float *a, const float *b, int64_t n);
+int nrs_bias_add(float *out, const float *a, const float *bias, int64_t rows, int64_t cols);
+/* sum_axis0 (src/cuda/reduce.rs:12-21): out[c] = sum_r in[r,c] (+ beta*out). */
+int nrs_sum_axis0(float *out, const float *in, int64_t rows, int64_t cols, float beta);
+
+/* maxpool_forward / maxpool_backward (src/cuda/nn/maxpool.rs:18-52), the glue
+ * between the two convolutions of the CNN workload. Forward records the flat
+ * input index of the first maximum (strict >). Backward adds grad to the
+ * winners: dinput += scatter(grad, argmax); done as a gather over the windows
+ * that cover each input element, so it needs no atomics and is deterministic
+ * (the reference scatters with atomicAdd).                                    */
+int nrs_maxpool_forward(float *out, int32_t *argmax, const float *input, int64_t N,
+                        int64_t C, int64_t in_h, int64_t in_w, int64_t k, int64_t stride);
+int nrs_maxpool_backward(float *dinput, const float *grad, const int32_t *argmax,
+                         int64_t N, int64_t C, int64_t in_h, int64_t in_w, int64_t k,
+                         int64_t stride);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NRS_HIP_H */

@@ -1,0 +1,199 @@
+// Runtime part of the C ABI: device selection, stream, buffers, copies,
+// errors and the library's lazily grown scratch. Replaces the reference's
+// process-global cudarc backend (src/cuda/backend.rs:10-42) and the
+// residency helpers of src/cuda/runtime.rs:39-124.
+#include <cstdarg>
+#include <cstring>
+
+#include "nrs_internal.hpp"
+
+namespace nrs {
+namespace {
+
+constexpr int kSlots = 4;
+
+struct State {
+    bool init = false;
+    int device = 0;
+    hipStream_t stream = nullptr;  // null stream unless the caller sets one
+    float* ws[kSlots] = {};
+    size_t ws_bytes[kSlots] = {};
+};
+
+State g;
+thread_local char g_err[1024] = "";
+
+// Zero fill in 16-byte units where aligned; a kernel rather than
+// hipMemsetAsync so the call stays correct inside a captured HIP graph.
+__global__ void fill_zero_kernel(unsigned char* p, size_t bytes) {
+    size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t nthreads = (size_t)gridDim.x * blockDim.x;
+    size_t head = (16 - ((uintptr_t)p & 15)) & 15;
+    if (head > bytes) head = bytes;
+    for (size_t i = tid; i < head; i += nthreads) p[i] = 0;
+    unsigned char* body = p + head;
+    size_t nvec = (bytes - head) / 16;
+    uint4* v = reinterpret_cast<uint4*>(body);
+    for (size_t i = tid; i < nvec; i += nthreads) v[i] = make_uint4(0, 0, 0, 0);
+    size_t tail0 = head + nvec * 16;
+    for (size_t i = tail0 + tid; i < bytes; i += nthreads) p[i] = 0;
+}
+
+}  // namespace
+
+hipStream_t stream() { return g.stream; }
+
+int num_cus() {
+    static int cus = 0;
+    if (cus == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, g.device) != hipSuccess || v <= 0)
+            v = 256;
+        cus = v;
+    }
+    return cus;
+}
+int device() { return g.device; }
+bool initialized() { return g.init; }
+
+int set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+float* workspace(size_t bytes, int slot) {
+    if (slot < 0 || slot >= kSlots) {
+        set_error(NRS_ERR_ARG, "internal: bad scratch slot %d", slot);
+        return nullptr;
+    }
+    if (bytes <= g.ws_bytes[slot]) return g.ws[slot];
+    if (g.ws[slot]) {
+        // The old buffer may still be read by queued kernels.
+        if (hipStreamSynchronize(g.stream) != hipSuccess) return nullptr;
+        (void)hipFree(g.ws[slot]);
+        g.ws[slot] = nullptr;
+        g.ws_bytes[slot] = 0;
+    }
+    size_t want = bytes + bytes / 4;  // grow with headroom
+    want = (want + 255) & ~(size_t)255;
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+        set_error(NRS_ERR_ALLOC, "scratch allocation of %zu bytes failed: %s", want,
+                  hipGetErrorString(e));
+        return nullptr;
+    }
+    g.ws[slot] = static_cast<float*>(p);
+    g.ws_bytes[slot] = want;
+    return g.ws[slot];
+}
+
+int zero_fill(void* ptr, size_t bytes) {
+    if (bytes == 0) return NRS_OK;
+    size_t units = (bytes + 15) / 16;
+    unsigned blocks = (unsigned)std::min<size_t>((units + 255) / 256, 4096);
+    if (blocks == 0) blocks = 1;
+    fill_zero_kernel<<<blocks, 256, 0, g.stream>>>(static_cast<unsigned char*>(ptr), bytes);
+    NRS_LAUNCH_CHECK("memset_zero");
+    return NRS_OK;
+}
+
+}  // namespace nrs
+
+using nrs::g;
+
+extern "C" {
+
+int nrs_init(int device) {
+    int count = 0;
+    NRS_HIP_CHECK(hipGetDeviceCount(&count));
+    NRS_ARG_CHECK(device >= 0 && device < count, "nrs_init: device %d out of range (count %d)",
+                  device, count);
+    NRS_HIP_CHECK(hipSetDevice(device));
+    g.device = device;
+    g.init = true;
+    return NRS_OK;
+}
+
+int nrs_shutdown(void) {
+    if (!g.init) return NRS_OK;
+    NRS_HIP_CHECK(hipStreamSynchronize(g.stream));
+    for (int s = 0; s < nrs::kSlots; ++s) {
+        if (g.ws[s]) NRS_HIP_CHECK(hipFree(g.ws[s]));
+        g.ws[s] = nullptr;
+        g.ws_bytes[s] = 0;
+    }
+    return NRS_OK;
+}
+
+int nrs_set_stream(void* stream) {
+    g.stream = static_cast<hipStream_t>(stream);
+    return NRS_OK;
+}
+
+void* nrs_get_stream(void) { return static_cast<void*>(g.stream); }
+
+const char* nrs_last_error(void) { return nrs::g_err; }
+
+int nrs_malloc(void** ptr, size_t bytes) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(ptr != nullptr, "nrs_malloc: null out-pointer");
+    *ptr = nullptr;
+    if (bytes == 0) bytes = 4;  // distinct non-null handle for empty tensors
+    hipError_t e = hipMalloc(ptr, bytes);
+    if (e != hipSuccess)
+        return nrs::set_error(NRS_ERR_ALLOC, "nrs_malloc(%zu): %s", bytes, hipGetErrorString(e));
+    return NRS_OK;
+}
+
+int nrs_free(void* ptr) {
+    if (!ptr) return NRS_OK;
+    NRS_HIP_CHECK(hipFree(ptr));
+    return NRS_OK;
+}
+
+int nrs_memcpy_htod(void* dst, const void* src, size_t bytes) {
+    NRS_REQUIRE_INIT();
+    if (bytes == 0) return NRS_OK;
+    NRS_ARG_CHECK(dst && src, "nrs_memcpy_htod: null pointer");
+    NRS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g.stream));
+    // Pageable source: make the copy complete before the caller may reuse it.
+    NRS_HIP_CHECK(hipStreamSynchronize(g.stream));
+    return NRS_OK;
+}
+
+int nrs_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+    NRS_REQUIRE_INIT();
+    if (bytes == 0) return NRS_OK;
+    NRS_ARG_CHECK(dst && src, "nrs_memcpy_dtoh: null pointer");
+    NRS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g.stream));
+    NRS_HIP_CHECK(hipStreamSynchronize(g.stream));
+    return NRS_OK;
+}
+
+int nrs_memcpy_dtod(void* dst, const void* src, size_t bytes) {
+    NRS_REQUIRE_INIT();
+    if (bytes == 0) return NRS_OK;
+    NRS_ARG_CHECK(dst && src, "nrs_memcpy_dtod: null pointer");
+    NRS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g.stream));
+    return NRS_OK;
+}
+
+int nrs_memset_zero(void* ptr, size_t bytes) {
+    NRS_REQUIRE_INIT();
+    if (bytes == 0) return NRS_OK;
+    NRS_ARG_CHECK(ptr != nullptr, "nrs_memset_zero: null pointer");
+    return nrs::zero_fill(ptr, bytes);
+}
+
+int nrs_sync(void) {
+    NRS_REQUIRE_INIT();
+    NRS_HIP_CHECK(hipStreamSynchronize(g.stream));
+    NRS_HIP_CHECK(hipGetLastError());
+    return NRS_OK;
+}
+
+}  // extern "C"

@@ -19,3 +19,13 @@ def orc():
     if not os.path.exists(oracle._LIB_PATH):
         oracle.build()
     return oracle
+
+
+@pytest.fixture(scope="session")
+def hip():
+    """The C ABI, initialised on device 0. GPU tests only."""
+    from neuralrs_amd import _abi
+
+    _abi.load()
+    _abi.init(0)
+    return _abi

@@ -1,0 +1,227 @@
+"""Parity of the conv2d path (primitives and whole-op forward/backward) and
+the gradient-plumbing kernels against the CPU oracle, through the C ABI.
+
+Index work (im2col, col2out, out2mm, col2im, maxpool) must match bit for bit;
+the reductions match exactly on small-integer data and to the reference
+twin-test tolerances (tests/cuda_conv2d_test.rs) on its own inputs.
+"""
+import numpy as np
+import pytest
+
+from kat import close, formula, gemm_tol, int_matrix, kats, rel_err
+
+pytestmark = pytest.mark.gpu
+
+CONV_SHAPES = [  # (n, c_in, c_out, h, w, kh, kw, stride, pad)
+    (2, 3, 4, 8, 8, 3, 3, 1, 1),
+    (2, 3, 5, 7, 7, 3, 3, 1, 1),
+    (1, 2, 3, 9, 6, 3, 2, 2, 1),
+    (3, 1, 2, 5, 5, 2, 2, 1, 0),
+    (2, 2, 2, 7, 9, 3, 3, 3, 2),
+    (4, 16, 32, 12, 12, 3, 3, 1, 1),
+    (1, 1, 1, 3, 3, 3, 3, 1, 0),
+]
+ids = ["x".join(map(str, s)) for s in CONV_SHAPES]
+
+
+def D(hip, x, dtype=np.float32):
+    return hip.DeviceBuffer.from_host(x, dtype)
+
+
+@pytest.mark.parametrize("shape", CONV_SHAPES, ids=ids)
+def test_conv_primitives_bit_exact(hip, orc, shape):
+    n, ci, co, h, w, kh, kw, s, p = shape
+    rng = np.random.default_rng(sum(shape))
+    x = rng.standard_normal(n * ci * h * w).astype(np.float32)
+    oh, ow = orc.conv_out_hw(h, w, kh, kw, s, p)
+    P = oh * ow
+    ch = ci * kh * kw
+
+    cols = hip.DeviceBuffer(ch * n * P)
+    hip.call("nrs_im2col", cols.ptr, D(hip, x), n, ci, h, w, kh, kw, s, p)
+    assert np.array_equal(cols.to_host((ch, n * P)), orc.gpu_im2col(x, n, ci, h, w, kh, kw, s, p))
+
+    mm = rng.standard_normal((co, n * P)).astype(np.float32)
+    bias = rng.standard_normal(co).astype(np.float32)
+    out = hip.DeviceBuffer(n * co * P)
+    hip.call("nrs_col2out", out.ptr, D(hip, mm), D(hip, bias), n, co, oh, ow)
+    assert np.array_equal(out.to_host(), orc.gpu_col2out(mm, bias, n, co, P))
+
+    g = rng.standard_normal(n * co * P).astype(np.float32)
+    gm = hip.DeviceBuffer(co * n * P)
+    hip.call("nrs_out2mm", gm.ptr, D(hip, g), n, co, oh, ow)
+    assert np.array_equal(gm.to_host((co, n * P)), orc.gpu_out2mm(g, n, co, P))
+
+    dcols = rng.standard_normal((ch, n * P)).astype(np.float32)
+    di = hip.DeviceBuffer(n * ci * h * w)
+    hip.call("nrs_col2im", di.ptr, D(hip, dcols), n, ci, h, w, kh, kw, s, p, 0.0)
+    assert np.array_equal(di.to_host(), orc.gpu_col2im(dcols, n, ci, h, w, kh, kw, s, p))
+    # beta = 1 accumulates: dinput_old + col2im
+    d0 = rng.standard_normal(n * ci * h * w).astype(np.float32)
+    di2 = D(hip, d0)
+    hip.call("nrs_col2im", di2.ptr, D(hip, dcols), n, ci, h, w, kh, kw, s, p, 1.0)
+    assert np.array_equal(di2.to_host(), orc.gpu_col2im(dcols, n, ci, h, w, kh, kw, s, p) + d0)
+
+    gi = int_matrix(rng, (n * co * P,))
+    db = hip.DeviceBuffer(co)
+    hip.call("nrs_conv2d_bias_grad", db.ptr, D(hip, gi), n, co, oh, ow, 0.0)
+    assert np.array_equal(db.to_host(), orc.gpu_bias_grad(gi, n, co, P))
+
+
+@pytest.mark.parametrize("shape", CONV_SHAPES, ids=ids)
+def test_conv2d_whole_op_exact_integers(hip, orc, shape):
+    n, ci, co, h, w, kh, kw, s, p = shape
+    rng = np.random.default_rng(1000 + sum(shape))
+    x = int_matrix(rng, (n * ci * h * w,), -3, 3)
+    wt = int_matrix(rng, (co * ci * kh * kw,), -3, 3)
+    b = int_matrix(rng, (co,), -3, 3)
+    oh, ow = orc.conv_out_hw(h, w, kh, kw, s, p)
+    ref, _, _ = orc.conv2d_forward(x, wt, b, n, ci, co, h, w, kh, kw, s, p)
+    out = hip.DeviceBuffer(n * co * oh * ow)
+    dx, dw, db = D(hip, x), D(hip, wt), D(hip, b)
+    hip.call("nrs_conv2d_forward", out.ptr, dx.ptr, dw.ptr, db.ptr, n, ci, h, w, co, kh, kw, s, p)
+    assert np.array_equal(out.to_host(), ref)
+
+    g = int_matrix(rng, (n * co * oh * ow,), -3, 3)
+    di_ref, dw_ref, db_ref = orc.conv2d_backward(x, wt, g, n, ci, co, h, w, kh, kw, s, p)
+    gi0 = int_matrix(rng, (x.size,))
+    gw0 = int_matrix(rng, (wt.size,))
+    gb0 = int_matrix(rng, (co,))
+    gI, gW, gB = D(hip, gi0), D(hip, gw0), D(hip, gb0)
+    hip.call("nrs_conv2d_backward", gI.ptr, gW.ptr, gB.ptr, D(hip, g), dx.ptr, dw.ptr,
+             n, ci, h, w, co, kh, kw, s, p)
+    assert np.array_equal(gI.to_host(), gi0 + di_ref)
+    assert np.array_equal(gW.to_host(), gw0 + dw_ref)
+    assert np.array_equal(gB.to_host(), gb0 + db_ref)
+
+
+def test_conv2d_forward_twin(hip, orc):
+    """tests/cuda_conv2d_test.rs:15-43: GPU conv2d vs CPU conv2d_im2col, tol 1e-4."""
+    t = kats()["gpu_twin"]["conv2d_forward"]
+    n, ci, h, w, co, kh, kw, s, p = (t[k] for k in ("n", "c_in", "in_h", "in_w", "c_out", "kh", "kw", "stride", "pad"))
+    x = formula(t["input"], n * ci * h * w)
+    wt = formula(t["weight"], co * ci * kh * kw)
+    b = formula(t["bias"], co)
+    cpu, oh, ow = orc.conv2d_im2col(x, wt, b, n, ci, co, h, w, kh, kw, s, p)
+    out = hip.DeviceBuffer(n * co * oh * ow)
+    hip.call("nrs_conv2d_forward", out.ptr, D(hip, x), D(hip, wt), D(hip, b),
+             n, ci, h, w, co, kh, kw, s, p)
+    close(out.to_host(), cpu, t["tol"], "conv")
+
+
+def test_conv2d_backward_twin(hip, orc):
+    """tests/cuda_conv2d_test.rs:46-96: GPU grads vs CPU Conv2d, tol 1e-3."""
+    t = kats()["gpu_twin"]["conv2d_backward"]
+    n, ci, h, w, co, kh, kw, s, p = (t[k] for k in ("n", "c_in", "in_h", "in_w", "c_out", "kh", "kw", "stride", "pad"))
+    x = formula(t["input"], n * ci * h * w)
+    wt = formula(t["weight"], co * ci * kh * kw)
+    b = formula(t["bias"], co)
+    out, oh, ow = orc.conv2d_forward(x, wt, b, n, ci, co, h, w, kh, kw, s, p)
+    seed = formula(t["seed"], out.size)
+    ci_g, cw_g, cb_g = orc.conv2d_backward(x, wt, seed, n, ci, co, h, w, kh, kw, s, p)
+    gI, gW, gB = hip.DeviceBuffer.zeros(x.size), hip.DeviceBuffer.zeros(wt.size), hip.DeviceBuffer.zeros(co)
+    hip.call("nrs_conv2d_backward", gI.ptr, gW.ptr, gB.ptr, D(hip, seed), D(hip, x),
+             D(hip, wt), n, ci, h, w, co, kh, kw, s, p)
+    close(gI.to_host(), ci_g, t["tol"], "input.grad")
+    close(gW.to_host(), cw_g, t["tol"], "weight.grad")
+    close(gB.to_host(), cb_g, t["tol"], "bias.grad")
+
+
+def test_conv2d_backward_without_input_grad(hip, orc):
+    """dinput = NULL skips the input gradient (conv.rs:304, requires_grad = false)."""
+    n, ci, co, h, w, kh, kw, s, p = 2, 1, 4, 6, 6, 3, 3, 1, 1
+    rng = np.random.default_rng(77)
+    x = int_matrix(rng, (n * ci * h * w,), -3, 3)
+    wt = int_matrix(rng, (co * ci * kh * kw,), -3, 3)
+    g = int_matrix(rng, (n * co * h * w,), -3, 3)
+    _, dw_ref, db_ref = orc.conv2d_backward(x, wt, g, n, ci, co, h, w, kh, kw, s, p)
+    gW, gB = hip.DeviceBuffer.zeros(wt.size), hip.DeviceBuffer.zeros(co)
+    hip.call("nrs_conv2d_backward", None, gW.ptr, gB.ptr, D(hip, g), D(hip, x),
+             D(hip, wt), n, ci, h, w, co, kh, kw, s, p)
+    assert np.array_equal(gW.to_host(), dw_ref)
+    assert np.array_equal(gB.to_host(), db_ref)
+
+
+def test_conv2d_cfg3_layers(hip, orc):
+    """cfg3 shapes (batch 128, 1->32 @28x28 and 32->64 @14x14, 3x3 pad 1):
+    GPU forward/backward against the restated CPU Conv2d on the same data."""
+    rng = np.random.default_rng(3)
+    for (n, ci, co, h, w) in ((128, 1, 32, 28, 28), (128, 32, 64, 14, 14)):
+        x = rng.uniform(0, 1, n * ci * h * w).astype(np.float32)
+        wt = (rng.standard_normal(co * ci * 9) * np.sqrt(2.0 / (ci * 9))).astype(np.float32)
+        b = np.zeros(co, np.float32)
+        ref, oh, ow = orc.conv2d_forward(x, wt, b, n, ci, co, h, w, 3, 3, 1, 1)
+        out = hip.DeviceBuffer(ref.size)
+        dx, dw = D(hip, x), D(hip, wt)
+        hip.call("nrs_conv2d_forward", out.ptr, dx.ptr, dw.ptr, D(hip, b),
+                 n, ci, h, w, co, 3, 3, 1, 1)
+        close(out.to_host(), ref, 1e-4, f"cfg3 fwd {ci}->{co}")
+        g = rng.standard_normal(ref.size).astype(np.float32)
+        di, dwr, dbr = orc.conv2d_backward(x, wt, g, n, ci, co, h, w, 3, 3, 1, 1)
+        gI, gW, gB = hip.DeviceBuffer.zeros(x.size), hip.DeviceBuffer.zeros(wt.size), hip.DeviceBuffer.zeros(co)
+        hip.call("nrs_conv2d_backward", gI.ptr, gW.ptr, gB.ptr, D(hip, g), dx.ptr, dw.ptr,
+                 n, ci, h, w, co, 3, 3, 1, 1)
+        close(gI.to_host(), di, 1e-3, "cfg3 dinput")
+        # weight/bias grads sum N*P = 100352 / 25088 terms: f64 ground truth
+        # with the f32-accumulation bar, for the GPU and the CPU restatement.
+        gm = orc.gpu_out2mm(g, n, co, oh * ow).astype(np.float64)
+        cols = orc.gpu_im2col(x, n, ci, h, w, 3, 3, 1, 1).astype(np.float64)
+        dw64 = gm @ cols.T
+        dwab = np.abs(gm) @ np.abs(cols).T
+        db64 = gm.sum(axis=1)
+        dbab = np.abs(gm).sum(axis=1)
+        K = n * oh * ow
+        for got in (gW.to_host().reshape(co, -1), dwr.reshape(co, -1)):
+            assert rel_err(got, dw64, dwab) <= gemm_tol(K)
+        for got in (gB.to_host(), dbr):
+            assert rel_err(got, db64, dbab) <= gemm_tol(K)
+
+
+# ------------------------------------------------------------ plumbing kernels
+def test_accumulate_vadd_bias_add_sum_axis0(hip, orc):
+    rng = np.random.default_rng(21)
+    for n in (1, 3, 1000, 1 << 20, (1 << 20) + 3):
+        a = rng.standard_normal(n).astype(np.float32)
+        b = rng.standard_normal(n).astype(np.float32)
+        da = D(hip, a)
+        hip.call("nrs_accumulate", da.ptr, D(hip, b), n)
+        assert np.array_equal(da.to_host(), a + b)
+        out = hip.DeviceBuffer(n)
+        hip.call("nrs_vadd", out.ptr, D(hip, a), D(hip, b), n)
+        assert np.array_equal(out.to_host(), a + b)
+    for rows, cols in ((16, 10), (4096, 1024), (256, 128), (1, 7), (3000, 3)):
+        a = rng.standard_normal((rows, cols)).astype(np.float32)
+        bias = rng.standard_normal(cols).astype(np.float32)
+        out = hip.DeviceBuffer(rows * cols)
+        hip.call("nrs_bias_add", out.ptr, D(hip, a), D(hip, bias), rows, cols)
+        assert np.array_equal(out.to_host((rows, cols)), orc.graph_add_bias_forward(a, bias))
+        ai = int_matrix(rng, (rows, cols))
+        s = hip.DeviceBuffer(cols)
+        hip.call("nrs_sum_axis0", s.ptr, D(hip, ai), rows, cols, 0.0)
+        assert np.array_equal(s.to_host(), orc.sum_axis0(ai))
+        s0 = int_matrix(rng, (cols,))
+        s2 = D(hip, s0)
+        hip.call("nrs_sum_axis0", s2.ptr, D(hip, a), rows, cols, 1.0)
+        close(s2.to_host(), orc.sum_axis0(a) + s0, 1e-5 * np.sqrt(rows) * 4, "sum_axis0 float")
+
+
+@pytest.mark.parametrize("dims", [(2, 3, 6, 8, 2, 2), (128, 32, 28, 28, 2, 2), (1, 2, 7, 7, 3, 2),
+                                  (2, 1, 5, 5, 2, 1)])
+def test_maxpool_bit_exact(hip, orc, dims):
+    n, c, h, w, k, s = dims
+    rng = np.random.default_rng(sum(dims))
+    x = rng.standard_normal(n * c * h * w).astype(np.float32)
+    tie = np.arange(0, x.size - 1, 7)
+    x[tie] = x[tie + 1]  # plant ties: the first maximum must win
+    out_ref, am_ref = orc.maxpool_forward(x, n, c, h, w, k, s)
+    out = hip.DeviceBuffer(out_ref.size)
+    am = hip.DeviceBuffer(out_ref.size, np.int32)
+    dx = D(hip, x)
+    hip.call("nrs_maxpool_forward", out.ptr, am.ptr, dx.ptr, n, c, h, w, k, s)
+    assert np.array_equal(out.to_host(), out_ref)
+    assert np.array_equal(am.to_host(), am_ref)
+    g = int_matrix(rng, out_ref.shape)
+    d0 = int_matrix(rng, x.shape)
+    di = D(hip, d0)
+    hip.call("nrs_maxpool_backward", di.ptr, D(hip, g), am.ptr, n, c, h, w, k, s)
+    assert np.array_equal(di.to_host(), orc.maxpool_backward(g, am_ref, x.size, d0))

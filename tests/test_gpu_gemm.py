@@ -1,0 +1,227 @@
+"""Parity of the HIP GEMM core (nrs_gemm / nrs_gemm_nt_splitk / nrs_bmm)
+against the CPU oracle, through the C ABI.
+
+Bars:
+  * small-integer inputs: bit-exact (every summation order is exact);
+  * random f32 inputs: max_ij |C - C64| / (|A||B|)_ij <= 1e-5 * sqrt(K)
+    (the north-star tolerance for f32 accumulation), against f64 ground truth;
+  * the reference's twin-test tolerances against the restated CPU autograd ops.
+"""
+import numpy as np
+import pytest
+
+from kat import close, formula, gemm_tol, int_matrix, kats, rel_err
+
+pytestmark = pytest.mark.gpu
+
+NN, NT, TN = 0, 1, 2
+LNAME = {NN: "nn", NT: "nt", TN: "tn"}
+
+
+def operands(layout, rows, cols, inner, make):
+    a = make((rows, inner) if layout != TN else (inner, rows))
+    b = make((inner, cols) if layout != NT else (cols, inner))
+    return a, b
+
+
+def logical(layout, a, b):
+    A = a if layout != TN else a.T
+    B = b if layout != NT else b.T
+    return A.astype(np.float64), B.astype(np.float64)
+
+
+def run_gemm(hip, layout, a, b, rows, cols, inner, beta=0.0, c0=None, bias=None, epi=0):
+    dA = hip.DeviceBuffer.from_host(a)
+    dB = hip.DeviceBuffer.from_host(b)
+    dC = hip.DeviceBuffer.from_host(c0) if c0 is not None else hip.DeviceBuffer(rows * cols)
+    dbias = hip.DeviceBuffer.from_host(bias) if bias is not None else None
+    hip.gemm(layout, dC, dA, dB, rows, cols, inner, beta, dbias, epi)
+    return dC.to_host((rows, cols))
+
+
+SHAPES = [  # (rows, cols, inner)
+    (1, 1, 1), (2, 2, 2), (5, 7, 11), (17, 9, 5), (40, 32, 56), (64, 64, 16), (33, 65, 129),
+    (128, 256, 64), (256, 128, 784), (100, 10, 9), (256, 10, 128), (300, 300, 300),
+    (512, 512, 512), (32, 1024, 512), (1, 513, 257), (1000, 3, 2),
+]
+
+
+@pytest.mark.parametrize("layout", [NN, NT, TN])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_gemm_exact_integers(hip, layout, shape):
+    rows, cols, inner = shape
+    rng = np.random.default_rng(rows * 7919 + cols * 31 + inner)
+    a, b = operands(layout, rows, cols, inner, lambda s: int_matrix(rng, s, -4, 4))
+    A, B = logical(layout, a, b)
+    c = run_gemm(hip, layout, a, b, rows, cols, inner)
+    assert np.array_equal(c, (A @ B).astype(np.float32)), f"{LNAME[layout]} {shape}"
+
+
+@pytest.mark.parametrize("layout", [NN, NT, TN])
+@pytest.mark.parametrize("shape", [(40, 32, 56), (300, 300, 300), (512, 512, 512),
+                                   (256, 128, 784), (1024, 1024, 1024), (32, 2048, 2048)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_gemm_f64_tolerance(hip, orc, layout, shape):
+    rows, cols, inner = shape
+    rng = np.random.default_rng(sum(shape) + layout)
+    a, b = operands(layout, rows, cols, inner,
+                    lambda s: rng.uniform(-1, 1, s).astype(np.float32))
+    c = run_gemm(hip, layout, a, b, rows, cols, inner)
+    c64, ab = orc.gemm_f64(LNAME[layout], a, b, rows, cols, inner)
+    err = rel_err(c, c64, ab)
+    assert err <= gemm_tol(inner), (err, gemm_tol(inner))
+
+
+def test_gemm_cfg1_512_vs_cpu_simd(hip, orc):
+    """cfg1: 512^3, U(-1,1) seed 0; the GPU and the reference's AVX2 path both
+    sit within the f32 tolerance of f64, and within 2x that of each other."""
+    rng = np.random.default_rng(0)
+    a = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    b = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    c = run_gemm(hip, NN, a, b, 512, 512, 512)
+    cpu = orc.matmul_simd(a, b)
+    c64, ab = orc.gemm_f64("nn", a, b, 512, 512, 512)
+    assert rel_err(c, c64, ab) <= gemm_tol(512)
+    assert rel_err(cpu, c64, ab) <= gemm_tol(512)
+    assert rel_err(c, cpu.astype(np.float64), ab) <= 2 * gemm_tol(512)
+
+
+@pytest.mark.parametrize("n", [2048, 4096])
+def test_gemm_large_square_sampled_rows(hip, orc, n):
+    """cfg5 squares: f64 check on a sample of rows (every tile row touched)."""
+    rng = np.random.default_rng(n)
+    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    c = run_gemm(hip, NN, a, b, n, n, n)
+    rows = np.unique(np.concatenate([np.arange(0, n, 61), np.arange(n - 40, n)]))
+    c64, ab = orc.gemm_f64("nn", a, b, n, n, n, rowidx=rows)
+    assert rel_err(c[rows], c64, ab) <= gemm_tol(n)
+
+
+def test_gemm_skinny_cfg5(hip, orc):
+    """cfg5 skinny M=32, N=K=8192 (split-K path), f64 check on all rows."""
+    rng = np.random.default_rng(32)
+    m, n, k = 32, 8192, 8192
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    c = run_gemm(hip, NN, a, b, m, n, k)
+    c64, ab = orc.gemm_f64("nn", a, b, m, n, k)
+    assert rel_err(c, c64, ab) <= gemm_tol(k)
+
+
+def test_gemm_beta_bias_relu_epilogues(hip):
+    rng = np.random.default_rng(9)
+    rows, cols, inner = 70, 50, 33
+    a, b = operands(NN, rows, cols, inner, lambda s: int_matrix(rng, s, -3, 3))
+    A, B = logical(NN, a, b)
+    prod = (A @ B).astype(np.float32)
+    c0 = int_matrix(rng, (rows, cols))
+    bc = int_matrix(rng, (cols,))
+    br = int_matrix(rng, (rows,))
+    # beta = 1 fuses accumulate_into: C = C_old + A.B
+    assert np.array_equal(run_gemm(hip, NN, a, b, rows, cols, inner, 1.0, c0), c0 + prod)
+    # Linear: A.B + bias[col]
+    assert np.array_equal(run_gemm(hip, NN, a, b, rows, cols, inner, 0.0, None, bc, 1),
+                          prod + bc[None, :])
+    # conv-style row bias, then ReLU
+    assert np.array_equal(run_gemm(hip, NN, a, b, rows, cols, inner, 0.0, None, br, 2 | 4),
+                          np.maximum(prod + br[:, None], 0))
+
+
+def test_gemm_empty_and_zero_inner(hip):
+    # K = 0: C = beta*C (here 0), no operand reads.
+    dC = hip.DeviceBuffer.from_host(np.full((3, 4), 7.0, np.float32))
+    hip.gemm(NN, dC, None, None, 3, 4, 0, 0.0)
+    assert np.array_equal(dC.to_host((3, 4)), np.zeros((3, 4), np.float32))
+    hip.gemm(NN, dC, None, None, 0, 4, 5, 0.0)  # empty output: no-op
+
+
+def test_gemm_errors_raise(hip):
+    dC = hip.DeviceBuffer(4)
+    with pytest.raises(hip.NrsError):
+        hip.gemm(7, dC, dC, dC, 2, 2, 1)
+    with pytest.raises(hip.NrsError):
+        hip.gemm(NN, dC, dC, dC, -1, 2, 1)
+    with pytest.raises(hip.NrsError):
+        hip.gemm(NN, dC, dC, dC, 2, 2, 1, 0.0, None, 1)  # bias flag, null bias
+
+
+# ------------------------------------------------------------------ split-K
+@pytest.mark.parametrize("shape", [(32, 9, 100352), (64, 288, 25088), (5, 7, 3000), (3, 2, 1)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_splitk_nt(hip, orc, shape):
+    rows, cols, inner = shape
+    rng = np.random.default_rng(rows + cols + inner)
+    a = rng.standard_normal((rows, inner)).astype(np.float32)
+    b = rng.uniform(-1, 1, (cols, inner)).astype(np.float32)
+    c0 = rng.standard_normal((rows, cols)).astype(np.float32)
+    dA, dB = hip.DeviceBuffer.from_host(a), hip.DeviceBuffer.from_host(b)
+    dC = hip.DeviceBuffer.from_host(c0)
+    hip.gemm_nt_splitk(dC, dA, dB, rows, cols, inner, 1.0)
+    c = dC.to_host((rows, cols))
+    c64, ab = orc.gemm_f64("nt", a, b, rows, cols, inner)
+    assert rel_err(c - c0, c64, ab + np.abs(c0)) <= gemm_tol(inner)
+    # deterministic: the same call gives the same bits
+    dC2 = hip.DeviceBuffer.from_host(c0)
+    hip.gemm_nt_splitk(dC2, dA, dB, rows, cols, inner, 1.0)
+    assert np.array_equal(dC2.to_host((rows, cols)), c)
+
+
+def test_splitk_cfg5_wgrad_shape(hip, orc):
+    """cfg5 split-K wgrad M=64, N=576, K=100352 (NT), f64 on sampled rows."""
+    rng = np.random.default_rng(576)
+    rows, cols, inner = 64, 576, 100352
+    a = rng.uniform(-1, 1, (rows, inner)).astype(np.float32)
+    b = rng.uniform(-1, 1, (cols, inner)).astype(np.float32)
+    dA, dB = hip.DeviceBuffer.from_host(a), hip.DeviceBuffer.from_host(b)
+    dC = hip.DeviceBuffer(rows * cols)
+    hip.gemm_nt_splitk(dC, dA, dB, rows, cols, inner, 0.0)
+    c = dC.to_host((rows, cols))
+    sel = np.arange(0, rows, 9)
+    c64, ab = orc.gemm_f64("nt", a, b, rows, cols, inner, rowidx=sel)
+    assert rel_err(c[sel], c64, ab) <= gemm_tol(inner)
+
+
+# ---------------------------------------------------------------------- bmm
+def test_bmm_twin(hip, orc):
+    """tests/cuda_manip_test.rs:76-104 (batch 2, 3x4 . 4x5), tol 1e-4."""
+    t = kats()["gpu_twin"]["bmm"]
+    bt, m, k, n = t["batch"], t["m"], t["k"], t["n"]
+    a = formula(t["a"], bt * m * k).reshape(bt, m, k)
+    b = formula(t["b"], bt * k * n).reshape(bt, k, n)
+    seed = formula(t["seed"], bt * m * n).reshape(bt, m, n)
+    cf = orc.graph_bmm_forward(a, b)
+    cga, cgb = orc.graph_bmm_backward(a, b, seed)
+    dA, dB, dG = (hip.DeviceBuffer.from_host(x) for x in (a, b, seed))
+    dO = hip.DeviceBuffer(bt * m * n)
+    hip.bmm(NN, dO, dA, dB, bt, m, n, k)
+    gA, gB = hip.DeviceBuffer.zeros(a.size), hip.DeviceBuffer.zeros(b.size)
+    hip.bmm(NT, gA, dG, dB, bt, m, k, n, 1.0)   # grad_a: G . B^T, accumulated
+    hip.bmm(TN, gB, dA, dG, bt, k, n, m, 1.0)   # grad_b: A^T . G, accumulated
+    close(dO.to_host(), cf, t["tol"], "bmm fwd")
+    close(gA.to_host(), cga, t["tol"], "bmm grad_a")
+    close(gB.to_host(), cgb, t["tol"], "bmm grad_b")
+
+
+@pytest.mark.parametrize("shape", [(3, 5, 7, 4), (256, 128, 128, 32), (256, 128, 32, 128),
+                                   (8, 33, 17, 65)], ids=lambda s: "x".join(map(str, s)))
+def test_bmm_exact_integers(hip, shape):
+    """cfg4 per-head shapes folded into one batch (256 = 32 x 8 heads)."""
+    bt, m, n, k = shape
+    rng = np.random.default_rng(sum(shape))
+    a = int_matrix(rng, (bt, m, k), -3, 3)
+    b = int_matrix(rng, (bt, k, n), -3, 3)
+    g = int_matrix(rng, (bt, m, n), -3, 3)
+    ai, bi, gi = (x.astype(np.int64) for x in (a, b, g))
+    dA, dB, dG = (hip.DeviceBuffer.from_host(x) for x in (a, b, g))
+    dO = hip.DeviceBuffer(bt * m * n)
+    hip.bmm(NN, dO, dA, dB, bt, m, n, k)
+    assert np.array_equal(dO.to_host((bt, m, n)), np.matmul(ai, bi).astype(np.float32))
+    gA = hip.DeviceBuffer(bt * m * k)
+    hip.bmm(NT, gA, dG, dB, bt, m, k, n)
+    assert np.array_equal(gA.to_host((bt, m, k)),
+                          np.matmul(gi, bi.transpose(0, 2, 1)).astype(np.float32))
+    gB = hip.DeviceBuffer(bt * k * n)
+    hip.bmm(TN, gB, dA, dG, bt, k, n, m)
+    assert np.array_equal(gB.to_host((bt, k, n)),
+                          np.matmul(ai.transpose(0, 2, 1), gi).astype(np.float32))
