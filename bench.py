@@ -138,16 +138,22 @@ def cpu_baseline_gemm(a, b, target_s=10.0):
     import oracle
     threads = oracle.max_threads()
     n = a.shape[0]
-    rows = 8
-    t0 = time.perf_counter()
-    oracle.matmul_simd_rows(a, b, 0, rows)
-    dt = time.perf_counter() - t0
-    rows = int(min(n, max(rows, rows * target_s / max(dt, 1e-6))))
-    rows = max(threads, (rows // threads) * threads)
-    rows = min(rows, n)
-    t0 = time.perf_counter()
-    oracle.matmul_simd_rows(a, b, 0, rows)
-    dt = time.perf_counter() - t0
+    # Calibrate on growing row counts until one run takes >= 1 s, so thread
+    # start-up does not dominate the estimate, then time ~target_s of work.
+    rows = threads
+    while True:
+        t0 = time.perf_counter()
+        oracle.matmul_simd_rows(a, b, 0, rows)
+        dt = time.perf_counter() - t0
+        if dt >= 1.0 or rows >= n:
+            break
+        rows = min(n, rows * 4)
+    if dt < target_s and rows < n:
+        rows = int(min(n, rows * target_s / max(dt, 1e-6)))
+        rows = min(n, max(threads, (rows // threads) * threads))
+        t0 = time.perf_counter()
+        oracle.matmul_simd_rows(a, b, 0, rows)
+        dt = time.perf_counter() - t0
     flops = 2.0 * rows * b.shape[1] * a.shape[1]
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"rows 0..{rows} of the {n}^3 GEMM via matmul_simd (src/ops/simd.rs:42-77), "
