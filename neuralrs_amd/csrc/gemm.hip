@@ -17,38 +17,41 @@ struct TileShape {
     int bm, bn, bk, threads;
 };
 
-template <int BM, int BN, int BK, int WM_, int WN_, bool AK, bool BKC>
+template <int BM, int BN, int BK, int WM_, int WN_, int PF, bool AK, bool BKC>
 KernelFn pick_vec(bool vec4) {
-    return vec4 ? gemm_kernel<BM, BN, BK, WM_, WN_, AK, BKC, 4, 2>
-                : gemm_kernel<BM, BN, BK, WM_, WN_, AK, BKC, 1, 2>;
+    return vec4 ? gemm_kernel<BM, BN, BK, WM_, WN_, AK, BKC, 4, 2, PF>
+                : gemm_kernel<BM, BN, BK, WM_, WN_, AK, BKC, 1, 2, PF>;
 }
 
-template <int BM, int BN, int BK, int WM_, int WN_>
+template <int BM, int BN, int BK, int WM_, int WN_, int PF>
 KernelFn pick_layout(int layout, bool vec4) {
     switch (layout) {
-        case NRS_NN: return pick_vec<BM, BN, BK, WM_, WN_, true, false>(vec4);
-        case NRS_NT: return pick_vec<BM, BN, BK, WM_, WN_, true, true>(vec4);
-        default: return pick_vec<BM, BN, BK, WM_, WN_, false, false>(vec4);
+        case NRS_NN: return pick_vec<BM, BN, BK, WM_, WN_, PF, true, false>(vec4);
+        case NRS_NT: return pick_vec<BM, BN, BK, WM_, WN_, PF, true, true>(vec4);
+        default: return pick_vec<BM, BN, BK, WM_, WN_, PF, false, false>(vec4);
     }
 }
 
-// Tile configurations, largest first. All run two waves per SIMD (the
-// register budget is capped at 256 per lane, accumulators in VGPRs); the
-// 256x256 tile uses 8 waves (2 x 4, each 128x64) and ~140 KB of LDS.
-enum TileId { T256x256 = 0, T128x128, T64x64, T32x256, T_COUNT };
+// Tile configurations (chosen by a sweep over the workload shapes on MI355X).
+// All run two waves per SIMD (register budget capped at 256 per lane,
+// accumulators in VGPRs):
+//  * 256x256x32, 8 waves of 128x64, ~140 KB LDS, prefetch depth 1: large
+//    GEMMs (83-85% of FP32 MFMA peak at 4096^3 and 8192^3);
+//  * 64x64x32, 4 waves of 32x32, prefetch depth 2: everything mid-sized
+//    (bmm items, conv GEMMs, projections, split-K weight gradients);
+//  * 32x256x32, 4 waves of 32x64: outputs with at most 32 rows.
+enum TileId { T256x256 = 0, T64x64, T32x256, T_COUNT };
 const TileShape kShapes[T_COUNT] = {
     {256, 256, 32, 512},
-    {128, 128, 16, 256},
-    {64, 64, 16, 256},
+    {64, 64, 32, 256},
     {32, 256, 32, 256},
 };
 
 KernelFn kernel_for(int tile, int layout, bool vec4) {
     switch (tile) {
-        case T256x256: return pick_layout<256, 256, 32, 2, 4>(layout, vec4);
-        case T128x128: return pick_layout<128, 128, 16, 2, 2>(layout, vec4);
-        case T64x64: return pick_layout<64, 64, 16, 2, 2>(layout, vec4);
-        default: return pick_layout<32, 256, 32, 1, 4>(layout, vec4);
+        case T256x256: return pick_layout<256, 256, 32, 2, 4, 1>(layout, vec4);
+        case T64x64: return pick_layout<64, 64, 32, 2, 2, 2>(layout, vec4);
+        default: return pick_layout<32, 256, 32, 1, 4, 1>(layout, vec4);
     }
 }
 
@@ -62,33 +65,28 @@ struct Plan {
     int64_t k_per_slice;
 };
 
-// Chooses the tile shape and the number of K slices.
-Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool allow_split, int force_slices) {
+// Chooses the tile shape and the number of K slices. The 256x256 tile is
+// used only with 128-bit loads (its scalar-load variant spills).
+Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool allow_split,
+               int force_slices) {
     const int cus = num_cus();
+    auto tiles_of = [&](int t) {
+        return cdiv(M, kShapes[t].bm) * cdiv(N, kShapes[t].bn) * batch;
+    };
     Plan pl{T64x64, 1, K};
-    // Largest square-ish tile that still yields a full wave of workgroups.
-    const int order[3] = {T256x256, T128x128, T64x64};
-    pl.tile = T64x64;
-    for (int t : order) {
-        const TileShape& s = kShapes[t];
-        if (M < s.bm / 2 || N < s.bn / 2) continue;
-        int64_t tiles = cdiv(M, s.bm) * cdiv(N, s.bn) * batch;
-        if (tiles >= cus) {
-            pl.tile = t;
-            break;
-        }
-    }
-    // Very skinny M: a 32-row tile avoids computing padding rows.
-    if (M <= 32 && N >= 256) pl.tile = T32x256;
+    if (M <= 32 && N >= 256)
+        pl.tile = T32x256;
+    else if (vec4 && tiles_of(T256x256) >= cus)
+        pl.tile = T256x256;
     const TileShape& s = kShapes[pl.tile];
-    const int64_t tiles = cdiv(M, s.bm) * cdiv(N, s.bn) * batch;
+    const int64_t tiles = tiles_of(pl.tile);
     int slices = 1;
     if (force_slices > 0) {
         slices = force_slices;
-    } else if (allow_split && batch == 1 && tiles < cus) {
-        // Enough slices for ~2 workgroups per CU, each slice >= 8 k-tiles.
-        int64_t want = cdiv(2 * cus, tiles);
-        int64_t max_by_k = std::max<int64_t>(1, K / (8 * s.bk));
+    } else if (allow_split && batch == 1 && tiles < cus && (2 * tiles <= cus || K >= 2048)) {
+        // About three workgroups per CU, each slice at least two k-tiles.
+        const int64_t want = cdiv(3 * (int64_t)cus, tiles);
+        const int64_t max_by_k = std::max<int64_t>(1, K / (2 * s.bk));
         slices = (int)std::min<int64_t>(want, max_by_k);
     }
     if (slices < 1) slices = 1;
@@ -118,17 +116,17 @@ int gemm_launch(int layout, float* C, const float* A, const float* B, int64_t M,
     const int64_t lda = (layout == NRS_TN) ? M : K;
     const int64_t ldb = (layout == NRS_NT) ? K : N;
 
-    Plan pl = plan_gemm(M, N, K, batch, allow_split && nchw_P == 0, force_slices);
-    const TileShape& s = kShapes[pl.tile];
-
-    // 128-bit loads need 16-byte aligned rows of both operands.
+    // 128-bit loads need 16-byte aligned rows of both operands (k-slices
+    // are multiples of BK, hence of 4).
     bool vec4 = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
-                (sA % 4 == 0 || batch == 1) && (sB % 4 == 0 || batch == 1) &&
-                (pl.k_per_slice % 4 == 0);
+                (sA % 4 == 0 || batch == 1) && (sB % 4 == 0 || batch == 1);
     // Bounds are checked per vector: the guarded dimension must be a multiple of 4.
     if (layout == NRS_NN) vec4 = vec4 && (K % 4 == 0) && (N % 4 == 0);
     if (layout == NRS_NT) vec4 = vec4 && (K % 4 == 0);
     if (layout == NRS_TN) vec4 = vec4 && (M % 4 == 0) && (N % 4 == 0);
+
+    Plan pl = plan_gemm(M, N, K, batch, vec4, allow_split && nchw_P == 0, force_slices);
+    const TileShape& s = kShapes[pl.tile];
 
     GemmArgs p{};
     p.A = A;
@@ -164,9 +162,9 @@ int gemm_launch(int layout, float* C, const float* A, const float* B, int64_t M,
         hipLaunchKernelGGL(fn, grid, dim3(s.threads), 0, stream(), p);
         NRS_LAUNCH_CHECK("gemm (split-K partials)");
         const int64_t total = M * N;
-        unsigned blocks = (unsigned)std::min<int64_t>(cdiv(total, 256), 8 * (int64_t)num_cus());
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream(), p,
-                           pl.slices);
+        unsigned blocks = (unsigned)std::min<int64_t>(cdiv(total, 64), 4 * (int64_t)num_cus());
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(64 * kSplitGroups), 0,
+                           stream(), p, pl.slices);
         NRS_LAUNCH_CHECK("gemm (split-K reduce)");
     } else {
         p.partial = nullptr;

@@ -8,11 +8,13 @@
 //    sums rounded to f32, like the reference's FMA loop, only in another
 //    order). A workgroup of WAVES_M x WAVES_N waves owns a BM x BN block of C;
 //    each wave owns a (32*FM) x (32*FN) sub-block in FM*FN 16-float
-//    accumulators (kept in AGPRs by the compiler).
+//    accumulators. Kernels are compiled for two waves per SIMD (at most 256
+//    registers per lane), so the accumulators live in VGPRs and nothing
+//    spills.
 //  * A and B tiles are staged through LDS, double-buffered, one barrier per
 //    k-tile. Global loads are 128-bit where alignment allows and are issued
-//    one k-tile ahead into registers, so their latency hides behind the MFMAs
-//    of the current tile.
+//    PF k-tiles ahead into a register ring, so their latency hides behind the
+//    MFMAs of the tiles in between.
 //  * An operand whose reduction dimension is contiguous in memory (A of NN/NT,
 //    B of NT) keeps it contiguous in LDS ([mn][k], row stride BK+4 floats:
 //    16-byte fragment reads are bank-conflict-free); the other kind is kept
@@ -166,7 +168,12 @@ __device__ __forceinline__ f32x4 read_frag(const float* s, int mn, int g, int h)
 }
 
 // WPE: minimum waves per SIMD the register allocation must allow.
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool AK, bool BKC, int VEC, int WPE>
+// PF: prefetch depth. Global loads for k-tile j go into register slot j % PF
+// and are issued PF tiles before tile j is stored to LDS, so each load has
+// PF tiles of MFMA work to land in (small tiles need PF > 1 to cover HBM
+// latency; the 256x256 tile has enough work per k-tile with PF = 1).
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool AK, bool BKC, int VEC, int WPE,
+          int PF = 1>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(WPE)))
 void gemm_kernel(GemmArgs p) {
     using C_ = Cfg<BM, BN, BK, WAVES_M, WAVES_N, AK, BKC, VEC>;
@@ -200,51 +207,66 @@ void gemm_kernel(GemmArgs p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    float ra[C_::A_LOADS][VEC];
-    float rb[C_::B_LOADS][VEC];
+    float ra[PF][C_::A_LOADS][VEC];
+    float rb[PF][C_::B_LOADS][VEC];
 
     const int ntiles = kend > kbeg ? (int)((kend - kbeg + BK - 1) / BK) : 0;
     if (ntiles > 0) {
-        load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(ra, A, p.lda, m0, p.M, kbeg, kend, tid);
-        load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT>(rb, B, p.ldb, n0, p.N, kbeg, kend, tid);
-        store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT>(smem, ra, tid);
-        store_tile<BN, BK, BKC, VEC, C_::B_LOADS, C_::SB, NT>(smem + C_::A_ELEMS, rb, tid);
-        if (ntiles > 1) {
-            load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(ra, A, p.lda, m0, p.M, kbeg + BK, kend, tid);
-            load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT>(rb, B, p.ldb, n0, p.N, kbeg + BK, kend, tid);
+        load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(ra[0], A, p.lda, m0, p.M, kbeg, kend, tid);
+        load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT>(rb[0], B, p.ldb, n0, p.N, kbeg, kend, tid);
+        store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT>(smem, ra[0], tid);
+        store_tile<BN, BK, BKC, VEC, C_::B_LOADS, C_::SB, NT>(smem + C_::A_ELEMS, rb[0], tid);
+#pragma unroll
+        for (int j = 1; j <= PF; ++j) {
+            if (j < ntiles) {
+                const int64_t kj = kbeg + (int64_t)j * BK;
+                load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(ra[j % PF], A, p.lda, m0, p.M, kj, kend, tid);
+                load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT>(rb[j % PF], B, p.ldb, n0, p.N, kj, kend, tid);
+            }
         }
         __syncthreads();
     }
 
-    for (int t = 0; t < ntiles; ++t) {
-        const float* sA = smem + (t & 1) * C_::STAGE;
-        const float* sB = sA + C_::A_ELEMS;
+    // The loop is unrolled by PF so every register-slot index is a constant.
+    for (int t0 = 0; t0 < ntiles; t0 += PF) {
 #pragma unroll
-        for (int g = 0; g < BK / 8; ++g) {
-            f32x4 af[FM], bf[FN];
+        for (int u = 0; u < PF; ++u) {
+            const int t = t0 + u;
+            if (t < ntiles) {
+                const float* sA = smem + (t & 1) * C_::STAGE;
+                const float* sB = sA + C_::A_ELEMS;
 #pragma unroll
-            for (int i = 0; i < FM; ++i) af[i] = read_frag<AK, C_::SA>(sA, wm0 + 32 * i + l32, g, h);
+                for (int g = 0; g < BK / 8; ++g) {
+                    f32x4 af[FM], bf[FN];
 #pragma unroll
-            for (int j = 0; j < FN; ++j) bf[j] = read_frag<BKC, C_::SB>(sB, wn0 + 32 * j + l32, g, h);
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
+                    for (int i = 0; i < FM; ++i)
+                        af[i] = read_frag<AK, C_::SA>(sA, wm0 + 32 * i + l32, g, h);
 #pragma unroll
                     for (int j = 0; j < FN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
-        }
-        if (t + 1 < ntiles) {
-            float* dA = smem + ((t + 1) & 1) * C_::STAGE;
-            store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT>(dA, ra, tid);
-            store_tile<BN, BK, BKC, VEC, C_::B_LOADS, C_::SB, NT>(dA + C_::A_ELEMS, rb, tid);
-            if (t + 2 < ntiles) {
-                const int64_t kn = kbeg + (int64_t)(t + 2) * BK;
-                load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(ra, A, p.lda, m0, p.M, kn, kend, tid);
-                load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT>(rb, B, p.ldb, n0, p.N, kn, kend, tid);
+                        bf[j] = read_frag<BKC, C_::SB>(sB, wn0 + 32 * j + l32, g, h);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int i = 0; i < FM; ++i)
+#pragma unroll
+                            for (int j = 0; j < FN; ++j)
+                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s],
+                                                                                acc[i][j], 0, 0, 0);
+                }
+                if (t + 1 < ntiles) {
+                    const int slot = (u + 1) % PF;
+                    float* dA = smem + ((t + 1) & 1) * C_::STAGE;
+                    store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT>(dA, ra[slot], tid);
+                    store_tile<BN, BK, BKC, VEC, C_::B_LOADS, C_::SB, NT>(dA + C_::A_ELEMS, rb[slot], tid);
+                    if (t + 1 + PF < ntiles) {
+                        const int64_t kn = kbeg + (int64_t)(t + 1 + PF) * BK;
+                        load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(ra[slot], A, p.lda, m0, p.M, kn, kend, tid);
+                        load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT>(rb[slot], B, p.ldb, n0, p.N, kn, kend, tid);
+                    }
+                }
+                __syncthreads();
             }
         }
-        __syncthreads();
     }
 
     // Accumulator (i, j) element r of this lane is C[row, col] with
@@ -278,15 +300,35 @@ void gemm_kernel(GemmArgs p) {
     }
 }
 
-// Sums split-K partials in slice order 0..S-1 and applies the epilogue.
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int slices) {
+// Sums split-K partials and applies the epilogue. A workgroup covers 64
+// consecutive outputs with kSplitGroups slice groups: group y sums slices
+// [y*per, (y+1)*per) in ascending order, then the group sums are added in
+// group order. The order depends only on the slice count, so the result is
+// deterministic; every partial read is a coalesced 64-float row segment.
+constexpr int kSplitGroups = 16;
+
+__global__ __launch_bounds__(64 * kSplitGroups) void splitk_reduce_kernel(GemmArgs p,
+                                                                         int slices) {
+    __shared__ float red[kSplitGroups][64];
     const int64_t total = p.M * p.N;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
-        float v = p.partial[e];
-        for (int s = 1; s < slices; ++s) v += p.partial[(int64_t)s * total + e];
-        const int64_t row = e / p.N, col = e - (e / p.N) * p.N;
-        epilogue_store(p, p.C, row, col, v);
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const int per = (slices + kSplitGroups - 1) / kSplitGroups;
+    const int s0 = min(slices, ty * per), s1 = min(slices, s0 + per);
+    for (int64_t base = (int64_t)blockIdx.x * 64; base < total; base += (int64_t)gridDim.x * 64) {
+        const int64_t e = base + tx;
+        float v = 0.0f;
+        if (e < total)
+            for (int s = s0; s < s1; ++s) v += p.partial[(int64_t)s * total + e];
+        red[ty][tx] = v;
+        __syncthreads();
+        if (ty == 0 && e < total) {
+            float r = red[0][tx];
+#pragma unroll
+            for (int y = 1; y < kSplitGroups; ++y) r += red[y][tx];
+            const int64_t row = e / p.N;
+            epilogue_store(p, p.C, row, e - row * p.N, r);
+        }
+        __syncthreads();
     }
 }
 
