@@ -159,6 +159,25 @@ int nrs_maxpool_backward(float *dinput, const float *grad, const int32_t *argmax
                          int64_t N, int64_t C, int64_t in_h, int64_t in_w, int64_t k,
                          int64_t stride);
 
+
+/* ------------------------------------------------------- attention / MLP glue */
+/* transpose2d (src/cuda/graph/transpose.rs:10-24): out[b,j,i] = in[b,i,j] for
+ * `batch` row-major rows x cols matrices; out must not alias in.             */
+int nrs_transpose(float *out, const float *in, int64_t batch, int64_t rows, int64_t cols);
+/* vscale / scale_grad (src/cuda/graph/scale.rs:10-20): out = x*s + beta*out. */
+int nrs_scale(float *out, const float *x, float s, int64_t n, float beta);
+/* softmax_forward (src/cuda/graph/softmax.rs:11-22): softmax over the last
+ * dim of rows x width, max-subtracted.                                       */
+int nrs_softmax_forward(float *out, const float *in, int64_t rows, int64_t width);
+/* softmax_backward (src/cuda/graph/softmax.rs:23-35), from the forward output
+ * y: gin = y*(grad - sum(y*grad)) + beta*gin.                                */
+int nrs_softmax_backward(float *gin, const float *y, const float *grad, int64_t rows,
+                         int64_t width, float beta);
+/* vrelu / relu_grad (src/cuda/graph/relu.rs:16-28): out = max(x, 0);
+ * gin = (x > 0 ? grad : 0) + beta*gin.                                       */
+int nrs_relu_forward(float *out, const float *x, int64_t n);
+int nrs_relu_backward(float *gin, const float *grad, const float *x, int64_t n, float beta);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,12 @@ SIGNATURES = {
     "nrs_sum_axis0": [_P, _P, _I, _I, _F],
     "nrs_maxpool_forward": [_P, _P, _P] + [_I] * 6,
     "nrs_maxpool_backward": [_P, _P, _P] + [_I] * 6,
+    "nrs_transpose": [_P, _P, _I, _I, _I],
+    "nrs_scale": [_P, _P, _F, _I, _F],
+    "nrs_softmax_forward": [_P, _P, _I, _I],
+    "nrs_softmax_backward": [_P, _P, _P, _I, _I, _F],
+    "nrs_relu_forward": [_P, _P, _I],
+    "nrs_relu_backward": [_P, _P, _P, _I, _F],
 }
 _RET = {"nrs_get_stream": ctypes.c_void_p, "nrs_last_error": ctypes.c_char_p}
 

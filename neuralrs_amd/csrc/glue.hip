@@ -1,0 +1,208 @@
+// Glue kernels around the GEMMs of the attention and Linear paths, so the
+// resident ops that feed bmm/matmul stay on the device:
+//   transpose2d      src/cuda/graph/transpose.rs:10-24   (batched 2-D transpose)
+//   vscale           src/cuda/graph/scale.rs:10-20       (x * s)
+//   softmax fwd/bwd  src/cuda/graph/softmax.rs:11-35     (last dim)
+//   vrelu/relu_grad  src/cuda/graph/relu.rs:16-28
+// Every backward entry point takes beta: gin = local + beta * gin, so beta = 1
+// fuses the accumulate_into() the reference launches after each of them
+// (src/cuda/runtime.rs:67-83).
+#include <algorithm>
+
+#include "nrs_internal.hpp"
+
+namespace nrs {
+namespace {
+
+inline unsigned grid_for(int64_t n) {
+    int64_t b = (n + 255) / 256;
+    int64_t cap = 16 * (int64_t)num_cus();
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(b, cap));
+}
+
+// out[b, j, i] = in[b, i, j] through a 32x33 LDS tile: reads and writes are
+// both row-contiguous (coalesced), the odd stride keeps the column reads of
+// the tile free of bank conflicts.
+__global__ __launch_bounds__(256) void transpose_kernel(float* __restrict__ out,
+                                                        const float* __restrict__ in, int64_t R,
+                                                        int64_t C, int64_t tiles_r,
+                                                        int64_t tiles_c) {
+    __shared__ float t[32][33];
+    const int64_t per_batch = tiles_r * tiles_c;
+    const int64_t b = blockIdx.x / per_batch;
+    const int64_t rem = blockIdx.x - b * per_batch;
+    const int64_t r0 = (rem / tiles_c) * 32, c0 = (rem % tiles_c) * 32;
+    const float* src = in + b * R * C;
+    float* dst = out + b * R * C;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    for (int i = ty; i < 32; i += 8) {
+        const int64_t r = r0 + i, c = c0 + tx;
+        if (r < R && c < C) t[i][tx] = src[r * C + c];
+    }
+    __syncthreads();
+    for (int i = ty; i < 32; i += 8) {
+        const int64_t c = c0 + i, r = r0 + tx;  // out row c, column r
+        if (r < R && c < C) dst[c * R + r] = t[tx][i];
+    }
+}
+
+__global__ __launch_bounds__(256) void scale_kernel(float* out, const float* x, float s,
+                                                    int64_t n, float beta) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+        float v = x[i] * s;
+        if (beta != 0.0f) v = v + beta * out[i];
+        out[i] = v;
+    }
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// One wave per row: max, sum of exp(x - max), then exp(x - max) / sum.
+__global__ __launch_bounds__(256) void softmax_fwd_kernel(float* __restrict__ out,
+                                                          const float* __restrict__ in,
+                                                          int64_t rows, int64_t width) {
+    const int lane = threadIdx.x & 63;
+    const int64_t waves = (int64_t)gridDim.x * 4;
+    for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += waves) {
+        const float* x = in + r * width;
+        float m = -INFINITY;
+        for (int64_t f = lane; f < width; f += 64) m = fmaxf(m, x[f]);
+        m = wave_max(m);
+        float s = 0.0f;
+        for (int64_t f = lane; f < width; f += 64) s += expf(x[f] - m);
+        s = wave_sum(s);
+        float* y = out + r * width;
+        for (int64_t f = lane; f < width; f += 64) y[f] = expf(x[f] - m) / s;
+    }
+}
+
+// gin = y * (g - sum(y * g)) + beta * gin, with y the forward output.
+__global__ __launch_bounds__(256) void softmax_bwd_kernel(float* __restrict__ gin,
+                                                          const float* __restrict__ y,
+                                                          const float* __restrict__ g,
+                                                          int64_t rows, int64_t width,
+                                                          float beta) {
+    const int lane = threadIdx.x & 63;
+    const int64_t waves = (int64_t)gridDim.x * 4;
+    for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += waves) {
+        const float* yr = y + r * width;
+        const float* gr = g + r * width;
+        float d = 0.0f;
+        for (int64_t f = lane; f < width; f += 64) d += yr[f] * gr[f];
+        d = wave_sum(d);
+        float* o = gin + r * width;
+        for (int64_t f = lane; f < width; f += 64) {
+            float v = yr[f] * (gr[f] - d);
+            if (beta != 0.0f) v = v + beta * o[f];
+            o[f] = v;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void relu_fwd_kernel(float* out, const float* x, int64_t n) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step)
+        out[i] = x[i] > 0.0f ? x[i] : 0.0f;
+}
+
+__global__ __launch_bounds__(256) void relu_bwd_kernel(float* gin, const float* grad,
+                                                       const float* x, int64_t n, float beta) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+        float v = x[i] > 0.0f ? grad[i] : 0.0f;
+        if (beta != 0.0f) v = v + beta * gin[i];
+        gin[i] = v;
+    }
+}
+
+inline unsigned rows_grid(int64_t rows) {
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>((rows + 3) / 4, 32 * (int64_t)num_cus()));
+}
+
+}  // namespace
+}  // namespace nrs
+
+extern "C" {
+
+int nrs_transpose(float* out, const float* in, int64_t batch, int64_t rows, int64_t cols) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(batch >= 0 && rows >= 0 && cols >= 0, "transpose: negative size");
+    if (batch == 0 || rows == 0 || cols == 0) return NRS_OK;
+    NRS_ARG_CHECK(out && in && out != in, "transpose: null or aliased pointer");
+    const int64_t tr = (rows + 31) / 32, tc = (cols + 31) / 32;
+    const int64_t blocks = batch * tr * tc;
+    NRS_ARG_CHECK(blocks <= INT32_MAX, "transpose: too many tiles");
+    hipLaunchKernelGGL(nrs::transpose_kernel, dim3((unsigned)blocks), dim3(256), 0, nrs::stream(),
+                       out, in, rows, cols, tr, tc);
+    NRS_LAUNCH_CHECK("transpose");
+    return NRS_OK;
+}
+
+int nrs_scale(float* out, const float* x, float s, int64_t n, float beta) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(n >= 0, "scale: negative size");
+    if (n == 0) return NRS_OK;
+    NRS_ARG_CHECK(out && x, "scale: null pointer");
+    hipLaunchKernelGGL(nrs::scale_kernel, dim3(nrs::grid_for(n)), dim3(256), 0, nrs::stream(), out,
+                       x, s, n, beta);
+    NRS_LAUNCH_CHECK("scale");
+    return NRS_OK;
+}
+
+int nrs_softmax_forward(float* out, const float* in, int64_t rows, int64_t width) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(rows >= 0 && width > 0, "softmax: bad shape");
+    if (rows == 0) return NRS_OK;
+    NRS_ARG_CHECK(out && in, "softmax: null pointer");
+    hipLaunchKernelGGL(nrs::softmax_fwd_kernel, dim3(nrs::rows_grid(rows)), dim3(256), 0,
+                       nrs::stream(), out, in, rows, width);
+    NRS_LAUNCH_CHECK("softmax forward");
+    return NRS_OK;
+}
+
+int nrs_softmax_backward(float* gin, const float* y, const float* grad, int64_t rows,
+                         int64_t width, float beta) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(rows >= 0 && width > 0, "softmax backward: bad shape");
+    if (rows == 0) return NRS_OK;
+    NRS_ARG_CHECK(gin && y && grad, "softmax backward: null pointer");
+    hipLaunchKernelGGL(nrs::softmax_bwd_kernel, dim3(nrs::rows_grid(rows)), dim3(256), 0,
+                       nrs::stream(), gin, y, grad, rows, width, beta);
+    NRS_LAUNCH_CHECK("softmax backward");
+    return NRS_OK;
+}
+
+int nrs_relu_forward(float* out, const float* x, int64_t n) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(n >= 0, "relu: negative size");
+    if (n == 0) return NRS_OK;
+    NRS_ARG_CHECK(out && x, "relu: null pointer");
+    hipLaunchKernelGGL(nrs::relu_fwd_kernel, dim3(nrs::grid_for(n)), dim3(256), 0, nrs::stream(),
+                       out, x, n);
+    NRS_LAUNCH_CHECK("relu forward");
+    return NRS_OK;
+}
+
+int nrs_relu_backward(float* gin, const float* grad, const float* x, int64_t n, float beta) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(n >= 0, "relu backward: negative size");
+    if (n == 0) return NRS_OK;
+    NRS_ARG_CHECK(gin && grad && x, "relu backward: null pointer");
+    hipLaunchKernelGGL(nrs::relu_bwd_kernel, dim3(nrs::grid_for(n)), dim3(256), 0, nrs::stream(),
+                       gin, grad, x, n, beta);
+    NRS_LAUNCH_CHECK("relu backward");
+    return NRS_OK;
+}
+
+}  // extern "C"

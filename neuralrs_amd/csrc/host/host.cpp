@@ -1,0 +1,391 @@
+// Implementation of the C++ host layer (neuralrs.hpp) over the C ABI of
+// libnrs_hip.so. Each op follows the reference op it names: same operand
+// checks and panic messages, same output shape, same gradient flow.
+#include "neuralrs.hpp"
+
+#include <cmath>
+#include <unordered_set>
+
+#include "nrs_hip.h"
+
+namespace neuralrs {
+
+namespace {
+
+void check(int rc, const char* what) {
+    if (rc != NRS_OK) throw Panic(std::string(what) + ": " + nrs_last_error());
+}
+
+size_t product(const std::vector<size_t>& s) {
+    size_t p = 1;
+    for (size_t d : s) p *= d;
+    return p;
+}
+
+GpuBuffers& gpu_of(const NodeRef& n, const char* msg) {
+    if (!n || !n->gpu) throw Panic(msg);
+    return *n->gpu;
+}
+
+// An op output: empty host data, device data, zeroed device gradient
+// (the `Node::new(vec![], shape)` + `GpuBuffers{..}` pattern of every op).
+NodeRef make_output(std::vector<size_t> shape, std::vector<NodeRef> parents, DeviceBuffer data) {
+    NodeRef out = std::make_shared<Node>();
+    const size_t len = product(shape);
+    out->shape = std::move(shape);
+    out->parents = std::move(parents);
+    out->gpu = std::make_unique<GpuBuffers>();
+    out->gpu->data = std::move(data);
+    out->gpu->grad = std::make_shared<DeviceBuffer>(len, true);
+    return out;
+}
+
+void build_topo(const NodeRef& n, std::unordered_set<const Node*>& visited,
+                std::vector<NodeRef>& topo) {
+    if (!visited.insert(n.get()).second) return;
+    for (const NodeRef& p : n->parents) build_topo(p, visited, topo);
+    topo.push_back(n);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ DeviceBuffer
+DeviceBuffer::DeviceBuffer(size_t len, bool zero) : len_(len) {
+    void* p = nullptr;
+    check(nrs_malloc(&p, len * sizeof(float)), "device alloc failed");
+    ptr_ = static_cast<float*>(p);
+    if (zero) check(nrs_memset_zero(ptr_, len * sizeof(float)), "device memset failed");
+}
+
+DeviceBuffer DeviceBuffer::from_host(const std::vector<float>& v) {
+    DeviceBuffer b(v.size(), false);
+    check(nrs_memcpy_htod(b.ptr_, v.data(), v.size() * sizeof(float)), "htod failed");
+    return b;
+}
+
+DeviceBuffer::~DeviceBuffer() {
+    if (ptr_) nrs_free(ptr_);
+}
+
+DeviceBuffer::DeviceBuffer(DeviceBuffer&& o) noexcept : ptr_(o.ptr_), len_(o.len_) {
+    o.ptr_ = nullptr;
+    o.len_ = 0;
+}
+
+DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
+    if (this != &o) {
+        if (ptr_) nrs_free(ptr_);
+        ptr_ = o.ptr_;
+        len_ = o.len_;
+        o.ptr_ = nullptr;
+        o.len_ = 0;
+    }
+    return *this;
+}
+
+std::vector<float> DeviceBuffer::to_host() const {
+    std::vector<float> v(len_);
+    check(nrs_memcpy_dtoh(v.data(), ptr_, len_ * sizeof(float)), "dtoh failed");
+    return v;
+}
+
+void DeviceBuffer::zero() { check(nrs_memset_zero(ptr_, len_ * sizeof(float)), "memset failed"); }
+
+// -------------------------------------------------------------------- Node
+NodeRef Node::create(std::vector<float> data, std::vector<size_t> shape) {
+    NodeRef n = std::make_shared<Node>();
+    n->grad.assign(data.size(), 0.0f);
+    n->data = std::move(data);
+    n->shape = std::move(shape);
+    return n;
+}
+
+size_t Node::numel() const { return product(shape); }
+
+void backward_graph(const NodeRef& root) {
+    std::vector<NodeRef> topo;
+    std::unordered_set<const Node*> visited;
+    build_topo(root, visited, topo);
+    for (auto it = topo.rbegin(); it != topo.rend(); ++it) {
+        const std::vector<float> grad = (*it)->grad;
+        if ((*it)->backward_fn) (*it)->backward_fn(grad);
+    }
+}
+
+namespace hip {
+
+// ----------------------------------------------------------------- runtime
+namespace runtime {
+
+void to_cuda(const NodeRef& node) {
+    node->gpu = std::make_unique<GpuBuffers>();
+    node->gpu->data = DeviceBuffer::from_host(node->data);
+    node->gpu->grad = std::make_shared<DeviceBuffer>(node->data.size(), true);
+}
+
+std::vector<float> to_host(const NodeRef& node) {
+    return gpu_of(node, "to_host: node is not on the GPU").data.to_host();
+}
+
+void set_grad(const NodeRef& node, const std::vector<float>& grad) {
+    GpuBuffers& g = gpu_of(node, "set_grad: node not on GPU");
+    if (grad.size() != g.data.len()) throw Panic("set_grad: gradient length mismatch");
+    *g.grad = DeviceBuffer::from_host(grad);
+}
+
+std::vector<float> read_grad(const NodeRef& node) {
+    return gpu_of(node, "read_grad: node not on GPU").grad->to_host();
+}
+
+void zero_grad(const std::vector<NodeRef>& params) {
+    for (const NodeRef& p : params) gpu_of(p, "zero_grad: node not on GPU").grad->zero();
+}
+
+void synchronize() { check(nrs_sync(), "cuda synchronize failed"); }
+
+}  // namespace runtime
+
+// ------------------------------------------------------------------- graph
+namespace graph {
+
+NodeRef matmul(const NodeRef& a, const NodeRef& b) {
+    GpuBuffers& ag = gpu_of(a, "cuda matmul: lhs not on GPU");
+    GpuBuffers& bg = gpu_of(b, "cuda matmul: rhs not on GPU");
+    if (a->shape.size() != 2 || b->shape.size() != 2) throw Panic("cuda matmul: operands must be 2-D");
+    const size_t m = a->shape[0], k = a->shape[1], n = b->shape[1];
+    if (b->shape[0] != k) throw Panic("cuda matmul: inner dims mismatch");
+    DeviceBuffer out(m * n, false);
+    check(nrs_gemm(NRS_NN, out.ptr(), ag.data.ptr(), bg.data.ptr(), m, n, k, 0.0f, nullptr,
+                   NRS_EPI_NONE),
+          "cuda matmul: launch failed");
+    NodeRef node = make_output({m, n}, {a, b}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, a, b, m, k, n](const std::vector<float>&) {
+        GpuBuffers& ag = gpu_of(a, "cuda matmul bwd: lhs not on GPU");
+        GpuBuffers& bg = gpu_of(b, "cuda matmul bwd: rhs not on GPU");
+        // dA += dC . B^T   (matmul_nt, then accumulate_into: matmul.rs:418-423)
+        check(nrs_gemm(NRS_NT, ag.grad->ptr(), grad->ptr(), bg.data.ptr(), m, k, n, 1.0f, nullptr,
+                       NRS_EPI_NONE),
+              "cuda matmul bwd: launch failed");
+        // dB += A^T . dC   (matmul_tn, then accumulate_into: matmul.rs:425-431)
+        check(nrs_gemm(NRS_TN, bg.grad->ptr(), ag.data.ptr(), grad->ptr(), k, n, m, 1.0f, nullptr,
+                       NRS_EPI_NONE),
+              "cuda matmul bwd: launch failed");
+    };
+    return node;
+}
+
+NodeRef bmm(const NodeRef& a, const NodeRef& b) {
+    GpuBuffers& ag = gpu_of(a, "cuda bmm: lhs not on GPU");
+    GpuBuffers& bg = gpu_of(b, "cuda bmm: rhs not on GPU");
+    if (a->shape.size() != 3 || b->shape.size() != 3) throw Panic("cuda bmm: operands must be 3-D");
+    const size_t batch = a->shape[0], m = a->shape[1], k = a->shape[2], n = b->shape[2];
+    if (b->shape[0] != batch || b->shape[1] != k) throw Panic("cuda bmm: shape mismatch");
+    DeviceBuffer out(batch * m * n, false);
+    check(nrs_bmm(NRS_NN, out.ptr(), ag.data.ptr(), bg.data.ptr(), batch, m, n, k, 0.0f),
+          "cuda bmm: launch failed");
+    NodeRef node = make_output({batch, m, n}, {a, b}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, a, b, batch, m, k, n](const std::vector<float>&) {
+        GpuBuffers& ag = gpu_of(a, "cuda bmm bwd: lhs not on GPU");
+        GpuBuffers& bg = gpu_of(b, "cuda bmm bwd: rhs not on GPU");
+        // bmm_grad_a: da[b] += g[b] . B[b]^T   (bmm.rs:27-41, 95-105)
+        check(nrs_bmm(NRS_NT, ag.grad->ptr(), grad->ptr(), bg.data.ptr(), batch, m, k, n, 1.0f),
+              "cuda bmm bwd: grad_a launch");
+        // bmm_grad_b: db[b] += A[b]^T . g[b]   (bmm.rs:42-56, 109-119)
+        check(nrs_bmm(NRS_TN, bg.grad->ptr(), ag.data.ptr(), grad->ptr(), batch, k, n, m, 1.0f),
+              "cuda bmm bwd: grad_b launch");
+    };
+    return node;
+}
+
+NodeRef add(const NodeRef& a, const NodeRef& b) {
+    GpuBuffers& ag = gpu_of(a, "cuda add: lhs not on GPU");
+    GpuBuffers& bg = gpu_of(b, "cuda add: rhs not on GPU");
+    const bool broadcast =
+        a->shape.size() == 2 && b->shape.size() == 1 && a->shape[1] == b->shape[0];
+    const size_t len = product(a->shape);
+    if (!broadcast && product(b->shape) != len) throw Panic("cuda add: shape mismatch");
+    DeviceBuffer out(len, false);
+    if (broadcast)
+        check(nrs_bias_add(out.ptr(), ag.data.ptr(), bg.data.ptr(), a->shape[0], a->shape[1]),
+              "cuda add: bias_add launch failed");
+    else
+        check(nrs_vadd(out.ptr(), ag.data.ptr(), bg.data.ptr(), len), "cuda add: launch failed");
+    NodeRef node = make_output(a->shape, {a, b}, std::move(out));
+    const size_t rows = broadcast ? a->shape[0] : 0, cols = broadcast ? a->shape[1] : 0;
+    node->backward_fn = [grad = node->gpu->grad, a, b, len, broadcast, rows,
+                         cols](const std::vector<float>&) {
+        check(nrs_accumulate(gpu_of(a, "backward: parent not on GPU").grad->ptr(), grad->ptr(), len),
+              "accumulate launch failed");
+        float* bgrad = gpu_of(b, "backward: parent not on GPU").grad->ptr();
+        if (broadcast)  // bias gradient: column sums (add.rs:91-100, reduce.rs:28-43)
+            check(nrs_sum_axis0(bgrad, grad->ptr(), rows, cols, 1.0f), "sum_axis0 launch failed");
+        else
+            check(nrs_accumulate(bgrad, grad->ptr(), len), "accumulate launch failed");
+    };
+    return node;
+}
+
+NodeRef transpose(const NodeRef& a) {
+    GpuBuffers& ag = gpu_of(a, "cuda transpose: input not on GPU");
+    const size_t nd = a->shape.size();
+    if (nd < 2) throw Panic("cuda transpose: needs at least 2 dims");
+    const size_t rows = a->shape[nd - 2], cols = a->shape[nd - 1], len = product(a->shape);
+    const size_t batch = (rows != 0 && cols != 0) ? len / (rows * cols) : 0;
+    DeviceBuffer out(len, false);
+    check(nrs_transpose(out.ptr(), ag.data.ptr(), batch, rows, cols), "cuda transpose: launch failed");
+    std::vector<size_t> shape = a->shape;
+    shape[nd - 2] = cols;
+    shape[nd - 1] = rows;
+    NodeRef node = make_output(shape, {a}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, a, batch, rows, cols, len](const std::vector<float>&) {
+        // the gradient is [.., cols, rows]: transpose back, then accumulate (transpose.rs:53-69)
+        DeviceBuffer tmp(len, false);
+        check(nrs_transpose(tmp.ptr(), grad->ptr(), batch, cols, rows), "cuda transpose bwd: launch");
+        check(nrs_accumulate(gpu_of(a, "backward: parent not on GPU").grad->ptr(), tmp.ptr(), len),
+              "accumulate launch failed");
+    };
+    return node;
+}
+
+NodeRef scale(const NodeRef& a, float s) {
+    GpuBuffers& ag = gpu_of(a, "cuda scale: input not on GPU");
+    const size_t len = product(a->shape);
+    DeviceBuffer out(len, false);
+    check(nrs_scale(out.ptr(), ag.data.ptr(), s, len, 0.0f), "cuda scale: launch failed");
+    NodeRef node = make_output(a->shape, {a}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, a, s, len](const std::vector<float>&) {
+        check(nrs_scale(gpu_of(a, "backward: parent not on GPU").grad->ptr(), grad->ptr(), s, len, 1.0f),
+              "cuda scale bwd: launch");
+    };
+    return node;
+}
+
+NodeRef softmax(const NodeRef& a) {
+    GpuBuffers& ag = gpu_of(a, "cuda softmax: input not on GPU");
+    if (a->shape.empty()) throw Panic("cuda softmax: scalar input");
+    const size_t width = a->shape.back(), len = product(a->shape);
+    const size_t rows = width ? len / width : 0;
+    DeviceBuffer out(len, false);
+    check(nrs_softmax_forward(out.ptr(), ag.data.ptr(), rows, width), "cuda softmax: launch failed");
+    NodeRef node = make_output(a->shape, {a}, std::move(out));
+    // The closure lives inside the node, so the node's own output buffer is
+    // alive whenever the closure runs.
+    const float* y = node->gpu->data.ptr();
+    node->backward_fn = [grad = node->gpu->grad, a, y, rows, width](const std::vector<float>&) {
+        check(nrs_softmax_backward(gpu_of(a, "cuda softmax bwd: input not on GPU").grad->ptr(), y,
+                                   grad->ptr(), rows, width, 1.0f),
+              "cuda softmax bwd: launch");
+    };
+    return node;
+}
+
+NodeRef relu(const NodeRef& a) {
+    GpuBuffers& ag = gpu_of(a, "cuda relu: input not on GPU");
+    const size_t len = product(a->shape);
+    DeviceBuffer out(len, false);
+    check(nrs_relu_forward(out.ptr(), ag.data.ptr(), len), "cuda relu: launch failed");
+    NodeRef node = make_output(a->shape, {a}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, a, len](const std::vector<float>&) {
+        GpuBuffers& g = gpu_of(a, "cuda relu bwd: input not on GPU");
+        check(nrs_relu_backward(g.grad->ptr(), grad->ptr(), g.data.ptr(), len, 1.0f),
+              "cuda relu bwd: launch");
+    };
+    return node;
+}
+
+}  // namespace graph
+
+// ---------------------------------------------------------------------- nn
+namespace nn {
+
+NodeRef conv2d(const NodeRef& input, const NodeRef& weight, const NodeRef& bias, size_t stride,
+               size_t pad) {
+    GpuBuffers& ig = gpu_of(input, "cuda conv2d: input not on GPU");
+    GpuBuffers& wg = gpu_of(weight, "cuda conv2d: weight not on GPU");
+    GpuBuffers& bg = gpu_of(bias, "cuda conv2d: bias not on GPU");
+    if (input->shape.size() != 4 || weight->shape.size() != 4)
+        throw Panic("cuda conv2d: input and weight must be 4-D");
+    const size_t n = input->shape[0], c_in = input->shape[1], in_h = input->shape[2],
+                 in_w = input->shape[3];
+    const size_t c_out = weight->shape[0], kh = weight->shape[2], kw = weight->shape[3];
+    if (weight->shape[1] != c_in) throw Panic("cuda conv2d: channel mismatch");
+    if (product(bias->shape) != c_out) throw Panic("cuda conv2d: bias length mismatch");
+    if (stride == 0 || in_h + 2 * pad < kh || in_w + 2 * pad < kw)
+        throw Panic("cuda conv2d: bad stride/padding for the kernel size");
+    const size_t out_h = (in_h + 2 * pad - kh) / stride + 1;
+    const size_t out_w = (in_w + 2 * pad - kw) / stride + 1;
+    DeviceBuffer out(n * c_out * out_h * out_w, false);
+    check(nrs_conv2d_forward(out.ptr(), ig.data.ptr(), wg.data.ptr(), bg.data.ptr(), n, c_in, in_h,
+                             in_w, c_out, kh, kw, stride, pad),
+          "cuda conv2d: launch failed");
+    NodeRef node = make_output({n, c_out, out_h, out_w}, {input, weight, bias}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, input, weight, bias, n, c_in, in_h, in_w, c_out,
+                         kh, kw, stride, pad](const std::vector<float>&) {
+        GpuBuffers& ig = gpu_of(input, "conv2d bwd: input not on GPU");
+        GpuBuffers& wg = gpu_of(weight, "conv2d bwd: weight not on GPU");
+        GpuBuffers& bg = gpu_of(bias, "conv2d bwd: bias not on GPU");
+        float* dinput = input->requires_grad ? ig.grad->ptr() : nullptr;  // conv.rs:304
+        check(nrs_conv2d_backward(dinput, wg.grad->ptr(), bg.grad->ptr(), grad->ptr(),
+                                  ig.data.ptr(), wg.data.ptr(), n, c_in, in_h, in_w, c_out, kh, kw,
+                                  stride, pad),
+              "cuda conv2d bwd: launch failed");
+    };
+    return node;
+}
+
+NodeRef Linear::forward(const NodeRef& input) const {
+    GpuBuffers& xg = gpu_of(input, "cuda matmul: lhs not on GPU");
+    GpuBuffers& wg = gpu_of(weights, "cuda matmul: rhs not on GPU");
+    GpuBuffers& bg = gpu_of(bias, "cuda add: rhs not on GPU");
+    if (input->shape.size() != 2 || weights->shape.size() != 2)
+        throw Panic("cuda matmul: operands must be 2-D");
+    const size_t batch = input->shape[0], in_f = input->shape[1], out_f = weights->shape[1];
+    if (weights->shape[0] != in_f) throw Panic("cuda matmul: inner dims mismatch");
+    if (product(bias->shape) != out_f) throw Panic("cuda add: bias length mismatch");
+    // x . W + bias in one GEMM: bias added in the epilogue (matmul + add).
+    DeviceBuffer out(batch * out_f, false);
+    check(nrs_gemm(NRS_NN, out.ptr(), xg.data.ptr(), wg.data.ptr(), batch, out_f, in_f, 0.0f,
+                   bg.data.ptr(), NRS_EPI_BIAS_COL),
+          "cuda linear: launch failed");
+    NodeRef x = input, w = weights, b = bias;
+    NodeRef node = make_output({batch, out_f}, {x, w, b}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, x, w, b, batch, in_f,
+                         out_f](const std::vector<float>&) {
+        GpuBuffers& xg = gpu_of(x, "cuda matmul bwd: lhs not on GPU");
+        GpuBuffers& wg = gpu_of(w, "cuda matmul bwd: rhs not on GPU");
+        GpuBuffers& bg = gpu_of(b, "backward: parent not on GPU");
+        check(nrs_gemm(NRS_NT, xg.grad->ptr(), grad->ptr(), wg.data.ptr(), batch, in_f, out_f, 1.0f,
+                       nullptr, NRS_EPI_NONE),
+              "cuda linear bwd: dx launch");
+        check(nrs_gemm(NRS_TN, wg.grad->ptr(), xg.data.ptr(), grad->ptr(), in_f, out_f, batch, 1.0f,
+                       nullptr, NRS_EPI_NONE),
+              "cuda linear bwd: dw launch");
+        check(nrs_sum_axis0(bg.grad->ptr(), grad->ptr(), batch, out_f, 1.0f),
+              "cuda linear bwd: bias launch");
+    };
+    return node;
+}
+
+NodeRef attention(const NodeRef& q, const NodeRef& k, const NodeRef& v) {
+    if (q->shape.size() != 2) throw Panic("attention: q must be [seq, d]");
+    const float s = 1.0f / std::sqrt(static_cast<float>(q->shape[1]));
+    NodeRef kt = graph::transpose(k);
+    NodeRef scores = graph::matmul(q, kt);
+    NodeRef scaled = graph::scale(scores, s);
+    NodeRef weights = graph::softmax(scaled);
+    return graph::matmul(weights, v);
+}
+
+NodeRef attention_batch(const NodeRef& q, const NodeRef& k, const NodeRef& v) {
+    if (q->shape.size() != 3) throw Panic("attention_batch: q must be [batch, seq, d]");
+    const float s = 1.0f / std::sqrt(static_cast<float>(q->shape[2]));
+    NodeRef kt = graph::transpose(k);
+    NodeRef scores = graph::bmm(q, kt);
+    NodeRef scaled = graph::scale(scores, s);
+    NodeRef weights = graph::softmax(scaled);
+    return graph::bmm(weights, v);
+}
+
+}  // namespace nn
+}  // namespace hip
+}  // namespace neuralrs

@@ -1,0 +1,150 @@
+// C++ host layer of the MI355X backend: the reference's resident GPU operator
+// API (Tensor/Node device placement, resident matmul, bmm, Linear, Conv2d and
+// the attention composition), restated over the C ABI of libnrs_hip.so.
+//
+// The reference is Rust. Its GPU path is the `cuda` module behind
+// `--features cuda` (Cargo.toml:23-26, src/lib.rs:53-54). This header keeps
+// the same shape so the same call sites read the same:
+//   Node / GpuBuffers / backward_graph   src/autograd/node.rs:38-126
+//   runtime::{to_cuda, to_host, set_grad, read_grad, zero_grad, synchronize}
+//                                        src/cuda/runtime.rs:39-124
+//   graph::{matmul, bmm, add, transpose, scale, softmax, relu}
+//                                        src/cuda/graph/*.rs
+//   nn::{conv2d, Linear, attention, attention_batch}
+//                                        src/cuda/nn/{conv,linear,attention}.rs
+// Rc<RefCell<Node>> becomes std::shared_ptr<Node>; a panic ("cuda matmul: lhs
+// not on GPU") becomes a thrown neuralrs::Panic with the same message. Like
+// the reference it is single-threaded, device 0, one stream.
+//
+// Differences that change no result: backward closures write straight into
+// the parents' gradients through the kernels' beta = 1 epilogues instead of
+// allocating a temporary and launching accumulate (src/cuda/runtime.rs:67-83);
+// Linear::forward is one GEMM with a fused bias epilogue instead of matmul
+// followed by add (src/cuda/nn/linear.rs:22-25).
+#pragma once
+
+#include <cstddef>
+#include <functional>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace neuralrs {
+
+// A reference panic (`.expect(...)`, `assert_eq!`) surfaces as this exception.
+struct Panic : std::runtime_error {
+    explicit Panic(const std::string& m) : std::runtime_error(m) {}
+};
+
+// src/device.rs:3-7. The reference calls the GPU variant CUDA(usize); here the
+// GPU is the HIP device (always index 0, like src/cuda/backend.rs:21).
+enum class Device { CPU, GPU };
+
+// Owning f32 device allocation: the reference's CudaSlice<f32>.
+class DeviceBuffer {
+public:
+    DeviceBuffer() = default;
+    explicit DeviceBuffer(size_t len, bool zero = true);  // stream.alloc_zeros
+    static DeviceBuffer from_host(const std::vector<float>& v);  // stream.clone_htod
+    ~DeviceBuffer();
+    DeviceBuffer(DeviceBuffer&& o) noexcept;
+    DeviceBuffer& operator=(DeviceBuffer&& o) noexcept;
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+
+    float* ptr() const { return ptr_; }
+    size_t len() const { return len_; }
+    std::vector<float> to_host() const;  // stream.clone_dtoh (synchronises)
+    void zero();                          // stream.memset_zeros
+
+private:
+    float* ptr_ = nullptr;
+    size_t len_ = 0;
+};
+
+// src/autograd/node.rs:49-53: device data plus a shared, swappable gradient.
+struct GpuBuffers {
+    DeviceBuffer data;
+    std::shared_ptr<DeviceBuffer> grad;
+};
+
+struct Node;
+using NodeRef = std::shared_ptr<Node>;
+
+// src/autograd/node.rs:38-47.
+struct Node {
+    std::vector<float> data;
+    std::vector<float> grad;
+    std::vector<size_t> shape;
+    std::vector<NodeRef> parents;
+    std::function<void(const std::vector<float>&)> backward_fn;
+    bool requires_grad = true;
+    std::unique_ptr<GpuBuffers> gpu;  // Option<GpuBuffers>
+
+    // Node::new (src/autograd/node.rs:61-74).
+    static NodeRef create(std::vector<float> data, std::vector<size_t> shape);
+    // Node::device (src/autograd/node.rs:77-82).
+    Device device() const { return gpu ? Device::GPU : Device::CPU; }
+    size_t numel() const;
+};
+
+// Topological backward over the whole graph (src/autograd/node.rs:113-151).
+void backward_graph(const NodeRef& root);
+
+namespace hip {
+
+namespace runtime {
+// src/cuda/runtime.rs:39-51: H->D copy of data and a zeroed device gradient.
+void to_cuda(const NodeRef& node);
+// src/cuda/runtime.rs:57-63.
+std::vector<float> to_host(const NodeRef& node);
+// src/cuda/runtime.rs:87-93: replaces the gradient buffer with a copy of grad.
+void set_grad(const NodeRef& node, const std::vector<float>& grad);
+// src/cuda/runtime.rs:96-103.
+std::vector<float> read_grad(const NodeRef& node);
+// src/cuda/runtime.rs:108-117.
+void zero_grad(const std::vector<NodeRef>& params);
+// src/cuda/runtime.rs:122-124.
+void synchronize();
+}  // namespace runtime
+
+namespace graph {
+// src/cuda/graph/matmul.rs:386-436: [m,k] x [k,n] -> [m,n].
+NodeRef matmul(const NodeRef& a, const NodeRef& b);
+// src/cuda/graph/bmm.rs:65-131: [b,m,k] x [b,k,n] -> [b,m,n].
+NodeRef bmm(const NodeRef& a, const NodeRef& b);
+// src/cuda/graph/add.rs:41-110: same-shape add, or [rows,cols] + bias[cols].
+NodeRef add(const NodeRef& a, const NodeRef& b);
+// src/cuda/graph/transpose.rs:26-72: swaps the last two dims.
+NodeRef transpose(const NodeRef& a);
+// src/cuda/graph/scale.rs:22-58.
+NodeRef scale(const NodeRef& a, float s);
+// src/cuda/graph/softmax.rs:38-85: softmax over the last dim.
+NodeRef softmax(const NodeRef& a);
+// src/cuda/graph/relu.rs:30-80.
+NodeRef relu(const NodeRef& a);
+}  // namespace graph
+
+namespace nn {
+// src/cuda/nn/conv.rs:244-328: input [N,c_in,H,W], weight [c_out,c_in,kh,kw],
+// bias [c_out] -> [N,c_out,oh,ow]. The input gradient is skipped when
+// input->requires_grad is false (conv.rs:304).
+NodeRef conv2d(const NodeRef& input, const NodeRef& weight, const NodeRef& bias, size_t stride,
+               size_t pad);
+
+// src/cuda/nn/linear.rs:11-26: weights [in,out], bias [out].
+struct Linear {
+    NodeRef weights;
+    NodeRef bias;
+    Linear(NodeRef w, NodeRef b) : weights(std::move(w)), bias(std::move(b)) {}
+    NodeRef forward(const NodeRef& input) const;  // [batch,in] -> [batch,out]
+};
+
+// src/cuda/nn/attention.rs:10-32: softmax(Q K^T / sqrt(d)) V.
+NodeRef attention(const NodeRef& q, const NodeRef& k, const NodeRef& v);
+NodeRef attention_batch(const NodeRef& q, const NodeRef& k, const NodeRef& v);
+}  // namespace nn
+
+}  // namespace hip
+}  // namespace neuralrs

@@ -75,6 +75,14 @@ def lib():
             "orc_gemm_f64_rowset": (None, [ctypes.c_int, f32p, f32p, f64p, f64p, I64, I64, I64,
                                            i64p, I64]),
             "orc_max_threads": (ctypes.c_int, []),
+            "orc_transpose": (None, [f32p, f32p, I64, I64, I64]),
+            "orc_transpose_backward": (None, [f32p, f32p, I64, I64, I64]),
+            "orc_scale": (None, [f32p, f32p, ctypes.c_float, I64]),
+            "orc_scale_backward": (None, [f32p, f32p, ctypes.c_float, I64]),
+            "orc_softmax_forward": (None, [f32p, f32p, I64, I64]),
+            "orc_softmax_backward": (None, [f32p, f32p, f32p, I64, I64]),
+            "orc_relu_forward": (None, [f32p, f32p, I64]),
+            "orc_relu_backward": (None, [f32p, f32p, f32p, I64]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -304,6 +312,52 @@ def gemm_f64(layout, a, b, rows, cols, inner, rowidx=None):
         ab = np.empty((rowidx.size, cols), np.float64)
         lib().orc_gemm_f64_rowset(lay, a, b, c, ab, rows, cols, inner, rowidx, rowidx.size)
     return c, ab
+
+
+def transpose(x, batch, rows, cols):
+    x = _f32(x)
+    out = np.empty(batch * rows * cols, np.float32)
+    lib().orc_transpose(x.ravel(), out, batch, rows, cols)
+    return out
+
+
+def transpose_backward(g, ga, batch, rows, cols):
+    lib().orc_transpose_backward(_f32(g).ravel(), ga, batch, rows, cols)
+
+
+def scale(x, s):
+    x = _f32(x).ravel()
+    out = np.empty_like(x)
+    lib().orc_scale(x, out, float(s), x.size)
+    return out
+
+
+def scale_backward(g, ga, s):
+    lib().orc_scale_backward(_f32(g).ravel(), ga, float(s), ga.size)
+
+
+def softmax_forward(x, width):
+    x = _f32(x).ravel()
+    out = np.empty_like(x)
+    lib().orc_softmax_forward(x, out, x.size // width, width)
+    return out
+
+
+def softmax_backward(y, g, ga, width):
+    y = _f32(y).ravel()
+    lib().orc_softmax_backward(y, _f32(g).ravel(), ga, y.size // width, width)
+
+
+def relu_forward(x):
+    x = _f32(x).ravel()
+    out = np.empty_like(x)
+    lib().orc_relu_forward(x, out, x.size)
+    return out
+
+
+def relu_backward(x, g, ga):
+    x = _f32(x).ravel()
+    lib().orc_relu_backward(x, _f32(g).ravel(), ga, x.size)
 
 
 def max_threads() -> int:

@@ -545,6 +545,77 @@ EXPORT void orc_gemm_f64(int layout, const float *A, const float *B, double *C, 
     orc_gemm_f64_rowset(layout, A, B, C, absprod, rows, cols, inner, NULL, rows);
 }
 
+/* ------------------------------------------------------------------------ */
+/* Attention / MLP glue twins (CPU autograd ops), used by the composed-op    */
+/* parity tests.                                                              */
+/* src/autograd/graph/transpose.rs:4-25 forward: out[b, j, i] = in[b, i, j]. */
+/* ------------------------------------------------------------------------ */
+EXPORT void orc_transpose(const float *in, float *out, int64_t batch, int64_t rows,
+                          int64_t cols) {
+    for (int64_t b = 0; b < batch; ++b) {
+        int64_t off = b * rows * cols;
+        for (int64_t i = 0; i < rows; ++i)
+            for (int64_t j = 0; j < cols; ++j) out[off + j * rows + i] = in[off + i * cols + j];
+    }
+}
+
+/* src/autograd/graph/transpose.rs:35-45 backward: ga[b,i,j] += g[b,j,i].    */
+EXPORT void orc_transpose_backward(const float *g, float *ga, int64_t batch, int64_t rows,
+                                   int64_t cols) {
+    for (int64_t b = 0; b < batch; ++b) {
+        int64_t off = b * rows * cols;
+        for (int64_t i = 0; i < rows; ++i)
+            for (int64_t j = 0; j < cols; ++j)
+                ga[off + i * cols + j] = ga[off + i * cols + j] + g[off + j * rows + i];
+    }
+}
+
+/* src/autograd/graph/scale.rs:7-33: out = x*s; backward ga += g*s.          */
+EXPORT void orc_scale(const float *x, float *out, float s, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = x[i] * s;
+}
+EXPORT void orc_scale_backward(const float *g, float *ga, float s, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) ga[i] = ga[i] + g[i] * s;
+}
+
+/* src/autograd/graph/softmax.rs:14-35 forward: per row, max folded from     */
+/* -inf, exps = exp(x - max), sum of exps left to right, out = exp / sum.   */
+EXPORT void orc_softmax_forward(const float *in, float *out, int64_t rows, int64_t width) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *x = in + r * width;
+        float mx = -INFINITY;
+        for (int64_t f = 0; f < width; ++f) mx = fmaxf(mx, x[f]);
+        float sum = 0.0f;
+        for (int64_t f = 0; f < width; ++f) {
+            out[r * width + f] = expf(x[f] - mx);
+            sum = sum + out[r * width + f];
+        }
+        for (int64_t f = 0; f < width; ++f) out[r * width + f] = out[r * width + f] / sum;
+    }
+}
+
+/* src/autograd/graph/softmax.rs:43-57 backward from the forward output y:  */
+/* dot = sum_f y*g (left to right); ga += y*(g - dot).                       */
+EXPORT void orc_softmax_backward(const float *y, const float *g, float *ga, int64_t rows,
+                                 int64_t width) {
+    for (int64_t r = 0; r < rows; ++r) {
+        float dot = 0.0f;
+        for (int64_t f = 0; f < width; ++f) dot = dot + y[r * width + f] * g[r * width + f];
+        for (int64_t f = 0; f < width; ++f) {
+            int64_t i = r * width + f;
+            ga[i] = ga[i] + y[i] * (g[i] - dot);
+        }
+    }
+}
+
+/* src/autograd/graph/relu.rs:10-45: out = x > 0 ? x : 0; ga += x > 0 ? g : 0. */
+EXPORT void orc_relu_forward(const float *x, float *out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = x[i] > 0.0f ? x[i] : 0.0f;
+}
+EXPORT void orc_relu_backward(const float *x, const float *g, float *ga, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) ga[i] = ga[i] + (x[i] > 0.0f ? g[i] : 0.0f);
+}
+
 EXPORT int orc_max_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

@@ -1,0 +1,471 @@
+// GPU-vs-CPU twin tests of the C++ host layer (neuralrs_amd/csrc/host),
+// restating the reference's tests/cuda_*_test.rs: the same deterministic
+// inputs `(i % p) * s - o`, the same seeded upstream gradient, backward_graph,
+// and the same absolute tolerances. The CPU side is the oracle's C
+// restatement of the reference's CPU ops (liboracle.so), composed the way the
+// reference's CPU autograd composes them.
+//
+// Usage: twin_tests [name-substring]. Prints one "PASS <name>" or
+// "FAIL <name>: <reason>" line per test; exit status 1 if any failed.
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "neuralrs.hpp"
+
+extern "C" {
+void orc_graph_matmul_forward(const float*, const float*, float*, int64_t, int64_t, int64_t);
+void orc_graph_matmul_backward(const float*, const float*, const float*, float*, float*, int64_t,
+                               int64_t, int64_t);
+void orc_graph_bmm_forward(const float*, const float*, float*, int64_t, int64_t, int64_t, int64_t);
+void orc_graph_bmm_backward(const float*, const float*, const float*, float*, float*, int64_t,
+                            int64_t, int64_t, int64_t);
+void orc_graph_add_bias_forward(const float*, const float*, float*, int64_t, int64_t);
+void orc_graph_add_bias_backward(const float*, float*, float*, int64_t, int64_t);
+void orc_conv2d_im2col(const float*, const float*, const float*, float*, int64_t, int64_t, int64_t,
+                       int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int);
+void orc_conv2d_forward(const float*, const float*, const float*, float*, int64_t, int64_t, int64_t,
+                        int64_t, int64_t, int64_t, int64_t, int64_t, int64_t);
+void orc_conv2d_backward(const float*, const float*, const float*, float*, float*, float*, int64_t,
+                         int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t);
+void orc_transpose(const float*, float*, int64_t, int64_t, int64_t);
+void orc_transpose_backward(const float*, float*, int64_t, int64_t, int64_t);
+void orc_scale(const float*, float*, float, int64_t);
+void orc_scale_backward(const float*, float*, float, int64_t);
+void orc_softmax_forward(const float*, float*, int64_t, int64_t);
+void orc_softmax_backward(const float*, const float*, float*, int64_t, int64_t);
+void orc_relu_forward(const float*, float*, int64_t);
+void orc_relu_backward(const float*, const float*, float*, int64_t);
+}
+
+using namespace neuralrs;
+namespace gpu = neuralrs::hip::runtime;
+using Vec = std::vector<float>;
+
+struct Failure : std::runtime_error {
+    explicit Failure(const std::string& m) : std::runtime_error(m) {}
+};
+
+// (i % p) as f32 * s + o, evaluated in f32 like the Rust tests.
+Vec formula(size_t n, int p, float s, float o) {
+    Vec v(n);
+    for (size_t i = 0; i < n; ++i) v[i] = static_cast<float>(static_cast<int>(i % p)) * s + o;
+    return v;
+}
+
+// tests/cuda_assembly_test.rs:9-14 `close`: |gpu - cpu| < tol elementwise.
+void close(const Vec& g, const Vec& c, float tol, const std::string& what) {
+    if (g.size() != c.size()) {
+        std::ostringstream m;
+        m << what << ": length mismatch " << g.size() << " vs " << c.size();
+        throw Failure(m.str());
+    }
+    for (size_t i = 0; i < g.size(); ++i)
+        if (!(std::fabs(g[i] - c[i]) < tol)) {
+            std::ostringstream m;
+            m << what << " [" << i << "]: gpu " << g[i] << " cpu " << c[i] << " (tol " << tol << ")";
+            throw Failure(m.str());
+        }
+}
+
+NodeRef resident(const Vec& d, std::vector<size_t> shape) {
+    NodeRef n = Node::create(d, std::move(shape));
+    gpu::to_cuda(n);
+    return n;
+}
+
+// ------------------------------------------------------ CPU compositions
+struct CpuMatmul {  // autograd::graph::matmul forward + backward
+    Vec c, da, db;
+    CpuMatmul(const Vec& a, const Vec& b, const Vec& seed, size_t m, size_t k, size_t n)
+        : c(m * n), da(m * k, 0.0f), db(k * n, 0.0f) {
+        orc_graph_matmul_forward(a.data(), b.data(), c.data(), m, k, n);
+        orc_graph_matmul_backward(a.data(), b.data(), seed.data(), da.data(), db.data(), m, k, n);
+    }
+};
+
+// CPU attention_batch (src/nn/attention.rs:26-39) on [batch, seq, d]; batch = 1
+// gives the single-sequence attention (matmul == bmm with one item).
+struct CpuAttention {
+    Vec out, dq, dk, dv;
+    CpuAttention(const Vec& q, const Vec& k, const Vec& v, const Vec& seed, size_t B, size_t S,
+                 size_t D) {
+        const float s = 1.0f / std::sqrt(static_cast<float>(D));
+        Vec kt(B * S * D), scores(B * S * S), scaled(B * S * S), w(B * S * S);
+        out.assign(B * S * D, 0.0f);
+        orc_transpose(k.data(), kt.data(), B, S, D);
+        orc_graph_bmm_forward(q.data(), kt.data(), scores.data(), B, S, D, S);
+        orc_scale(scores.data(), scaled.data(), s, B * S * S);
+        orc_softmax_forward(scaled.data(), w.data(), B * S, S);
+        orc_graph_bmm_forward(w.data(), v.data(), out.data(), B, S, S, D);
+        Vec dw(B * S * S, 0.0f), dscaled(B * S * S, 0.0f), dscores(B * S * S, 0.0f),
+            dkt(B * S * D, 0.0f);
+        dq.assign(B * S * D, 0.0f);
+        dk.assign(B * S * D, 0.0f);
+        dv.assign(B * S * D, 0.0f);
+        orc_graph_bmm_backward(w.data(), v.data(), seed.data(), dw.data(), dv.data(), B, S, S, D);
+        orc_softmax_backward(w.data(), dw.data(), dscaled.data(), B * S, S);
+        orc_scale_backward(dscaled.data(), dscores.data(), s, B * S * S);
+        orc_graph_bmm_backward(q.data(), kt.data(), dscores.data(), dq.data(), dkt.data(), B, S, D, S);
+        orc_transpose_backward(dkt.data(), dk.data(), B, S, D);
+    }
+};
+
+// ------------------------------------------------------------------ tests
+// tests/cuda_matmul_resident_test.rs:9-45
+void cuda_resident_matmul_backward() {
+    const size_t m = 40, k = 56, n = 32;
+    Vec a = formula(m * k, 13, 0.1f, -0.6f), b = formula(k * n, 7, 0.2f, -0.6f);
+    Vec seed = formula(m * n, 5, 0.2f, 0.1f);
+    CpuMatmul cpu(a, b, seed, m, k, n);
+    NodeRef ga = resident(a, {m, k}), gb = resident(b, {k, n});
+    NodeRef gc = hip::graph::matmul(ga, gb);
+    Vec gc_data = gpu::to_host(gc);
+    gpu::set_grad(gc, seed);
+    backward_graph(gc);
+    close(gc_data, cpu.c, 1e-3f, "fwd");
+    close(gpu::read_grad(ga), cpu.da, 1e-3f, "a.grad");
+    close(gpu::read_grad(gb), cpu.db, 1e-3f, "b.grad");
+}
+
+// tests/cuda_linear_test.rs:9-54: add(matmul(x, w), bias)
+void cuda_resident_linear_chain() {
+    const size_t batch = 16, in_f = 24, out_f = 10;
+    Vec x = formula(batch * in_f, 17, 0.1f, -0.8f), w = formula(in_f * out_f, 13, 0.05f, -0.3f);
+    Vec bias = formula(out_f, 5, 0.2f, -0.4f), seed = formula(batch * out_f, 7, 0.2f, 0.1f);
+    Vec mm(batch * out_f), y(batch * out_f), dmm(batch * out_f, 0.0f), db(out_f, 0.0f);
+    Vec dx(batch * in_f, 0.0f), dw(in_f * out_f, 0.0f);
+    orc_graph_matmul_forward(x.data(), w.data(), mm.data(), batch, in_f, out_f);
+    orc_graph_add_bias_forward(mm.data(), bias.data(), y.data(), batch, out_f);
+    orc_graph_add_bias_backward(seed.data(), dmm.data(), db.data(), batch, out_f);
+    orc_graph_matmul_backward(x.data(), w.data(), dmm.data(), dx.data(), dw.data(), batch, in_f, out_f);
+
+    NodeRef gx = resident(x, {batch, in_f}), gw = resident(w, {in_f, out_f});
+    NodeRef gb = resident(bias, {out_f});
+    NodeRef gy = hip::graph::add(hip::graph::matmul(gx, gw), gb);
+    Vec gy_data = gpu::to_host(gy);
+    gpu::set_grad(gy, seed);
+    backward_graph(gy);
+    close(gy_data, y, 1e-3f, "fwd");
+    close(gpu::read_grad(gx), dx, 1e-3f, "x.grad");
+    close(gpu::read_grad(gw), dw, 1e-3f, "w.grad");
+    close(gpu::read_grad(gb), db, 1e-3f, "bias.grad");
+}
+
+// tests/cuda_assembly_test.rs:17-56: nn::Linear (fused bias epilogue here)
+void cuda_linear() {
+    const size_t batch = 3, in_d = 4, out_d = 5;
+    Vec x = formula(batch * in_d, 11, 0.1f, -0.5f), w = formula(in_d * out_d, 13, 0.1f, -0.6f);
+    Vec b = formula(out_d, 5, 0.1f, -0.2f), seed = formula(batch * out_d, 6, 0.1f, 0.2f);
+    Vec mm(batch * out_d), y(batch * out_d), dmm(batch * out_d, 0.0f), db(out_d, 0.0f);
+    Vec dx(batch * in_d, 0.0f), dw(in_d * out_d, 0.0f);
+    orc_graph_matmul_forward(x.data(), w.data(), mm.data(), batch, in_d, out_d);
+    orc_graph_add_bias_forward(mm.data(), b.data(), y.data(), batch, out_d);
+    orc_graph_add_bias_backward(seed.data(), dmm.data(), db.data(), batch, out_d);
+    orc_graph_matmul_backward(x.data(), w.data(), dmm.data(), dx.data(), dw.data(), batch, in_d, out_d);
+
+    NodeRef gw = resident(w, {in_d, out_d}), gb = resident(b, {out_d});
+    hip::nn::Linear lin(gw, gb);
+    NodeRef gx = resident(x, {batch, in_d});
+    NodeRef gout = lin.forward(gx);
+    Vec gf = gpu::to_host(gout);
+    gpu::set_grad(gout, seed);
+    backward_graph(gout);
+    close(gf, y, 1e-4f, "linear fwd");
+    close(gpu::read_grad(gw), dw, 1e-4f, "linear dw");
+    close(gpu::read_grad(gb), db, 1e-4f, "linear db");
+    close(gpu::read_grad(gx), dx, 1e-4f, "linear dx");
+}
+
+// tests/cuda_conv2d_test.rs:15-43
+void cuda_conv2d_forward() {
+    const size_t n = 2, c_in = 3, in_h = 8, in_w = 8, c_out = 4, kh = 3, kw = 3, stride = 1, pad = 1;
+    Vec input = formula(n * c_in * in_h * in_w, 23, 0.05f, -0.5f);
+    Vec weight = formula(c_out * c_in * kh * kw, 13, 0.07f, -0.4f);
+    Vec bias = formula(c_out, 5, 0.1f, -0.2f);
+    const size_t oh = (in_h + 2 * pad - kh) / stride + 1, ow = (in_w + 2 * pad - kw) / stride + 1;
+    Vec cpu_out(n * c_out * oh * ow);
+    orc_conv2d_im2col(input.data(), weight.data(), bias.data(), cpu_out.data(), n, c_in, c_out,
+                      in_h, in_w, kh, kw, stride, pad, 1);
+    NodeRef gi = resident(input, {n, c_in, in_h, in_w});
+    NodeRef gw = resident(weight, {c_out, c_in, kh, kw});
+    NodeRef gb = resident(bias, {c_out});
+    NodeRef gout = hip::nn::conv2d(gi, gw, gb, stride, pad);
+    if (gout->shape != std::vector<size_t>{n, c_out, oh, ow}) throw Failure("output shape");
+    close(gpu::to_host(gout), cpu_out, 1e-4f, "conv");
+}
+
+// tests/cuda_conv2d_test.rs:46-96, plus the stride-2 and no-input-grad cases.
+void conv_backward_case(size_t n, size_t c_in, size_t in_h, size_t in_w, size_t c_out, size_t k,
+                        size_t stride, size_t pad, bool input_grad) {
+    Vec input = formula(n * c_in * in_h * in_w, 23, 0.05f, -0.5f);
+    Vec weight = formula(c_out * c_in * k * k, 13, 0.07f, -0.4f);
+    Vec bias = formula(c_out, 5, 0.1f, -0.2f);
+    const size_t oh = (in_h + 2 * pad - k) / stride + 1, ow = (in_w + 2 * pad - k) / stride + 1;
+    const size_t out_len = n * c_out * oh * ow;
+    Vec seed = formula(out_len, 7, 0.2f, 0.1f);
+    Vec cpu_out(out_len), c_ig(input.size(), 0.0f), c_wg(weight.size(), 0.0f), c_bg(c_out, 0.0f);
+    orc_conv2d_forward(input.data(), weight.data(), bias.data(), cpu_out.data(), n, c_in, c_out,
+                       in_h, in_w, k, k, stride, pad);
+    orc_conv2d_backward(input.data(), weight.data(), seed.data(), c_ig.data(), c_wg.data(),
+                        c_bg.data(), n, c_in, c_out, in_h, in_w, k, k, stride, pad);
+    NodeRef gi = resident(input, {n, c_in, in_h, in_w});
+    gi->requires_grad = input_grad;
+    NodeRef gw = resident(weight, {c_out, c_in, k, k});
+    NodeRef gb = resident(bias, {c_out});
+    NodeRef gout = hip::nn::conv2d(gi, gw, gb, stride, pad);
+    close(gpu::to_host(gout), cpu_out, 1e-4f, "conv fwd");
+    gpu::set_grad(gout, seed);
+    backward_graph(gout);
+    close(gpu::read_grad(gi), input_grad ? c_ig : Vec(input.size(), 0.0f), 1e-3f, "input.grad");
+    close(gpu::read_grad(gw), c_wg, 1e-3f, "weight.grad");
+    close(gpu::read_grad(gb), c_bg, 1e-3f, "bias.grad");
+}
+
+void cuda_conv2d_backward() { conv_backward_case(2, 3, 7, 7, 5, 3, 1, 1, true); }
+void cuda_conv2d_backward_stride2() { conv_backward_case(2, 3, 9, 9, 4, 3, 2, 1, true); }
+void cuda_conv2d_backward_no_input_grad() { conv_backward_case(2, 3, 7, 7, 5, 3, 1, 1, false); }
+
+// tests/cuda_manip_test.rs:38-48
+void cuda_transpose() {
+    const size_t b = 2, r = 3, c = 4;
+    Vec input = formula(b * r * c, 11, 0.1f, -0.5f), seed = formula(b * r * c, 7, 0.1f, 0.2f);
+    Vec cf(b * r * c), cg(b * r * c, 0.0f);
+    orc_transpose(input.data(), cf.data(), b, r, c);
+    orc_transpose_backward(seed.data(), cg.data(), b, r, c);
+    NodeRef x = resident(input, {b, r, c});
+    NodeRef out = hip::graph::transpose(x);
+    Vec gf = gpu::to_host(out);
+    gpu::set_grad(out, seed);
+    backward_graph(out);
+    close(gf, cf, 1e-5f, "transpose fwd");
+    close(gpu::read_grad(x), cg, 1e-5f, "transpose grad");
+}
+
+// tests/cuda_manip_test.rs:64-74
+void cuda_softmax() {
+    const size_t rows = 4, width = 5;
+    Vec input = formula(rows * width, 9, 0.3f, -1.0f), seed = formula(rows * width, 7, 0.1f, 0.2f);
+    Vec cf(rows * width), cg(rows * width, 0.0f);
+    orc_softmax_forward(input.data(), cf.data(), rows, width);
+    orc_softmax_backward(cf.data(), seed.data(), cg.data(), rows, width);
+    NodeRef x = resident(input, {rows, width});
+    NodeRef out = hip::graph::softmax(x);
+    Vec gf = gpu::to_host(out);
+    gpu::set_grad(out, seed);
+    backward_graph(out);
+    close(gf, cf, 1e-4f, "softmax fwd");
+    close(gpu::read_grad(x), cg, 1e-4f, "softmax grad");
+}
+
+// tests/cuda_manip_test.rs:76-104
+void cuda_bmm() {
+    const size_t batch = 2, m = 3, k = 4, n = 5;
+    Vec a = formula(batch * m * k, 11, 0.1f, -0.5f), bb = formula(batch * k * n, 13, 0.1f, -0.6f);
+    Vec seed = formula(batch * m * n, 7, 0.1f, 0.2f);
+    Vec cf(batch * m * n), cga(a.size(), 0.0f), cgb(bb.size(), 0.0f);
+    orc_graph_bmm_forward(a.data(), bb.data(), cf.data(), batch, m, k, n);
+    orc_graph_bmm_backward(a.data(), bb.data(), seed.data(), cga.data(), cgb.data(), batch, m, k, n);
+    NodeRef ga = resident(a, {batch, m, k}), gbn = resident(bb, {batch, k, n});
+    NodeRef gout = hip::graph::bmm(ga, gbn);
+    Vec gf = gpu::to_host(gout);
+    gpu::set_grad(gout, seed);
+    backward_graph(gout);
+    close(gf, cf, 1e-4f, "bmm fwd");
+    close(gpu::read_grad(ga), cga, 1e-4f, "bmm grad_a");
+    close(gpu::read_grad(gbn), cgb, 1e-4f, "bmm grad_b");
+}
+
+void attention_case(size_t B, size_t S, size_t D, bool batched, float tol, Vec q, Vec k, Vec v,
+                    Vec seed) {
+    CpuAttention cpu(q, k, v, seed, B, S, D);
+    std::vector<size_t> shape = batched ? std::vector<size_t>{B, S, D} : std::vector<size_t>{S, D};
+    NodeRef gq = resident(q, shape), gk = resident(k, shape), gv = resident(v, shape);
+    NodeRef gout = batched ? hip::nn::attention_batch(gq, gk, gv) : hip::nn::attention(gq, gk, gv);
+    Vec gf = gpu::to_host(gout);
+    gpu::set_grad(gout, seed);
+    backward_graph(gout);
+    close(gf, cpu.out, tol, "attention fwd");
+    close(gpu::read_grad(gq), cpu.dq, tol, "attention dq");
+    close(gpu::read_grad(gk), cpu.dk, tol, "attention dk");
+    close(gpu::read_grad(gv), cpu.dv, tol, "attention dv");
+}
+
+// tests/cuda_composite_test.rs:16-48
+void cuda_attention() {
+    const size_t S = 4, D = 6;
+    attention_case(1, S, D, false, 1e-3f, formula(S * D, 11, 0.1f, -0.5f),
+                   formula(S * D, 13, 0.1f, -0.6f), formula(S * D, 7, 0.1f, -0.3f),
+                   formula(S * D, 5, 0.1f, 0.2f));
+}
+
+// tests/cuda_composite_test.rs:50-82
+void cuda_attention_batch() {
+    const size_t B = 2, S = 3, D = 4, n = B * S * D;
+    attention_case(B, S, D, true, 1e-3f, formula(n, 11, 0.1f, -0.5f), formula(n, 13, 0.1f, -0.6f),
+                   formula(n, 7, 0.1f, -0.3f), formula(n, 5, 0.1f, 0.2f));
+}
+
+// Panics of the reference ops surface as neuralrs::Panic with its message.
+void panics_on_misuse() {
+    auto expect_panic = [](auto fn, const std::string& msg) {
+        try {
+            fn();
+        } catch (const Panic& p) {
+            if (std::string(p.what()).find(msg) == std::string::npos)
+                throw Failure("wrong panic: " + std::string(p.what()));
+            return;
+        }
+        throw Failure("no panic for: " + msg);
+    };
+    NodeRef host_only = Node::create(Vec(6, 1.0f), {2, 3});
+    NodeRef r = resident(Vec(6, 1.0f), {3, 2});
+    NodeRef bad = resident(Vec(8, 1.0f), {4, 2});
+    expect_panic([&] { hip::graph::matmul(host_only, r); }, "cuda matmul: lhs not on GPU");
+    expect_panic([&] { hip::graph::matmul(r, host_only); }, "cuda matmul: rhs not on GPU");
+    expect_panic([&] { hip::graph::matmul(r, bad); }, "cuda matmul: inner dims mismatch");
+    expect_panic([&] { gpu::to_host(host_only); }, "to_host: node is not on the GPU");
+    expect_panic([&] { gpu::read_grad(host_only); }, "read_grad: node not on GPU");
+}
+
+// ------------------------------------------------ BASELINE-sized twins
+std::mt19937_64& rng() {
+    static std::mt19937_64 g(1234);
+    return g;
+}
+Vec normal(size_t n, float std) {
+    std::normal_distribution<float> d(0.0f, std);
+    Vec v(n);
+    for (float& x : v) x = d(rng());
+    return v;
+}
+Vec uniform(size_t n, float lo, float hi) {
+    std::uniform_real_distribution<float> d(lo, hi);
+    Vec v(n);
+    for (float& x : v) x = d(rng());
+    return v;
+}
+
+// cfg2: Linear 784->128, ReLU, Linear 128->10, batch 256, He init, zero bias,
+// upstream grad (softmax - onehot) / 256 from the CPU logits.
+void cfg2_mlp_step() {
+    const size_t B = 256, I = 784, H = 128, O = 10;
+    Vec x = normal(B * I, 1.0f), w1 = normal(I * H, std::sqrt(2.0f / I));
+    Vec w2 = normal(H * O, std::sqrt(2.0f / H)), b1(H, 0.0f), b2(O, 0.0f);
+    Vec mm1(B * H), h1(B * H), r1(B * H), mm2(B * O), y(B * O);
+    orc_graph_matmul_forward(x.data(), w1.data(), mm1.data(), B, I, H);
+    orc_graph_add_bias_forward(mm1.data(), b1.data(), h1.data(), B, H);
+    orc_relu_forward(h1.data(), r1.data(), B * H);
+    orc_graph_matmul_forward(r1.data(), w2.data(), mm2.data(), B, H, O);
+    orc_graph_add_bias_forward(mm2.data(), b2.data(), y.data(), B, O);
+    Vec seed(B * O), sm(B * O);
+    orc_softmax_forward(y.data(), sm.data(), B, O);
+    std::uniform_int_distribution<int> cls(0, (int)O - 1);
+    for (size_t r = 0; r < B; ++r) {
+        const int t = cls(rng());
+        for (size_t c = 0; c < O; ++c)
+            seed[r * O + c] = (sm[r * O + c] - (static_cast<int>(c) == t ? 1.0f : 0.0f)) / B;
+    }
+    Vec dmm2(B * O, 0.0f), db2(O, 0.0f), dr1(B * H, 0.0f), dw2(H * O, 0.0f), dh1(B * H, 0.0f);
+    Vec dmm1(B * H, 0.0f), db1(H, 0.0f), dx(B * I, 0.0f), dw1(I * H, 0.0f);
+    orc_graph_add_bias_backward(seed.data(), dmm2.data(), db2.data(), B, O);
+    orc_graph_matmul_backward(r1.data(), w2.data(), dmm2.data(), dr1.data(), dw2.data(), B, H, O);
+    orc_relu_backward(h1.data(), dr1.data(), dh1.data(), B * H);
+    orc_graph_add_bias_backward(dh1.data(), dmm1.data(), db1.data(), B, H);
+    orc_graph_matmul_backward(x.data(), w1.data(), dmm1.data(), dx.data(), dw1.data(), B, I, H);
+
+    NodeRef gx = resident(x, {B, I}), gw1 = resident(w1, {I, H}), gb1 = resident(b1, {H});
+    NodeRef gw2 = resident(w2, {H, O}), gb2 = resident(b2, {O});
+    hip::nn::Linear l1(gw1, gb1), l2(gw2, gb2);
+    NodeRef out = l2.forward(hip::graph::relu(l1.forward(gx)));
+    close(gpu::to_host(out), y, 1e-3f, "cfg2 logits");
+    gpu::set_grad(out, seed);
+    backward_graph(out);
+    close(gpu::read_grad(gw1), dw1, 1e-3f, "cfg2 dW1");
+    close(gpu::read_grad(gb1), db1, 1e-3f, "cfg2 db1");
+    close(gpu::read_grad(gw2), dw2, 1e-3f, "cfg2 dW2");
+    close(gpu::read_grad(gb2), db2, 1e-3f, "cfg2 db2");
+    close(gpu::read_grad(gx), dx, 1e-3f, "cfg2 dx");
+}
+
+// cfg4 per-head attention, heads folded into the batch: [32*8, 128, 32].
+void cfg4_attention_heads() {
+    const size_t B = 256, S = 128, D = 32, n = B * S * D;
+    attention_case(B, S, D, true, 1e-3f, normal(n, 1.0f), normal(n, 1.0f), normal(n, 1.0f),
+                   normal(n, 0.1f));
+}
+
+// cfg3 conv2 layer at a reduced batch: 32 -> 64 channels, 14x14, k3 p1.
+void cfg3_conv2_layer() {
+    const size_t N = 16, C = 32, H = 14, W = 14, CO = 64;
+    Vec input = uniform(N * C * H * W, 0.0f, 1.0f), weight = normal(CO * C * 9, std::sqrt(2.0f / 288));
+    Vec bias(CO, 0.0f), seed = normal(N * CO * H * W, 1.0f);
+    Vec cpu_out(N * CO * H * W), c_ig(input.size(), 0.0f), c_wg(weight.size(), 0.0f), c_bg(CO, 0.0f);
+    orc_conv2d_forward(input.data(), weight.data(), bias.data(), cpu_out.data(), N, C, CO, H, W, 3,
+                       3, 1, 1);
+    orc_conv2d_backward(input.data(), weight.data(), seed.data(), c_ig.data(), c_wg.data(),
+                        c_bg.data(), N, C, CO, H, W, 3, 3, 1, 1);
+    NodeRef gi = resident(input, {N, C, H, W}), gw = resident(weight, {CO, C, 3, 3});
+    NodeRef gb = resident(bias, {CO});
+    NodeRef gout = hip::nn::conv2d(gi, gw, gb, 1, 1);
+    close(gpu::to_host(gout), cpu_out, 1e-4f, "cfg3 conv2 fwd");
+    gpu::set_grad(gout, seed);
+    backward_graph(gout);
+    close(gpu::read_grad(gi), c_ig, 1e-3f, "cfg3 conv2 input.grad");
+    // weight/bias grads sum N*H*W = 3136 terms of O(1): scale the tolerance.
+    close(gpu::read_grad(gw), c_wg, 2e-3f, "cfg3 conv2 weight.grad");
+    close(gpu::read_grad(gb), c_bg, 2e-3f, "cfg3 conv2 bias.grad");
+}
+
+struct Case {
+    const char* name;
+    void (*fn)();
+};
+
+const Case kCases[] = {
+    {"cuda_resident_matmul_backward", cuda_resident_matmul_backward},
+    {"cuda_resident_linear_chain", cuda_resident_linear_chain},
+    {"cuda_linear", cuda_linear},
+    {"cuda_conv2d_forward", cuda_conv2d_forward},
+    {"cuda_conv2d_backward", cuda_conv2d_backward},
+    {"cuda_conv2d_backward_stride2", cuda_conv2d_backward_stride2},
+    {"cuda_conv2d_backward_no_input_grad", cuda_conv2d_backward_no_input_grad},
+    {"cuda_transpose", cuda_transpose},
+    {"cuda_softmax", cuda_softmax},
+    {"cuda_bmm", cuda_bmm},
+    {"cuda_attention", cuda_attention},
+    {"cuda_attention_batch", cuda_attention_batch},
+    {"panics_on_misuse", panics_on_misuse},
+    {"cfg2_mlp_step", cfg2_mlp_step},
+    {"cfg3_conv2_layer", cfg3_conv2_layer},
+    {"cfg4_attention_heads", cfg4_attention_heads},
+};
+
+int main(int argc, char** argv) {
+    const char* filter = argc > 1 ? argv[1] : "";
+    if (!std::strcmp(filter, "--list")) {
+        for (const Case& c : kCases) std::printf("%s\n", c.name);
+        return 0;
+    }
+    int failed = 0;
+    for (const Case& c : kCases) {
+        if (!std::strstr(c.name, filter)) continue;
+        std::printf("RUN  %s\n", c.name);
+        std::fflush(stdout);
+        try {
+            c.fn();
+            gpu::synchronize();
+            std::printf("PASS %s\n", c.name);
+        } catch (const std::exception& e) {
+            ++failed;
+            std::printf("FAIL %s: %s\n", c.name, e.what());
+        }
+        std::fflush(stdout);
+    }
+    return failed ? 1 : 0;
+}

@@ -330,3 +330,73 @@ def test_maxpool_exact(orc):
     g = int_matrix(rng, out.shape)
     di = orc.maxpool_backward(g, am, x.size)
     assert di.sum() == g.sum() and np.array_equal(di[am], g)
+
+
+# ------------------------------------------------- attention / MLP glue twins
+def test_transpose_matches_numpy_and_adjoint(orc):
+    rng = np.random.default_rng(5)
+    b, r, c = 3, 5, 7
+    x = int_matrix(rng, (b, r, c))
+    assert np.array_equal(orc.transpose(x, b, r, c), x.transpose(0, 2, 1).ravel())
+    # backward is the adjoint: <T x, g> == <x, T^T g>, exactly for integers
+    g = int_matrix(rng, (b, c, r))
+    ga = np.zeros(b * r * c, np.float32)
+    orc.transpose_backward(g, ga, b, r, c)
+    assert np.array_equal(ga, g.transpose(0, 2, 1).ravel())
+    lhs = np.dot(orc.transpose(x, b, r, c).astype(np.int64), g.ravel().astype(np.int64))
+    assert lhs == np.dot(x.ravel().astype(np.int64), ga.astype(np.int64))
+
+
+def test_scale_exact_and_backward(orc):
+    rng = np.random.default_rng(6)
+    x = int_matrix(rng, (257,))
+    assert np.array_equal(orc.scale(x, 0.5), x * np.float32(0.5))
+    ga = np.ones(257, np.float32)
+    orc.scale_backward(x, ga, 0.25)
+    assert np.array_equal(ga, 1 + x * np.float32(0.25))
+
+
+def test_softmax_forward_vs_scipy(orc):
+    from scipy.special import softmax as sp_softmax
+
+    rng = np.random.default_rng(7)
+    for rows, width in [(1, 1), (4, 5), (32, 128), (3, 1000)]:
+        x = (rng.standard_normal((rows, width)) * 3).astype(np.float32)
+        y = orc.softmax_forward(x, width).reshape(rows, width)
+        ref = sp_softmax(x.astype(np.float64), axis=1)
+        assert np.max(np.abs(y - ref)) < 1e-6 * max(1, width) ** 0.5
+        # shift invariance (the max subtraction) and huge inputs stay finite
+        y2 = orc.softmax_forward(x + np.float32(80.0), width).reshape(rows, width)
+        assert np.all(np.isfinite(y2)) and np.max(np.abs(y2 - y)) < 1e-5
+
+
+def test_softmax_backward_gradcheck(orc):
+    """ga = J^T g against central differences of the oracle's own forward."""
+    rng = np.random.default_rng(8)
+    rows, width = 3, 6
+    x = rng.standard_normal((rows, width)).astype(np.float32)
+    g = rng.standard_normal((rows, width)).astype(np.float32)
+    y = orc.softmax_forward(x, width)
+    ga = np.zeros(rows * width, np.float32)
+    orc.softmax_backward(y, g, ga, width)
+    h = 1e-3
+    num = np.zeros(rows * width)
+    xf = x.ravel().astype(np.float64)
+    for i in range(rows * width):
+        xp, xm = xf.copy(), xf.copy()
+        xp[i] += h
+        xm[i] -= h
+        fp = np.dot(orc.softmax_forward(xp.astype(np.float32), width), g.ravel())
+        fm = np.dot(orc.softmax_forward(xm.astype(np.float32), width), g.ravel())
+        num[i] = (fp - fm) / (2 * h)
+    assert np.max(np.abs(ga - num)) < 1e-2
+
+
+def test_relu_exact_and_mask(orc):
+    rng = np.random.default_rng(9)
+    x = int_matrix(rng, (300,))
+    assert np.array_equal(orc.relu_forward(x), np.maximum(x, 0))
+    g = int_matrix(rng, (300,))
+    ga = np.zeros(300, np.float32)
+    orc.relu_backward(x, g, ga)
+    assert np.array_equal(ga, np.where(x > 0, g, 0).astype(np.float32))
