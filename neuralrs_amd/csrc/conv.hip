@@ -8,22 +8,27 @@
 // following the weight layout (row = (ic*kh + i)*kw + j), so the weight
 // [c_out, c_in*kh*kw] multiplies it directly.
 //
-// Differences from the reference's launch sequence, all numerically neutral:
-//  * forward: the GEMM epilogue writes NCHW + bias itself (col2out fused);
-//  * backward: the reference's second im2col (conv.rs:317) remains, but the
-//    dcols/col2im, wgrad and bias-grad results are added straight into the
-//    caller's gradients (beta = 1), replacing three accumulate passes;
-//  * wgrad split-K combines slices deterministically, bias grad is a
-//    two-level deterministic reduction instead of c_out serial threads.
+// How the whole-op entry points differ from the reference's launch sequence
+// (the arithmetic is the same products and f32 sums, in another order):
+//  * forward is ONE implicit-GEMM kernel: the GEMM's B operand gathers the
+//    column matrix straight from the NCHW input (no cols buffer, no second
+//    pass) and its epilogue adds the bias and stores NCHW (no col2out);
+//  * the stride-1 input gradient is the implicit-GEMM convolution of the
+//    output gradient with the flipped, channel-transposed weights and padding
+//    k-1-pad, added into dinput (replaces out2mm + TN GEMM + dcols + col2im;
+//    other strides keep that explicit sequence);
+//  * the weight gradient reads the output gradient in place as an NCHW
+//    operand (no out2mm) against the im2col matrix, split-K with a
+//    deterministic slice reduction instead of float atomics;
+//  * the bias gradient is a two-level deterministic reduction instead of
+//    c_out serial threads;
+//  * all three gradients are added into the caller's buffers (beta = 1),
+//    replacing the reference's three accumulate passes.
 #include <algorithm>
 
-#include "nrs_internal.hpp"
+#include "gemm_call.hpp"
 
 namespace nrs {
-
-int gemm_launch(int layout, float* C, const float* A, const float* B, int64_t M, int64_t N,
-                int64_t K, int64_t batch, int64_t sA, int64_t sB, int64_t sC, float beta,
-                const float* bias, int epi, int64_t nchw_P, bool allow_split, int force_slices);
 
 namespace {
 
@@ -60,6 +65,182 @@ __global__ __launch_bounds__(256) void im2col_kernel(float* __restrict__ cols,
         if (iy >= 0 && iy < in_h && ix >= 0 && ix < in_w)
             v = input[((ni * c_in + ic) * in_h + iy) * in_w + ix];
         cols[idx] = v;
+    }
+}
+
+// Same column matrix, four consecutive columns per thread written with one
+// 128-bit store: blockIdx.y is the row (ic, i, j), so its decomposition is
+// uniform across the workgroup, and all column index math is 32-bit. Needs
+// P % 4 == 0 (four columns never straddle an image) and sizes < 2^31.
+__global__ __launch_bounds__(256) void im2col_rows_kernel(float* __restrict__ cols,
+                                                          const float* __restrict__ input,
+                                                          int c_in, int in_h, int in_w, int kh,
+                                                          int kw, int stride, int pad,
+                                                          FastDiv div_P, FastDiv div_ow,
+                                                          int width4) {
+    const int row = blockIdx.y;
+    const int j = row % kw;
+    const int i = (row / kw) % kh;
+    const int ic = row / (kw * kh);
+    const float* src = input + (int64_t)ic * in_h * in_w;
+    float4* dst = reinterpret_cast<float4*>(cols + (int64_t)row * width4 * 4);
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < width4; t += gridDim.x * blockDim.x) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            uint32_t ni, pp, oy, ox;
+            fast_divmod((uint32_t)(4 * t + u), div_P, ni, pp);
+            fast_divmod(pp, div_ow, oy, ox);
+            const int iy = (int)oy * stride + i - pad, ix = (int)ox * stride + j - pad;
+            const bool ok = ((unsigned)iy < (unsigned)in_h) & ((unsigned)ix < (unsigned)in_w);
+            const float x = src[ok ? ((int64_t)ni * c_in * in_h + iy) * in_w + ix : 0];
+            v[u] = ok ? x : 0.0f;
+        }
+        dst[t] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
+// wf[ic, oc, i, j] = w[oc, ic, kh-1-i, kw-1-j]: the weights of the
+// convolution whose output is the stride-1 input gradient.
+__global__ __launch_bounds__(256) void flip_weights_kernel(float* __restrict__ wf,
+                                                           const float* __restrict__ w, int c_out,
+                                                           int c_in, int kh, int kw) {
+    const int total = c_out * c_in * kh * kw;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+        const int j = e % kw;
+        const int i = (e / kw) % kh;
+        const int oc = (e / (kw * kh)) % c_out;
+        const int ic = e / (kw * kh * c_out);
+        wf[e] = w[((oc * c_in + ic) * kh + (kh - 1 - i)) * kw + (kw - 1 - j)];
+    }
+}
+
+// Direct convolution for layers with very few input taps (c_in*kh*kw <=
+// kDirectTaps), e.g. a first layer over grayscale images, where a GEMM tile
+// would be mostly padding. One thread per (output pixel, output channel):
+// blockIdx.y is the channel, so its weights and bias are uniform per
+// workgroup, and consecutive lanes are consecutive pixels (coalesced input
+// reads and output stores). The taps are loaded branch-free (clamped index,
+// then zeroed) so they are all in flight together; the sum runs over the taps
+// in (ic, i, j) order. 32-bit indexing (checked on the host).
+constexpr int kDirectTaps = 32;
+
+template <int TAPS>
+__global__ __launch_bounds__(256) void conv_fwd_direct_kernel(
+    float* __restrict__ out, const float* __restrict__ input, const float* __restrict__ weight,
+    const float* __restrict__ bias, int N, int c_in, int in_h, int in_w, int c_out, int kh, int kw,
+    int stride, int pad, FastDiv div_P, FastDiv div_ow) {
+    // tap t = (ic*kh + i)*kw + j: offset inside one image and (i, j)
+    __shared__ int2 tab[TAPS];
+    const int taps = c_in * kh * kw;
+    if (threadIdx.x < TAPS) {
+        const int t = threadIdx.x < taps ? threadIdx.x : 0;
+        const int j = t % kw, i = (t / kw) % kh, ic = t / (kw * kh);
+        tab[threadIdx.x] = make_int2((ic * in_h + i) * in_w + j, i | (j << 16));
+    }
+    __syncthreads();
+    const int oc = blockIdx.y;
+    const float* w = weight + oc * taps;
+    const float b = bias ? bias[oc] : 0.0f;
+    const int P = (int)div_P.d, total = N * P;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += gridDim.x * blockDim.x) {
+        uint32_t n, pp, oy, ox;
+        fast_divmod((uint32_t)idx, div_P, n, pp);
+        fast_divmod(pp, div_ow, oy, ox);
+        const int iy0 = (int)oy * stride - pad, ix0 = (int)ox * stride - pad;
+        const float* img = input + (int64_t)n * c_in * in_h * in_w + iy0 * in_w + ix0;
+        float x[TAPS];
+#pragma unroll
+        for (int t = 0; t < TAPS; ++t) {
+            const int2 e = tab[t];
+            const int i = e.y & 0xffff, j = e.y >> 16;
+            const bool ok = (t < taps) & ((unsigned)(iy0 + i) < (unsigned)in_h) &
+                            ((unsigned)(ix0 + j) < (unsigned)in_w);
+            const float v = ok ? img[e.x] : 0.0f;
+            x[t] = v;
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int t = 0; t < TAPS; ++t)
+            if (t < taps) acc += w[t] * x[t];
+        out[((int64_t)n * c_out + oc) * P + pp] = acc + b;
+    }
+}
+
+// Direct input gradient for c_in <= kDirectCin (any stride): one thread per
+// input pixel accumulates, for its c_in channels, every (oc, i, j) whose
+// window covers it, with weights (c_out*c_in*kh*kw <= kDirectWeights) from
+// LDS. The covering output positions are found once; the output channels
+// are then taken kDirectBatch at a time with all their loads issued before
+// any is used. dinput = that sum + beta * dinput.
+constexpr int kDirectCin = 4, kDirectWeights = 8192, kDirectBatch = 8, kDirectWin = 9;
+
+__global__ __launch_bounds__(256) void conv_dgrad_direct_kernel(
+    float* __restrict__ dinput, const float* __restrict__ grad, const float* __restrict__ weight,
+    int N, int c_in, int in_h, int in_w, int c_out, int kh, int kw, FastDiv div_stride, int pad,
+    int out_h, int out_w, FastDiv div_HW, FastDiv div_inw, float beta) {
+    __shared__ float wsh[kDirectWeights];
+    const int wn = c_out * c_in * kh * kw;
+    for (int e = threadIdx.x; e < wn; e += blockDim.x) wsh[e] = weight[e];
+    __syncthreads();
+    const int HW = in_h * in_w, total = N * HW, P = out_h * out_w;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += gridDim.x * blockDim.x) {
+        uint32_t n, pix, y, x;
+        fast_divmod((uint32_t)idx, div_HW, n, pix);
+        fast_divmod(pix, div_inw, y, x);
+        // covering windows: output offset and tap index (i*kw + j), at most
+        // kDirectWin of them (the host checks kh*kw <= kDirectWin)
+        int off[kDirectWin], tap[kDirectWin];
+        int nwin = 0;
+        for (int i = 0; i < kh; ++i) {
+            const int oyn = (int)y + pad - i;
+            if (oyn < 0) continue;
+            uint32_t oy, ry;
+            fast_divmod((uint32_t)oyn, div_stride, oy, ry);
+            if (ry != 0 || (int)oy >= out_h) continue;
+            for (int j = 0; j < kw; ++j) {
+                const int oxn = (int)x + pad - j;
+                if (oxn < 0) continue;
+                uint32_t ox, rx;
+                fast_divmod((uint32_t)oxn, div_stride, ox, rx);
+                if (rx != 0 || (int)ox >= out_w) continue;
+                off[nwin] = (int)oy * out_w + (int)ox;
+                tap[nwin] = i * kw + j;
+                ++nwin;
+            }
+        }
+        float acc[kDirectCin] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float* gn = grad + n * c_out * P;
+        for (int oc0 = 0; oc0 < c_out; oc0 += kDirectBatch) {
+            float gv[kDirectBatch][kDirectWin];
+#pragma unroll
+            for (int b = 0; b < kDirectBatch; ++b)
+#pragma unroll
+                for (int w = 0; w < kDirectWin; ++w) {
+                    const bool ok = (oc0 + b < c_out) & (w < nwin);
+                    const float v = gn[ok ? (oc0 + b) * P + off[w] : 0];
+                    gv[b][w] = ok ? v : 0.0f;
+                }
+#pragma unroll
+            for (int b = 0; b < kDirectBatch; ++b)
+#pragma unroll
+                for (int w = 0; w < kDirectWin; ++w)
+                    if ((oc0 + b < c_out) & (w < nwin))
+#pragma unroll
+                        for (int ic = 0; ic < kDirectCin; ++ic)
+                            if (ic < c_in)
+                                acc[ic] += wsh[((oc0 + b) * c_in + ic) * kh * kw + tap[w]] * gv[b][w];
+        }
+#pragma unroll
+        for (int ic = 0; ic < kDirectCin; ++ic)
+            if (ic < c_in) {
+                float* dst = dinput + (n * c_in + ic) * HW + pix;
+                float v = acc[ic];
+                if (beta != 0.0f) v = v + beta * *dst;
+                *dst = v;
+            }
     }
 }
 
@@ -128,80 +309,73 @@ __global__ __launch_bounds__(256) void col2im_kernel(float* __restrict__ dinput,
     }
 }
 
-constexpr int kRedThreads = 256;
+constexpr int kBiasThreads = 1024;
 
-// Block-wide deterministic sum (fixed tree over the 256 lanes).
-__device__ __forceinline__ float block_sum(float v, float* red) {
+// dbias[oc] = sum over (ni, p) of grad[ni, oc, p] (+ beta * dbias[oc]), one
+// workgroup per channel. Each thread sums a fixed strided subset in
+// ascending order, then the 1024 partial sums are combined by a fixed tree,
+// so the result is deterministic. Reads are 128-bit when P % 4 == 0 and the
+// tensor is 16-byte aligned.
+__global__ __launch_bounds__(kBiasThreads) void bias_grad_kernel(float* __restrict__ dbias,
+                                                                 const float* __restrict__ grad,
+                                                                 int N, int c_out, FastDiv div_P,
+                                                                 float beta, bool vec4) {
+    __shared__ float red[kBiasThreads];
+    const int oc = blockIdx.x;
     const int t = threadIdx.x;
-    red[t] = v;
+    const int P = (int)div_P.d;
+    float acc = 0.0f;
+    if (vec4) {  // div_P divides by P / 4 here
+        const int P4 = P, total4 = N * P4;
+        for (int e = t; e < total4; e += kBiasThreads) {
+            uint32_t ni, q;
+            fast_divmod((uint32_t)e, div_P, ni, q);
+            const float4 v = reinterpret_cast<const float4*>(
+                grad + ((int64_t)ni * c_out + oc) * (4 * P4))[q];
+            acc += (v.x + v.y) + (v.z + v.w);
+        }
+    } else {
+        const int total = N * P;
+        for (int e = t; e < total; e += kBiasThreads) {
+            uint32_t ni, q;
+            fast_divmod((uint32_t)e, div_P, ni, q);
+            acc += grad[((int64_t)ni * c_out + oc) * P + q];
+        }
+    }
+    red[t] = acc;
     __syncthreads();
 #pragma unroll
-    for (int s = kRedThreads / 2; s > 0; s >>= 1) {
+    for (int s = kBiasThreads / 2; s > 0; s >>= 1) {
         if (t < s) red[t] += red[t + s];
         __syncthreads();
     }
-    return red[0];
-}
-
-// Stage 1 of the bias gradient: partial[oc, chunk] = sum of grad[ni, oc, p]
-// over the chunk's slice of the flattened (ni, p) range.
-__global__ __launch_bounds__(kRedThreads) void bias_grad_partial_kernel(
-    float* __restrict__ partial, const float* __restrict__ grad, int64_t N, int64_t c_out,
-    int64_t P, int64_t per_chunk) {
-    __shared__ float red[kRedThreads];
-    const int64_t oc = blockIdx.y;
-    const int64_t chunk = blockIdx.x;
-    const int64_t total = N * P;
-    const int64_t e0 = chunk * per_chunk;
-    const int64_t e1 = min(total, e0 + per_chunk);
-    float acc = 0.0f;
-    for (int64_t e = e0 + threadIdx.x; e < e1; e += kRedThreads) {
-        const int64_t ni = e / P;
-        const int64_t p = e - ni * P;
-        acc += grad[(ni * c_out + oc) * P + p];
+    if (t == 0) {
+        float v = red[0];
+        if (beta != 0.0f) v = v + beta * dbias[oc];
+        dbias[oc] = v;
     }
-    const float s = block_sum(acc, red);
-    if (threadIdx.x == 0) partial[oc * gridDim.x + chunk] = s;
-}
-
-// Stage 2: out[c] = sum_k partial[c, k] (k ascending) + beta * out[c].
-__global__ __launch_bounds__(kRedThreads) void rows_sum_kernel(float* __restrict__ out,
-                                                               const float* __restrict__ partial,
-                                                               int64_t n_out, int64_t n_part,
-                                                               float beta) {
-    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= n_out) return;
-    float v = 0.0f;
-    for (int64_t k = 0; k < n_part; ++k) v += partial[c * n_part + k];
-    if (beta != 0.0f) v = v + beta * out[c];
-    out[c] = v;
 }
 
 }  // namespace
 
+// dbias = beta * dbias when there is nothing to sum.
+int zero_or_scale_bias(float* dbias, int64_t c_out, float beta) {
+    if (beta == 1.0f) return NRS_OK;
+    if (beta == 0.0f) return zero_fill(dbias, sizeof(float) * (size_t)c_out);
+    return nrs_scale(dbias, dbias, beta, c_out, 0.0f);
+}
+
 int bias_grad_launch(float* dbias, const float* grad, int64_t N, int64_t c_out, int64_t P,
                      float beta) {
     if (c_out == 0) return NRS_OK;
-    const int64_t total = N * P;
-    // Chunks so that ~4 workgroups per CU run in total, each >= 4096 elements.
-    int64_t chunks = std::max<int64_t>(1, (4 * (int64_t)num_cus() + c_out - 1) / c_out);
-    chunks = std::min<int64_t>(chunks, std::max<int64_t>(1, total / 4096));
-    const int64_t per_chunk = std::max<int64_t>(1, (total + chunks - 1) / chunks);
-    chunks = std::max<int64_t>(1, (total + per_chunk - 1) / per_chunk);
-    NRS_ARG_CHECK(c_out <= 65535, "conv2d bias grad: c_out too large");
-    float* part = workspace(sizeof(float) * (size_t)(c_out * chunks), 3);
-    if (!part) return NRS_ERR_ALLOC;
-    if (total == 0) {
-        int zrc = zero_fill(part, sizeof(float) * (size_t)(c_out * chunks));
-        if (zrc) return zrc;
-    } else {
-        hipLaunchKernelGGL(bias_grad_partial_kernel, dim3((unsigned)chunks, (unsigned)c_out),
-                           dim3(kRedThreads), 0, stream(), part, grad, N, c_out, P, per_chunk);
-        NRS_LAUNCH_CHECK("conv2d bias grad (partials)");
-    }
-    hipLaunchKernelGGL(rows_sum_kernel, dim3((unsigned)((c_out + 255) / 256)), dim3(kRedThreads),
-                       0, stream(), dbias, part, c_out, chunks, beta);
-    NRS_LAUNCH_CHECK("conv2d bias grad (combine)");
+    NRS_ARG_CHECK(c_out <= INT32_MAX && N * P <= INT32_MAX && N * c_out * P <= INT32_MAX * 4ll,
+                  "conv2d bias grad: tensor too large");
+    if (N * P == 0) return zero_or_scale_bias(dbias, c_out, beta);
+    const bool vec4 = ((uintptr_t)grad & 15) == 0 && P % 4 == 0;
+    hipLaunchKernelGGL(bias_grad_kernel, dim3((unsigned)c_out), dim3(kBiasThreads), 0, stream(),
+                       dbias, grad, (int)N, (int)c_out,
+                       make_fastdiv((uint32_t)(vec4 ? P / 4 : P)), beta, vec4);
+    NRS_LAUNCH_CHECK("conv2d bias grad");
     return NRS_OK;
 }
 
@@ -224,14 +398,53 @@ int conv_dims(ConvDims& d, int64_t N, int64_t c_in, int64_t in_h, int64_t in_w, 
 }
 
 int launch_im2col(float* cols, const float* input, const ConvDims& d) {
-    const int64_t total = d.c_in * d.kh * d.kw * d.N * d.out_h * d.out_w;
+    const int64_t rows = d.c_in * d.kh * d.kw, P = d.out_h * d.out_w, width = d.N * P;
+    const int64_t total = rows * width;
     if (total == 0) return NRS_OK;
-    hipLaunchKernelGGL(im2col_kernel, dim3(grid_for(total)), dim3(256), 0, stream(), cols, input,
-                       d.N, d.c_in, d.in_h, d.in_w, (int)d.kh, (int)d.kw, (int)d.stride,
-                       (int)d.pad, d.out_h, d.out_w);
+    const bool fast = P % 4 == 0 && ((uintptr_t)cols & 15) == 0 && rows <= 65535 &&
+                      d.N * d.c_in * d.in_h * d.in_w <= INT32_MAX && width <= INT32_MAX;
+    if (fast) {
+        const int64_t width4 = width / 4;
+        const unsigned bx = (unsigned)std::max<int64_t>(
+            1, std::min<int64_t>((width4 + 255) / 256, (8 * (int64_t)num_cus() + rows - 1) / rows));
+        hipLaunchKernelGGL(im2col_rows_kernel, dim3(bx, (unsigned)rows), dim3(256), 0, stream(),
+                           cols, input, (int)d.c_in, (int)d.in_h, (int)d.in_w, (int)d.kh,
+                           (int)d.kw, (int)d.stride, (int)d.pad, make_fastdiv((uint32_t)P),
+                           make_fastdiv((uint32_t)d.out_w), (int)width4);
+    } else {
+        hipLaunchKernelGGL(im2col_kernel, dim3(grid_for(total)), dim3(256), 0, stream(), cols,
+                           input, d.N, d.c_in, d.in_h, d.in_w, (int)d.kh, (int)d.kw,
+                           (int)d.stride, (int)d.pad, d.out_h, d.out_w);
+    }
     NRS_LAUNCH_CHECK("conv2d im2col");
     return NRS_OK;
 }
+
+// The implicit-GEMM convolution out = conv(image, weight) (+ bias) + beta*out,
+// NCHW in and out, for the stride and padding of g.
+int implicit_conv(float* out, const float* image, const float* weight, const float* bias,
+                  int64_t N, int64_t c_out, const ConvGeom& g, float beta) {
+    GemmCall c;
+    c.layout = NRS_NN;
+    c.C = out;
+    c.A = weight;
+    c.B = image;
+    c.M = c_out;
+    c.N = N * g.P;
+    c.K = g.C * g.kh * g.kw;
+    c.beta = beta;
+    c.bias = bias;
+    c.epi = bias ? NRS_EPI_BIAS_ROW : NRS_EPI_NONE;
+    c.nchw_P = g.P;
+    c.allow_split = false;
+    c.bmode = OP_IM2COL;
+    c.cg = g;
+    c.gather_bytes = N * g.C * g.H * g.W * (int64_t)sizeof(float);
+    return gemm_run(c);
+}
+
+// Gathered operands are read through 32-bit buffer offsets.
+constexpr int64_t kMaxGatherBytes = 0x80000000ll;
 
 int launch_col2im(float* dinput, const float* dcols, const ConvDims& d, float beta) {
     const int64_t total = d.N * d.c_in * d.in_h * d.in_w;
@@ -310,15 +523,54 @@ int nrs_conv2d_forward(float* out, const float* input, const float* weight, cons
     nrs::ConvDims d;
     int rc = nrs::conv_dims(d, N, c_in, in_h, in_w, c_out, kh, kw, stride, pad);
     if (rc) return rc;
-    const int64_t col_h = c_in * kh * kw, P = d.out_h * d.out_w, width = N * P;
-    if (c_out == 0 || width == 0) return NRS_OK;
-    float* cols = nrs::workspace(sizeof(float) * (size_t)std::max<int64_t>(1, col_h * width), 1);
+    const int64_t P = d.out_h * d.out_w;
+    if (c_out == 0 || N * P == 0) return NRS_OK;
+    NRS_ARG_CHECK(kh < 32768 && kw < 32768 && c_in * in_h * in_w <= INT32_MAX &&
+                      c_in * kh * kw <= INT32_MAX,
+                  "conv2d: kernel or image too large");
+    nrs::ConvGeom g{c_in, in_h, in_w, (int)kh, (int)kw, (int)stride, (int)pad, (int)pad,
+                    d.out_h, d.out_w, P};
+    if (c_in * kh * kw <= nrs::kDirectTaps && c_out <= 65535 &&
+        N * std::max(c_in * in_h * in_w, c_out * P) <= INT32_MAX) {
+        // few taps per output: direct convolution, one thread per (pixel, channel)
+        const int64_t taps = c_in * kh * kw;
+        auto fn = taps <= 9 ? nrs::conv_fwd_direct_kernel<9>
+                            : (taps <= 16 ? nrs::conv_fwd_direct_kernel<16>
+                                          : nrs::conv_fwd_direct_kernel<32>);
+        const unsigned bx = (unsigned)std::min<int64_t>((N * P + 255) / 256, 4096);
+        hipLaunchKernelGGL(fn, dim3(bx, (unsigned)c_out), dim3(256), 0, nrs::stream(), out, input,
+                           weight, bias, (int)N, (int)c_in, (int)in_h, (int)in_w, (int)c_out,
+                           (int)kh, (int)kw, (int)stride, (int)pad, nrs::make_fastdiv((uint32_t)P),
+                           nrs::make_fastdiv((uint32_t)d.out_w));
+        NRS_LAUNCH_CHECK("conv2d forward (direct)");
+        return NRS_OK;
+    }
+    if (N * c_in * in_h * in_w * (int64_t)sizeof(float) <= nrs::kMaxGatherBytes) {
+        // out(NCHW) = W[c_out, c_in*kh*kw] . im2col(input) + bias[oc], the
+        // column matrix gathered inside the GEMM (conv.rs:266-277 without the
+        // cols buffer and col2out).
+        return nrs::implicit_conv(out, input, weight, bias, N, c_out, g, 0.0f);
+    }
+    // Inputs over 2 GiB: materialised im2col, then the GEMM with the NCHW +
+    // bias epilogue.
+    const int64_t col_h = c_in * kh * kw, width = N * P;
+    float* cols = nrs::workspace(sizeof(float) * (size_t)(col_h * width), 1);
     if (!cols) return NRS_ERR_ALLOC;
     rc = nrs::launch_im2col(cols, input, d);
     if (rc) return rc;
-    // out(NCHW) = W[c_out, col_h] . cols[col_h, N*P] + bias[oc]
-    return nrs::gemm_launch(NRS_NN, out, weight, cols, c_out, width, col_h, 1, 0, 0, 0, 0.0f, bias,
-                            bias ? NRS_EPI_BIAS_ROW : NRS_EPI_NONE, P, false, 0);
+    nrs::GemmCall c;
+    c.layout = NRS_NN;
+    c.C = out;
+    c.A = weight;
+    c.B = cols;
+    c.M = c_out;
+    c.N = width;
+    c.K = col_h;
+    c.bias = bias;
+    c.epi = bias ? NRS_EPI_BIAS_ROW : NRS_EPI_NONE;
+    c.nchw_P = P;
+    c.allow_split = false;
+    return nrs::gemm_run(c);
 }
 
 int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float* grad,
@@ -331,26 +583,88 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
     if (rc) return rc;
     const int64_t col_h = c_in * kh * kw, P = d.out_h * d.out_w, width = N * P;
     if (c_out == 0) return NRS_OK;
-    float* gmm = nrs::workspace(sizeof(float) * (size_t)std::max<int64_t>(1, c_out * width), 2);
-    if (!gmm) return NRS_ERR_ALLOC;
-    rc = nrs::launch_out2mm(gmm, grad, d);  // [c_out, N*P]
-    if (rc) return rc;
-    float* cols = nrs::workspace(sizeof(float) * (size_t)std::max<int64_t>(1, col_h * width), 1);
-    if (!cols) return NRS_ERR_ALLOC;
+    NRS_ARG_CHECK(kh < 32768 && kw < 32768 && c_in * in_h * in_w <= INT32_MAX &&
+                      c_out * d.out_h * d.out_w <= INT32_MAX && c_out * kh * kw <= INT32_MAX,
+                  "conv2d: kernel or image too large");
     if (dinput) {
-        // dcols[col_h, N*P] = W^T . G ; dinput += col2im(dcols)   (conv.rs:304-312)
-        rc = nrs::gemm_launch(NRS_TN, cols, weight, gmm, col_h, width, c_out, 1, 0, 0, 0, 0.0f,
-                              nullptr, NRS_EPI_NONE, 0, true, 0);
-        if (rc) return rc;
-        rc = nrs::launch_col2im(dinput, cols, d, 1.0f);
-        if (rc) return rc;
+        const int64_t grad_bytes = N * c_out * P * (int64_t)sizeof(float);
+        if (c_in <= nrs::kDirectCin && c_out * c_in * kh * kw <= nrs::kDirectWeights &&
+            kh * kw <= nrs::kDirectWin &&
+            N * std::max(c_in * in_h * in_w, c_out * P) <= INT32_MAX) {
+            // a handful of input channels: direct gather per input pixel
+            hipLaunchKernelGGL(nrs::conv_dgrad_direct_kernel, dim3(nrs::grid_for(N * in_h * in_w)),
+                               dim3(256), 0, nrs::stream(), dinput, grad, weight, (int)N, (int)c_in,
+                               (int)in_h, (int)in_w, (int)c_out, (int)kh, (int)kw,
+                               nrs::make_fastdiv((uint32_t)stride), (int)pad, (int)d.out_h,
+                               (int)d.out_w, nrs::make_fastdiv((uint32_t)(in_h * in_w)),
+                               nrs::make_fastdiv((uint32_t)in_w), 1.0f);
+            NRS_LAUNCH_CHECK("conv2d input gradient (direct)");
+        } else if (stride == 1 && pad <= kh - 1 && pad <= kw - 1 &&
+                   grad_bytes <= nrs::kMaxGatherBytes) {
+            // dinput += conv(grad, flipped W) with padding k-1-pad: the
+            // TN GEMM + col2im of conv.rs:304-312 as one implicit GEMM.
+            const int64_t wn = c_out * c_in * kh * kw;
+            float* wf = nrs::workspace(sizeof(float) * (size_t)std::max<int64_t>(1, wn), 2);
+            if (!wf) return NRS_ERR_ALLOC;
+            hipLaunchKernelGGL(nrs::flip_weights_kernel, dim3(nrs::grid_for(wn)), dim3(256), 0,
+                               nrs::stream(), wf, weight, (int)c_out, (int)c_in, (int)kh, (int)kw);
+            NRS_LAUNCH_CHECK("conv2d flip weights");
+            nrs::ConvGeom g{c_out, d.out_h, d.out_w, (int)kh, (int)kw, 1, (int)(kh - 1 - pad),
+                            (int)(kw - 1 - pad), in_h, in_w, in_h * in_w};
+            rc = nrs::implicit_conv(dinput, grad, wf, nullptr, N, c_in, g, 1.0f);
+            if (rc) return rc;
+        } else {
+            // dcols[col_h, N*P] = W^T . G ; dinput += col2im(dcols)   (conv.rs:304-312)
+            float* gmm = nrs::workspace(sizeof(float) * (size_t)std::max<int64_t>(1, c_out * width), 2);
+            if (!gmm) return NRS_ERR_ALLOC;
+            rc = nrs::launch_out2mm(gmm, grad, d);  // [c_out, N*P]
+            if (rc) return rc;
+            float* cols = nrs::workspace(sizeof(float) * (size_t)std::max<int64_t>(1, col_h * width), 1);
+            if (!cols) return NRS_ERR_ALLOC;
+            nrs::GemmCall c;
+            c.layout = NRS_TN;
+            c.C = cols;
+            c.A = weight;
+            c.B = gmm;
+            c.M = col_h;
+            c.N = width;
+            c.K = c_out;
+            rc = nrs::gemm_run(c);
+            if (rc) return rc;
+            rc = nrs::launch_col2im(dinput, cols, d, 1.0f);
+            if (rc) return rc;
+        }
     }
     if (dweight) {
-        // dW[c_out, col_h] += G . cols^T   (conv.rs:314-320, split-K NT)
+        // dW[c_out, col_h] += G . cols^T   (conv.rs:314-320, split-K NT), with
+        // G read in place from NCHW when it fits a buffer (no out2mm).
+        float* cols = nrs::workspace(sizeof(float) * (size_t)std::max<int64_t>(1, col_h * width), 1);
+        if (!cols) return NRS_ERR_ALLOC;
         rc = nrs::launch_im2col(cols, input, d);
         if (rc) return rc;
-        rc = nrs::gemm_launch(NRS_NT, dweight, gmm, cols, c_out, col_h, width, 1, 0, 0, 0, 1.0f,
-                              nullptr, NRS_EPI_NONE, 0, true, 0);
+        nrs::GemmCall c;
+        c.layout = NRS_NT;
+        c.C = dweight;
+        c.B = cols;
+        c.M = c_out;
+        c.N = col_h;
+        c.K = width;
+        c.beta = 1.0f;
+        const int64_t grad_bytes = N * c_out * P * (int64_t)sizeof(float);
+        if (grad_bytes <= nrs::kMaxGatherBytes) {
+            c.A = grad;
+            c.amode = nrs::OP_NCHW;
+            c.cg.P = P;
+            c.cg.ow = d.out_w;
+            c.gather_bytes = grad_bytes;
+        } else {
+            float* gmm = nrs::workspace(sizeof(float) * (size_t)(c_out * width), 2);
+            if (!gmm) return NRS_ERR_ALLOC;
+            rc = nrs::launch_out2mm(gmm, grad, d);
+            if (rc) return rc;
+            c.A = gmm;
+        }
+        rc = nrs::gemm_run(c);
         if (rc) return rc;
     }
     if (dbias) {

@@ -8,6 +8,7 @@
 // grid-stride loops capped at a few workgroups per CU.
 #include <algorithm>
 
+#include "fastdiv.hpp"
 #include "nrs_internal.hpp"
 
 namespace nrs {
@@ -140,6 +141,58 @@ __global__ __launch_bounds__(256) void maxpool_bwd_kernel(float* __restrict__ di
     }
 }
 
+// Non-overlapping windows (k == stride), 32-bit indexing (the host checks
+// the input fits): one output per thread, window scanned row by row with a
+// strict > so the first maximum wins, as maxpool_forward does.
+__global__ __launch_bounds__(256) void maxpool_fwd_tiled_kernel(float* __restrict__ out,
+                                                                int32_t* __restrict__ argmax,
+                                                                const float* __restrict__ input,
+                                                                int total, int in_h, int in_w,
+                                                                int k, FastDiv div_ow,
+                                                                FastDiv div_oh) {
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += gridDim.x * blockDim.x) {
+        uint32_t r, ox, nc, oy;
+        fast_divmod((uint32_t)idx, div_ow, r, ox);
+        fast_divmod(r, div_oh, nc, oy);
+        const int base = nc * in_h * in_w + (oy * k) * in_w + ox * k;
+        int best_i = base;
+        float best = input[base];
+        for (int i = 0; i < k; ++i)
+            for (int j = 0; j < k; ++j) {
+                const int ii = base + i * in_w + j;
+                const float v = input[ii];
+                if (v > best) {
+                    best = v;
+                    best_i = ii;
+                }
+            }
+        out[idx] = best;
+        argmax[idx] = best_i;
+    }
+}
+
+// k == stride: every input element lies in at most one window, so
+// dinput[e] += grad[w] exactly when argmax[w] == e; other elements are not
+// touched.
+__global__ __launch_bounds__(256) void maxpool_bwd_tiled_kernel(float* __restrict__ dinput,
+                                                                const float* __restrict__ grad,
+                                                                const int32_t* __restrict__ argmax,
+                                                                int total, FastDiv div_inw,
+                                                                FastDiv div_inh, FastDiv div_k,
+                                                                int out_h, int out_w) {
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+        uint32_t r, x, nc, y;
+        fast_divmod((uint32_t)e, div_inw, r, x);
+        fast_divmod(r, div_inh, nc, y);
+        const int oy = (int)fast_div(y, div_k), ox = (int)fast_div(x, div_k);
+        if (oy < out_h && ox < out_w) {
+            const int w = ((int)nc * out_h + oy) * out_w + ox;
+            if (argmax[w] == e) dinput[e] = dinput[e] + grad[w];
+        }
+    }
+}
+
 }  // namespace
 }  // namespace nrs
 
@@ -217,9 +270,14 @@ int nrs_maxpool_forward(float* out, int32_t* argmax, const float* input, int64_t
     const int64_t oh = (in_h - k) / stride + 1, ow = (in_w - k) / stride + 1;
     const int64_t total = N * C * oh * ow;
     if (total == 0) return NRS_OK;
-    hipLaunchKernelGGL(nrs::maxpool_fwd_kernel, dim3(nrs::grid_for(total)), dim3(256), 0,
-                       nrs::stream(), out, argmax, input, N, C, in_h, in_w, (int)k, (int)stride,
-                       oh, ow);
+    if (k == stride)
+        hipLaunchKernelGGL(nrs::maxpool_fwd_tiled_kernel, dim3(nrs::grid_for(total)), dim3(256), 0,
+                           nrs::stream(), out, argmax, input, (int)total, (int)in_h, (int)in_w,
+                           (int)k, nrs::make_fastdiv((uint32_t)ow), nrs::make_fastdiv((uint32_t)oh));
+    else
+        hipLaunchKernelGGL(nrs::maxpool_fwd_kernel, dim3(nrs::grid_for(total)), dim3(256), 0,
+                           nrs::stream(), out, argmax, input, N, C, in_h, in_w, (int)k,
+                           (int)stride, oh, ow);
     NRS_LAUNCH_CHECK("maxpool forward");
     return NRS_OK;
 }
@@ -228,12 +286,19 @@ int nrs_maxpool_backward(float* dinput, const float* grad, const int32_t* argmax
                          int64_t C, int64_t in_h, int64_t in_w, int64_t k, int64_t stride) {
     NRS_REQUIRE_INIT();
     NRS_ARG_CHECK(k > 0 && stride > 0 && in_h >= k && in_w >= k, "maxpool: bad window");
+    NRS_ARG_CHECK(N * C * in_h * in_w <= INT32_MAX, "maxpool: input too large for int32 argmax");
     const int64_t oh = (in_h - k) / stride + 1, ow = (in_w - k) / stride + 1;
     const int64_t total = N * C * in_h * in_w;
     if (total == 0) return NRS_OK;
-    hipLaunchKernelGGL(nrs::maxpool_bwd_kernel, dim3(nrs::grid_for(total)), dim3(256), 0,
-                       nrs::stream(), dinput, grad, argmax, N, C, in_h, in_w, (int)k, (int)stride,
-                       oh, ow);
+    if (k == stride)
+        hipLaunchKernelGGL(nrs::maxpool_bwd_tiled_kernel, dim3(nrs::grid_for(total)), dim3(256), 0,
+                           nrs::stream(), dinput, grad, argmax, (int)total,
+                           nrs::make_fastdiv((uint32_t)in_w), nrs::make_fastdiv((uint32_t)in_h),
+                           nrs::make_fastdiv((uint32_t)k), (int)oh, (int)ow);
+    else
+        hipLaunchKernelGGL(nrs::maxpool_bwd_kernel, dim3(nrs::grid_for(total)), dim3(256), 0,
+                           nrs::stream(), dinput, grad, argmax, N, C, in_h, in_w, (int)k,
+                           (int)stride, oh, ow);
     NRS_LAUNCH_CHECK("maxpool backward");
     return NRS_OK;
 }

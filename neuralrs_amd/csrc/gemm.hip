@@ -17,10 +17,11 @@ struct TileShape {
     int bm, bn, bk, threads;
 };
 
-template <int BM, int BN, int BK, int WM_, int WN_, int PF, bool AK, bool BKC>
+template <int BM, int BN, int BK, int WM_, int WN_, int PF, bool AK, bool BKC, int AM = OP_DENSE,
+          int BMD = OP_DENSE>
 KernelFn pick_vec(bool vec4) {
-    return vec4 ? gemm_kernel<BM, BN, BK, WM_, WN_, AK, BKC, 4, 2, PF>
-                : gemm_kernel<BM, BN, BK, WM_, WN_, AK, BKC, 1, 2, PF>;
+    return vec4 ? gemm_kernel<BM, BN, BK, WM_, WN_, AK, BKC, 4, 2, PF, AM, BMD>
+                : gemm_kernel<BM, BN, BK, WM_, WN_, AK, BKC, 1, 2, PF, AM, BMD>;
 }
 
 template <int BM, int BN, int BK, int WM_, int WN_, int PF>
@@ -32,6 +33,18 @@ KernelFn pick_layout(int layout, bool vec4) {
     }
 }
 
+// The implicit-GEMM convolution variants exist for the two tiles the conv
+// shapes use: NN with an OP_IM2COL B (forward, stride-1 input gradient) and
+// NT with an OP_NCHW A (weight gradient).
+template <int BM, int BN, int BK, int WM_, int WN_, int PF>
+KernelFn pick_conv(int layout, int amode, int bmode, bool vec4) {
+    if (layout == NRS_NN && amode == OP_DENSE && bmode == OP_IM2COL)
+        return pick_vec<BM, BN, BK, WM_, WN_, PF, true, false, OP_DENSE, OP_IM2COL>(vec4);
+    if (layout == NRS_NT && amode == OP_NCHW && bmode == OP_DENSE)
+        return pick_vec<BM, BN, BK, WM_, WN_, PF, true, true, OP_NCHW, OP_DENSE>(vec4);
+    return nullptr;
+}
+
 // Tile configurations (chosen by a sweep over the workload shapes on MI355X).
 // All run two waves per SIMD (register budget capped at 256 per lane,
 // accumulators in VGPRs):
@@ -39,19 +52,30 @@ KernelFn pick_layout(int layout, bool vec4) {
 //    GEMMs (83-85% of FP32 MFMA peak at 4096^3 and 8192^3);
 //  * 64x64x32, 4 waves of 32x32, prefetch depth 2: everything mid-sized
 //    (bmm items, conv GEMMs, projections, split-K weight gradients);
-//  * 32x256x32, 4 waves of 32x64: outputs with at most 32 rows.
-enum TileId { T256x256 = 0, T64x64, T32x256, T_COUNT };
+//  * 32x256x32, 4 waves of 32x64: outputs with at most 32 rows;
+//  * 32x128x32, 4 waves of 32x32, prefetch depth 2: convolutions whose GEMM
+//    has at most 32 rows (a 64-row tile would double the MFMA work).
+enum TileId { T256x256 = 0, T64x64, T32x256, T32x128, T_COUNT };
 const TileShape kShapes[T_COUNT] = {
     {256, 256, 32, 512},
     {64, 64, 32, 256},
     {32, 256, 32, 256},
+    {32, 128, 32, 256},
 };
 
-KernelFn kernel_for(int tile, int layout, bool vec4) {
+KernelFn kernel_for(int tile, int layout, bool vec4, int amode, int bmode) {
+    if (amode != OP_DENSE || bmode != OP_DENSE) {
+        switch (tile) {
+            case T64x64: return pick_conv<64, 64, 32, 2, 2, 2>(layout, amode, bmode, vec4);
+            case T32x128: return pick_conv<32, 128, 32, 1, 4, 2>(layout, amode, bmode, vec4);
+            default: return nullptr;
+        }
+    }
     switch (tile) {
         case T256x256: return pick_layout<256, 256, 32, 2, 4, 1>(layout, vec4);
         case T64x64: return pick_layout<64, 64, 32, 2, 2, 2>(layout, vec4);
-        default: return pick_layout<32, 256, 32, 1, 4, 1>(layout, vec4);
+        case T32x256: return pick_layout<32, 256, 32, 1, 4, 1>(layout, vec4);
+        default: return nullptr;
     }
 }
 
@@ -67,25 +91,30 @@ struct Plan {
 
 // Chooses the tile shape and the number of K slices. The 256x256 tile is
 // used only with 128-bit loads (its scalar-load variant spills).
-Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool allow_split,
-               int force_slices) {
+Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool dense,
+               bool allow_split, int force_slices) {
     const int cus = num_cus();
     auto tiles_of = [&](int t) {
         return cdiv(M, kShapes[t].bm) * cdiv(N, kShapes[t].bn) * batch;
     };
     Plan pl{T64x64, 1, K};
-    if (M <= 32 && N >= 256)
-        pl.tile = T32x256;
-    else if (vec4 && tiles_of(T256x256) >= cus)
-        pl.tile = T256x256;
+    if (dense) {
+        if (M <= 32 && N >= 256)
+            pl.tile = T32x256;
+        else if (vec4 && tiles_of(T256x256) >= cus)
+            pl.tile = T256x256;
+    } else if (M <= 32) {  // gathered (convolution) operands: 64x64 or 32x128
+        pl.tile = T32x128;
+    }
     const TileShape& s = kShapes[pl.tile];
     const int64_t tiles = tiles_of(pl.tile);
     int slices = 1;
     if (force_slices > 0) {
         slices = force_slices;
     } else if (allow_split && batch == 1 && tiles < cus && (2 * tiles <= cus || K >= 2048)) {
-        // About three workgroups per CU, each slice at least two k-tiles.
-        const int64_t want = cdiv(3 * (int64_t)cus, tiles);
+        // About three workgroups per CU, each slice at least two k-tiles, at
+        // most 256 slices (the reduction reads every slice of every output).
+        const int64_t want = std::min<int64_t>(256, cdiv(3 * (int64_t)cus, tiles));
         const int64_t max_by_k = std::max<int64_t>(1, K / (2 * s.bk));
         slices = (int)std::min<int64_t>(want, max_by_k);
     }
@@ -100,59 +129,84 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool a
 
 }  // namespace
 
-// Shared launcher: C[b] = epi(op(A[b]) op(B[b])) + beta*C[b] for b < batch.
-int gemm_launch(int layout, float* C, const float* A, const float* B, int64_t M, int64_t N,
-                int64_t K, int64_t batch, int64_t sA, int64_t sB, int64_t sC, float beta,
-                const float* bias, int epi, int64_t nchw_P, bool allow_split, int force_slices) {
+int gemm_run(const GemmCall& c) {
+    const int layout = c.layout;
+    const int64_t M = c.M, N = c.N, K = c.K, batch = c.batch;
     NRS_ARG_CHECK(layout >= NRS_NN && layout <= NRS_TN, "gemm: unknown layout %d", layout);
     NRS_ARG_CHECK(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "gemm: negative size");
     if (M == 0 || N == 0 || batch == 0) return NRS_OK;
-    NRS_ARG_CHECK(C != nullptr, "gemm: null C");
-    NRS_ARG_CHECK(K == 0 || (A != nullptr && B != nullptr), "gemm: null operand");
-    NRS_ARG_CHECK(!(epi & (NRS_EPI_BIAS_COL | NRS_EPI_BIAS_ROW)) || bias != nullptr,
+    NRS_ARG_CHECK(c.C != nullptr, "gemm: null C");
+    NRS_ARG_CHECK(K == 0 || (c.A != nullptr && c.B != nullptr), "gemm: null operand");
+    NRS_ARG_CHECK(!(c.epi & (NRS_EPI_BIAS_COL | NRS_EPI_BIAS_ROW)) || c.bias != nullptr,
                   "gemm: bias epilogue with null bias");
     NRS_ARG_CHECK(M <= INT32_MAX && N <= INT32_MAX, "gemm: dimension too large");
+    const bool dense = c.amode == OP_DENSE && c.bmode == OP_DENSE;
+    NRS_ARG_CHECK(dense || (c.gather_bytes > 0 && c.gather_bytes <= 0x80000000ll),
+                  "gemm: gathered operand must be 1 B .. 2 GiB");
 
     const int64_t lda = (layout == NRS_TN) ? M : K;
     const int64_t ldb = (layout == NRS_NT) ? K : N;
 
     // 128-bit loads need 16-byte aligned rows of both operands (k-slices
-    // are multiples of BK, hence of 4).
-    bool vec4 = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
-                (sA % 4 == 0 || batch == 1) && (sB % 4 == 0 || batch == 1);
-    // Bounds are checked per vector: the guarded dimension must be a multiple of 4.
-    if (layout == NRS_NN) vec4 = vec4 && (K % 4 == 0) && (N % 4 == 0);
-    if (layout == NRS_NT) vec4 = vec4 && (K % 4 == 0);
-    if (layout == NRS_TN) vec4 = vec4 && (M % 4 == 0) && (N % 4 == 0);
+    // are multiples of BK, hence of 4). Bounds are checked per vector, so the
+    // guarded dimension must be a multiple of 4.
+    bool a_vec, b_vec;
+    if (c.amode == OP_NCHW)  // four columns never straddle an image
+        a_vec = aligned16(c.A) && c.cg.P % 4 == 0 && K % 4 == 0;
+    else
+        a_vec = aligned16(c.A) && lda % 4 == 0 && (c.sA % 4 == 0 || batch == 1) &&
+                (layout == NRS_TN ? M % 4 == 0 : K % 4 == 0);
+    if (c.bmode == OP_IM2COL)  // gathered element-wise; only the LDS store is vectorised
+        b_vec = true;
+    else
+        b_vec = aligned16(c.B) && ldb % 4 == 0 && (c.sB % 4 == 0 || batch == 1) &&
+                (layout == NRS_NT ? K % 4 == 0 : N % 4 == 0);
+    const bool vec4 = a_vec && b_vec;
 
-    Plan pl = plan_gemm(M, N, K, batch, vec4, allow_split && nchw_P == 0, force_slices);
+    Plan pl = plan_gemm(M, N, K, batch, vec4, dense, c.allow_split && c.nchw_P == 0,
+                        c.force_slices);
     const TileShape& s = kShapes[pl.tile];
 
     GemmArgs p{};
-    p.A = A;
-    p.B = B;
-    p.C = C;
-    p.bias = bias;
+    p.A = c.A;
+    p.B = c.B;
+    p.C = c.C;
+    p.bias = c.bias;
     p.M = M;
     p.N = N;
     p.K = K;
     p.lda = lda;
     p.ldb = ldb;
     p.ldc = N;
-    p.sA = sA;
-    p.sB = sB;
-    p.sC = sC;
+    p.sA = c.sA;
+    p.sB = c.sB;
+    p.sC = c.sC;
     p.tiles_m = (int)cdiv(M, s.bm);
     p.tiles_n = (int)cdiv(N, s.bn);
     p.group_m = 8;
-    p.beta = beta;
-    p.epi = epi;
-    p.nchw_P = nchw_P;
+    p.beta = c.beta;
+    p.epi = c.epi;
+    p.nchw_P = c.nchw_P;
     p.k_per_slice = pl.k_per_slice;
+    p.cg = c.cg;
+    p.gather_bytes = c.gather_bytes;
+    if (!dense) {
+        NRS_ARG_CHECK(c.cg.P >= 1 && c.cg.P <= INT32_MAX && c.cg.ow >= 1 && c.cg.ow <= INT32_MAX &&
+                          K <= INT32_MAX,
+                      "gemm: convolution geometry out of range");
+        p.cg.div_P = make_fastdiv((uint32_t)c.cg.P);
+        p.cg.div_ow = make_fastdiv((uint32_t)c.cg.ow);
+    }
+    if (c.nchw_P > 0) {
+        NRS_ARG_CHECK(c.nchw_P <= INT32_MAX, "gemm: NCHW plane too large");
+        p.div_nchw = make_fastdiv((uint32_t)c.nchw_P);
+    }
     NRS_ARG_CHECK((int64_t)p.tiles_m * p.tiles_n <= INT32_MAX && batch <= 65535,
                   "gemm: grid too large");
 
-    KernelFn fn = kernel_for(pl.tile, layout, vec4);
+    KernelFn fn = kernel_for(pl.tile, layout, vec4, c.amode, c.bmode);
+    NRS_ARG_CHECK(fn != nullptr, "gemm: no kernel for layout %d with operand modes %d/%d", layout,
+                  c.amode, c.bmode);
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)pl.slices, (unsigned)batch);
     if (pl.slices > 1) {
         NRS_ARG_CHECK(batch == 1, "gemm: split-K with batch > 1 unsupported");
@@ -181,22 +235,53 @@ extern "C" {
 int nrs_gemm(int layout, float* C, const float* A, const float* B, int64_t rows, int64_t cols,
              int64_t inner, float beta, const float* bias, int epilogue) {
     NRS_REQUIRE_INIT();
-    return nrs::gemm_launch(layout, C, A, B, rows, cols, inner, 1, 0, 0, 0, beta, bias, epilogue,
-                            0, true, 0);
+    nrs::GemmCall c;
+    c.layout = layout;
+    c.C = C;
+    c.A = A;
+    c.B = B;
+    c.M = rows;
+    c.N = cols;
+    c.K = inner;
+    c.beta = beta;
+    c.bias = bias;
+    c.epi = epilogue;
+    return nrs::gemm_run(c);
 }
 
 int nrs_gemm_nt_splitk(float* C, const float* A, const float* B, int64_t rows, int64_t cols,
                        int64_t inner, float beta) {
     NRS_REQUIRE_INIT();
-    return nrs::gemm_launch(NRS_NT, C, A, B, rows, cols, inner, 1, 0, 0, 0, beta, nullptr,
-                            NRS_EPI_NONE, 0, true, 0);
+    nrs::GemmCall c;
+    c.layout = NRS_NT;
+    c.C = C;
+    c.A = A;
+    c.B = B;
+    c.M = rows;
+    c.N = cols;
+    c.K = inner;
+    c.beta = beta;
+    return nrs::gemm_run(c);
 }
 
 int nrs_bmm(int layout, float* C, const float* A, const float* B, int64_t batch, int64_t rows,
             int64_t cols, int64_t inner, float beta) {
     NRS_REQUIRE_INIT();
-    return nrs::gemm_launch(layout, C, A, B, rows, cols, inner, batch, rows * inner,
-                            cols * inner, rows * cols, beta, nullptr, NRS_EPI_NONE, 0, false, 0);
+    nrs::GemmCall c;
+    c.layout = layout;
+    c.C = C;
+    c.A = A;
+    c.B = B;
+    c.M = rows;
+    c.N = cols;
+    c.K = inner;
+    c.batch = batch;
+    c.sA = rows * inner;
+    c.sB = cols * inner;
+    c.sC = rows * cols;
+    c.beta = beta;
+    c.allow_split = false;
+    return nrs::gemm_run(c);
 }
 
 }  // extern "C"

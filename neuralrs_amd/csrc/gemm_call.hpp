@@ -1,0 +1,53 @@
+// Host-facing description of one GEMM launch, shared by the GEMM entry
+// points (gemm.hip) and the convolution lowering (conv.hip).
+#pragma once
+
+#include "fastdiv.hpp"
+#include "nrs_internal.hpp"
+
+namespace nrs {
+
+// Geometry of an implicit-GEMM convolution operand: the NCHW image an
+// operand is read from and the convolution that maps it to GEMM columns
+// (column = img * P + oy * ow + ox, P = oh * ow).
+struct ConvGeom {
+    int64_t C, H, W;            // channels and spatial size of the image read
+    int kh, kw, stride, pad_h, pad_w;
+    int64_t oh, ow, P;          // output spatial size of the convolution
+    FastDiv div_P, div_ow;      // dividers for P and ow (set by gemm_run)
+};
+
+// Operand modes of the GEMM kernel:
+//   OP_DENSE   row-major matrix (leading dimension from the layout);
+//   OP_IM2COL  B only, k-major [k = (ic*kh + i)*kw + j][n = column]: the
+//              im2col matrix of the NCHW image `cg`, gathered on the fly with
+//              zero padding (the column matrix of src/cuda/nn/conv.rs:27-58
+//              without materialising it);
+//   OP_NCHW    A only, reduction-contiguous [m = channel][k = column]: an NCHW
+//              tensor with M channels and cg.P pixels per image, read in place
+//              as the [M, N*P] operand (the out2mm reorder of
+//              src/cuda/nn/conv.rs:94-108 without materialising it).
+enum OperandMode { OP_DENSE = 0, OP_IM2COL = 1, OP_NCHW = 2 };
+
+// C[b] = epi(op(A[b]) op(B[b])) + beta * C[b], b < batch.
+struct GemmCall {
+    int layout = NRS_NN;
+    float* C = nullptr;
+    const float* A = nullptr;
+    const float* B = nullptr;
+    int64_t M = 0, N = 0, K = 0, batch = 1;
+    int64_t sA = 0, sB = 0, sC = 0;  // batch strides in elements
+    float beta = 0.0f;
+    const float* bias = nullptr;
+    int epi = NRS_EPI_NONE;
+    int64_t nchw_P = 0;       // > 0: C is stored NCHW [img][M][nchw_P]
+    bool allow_split = true;  // split-K allowed (batch == 1, row-major C only)
+    int force_slices = 0;
+    int amode = OP_DENSE, bmode = OP_DENSE;
+    ConvGeom cg{};
+    int64_t gather_bytes = 0;  // bytes of the gathered (non-dense) operand's tensor
+};
+
+int gemm_run(const GemmCall& c);
+
+}  // namespace nrs

@@ -30,12 +30,33 @@
 //    keeps the A rows and B columns those tiles share inside that XCD's L2.
 #pragma once
 
-#include "nrs_internal.hpp"
+#include "gemm_call.hpp"
 
 namespace nrs {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Raw buffer resource over `bytes` bytes at `base` (gfx9 descriptor format).
+// A buffer load whose byte offset is >= bytes returns zero in hardware, so a
+// gathered operand needs neither a branch nor a select for its padding: out
+// of range elements use kOutOfRange. The host keeps gathered tensors at most
+// 2 GiB so every valid offset is below kOutOfRange.
+constexpr int kOutOfRange = (int)0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float* base, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0,
+                                             (int)(bytes < 0x80000000ll ? bytes : 0x80000000ll),
+                                             0x00020000);
+}
+
+__device__ __forceinline__ float buffer_load1(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
+}
+
+__device__ __forceinline__ f32x4 buffer_load4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
 
 struct GemmArgs {
     const float* A;
@@ -52,7 +73,12 @@ struct GemmArgs {
     float beta;
     int epi;
     int64_t nchw_P;      // > 0: C is NCHW [N_img][M][P] with column = img*P + p
+    ConvGeom cg;         // operand geometry for the implicit-GEMM operand modes
+    int64_t gather_bytes;  // size of the gathered operand's tensor (<= 2 GiB)
+    FastDiv div_nchw;      // divider for nchw_P
 };
+
+
 
 // v (+bias) (relu) (+ beta*C_old), stored at row-major or NCHW position.
 __device__ __forceinline__ void epilogue_store(const GemmArgs& p, float* C, int64_t row,
@@ -62,8 +88,9 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs& p, float* C, int6
     if (p.epi & NRS_EPI_RELU) v = fmaxf(v, 0.0f);
     int64_t idx;
     if (p.nchw_P > 0) {
-        int64_t img = col / p.nchw_P;
-        idx = (img * p.M + row) * p.nchw_P + (col - img * p.nchw_P);
+        uint32_t img, pc;
+        fast_divmod((uint32_t)col, p.div_nchw, img, pc);
+        idx = ((int64_t)img * p.M + row) * p.nchw_P + pc;
     } else {
         idx = row * p.ldc + col;
     }
@@ -106,39 +133,52 @@ struct Cfg {
     static_assert(2 * STAGE * 4 <= 160 * 1024, "LDS budget");
 };
 
-// Loads the k-tile [k0, k0+BK) of one operand into registers.
+// Position of load q of a k-tile of one operand (same mapping for the global
+// load and the LDS store).
+template <int BMN, int BK, bool KC, int VEC>
+__device__ __forceinline__ void tile_pos(int q, int64_t mn0, int64_t k0, int64_t& mn, int64_t& k) {
+    if (KC) {
+        mn = mn0 + q / (BK / VEC);
+        k = k0 + (q % (BK / VEC)) * VEC;
+    } else {
+        k = k0 + q / (BMN / VEC);
+        mn = mn0 + (q % (BMN / VEC)) * VEC;
+    }
+}
+
+// Loads the k-tile [k0, k0+BK) of one dense operand into registers.
 // KC: reduction dim contiguous (X[mn*ld + k]); else X[k*ld + mn].
+// Out-of-range elements read the operand's first element instead; store_tile
+// replaces them by zero. The loads stay unconditional and their values are
+// not touched until the LDS store, so the compiler waits only for the oldest
+// prefetch slot.
 template <int BMN, int BK, bool KC, int VEC, int LOADS, int NT>
 __device__ __forceinline__ void load_tile(float (&r)[LOADS][VEC], const float* X, int64_t ld,
                                           int64_t mn0, int64_t MN, int64_t k0, int64_t kend,
                                           int tid) {
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-        const int q = tid + i * NT;
         int64_t mn, k;
-        if (KC) {
-            mn = mn0 + q / (BK / VEC);
-            k = k0 + (q % (BK / VEC)) * VEC;
-        } else {
-            k = k0 + q / (BMN / VEC);
-            mn = mn0 + (q % (BMN / VEC)) * VEC;
-        }
-        const bool ok = (mn < MN) && (k < kend);
-        const float* src = KC ? X + mn * ld + k : X + k * ld + mn;
+        tile_pos<BMN, BK, KC, VEC>(tid + i * NT, mn0, k0, mn, k);
+        const bool ok = (mn < MN) & (k < kend);
+        const float* src = ok ? (KC ? X + mn * ld + k : X + k * ld + mn) : X;
         if constexpr (VEC == 4) {
-            const f32x4 v = ok ? *reinterpret_cast<const f32x4*>(src) : f32x4{0.f, 0.f, 0.f, 0.f};
+            const f32x4 v = *reinterpret_cast<const f32x4*>(src);
             r[i][0] = v[0];
             r[i][1] = v[1];
             r[i][2] = v[2];
             r[i][3] = v[3];
         } else {
-            r[i][0] = ok ? *src : 0.0f;
+            r[i][0] = *src;
         }
     }
 }
 
-template <int BMN, int BK, bool KC, int VEC, int LOADS, int S, int NT>
-__device__ __forceinline__ void store_tile(float* s, const float (&r)[LOADS][VEC], int tid) {
+// Stores a k-tile to LDS. MASK: zero the elements load_tile read out of
+// range (dense operands); gathered operands arrive already zero-filled.
+template <int BMN, int BK, bool KC, int VEC, int LOADS, int S, int NT, bool MASK>
+__device__ __forceinline__ void store_tile(float* s, const float (&r)[LOADS][VEC], int tid,
+                                           int64_t mn0, int64_t MN, int64_t k0, int64_t kend) {
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
         const int q = tid + i * NT;
@@ -147,10 +187,17 @@ __device__ __forceinline__ void store_tile(float* s, const float (&r)[LOADS][VEC
             off = (q / (BK / VEC)) * S + (q % (BK / VEC)) * VEC;
         else
             off = (q / (BMN / VEC)) * S + (q % (BMN / VEC)) * VEC;
+        bool ok = true;
+        if constexpr (MASK) {
+            int64_t mn, k;
+            tile_pos<BMN, BK, KC, VEC>(q, mn0, k0, mn, k);
+            ok = (mn < MN) & (k < kend);
+        }
         if constexpr (VEC == 4) {
-            *reinterpret_cast<f32x4*>(s + off) = f32x4{r[i][0], r[i][1], r[i][2], r[i][3]};
+            *reinterpret_cast<f32x4*>(s + off) =
+                ok ? f32x4{r[i][0], r[i][1], r[i][2], r[i][3]} : f32x4{0.f, 0.f, 0.f, 0.f};
         } else {
-            s[off] = r[i][0];
+            s[off] = ok ? r[i][0] : 0.0f;
         }
     }
 }
@@ -167,16 +214,126 @@ __device__ __forceinline__ f32x4 read_frag(const float* s, int mn, int g, int h)
     }
 }
 
+// OP_IM2COL lane mapping: lane <-> column. A workgroup's BN columns are
+// spread over consecutive lanes and each thread walks k-rows
+// tid / BN + e * (NT / BN), e < BK * BN / NT, so one wave-wide load reads one
+// k-row across BN consecutive output pixels (contiguous input for stride 1)
+// and the k-row, hence its table entry, is the same for the whole wave. The
+// values are kept in the operand's [LOADS][VEC] register slot in flat order
+// e = i * VEC + v.
+struct Im2colCol {
+    int base;  // element offset of (img, channel 0, iy0, ix0) in the tensor
+    int iy0, ix0;
+};
+
+template <int BN>
+__device__ __forceinline__ void im2col_col(Im2colCol& ci, const GemmArgs& p, int64_t n0, int tid) {
+    // 32-bit math: the host keeps N and the gathered tensor below 2^31 elements.
+    const ConvGeom& g = p.cg;
+    const int col = (int)(n0 + tid % BN);
+    if (col < (int)p.N) {
+        uint32_t img, pp, oy, ox;
+        fast_divmod((uint32_t)col, g.div_P, img, pp);
+        fast_divmod(pp, g.div_ow, oy, ox);
+        ci.iy0 = oy * g.stride - g.pad_h;
+        ci.ix0 = ox * g.stride - g.pad_w;
+        ci.base = (int)img * (int)(g.C * g.H * g.W) + ci.iy0 * (int)g.W + ci.ix0;
+    } else {  // out of range: fails every bounds test of load_im2col
+        ci.iy0 = -(1 << 29);
+        ci.ix0 = -(1 << 29);
+        ci.base = 0;
+    }
+}
+
+// Decomposition of reduction index k = (ic*kh + i)*kw + j of an OP_IM2COL
+// operand: x = offset (ic*H + i)*W + j inside one image, y = i | j << 16.
+// Built once per workgroup into LDS for the first kIm2colTable k values, so
+// the k-loop does one LDS read per k-row instead of two integer divisions.
+constexpr int kIm2colTable = 2048;
+
+__device__ __forceinline__ int2 im2col_k_entry(const ConvGeom& g, int k) {
+    const int khkw = g.kh * g.kw;
+    const int ic = k / khkw;
+    const int rem = k - ic * khkw;
+    const int ii = rem / g.kw;
+    const int jj = rem - ii * g.kw;
+    return make_int2((int)(((int64_t)ic * g.H + ii) * g.W + jj), ii | (jj << 16));
+}
+
+// k-tile of an OP_IM2COL operand (k-major, BN columns): element (k, n) is
+// image[img(n), ic(k), iy0(n) + i(k), ix0(n) + j(k)] or 0 outside the image.
+// `ktab` holds im2col_k_entry for k < kIm2colTable (null: compute it).
+template <int BN, int BK, int VEC, int LOADS, int NT>
+__device__ __forceinline__ void load_im2col(float (&r)[LOADS][VEC], __amdgpu_buffer_rsrc_t X,
+                                            const ConvGeom& g, const Im2colCol& ci,
+                                            const int2* ktab, int64_t k0, int64_t kend, int tid) {
+    constexpr int RSTEP = NT / BN;  // k-rows covered by one pass of the workgroup
+    static_assert(NT % BN == 0 && LOADS * VEC * RSTEP == BK, "im2col lane mapping");
+#pragma unroll
+    for (int e = 0; e < LOADS * VEC; ++e) {
+        const int64_t k = k0 + tid / BN + e * RSTEP;
+        const bool kin = k < kend;
+        const int2 t = ktab ? ktab[kin ? (int)k : 0] : im2col_k_entry(g, kin ? (int)k : 0);
+        const int ii = t.y & 0xffff, jj = t.y >> 16;
+        const bool ok = kin & ((unsigned)(ci.iy0 + ii) < (unsigned)g.H) &
+                        ((unsigned)(ci.ix0 + jj) < (unsigned)g.W);
+        r[e / VEC][e % VEC] = buffer_load1(X, ok ? (ci.base + t.x) * 4 : kOutOfRange);
+    }
+}
+
+// LDS store of a k-tile loaded by load_im2col ([k][n] layout, row stride S).
+template <int BN, int BK, int VEC, int LOADS, int S, int NT>
+__device__ __forceinline__ void store_im2col(float* s, const float (&r)[LOADS][VEC], int tid) {
+    constexpr int RSTEP = NT / BN;
+#pragma unroll
+    for (int e = 0; e < LOADS * VEC; ++e)
+        s[(tid / BN + e * RSTEP) * S + tid % BN] = r[e / VEC][e % VEC];
+}
+
+// k-tile of an OP_NCHW operand (reduction-contiguous, BM channels): element
+// (m, k) is T[img(k), m, p(k)] of an NCHW tensor with M channels. With VEC = 4
+// the host guarantees P % 4 == 0, so four consecutive columns never straddle
+// an image and the load is one aligned 128-bit access.
+template <int BM, int BK, int VEC, int LOADS, int NT>
+__device__ __forceinline__ void load_nchw(float (&r)[LOADS][VEC], __amdgpu_buffer_rsrc_t X,
+                                          const FastDiv& divP, int64_t m0, int64_t M, int64_t k0,
+                                          int64_t kend, int tid) {
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int q = tid + i * NT;
+        const int64_t m = m0 + q / (BK / VEC);
+        const int64_t k = k0 + (q % (BK / VEC)) * VEC;
+        const bool ok = (m < M) & (k < kend);
+        uint32_t img, pp;  // the host keeps K = N*P below 2^31
+        fast_divmod((uint32_t)(ok ? k : 0), divP, img, pp);
+        const int off = ok ? (int)((((int64_t)img * M + m) * divP.d + pp) * 4) : kOutOfRange;
+        if constexpr (VEC == 4) {
+            const f32x4 v = buffer_load4(X, off);
+            r[i][0] = v[0];
+            r[i][1] = v[1];
+            r[i][2] = v[2];
+            r[i][3] = v[3];
+        } else {
+            r[i][0] = buffer_load1(X, off);
+        }
+    }
+}
+
 // WPE: minimum waves per SIMD the register allocation must allow.
 // PF: prefetch depth. Global loads for k-tile j go into register slot j % PF
 // and are issued PF tiles before tile j is stored to LDS, so each load has
 // PF tiles of MFMA work to land in (small tiles need PF > 1 to cover HBM
 // latency; the 256x256 tile has enough work per k-tile with PF = 1).
+// AMODE / BMODE: OperandMode of A and B (OP_NCHW needs AK, OP_IM2COL needs
+// !BKC).
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool AK, bool BKC, int VEC, int WPE,
-          int PF = 1>
+          int PF = 1, int AMODE = OP_DENSE, int BMODE = OP_DENSE>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(WPE)))
 void gemm_kernel(GemmArgs p) {
     using C_ = Cfg<BM, BN, BK, WAVES_M, WAVES_N, AK, BKC, VEC>;
+    static_assert(AMODE != OP_IM2COL && BMODE != OP_NCHW, "unsupported operand mode");
+    static_assert(AMODE != OP_NCHW || AK, "OP_NCHW is a reduction-contiguous operand");
+    static_assert(BMODE != OP_IM2COL || !BKC, "OP_IM2COL is a k-major operand");
     constexpr int FM = C_::FM, FN = C_::FN, NT = C_::NT;
     __shared__ __attribute__((aligned(16))) float smem[2 * C_::STAGE];
 
@@ -210,93 +367,181 @@ void gemm_kernel(GemmArgs p) {
     float ra[PF][C_::A_LOADS][VEC];
     float rb[PF][C_::B_LOADS][VEC];
 
+    Im2colCol icol;
+    __shared__ int2 ktab_s[BMODE == OP_IM2COL ? kIm2colTable : 1];
+    const int2* ktab = nullptr;
+    if constexpr (BMODE == OP_IM2COL) {
+        im2col_col<BN>(icol, p, n0, tid);
+        if (p.K <= kIm2colTable) {
+            for (int k = tid; k < (int)p.K; k += NT) ktab_s[k] = im2col_k_entry(p.cg, k);
+            __syncthreads();
+            ktab = ktab_s;
+        }
+    }
+    const __amdgpu_buffer_rsrc_t gather = buffer_rsrc(AMODE == OP_NCHW ? A : B, p.gather_bytes);
+    auto loadA = [&](float (&r)[C_::A_LOADS][VEC], int64_t k0) {
+        if constexpr (AMODE == OP_NCHW)
+            load_nchw<BM, BK, VEC, C_::A_LOADS, NT>(r, gather, p.cg.div_P, m0, p.M, k0, kend, tid);
+        else
+            load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(r, A, p.lda, m0, p.M, k0, kend, tid);
+    };
+    auto storeA = [&](float* dst, const float (&r)[C_::A_LOADS][VEC], int64_t k0) {
+        store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT, AMODE == OP_DENSE>(dst, r, tid, m0,
+                                                                               p.M, k0, kend);
+    };
+    auto storeB = [&](float* dst, const float (&r)[C_::B_LOADS][VEC], int64_t k0) {
+        if constexpr (BMODE == OP_IM2COL)
+            store_im2col<BN, BK, VEC, C_::B_LOADS, C_::SB, NT>(dst, r, tid);
+        else
+            store_tile<BN, BK, BKC, VEC, C_::B_LOADS, C_::SB, NT, true>(dst, r, tid, n0, p.N, k0,
+                                                                         kend);
+    };
+    auto loadB = [&](float (&r)[C_::B_LOADS][VEC], int64_t k0) {
+        if constexpr (BMODE == OP_IM2COL)
+            load_im2col<BN, BK, VEC, C_::B_LOADS, NT>(r, gather, p.cg, icol, ktab, k0, kend, tid);
+        else
+            load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT>(r, B, p.ldb, n0, p.N, k0, kend, tid);
+    };
+
+    // The k-tile count is padded to a multiple of PF (padding tiles load as
+    // zeros), and every iteration stores and prefetches unconditionally (the
+    // loads past the end are masked): the loop body is straight-line, so the
+    // compiler can count the loads in flight and wait only for the slot it
+    // stores, PF tiles after issuing it.
     const int ntiles = kend > kbeg ? (int)((kend - kbeg + BK - 1) / BK) : 0;
-    if (ntiles > 0) {
-        load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(ra[0], A, p.lda, m0, p.M, kbeg, kend, tid);
-        load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT>(rb[0], B, p.ldb, n0, p.N, kbeg, kend, tid);
-        store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT>(smem, ra[0], tid);
-        store_tile<BN, BK, BKC, VEC, C_::B_LOADS, C_::SB, NT>(smem + C_::A_ELEMS, rb[0], tid);
+    const int nt = (ntiles + PF - 1) / PF * PF;
+    if (nt > 0) {
+        loadA(ra[0], kbeg);
+        loadB(rb[0], kbeg);
+        storeA(smem, ra[0], kbeg);
+        storeB(smem + C_::A_ELEMS, rb[0], kbeg);
 #pragma unroll
         for (int j = 1; j <= PF; ++j) {
-            if (j < ntiles) {
-                const int64_t kj = kbeg + (int64_t)j * BK;
-                load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(ra[j % PF], A, p.lda, m0, p.M, kj, kend, tid);
-                load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT>(rb[j % PF], B, p.ldb, n0, p.N, kj, kend, tid);
-            }
+            const int64_t kj = kbeg + (int64_t)j * BK;
+            loadA(ra[j % PF], kj);
+            loadB(rb[j % PF], kj);
         }
         __syncthreads();
     }
 
     // The loop is unrolled by PF so every register-slot index is a constant.
-    for (int t0 = 0; t0 < ntiles; t0 += PF) {
+    for (int t0 = 0; t0 < nt; t0 += PF) {
 #pragma unroll
         for (int u = 0; u < PF; ++u) {
             const int t = t0 + u;
-            if (t < ntiles) {
-                const float* sA = smem + (t & 1) * C_::STAGE;
-                const float* sB = sA + C_::A_ELEMS;
+            const float* sA = smem + (t & 1) * C_::STAGE;
+            const float* sB = sA + C_::A_ELEMS;
 #pragma unroll
-                for (int g = 0; g < BK / 8; ++g) {
-                    f32x4 af[FM], bf[FN];
+            for (int g = 0; g < BK / 8; ++g) {
+                f32x4 af[FM], bf[FN];
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+                    af[i] = read_frag<AK, C_::SA>(sA, wm0 + 32 * i + l32, g, h);
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    bf[j] = read_frag<BKC, C_::SB>(sB, wn0 + 32 * j + l32, g, h);
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
 #pragma unroll
                     for (int i = 0; i < FM; ++i)
-                        af[i] = read_frag<AK, C_::SA>(sA, wm0 + 32 * i + l32, g, h);
 #pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        bf[j] = read_frag<BKC, C_::SB>(sB, wn0 + 32 * j + l32, g, h);
-#pragma unroll
-                    for (int s = 0; s < 4; ++s)
-#pragma unroll
-                        for (int i = 0; i < FM; ++i)
-#pragma unroll
-                            for (int j = 0; j < FN; ++j)
-                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s],
-                                                                                acc[i][j], 0, 0, 0);
-                }
-                if (t + 1 < ntiles) {
-                    const int slot = (u + 1) % PF;
-                    float* dA = smem + ((t + 1) & 1) * C_::STAGE;
-                    store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT>(dA, ra[slot], tid);
-                    store_tile<BN, BK, BKC, VEC, C_::B_LOADS, C_::SB, NT>(dA + C_::A_ELEMS, rb[slot], tid);
-                    if (t + 1 + PF < ntiles) {
-                        const int64_t kn = kbeg + (int64_t)(t + 1 + PF) * BK;
-                        load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(ra[slot], A, p.lda, m0, p.M, kn, kend, tid);
-                        load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT>(rb[slot], B, p.ldb, n0, p.N, kn, kend, tid);
-                    }
-                }
-                __syncthreads();
+                        for (int j = 0; j < FN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s],
+                                                                            acc[i][j], 0, 0, 0);
             }
+            // Tile t+1 goes to the other LDS buffer (after the last tile this
+            // writes a buffer nobody reads), then its slot is refilled with
+            // tile t+1+PF.
+            const int slot = (u + 1) % PF;
+            float* dA = smem + ((t + 1) & 1) * C_::STAGE;
+            const int64_t ks = kbeg + (int64_t)(t + 1) * BK;
+            storeA(dA, ra[slot], ks);
+            storeB(dA + C_::A_ELEMS, rb[slot], ks);
+            const int64_t kn = kbeg + (int64_t)(t + 1 + PF) * BK;
+            loadA(ra[slot], kn);
+            loadB(rb[slot], kn);
+            __syncthreads();
         }
     }
 
     // Accumulator (i, j) element r of this lane is C[row, col] with
     // row = 32i + 8(r/4) + 4h + r%4, col = 32j + lane%32 inside the wave tile.
+    // Every output column gets one base offset and a row stride, so element
+    // (row, col) lands at base + row * stride: row-major C has base = col and
+    // stride = ldc; NCHW C has base = img*M*P + (col - img*P) and stride = P;
+    // split-K partials are row-major [M][N] per slice. The options (bias,
+    // ReLU, beta) and the bounds tests are uniform per workgroup and hoisted
+    // out of the element loop.
+    const bool full = (m0 + BM <= p.M) && (n0 + BN <= p.N);
+    const bool plain = p.partial != nullptr || (p.epi == NRS_EPI_NONE && p.beta == 0.0f);
+    float* out;
+    int64_t stride;
     if (p.partial) {
-        float* P = p.partial + (int64_t)slice * p.M * p.N;
+        out = p.partial + (int64_t)slice * p.M * p.N;
+        stride = p.N;
+    } else {
+        out = p.C + batch * p.sC;
+        stride = p.nchw_P > 0 ? p.nchw_P : p.ldc;
+    }
+    int64_t cbase[FN];
+    bool colok[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int64_t col = n0 + wn0 + 32 * j + l32;
+        colok[j] = col < p.N;
+        if (p.partial == nullptr && p.nchw_P > 0) {
+            uint32_t img, pc;  // N < 2^31 (checked on the host)
+            fast_divmod((uint32_t)col, p.div_nchw, img, pc);
+            cbase[j] = (int64_t)img * p.M * p.nchw_P + pc;
+        } else {
+            cbase[j] = col;
+        }
+    }
+    const int64_t row0 = m0 + wm0 + 4 * h;  // row of element r = 0 of fragment i = 0
+    if (plain && full) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                const int64_t col = n0 + wn0 + 32 * j + l32;
+                float* dst = out + cbase[j] + (row0 + 32 * i) * stride;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int64_t row = m0 + wm0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (row < p.M && col < p.N) P[row * p.N + col] = acc[i][j][r];
-                }
+                for (int r = 0; r < 16; ++r) dst[(8 * (r >> 2) + (r & 3)) * stride] = acc[i][j][r];
             }
     } else {
-        float* C = p.C + batch * p.sC;
+        const bool bias_col = !p.partial && (p.epi & NRS_EPI_BIAS_COL);
+        const bool bias_row = !p.partial && (p.epi & NRS_EPI_BIAS_ROW);
+        const bool relu = !p.partial && (p.epi & NRS_EPI_RELU);
+        const float beta = p.partial ? 0.0f : p.beta;
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+        for (int j = 0; j < FN; ++j) {
+            const float bc = (bias_col && colok[j]) ? p.bias[n0 + wn0 + 32 * j + l32] : 0.0f;
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int64_t col = n0 + wn0 + 32 * j + l32;
+            for (int i = 0; i < FM; ++i) {
+                // All 16 old values of the fragment are read before any is
+                // used, so their loads overlap.
+                float old[16];
+                if (beta != 0.0f) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int64_t row = row0 + 32 * i + 8 * (r >> 2) + (r & 3);
+                        const bool ok = colok[j] & (row < p.M);
+                        old[r] = ok ? out[cbase[j] + row * stride] : 0.0f;
+                    }
+                }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int64_t row = m0 + wm0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (row < p.M && col < p.N) epilogue_store(p, C, row, col, acc[i][j][r]);
+                    const int64_t row = row0 + 32 * i + 8 * (r >> 2) + (r & 3);
+                    if (colok[j] && row < p.M) {
+                        float v = acc[i][j][r];
+                        if (bias_col) v += bc;
+                        if (bias_row) v += p.bias[row];
+                        if (relu) v = fmaxf(v, 0.0f);
+                        if (beta != 0.0f) v = v + beta * old[r];
+                        out[cbase[j] + row * stride] = v;
+                    }
                 }
             }
+        }
     }
 }
 

@@ -20,6 +20,13 @@ CONV_SHAPES = [  # (n, c_in, c_out, h, w, kh, kw, stride, pad)
     (2, 2, 2, 7, 9, 3, 3, 3, 2),
     (4, 16, 32, 12, 12, 3, 3, 1, 1),
     (1, 1, 1, 3, 3, 3, 3, 1, 0),
+    (2, 2, 3, 6, 6, 2, 2, 1, 2),     # stride 1, pad > k-1: explicit input-gradient path
+    (2, 4, 8, 10, 12, 3, 5, 1, 1),   # kh != kw: flipped-weight padding differs per axis
+    # c_in > 4 and more than 32 taps: implicit-GEMM forward and input gradient
+    (2, 6, 5, 9, 9, 3, 3, 1, 1),
+    (2, 5, 4, 8, 6, 3, 2, 1, 0),
+    (1, 8, 3, 7, 7, 3, 3, 2, 1),     # stride 2: explicit input-gradient path
+    (2, 7, 9, 11, 13, 5, 5, 1, 2),   # 5x5, pad 2, ragged sizes
 ]
 ids = ["x".join(map(str, s)) for s in CONV_SHAPES]
 
@@ -206,7 +213,7 @@ def test_accumulate_vadd_bias_add_sum_axis0(hip, orc):
 
 
 @pytest.mark.parametrize("dims", [(2, 3, 6, 8, 2, 2), (128, 32, 28, 28, 2, 2), (1, 2, 7, 7, 3, 2),
-                                  (2, 1, 5, 5, 2, 1)])
+                                  (2, 1, 5, 5, 2, 1), (3, 2, 7, 9, 2, 2)])
 def test_maxpool_bit_exact(hip, orc, dims):
     n, c, h, w, k, s = dims
     rng = np.random.default_rng(sum(dims))
