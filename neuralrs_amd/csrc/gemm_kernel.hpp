@@ -174,25 +174,41 @@ __device__ __forceinline__ void load_tile(float (&r)[LOADS][VEC], const float* X
     }
 }
 
+// Bit i set: load i of this thread (see tile_pos) lies in the operand's
+// [0, MN) rows/columns. Fixed for the whole k loop, so computed once.
+template <int BMN, int BK, bool KC, int VEC, int LOADS, int NT>
+__device__ __forceinline__ uint32_t tile_mn_bits(int64_t mn0, int64_t MN, int tid) {
+    static_assert(LOADS <= 32, "mask bits");
+    uint32_t bits = 0;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        int64_t mn, k;
+        tile_pos<BMN, BK, KC, VEC>(tid + i * NT, mn0, 0, mn, k);
+        bits |= (uint32_t)(mn < MN) << i;
+    }
+    return bits;
+}
+
 // Stores a k-tile to LDS. MASK: zero the elements load_tile read out of
-// range (dense operands); gathered operands arrive already zero-filled.
+// range (dense operands; gathered operands arrive already zero-filled):
+// load i is in range iff bit i of mn_bits is set and its k offset inside the
+// tile is below krem = kend - k0.
 template <int BMN, int BK, bool KC, int VEC, int LOADS, int S, int NT, bool MASK>
 __device__ __forceinline__ void store_tile(float* s, const float (&r)[LOADS][VEC], int tid,
-                                           int64_t mn0, int64_t MN, int64_t k0, int64_t kend) {
+                                           uint32_t mn_bits, int64_t krem) {
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
         const int q = tid + i * NT;
-        int off;
-        if (KC)
+        int off, kofs;
+        if (KC) {
             off = (q / (BK / VEC)) * S + (q % (BK / VEC)) * VEC;
-        else
+            kofs = (q % (BK / VEC)) * VEC;
+        } else {
             off = (q / (BMN / VEC)) * S + (q % (BMN / VEC)) * VEC;
-        bool ok = true;
-        if constexpr (MASK) {
-            int64_t mn, k;
-            tile_pos<BMN, BK, KC, VEC>(q, mn0, k0, mn, k);
-            ok = (mn < MN) & (k < kend);
+            kofs = q / (BMN / VEC);
         }
+        bool ok = true;
+        if constexpr (MASK) ok = ((mn_bits >> i) & 1u) & (kofs < krem);
         if constexpr (VEC == 4) {
             *reinterpret_cast<f32x4*>(s + off) =
                 ok ? f32x4{r[i][0], r[i][1], r[i][2], r[i][3]} : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -385,16 +401,18 @@ void gemm_kernel(GemmArgs p) {
         else
             load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(r, A, p.lda, m0, p.M, k0, kend, tid);
     };
+    const uint32_t a_bits = tile_mn_bits<BM, BK, AK, VEC, C_::A_LOADS, NT>(m0, p.M, tid);
+    const uint32_t b_bits = tile_mn_bits<BN, BK, BKC, VEC, C_::B_LOADS, NT>(n0, p.N, tid);
     auto storeA = [&](float* dst, const float (&r)[C_::A_LOADS][VEC], int64_t k0) {
-        store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT, AMODE == OP_DENSE>(dst, r, tid, m0,
-                                                                               p.M, k0, kend);
+        store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT, AMODE == OP_DENSE>(dst, r, tid, a_bits,
+                                                                               kend - k0);
     };
     auto storeB = [&](float* dst, const float (&r)[C_::B_LOADS][VEC], int64_t k0) {
         if constexpr (BMODE == OP_IM2COL)
             store_im2col<BN, BK, VEC, C_::B_LOADS, C_::SB, NT>(dst, r, tid);
         else
-            store_tile<BN, BK, BKC, VEC, C_::B_LOADS, C_::SB, NT, true>(dst, r, tid, n0, p.N, k0,
-                                                                         kend);
+            store_tile<BN, BK, BKC, VEC, C_::B_LOADS, C_::SB, NT, true>(dst, r, tid, b_bits,
+                                                                         kend - k0);
     };
     auto loadB = [&](float (&r)[C_::B_LOADS][VEC], int64_t k0) {
         if constexpr (BMODE == OP_IM2COL)
