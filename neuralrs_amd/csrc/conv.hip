@@ -26,6 +26,7 @@
 //    replacing the reference's three accumulate passes.
 #include <algorithm>
 
+#include "conv_slab.hpp"
 #include "gemm_call.hpp"
 
 namespace nrs {
@@ -466,6 +467,34 @@ int launch_out2mm(float* mm, const float* grad, const ConvDims& d) {
     return NRS_OK;
 }
 
+// dinput += the stride-1 input gradient as a slab convolution of the output
+// gradient with the flipped, channel-transposed weights (padding k-1-pad).
+int slab_dgrad(float* dinput, const float* grad, const float* weight, int64_t N, int64_t c_in,
+               int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw, int64_t pad,
+               const ConvDims& d) {
+    if (c_in > INT32_MAX || c_out > INT32_MAX || in_h > INT32_MAX || in_w > INT32_MAX)
+        return kSlabUnsupported;
+    SlabConv s;
+    s.x = grad;
+    s.w = weight;
+    s.out = dinput;
+    s.N = N;
+    s.C = (int)c_out;
+    s.H = (int)d.out_h;
+    s.W = (int)d.out_w;
+    s.M = (int)c_in;
+    s.kh = (int)kh;
+    s.kw = (int)kw;
+    s.stride = 1;
+    s.pad_h = (int)(kh - 1 - pad);
+    s.pad_w = (int)(kw - 1 - pad);
+    s.OH = (int)in_h;
+    s.OW = (int)in_w;
+    s.flip = true;
+    s.beta = 1.0f;
+    return slab_conv(s);
+}
+
 }  // namespace
 }  // namespace nrs
 
@@ -545,6 +574,29 @@ int nrs_conv2d_forward(float* out, const float* input, const float* weight, cons
         NRS_LAUNCH_CHECK("conv2d forward (direct)");
         return NRS_OK;
     }
+    {
+        // input slab and weights staged in LDS, reduction on the matrix cores
+        nrs::SlabConv s;
+        s.x = input;
+        s.w = weight;
+        s.bias = bias;
+        s.out = out;
+        s.N = N;
+        s.C = (int)c_in;
+        s.H = (int)in_h;
+        s.W = (int)in_w;
+        s.M = (int)c_out;
+        s.kh = (int)kh;
+        s.kw = (int)kw;
+        s.stride = (int)stride;
+        s.pad_h = s.pad_w = (int)pad;
+        s.OH = (int)d.out_h;
+        s.OW = (int)d.out_w;
+        if (c_out <= INT32_MAX && d.out_h <= INT32_MAX && d.out_w <= INT32_MAX) {
+            rc = nrs::slab_conv(s);
+            if (rc != nrs::kSlabUnsupported) return rc;
+        }
+    }
     if (N * c_in * in_h * in_w * (int64_t)sizeof(float) <= nrs::kMaxGatherBytes) {
         // out(NCHW) = W[c_out, c_in*kh*kw] . im2col(input) + bias[oc], the
         // column matrix gathered inside the GEMM (conv.rs:266-277 without the
@@ -599,6 +651,11 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
                                (int)d.out_w, nrs::make_fastdiv((uint32_t)(in_h * in_w)),
                                nrs::make_fastdiv((uint32_t)in_w), 1.0f);
             NRS_LAUNCH_CHECK("conv2d input gradient (direct)");
+        } else if (stride == 1 && pad <= kh - 1 && pad <= kw - 1 &&
+                   (rc = slab_dgrad(dinput, grad, weight, N, c_in, in_h, in_w, c_out, kh, kw,
+                                    pad, d)) != nrs::kSlabUnsupported) {
+            // dinput += conv(grad, flipped W) with padding k-1-pad, staged in LDS
+            if (rc) return rc;
         } else if (stride == 1 && pad <= kh - 1 && pad <= kw - 1 &&
                    grad_bytes <= nrs::kMaxGatherBytes) {
             // dinput += conv(grad, flipped W) with padding k-1-pad: the

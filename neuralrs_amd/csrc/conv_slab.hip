@@ -1,0 +1,391 @@
+// Slab-resident convolution on the f32 matrix cores (v_mfma_f32_16x16x4f32).
+//
+// The implicit GEMM of src/cuda/nn/conv.rs:266-277 (forward) and of the
+// stride-1 input gradient (conv.rs:304-312 as a convolution of the output
+// gradient with flipped weights) without a column matrix and without global
+// loads inside the reduction: each workgroup owns one image, a band of `band`
+// consecutive output pixels and BM output channels. Per chunk of CC input
+// channels it stages
+//   * the input slab: every input row the band's windows touch, full padded
+//     width, zero outside the image, pixel-major with the chunk's channels
+//     contiguous ([row][col][CC + 4 pad]);
+//   * the weight block: [BM][kh*kw][CC] (+4 pad per row), flipped and
+//     channel-transposed on the fly for the input gradient;
+// once into LDS, then runs the whole chunk's reduction from LDS.
+//
+// MFMA mapping (16x16x4): A = weights (rows = output channels), B = slab
+// windows (columns = output pixels). Lane l supplies A[m = l%16][k = l/16]
+// and B[k = l/16][n = l%16]; the four lane quarters q = l/16 take channel
+// quarters (channel = q*CC/4 + j at step j) of the same tap, so both operands
+// come from one 128-bit LDS read per four steps: the four channels are
+// contiguous in both layouts, and every address offset inside the loop is
+// uniform across the wavefront. Lane l's accumulator holds
+// D[m = 4*(l/16) + r][n = l%16], r < 4.
+//
+// The summation order per output is taps outer, channels inner (the
+// reference sums channel-major); results agree to f32 rounding.
+#include <algorithm>
+
+#include "conv_slab.hpp"
+
+namespace nrs {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct SlabArgs {
+    const float* x;
+    const float* w;
+    const float* bias;
+    float* out;
+    int C, H, W, M, kh, kw, taps, stride, pad_h, pad_w, OW, P;
+    const float* wpack;    // weights packed per (chunk, channel block) in LDS layout
+    int nblk;              // output-channel blocks (gridDim.y)
+    float beta;
+    int CC, CC4;           // channels per chunk (multiple of 16) and CC / 4
+    int band;              // output pixels per band
+    int slab_rows, slab_w; // LDS slab rows reserved and columns
+    int ps, wrow;          // LDS floats per slab pixel and per weight row
+    int x_items, w_items;  // staging items per chunk: 4-channel slab pixels, weight float4s
+    FastDiv div_bands, div_ow, div_psn, div_slab_w;
+};
+
+constexpr int kStageBatch = 8;    // input-slab items (4 loads each) per thread per batch
+constexpr int kWeightBatch = 16;  // weight float4s per thread per batch
+
+template <int WM, int WN, int MSW, int NSW>
+struct SlabCfg {
+    static constexpr int NT = 64 * WM * WN;
+    static constexpr int BM = 16 * WM * MSW;  // output channels per workgroup
+    static constexpr int BN = 16 * WN * NSW;  // output pixels per workgroup (max band)
+};
+
+// Two waves per SIMD: the LDS budget targets two workgroups per CU, and the
+// 256-VGPR cap keeps the accumulators in place in VGPRs.
+template <int WM, int WN, int MSW, int NSW>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2)))
+void conv_slab_kernel(SlabArgs a) {
+    using Cfg = SlabCfg<WM, WN, MSW, NSW>;
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    // the wave index is uniform; readfirstlane lets the compiler know, so
+    // per-wave conditions below are scalar branches
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % WM, wn = wave / WM;
+    const int q = lane >> 4, l16 = lane & 15;
+
+    uint32_t img, bi;
+    fast_divmod(blockIdx.x, a.div_bands, img, bi);
+    const int m0 = blockIdx.y * Cfg::BM;
+    const int p0 = (int)bi * a.band;
+    const int p_end = min(p0 + a.band, a.P);
+    const int oy_first = (int)fast_div((uint32_t)p0, a.div_ow);
+    const int oy_last = (int)fast_div((uint32_t)(p_end - 1), a.div_ow);
+    const int rows = (oy_last - oy_first) * a.stride + a.kh;
+    const int iy0 = oy_first * a.stride - a.pad_h;
+    const int HW = a.H * a.W;
+    float* xs = lds;
+    float* ws = lds + a.slab_rows * a.slab_w * a.ps;
+    const int CQ = a.CC4;  // channels per lane quarter
+
+    // per-lane slab offsets of this wave's pixel columns (masked pixels read
+    // row 0, which is always staged)
+    int poff[NSW];
+#pragma unroll
+    for (int t = 0; t < NSW; ++t) {
+        const int p = p0 + 16 * (wn * NSW + t) + l16;
+        int o = 0;
+        if (p < p_end) {
+            uint32_t oy, ox;
+            fast_divmod((uint32_t)p, a.div_ow, oy, ox);
+            o = (((int)oy - oy_first) * a.stride * a.slab_w + (int)ox * a.stride) * a.ps;
+        }
+        poff[t] = o + q * CQ;
+    }
+    int aoff[MSW];
+#pragma unroll
+    for (int ms = 0; ms < MSW; ++ms) aoff[ms] = (16 * (wm * MSW + ms) + l16) * a.wrow + q * CQ;
+
+    f32x4 acc[MSW][NSW];
+#pragma unroll
+    for (int ms = 0; ms < MSW; ++ms)
+#pragma unroll
+        for (int t = 0; t < NSW; ++t) acc[ms][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const float* ximg = a.x + (int64_t)img * a.C * HW;
+    for (int c0 = 0; c0 < a.C; c0 += a.CC) {
+        if (c0) __syncthreads();  // the previous chunk's reads are done
+        // Staging runs in batches of kStageBatch items per thread: all loads
+        // of a batch are issued before its LDS stores, so a thread waits for
+        // global memory once per batch rather than once per item.
+        // Input slab: item = (channel quad, slab pixel), pixels fastest so
+        // consecutive lanes read consecutive input columns.
+        for (int base = tid; base < a.x_items; base += Cfg::NT * kStageBatch) {
+            f32x4 v[kStageBatch];
+            int dst[kStageBatch];
+#pragma unroll
+            for (int b = 0; b < kStageBatch; ++b) {
+                const int idx = base + b * Cfg::NT;
+                uint32_t c4, pos, r, col;
+                fast_divmod((uint32_t)min(idx, a.x_items - 1), a.div_psn, c4, pos);
+                fast_divmod(pos, a.div_slab_w, r, col);
+                const bool live = (idx < a.x_items) & ((int)r < rows);
+                const int iy = iy0 + (int)r, ix = (int)col - a.pad_w;
+                const bool in = live & ((unsigned)iy < (unsigned)a.H) & ((unsigned)ix < (unsigned)a.W);
+                const int c = c0 + 4 * (int)c4;
+                const float* src = ximg + (int64_t)c * HW + iy * a.W + ix;
+                // branch-free: masked lanes load the image's first element
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const bool ok = in & (c + u < a.C);
+                    const float t = *(ok ? src + u * HW : ximg);
+                    v[b][u] = ok ? t : 0.0f;
+                }
+                dst[b] = live ? (int)(pos * a.ps + 4 * c4) : -1;
+            }
+#pragma unroll
+            for (int b = 0; b < kStageBatch; ++b)
+                if (dst[b] >= 0) *reinterpret_cast<f32x4*>(xs + dst[b]) = v[b];
+        }
+        // Weight block: a straight copy of its packed LDS image.
+        {
+            const f32x4* src = reinterpret_cast<const f32x4*>(
+                a.wpack + ((int64_t)(c0 / a.CC) * a.nblk + blockIdx.y) * Cfg::BM * a.wrow);
+            f32x4* dst = reinterpret_cast<f32x4*>(ws);
+            for (int base = tid; base < a.w_items; base += Cfg::NT * kWeightBatch) {
+                f32x4 v[kWeightBatch];
+#pragma unroll
+                for (int b = 0; b < kWeightBatch; ++b)
+                    v[b] = src[min(base + b * Cfg::NT, a.w_items - 1)];
+#pragma unroll
+                for (int b = 0; b < kWeightBatch; ++b)
+                    if (base + b * Cfg::NT < a.w_items) dst[base + b * Cfg::NT] = v[b];
+            }
+        }
+        __syncthreads();
+
+        // The reduction runs over (tap, 4-channel group) steps; the operands
+        // of step it+1 are read from LDS while step it's MFMAs issue. The
+        // read after the last step goes to offset 0 (in bounds, unused).
+        const int steps = a.taps * (CQ / 4);
+        int tap = 0, j4 = 0, i = 0, j = 0;
+        int woff = 0, toff = 0;
+        f32x4 av[MSW], bv[NSW];
+#pragma unroll
+        for (int ms = 0; ms < MSW; ++ms)
+            av[ms] = *reinterpret_cast<const f32x4*>(ws + aoff[ms]);
+#pragma unroll
+        for (int t = 0; t < NSW; ++t) bv[t] = *reinterpret_cast<const f32x4*>(xs + poff[t]);
+        for (int it = 0; it < steps; ++it) {
+            j4 += 4;
+            if (j4 == CQ) {
+                j4 = 0;
+                ++tap;
+                if (++j == a.kw) {
+                    j = 0;
+                    ++i;
+                }
+            }
+            const bool more = it + 1 < steps;
+            woff = more ? tap * a.CC + j4 : 0;
+            toff = more ? (i * a.slab_w + j) * a.ps + j4 : 0;
+            f32x4 an[MSW], bn[NSW];
+#pragma unroll
+            for (int ms = 0; ms < MSW; ++ms)
+                an[ms] = *reinterpret_cast<const f32x4*>(ws + aoff[ms] + woff);
+#pragma unroll
+            for (int t = 0; t < NSW; ++t)
+                bn[t] = *reinterpret_cast<const f32x4*>(xs + poff[t] + toff);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int ms = 0; ms < MSW; ++ms)
+#pragma unroll
+                    for (int t = 0; t < NSW; ++t)
+                        acc[ms][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[ms][s], bv[t][s],
+                                                                          acc[ms][t], 0, 0, 0);
+#pragma unroll
+            for (int ms = 0; ms < MSW; ++ms) av[ms] = an[ms];
+#pragma unroll
+            for (int t = 0; t < NSW; ++t) bv[t] = bn[t];
+        }
+    }
+
+    // epilogue: NCHW store, + bias, + beta * out
+    float* oimg = a.out + (int64_t)img * a.M * a.P;
+#pragma unroll
+    for (int ms = 0; ms < MSW; ++ms)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int oc = m0 + 16 * (wm * MSW + ms) + 4 * q + r;
+            if (oc >= a.M) continue;
+            const float b = a.bias ? a.bias[oc] : 0.0f;
+#pragma unroll
+            for (int t = 0; t < NSW; ++t) {
+                const int p = p0 + 16 * (wn * NSW + t) + l16;
+                if (p >= p_end) continue;
+                float* dst = oimg + (int64_t)oc * a.P + p;
+                float v = acc[ms][t][r] + b;
+                if (a.beta != 0.0f) v = v + a.beta * *dst;
+                *dst = v;
+            }
+        }
+}
+
+// Packs the weights of a slab convolution into the LDS image the kernel
+// stages: packed[((chunk * nblk + blk) * BM + m) * wrow + tap * CC + c] =
+// weight (m0 + m, c0 + c, tap), zero outside the tensor and in the row pad,
+// with m0 = blk * BM, c0 = chunk * CC. The weight element (m, c, tap) is
+// w[m][c][tap] forward and w[c][m][taps-1-tap] for the input gradient.
+__global__ __launch_bounds__(256) void pack_slab_weights_kernel(
+    float* __restrict__ packed, const float* __restrict__ w, int C, int M, int taps, int CC,
+    int BM, int nblk, int wrow, int flip, int total) {
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+        const int row = e / wrow, col = e - row * wrow;
+        const int cb = row / BM, m = row - cb * BM;
+        const int chunk = cb / nblk, blk = cb - chunk * nblk;
+        const int tap = col / CC, c = col - tap * CC;
+        const int mg = blk * BM + m, cg = chunk * CC + c;
+        float v = 0.0f;
+        if (tap < taps && mg < M && cg < C)
+            v = flip ? w[((int64_t)cg * M + mg) * taps + (taps - 1 - tap)]
+                     : w[((int64_t)mg * C + cg) * taps + tap];
+        packed[e] = v;
+    }
+}
+
+constexpr int kLdsBytes = 160 * 1024;
+
+int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// Launch geometry of one configuration: bands, slab size, channel chunk and
+// LDS bytes (0 when the configuration cannot take the convolution).
+struct SlabPlan {
+    int64_t band = 0, nb = 0, slab_rows = 0, slab_w = 0, CC = 0;
+    size_t lds = 0;
+};
+
+template <int WM, int WN, int MSW, int NSW>
+SlabPlan plan_slab(const SlabConv& s) {
+    using Cfg = SlabCfg<WM, WN, MSW, NSW>;
+    SlabPlan pl;
+    const int64_t P = (int64_t)s.OH * s.OW, taps = (int64_t)s.kh * s.kw;
+    const int64_t bands = (P + Cfg::BN - 1) / Cfg::BN;
+    pl.band = std::min<int64_t>(Cfg::BN, round_up((P + bands - 1) / bands, 16));
+    pl.nb = (P + pl.band - 1) / pl.band;
+    // input rows the windows of one band touch: exact maximum over the bands
+    // when there are few, else the bound for a band starting anywhere
+    int64_t out_rows = std::min<int64_t>(s.OH, (pl.band - 1 + s.OW - 1) / s.OW + 1);
+    if (pl.nb <= 4096) {
+        out_rows = 0;
+        for (int64_t b = 0; b < pl.nb; ++b) {
+            const int64_t p0 = b * pl.band, p1 = std::min(p0 + pl.band, P) - 1;
+            out_rows = std::max(out_rows, p1 / s.OW - p0 / s.OW + 1);
+        }
+    }
+    pl.slab_rows = (out_rows - 1) * s.stride + s.kh;
+    pl.slab_w = (int64_t)(s.OW - 1) * s.stride + s.kw;
+    // the largest channel chunk (multiple of 16) whose slab and weights fit
+    auto bytes = [&](int64_t cc) {
+        return 4 * (pl.slab_rows * pl.slab_w * (cc + 4) + Cfg::BM * (taps * cc + 4));
+    };
+    int64_t CC = round_up(s.C, 16);
+    while (CC > 16 && bytes(CC) > kLdsBytes) CC -= 16;
+    const int64_t grid_x = s.N * pl.nb, grid_y = (s.M + Cfg::BM - 1) / Cfg::BM;
+    if (bytes(CC) > kLdsBytes || grid_x > INT32_MAX || grid_y > 65535 ||
+        pl.slab_rows * pl.slab_w * (CC / 4) > INT32_MAX / 2 ||
+        Cfg::BM * taps * CC > INT32_MAX / 2)
+        return SlabPlan{};
+    pl.CC = CC;
+    pl.lds = (size_t)bytes(CC);
+    return pl;
+}
+
+template <int WM, int WN, int MSW, int NSW>
+int launch_slab(const SlabConv& s, const SlabPlan& pl) {
+    using Cfg = SlabCfg<WM, WN, MSW, NSW>;
+    const int64_t P = (int64_t)s.OH * s.OW, taps = (int64_t)s.kh * s.kw;
+    SlabArgs a;
+    a.x = s.x;
+    a.w = s.w;
+    a.bias = s.bias;
+    a.out = s.out;
+    a.C = s.C;
+    a.H = s.H;
+    a.W = s.W;
+    a.M = s.M;
+    a.kh = s.kh;
+    a.kw = s.kw;
+    a.taps = (int)taps;
+    a.stride = s.stride;
+    a.pad_h = s.pad_h;
+    a.pad_w = s.pad_w;
+    a.OW = s.OW;
+    a.P = (int)P;
+    const int64_t nblk = (s.M + Cfg::BM - 1) / Cfg::BM, nchunk = (s.C + pl.CC - 1) / pl.CC;
+    const int64_t wrow = taps * pl.CC + 4, packed_n = nchunk * nblk * Cfg::BM * wrow;
+    if (packed_n > INT32_MAX) return kSlabUnsupported;
+    float* packed = workspace(sizeof(float) * (size_t)packed_n, 4);
+    if (!packed) return NRS_ERR_ALLOC;
+    hipLaunchKernelGGL(pack_slab_weights_kernel,
+                       dim3((unsigned)std::min<int64_t>((packed_n + 255) / 256, 4096)), dim3(256),
+                       0, stream(), packed, s.w, s.C, s.M, (int)taps, (int)pl.CC, Cfg::BM,
+                       (int)nblk, (int)wrow, s.flip ? 1 : 0, (int)packed_n);
+    NRS_LAUNCH_CHECK("conv2d (slab weight pack)");
+    a.wpack = packed;
+    a.nblk = (int)nblk;
+    a.beta = s.beta;
+    a.CC = (int)pl.CC;
+    a.CC4 = (int)(pl.CC / 4);
+    a.band = (int)pl.band;
+    a.slab_rows = (int)pl.slab_rows;
+    a.slab_w = (int)pl.slab_w;
+    a.ps = (int)(pl.CC + 4);
+    a.wrow = (int)(taps * pl.CC + 4);
+    a.x_items = (int)(pl.slab_rows * pl.slab_w * (pl.CC / 4));
+    a.w_items = (int)(Cfg::BM * wrow / 4);
+    a.div_bands = make_fastdiv((uint32_t)pl.nb);
+    a.div_ow = make_fastdiv((uint32_t)s.OW);
+    a.div_psn = make_fastdiv((uint32_t)(pl.slab_rows * pl.slab_w));
+    a.div_slab_w = make_fastdiv((uint32_t)pl.slab_w);
+
+    auto fn = conv_slab_kernel<WM, WN, MSW, NSW>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        NRS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes));
+        attr_set = true;
+    }
+    const unsigned gx = (unsigned)(s.N * pl.nb), gy = (unsigned)((s.M + Cfg::BM - 1) / Cfg::BM);
+    hipLaunchKernelGGL(fn, dim3(gx, gy), dim3(Cfg::NT), pl.lds, stream(), a);
+    NRS_LAUNCH_CHECK("conv2d (slab)");
+    return NRS_OK;
+}
+
+}  // namespace
+
+int slab_conv(const SlabConv& s) {
+    if (s.N == 0 || s.M == 0 || s.OH == 0 || s.OW == 0) return NRS_OK;
+    if (s.C <= 0 || s.kh <= 0 || s.kw <= 0 || s.stride <= 0) return kSlabUnsupported;
+    // staged channel chunks must be at least a quarter real channels
+    if (round_up(s.C, 16) > 4 * (int64_t)s.C) return kSlabUnsupported;
+    if ((int64_t)s.C * s.H * s.W > INT32_MAX || (int64_t)s.OH * s.OW > INT32_MAX / 2)
+        return kSlabUnsupported;
+    // Tile configurations, widest output-channel block first: 64 x 112,
+    // 32 x 128 and 16 x 128 (channels x pixels). Take the widest whose LDS
+    // lets two workgroups share a CU (one stages while the other computes),
+    // else the widest that fits at all.
+    const SlabPlan p64 = s.M >= 48 ? plan_slab<4, 1, 1, 7>(s) : SlabPlan{};
+    const SlabPlan p32 = s.M > 16 ? plan_slab<2, 2, 1, 4>(s) : SlabPlan{};
+    const SlabPlan p16 = plan_slab<1, 4, 1, 2>(s);
+    constexpr size_t kHalf = kLdsBytes / 2;
+    if (p64.lds && p64.lds <= kHalf) return launch_slab<4, 1, 1, 7>(s, p64);
+    if (p32.lds && p32.lds <= kHalf) return launch_slab<2, 2, 1, 4>(s, p32);
+    if (p16.lds && p16.lds <= kHalf) return launch_slab<1, 4, 1, 2>(s, p16);
+    if (p64.lds) return launch_slab<4, 1, 1, 7>(s, p64);
+    if (p32.lds) return launch_slab<2, 2, 1, 4>(s, p32);
+    if (p16.lds) return launch_slab<1, 4, 1, 2>(s, p16);
+    return kSlabUnsupported;
+}
+
+}  // namespace nrs

@@ -1,0 +1,34 @@
+// Slab-resident convolution: host-side interface (kernel in conv_slab.hip).
+//
+// out[n, m, oy, ox] = sum_{c,i,j} x[n, c, oy*s - pad_h + i, ox*s - pad_w + j] * Wt(m, c, i, j)
+//                     (+ bias[m]) + beta * out
+// with Wt(m, c, i, j) = w[m][c][i][j] (forward), or, with `flip`, the
+// flipped, channel-transposed w[c][m][kh-1-i][kw-1-j] (the stride-1 input
+// gradient of a convolution with weights w, read as a forward convolution of
+// the output gradient).
+#pragma once
+
+#include "fastdiv.hpp"
+#include "nrs_internal.hpp"
+
+namespace nrs {
+
+struct SlabConv {
+    const float* x = nullptr;     // NCHW [N][C][H][W]
+    const float* w = nullptr;     // [M][C][kh][kw], or [C][M][kh][kw] with flip
+    const float* bias = nullptr;  // [M] or null
+    float* out = nullptr;         // NCHW [N][M][OH][OW]
+    int64_t N = 0;
+    int C = 0, H = 0, W = 0, M = 0, kh = 0, kw = 0, stride = 1, pad_h = 0, pad_w = 0;
+    int OH = 0, OW = 0;
+    bool flip = false;
+    float beta = 0.0f;
+};
+
+// Launches the convolution when its tiles fit the slab kernel's limits and
+// returns NRS_OK; returns kSlabUnsupported (launching nothing) when they do
+// not, so the caller can take another lowering. Other codes are errors.
+constexpr int kSlabUnsupported = -1;
+int slab_conv(const SlabConv& s);
+
+}  // namespace nrs

@@ -24,7 +24,7 @@ int set_error(int code, const char* fmt, ...);
 
 // Library-owned scratch, grown lazily, one buffer per slot:
 //   0 split-K partials, 1 im2col / dcols columns, 2 conv grad in GEMM layout,
-//   3 reduction partials.
+//   3 reduction partials, 4 conv weights packed for LDS staging.
 // Returns nullptr (and records an error) when the allocation fails.
 float* workspace(size_t bytes, int slot = 0);
 

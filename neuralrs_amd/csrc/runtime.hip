@@ -10,7 +10,7 @@
 namespace nrs {
 namespace {
 
-constexpr int kSlots = 4;
+constexpr int kSlots = 5;
 
 struct State {
     bool init = false;

@@ -27,6 +27,13 @@ CONV_SHAPES = [  # (n, c_in, c_out, h, w, kh, kw, stride, pad)
     (2, 5, 4, 8, 6, 3, 2, 1, 0),
     (1, 8, 3, 7, 7, 3, 3, 2, 1),     # stride 2: explicit input-gradient path
     (2, 7, 9, 11, 13, 5, 5, 1, 2),   # 5x5, pad 2, ragged sizes
+    # LDS-slab path edge cases
+    (1, 40, 70, 6, 7, 3, 3, 1, 1),   # two output-channel blocks; channels padded to 48
+    (1, 160, 20, 5, 5, 3, 3, 1, 1),  # weights exceed LDS: two channel chunks
+    (1, 4, 8, 30, 33, 3, 3, 1, 1),   # many bands per image, bands straddling rows
+    (2, 16, 24, 11, 10, 3, 3, 2, 1), # stride 2 slab windows
+    (2, 40, 12, 5, 6, 1, 1, 1, 0),   # 1x1 kernel
+    (2, 12, 17, 9, 13, 2, 4, 2, 1),  # non-square kernel, stride 2
 ]
 ids = ["x".join(map(str, s)) for s in CONV_SHAPES]
 
