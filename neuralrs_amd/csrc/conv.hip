@@ -118,31 +118,41 @@ __global__ __launch_bounds__(256) void flip_weights_kernel(float* __restrict__ w
 
 // Direct convolution for layers with very few input taps (c_in*kh*kw <=
 // kDirectTaps), e.g. a first layer over grayscale images, where a GEMM tile
-// would be mostly padding. One thread per (output pixel, output channel):
-// blockIdx.y is the channel, so its weights and bias are uniform per
-// workgroup, and consecutive lanes are consecutive pixels (coalesced input
-// reads and output stores). The taps are loaded branch-free (clamped index,
-// then zeroed) so they are all in flight together; the sum runs over the taps
-// in (ic, i, j) order. 32-bit indexing (checked on the host).
-constexpr int kDirectTaps = 32;
+// would be mostly padding and the layer is bound by writing its output. One
+// thread per output pixel: its taps are loaded once (branch-free: clamped
+// index, then zeroed), then it produces a block of up to kDirectOcBlock
+// output channels (blockIdx.y) from wave-uniform weights (scalar loads), so
+// consecutive lanes store consecutive pixels of each channel plane. The sum
+// runs over the taps in (ic, i, j) order. 32-bit indexing (checked on the
+// host).
+constexpr int kDirectTaps = 32, kDirectOcBlock = 64;
 
 template <int TAPS>
 __global__ __launch_bounds__(256) void conv_fwd_direct_kernel(
     float* __restrict__ out, const float* __restrict__ input, const float* __restrict__ weight,
     const float* __restrict__ bias, int N, int c_in, int in_h, int in_w, int c_out, int kh, int kw,
     int stride, int pad, FastDiv div_P, FastDiv div_ow) {
-    // tap t = (ic*kh + i)*kw + j: offset inside one image and (i, j)
+    // tap t = (ic*kh + i)*kw + j: offset inside one image and (i, j); the
+    // block's weights (zero past the taps) and biases
+    constexpr int WROW = (TAPS + 3) & ~3;  // whole float4s per weight row
     __shared__ int2 tab[TAPS];
+    __shared__ __attribute__((aligned(16))) float wsh[kDirectOcBlock][WROW];
+    __shared__ float bsh[kDirectOcBlock];
     const int taps = c_in * kh * kw;
+    const int oc0 = blockIdx.y * kDirectOcBlock;
+    const int oc1 = min(c_out, oc0 + kDirectOcBlock);
     if (threadIdx.x < TAPS) {
         const int t = threadIdx.x < taps ? threadIdx.x : 0;
         const int j = t % kw, i = (t / kw) % kh, ic = t / (kw * kh);
         tab[threadIdx.x] = make_int2((ic * in_h + i) * in_w + j, i | (j << 16));
     }
+    for (int e = threadIdx.x; e < kDirectOcBlock * WROW; e += blockDim.x) {
+        const int o = e / WROW, t = e - o * WROW;
+        wsh[o][t] = (oc0 + o < oc1 && t < taps) ? weight[(int64_t)(oc0 + o) * taps + t] : 0.0f;
+    }
+    if (threadIdx.x < kDirectOcBlock)
+        bsh[threadIdx.x] = (bias && oc0 + (int)threadIdx.x < oc1) ? bias[oc0 + threadIdx.x] : 0.0f;
     __syncthreads();
-    const int oc = blockIdx.y;
-    const float* w = weight + oc * taps;
-    const float b = bias ? bias[oc] : 0.0f;
     const int P = (int)div_P.d, total = N * P;
     for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += gridDim.x * blockDim.x) {
@@ -150,7 +160,8 @@ __global__ __launch_bounds__(256) void conv_fwd_direct_kernel(
         fast_divmod((uint32_t)idx, div_P, n, pp);
         fast_divmod(pp, div_ow, oy, ox);
         const int iy0 = (int)oy * stride - pad, ix0 = (int)ox * stride - pad;
-        const float* img = input + (int64_t)n * c_in * in_h * in_w + iy0 * in_w + ix0;
+        const float* img = input + (int64_t)n * c_in * in_h * in_w;
+        const int base = iy0 * in_w + ix0;
         float x[TAPS];
 #pragma unroll
         for (int t = 0; t < TAPS; ++t) {
@@ -158,14 +169,20 @@ __global__ __launch_bounds__(256) void conv_fwd_direct_kernel(
             const int i = e.y & 0xffff, j = e.y >> 16;
             const bool ok = (t < taps) & ((unsigned)(iy0 + i) < (unsigned)in_h) &
                             ((unsigned)(ix0 + j) < (unsigned)in_w);
-            const float v = ok ? img[e.x] : 0.0f;
-            x[t] = v;
+            const float v = img[ok ? base + e.x : 0];
+            x[t] = ok ? v : 0.0f;
         }
-        float acc = 0.0f;
+        float* o = out + (int64_t)n * c_out * P + pp;
+        // weights past the taps are zero (and so are the taps): no guard, so
+        // the weight reads are not serialised behind per-tap branches
+#pragma unroll 2
+        for (int oc = oc0; oc < oc1; ++oc) {
+            const float* w = wsh[oc - oc0];
+            float acc = 0.0f;
 #pragma unroll
-        for (int t = 0; t < TAPS; ++t)
-            if (t < taps) acc += w[t] * x[t];
-        out[((int64_t)n * c_out + oc) * P + pp] = acc + b;
+            for (int t = 0; t < TAPS; ++t) acc += w[t] * x[t];
+            o[(int64_t)oc * P] = acc + bsh[oc - oc0];
+        }
     }
 }
 
@@ -242,6 +259,257 @@ __global__ __launch_bounds__(256) void conv_dgrad_direct_kernel(
                 if (beta != 0.0f) v = v + beta * *dst;
                 *dst = v;
             }
+    }
+}
+
+// Stride-1 input gradient for c_in <= kDirectCin, from LDS. A workgroup owns
+// one image and a band of `band` input rows; each thread owns kDgradRun
+// adjacent pixels of one row. Per chunk of `occ` output channels the block
+// stages the output-gradient rows the band's windows touch (band + kh - 1
+// rows of `pitch` floats, zero outside the gradient) and the chunk's weights
+// flipped along the row, wf[o][i][jj][c] = W[oc0+o, c, i, KW-1-jj]. Then for
+// each (oc, i) a thread reads the kDgradRun + KW - 1 gradient values its
+// pixels' windows share once and forms
+//   dinput[c, y, x] += grad[oc, y + pad - i, x + pad - KW + 1 + jj] * wf[oc][i][jj][c]
+// for all its pixels (the reference's sum over (oc, i, j), j = KW-1-jj).
+// dinput = that sum + dinput. KW is the exact kernel width and CIN covers
+// c_in (1, or 4 with zero weights past c_in).
+constexpr int kDgradRun = 4, kDgradStage = 16;
+
+template <int KW, int CIN>
+__global__ __launch_bounds__(256) void conv_dgrad_small_kernel(
+    float* __restrict__ dinput, const float* __restrict__ grad, const float* __restrict__ weight,
+    int c_in, int in_h, int in_w, int c_out, int kh, int pad, int out_h, int out_w, int band,
+    int bands, int occ, int ngx, int pitch, FastDiv div_ngx, FastDiv div_pitch,
+    FastDiv div_tile) {
+    constexpr int NG = kDgradRun + KW - 1;  // gradient values per (oc, i)
+    // [occ][gr][pitch] gradient tile, then the chunk's flipped weights
+    extern __shared__ __attribute__((aligned(16))) float gt[];
+    const int n = blockIdx.x / bands, y0 = (blockIdx.x - n * bands) * band;
+    const int rows = min(band, in_h - y0);
+    const int gr = band + kh - 1, tile = gr * pitch, gw = in_w + KW - 1;
+    const int oy_base = y0 + pad - (kh - 1), ox_base = pad - (KW - 1);
+    const int P = out_h * out_w, HW = in_h * in_w;
+    const float* gimg = grad + (int64_t)n * c_out * P;
+    uint32_t yy, xg;
+    fast_divmod(threadIdx.x, div_ngx, yy, xg);
+    const bool live = (int)yy < rows;
+    const int x0 = (int)xg * kDgradRun;
+    // this thread's tile row for kernel row i is yy + kh - 1 - i
+    const int tbase = ((live ? (int)yy : 0) + kh - 1) * pitch + x0;
+    float acc[kDgradRun][CIN] = {};
+    float* wsh = gt + ((occ * tile + 3) & ~3);
+    for (int oc0 = 0; oc0 < c_out; oc0 += occ) {
+        const int nch = min(occ, c_out - oc0);
+        if (oc0) __syncthreads();
+        const int items = nch * tile;
+        for (int b0 = threadIdx.x; b0 < items; b0 += blockDim.x * kDgradStage) {
+            float v[kDgradStage];
+#pragma unroll
+            for (int u = 0; u < kDgradStage; ++u) {
+                const int e = b0 + u * blockDim.x;
+                uint32_t ch, rc, r, c;
+                fast_divmod((uint32_t)min(e, items - 1), div_tile, ch, rc);
+                fast_divmod(rc, div_pitch, r, c);
+                const int oy = oy_base + (int)r, ox = ox_base + (int)c;
+                const bool ok = (e < items) & ((int)c < gw) & ((unsigned)oy < (unsigned)out_h) &
+                                ((unsigned)ox < (unsigned)out_w);
+                const float g = gimg[ok ? (int64_t)(oc0 + (int)ch) * P + oy * out_w + ox : 0];
+                v[u] = ok ? g : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < kDgradStage; ++u) {
+                const int e = b0 + u * blockDim.x;
+                if (e < items) gt[e] = v[u];
+            }
+        }
+        const int wn = nch * kh * KW;  // (o, i, jj)
+        for (int e = threadIdx.x; e < wn; e += blockDim.x) {
+            const int oi = e / KW, jj = e - oi * KW;
+            const int o = oi / kh, i = oi - o * kh;
+            const float* w = weight + ((int64_t)(oc0 + o) * c_in * kh + i) * KW + (KW - 1 - jj);
+#pragma unroll
+            for (int c = 0; c < CIN; ++c) wsh[e * CIN + c] = c < c_in ? w[(int64_t)c * kh * KW] : 0.0f;
+        }
+        __syncthreads();
+        if (live) {
+            // (o, i) steps in order; the gradient row pointer moves up one
+            // row per kernel row and to the next channel's tile after kh
+            // rows, the weights are contiguous per step
+            const float* g = gt + tbase;
+            const float* w = wsh;
+            int i = 0;
+#pragma unroll 4
+            for (int oi = 0; oi < nch * kh; ++oi) {
+                float gv[NG];
+#pragma unroll
+                for (int q = 0; q < NG; ++q) gv[q] = g[q];
+#pragma unroll
+                for (int jj = 0; jj < KW; ++jj)
+#pragma unroll
+                    for (int c = 0; c < CIN; ++c) {
+                        const float wv = w[jj * CIN + c];
+#pragma unroll
+                        for (int r = 0; r < kDgradRun; ++r) acc[r][c] += gv[r + jj] * wv;
+                    }
+                w += KW * CIN;
+                if (++i == kh) {
+                    i = 0;
+                    g += tile + (kh - 1) * pitch;
+                } else {
+                    g -= pitch;
+                }
+            }
+        }
+    }
+    if (!live) return;
+    float* drow = dinput + (int64_t)n * c_in * HW + (y0 + (int)yy) * in_w + x0;
+#pragma unroll
+    for (int c = 0; c < CIN; ++c)
+        if (c < c_in)
+#pragma unroll
+            for (int r = 0; r < kDgradRun; ++r)
+                if (x0 + r < in_w) {
+                    float* dst = drow + (int64_t)c * HW + r;
+                    *dst = acc[r][c] + *dst;
+                }
+}
+
+// Weight and bias gradient for layers with few taps (c_in*kh*kw <= TAPS):
+// one workgroup of kWgradWaves wavefronts per (image, block of OCW output
+// channels). Thread q takes pixels p = q, q + 256, ... (kWgradPix per batch,
+// all their loads issued together): it loads each pixel's taps once and, per
+// channel, one coalesced gradient value, accumulating
+//   dW[oc, t] += g[n, oc, p] * x_t(n, p),   db[oc] += g[n, oc, p]
+// in ascending pixel order; the 64 lanes of a wave are then added in lane
+// order and the waves in wave order. The per-image sums go to
+// pw[n][oc*taps + t] and pb[n][oc] for a fixed-order sum over images.
+constexpr int kWgradWaves = 4, kWgradPix = 4;
+
+template <int TAPS, int OCW>
+__global__ __launch_bounds__(64 * kWgradWaves) void conv_wgrad_small_kernel(
+    float* __restrict__ pw, float* __restrict__ pb, const float* __restrict__ grad,
+    const float* __restrict__ input, int c_in, int in_h, int in_w, int c_out, int kh, int kw,
+    int stride, int pad, FastDiv div_ow, int P) {
+    constexpr int NT = 64 * kWgradWaves, NV = OCW * (TAPS + 1);
+    __shared__ int2 tab[TAPS];
+    __shared__ float red[NT][NV + 1];
+    __shared__ float wsum[kWgradWaves][NV];
+    const int taps = c_in * kh * kw;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid < TAPS) {
+        const int t = tid < taps ? tid : 0;
+        const int j = t % kw, i = (t / kw) % kh, ic = t / (kw * kh);
+        tab[tid] = make_int2((ic * in_h + i) * in_w + j, i | (j << 16));
+    }
+    __syncthreads();
+    const int n = blockIdx.x, oc0 = blockIdx.y * OCW;
+    const float* img = input + (int64_t)n * c_in * in_h * in_w;
+    const float* gimg = grad + ((int64_t)n * c_out + oc0) * P;
+    float aw[OCW][TAPS] = {}, ab[OCW] = {};
+    for (int p0 = tid; p0 < P; p0 += NT * kWgradPix) {
+        float x[kWgradPix][TAPS], g[kWgradPix][OCW];
+#pragma unroll
+        for (int k = 0; k < kWgradPix; ++k) {
+            const int p = p0 + k * NT;
+            const bool pl = p < P;
+            uint32_t oy, ox;
+            fast_divmod((uint32_t)(pl ? p : 0), div_ow, oy, ox);
+            const int iy0 = (int)oy * stride - pad, ix0 = (int)ox * stride - pad;
+            const int base = iy0 * in_w + ix0;
+#pragma unroll
+            for (int t = 0; t < TAPS; ++t) {
+                const int2 e = tab[t];
+                const int i = e.y & 0xffff, j = e.y >> 16;
+                const bool ok = pl & (t < taps) & ((unsigned)(iy0 + i) < (unsigned)in_h) &
+                                ((unsigned)(ix0 + j) < (unsigned)in_w);
+                const float v = img[ok ? base + e.x : 0];
+                x[k][t] = ok ? v : 0.0f;
+            }
+#pragma unroll
+            for (int o = 0; o < OCW; ++o) {
+                const bool live = pl & (oc0 + o < c_out);
+                const float v = gimg[live ? (int64_t)o * P + p : 0];
+                g[k][o] = live ? v : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kWgradPix; ++k)
+#pragma unroll
+            for (int o = 0; o < OCW; ++o) {
+#pragma unroll
+                for (int t = 0; t < TAPS; ++t) aw[o][t] += g[k][o] * x[k][t];
+                ab[o] += g[k][o];
+            }
+    }
+    // every thread's NV sums go to LDS; value v of wave w is then summed
+    // over that wave's 64 lanes in lane order by lane v of the wave, and the
+    // wave sums are added in wave order
+#pragma unroll
+    for (int o = 0; o < OCW; ++o) {
+#pragma unroll
+        for (int t = 0; t < TAPS; ++t) red[tid][o * (TAPS + 1) + t] = aw[o][t];
+        red[tid][o * (TAPS + 1) + TAPS] = ab[o];
+    }
+    __syncthreads();
+    for (int v = lane; v < NV; v += 64) {
+        float r = 0.0f;
+#pragma unroll 16
+        for (int l = 0; l < 64; ++l) r += red[wave * 64 + l][v];
+        wsum[wave][v] = r;
+    }
+    __syncthreads();
+    for (int v = tid; v < NV; v += NT) {
+        const int o = v / (TAPS + 1), t = v - o * (TAPS + 1);
+        if (oc0 + o >= c_out || (t < TAPS && t >= taps)) continue;
+        float r = wsum[0][v];
+#pragma unroll
+        for (int w = 1; w < kWgradWaves; ++w) r += wsum[w][v];
+        if (t == TAPS)
+            pb[(int64_t)n * c_out + oc0 + o] = r;
+        else
+            pw[((int64_t)n * c_out + oc0 + o) * taps + t] = r;
+    }
+}
+
+// out[e] = sum over s of part[s * total + e] + beta * out[e]. The slices are
+// split into kSliceGroups contiguous groups summed in parallel (ascending s
+// inside a group, loads batched), then the group sums are added in group
+// order, so the result is deterministic.
+constexpr int kSliceGroups = 16;
+
+__global__ __launch_bounds__(64 * kSliceGroups) void slice_sum_kernel(float* __restrict__ out,
+                                                                      const float* __restrict__ part,
+                                                                      int slices, int total,
+                                                                      float beta) {
+    __shared__ float red[kSliceGroups][64];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const int per = (slices + kSliceGroups - 1) / kSliceGroups;
+    const int s0 = min(slices, ty * per), s1 = min(slices, s0 + per);
+    for (int base = blockIdx.x * 64; base < total; base += gridDim.x * 64) {
+        const int e = base + tx;
+        float v = 0.0f;
+        if (e < total) {
+            int s = s0;
+            for (; s + 8 <= s1; s += 8) {
+                float t[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) t[u] = part[(int64_t)(s + u) * total + e];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v += t[u];
+            }
+            for (; s < s1; ++s) v += part[(int64_t)s * total + e];
+        }
+        red[ty][tx] = v;
+        __syncthreads();
+        if (ty == 0 && e < total) {
+            float r = red[0][tx];
+#pragma unroll
+            for (int y = 1; y < kSliceGroups; ++y) r += red[y][tx];
+            if (beta != 0.0f) r = r + beta * out[e];
+            out[e] = r;
+        }
+        __syncthreads();
     }
 }
 
@@ -467,6 +735,86 @@ int launch_out2mm(float* mm, const float* grad, const ConvDims& d) {
     return NRS_OK;
 }
 
+// dinput += the stride-1 input gradient of a layer with c_in <= kDirectCin
+// and a kernel width the row kernel is built for, gathered from LDS;
+// kSlabUnsupported when it does not apply or its tiles do not fit.
+int small_dgrad(float* dinput, const float* grad, const float* weight, const ConvDims& d) {
+    if (d.stride != 1 || d.c_in > kDirectCin) return kSlabUnsupported;
+    const int64_t ngx = (d.in_w + kDgradRun - 1) / kDgradRun;
+    if (ngx > 256) return kSlabUnsupported;
+    // row pitch: the runs' windows, whole float4s
+    const int64_t pitch = (ngx * kDgradRun + d.kw - 1 + 3) / 4 * 4;
+    // about two workgroups per CU, at most 256 threads' rows per band
+    int64_t bands = std::max<int64_t>(1, std::min<int64_t>(d.in_h, (2 * num_cus() + d.N - 1) / d.N));
+    int64_t band = std::min<int64_t>((d.in_h + bands - 1) / bands, 256 / ngx);
+    bands = (d.in_h + band - 1) / band;
+    const int64_t tile = (band + d.kh - 1) * pitch, limit = 64 * 1024 / 4;
+    const int64_t per_ch = tile + 4 * d.kh * d.kw;  // gradient tile + weights
+    if (per_ch > limit - 3 || d.N * bands > INT32_MAX || d.c_out > INT32_MAX ||
+        d.c_out * d.out_h * d.out_w > INT32_MAX || d.in_h * d.in_w > INT32_MAX)
+        return kSlabUnsupported;
+    const int64_t occ = std::min<int64_t>(d.c_out, (limit - 3) / per_ch);
+    const size_t lds = (size_t)(((occ * tile + 3) & ~3ll) + occ * 4 * d.kh * d.kw) * 4;
+    const bool c1 = d.c_in == 1;
+    void (*fn)(float*, const float*, const float*, int, int, int, int, int, int, int, int, int,
+               int, int, int, int, FastDiv, FastDiv, FastDiv) = nullptr;
+    switch (d.kw) {
+        case 1: fn = c1 ? conv_dgrad_small_kernel<1, 1> : conv_dgrad_small_kernel<1, 4>; break;
+        case 2: fn = c1 ? conv_dgrad_small_kernel<2, 1> : conv_dgrad_small_kernel<2, 4>; break;
+        case 3: fn = c1 ? conv_dgrad_small_kernel<3, 1> : conv_dgrad_small_kernel<3, 4>; break;
+        case 5: fn = c1 ? conv_dgrad_small_kernel<5, 1> : conv_dgrad_small_kernel<5, 4>; break;
+        case 7: fn = c1 ? conv_dgrad_small_kernel<7, 1> : conv_dgrad_small_kernel<7, 4>; break;
+        default: return kSlabUnsupported;
+    }
+    hipLaunchKernelGGL(fn, dim3((unsigned)(d.N * bands)), dim3(256), lds, stream(), dinput, grad,
+                       weight, (int)d.c_in, (int)d.in_h, (int)d.in_w, (int)d.c_out, (int)d.kh,
+                       (int)d.pad, (int)d.out_h, (int)d.out_w, (int)band, (int)bands, (int)occ,
+                       (int)ngx, (int)pitch, make_fastdiv((uint32_t)ngx),
+                       make_fastdiv((uint32_t)pitch), make_fastdiv((uint32_t)tile));
+    NRS_LAUNCH_CHECK("conv2d input gradient (small)");
+    return NRS_OK;
+}
+
+// dweight += and dbias += (either may be null) for a layer with c_in*kh*kw <=
+// kDirectTaps: per-image sums, then a fixed-order sum over the images.
+int small_wgrad(float* dweight, float* dbias, const float* grad, const float* input,
+                const ConvDims& d) {
+    const int64_t taps = d.c_in * d.kh * d.kw, P = d.out_h * d.out_w;
+    if (d.N * P == 0) return NRS_OK;
+    const int ocw = taps <= 9 ? 4 : (taps <= 16 ? 2 : 1);
+    const int64_t blocks_y = (d.c_out + ocw - 1) / ocw;
+    NRS_ARG_CHECK(blocks_y <= 65535 && d.N <= INT32_MAX && P <= INT32_MAX &&
+                      d.N * d.c_out * (taps + 1) <= INT32_MAX &&
+                      d.c_in * d.in_h * d.in_w <= INT32_MAX,
+                  "conv2d weight gradient: tensor too large");
+    float* pw = workspace(sizeof(float) * (size_t)(d.N * d.c_out * (taps + 1)), 3);
+    if (!pw) return NRS_ERR_ALLOC;
+    float* pb = pw + d.N * d.c_out * taps;
+    auto fn = taps <= 9 ? conv_wgrad_small_kernel<9, 4>
+                        : (taps <= 16 ? conv_wgrad_small_kernel<16, 2>
+                                      : conv_wgrad_small_kernel<32, 1>);
+    hipLaunchKernelGGL(fn, dim3((unsigned)d.N, (unsigned)blocks_y), dim3(64 * kWgradWaves), 0,
+                       stream(), pw, pb,
+                       grad, input, (int)d.c_in, (int)d.in_h, (int)d.in_w, (int)d.c_out,
+                       (int)d.kh, (int)d.kw, (int)d.stride, (int)d.pad,
+                       make_fastdiv((uint32_t)d.out_w), (int)P);
+    NRS_LAUNCH_CHECK("conv2d weight gradient (small)");
+    if (dweight) {
+        const int64_t total = d.c_out * taps;
+        hipLaunchKernelGGL(slice_sum_kernel, dim3((unsigned)((total + 63) / 64)),
+                           dim3(64 * kSliceGroups), 0, stream(), dweight, pw, (int)d.N, (int)total,
+                           1.0f);
+        NRS_LAUNCH_CHECK("conv2d weight gradient (sum)");
+    }
+    if (dbias) {
+        hipLaunchKernelGGL(slice_sum_kernel, dim3((unsigned)((d.c_out + 63) / 64)),
+                           dim3(64 * kSliceGroups), 0, stream(), dbias, pb, (int)d.N, (int)d.c_out,
+                           1.0f);
+        NRS_LAUNCH_CHECK("conv2d bias gradient (sum)");
+    }
+    return NRS_OK;
+}
+
 // dinput += the stride-1 input gradient as a slab convolution of the output
 // gradient with the flipped, channel-transposed weights (padding k-1-pad).
 int slab_dgrad(float* dinput, const float* grad, const float* weight, int64_t N, int64_t c_in,
@@ -561,13 +909,14 @@ int nrs_conv2d_forward(float* out, const float* input, const float* weight, cons
                     d.out_h, d.out_w, P};
     if (c_in * kh * kw <= nrs::kDirectTaps && c_out <= 65535 &&
         N * std::max(c_in * in_h * in_w, c_out * P) <= INT32_MAX) {
-        // few taps per output: direct convolution, one thread per (pixel, channel)
+        // few taps per output: direct convolution, one thread per pixel
         const int64_t taps = c_in * kh * kw;
         auto fn = taps <= 9 ? nrs::conv_fwd_direct_kernel<9>
                             : (taps <= 16 ? nrs::conv_fwd_direct_kernel<16>
                                           : nrs::conv_fwd_direct_kernel<32>);
-        const unsigned bx = (unsigned)std::min<int64_t>((N * P + 255) / 256, 4096);
-        hipLaunchKernelGGL(fn, dim3(bx, (unsigned)c_out), dim3(256), 0, nrs::stream(), out, input,
+        const unsigned bx = (unsigned)std::min<int64_t>((N * P + 255) / 256, 65535);
+        const unsigned by = (unsigned)((c_out + nrs::kDirectOcBlock - 1) / nrs::kDirectOcBlock);
+        hipLaunchKernelGGL(fn, dim3(bx, by), dim3(256), 0, nrs::stream(), out, input,
                            weight, bias, (int)N, (int)c_in, (int)in_h, (int)in_w, (int)c_out,
                            (int)kh, (int)kw, (int)stride, (int)pad, nrs::make_fastdiv((uint32_t)P),
                            nrs::make_fastdiv((uint32_t)d.out_w));
@@ -640,9 +989,12 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
                   "conv2d: kernel or image too large");
     if (dinput) {
         const int64_t grad_bytes = N * c_out * P * (int64_t)sizeof(float);
-        if (c_in <= nrs::kDirectCin && c_out * c_in * kh * kw <= nrs::kDirectWeights &&
-            kh * kw <= nrs::kDirectWin &&
-            N * std::max(c_in * in_h * in_w, c_out * P) <= INT32_MAX) {
+        if ((rc = nrs::small_dgrad(dinput, grad, weight, d)) != nrs::kSlabUnsupported) {
+            // a handful of input channels, stride 1: gather from LDS
+            if (rc) return rc;
+        } else if (c_in <= nrs::kDirectCin && c_out * c_in * kh * kw <= nrs::kDirectWeights &&
+                   kh * kw <= nrs::kDirectWin &&
+                   N * std::max(c_in * in_h * in_w, c_out * P) <= INT32_MAX) {
             // a handful of input channels: direct gather per input pixel
             hipLaunchKernelGGL(nrs::conv_dgrad_direct_kernel, dim3(nrs::grid_for(N * in_h * in_w)),
                                dim3(256), 0, nrs::stream(), dinput, grad, weight, (int)N, (int)c_in,
@@ -691,6 +1043,11 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
             rc = nrs::launch_col2im(dinput, cols, d, 1.0f);
             if (rc) return rc;
         }
+    }
+    if ((dweight || dbias) && col_h <= nrs::kDirectTaps) {
+        // few taps: both gradients from one pass over the output gradient
+        // (conv.rs:314-322 without the cols matrix)
+        return nrs::small_wgrad(dweight, dbias, grad, input, d);
     }
     if (dweight) {
         // dW[c_out, col_h] += G . cols^T   (conv.rs:314-320, split-K NT), with

@@ -34,6 +34,7 @@ CONV_SHAPES = [  # (n, c_in, c_out, h, w, kh, kw, stride, pad)
     (2, 16, 24, 11, 10, 3, 3, 2, 1), # stride 2 slab windows
     (2, 40, 12, 5, 6, 1, 1, 1, 0),   # 1x1 kernel
     (2, 12, 17, 9, 13, 2, 4, 2, 1),  # non-square kernel, stride 2
+    (2, 1, 70, 9, 9, 3, 3, 1, 1),    # few taps, 70 channels: two forward channel blocks, ragged weight-grad block
 ]
 ids = ["x".join(map(str, s)) for s in CONV_SHAPES]
 
@@ -153,6 +154,24 @@ def test_conv2d_backward_without_input_grad(hip, orc):
     hip.call("nrs_conv2d_backward", None, gW.ptr, gB.ptr, D(hip, g), D(hip, x),
              D(hip, wt), n, ci, h, w, co, kh, kw, s, p)
     assert np.array_equal(gW.to_host(), dw_ref)
+    assert np.array_equal(gB.to_host(), db_ref)
+
+
+@pytest.mark.parametrize("shape", [(2, 1, 4, 6, 6, 3, 3, 1, 1), (2, 6, 5, 9, 9, 3, 3, 1, 1)],
+                         ids=["few-taps", "gemm"])
+def test_conv2d_backward_bias_only(hip, orc, shape):
+    """dweight = NULL, dbias given: only the bias (and input) gradients change."""
+    n, ci, co, h, w, kh, kw, s, p = shape
+    rng = np.random.default_rng(78)
+    x = int_matrix(rng, (n * ci * h * w,), -3, 3)
+    wt = int_matrix(rng, (co * ci * kh * kw,), -3, 3)
+    oh, ow = orc.conv_out_hw(h, w, kh, kw, s, p)
+    g = int_matrix(rng, (n * co * oh * ow,), -3, 3)
+    di_ref, _, db_ref = orc.conv2d_backward(x, wt, g, n, ci, co, h, w, kh, kw, s, p)
+    gI, gB = hip.DeviceBuffer.zeros(x.size), hip.DeviceBuffer.zeros(co)
+    hip.call("nrs_conv2d_backward", gI.ptr, None, gB.ptr, D(hip, g), D(hip, x),
+             D(hip, wt), n, ci, h, w, co, kh, kw, s, p)
+    assert np.array_equal(gI.to_host(), di_ref)
     assert np.array_equal(gB.to_host(), db_ref)
 
 
