@@ -1049,6 +1049,29 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
         // (conv.rs:314-322 without the cols matrix)
         return nrs::small_wgrad(dweight, dbias, grad, input, d);
     }
+    if (dweight && c_in <= INT32_MAX && c_out <= INT32_MAX && in_h <= INT32_MAX &&
+        in_w <= INT32_MAX) {
+        // input slab and gradient rows staged in LDS, reduction on the matrix
+        // cores, per-image partials summed in a fixed order
+        nrs::SlabWgrad w;
+        w.x = input;
+        w.g = grad;
+        w.dw = dweight;
+        w.db = dbias;
+        w.N = N;
+        w.C = (int)c_in;
+        w.H = (int)in_h;
+        w.W = (int)in_w;
+        w.M = (int)c_out;
+        w.kh = (int)kh;
+        w.kw = (int)kw;
+        w.stride = (int)stride;
+        w.pad = (int)pad;
+        w.OH = (int)d.out_h;
+        w.OW = (int)d.out_w;
+        rc = nrs::slab_wgrad(w);
+        if (rc != nrs::kSlabUnsupported) return rc;
+    }
     if (dweight) {
         // dW[c_out, col_h] += G . cols^T   (conv.rs:314-320, split-K NT), with
         // G read in place from NCHW when it fits a buffer (no out2mm).

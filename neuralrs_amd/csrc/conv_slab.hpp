@@ -31,4 +31,18 @@ struct SlabConv {
 constexpr int kSlabUnsupported = -1;
 int slab_conv(const SlabConv& s);
 
+// Weight gradient dw[m][c][i][j] += sum g[n,m,oy,ox] * x[n,c,oy*s-pad+i,ox*s-pad+j]
+// and, when db is given, bias gradient db[m] += sum g[n,m,oy,ox], with
+// per-image partial sums added in a fixed order. dw is required; returns
+// kSlabUnsupported (launching nothing) for shapes outside the kernel's limits.
+struct SlabWgrad {
+    const float* x = nullptr;  // NCHW [N][C][H][W]
+    const float* g = nullptr;  // NCHW [N][M][OH][OW]
+    float* dw = nullptr;       // [M][C][kh][kw]
+    float* db = nullptr;       // [M] or null
+    int64_t N = 0;
+    int C = 0, H = 0, W = 0, M = 0, kh = 0, kw = 0, stride = 1, pad = 0, OH = 0, OW = 0;
+};
+int slab_wgrad(const SlabWgrad& s);
+
 }  // namespace nrs
