@@ -59,6 +59,32 @@ class HipEvents:
         return ms.value
 
 
+def event_ms(hip, fn, reps, warmup):
+    """Average GPU time of fn() in ms: HIP events on the library stream
+    around `reps` calls after `warmup` untimed calls."""
+    for _ in range(warmup):
+        fn()
+    hip.sync()
+    ev = HipEvents(hip.load().nrs_get_stream())
+    e0, e1 = ev.event(), ev.event()
+    ev.record(e0)
+    for _ in range(reps):
+        fn()
+    ev.record(e1)
+    return ev.elapsed_ms(e0, e1) / reps
+
+
+def roofline_us(flops, nbytes):
+    """max(FLOP / FP32 MFMA peak, bytes / HBM bandwidth) in microseconds."""
+    return max(flops / (PEAK_FP32_MFMA_TFLOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9)) * 1e6
+
+
+def gemm_roof(m, n, k, batch=1):
+    """(flops, algorithmic bytes) of C[m,n] = A[m,k] . B[k,n]: each operand
+    read once, C written once, f32."""
+    return 2.0 * m * n * k * batch, 4.0 * (m * k + k * n + m * n) * batch
+
+
 def bench_gemm(hip, n, steps, warmup):
     rng = np.random.default_rng(0)
     a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
@@ -122,6 +148,16 @@ def bench_conv_cfg3(hip, steps, warmup):
         hip.call("nrs_conv2d_backward", gx.ptr, gw1.ptr, gb1.ptr, gy1.ptr, dx.ptr, dw1.ptr,
                  N, 1, 28, 28, 32, 3, 3, 1, 1)
 
+    def conv_fwd():
+        hip.call("nrs_conv2d_forward", y1.ptr, dx.ptr, dw1.ptr, db1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1)
+        hip.call("nrs_conv2d_forward", y2.ptr, p1.ptr, dw2.ptr, db2.ptr, N, 32, 14, 14, 64, 3, 3, 1, 1)
+
+    def conv_bwd():
+        hip.call("nrs_conv2d_backward", gp1.ptr, gw2.ptr, gb2.ptr, dg2.ptr, p1.ptr, dw2.ptr,
+                 N, 32, 14, 14, 64, 3, 3, 1, 1)
+        hip.call("nrs_conv2d_backward", gx.ptr, gw1.ptr, gb1.ptr, gy1.ptr, dx.ptr, dw1.ptr,
+                 N, 1, 28, 28, 32, 3, 3, 1, 1)
+
     for _ in range(warmup):
         step()
     hip.sync()
@@ -130,7 +166,175 @@ def bench_conv_cfg3(hip, steps, warmup):
         step()
     hip.sync()
     ms = (time.perf_counter() - t0) * 1e3 / steps
-    return {"ms_per_step": ms, "imgs_per_s": N / (ms / 1e3)}
+    fwd_ms = event_ms(hip, conv_fwd, steps, 3)
+    bwd_ms = event_ms(hip, conv_bwd, steps, 3)
+    # rooflines per layer (implicit-GEMM FLOPs; bytes = each tensor read or
+    # written once): forward x, W, b, y; input grad g, W, dx; weight+bias
+    # grad g, x, dW, db
+    roof_f = roof_b = 0.0
+    for (ci, co, h) in ((1, 32, 28), (32, 64, 14)):
+        P, taps = h * h, ci * 9
+        fl = 2.0 * co * N * P * taps
+        x_b, y_b, w_b = 4.0 * N * ci * P, 4.0 * N * co * P, 4.0 * co * taps
+        roof_f += roofline_us(fl, x_b + w_b + 4 * co + y_b)
+        roof_b += roofline_us(fl, y_b + w_b + x_b) + roofline_us(fl, y_b + x_b + w_b + 4 * co)
+    return {"ms_per_step": ms, "imgs_per_s": N / (ms / 1e3),
+            "fwd_us": fwd_ms * 1e3, "bwd_us": bwd_ms * 1e3,
+            "fwd_roof_us": roof_f, "bwd_roof_us": roof_b}
+
+
+def bench_mlp_cfg2(hip, steps, warmup):
+    """cfg2 training step: x[256,784] -> Linear(784,128) -> ReLU ->
+    Linear(128,10) -> softmax cross-entropy gradient (softmax - onehot)/256 ->
+    backward (dW, db of both layers, dh, dx)."""
+    rng = np.random.default_rng(2)
+    B, I, Hd, O = 256, 784, 128, 10
+    D = hip.DeviceBuffer.from_host
+    x = D(rng.standard_normal(B * I).astype(np.float32))
+    w1 = D((rng.standard_normal(I * Hd) * np.sqrt(2.0 / I)).astype(np.float32))
+    w2 = D((rng.standard_normal(Hd * O) * np.sqrt(2.0 / Hd)).astype(np.float32))
+    b1, b2 = hip.DeviceBuffer.zeros(Hd), hip.DeviceBuffer.zeros(O)
+    t = np.zeros((B, O), np.float32)
+    t[np.arange(B), rng.integers(0, O, B)] = 1.0
+    negt = D(-t)
+    h, a, z, sm, gz = (hip.DeviceBuffer(B * Hd), hip.DeviceBuffer(B * Hd), hip.DeviceBuffer(B * O),
+                       hip.DeviceBuffer(B * O), hip.DeviceBuffer(B * O))
+    ga, gh, gx = hip.DeviceBuffer(B * Hd), hip.DeviceBuffer(B * Hd), hip.DeviceBuffer(B * I)
+    gw1, gw2 = hip.DeviceBuffer.zeros(I * Hd), hip.DeviceBuffer.zeros(Hd * O)
+    gb1, gb2 = hip.DeviceBuffer.zeros(Hd), hip.DeviceBuffer.zeros(O)
+
+    def step():
+        hip.gemm(hip.NN, h, x, w1, B, Hd, I, 0.0, b1, hip.EPI_BIAS_COL)
+        hip.call("nrs_relu_forward", a.ptr, h.ptr, B * Hd)
+        hip.gemm(hip.NN, z, a, w2, B, O, Hd, 0.0, b2, hip.EPI_BIAS_COL)
+        hip.call("nrs_softmax_forward", sm.ptr, z.ptr, B, O)
+        hip.call("nrs_vadd", gz.ptr, sm.ptr, negt.ptr, B * O)
+        hip.call("nrs_scale", gz.ptr, gz.ptr, 1.0 / B, B * O, 0.0)
+        hip.gemm(hip.TN, gw2, a, gz, Hd, O, B, 1.0)
+        hip.call("nrs_sum_axis0", gb2.ptr, gz.ptr, B, O, 1.0)
+        hip.gemm(hip.NT, ga, gz, w2, B, Hd, O)
+        hip.call("nrs_relu_backward", gh.ptr, ga.ptr, h.ptr, B * Hd, 0.0)
+        hip.gemm(hip.TN, gw1, x, gh, I, Hd, B, 1.0)
+        hip.call("nrs_sum_axis0", gb1.ptr, gh.ptr, B, Hd, 1.0)
+        hip.gemm(hip.NT, gx, gh, w1, B, I, Hd)
+
+    us = event_ms(hip, step, steps, warmup) * 1e3
+    roof = 0.0
+    for (m, n, k) in ((B, Hd, I), (B, O, Hd), (Hd, O, B), (B, Hd, O), (I, Hd, B), (B, I, Hd)):
+        roof += roofline_us(*gemm_roof(m, n, k))
+    flops = 3 * (2.0 * B * I * Hd + 2.0 * B * Hd * O)
+    return {"us_per_step": us, "tflops": flops / (us * 1e-6) / 1e12, "gemm_roof_us": roof}
+
+
+def bench_attention_cfg4(hip, steps, warmup):
+    """cfg4 attention core as one batched call over batch*heads = 256:
+    S = Q.K^T / sqrt(32), P = softmax(S), O = P.V, then the backward bmm
+    products dP = dO.V^T, dV = P^T.dO, dS = softmax'(P, dP)/sqrt(32),
+    dQ = dS.K, dK = dS^T.Q (fresh outputs). Plus the block's Linear GEMMs
+    (Q/K/V/O projections 4096x256x256 and FFN 256->1024->256, forward and
+    both backward products)."""
+    rng = np.random.default_rng(4)
+    BH, T, Dh = 256, 128, 32
+    D = hip.DeviceBuffer.from_host
+    q, k, v, do = (D(rng.standard_normal(BH * T * Dh).astype(np.float32)) for _ in range(4))
+    S, P, dP, dS = (hip.DeviceBuffer(BH * T * T) for _ in range(4))
+    o, dq, dk, dv = (hip.DeviceBuffer(BH * T * Dh) for _ in range(4))
+    sc = 1.0 / np.sqrt(Dh)
+
+    def fwd():
+        hip.bmm(hip.NT, S, q, k, BH, T, T, Dh)
+        hip.call("nrs_scale", S.ptr, S.ptr, sc, BH * T * T, 0.0)
+        hip.call("nrs_softmax_forward", P.ptr, S.ptr, BH * T, T)
+        hip.bmm(hip.NN, o, P, v, BH, T, Dh, T)
+
+    def bwd():
+        hip.bmm(hip.NT, dP, do, v, BH, T, T, Dh)
+        hip.bmm(hip.TN, dv, P, do, BH, T, Dh, T)
+        hip.call("nrs_softmax_backward", dS.ptr, P.ptr, dP.ptr, BH * T, T, 0.0)
+        hip.call("nrs_scale", dS.ptr, dS.ptr, sc, BH * T * T, 0.0)
+        hip.bmm(hip.NN, dq, dS, k, BH, T, Dh, T)
+        hip.bmm(hip.TN, dk, dS, q, BH, T, Dh, T)
+
+    def bmms_only():
+        hip.bmm(hip.NT, S, q, k, BH, T, T, Dh)
+        hip.bmm(hip.NN, o, P, v, BH, T, Dh, T)
+        hip.bmm(hip.NT, dP, do, v, BH, T, T, Dh)
+        hip.bmm(hip.TN, dv, P, do, BH, T, Dh, T)
+        hip.bmm(hip.NN, dq, dS, k, BH, T, Dh, T)
+        hip.bmm(hip.TN, dk, dS, q, BH, T, Dh, T)
+
+    fwd()
+    fwd_us = event_ms(hip, fwd, steps, warmup) * 1e3
+    bwd_us = event_ms(hip, bwd, steps, warmup) * 1e3
+    bmm_us = event_ms(hip, bmms_only, steps, warmup) * 1e3
+    bmm_roof = 6 * roofline_us(*gemm_roof(T, T, Dh, BH))  # every product moves 25.2 MB
+
+    # the block's Linear GEMMs: X[4096,256] through 4 projections and the FFN
+    R, dm, ff = 32 * 128, 256, 1024
+    X = D(rng.standard_normal(R * dm).astype(np.float32))
+    H = D(rng.standard_normal(R * ff).astype(np.float32))
+    Wp = D((rng.standard_normal(dm * dm) * np.sqrt(1.0 / dm)).astype(np.float32))
+    W1 = D((rng.standard_normal(dm * ff) * np.sqrt(1.0 / dm)).astype(np.float32))
+    W2 = D((rng.standard_normal(ff * dm) * np.sqrt(1.0 / ff)).astype(np.float32))
+    Yd, Yf, gXd, gXf = (hip.DeviceBuffer(R * dm), hip.DeviceBuffer(R * ff),
+                        hip.DeviceBuffer(R * dm), hip.DeviceBuffer(R * ff))
+    gWp, gW1, gW2 = hip.DeviceBuffer(dm * dm), hip.DeviceBuffer(dm * ff), hip.DeviceBuffer(ff * dm)
+    shapes = []
+
+    def linears():
+        for _ in range(4):  # projections: Y = X.Wp, dX = dY.Wp^T, dW = X^T.dY
+            hip.gemm(hip.NN, Yd, X, Wp, R, dm, dm)
+            hip.gemm(hip.NT, gXd, Yd, Wp, R, dm, dm)
+            hip.gemm(hip.TN, gWp, X, Yd, dm, dm, R)
+        hip.gemm(hip.NN, Yf, X, W1, R, ff, dm)
+        hip.gemm(hip.NT, gXd, Yf, W1, R, dm, ff)
+        hip.gemm(hip.TN, gW1, X, Yf, dm, ff, R)
+        hip.gemm(hip.NN, Yd, H, W2, R, dm, ff)
+        hip.gemm(hip.NT, gXf, Yd, W2, R, ff, dm)
+        hip.gemm(hip.TN, gW2, H, Yd, ff, dm, R)
+
+    for _ in range(4):
+        shapes += [(R, dm, dm), (R, dm, dm), (dm, dm, R)]
+    shapes += [(R, ff, dm), (R, dm, ff), (dm, ff, R), (R, dm, ff), (R, ff, dm), (ff, dm, R)]
+    lin_us = event_ms(hip, linears, steps, warmup) * 1e3
+    lin_flops = sum(gemm_roof(*s)[0] for s in shapes)
+    lin_roof = sum(roofline_us(*gemm_roof(*s)) for s in shapes)
+    return {"fwd_us": fwd_us, "bwd_us": bwd_us, "bmm_us": bmm_us, "bmm_roof_us": bmm_roof,
+            "linear_us": lin_us, "linear_tflops": lin_flops / (lin_us * 1e-6) / 1e12,
+            "linear_roof_us": lin_roof}
+
+
+def bench_sweep_cfg5(hip, reps):
+    """cfg5 sweep: square NN GEMMs 2048^3 and 8192^3, skinny 32x8192x8192,
+    and the split-K weight-gradient NT shape 64x576 over K = 100352. Each is
+    spot-checked against f64 on a few rows."""
+    import oracle
+    rng = np.random.default_rng(5)
+    out = {}
+    cases = (("nn_2048", hip.NN, 2048, 2048, 2048), ("nn_8192", hip.NN, 8192, 8192, 8192),
+             ("skinny_32x8192x8192", hip.NN, 32, 8192, 8192),
+             ("wgrad_nt_64x576x100352", hip.NT, 64, 576, 100352))
+    for name, layout, m, n, k in cases:
+        a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+        b = rng.uniform(-1, 1, (k, n) if layout == hip.NN else (n, k)).astype(np.float32)
+        dA, dB, dC = hip.DeviceBuffer.from_host(a), hip.DeviceBuffer.from_host(b), hip.DeviceBuffer(m * n)
+        if layout == hip.NN:
+            fn = lambda: hip.gemm(hip.NN, dC, dA, dB, m, n, k)
+        else:
+            fn = lambda: hip.gemm_nt_splitk(dC, dA, dB, m, n, k)
+        r = max(2, reps if m * n * k < 2 ** 36 else reps // 10)
+        ms = event_ms(hip, fn, r, 2)
+        c = dC.to_host((m, n))
+        rows = np.arange(0, m, max(1, m // 4))
+        c64, ab = oracle.gemm_f64("nn" if layout == hip.NN else "nt", a, b, m, n, k, rowidx=rows)
+        err = float(np.max(np.abs(c[rows] - c64) / np.maximum(ab, 1e-30)))
+        fl, by = gemm_roof(m, n, k)
+        roof = roofline_us(fl, by)
+        out[name] = {"us": round(ms * 1e3, 2), "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+                     "bound": "hbm" if by / (PEAK_HBM_GBS * 1e9) > fl / (PEAK_FP32_MFMA_TFLOPS * 1e12) else "mfma",
+                     "roofline_frac": round(roof / (ms * 1e3), 4), "max_rel_err_vs_f64": err}
+        del dA, dB, dC
+    return out
 
 
 def cpu_baseline_gemm(a, b, target_s=10.0):
@@ -211,6 +415,8 @@ def main():
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-conv", action="store_true", help="skip the conv2d leg")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="skip the cfg2 / cfg4 / cfg5 legs (MLP step, attention, GEMM sweep)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="only launch a 256 MiB device copy (counter calibration) and then "
                          "--steps GEMMs, for rocprofv3 --pmc runs; prints nothing else")
@@ -252,15 +458,38 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
                      "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic,
-                     "kernel": "gemm_kernel<256,256,16,2,NN,vec4>",
+                     "kernel": "gemm_kernel 256x256x32 tile, 2x4 waves, NN",
                      "kernel_ms": round(g["kernel_ms"], 4)},
     }
     if not args.no_conv:
         c = bench_conv_cfg3(hip, max(5, args.steps // 2), args.warmup)
-        out["conv2d_fwd_bwd"] = {"value": round(c["imgs_per_s"], 1), "unit": "imgs/s",
-                                 "ms_per_step": round(c["ms_per_step"], 4),
-                                 "config": "cfg3 batch 128 conv1 1->32, maxpool, conv2 32->64, "
-                                           "fwd+bwd with input and weight grads"}
+        out["conv2d_fwd_bwd"] = {
+            "value": round(c["imgs_per_s"], 1), "unit": "imgs/s",
+            "ms_per_step": round(c["ms_per_step"], 4),
+            "config": "cfg3 batch 128 conv1 1->32, maxpool, conv2 32->64, "
+                      "fwd+bwd with input and weight grads",
+            "conv_fwd_us": round(c["fwd_us"], 2), "conv_bwd_us": round(c["bwd_us"], 2),
+            "fwd_roofline_us": round(c["fwd_roof_us"], 2),
+            "bwd_roofline_us": round(c["bwd_roof_us"], 2),
+            "fwd_roofline_frac": round(c["fwd_roof_us"] / c["fwd_us"], 4),
+            "bwd_roofline_frac": round(c["bwd_roof_us"] / c["bwd_us"], 4)}
+    if not args.no_legs:
+        m = bench_mlp_cfg2(hip, args.steps, 5)
+        out["mlp_cfg2"] = {"us_per_step": round(m["us_per_step"], 2),
+                           "tflops": round(m["tflops"], 3),
+                           "gemm_roofline_us": round(m["gemm_roof_us"], 3),
+                           "config": "cfg2 Linear 784->128, ReLU, Linear 128->10, batch 256, "
+                                     "softmax-CE grad, fwd+bwd incl. dx"}
+        at = bench_attention_cfg4(hip, args.steps, 5)
+        out["attention_cfg4"] = {
+            "bmm_us": round(at["bmm_us"], 2), "bmm_roofline_us": round(at["bmm_roof_us"], 2),
+            "bmm_roofline_frac": round(at["bmm_roof_us"] / at["bmm_us"], 4),
+            "attn_fwd_us": round(at["fwd_us"], 2), "attn_bwd_us": round(at["bwd_us"], 2),
+            "linear_us": round(at["linear_us"], 2), "linear_tflops": round(at["linear_tflops"], 2),
+            "linear_roofline_frac": round(at["linear_roof_us"] / at["linear_us"], 4),
+            "config": "cfg4 batch 32 x 8 heads, seq 128, d_head 32: 6 bmm (QK^T, PV and the 4 "
+                      "backward products) + 4 proj and 2 FFN Linear GEMMs fwd+bwd"}
+        out["gemm_sweep_cfg5"] = bench_sweep_cfg5(hip, args.steps)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_gemm(g["a"], g["b"])
     print(json.dumps(out), flush=True)

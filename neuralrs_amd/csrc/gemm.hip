@@ -54,16 +54,21 @@ KernelFn pick_conv(int layout, int amode, int bmode, bool vec4) {
 //    (bmm items, conv GEMMs, projections, split-K weight gradients);
 //  * 32x256x32, 4 waves of 32x64: outputs with at most 32 rows;
 //  * 32x128x32, 4 waves of 32x32, prefetch depth 2: convolutions whose GEMM
-//    has at most 32 rows (a 64-row tile would double the MFMA work).
-enum TileId { T256x256 = 0, T64x64, T32x256, T32x128, T_COUNT };
+//    has at most 32 rows (a 64-row tile would double the MFMA work);
+//  * 128x32x32, 4 waves of 32x32, prefetch depth 2: outputs with at most 32
+//    columns, e.g. attention's P.V and its input gradients (d_head 32).
+enum TileId { T256x256 = 0, T64x64, T32x256, T32x128, T128x32, T_COUNT };
 const TileShape kShapes[T_COUNT] = {
     {256, 256, 32, 512},
     {64, 64, 32, 256},
     {32, 256, 32, 256},
     {32, 128, 32, 256},
+    {128, 32, 32, 256},
 };
 
-KernelFn kernel_for(int tile, int layout, bool vec4, int amode, int bmode) {
+// `pf` is the register prefetch depth the plan asks for; tiles that have no
+// variant for it return nullptr.
+KernelFn kernel_for(int tile, int pf, int layout, bool vec4, int amode, int bmode) {
     if (amode != OP_DENSE || bmode != OP_DENSE) {
         switch (tile) {
             case T64x64: return pick_conv<64, 64, 32, 2, 2, 2>(layout, amode, bmode, vec4);
@@ -73,8 +78,13 @@ KernelFn kernel_for(int tile, int layout, bool vec4, int amode, int bmode) {
     }
     switch (tile) {
         case T256x256: return pick_layout<256, 256, 32, 2, 4, 1>(layout, vec4);
-        case T64x64: return pick_layout<64, 64, 32, 2, 2, 2>(layout, vec4);
+        case T64x64:
+            return pf == 1 ? pick_layout<64, 64, 32, 2, 2, 1>(layout, vec4)
+                           : pick_layout<64, 64, 32, 2, 2, 2>(layout, vec4);
         case T32x256: return pick_layout<32, 256, 32, 1, 4, 1>(layout, vec4);
+        case T128x32:
+            return pf == 1 ? pick_layout<128, 32, 32, 4, 1, 1>(layout, vec4)
+                           : pick_layout<128, 32, 32, 4, 1, 2>(layout, vec4);
         default: return nullptr;
     }
 }
@@ -87,21 +97,30 @@ struct Plan {
     int tile;
     int slices;
     int64_t k_per_slice;
+    int pf;  // register prefetch depth (k-tiles in flight per thread)
 };
 
 // Chooses the tile shape and the number of K slices. The 256x256 tile is
-// used only with 128-bit loads (its scalar-load variant spills).
+// used only with 128-bit loads (its scalar-load variant spills) and when at
+// least 85% of its tile grid is real output.
 Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool dense,
                bool allow_split, int force_slices) {
     const int cus = num_cus();
     auto tiles_of = [&](int t) {
         return cdiv(M, kShapes[t].bm) * cdiv(N, kShapes[t].bn) * batch;
     };
-    Plan pl{T64x64, 1, K};
+    // fraction of a tile grid's area that is real output (the rest is padding)
+    auto fill = [&](int t) {
+        return (double)(M * N) / ((double)cdiv(M, kShapes[t].bm) * kShapes[t].bm *
+                                  cdiv(N, kShapes[t].bn) * kShapes[t].bn);
+    };
+    Plan pl{T64x64, 1, K, 2};
     if (dense) {
         if (M <= 32 && N >= 256)
             pl.tile = T32x256;
-        else if (vec4 && tiles_of(T256x256) >= cus)
+        else if (N <= 32 && M >= 128 && vec4)  // its scalar-load variants spill
+            pl.tile = T128x32;
+        else if (vec4 && tiles_of(T256x256) >= cus && fill(T256x256) >= 0.85)
             pl.tile = T256x256;
     } else if (M <= 32) {  // gathered (convolution) operands: 64x64 or 32x128
         pl.tile = T32x128;
@@ -124,6 +143,9 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool d
     slices = (int)std::max<int64_t>(1, cdiv(K, kps));
     pl.slices = slices;
     pl.k_per_slice = kps;
+    // Prefetch depth of the mid-size dense tiles (the k loop is padded to a
+    // multiple of it): a single k-tile runs unpadded at depth 1.
+    if (dense && (pl.tile == T64x64 || pl.tile == T128x32) && cdiv(kps, s.bk) <= 1) pl.pf = 1;
     return pl;
 }
 
@@ -204,7 +226,7 @@ int gemm_run(const GemmCall& c) {
     NRS_ARG_CHECK((int64_t)p.tiles_m * p.tiles_n <= INT32_MAX && batch <= 65535,
                   "gemm: grid too large");
 
-    KernelFn fn = kernel_for(pl.tile, layout, vec4, c.amode, c.bmode);
+    KernelFn fn = kernel_for(pl.tile, pl.pf, layout, vec4, c.amode, c.bmode);
     NRS_ARG_CHECK(fn != nullptr, "gemm: no kernel for layout %d with operand modes %d/%d", layout,
                   c.amode, c.bmode);
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)pl.slices, (unsigned)batch);

@@ -43,6 +43,7 @@ SHAPES = [  # (rows, cols, inner)
     (1, 1, 1), (2, 2, 2), (5, 7, 11), (17, 9, 5), (40, 32, 56), (64, 64, 16), (33, 65, 129),
     (128, 256, 64), (256, 128, 784), (100, 10, 9), (256, 10, 128), (300, 300, 300),
     (512, 512, 512), (32, 1024, 512), (1, 513, 257), (1000, 3, 2),
+    (130, 17, 33), (257, 32, 96),  # at most 32 columns: 128x32 tiles, ragged rows
 ]
 
 
@@ -204,7 +205,11 @@ def test_bmm_twin(hip, orc):
 
 
 @pytest.mark.parametrize("shape", [(3, 5, 7, 4), (256, 128, 128, 32), (256, 128, 32, 128),
-                                   (8, 33, 17, 65)], ids=lambda s: "x".join(map(str, s)))
+                                   (8, 33, 17, 65),
+                                   # LDS-staged items: K split over waves with empty parts,
+                                   # 9 blocks (a wave takes two), 16 blocks with K = 128
+                                   (4, 36, 20, 12), (2, 96, 96, 40), (4, 128, 128, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
 def test_bmm_exact_integers(hip, shape):
     """cfg4 per-head shapes folded into one batch (256 = 32 x 8 heads)."""
     bt, m, n, k = shape
