@@ -472,47 +472,6 @@ __global__ __launch_bounds__(64 * kWgradWaves) void conv_wgrad_small_kernel(
     }
 }
 
-// out[e] = sum over s of part[s * total + e] + beta * out[e]. The slices are
-// split into kSliceGroups contiguous groups summed in parallel (ascending s
-// inside a group, loads batched), then the group sums are added in group
-// order, so the result is deterministic.
-constexpr int kSliceGroups = 16;
-
-__global__ __launch_bounds__(64 * kSliceGroups) void slice_sum_kernel(float* __restrict__ out,
-                                                                      const float* __restrict__ part,
-                                                                      int slices, int total,
-                                                                      float beta) {
-    __shared__ float red[kSliceGroups][64];
-    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    const int per = (slices + kSliceGroups - 1) / kSliceGroups;
-    const int s0 = min(slices, ty * per), s1 = min(slices, s0 + per);
-    for (int base = blockIdx.x * 64; base < total; base += gridDim.x * 64) {
-        const int e = base + tx;
-        float v = 0.0f;
-        if (e < total) {
-            int s = s0;
-            for (; s + 8 <= s1; s += 8) {
-                float t[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) t[u] = part[(int64_t)(s + u) * total + e];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) v += t[u];
-            }
-            for (; s < s1; ++s) v += part[(int64_t)s * total + e];
-        }
-        red[ty][tx] = v;
-        __syncthreads();
-        if (ty == 0 && e < total) {
-            float r = red[0][tx];
-#pragma unroll
-            for (int y = 1; y < kSliceGroups; ++y) r += red[y][tx];
-            if (beta != 0.0f) r = r + beta * out[e];
-            out[e] = r;
-        }
-        __syncthreads();
-    }
-}
-
 // out[ni, oc, p] = mm[oc, ni*P + p] + bias[oc]
 __global__ __launch_bounds__(256) void col2out_kernel(float* __restrict__ out,
                                                       const float* __restrict__ mm,
@@ -799,20 +758,9 @@ int small_wgrad(float* dweight, float* dbias, const float* grad, const float* in
                        (int)d.kh, (int)d.kw, (int)d.stride, (int)d.pad,
                        make_fastdiv((uint32_t)d.out_w), (int)P);
     NRS_LAUNCH_CHECK("conv2d weight gradient (small)");
-    if (dweight) {
-        const int64_t total = d.c_out * taps;
-        hipLaunchKernelGGL(slice_sum_kernel, dim3((unsigned)((total + 63) / 64)),
-                           dim3(64 * kSliceGroups), 0, stream(), dweight, pw, (int)d.N, (int)total,
-                           1.0f);
-        NRS_LAUNCH_CHECK("conv2d weight gradient (sum)");
-    }
-    if (dbias) {
-        hipLaunchKernelGGL(slice_sum_kernel, dim3((unsigned)((d.c_out + 63) / 64)),
-                           dim3(64 * kSliceGroups), 0, stream(), dbias, pb, (int)d.N, (int)d.c_out,
-                           1.0f);
-        NRS_LAUNCH_CHECK("conv2d bias gradient (sum)");
-    }
-    return NRS_OK;
+    // the per-image partials are [n][oc][taps]: the slab layout with one
+    // channel of `taps` taps; weights and bias summed in one launch
+    return wgrad_partial_sum(dweight, dbias, pw, pb, (int)d.N, (int)d.c_out, 1, (int)taps);
 }
 
 // dinput += the stride-1 input gradient as a slab convolution of the output

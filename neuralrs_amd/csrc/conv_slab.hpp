@@ -45,4 +45,10 @@ struct SlabWgrad {
 };
 int slab_wgrad(const SlabWgrad& s);
 
+// dw[m][c][tap] += sum over slices of part_w[slice][m][tap][c] (when dw is
+// given) and db[m] += sum over slices of part_b[slice][m] (when db is given),
+// the slices added in a fixed order; one launch.
+int wgrad_partial_sum(float* dw, float* db, const float* part_w, const float* part_b, int slices,
+                      int M, int C, int taps);
+
 }  // namespace nrs

@@ -317,10 +317,17 @@ int slab_wgrad(const SlabWgrad& s) {
                        dim3(256), lds, stream(), a);
     NRS_LAUNCH_CHECK("conv2d weight gradient (slab)");
     // dW and (when requested) dB from the partials
-    const int64_t total = nw + (s.db ? s.M : 0);
+    return wgrad_partial_sum(s.dw, s.db, part, part + slices * nw, (int)slices, s.M, s.C,
+                             (int)taps);
+}
+
+int wgrad_partial_sum(float* dw, float* db, const float* part_w, const float* part_b, int slices,
+                      int M, int C, int taps) {
+    const int64_t total = (dw ? (int64_t)M * taps * C : 0) + (db ? M : 0);
+    if (total == 0) return NRS_OK;
     hipLaunchKernelGGL(wgrad_sum_kernel, dim3((unsigned)((total + 63) / 64)),
-                       dim3(64 * kSumGroups), 0, stream(), s.dw, s.db, part,
-                       part + slices * nw, (int)slices, s.M, s.C, (int)taps);
+                       dim3(64 * kSumGroups), 0, stream(), dw, db, part_w, part_b, slices, M, C,
+                       taps);
     NRS_LAUNCH_CHECK("conv2d weight gradient (sum)");
     return NRS_OK;
 }
