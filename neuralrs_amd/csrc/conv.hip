@@ -267,12 +267,14 @@ __global__ __launch_bounds__(256) void conv_dgrad_direct_kernel(
 // adjacent pixels of one row. Per chunk of `occ` output channels the block
 // stages the output-gradient rows the band's windows touch (band + kh - 1
 // rows of `pitch` floats, zero outside the gradient) and the chunk's weights
-// flipped along the row, wf[o][i][jj][c] = W[oc0+o, c, i, KW-1-jj]. Then for
-// each (oc, i) a thread reads the kDgradRun + KW - 1 gradient values its
-// pixels' windows share once and forms
+// flipped along the row, wf[o][i][jj][c] = W[oc0+o, c, i, KW-1-jj]. The
+// workgroup's threads form `groups` channel groups over the same pixel runs
+// (more waves busy when a band has few runs); for each (oc, i) of its
+// channels a thread reads the kDgradRun + KW - 1 gradient values its pixels'
+// windows share once and forms
 //   dinput[c, y, x] += grad[oc, y + pad - i, x + pad - KW + 1 + jj] * wf[oc][i][jj][c]
-// for all its pixels (the reference's sum over (oc, i, j), j = KW-1-jj).
-// dinput = that sum + dinput. KW is the exact kernel width and CIN covers
+// for all its pixels (the reference's sum over (oc, i, j), j = KW-1-jj);
+// the groups' sums are added in group order. dinput = that sum + dinput. KW is the exact kernel width and CIN covers
 // c_in (1, or 4 with zero weights past c_in).
 constexpr int kDgradRun = 4, kDgradStage = 16;
 
@@ -280,8 +282,8 @@ template <int KW, int CIN>
 __global__ __launch_bounds__(256) void conv_dgrad_small_kernel(
     float* __restrict__ dinput, const float* __restrict__ grad, const float* __restrict__ weight,
     int c_in, int in_h, int in_w, int c_out, int kh, int pad, int out_h, int out_w, int band,
-    int bands, int occ, int ngx, int pitch, FastDiv div_ngx, FastDiv div_pitch,
-    FastDiv div_tile) {
+    int bands, int occ, int ngx, int pitch, int groups, int tpg, FastDiv div_ngx,
+    FastDiv div_pitch, FastDiv div_tile) {
     constexpr int NG = kDgradRun + KW - 1;  // gradient values per (oc, i)
     // [occ][gr][pitch] gradient tile, then the chunk's flipped weights
     extern __shared__ __attribute__((aligned(16))) float gt[];
@@ -291,8 +293,12 @@ __global__ __launch_bounds__(256) void conv_dgrad_small_kernel(
     const int oy_base = y0 + pad - (kh - 1), ox_base = pad - (KW - 1);
     const int P = out_h * out_w, HW = in_h * in_w;
     const float* gimg = grad + (int64_t)n * c_out * P;
+    // `groups` channel groups of tpg threads (whole waves) cover the same
+    // pixel runs, each over its share of every chunk's output channels
+    const int grp = __builtin_amdgcn_readfirstlane((int)threadIdx.x / tpg);
+    const int tig = (int)threadIdx.x - grp * tpg;
     uint32_t yy, xg;
-    fast_divmod(threadIdx.x, div_ngx, yy, xg);
+    fast_divmod((uint32_t)tig, div_ngx, yy, xg);
     const bool live = (int)yy < rows;
     const int x0 = (int)xg * kDgradRun;
     // this thread's tile row for kernel row i is yy + kh - 1 - i
@@ -332,15 +338,17 @@ __global__ __launch_bounds__(256) void conv_dgrad_small_kernel(
             for (int c = 0; c < CIN; ++c) wsh[e * CIN + c] = c < c_in ? w[(int64_t)c * kh * KW] : 0.0f;
         }
         __syncthreads();
+        const int per = (nch + groups - 1) / groups;
+        const int o_lo = min(nch, grp * per), o_hi = min(nch, o_lo + per);
         if (live) {
-            // (o, i) steps in order; the gradient row pointer moves up one
-            // row per kernel row and to the next channel's tile after kh
-            // rows, the weights are contiguous per step
-            const float* g = gt + tbase;
-            const float* w = wsh;
+            // (o, i) steps in order over this group's channels; the gradient
+            // row pointer moves up one row per kernel row and to the next
+            // channel's tile after kh rows, the weights are contiguous per step
+            const float* g = gt + o_lo * tile + tbase;
+            const float* w = wsh + o_lo * kh * KW * CIN;
             int i = 0;
 #pragma unroll 4
-            for (int oi = 0; oi < nch * kh; ++oi) {
+            for (int oi = o_lo * kh; oi < o_hi * kh; ++oi) {
                 float gv[NG];
 #pragma unroll
                 for (int q = 0; q < NG; ++q) gv[q] = g[q];
@@ -361,6 +369,25 @@ __global__ __launch_bounds__(256) void conv_dgrad_small_kernel(
                 }
             }
         }
+    }
+    if (groups > 1) {
+        // the groups' partial sums, added in group order by group 0
+        __syncthreads();  // every group is done reading the tiles
+        float* red = gt;   // [groups][tpg][kDgradRun][CIN]
+#pragma unroll
+        for (int r = 0; r < kDgradRun; ++r)
+#pragma unroll
+            for (int c = 0; c < CIN; ++c) red[((grp * tpg + tig) * kDgradRun + r) * CIN + c] = acc[r][c];
+        __syncthreads();
+        if (grp != 0) return;
+#pragma unroll
+        for (int r = 0; r < kDgradRun; ++r)
+#pragma unroll
+            for (int c = 0; c < CIN; ++c) {
+                float v = red[(tig * kDgradRun + r) * CIN + c];
+                for (int g2 = 1; g2 < groups; ++g2) v += red[((g2 * tpg + tig) * kDgradRun + r) * CIN + c];
+                acc[r][c] = v;
+            }
     }
     if (!live) return;
     float* drow = dinput + (int64_t)n * c_in * HW + (y0 + (int)yy) * in_w + x0;
@@ -713,10 +740,17 @@ int small_dgrad(float* dinput, const float* grad, const float* weight, const Con
         d.c_out * d.out_h * d.out_w > INT32_MAX || d.in_h * d.in_w > INT32_MAX)
         return kSlabUnsupported;
     const int64_t occ = std::min<int64_t>(d.c_out, (limit - 3) / per_ch);
-    const size_t lds = (size_t)(((occ * tile + 3) & ~3ll) + occ * 4 * d.kh * d.kw) * 4;
+    // channel groups: whole waves of threads per group, enough for the runs
+    const int64_t runs = band * ngx;
+    int groups = 4;
+    while (groups > 1 && (256 / groups < runs || groups > d.c_out)) groups /= 2;
+    const int tpg = 256 / groups;
+    const int64_t red = (int64_t)groups * tpg * kDgradRun * 4;  // group partials, CIN <= 4
+    const size_t lds = (size_t)std::max<int64_t>(((occ * tile + 3) & ~3ll) + occ * 4 * d.kh * d.kw,
+                                                 groups > 1 ? red : 0) * 4;
     const bool c1 = d.c_in == 1;
     void (*fn)(float*, const float*, const float*, int, int, int, int, int, int, int, int, int,
-               int, int, int, int, FastDiv, FastDiv, FastDiv) = nullptr;
+               int, int, int, int, int, int, FastDiv, FastDiv, FastDiv) = nullptr;
     switch (d.kw) {
         case 1: fn = c1 ? conv_dgrad_small_kernel<1, 1> : conv_dgrad_small_kernel<1, 4>; break;
         case 2: fn = c1 ? conv_dgrad_small_kernel<2, 1> : conv_dgrad_small_kernel<2, 4>; break;
@@ -728,7 +762,7 @@ int small_dgrad(float* dinput, const float* grad, const float* weight, const Con
     hipLaunchKernelGGL(fn, dim3((unsigned)(d.N * bands)), dim3(256), lds, stream(), dinput, grad,
                        weight, (int)d.c_in, (int)d.in_h, (int)d.in_w, (int)d.c_out, (int)d.kh,
                        (int)d.pad, (int)d.out_h, (int)d.out_w, (int)band, (int)bands, (int)occ,
-                       (int)ngx, (int)pitch, make_fastdiv((uint32_t)ngx),
+                       (int)ngx, (int)pitch, groups, tpg, make_fastdiv((uint32_t)ngx),
                        make_fastdiv((uint32_t)pitch), make_fastdiv((uint32_t)tile));
     NRS_LAUNCH_CHECK("conv2d input gradient (small)");
     return NRS_OK;
