@@ -374,6 +374,61 @@ def cpu_baseline_gemm(a, b, target_s=10.0):
                       f"does), {dt:.1f} s"}
 
 
+def cpu_baseline_extra():
+    """BASELINE's CPU plan beside the GEMM baseline: host CPU model, the
+    oracle's matmul_simd at 512^3 (cfg1) on all threads and on one, and the
+    cfg3 conv layers forward + backward (C restatement of nn::conv::Conv2d,
+    OpenMP over images) on a bounded 16-image sample, in imgs/s."""
+    import oracle
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    threads = oracle.max_threads()
+    rng = np.random.default_rng(1)
+    a = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    b = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    out = {"host_cpu": model, "threads": threads}
+    for nt, key in ((0, "matmul_simd_512_gflops"), (1, "matmul_simd_512_gflops_1thread")):
+        oracle.matmul_simd(a, b, nt)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 1.0:
+            oracle.matmul_simd(a, b, nt)
+            reps += 1
+        out[key] = round(2.0 * 512 ** 3 * reps / (time.perf_counter() - t0) / 1e9, 2)
+    n = 16
+    x = rng.uniform(0, 1, n * 784).astype(np.float32)
+    w1 = (rng.standard_normal(32 * 9) * np.sqrt(2.0 / 9)).astype(np.float32)
+    w2 = (rng.standard_normal(64 * 288) * np.sqrt(2.0 / 288)).astype(np.float32)
+    b1, b2 = np.zeros(32, np.float32), np.zeros(64, np.float32)
+    p1 = rng.uniform(0, 1, n * 32 * 196).astype(np.float32)   # pooled conv1 output
+    g2 = rng.standard_normal(n * 64 * 196).astype(np.float32)
+    g1 = rng.standard_normal(n * 32 * 784).astype(np.float32)
+
+    def layers():
+        oracle.conv2d_forward(x, w1, b1, n, 1, 32, 28, 28, 3, 3, 1, 1)
+        oracle.conv2d_forward(p1, w2, b2, n, 32, 64, 14, 14, 3, 3, 1, 1)
+        oracle.conv2d_backward(p1, w2, g2, n, 32, 64, 14, 14, 3, 3, 1, 1)
+        oracle.conv2d_backward(x, w1, g1, n, 1, 32, 28, 28, 3, 3, 1, 1)
+
+    layers()
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 3.0:
+        layers()
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    out["conv_cfg3_imgs_per_s"] = round(n / dt, 1)
+    out["conv_cfg3_sample"] = (f"{n} images of cfg3 (conv1 1->32 @28x28, conv2 32->64 @14x14, "
+                               f"forward + backward with input, weight and bias grads), "
+                               f"{reps} reps, {dt * 1e3:.1f} ms each")
+    return out
+
+
 COPY_BYTES = 256 << 20
 
 
@@ -492,6 +547,7 @@ def main():
         out["gemm_sweep_cfg5"] = bench_sweep_cfg5(hip, args.steps)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_gemm(g["a"], g["b"])
+        out["cpu_baseline_extra"] = cpu_baseline_extra()
     print(json.dumps(out), flush=True)
 
 
