@@ -1,0 +1,184 @@
+// Batched products of small matrices on the f32 matrix cores
+// (v_mfma_f32_32x32x2f32): the per-item bmm of src/cuda/graph/bmm.rs:12-56
+// (forward NN, grad_a NT, grad_b TN) for items of at most 128x128 outputs
+// and K <= 128, e.g. attention's per-head Q.K^T, P.V and their gradients.
+//
+// These products are short: ~17 MB of traffic and ~1.7 us of f32
+// matrix-core work over the whole chip, and a memory round trip under that
+// load costs microseconds. Measured on MI355X, one round trip per wave beats
+// every staged or pipelined form (LDS staging, phased loads with two phases
+// in flight, K split over waves), so the kernel is built around it:
+//  * a wave owns one 32-row block and JB 32-column blocks of an item and
+//    issues every load of its fragments at once: an operand whose reduction
+//    dim is contiguous in memory as 128-bit buffer loads, the other kind
+//    four bytes per lane (a half-wave reads one 128-byte row segment);
+//    the MFMA chain then consumes them in issue order;
+//  * the output is written with non-temporal stores: the 16.8 MB score
+//    matrices of attention would otherwise evict the operands from L2
+//    (Q.K^T: 8.8 -> 6.9 us);
+//  * reduction-dim padding (k >= K) and rows or columns past M and N read
+//    zero through the buffer bounds; only rows < M and columns < N are
+//    stored.
+//
+// MFMA mapping: lane half h takes k = 8g + 4h + p (p = 0..3), so one 128-bit
+// fragment load feeds four MFMAs; accumulator element e holds row
+// 8*(e/4) + 4h + e%4, column lane%32 of the block.
+#include "buffer_ops.hpp"
+#include "gemm_call.hpp"
+
+namespace nrs {
+namespace {
+
+typedef float f32x16v __attribute__((ext_vector_type(16)));
+
+constexpr int kSmallMax = 128;  // M, N and K limits of an item
+
+struct SmallArgs {
+    const float* A;
+    const float* B;
+    float* C;
+    int64_t sA, sB, sC;  // item strides (elements)
+    int M, N, K;
+    int NJ;              // waves per row block (ceil(column blocks / JB))
+    int waves;           // waves per item (row blocks * NJ)
+    int wg_per_item;
+    float beta;
+};
+
+// Fragment g of an operand for the lane's row r (m or n): k = 8g + 4h .. +3.
+// KC: stored [rows][K] (reduction contiguous), else [K][rows].
+template <bool KC>
+__device__ __forceinline__ f32x4 fragment(__amdgpu_buffer_rsrc_t rs, int r, int R, int K, int g,
+                                          int h) {
+    const int k = 8 * g + 4 * h;
+    if (KC) return buffer_load4(rs, (r < R) & (k < K) ? (r * K + k) * 4 : kOutOfRange);
+    f32x4 v;
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+        v[p] = buffer_load1(rs, (r < R) & (k + p < K) ? ((k + p) * R + r) * 4 : kOutOfRange);
+    return v;
+}
+
+template <bool AK, bool BKC, int G, int JB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void bmm_small_kernel(SmallArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l32 = lane & 31, h = lane >> 5;
+    const int item = blockIdx.x / a.wg_per_item;
+    const int wi = (blockIdx.x - item * a.wg_per_item) * 4 + wave;
+    if (wi >= a.waves) return;  // wave-uniform; no barriers follow
+    const int bm = wi / a.NJ, bn0 = (wi - bm * a.NJ) * JB;
+    const int m = 32 * bm + l32;
+    const auto ra = buffer_rsrc(a.A + item * a.sA, (int64_t)a.M * a.K * 4);
+    const auto rb = buffer_rsrc(a.B + item * a.sB, (int64_t)a.N * a.K * 4);
+
+    f32x4 af[G], bf[JB][G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        af[g] = fragment<AK>(ra, m, a.M, a.K, g, h);
+#pragma unroll
+        for (int j = 0; j < JB; ++j)
+            bf[j][g] = fragment<BKC>(rb, 32 * (bn0 + j) + l32, a.N, a.K, g, h);
+    }
+    // keep the loads ahead of the MFMA chain (left alone, the scheduler
+    // interleaves them to save registers, which costs a round trip each)
+    __builtin_amdgcn_sched_barrier(0);
+    // every MFMA chain before any store: vmcnt counts stores too, so a wait
+    // for a fragment issued after a store would also wait for the store
+    f32x16v acc[JB];
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+        acc[j] = f32x16v{};
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[g][p], bf[j][g][p], acc[j], 0, 0, 0);
+    }
+    float* c = a.C + item * a.sC;
+    const int row0 = 32 * bm + 4 * h;
+    if (a.beta == 0.0f) {
+#pragma unroll
+        for (int j = 0; j < JB; ++j) {
+            const int n = 32 * (bn0 + j) + l32;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = row0 + 8 * (e >> 2) + (e & 3);
+                if (row < a.M && n < a.N)
+                    __builtin_nontemporal_store(acc[j][e], c + (int64_t)row * a.N + n);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < JB; ++j) {
+            const int n = 32 * (bn0 + j) + l32;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = row0 + 8 * (e >> 2) + (e & 3);
+                if (row < a.M && n < a.N) {
+                    float* dst = c + (int64_t)row * a.N + n;
+                    __builtin_nontemporal_store(acc[j][e] + a.beta * *dst, dst);
+                }
+            }
+        }
+    }
+}
+
+template <bool AK, bool BKC, int JB>
+void* pick_g(int G) {
+    return G <= 4   ? reinterpret_cast<void*>(bmm_small_kernel<AK, BKC, 4, JB>)
+           : G <= 8 ? reinterpret_cast<void*>(bmm_small_kernel<AK, BKC, 8, JB>)
+                    : reinterpret_cast<void*>(bmm_small_kernel<AK, BKC, 16, JB>);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+int bmm_small(const GemmCall& c) {
+    const int64_t M = c.M, N = c.N, K = c.K, batch = c.batch;
+    // anything unusual (including invalid arguments, which gemm_run reports)
+    // goes to the general path
+    if (c.layout < NRS_NN || c.layout > NRS_TN || !c.A || !c.B || !c.C || c.amode != OP_DENSE ||
+        c.bmode != OP_DENSE || c.nchw_P != 0 || c.epi != NRS_EPI_NONE)
+        return kBmmUnsupported;
+    if (M < 1 || N < 1 || K < 1 || M > kSmallMax || N > kSmallMax || K > kSmallMax || batch < 1)
+        return kBmmUnsupported;
+    const bool AK = c.layout != NRS_TN, BKC = c.layout == NRS_NT;
+    // 128-bit fragment loads need 16-byte aligned rows of whole float4s
+    if (AK && (!aligned16(c.A) || c.sA % 4 || K % 4)) return kBmmUnsupported;
+    if (BKC && (!aligned16(c.B) || c.sB % 4 || K % 4)) return kBmmUnsupported;
+    const int MB = (int)((M + 31) / 32), NB = (int)((N + 31) / 32);
+    // two column blocks per wave for NT (its A fragments are then loaded
+    // once for both): measured 6.9 vs 7.2 us on attention's Q.K^T
+    const int JB = (c.layout == NRS_NT && NB >= 2) ? 2 : 1;
+    const int G = (int)((K + 7) / 8);
+    SmallArgs a;
+    a.A = c.A;
+    a.B = c.B;
+    a.C = c.C;
+    a.sA = c.sA;
+    a.sB = c.sB;
+    a.sC = c.sC;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.NJ = (NB + JB - 1) / JB;
+    a.waves = MB * a.NJ;
+    a.wg_per_item = (a.waves + 3) / 4;
+    a.beta = c.beta;
+    if (batch * a.wg_per_item > INT32_MAX) return kBmmUnsupported;
+    void* fn;
+    switch (c.layout) {
+        case NRS_NN: fn = pick_g<true, false, 1>(G); break;
+        case NRS_NT: fn = JB == 2 ? pick_g<true, true, 2>(G) : pick_g<true, true, 1>(G); break;
+        default: fn = pick_g<false, false, 1>(G); break;
+    }
+    hipLaunchKernelGGL(reinterpret_cast<void (*)(SmallArgs)>(fn),
+                       dim3((unsigned)(batch * a.wg_per_item)), dim3(256), 0, stream(), a);
+    NRS_LAUNCH_CHECK("bmm (small items)");
+    return NRS_OK;
+}
+
+}  // namespace nrs

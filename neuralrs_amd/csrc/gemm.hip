@@ -303,7 +303,8 @@ int nrs_bmm(int layout, float* C, const float* A, const float* B, int64_t batch,
     c.sC = rows * cols;
     c.beta = beta;
     c.allow_split = false;
-    return nrs::gemm_run(c);
+    const int rc = nrs::bmm_small(c);
+    return rc == nrs::kBmmUnsupported ? nrs::gemm_run(c) : rc;
 }
 
 }  // extern "C"

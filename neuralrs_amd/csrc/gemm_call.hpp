@@ -50,4 +50,10 @@ struct GemmCall {
 
 int gemm_run(const GemmCall& c);
 
+// Batched products of small dense items (M, N, K <= 128, 16-byte aligned
+// items, K or the transposed operand's rows in whole float4s), without
+// epilogue; returns kBmmUnsupported (launching nothing) for any other call.
+constexpr int kBmmUnsupported = -1;
+int bmm_small(const GemmCall& c);
+
 }  // namespace nrs

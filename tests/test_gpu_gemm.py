@@ -230,3 +230,25 @@ def test_bmm_exact_integers(hip, shape):
     hip.bmm(TN, gB, dA, dG, bt, k, n, m)
     assert np.array_equal(gB.to_host((bt, k, n)),
                           np.matmul(ai.transpose(0, 2, 1), gi).astype(np.float32))
+
+
+@pytest.mark.parametrize("shape", [(5, 40, 36, 24), (3, 20, 13, 8), (2, 128, 128, 100),
+                                   (7, 1, 4, 4), (3, 128, 64, 128), (6, 32, 32, 32),
+                                   (2, 68, 100, 36)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("layout", [NN, NT, TN], ids=lambda l: LNAME[l])
+def test_bmm_small_items_accumulate(hip, layout, shape):
+    """Items of at most 128x128x128 (the register-direct path when the item
+    rows are whole float4s, the tiled path otherwise), accumulated into a
+    non-zero C with beta 0.5: exact in f32 for these small integers."""
+    bt, m, n, k = shape
+    rng = np.random.default_rng(sum(shape) + 7 * layout)
+    a = int_matrix(rng, (bt, m, k) if layout != TN else (bt, k, m), -3, 3)
+    b = int_matrix(rng, (bt, k, n) if layout != NT else (bt, n, k), -3, 3)
+    c0 = int_matrix(rng, (bt, m, n), -8, 8)
+    A = a.astype(np.int64) if layout != TN else a.astype(np.int64).transpose(0, 2, 1)
+    B = b.astype(np.int64) if layout != NT else b.astype(np.int64).transpose(0, 2, 1)
+    want = (np.matmul(A, B) + 0.5 * c0).astype(np.float32)
+    dA, dB, dC = (hip.DeviceBuffer.from_host(x) for x in (a, b, c0))
+    hip.bmm(layout, dC, dA, dB, bt, m, n, k, 0.5)
+    assert np.array_equal(dC.to_host((bt, m, n)), want)
