@@ -26,6 +26,7 @@
 //    replacing the reference's three accumulate passes.
 #include <algorithm>
 
+#include "buffer_ops.hpp"
 #include "conv_slab.hpp"
 #include "gemm_call.hpp"
 
@@ -276,14 +277,14 @@ __global__ __launch_bounds__(256) void conv_dgrad_direct_kernel(
 // for all its pixels (the reference's sum over (oc, i, j), j = KW-1-jj);
 // the groups' sums are added in group order. dinput = that sum + dinput. KW is the exact kernel width and CIN covers
 // c_in (1, or 4 with zero weights past c_in).
-constexpr int kDgradRun = 4, kDgradStage = 16;
+constexpr int kDgradRun = 4, kDgradStage = 12, kDgradWStage = 2;
 
 template <int KW, int CIN>
 __global__ __launch_bounds__(256) void conv_dgrad_small_kernel(
     float* __restrict__ dinput, const float* __restrict__ grad, const float* __restrict__ weight,
     int c_in, int in_h, int in_w, int c_out, int kh, int pad, int out_h, int out_w, int band,
     int bands, int occ, int ngx, int pitch, int groups, int tpg, FastDiv div_ngx,
-    FastDiv div_pitch, FastDiv div_tile) {
+    FastDiv div_kh) {
     constexpr int NG = kDgradRun + KW - 1;  // gradient values per (oc, i)
     // [occ][gr][pitch] gradient tile, then the chunk's flipped weights
     extern __shared__ __attribute__((aligned(16))) float gt[];
@@ -305,32 +306,91 @@ __global__ __launch_bounds__(256) void conv_dgrad_small_kernel(
     const int tbase = ((live ? (int)yy : 0) + kh - 1) * pitch + x0;
     float acc[kDgradRun][CIN] = {};
     float* wsh = gt + ((occ * tile + 3) & ~3);
+    // the input-gradient values this thread adds to (group 0 writes them),
+    // loaded now so the final stores do not wait on a memory round trip
+    float* drow = dinput + (int64_t)n * c_in * HW + (y0 + (live ? (int)yy : 0)) * in_w + x0;
+    float old[kDgradRun][CIN];
+#pragma unroll
+    for (int c = 0; c < CIN; ++c)
+#pragma unroll
+        for (int r = 0; r < kDgradRun; ++r) {
+            const bool ok = live & (grp == 0) & (c < c_in) & (x0 + r < in_w);
+            const float v = *(ok ? drow + (int64_t)c * HW + r : dinput);
+            old[r][c] = ok ? v : 0.0f;
+        }
+    // this thread's staging items e = tid + k*256 over (channel, tile row,
+    // column quad): its first item's position, and the advance of 256 items
+    // as whole channels, rows and quads, applied with carries (no division
+    // per item: a wave64 VALU instruction costs four cycles, and a division
+    // some forty of them)
+    const int quads = pitch >> 2, slots = gr * quads;
+    const int ch_step = 256 / slots, slot_step = 256 - ch_step * slots;
+    const int r_step = slot_step / quads, c4_step = slot_step - r_step * quads;
+    const int ch_t = (int)threadIdx.x / slots, slot_t = (int)threadIdx.x - ch_t * slots;
+    const int r_t = slot_t / quads, c4_t = slot_t - r_t * quads;
     for (int oc0 = 0; oc0 < c_out; oc0 += occ) {
         const int nch = min(occ, c_out - oc0);
         if (oc0) __syncthreads();
-        const int items = nch * tile;
-        for (int b0 = threadIdx.x; b0 < items; b0 += blockDim.x * kDgradStage) {
-            float v[kDgradStage];
+        const int items = nch * slots;
+        // the chunk's flipped weights wf[o][i][jj][c]: up to kDgradWStage
+        // entries per thread, loaded alongside the gradient rows
+        const int wn = nch * kh * KW;  // (o, i, jj)
+        float wv[kDgradWStage][CIN];
 #pragma unroll
-            for (int u = 0; u < kDgradStage; ++u) {
-                const int e = b0 + u * blockDim.x;
-                uint32_t ch, rc, r, c;
-                fast_divmod((uint32_t)min(e, items - 1), div_tile, ch, rc);
-                fast_divmod(rc, div_pitch, r, c);
-                const int oy = oy_base + (int)r, ox = ox_base + (int)c;
-                const bool ok = (e < items) & ((int)c < gw) & ((unsigned)oy < (unsigned)out_h) &
-                                ((unsigned)ox < (unsigned)out_w);
-                const float g = gimg[ok ? (int64_t)(oc0 + (int)ch) * P + oy * out_w + ox : 0];
-                v[u] = ok ? g : 0.0f;
-            }
+        for (int k = 0; k < kDgradWStage; ++k) {
+            const int e = (int)threadIdx.x + k * 256;
+            const int ee = min(e, wn - 1);
+            const int oi = ee / KW, jj = ee - oi * KW;  // KW is a constant
+            const int o = (int)fast_div((uint32_t)oi, div_kh), i = oi - o * kh;
+            const float* w = weight + ((int64_t)(oc0 + o) * c_in * kh + i) * KW + (KW - 1 - jj);
 #pragma unroll
-            for (int u = 0; u < kDgradStage; ++u) {
-                const int e = b0 + u * blockDim.x;
-                if (e < items) gt[e] = v[u];
+            for (int c = 0; c < CIN; ++c) {
+                const bool ok = (e < wn) & (c < c_in);
+                const float v = *(ok ? w + (int64_t)c * kh * KW : weight);
+                wv[k][c] = ok ? v : 0.0f;
             }
         }
-        const int wn = nch * kh * KW;  // (o, i, jj)
-        for (int e = threadIdx.x; e < wn; e += blockDim.x) {
+        // the chunk's gradient rows: every load of a batch before its stores
+        int ch = ch_t, r = r_t, c4 = c4_t;
+        for (int b0 = 0; b0 < items; b0 += 256 * kDgradStage) {
+            f32x4 v[kDgradStage];
+            int dst[kDgradStage];
+#pragma unroll
+            for (int u = 0; u < kDgradStage; ++u) {
+                dst[u] = -1;
+                if (b0 + u * 256 < items) {  // uniform
+                    const int oy = oy_base + r, ox = ox_base + 4 * c4;
+                    const bool row_ok = (ch < nch) & ((unsigned)oy < (unsigned)out_h);
+                    const float* src = gimg + (int64_t)(oc0 + min(ch, nch - 1)) * P + oy * out_w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const bool ok = row_ok & ((unsigned)(ox + e) < (unsigned)out_w) &
+                                        (4 * c4 + e < gw);
+                        const float g = *(ok ? src + ox + e : gimg);
+                        v[u][e] = ok ? g : 0.0f;
+                    }
+                    if (ch < nch) dst[u] = ch * tile + r * pitch + 4 * c4;
+                }
+                c4 += c4_step;
+                int carry = c4 >= quads;
+                c4 -= carry ? quads : 0;
+                r += r_step + carry;
+                carry = r >= gr;
+                r -= carry ? gr : 0;
+                ch += ch_step + carry;
+            }
+#pragma unroll
+            for (int u = 0; u < kDgradStage; ++u)
+                if (dst[u] >= 0) *reinterpret_cast<f32x4*>(gt + dst[u]) = v[u];
+        }
+#pragma unroll
+        for (int k = 0; k < kDgradWStage; ++k) {
+            const int e = (int)threadIdx.x + k * 256;
+            if (e < wn)
+#pragma unroll
+                for (int c = 0; c < CIN; ++c) wsh[e * CIN + c] = wv[k][c];
+        }
+        for (int e = threadIdx.x + 256 * kDgradWStage; e < wn; e += blockDim.x) {
             const int oi = e / KW, jj = e - oi * KW;
             const int o = oi / kh, i = oi - o * kh;
             const float* w = weight + ((int64_t)(oc0 + o) * c_in * kh + i) * KW + (KW - 1 - jj);
@@ -390,16 +450,12 @@ __global__ __launch_bounds__(256) void conv_dgrad_small_kernel(
             }
     }
     if (!live) return;
-    float* drow = dinput + (int64_t)n * c_in * HW + (y0 + (int)yy) * in_w + x0;
 #pragma unroll
     for (int c = 0; c < CIN; ++c)
         if (c < c_in)
 #pragma unroll
             for (int r = 0; r < kDgradRun; ++r)
-                if (x0 + r < in_w) {
-                    float* dst = drow + (int64_t)c * HW + r;
-                    *dst = acc[r][c] + *dst;
-                }
+                if (x0 + r < in_w) drow[(int64_t)c * HW + r] = acc[r][c] + old[r][c];
 }
 
 // Weight and bias gradient for layers with few taps (c_in*kh*kw <= TAPS):
@@ -750,7 +806,7 @@ int small_dgrad(float* dinput, const float* grad, const float* weight, const Con
                                                  groups > 1 ? red : 0) * 4;
     const bool c1 = d.c_in == 1;
     void (*fn)(float*, const float*, const float*, int, int, int, int, int, int, int, int, int,
-               int, int, int, int, int, int, FastDiv, FastDiv, FastDiv) = nullptr;
+               int, int, int, int, int, int, FastDiv, FastDiv) = nullptr;
     switch (d.kw) {
         case 1: fn = c1 ? conv_dgrad_small_kernel<1, 1> : conv_dgrad_small_kernel<1, 4>; break;
         case 2: fn = c1 ? conv_dgrad_small_kernel<2, 1> : conv_dgrad_small_kernel<2, 4>; break;
@@ -763,7 +819,7 @@ int small_dgrad(float* dinput, const float* grad, const float* weight, const Con
                        weight, (int)d.c_in, (int)d.in_h, (int)d.in_w, (int)d.c_out, (int)d.kh,
                        (int)d.pad, (int)d.out_h, (int)d.out_w, (int)band, (int)bands, (int)occ,
                        (int)ngx, (int)pitch, groups, tpg, make_fastdiv((uint32_t)ngx),
-                       make_fastdiv((uint32_t)pitch), make_fastdiv((uint32_t)tile));
+                       make_fastdiv((uint32_t)d.kh));
     NRS_LAUNCH_CHECK("conv2d input gradient (small)");
     return NRS_OK;
 }
@@ -1028,7 +1084,25 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
     }
     if ((dweight || dbias) && col_h <= nrs::kDirectTaps) {
         // few taps: both gradients from one pass over the output gradient
-        // (conv.rs:314-322 without the cols matrix)
+        // (conv.rs:314-322 without the cols matrix), on the matrix cores
+        // when the layer fits that kernel
+        nrs::FewTapsWgrad f;
+        f.x = input;
+        f.g = grad;
+        f.dw = dweight;
+        f.db = dbias;
+        f.N = N;
+        f.C = (int)c_in;
+        f.H = (int)in_h;
+        f.W = (int)in_w;
+        f.M = (int)std::min<int64_t>(c_out, INT32_MAX);
+        f.kh = (int)kh;
+        f.kw = (int)kw;
+        f.stride = (int)stride;
+        f.pad = (int)pad;
+        f.OH = (int)d.out_h;
+        f.OW = (int)d.out_w;
+        if ((rc = nrs::few_taps_wgrad(f)) != nrs::kSlabUnsupported) return rc;
         return nrs::small_wgrad(dweight, dbias, grad, input, d);
     }
     if (dweight && c_in <= INT32_MAX && c_out <= INT32_MAX && in_h <= INT32_MAX &&

@@ -1,0 +1,199 @@
+// Weight and bias gradient of convolutions with few taps per output channel
+// (c_in*kh*kw <= 15, e.g. a first layer over grayscale images): the
+// reference's dW = G . cols^T and db = sum(G) (src/cuda/nn/conv.rs:314-322)
+// without the cols matrix, on the f32 matrix cores.
+//
+//   dW[m][t] = sum_{n,p} g[n,m,p] * x_t(n,p)     db[m] = sum_{n,p} g[n,m,p]
+//
+// is a product with the output channels and the taps as its 2-D output and
+// the N*P pixels as its reduction. v_mfma_f32_16x16x4f32 takes 16 channels
+// (m = lane%16) by 16 taps (n = lane%16) per block; tap column `taps` reads
+// the constant 1, so the same product yields the bias gradient. Lane group
+// kq = lane/16 holds pixels p0 + 4kq .. p0 + 4kq + 3: one 128-bit load of the
+// output gradient per channel block feeds four MFMAs. The input image is
+// staged in LDS with a zero halo, so a tap reads x_t(p) branch-free.
+//
+// A workgroup (4 waves) owns one image and `4*GPW` groups of 16 pixels.
+// A wave issues all its gradient loads at once (one memory round trip) and
+// then runs its MFMA chain over its pixel groups in order. The four waves'
+// sums are added in wave order into per-workgroup partials
+// pw[slice][m][t], pb[slice][m], which a second launch adds in slice order:
+// the result is deterministic.
+#include <algorithm>
+
+#include "buffer_ops.hpp"
+#include "conv_slab.hpp"
+
+namespace nrs {
+namespace {
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+constexpr int kFewTaps = 15;   // taps per channel (one MFMA column is the bias)
+constexpr int kFewMaxM = 64;   // output channels (four blocks of 16)
+constexpr int kFewImage = 16384;  // staged image floats (64 KB)
+
+struct FewTapsArgs {
+    const float* x;
+    const float* g;
+    float* pw;  // [slices][M][taps]
+    float* pb;  // [slices][M]
+    int C, H, W, M, kh, kw, stride, pad, OW, P, Hp, Wp, taps, chunks;
+    FastDiv div_ow;
+};
+
+template <int NBLK, int GPW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void wgrad_few_taps_kernel(FewTapsArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // [C][Hp][Wp]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = blockIdx.x / a.chunks, chunk = blockIdx.x - n * a.chunks;
+    const int t = lane & 15, kq = lane >> 4;
+
+    // gradient fragments first: [group][block], pixels 16*gi + 4*kq .. +3
+    // of channel 16*b + t (zero past P and M through the buffer bounds)
+    const int GPI = (a.P + 15) >> 4;
+    const int g0 = (chunk * 4 + wave) * GPW;
+    const auto rg = buffer_rsrc(a.g + (int64_t)n * a.M * a.P, (int64_t)a.M * a.P * 4);
+    f32x4v ga[GPW][NBLK];
+#pragma unroll
+    for (int q = 0; q < GPW; ++q) {
+        const int p = 16 * (g0 + q) + 4 * kq;
+#pragma unroll
+        for (int b = 0; b < NBLK; ++b) {
+            const int oc = 16 * b + t;
+            ga[q][b] = buffer_load4(rg, (p < a.P) & (oc < a.M) ? (oc * a.P + p) * 4 : kOutOfRange);
+        }
+    }
+
+    // the image with a zero halo of `pad` (rows and columns)
+    const float* img = a.x + (int64_t)n * a.C * a.H * a.W;
+    const int plane = a.Hp * a.Wp, xn = a.C * plane;
+    for (int e = tid; e < xn; e += 256) {
+        const int c = e / plane, r = e - c * plane, yy = r / a.Wp, xx = r - yy * a.Wp;
+        const int iy = yy - a.pad, ix = xx - a.pad;
+        const bool ok = ((unsigned)iy < (unsigned)a.H) & ((unsigned)ix < (unsigned)a.W);
+        const float v = img[ok ? (c * a.H + iy) * a.W + ix : 0];
+        xs[e] = ok ? v : 0.0f;
+    }
+    // this lane's tap: offset in the staged image, or the bias column
+    int toff = 0;
+    const bool tap_live = t < a.taps, ones = t == a.taps;
+    if (tap_live) {
+        const int j = t % a.kw, i = (t / a.kw) % a.kh, c = t / (a.kw * a.kh);
+        toff = (c * a.Hp + i) * a.Wp + j;
+    }
+    __syncthreads();
+
+    f32x4v acc[NBLK];
+#pragma unroll
+    for (int b = 0; b < NBLK; ++b) acc[b] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < GPW; ++q) {
+        int p = 16 * (g0 + q) + 4 * kq;
+        uint32_t oy, ox;
+        fast_divmod((uint32_t)min(p, a.P - 1), a.div_ow, oy, ox);
+        f32x4v xb;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const bool pl = p + s < a.P;
+            const float v = xs[toff + (pl ? ((int)oy * a.Wp + (int)ox) * a.stride : 0)];
+            xb[s] = pl ? (tap_live ? v : (ones ? 1.0f : 0.0f)) : 0.0f;
+            if ((int)++ox == a.OW) {
+                ox = 0;
+                ++oy;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int b = 0; b < NBLK; ++b)
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(ga[q][b][s], xb[s], acc[b], 0, 0, 0);
+    }
+
+    // lane holds D[m = 16b + 4kq + r][t]; the waves' sums in wave order
+    __syncthreads();  // the staged image is no longer read
+    float* red = xs;  // [4][NBLK*16][17]
+    constexpr int RS = 17, WS = NBLK * 16 * RS;
+#pragma unroll
+    for (int b = 0; b < NBLK; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave * WS + (16 * b + 4 * kq + r) * RS + t] = acc[b][r];
+    __syncthreads();
+    const int slice = blockIdx.x;
+    for (int e = tid; e < NBLK * 256; e += 256) {
+        const int m = e >> 4, tt = e & 15;
+        if (m >= a.M || tt > a.taps) continue;
+        float v = red[m * RS + tt];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) v += red[w * WS + m * RS + tt];
+        if (tt < a.taps)
+            a.pw[((int64_t)slice * a.M + m) * a.taps + tt] = v;
+        else
+            a.pb[(int64_t)slice * a.M + m] = v;
+    }
+}
+
+template <int NBLK>
+void* pick_gpw(int gpw) {
+    switch (gpw) {
+        case 1: return reinterpret_cast<void*>(wgrad_few_taps_kernel<NBLK, 1>);
+        case 2: return reinterpret_cast<void*>(wgrad_few_taps_kernel<NBLK, 2>);
+        case 4: return reinterpret_cast<void*>(wgrad_few_taps_kernel<NBLK, 4>);
+        default: return reinterpret_cast<void*>(wgrad_few_taps_kernel<NBLK, 8>);
+    }
+}
+
+}  // namespace
+
+int few_taps_wgrad(const FewTapsWgrad& s) {
+    const int taps = s.C * s.kh * s.kw;
+    const int64_t P = (int64_t)s.OH * s.OW;
+    const int Hp = s.H + 2 * s.pad, Wp = s.W + 2 * s.pad;
+    if (taps > kFewTaps || s.M > kFewMaxM || s.M < 1 || P % 4 || P < 1 || s.N < 1 ||
+        (int64_t)s.C * Hp * Wp > kFewImage || (int64_t)s.M * P > INT32_MAX / 4 ||
+        (int64_t)(s.OH - 1) * s.stride + s.kh > Hp || (int64_t)(s.OW - 1) * s.stride + s.kw > Wp)
+        return kSlabUnsupported;
+    const int nblk = s.M <= 16 ? 1 : (s.M <= 32 ? 2 : 4);  // channel blocks instantiated
+    const int64_t gpi = (P + 15) / 16;
+    // pixel groups per wave: the largest that still gives two workgroups
+    // per CU (fewer, longer waves amortise the staged image)
+    int gpw = 8;
+    auto chunks_for = [&](int gw) { return (gpi + 4 * gw - 1) / (4 * gw); };
+    while (gpw > 1 && s.N * chunks_for(gpw) < 2 * num_cus()) gpw /= 2;
+    const int64_t chunks = chunks_for(gpw), slices = s.N * chunks;
+    if (slices > INT32_MAX || slices * s.M * (taps + 1) > INT32_MAX) return kSlabUnsupported;
+    float* pw = workspace(sizeof(float) * (size_t)(slices * s.M * (taps + 1)), 3);
+    if (!pw) return NRS_ERR_ALLOC;
+    float* pb = pw + slices * s.M * taps;
+    FewTapsArgs a;
+    a.x = s.x;
+    a.g = s.g;
+    a.pw = pw;
+    a.pb = pb;
+    a.C = s.C;
+    a.H = s.H;
+    a.W = s.W;
+    a.M = s.M;
+    a.kh = s.kh;
+    a.kw = s.kw;
+    a.stride = s.stride;
+    a.pad = s.pad;
+    a.OW = s.OW;
+    a.P = (int)P;
+    a.Hp = Hp;
+    a.Wp = Wp;
+    a.taps = taps;
+    a.chunks = (int)chunks;
+    a.div_ow = make_fastdiv((uint32_t)s.OW);
+    const size_t lds =
+        sizeof(float) * (size_t)std::max<int64_t>((int64_t)s.C * Hp * Wp, 4 * nblk * 16 * 17);
+    void* fn = nblk == 1 ? pick_gpw<1>(gpw) : (nblk == 2 ? pick_gpw<2>(gpw) : pick_gpw<4>(gpw));
+    hipLaunchKernelGGL(reinterpret_cast<void (*)(FewTapsArgs)>(fn), dim3((unsigned)slices),
+                       dim3(256), lds, stream(), a);
+    NRS_LAUNCH_CHECK("conv2d weight gradient (few taps)");
+    return wgrad_partial_sum(s.dw, s.db, pw, pb, (int)slices, s.M, 1, taps);
+}
+
+}  // namespace nrs

@@ -42,6 +42,7 @@ struct SlabArgs {
     const float* wpack;    // weights packed per (chunk, channel block) in LDS layout
     int nblk;              // output-channel blocks (gridDim.y)
     float beta;
+    int vec_out;           // 128-bit output stores (P % 4 == 0, 16-byte aligned output)
     int CC, CC4;           // channels per chunk (multiple of 16) and CC / 4
     int band;              // output pixels per band
     int slab_rows, slab_w; // LDS slab rows reserved and columns
@@ -50,8 +51,8 @@ struct SlabArgs {
     FastDiv div_bands, div_ow, div_psn, div_slab_w;
 };
 
-constexpr int kStageBatch = 8;    // input-slab items (4 loads each) per thread per batch
-constexpr int kWeightBatch = 16;  // weight float4s per thread per batch
+constexpr int kStageBatch = 12;   // input-slab items (4 loads each) per thread per round
+constexpr int kWeightBatch = 20;  // weight float4s per thread per round
 
 template <int WM, int WN, int MSW, int NSW>
 struct SlabCfg {
@@ -111,55 +112,80 @@ void conv_slab_kernel(SlabArgs a) {
     for (int ms = 0; ms < MSW; ++ms)
 #pragma unroll
         for (int t = 0; t < NSW; ++t) acc[ms][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // the epilogue's biases, loaded now so the stores do not wait for them
+    float bias[MSW][4];
+#pragma unroll
+    for (int ms = 0; ms < MSW; ++ms)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int oc = m0 + 16 * (wm * MSW + ms) + 4 * q + r;
+            bias[ms][r] = (a.bias && oc < a.M) ? a.bias[oc] : 0.0f;
+        }
 
     const float* ximg = a.x + (int64_t)img * a.C * HW;
     for (int c0 = 0; c0 < a.C; c0 += a.CC) {
         if (c0) __syncthreads();  // the previous chunk's reads are done
-        // Staging runs in batches of kStageBatch items per thread: all loads
-        // of a batch are issued before its LDS stores, so a thread waits for
-        // global memory once per batch rather than once per item.
+        // Staging: each round issues up to kStageBatch slab items and
+        // kWeightBatch weight float4s per thread, every load of the round
+        // before any LDS store, so a thread waits for global memory once per
+        // round (one round for the common shapes).
         // Input slab: item = (channel quad, slab pixel), pixels fastest so
-        // consecutive lanes read consecutive input columns.
-        for (int base = tid; base < a.x_items; base += Cfg::NT * kStageBatch) {
-            f32x4 v[kStageBatch];
+        // consecutive lanes read consecutive input columns. Weight block: a
+        // straight copy of its packed LDS image.
+        const f32x4* wsrc = reinterpret_cast<const f32x4*>(
+            a.wpack + ((int64_t)(c0 / a.CC) * a.nblk + blockIdx.y) * Cfg::BM * a.wrow);
+        f32x4* wdst = reinterpret_cast<f32x4*>(ws);
+        const int rounds = max((a.x_items + Cfg::NT * kStageBatch - 1) / (Cfg::NT * kStageBatch),
+                               (a.w_items + Cfg::NT * kWeightBatch - 1) / (Cfg::NT * kWeightBatch));
+        for (int rd = 0; rd < rounds; ++rd) {
+            const int xbase = rd * Cfg::NT * kStageBatch, wbase = rd * Cfg::NT * kWeightBatch;
+            f32x4 v[kStageBatch], wv[kWeightBatch];
             int dst[kStageBatch];
+            const bool xrun = xbase < a.x_items, wrun = wbase < a.w_items;  // uniform
+            if (xrun) {
 #pragma unroll
-            for (int b = 0; b < kStageBatch; ++b) {
-                const int idx = base + b * Cfg::NT;
-                uint32_t c4, pos, r, col;
-                fast_divmod((uint32_t)min(idx, a.x_items - 1), a.div_psn, c4, pos);
-                fast_divmod(pos, a.div_slab_w, r, col);
-                const bool live = (idx < a.x_items) & ((int)r < rows);
-                const int iy = iy0 + (int)r, ix = (int)col - a.pad_w;
-                const bool in = live & ((unsigned)iy < (unsigned)a.H) & ((unsigned)ix < (unsigned)a.W);
-                const int c = c0 + 4 * (int)c4;
-                const float* src = ximg + (int64_t)c * HW + iy * a.W + ix;
-                // branch-free: masked lanes load the image's first element
+                for (int b = 0; b < kStageBatch; ++b) {
+                    dst[b] = -1;
+                    // slots past the last item are skipped (uniform condition)
+                    if (xbase + b * Cfg::NT >= a.x_items) continue;
+                    const int idx = xbase + tid + b * Cfg::NT;
+                    uint32_t c4, pos, r, col;
+                    fast_divmod((uint32_t)min(idx, a.x_items - 1), a.div_psn, c4, pos);
+                    fast_divmod(pos, a.div_slab_w, r, col);
+                    const bool live = (idx < a.x_items) & ((int)r < rows);
+                    const int iy = iy0 + (int)r, ix = (int)col - a.pad_w;
+                    const bool in =
+                        live & ((unsigned)iy < (unsigned)a.H) & ((unsigned)ix < (unsigned)a.W);
+                    const int c = c0 + 4 * (int)c4;
+                    const float* src = ximg + (int64_t)c * HW + iy * a.W + ix;
+                    // branch-free: masked lanes load the image's first element
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const bool ok = in & (c + u < a.C);
-                    const float t = *(ok ? src + u * HW : ximg);
-                    v[b][u] = ok ? t : 0.0f;
+                    for (int u = 0; u < 4; ++u) {
+                        const bool ok = in & (c + u < a.C);
+                        const float t = *(ok ? src + u * HW : ximg);
+                        v[b][u] = ok ? t : 0.0f;
+                    }
+                    dst[b] = live ? (int)(pos * a.ps + 4 * c4) : -1;
                 }
-                dst[b] = live ? (int)(pos * a.ps + 4 * c4) : -1;
             }
-#pragma unroll
-            for (int b = 0; b < kStageBatch; ++b)
-                if (dst[b] >= 0) *reinterpret_cast<f32x4*>(xs + dst[b]) = v[b];
-        }
-        // Weight block: a straight copy of its packed LDS image.
-        {
-            const f32x4* src = reinterpret_cast<const f32x4*>(
-                a.wpack + ((int64_t)(c0 / a.CC) * a.nblk + blockIdx.y) * Cfg::BM * a.wrow);
-            f32x4* dst = reinterpret_cast<f32x4*>(ws);
-            for (int base = tid; base < a.w_items; base += Cfg::NT * kWeightBatch) {
-                f32x4 v[kWeightBatch];
+            if (wrun) {
 #pragma unroll
                 for (int b = 0; b < kWeightBatch; ++b)
-                    v[b] = src[min(base + b * Cfg::NT, a.w_items - 1)];
+                    if (wbase + b * Cfg::NT < a.w_items)  // uniform
+                        wv[b] = wsrc[min(wbase + tid + b * Cfg::NT, a.w_items - 1)];
+            }
+            if (xrun) {
 #pragma unroll
-                for (int b = 0; b < kWeightBatch; ++b)
-                    if (base + b * Cfg::NT < a.w_items) dst[base + b * Cfg::NT] = v[b];
+                for (int b = 0; b < kStageBatch; ++b)
+                    if (xbase + b * Cfg::NT < a.x_items && dst[b] >= 0)
+                        *reinterpret_cast<f32x4*>(xs + dst[b]) = v[b];
+            }
+            if (wrun) {
+#pragma unroll
+                for (int b = 0; b < kWeightBatch; ++b) {
+                    const int e = wbase + tid + b * Cfg::NT;
+                    if (e < a.w_items) wdst[e] = wv[b];
+                }
             }
         }
         __syncthreads();
@@ -196,6 +222,10 @@ void conv_slab_kernel(SlabArgs a) {
 #pragma unroll
             for (int t = 0; t < NSW; ++t)
                 bn[t] = *reinterpret_cast<const f32x4*>(xs + poff[t] + toff);
+            // keep the next step's reads ahead of this step's MFMAs (left
+            // alone, the scheduler sinks them below to reuse registers and
+            // every step then waits out a full LDS round trip)
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -211,25 +241,78 @@ void conv_slab_kernel(SlabArgs a) {
         }
     }
 
-    // epilogue: NCHW store, + bias, + beta * out
+    // epilogue: NCHW store, + bias, + beta * out, with non-temporal stores
+    // (the output would otherwise evict the operands of the workgroups still
+    // running from L2)
     float* oimg = a.out + (int64_t)img * a.M * a.P;
+    if (a.vec_out) {
+        // Through a per-wave LDS tile [MSW*16 channels][NSW*16 pixels]: the
+        // MFMA layout holds four channels of one pixel per lane, the tile
+        // gives each lane four adjacent pixels of one channel, so a wave's
+        // stores are 128-bit and cover whole row segments.
+        constexpr int TR = NSW * 16 + 4;   // tile row stride (floats)
+        constexpr int TW = MSW * 16 * TR;  // floats per wave
+        __syncthreads();                   // every wave is done with the operands
+        float* tile = lds + wave * TW;
 #pragma unroll
-    for (int ms = 0; ms < MSW; ++ms)
+        for (int ms = 0; ms < MSW; ++ms)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int oc = m0 + 16 * (wm * MSW + ms) + 4 * q + r;
-            if (oc >= a.M) continue;
-            const float b = a.bias ? a.bias[oc] : 0.0f;
+            for (int t = 0; t < NSW; ++t)
 #pragma unroll
-            for (int t = 0; t < NSW; ++t) {
-                const int p = p0 + 16 * (wn * NSW + t) + l16;
-                if (p >= p_end) continue;
-                float* dst = oimg + (int64_t)oc * a.P + p;
-                float v = acc[ms][t][r] + b;
-                if (a.beta != 0.0f) v = v + a.beta * *dst;
-                *dst = v;
+                for (int r = 0; r < 4; ++r)
+                    tile[(16 * ms + 4 * q + r) * TR + 16 * t + l16] = acc[ms][t][r] + bias[ms][r];
+        __syncthreads();
+        const int pw0 = p0 + 16 * wn * NSW, ocw0 = m0 + 16 * wm * MSW;
+#pragma unroll
+        for (int k = 0; k < MSW * NSW; ++k) {
+            const int e = lane + 64 * k;
+            const int row = e / (NSW * 4), c4 = e - row * (NSW * 4);
+            const int oc = ocw0 + row, p = pw0 + 4 * c4;
+            if (oc >= a.M || p >= p_end) continue;
+            f32x4 v = *reinterpret_cast<const f32x4*>(tile + row * TR + 4 * c4);
+            float* dst = oimg + (int64_t)oc * a.P + p;
+            if (p + 4 <= p_end) {
+                if (a.beta != 0.0f) v = v + a.beta * *reinterpret_cast<const f32x4*>(dst);
+                __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst));
+            } else {
+                for (int u = 0; u < p_end - p; ++u)
+                    __builtin_nontemporal_store(a.beta != 0.0f ? v[u] + a.beta * dst[u] : v[u],
+                                                dst + u);
             }
         }
+        return;
+    }
+    if (a.beta == 0.0f) {
+#pragma unroll
+        for (int ms = 0; ms < MSW; ++ms)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int oc = m0 + 16 * (wm * MSW + ms) + 4 * q + r;
+                if (oc >= a.M) continue;
+#pragma unroll
+                for (int t = 0; t < NSW; ++t) {
+                    const int p = p0 + 16 * (wn * NSW + t) + l16;
+                    if (p < p_end)
+                        __builtin_nontemporal_store(acc[ms][t][r] + bias[ms][r],
+                                                    oimg + (int64_t)oc * a.P + p);
+                }
+            }
+    } else {
+#pragma unroll
+        for (int ms = 0; ms < MSW; ++ms)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int oc = m0 + 16 * (wm * MSW + ms) + 4 * q + r;
+                if (oc >= a.M) continue;
+#pragma unroll
+                for (int t = 0; t < NSW; ++t) {
+                    const int p = p0 + 16 * (wn * NSW + t) + l16;
+                    if (p >= p_end) continue;
+                    float* dst = oimg + (int64_t)oc * a.P + p;
+                    __builtin_nontemporal_store(acc[ms][t][r] + bias[ms][r] + a.beta * *dst, dst);
+                }
+            }
+    }
 }
 
 // Packs the weights of a slab convolution into the LDS image the kernel
@@ -297,7 +380,10 @@ SlabPlan plan_slab(const SlabConv& s) {
         Cfg::BM * taps * CC > INT32_MAX / 2)
         return SlabPlan{};
     pl.CC = CC;
-    pl.lds = (size_t)bytes(CC);
+    // the epilogue's per-wave tiles reuse the same LDS
+    const int64_t tile = (int64_t)(Cfg::NT / 64) * (16 * MSW) * (16 * NSW + 4) * 4;
+    pl.lds = (size_t)std::max<int64_t>(bytes(CC), tile);
+    if (pl.lds > kLdsBytes) return SlabPlan{};
     return pl;
 }
 
@@ -335,6 +421,7 @@ int launch_slab(const SlabConv& s, const SlabPlan& pl) {
     a.wpack = packed;
     a.nblk = (int)nblk;
     a.beta = s.beta;
+    a.vec_out = (P % 4 == 0 && ((uintptr_t)s.out & 15) == 0) ? 1 : 0;
     a.CC = (int)pl.CC;
     a.CC4 = (int)(pl.CC / 4);
     a.band = (int)pl.band;

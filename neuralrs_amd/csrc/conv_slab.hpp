@@ -45,6 +45,20 @@ struct SlabWgrad {
 };
 int slab_wgrad(const SlabWgrad& s);
 
+// Weight and bias gradient of a convolution with c_in*kh*kw <= 15 taps and at
+// most 64 output channels, on the matrix cores (conv_few_taps.hip): dw += and
+// db += (either may be null). Returns kSlabUnsupported (launching nothing)
+// for shapes outside the kernel's limits.
+struct FewTapsWgrad {
+    const float* x = nullptr;  // NCHW [N][C][H][W]
+    const float* g = nullptr;  // NCHW [N][M][OH][OW]
+    float* dw = nullptr;       // [M][C][kh][kw] or null
+    float* db = nullptr;       // [M] or null
+    int64_t N = 0;
+    int C = 0, H = 0, W = 0, M = 0, kh = 0, kw = 0, stride = 1, pad = 0, OH = 0, OW = 0;
+};
+int few_taps_wgrad(const FewTapsWgrad& s);
+
 // dw[m][c][tap] += sum over slices of part_w[slice][m][tap][c] (when dw is
 // given) and db[m] += sum over slices of part_b[slice][m] (when db is given),
 // the slices added in a fixed order; one launch.

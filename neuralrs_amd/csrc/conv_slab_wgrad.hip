@@ -188,8 +188,10 @@ void conv_slab_wgrad_kernel(WgradArgs a) {
 // db[m] += sum over slices of part_b[slice][m]: the slices are split into
 // kSumGroups contiguous groups summed in parallel (ascending within a group),
 // then the group sums are added in group order, so the result is
-// deterministic.
-constexpr int kSumGroups = 16;
+// deterministic. A thread issues the loads of up to kSumBatch slices (in
+// runs of 8, as many runs as its group needs) before adding any, so a group
+// of that size costs one memory round trip.
+constexpr int kSumGroups = 16, kSumBatch = 32;
 
 __global__ __launch_bounds__(64 * kSumGroups) void wgrad_sum_kernel(
     float* __restrict__ dw, float* __restrict__ db, const float* __restrict__ part_w,
@@ -206,15 +208,22 @@ __global__ __launch_bounds__(64 * kSumGroups) void wgrad_sum_kernel(
         const int64_t stride = is_w ? nw : M;
         float v = 0.0f;
         if (e < total) {
-            int s = s0;
-            for (; s + 8 <= s1; s += 8) {
-                float t[8];
+            for (int s = s0; s < s1; s += kSumBatch) {
+                float t[kSumBatch];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) t[u] = part[(int64_t)(s + u) * stride];
+                for (int b = 0; b < kSumBatch; b += 8) {
+                    if (s + b < s1) {  // uniform over the wave (one slice group)
 #pragma unroll
-                for (int u = 0; u < 8; ++u) v += t[u];
+                        for (int u = b; u < b + 8; ++u)
+                            t[u] = part[(int64_t)min(s + u, s1 - 1) * stride];
+                    } else {
+#pragma unroll
+                        for (int u = b; u < b + 8; ++u) t[u] = 0.0f;
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < kSumBatch; ++u) v += s + u < s1 ? t[u] : 0.0f;
             }
-            for (; s < s1; ++s) v += part[(int64_t)s * stride];
         }
         red[ty][tx] = v;
         __syncthreads();

@@ -35,6 +35,12 @@ CONV_SHAPES = [  # (n, c_in, c_out, h, w, kh, kw, stride, pad)
     (2, 40, 12, 5, 6, 1, 1, 1, 0),   # 1x1 kernel
     (2, 12, 17, 9, 13, 2, 4, 2, 1),  # non-square kernel, stride 2
     (2, 1, 70, 9, 9, 3, 3, 1, 1),    # few taps, 70 channels: two forward channel blocks, ragged weight-grad block
+    # few-taps weight gradient on the matrix cores (taps <= 15, <= 64 channels, P % 4 == 0)
+    (3, 1, 32, 28, 28, 3, 3, 1, 1),  # cfg3 conv1
+    (2, 1, 64, 16, 16, 3, 3, 1, 1),  # four channel blocks
+    (2, 1, 48, 20, 20, 1, 1, 1, 0),  # three channel blocks, one tap
+    (2, 1, 5, 9, 12, 3, 5, 1, 2),    # 15 taps: the bias column is the last MFMA column
+    (2, 3, 17, 12, 12, 2, 2, 2, 0),  # three input channels, stride 2
 ]
 ids = ["x".join(map(str, s)) for s in CONV_SHAPES]
 
