@@ -32,7 +32,8 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWgM = 64;  // output channels per workgroup: 4 waves x 16
 constexpr int kWgC = 16;  // input channels per workgroup
-constexpr int kWgStage = 8;
+constexpr int kWgStageG = 16;  // gradient float4 items per thread per staging round
+constexpr int kWgStageX = 16;  // input-slab floats per thread per staging round
 
 struct WgradArgs {
     const float* x;
@@ -43,7 +44,8 @@ struct WgradArgs {
     int band_rows, bands, ntg;  // output rows per band, bands per image, tap groups
     int KP, KQ, KPP;            // padded band pixels, KP / 4, gradient row stride in LDS
     int slab_rows, slab_w, CS;  // input slab rows, columns and channel stride in LDS
-    FastDiv div_bands, div_ntg, div_kp, div_srw, div_slab_w, div_ow, div_kw;
+    int vec_g;                  // gradient rows 16-byte aligned (128-bit staging loads)
+    FastDiv div_bands, div_ntg, div_kp4, div_srw, div_slab_w, div_ow, div_kw;
 };
 
 template <int TAPW>
@@ -69,25 +71,71 @@ void conv_slab_wgrad_kernel(WgradArgs a) {
     int* pofs = reinterpret_cast<int*>(gs + kWgM * a.KPP);  // [KP]
     float* xs = reinterpret_cast<float*>(pofs + a.KP);      // [kWgC][CS]
 
-    // gradient rows: the band's pixels are contiguous in each channel plane
+    // Staging, in rounds that issue every load before any LDS store (one
+    // memory round trip per round, one round for the common shapes):
+    //  * gradient rows: the band's pixels are contiguous in each channel
+    //    plane; item = (channel, pixel quad), one 128-bit load when the rows
+    //    are 16-byte aligned (vec_g), else four masked loads; pixels past the
+    //    band are zero;
+    //  * input slab of the 16 channels: one float per item, zero outside the
+    //    image.
     const float* gimg = a.g + ((int64_t)img * a.M + m0) * a.OH * a.OW + (int64_t)oy0 * a.OW;
-    const int g_items = kWgM * a.KP;
-    for (int base = tid; base < g_items; base += 256 * kWgStage) {
-        float v[kWgStage];
-        int dst[kWgStage];
+    const int KP4 = a.KP >> 2, g_items = kWgM * KP4;
+    const float* ximg = a.x + ((int64_t)img * a.C + c0) * a.H * a.W;
+    const int x_items = kWgC * srw;
+    const int rows_in = (rows_b - 1) * a.stride + a.kh;
+    const int rounds = max((g_items + 256 * kWgStageG - 1) / (256 * kWgStageG),
+                           (x_items + 256 * kWgStageX - 1) / (256 * kWgStageX));
+    for (int rd = 0; rd < rounds; ++rd) {
+        const int gbase = rd * 256 * kWgStageG, xbase = rd * 256 * kWgStageX;
+        f32x4 gv[kWgStageG];
+        float xv[kWgStageX];
+        int gdst[kWgStageG], xdst[kWgStageX];
 #pragma unroll
-        for (int b = 0; b < kWgStage; ++b) {
-            const int e = base + b * 256;
-            uint32_t m, kk;
-            fast_divmod((uint32_t)min(e, g_items - 1), a.div_kp, m, kk);
-            const bool ok = (e < g_items) & (m0 + (int)m < a.M) & ((int)kk < PB);
-            const float t = gimg[ok ? (int64_t)m * a.OH * a.OW + kk : 0];
-            v[b] = ok ? t : 0.0f;
-            dst[b] = e < g_items ? (int)m * a.KPP + (int)kk : -1;
+        for (int b = 0; b < kWgStageG; ++b) {
+            gdst[b] = -1;
+            if (gbase + b * 256 >= g_items) continue;  // uniform
+            const int e = gbase + b * 256 + tid;
+            uint32_t m, k4;
+            fast_divmod((uint32_t)min(e, g_items - 1), a.div_kp4, m, k4);
+            const int kk = 4 * (int)k4;
+            const bool row = (e < g_items) & (m0 + (int)m < a.M);
+            const float* src = gimg + (int64_t)m * a.OH * a.OW + kk;
+            if (a.vec_g) {
+                const bool ok = row & (kk < PB);
+                gv[b] = *reinterpret_cast<const f32x4*>(ok ? src : gimg);
+                if (!ok) gv[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const bool ok = row & (kk + u < PB);
+                    const float t = *(ok ? src + u : gimg);
+                    gv[b][u] = ok ? t : 0.0f;
+                }
+            }
+            gdst[b] = e < g_items ? (int)m * a.KPP + kk : -1;
         }
 #pragma unroll
-        for (int b = 0; b < kWgStage; ++b)
-            if (dst[b] >= 0) gs[dst[b]] = v[b];
+        for (int b = 0; b < kWgStageX; ++b) {
+            xdst[b] = -1;
+            if (xbase + b * 256 >= x_items) continue;  // uniform
+            const int e = xbase + b * 256 + tid;
+            uint32_t c, pos, r, col;
+            fast_divmod((uint32_t)min(e, x_items - 1), a.div_srw, c, pos);
+            fast_divmod(pos, a.div_slab_w, r, col);
+            const int iy = iy0 + (int)r, ix = (int)col - a.pad_w;
+            const bool ok = (e < x_items) & ((int)r < rows_in) & (c0 + (int)c < a.C) &
+                            ((unsigned)iy < (unsigned)a.H) & ((unsigned)ix < (unsigned)a.W);
+            const float t = ximg[ok ? ((int64_t)c * a.H + iy) * a.W + ix : 0];
+            xv[b] = ok ? t : 0.0f;
+            xdst[b] = e < x_items ? (int)c * a.CS + (int)pos : -1;
+        }
+#pragma unroll
+        for (int b = 0; b < kWgStageG; ++b)
+            if (gdst[b] >= 0) *reinterpret_cast<f32x4*>(gs + gdst[b]) = gv[b];
+#pragma unroll
+        for (int b = 0; b < kWgStageX; ++b)
+            if (xdst[b] >= 0) xs[xdst[b]] = xv[b];
     }
     // slab offset of each band pixel (0 for the padding pixels, whose
     // gradient is zero)
@@ -99,30 +147,6 @@ void conv_slab_wgrad_kernel(WgradArgs a) {
             o = (int)oy * a.stride * a.slab_w + (int)ox * a.stride;
         }
         pofs[kk] = o;
-    }
-    // input slab of the 16 channels
-    const float* ximg = a.x + ((int64_t)img * a.C + c0) * a.H * a.W;
-    const int x_items = kWgC * srw;
-    const int rows_in = (rows_b - 1) * a.stride + a.kh;
-    for (int base = tid; base < x_items; base += 256 * kWgStage) {
-        float v[kWgStage];
-        int dst[kWgStage];
-#pragma unroll
-        for (int b = 0; b < kWgStage; ++b) {
-            const int e = base + b * 256;
-            uint32_t c, pos, r, col;
-            fast_divmod((uint32_t)min(e, x_items - 1), a.div_srw, c, pos);
-            fast_divmod(pos, a.div_slab_w, r, col);
-            const int iy = iy0 + (int)r, ix = (int)col - a.pad_w;
-            const bool ok = (e < x_items) & ((int)r < rows_in) & (c0 + (int)c < a.C) &
-                            ((unsigned)iy < (unsigned)a.H) & ((unsigned)ix < (unsigned)a.W);
-            const float t = ximg[ok ? ((int64_t)c * a.H + iy) * a.W + ix : 0];
-            v[b] = ok ? t : 0.0f;
-            dst[b] = e < x_items ? (int)c * a.CS + (int)pos : -1;
-        }
-#pragma unroll
-        for (int b = 0; b < kWgStage; ++b)
-            if (dst[b] >= 0) xs[dst[b]] = v[b];
     }
     __syncthreads();
 
@@ -140,18 +164,35 @@ void conv_slab_wgrad_kernel(WgradArgs a) {
     f32x4 acc[TAPW];
 #pragma unroll
     for (int t = 0; t < TAPW; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // Software-pipelined: the B values of the next step (and the pixel
+    // offsets and A quad of the next group of four) are read from LDS
+    // before this step's MFMAs issue; with one wave per SIMD nothing else
+    // hides the LDS latency. Scheduling barriers keep the reads ahead.
+    i32x4 po = *reinterpret_cast<const i32x4*>(pofs + poff);
+    f32x4 av = *reinterpret_cast<const f32x4*>(gs + aoff);
+    float bcur[TAPW];
+#pragma unroll
+    for (int t = 0; t < TAPW; ++t) bcur[t] = xs[bb[t] + po[0]];
     for (int j = 0; j < a.KQ; j += 4) {
-        const i32x4 po = *reinterpret_cast<const i32x4*>(pofs + poff + j);
-        const f32x4 av = *reinterpret_cast<const f32x4*>(gs + aoff + j);
+        const int jn = j + 4 < a.KQ ? j + 4 : j;  // the last group re-reads itself (unused)
+        const i32x4 pon = *reinterpret_cast<const i32x4*>(pofs + poff + jn);
+        const f32x4 avn = *reinterpret_cast<const f32x4*>(gs + aoff + jn);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            float bv[TAPW];
+            float bnext[TAPW];
+            const int pn = s < 3 ? po[s + 1] : pon[0];
 #pragma unroll
-            for (int t = 0; t < TAPW; ++t) bv[t] = xs[bb[t] + po[s]];
+            for (int t = 0; t < TAPW; ++t) bnext[t] = xs[bb[t] + pn];
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int t = 0; t < TAPW; ++t)
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[t], acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bcur[t], acc[t], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < TAPW; ++t) bcur[t] = bnext[t];
         }
+        po = pon;
+        av = avn;
     }
 
     // partial sums: lane holds D[m = 4q + r][channel l16] of each tap subtile
@@ -308,7 +349,10 @@ int slab_wgrad(const SlabWgrad& s) {
     a.CS = (int)CS;
     a.div_bands = make_fastdiv((uint32_t)bands);
     a.div_ntg = make_fastdiv((uint32_t)ntg);
-    a.div_kp = make_fastdiv((uint32_t)KP);
+    a.div_kp4 = make_fastdiv((uint32_t)(KP / 4));
+    // 16-byte aligned gradient rows: every band starts on a float4
+    a.vec_g = ((int64_t)s.OH * s.OW % 4 == 0 && band_rows * s.OW % 4 == 0 &&
+               ((uintptr_t)s.g & 15) == 0) ? 1 : 0;
     a.div_srw = make_fastdiv((uint32_t)(slab_rows * slab_w));
     a.div_slab_w = make_fastdiv((uint32_t)slab_w);
     a.div_ow = make_fastdiv((uint32_t)s.OW);
