@@ -123,9 +123,10 @@ __global__ __launch_bounds__(256) void flip_weights_kernel(float* __restrict__ w
 // thread per output pixel: its taps are loaded once (branch-free: clamped
 // index, then zeroed), then it produces a block of up to kDirectOcBlock
 // output channels (blockIdx.y) from wave-uniform weights (scalar loads), so
-// consecutive lanes store consecutive pixels of each channel plane. The sum
-// runs over the taps in (ic, i, j) order. 32-bit indexing (checked on the
-// host).
+// consecutive lanes store consecutive pixels of each channel plane (with
+// non-temporal stores: the output is not read again here and would evict the
+// input from L2). The sum runs over the taps in (ic, i, j) order. 32-bit
+// indexing (checked on the host).
 constexpr int kDirectTaps = 32, kDirectOcBlock = 64;
 
 template <int TAPS>
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(256) void conv_fwd_direct_kernel(
             float acc = 0.0f;
 #pragma unroll
             for (int t = 0; t < TAPS; ++t) acc += w[t] * x[t];
-            o[(int64_t)oc * P] = acc + bsh[oc - oc0];
+            __builtin_nontemporal_store(acc + bsh[oc - oc0], o + (int64_t)oc * P);
         }
     }
 }

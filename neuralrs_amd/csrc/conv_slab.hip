@@ -51,14 +51,17 @@ struct SlabArgs {
     FastDiv div_bands, div_ow, div_psn, div_slab_w;
 };
 
-constexpr int kStageBatch = 12;   // input-slab items (4 loads each) per thread per round
-constexpr int kWeightBatch = 20;  // weight float4s per thread per round
 
 template <int WM, int WN, int MSW, int NSW>
 struct SlabCfg {
     static constexpr int NT = 64 * WM * WN;
     static constexpr int BM = 16 * WM * MSW;  // output channels per workgroup
     static constexpr int BN = 16 * WN * NSW;  // output pixels per workgroup (max band)
+    // staging items per thread per round: input-slab pixels (4 loads each)
+    // and weight float4s; smaller for the widest tile, whose accumulators
+    // and operand sets leave fewer registers
+    static constexpr int SB = NSW >= 7 ? 6 : 12;
+    static constexpr int WB = NSW >= 7 ? 10 : 20;
 };
 
 // Two waves per SIMD: the LDS budget targets two workgroups per CU, and the
@@ -125,8 +128,8 @@ void conv_slab_kernel(SlabArgs a) {
     const float* ximg = a.x + (int64_t)img * a.C * HW;
     for (int c0 = 0; c0 < a.C; c0 += a.CC) {
         if (c0) __syncthreads();  // the previous chunk's reads are done
-        // Staging: each round issues up to kStageBatch slab items and
-        // kWeightBatch weight float4s per thread, every load of the round
+        // Staging: each round issues up to Cfg::SB slab items and
+        // Cfg::WB weight float4s per thread, every load of the round
         // before any LDS store, so a thread waits for global memory once per
         // round (one round for the common shapes).
         // Input slab: item = (channel quad, slab pixel), pixels fastest so
@@ -135,16 +138,16 @@ void conv_slab_kernel(SlabArgs a) {
         const f32x4* wsrc = reinterpret_cast<const f32x4*>(
             a.wpack + ((int64_t)(c0 / a.CC) * a.nblk + blockIdx.y) * Cfg::BM * a.wrow);
         f32x4* wdst = reinterpret_cast<f32x4*>(ws);
-        const int rounds = max((a.x_items + Cfg::NT * kStageBatch - 1) / (Cfg::NT * kStageBatch),
-                               (a.w_items + Cfg::NT * kWeightBatch - 1) / (Cfg::NT * kWeightBatch));
+        const int rounds = max((a.x_items + Cfg::NT * Cfg::SB - 1) / (Cfg::NT * Cfg::SB),
+                               (a.w_items + Cfg::NT * Cfg::WB - 1) / (Cfg::NT * Cfg::WB));
         for (int rd = 0; rd < rounds; ++rd) {
-            const int xbase = rd * Cfg::NT * kStageBatch, wbase = rd * Cfg::NT * kWeightBatch;
-            f32x4 v[kStageBatch], wv[kWeightBatch];
-            int dst[kStageBatch];
+            const int xbase = rd * Cfg::NT * Cfg::SB, wbase = rd * Cfg::NT * Cfg::WB;
+            f32x4 v[Cfg::SB], wv[Cfg::WB];
+            int dst[Cfg::SB];
             const bool xrun = xbase < a.x_items, wrun = wbase < a.w_items;  // uniform
             if (xrun) {
 #pragma unroll
-                for (int b = 0; b < kStageBatch; ++b) {
+                for (int b = 0; b < Cfg::SB; ++b) {
                     dst[b] = -1;
                     // slots past the last item are skipped (uniform condition)
                     if (xbase + b * Cfg::NT >= a.x_items) continue;
@@ -170,19 +173,19 @@ void conv_slab_kernel(SlabArgs a) {
             }
             if (wrun) {
 #pragma unroll
-                for (int b = 0; b < kWeightBatch; ++b)
+                for (int b = 0; b < Cfg::WB; ++b)
                     if (wbase + b * Cfg::NT < a.w_items)  // uniform
                         wv[b] = wsrc[min(wbase + tid + b * Cfg::NT, a.w_items - 1)];
             }
             if (xrun) {
 #pragma unroll
-                for (int b = 0; b < kStageBatch; ++b)
+                for (int b = 0; b < Cfg::SB; ++b)
                     if (xbase + b * Cfg::NT < a.x_items && dst[b] >= 0)
                         *reinterpret_cast<f32x4*>(xs + dst[b]) = v[b];
             }
             if (wrun) {
 #pragma unroll
-                for (int b = 0; b < kWeightBatch; ++b) {
+                for (int b = 0; b < Cfg::WB; ++b) {
                     const int e = wbase + tid + b * Cfg::NT;
                     if (e < a.w_items) wdst[e] = wv[b];
                 }
@@ -190,19 +193,21 @@ void conv_slab_kernel(SlabArgs a) {
         }
         __syncthreads();
 
-        // The reduction runs over (tap, 4-channel group) steps; the operands
-        // of step it+1 are read from LDS while step it's MFMAs issue. The
-        // read after the last step goes to offset 0 (in bounds, unused).
+        // The reduction runs over (tap, 4-channel group) steps, two per
+        // iteration on two register sets: the operands of the next step are
+        // read from LDS before the current step's MFMAs issue (scheduling
+        // barriers keep them there), and the sets alternate, so no register
+        // copies sit between the MFMA groups. Past the last step the reads go
+        // to offset 0 (in bounds) and the A operand is zeroed.
         const int steps = a.taps * (CQ / 4);
         int tap = 0, j4 = 0, i = 0, j = 0;
-        int woff = 0, toff = 0;
-        f32x4 av[MSW], bv[NSW];
+        f32x4 a0[MSW], b0[NSW], a1[MSW], b1[NSW];
 #pragma unroll
         for (int ms = 0; ms < MSW; ++ms)
-            av[ms] = *reinterpret_cast<const f32x4*>(ws + aoff[ms]);
+            a0[ms] = *reinterpret_cast<const f32x4*>(ws + aoff[ms]);
 #pragma unroll
-        for (int t = 0; t < NSW; ++t) bv[t] = *reinterpret_cast<const f32x4*>(xs + poff[t]);
-        for (int it = 0; it < steps; ++it) {
+        for (int t = 0; t < NSW; ++t) b0[t] = *reinterpret_cast<const f32x4*>(xs + poff[t]);
+        for (int it = 0; it < steps; it += 2) {
             j4 += 4;
             if (j4 == CQ) {
                 j4 = 0;
@@ -212,19 +217,17 @@ void conv_slab_kernel(SlabArgs a) {
                     ++i;
                 }
             }
-            const bool more = it + 1 < steps;
-            woff = more ? tap * a.CC + j4 : 0;
-            toff = more ? (i * a.slab_w + j) * a.ps + j4 : 0;
-            f32x4 an[MSW], bn[NSW];
+            const bool has1 = it + 1 < steps;  // uniform
+            {
+                const int woff = has1 ? tap * a.CC + j4 : 0;
+                const int toff = has1 ? (i * a.slab_w + j) * a.ps + j4 : 0;
 #pragma unroll
-            for (int ms = 0; ms < MSW; ++ms)
-                an[ms] = *reinterpret_cast<const f32x4*>(ws + aoff[ms] + woff);
+                for (int ms = 0; ms < MSW; ++ms)
+                    a1[ms] = *reinterpret_cast<const f32x4*>(ws + aoff[ms] + woff);
 #pragma unroll
-            for (int t = 0; t < NSW; ++t)
-                bn[t] = *reinterpret_cast<const f32x4*>(xs + poff[t] + toff);
-            // keep the next step's reads ahead of this step's MFMAs (left
-            // alone, the scheduler sinks them below to reuse registers and
-            // every step then waits out a full LDS round trip)
+                for (int t = 0; t < NSW; ++t)
+                    b1[t] = *reinterpret_cast<const f32x4*>(xs + poff[t] + toff);
+            }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int s = 0; s < 4; ++s)
@@ -232,12 +235,42 @@ void conv_slab_kernel(SlabArgs a) {
                 for (int ms = 0; ms < MSW; ++ms)
 #pragma unroll
                     for (int t = 0; t < NSW; ++t)
-                        acc[ms][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[ms][s], bv[t][s],
+                        acc[ms][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[ms][s], b0[t][s],
                                                                           acc[ms][t], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            j4 += 4;
+            if (j4 == CQ) {
+                j4 = 0;
+                ++tap;
+                if (++j == a.kw) {
+                    j = 0;
+                    ++i;
+                }
+            }
+            const bool has2 = it + 2 < steps;  // uniform
+            {
+                const int woff = has2 ? tap * a.CC + j4 : 0;
+                const int toff = has2 ? (i * a.slab_w + j) * a.ps + j4 : 0;
 #pragma unroll
-            for (int ms = 0; ms < MSW; ++ms) av[ms] = an[ms];
+                for (int ms = 0; ms < MSW; ++ms)
+                    a0[ms] = *reinterpret_cast<const f32x4*>(ws + aoff[ms] + woff);
 #pragma unroll
-            for (int t = 0; t < NSW; ++t) bv[t] = bn[t];
+                for (int t = 0; t < NSW; ++t)
+                    b0[t] = *reinterpret_cast<const f32x4*>(xs + poff[t] + toff);
+            }
+#pragma unroll
+            for (int ms = 0; ms < MSW; ++ms)
+                if (!has1) a1[ms] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int ms = 0; ms < MSW; ++ms)
+#pragma unroll
+                    for (int t = 0; t < NSW; ++t)
+                        acc[ms][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[ms][s], b1[t][s],
+                                                                          acc[ms][t], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 

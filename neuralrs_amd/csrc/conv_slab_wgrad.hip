@@ -167,29 +167,31 @@ void conv_slab_wgrad_kernel(WgradArgs a) {
     // Software-pipelined: the B values of the next step (and the pixel
     // offsets and A quad of the next group of four) are read from LDS
     // before this step's MFMAs issue; with one wave per SIMD nothing else
-    // hides the LDS latency. Scheduling barriers keep the reads ahead.
+    // hides the LDS latency. Scheduling barriers keep the reads ahead. The
+    // four steps of a group alternate between two B register sets, so the
+    // first set is current again at the next group.
     i32x4 po = *reinterpret_cast<const i32x4*>(pofs + poff);
     f32x4 av = *reinterpret_cast<const f32x4*>(gs + aoff);
-    float bcur[TAPW];
+    // two B register sets, alternating over the (unrolled) steps, so no
+    // copies sit between the MFMA groups
+    float bset[2][TAPW];
 #pragma unroll
-    for (int t = 0; t < TAPW; ++t) bcur[t] = xs[bb[t] + po[0]];
+    for (int t = 0; t < TAPW; ++t) bset[0][t] = xs[bb[t] + po[0]];
     for (int j = 0; j < a.KQ; j += 4) {
         const int jn = j + 4 < a.KQ ? j + 4 : j;  // the last group re-reads itself (unused)
         const i32x4 pon = *reinterpret_cast<const i32x4*>(pofs + poff + jn);
         const f32x4 avn = *reinterpret_cast<const f32x4*>(gs + aoff + jn);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            float bnext[TAPW];
+            const int cur = s & 1, nxt = cur ^ 1;
             const int pn = s < 3 ? po[s + 1] : pon[0];
 #pragma unroll
-            for (int t = 0; t < TAPW; ++t) bnext[t] = xs[bb[t] + pn];
+            for (int t = 0; t < TAPW; ++t) bset[nxt][t] = xs[bb[t] + pn];
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int t = 0; t < TAPW; ++t)
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bcur[t], acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bset[cur][t], acc[t], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int t = 0; t < TAPW; ++t) bcur[t] = bnext[t];
         }
         po = pon;
         av = avn;
