@@ -115,7 +115,12 @@ def bench_gemm(hip, n, steps, warmup):
 
 
 def bench_conv_cfg3(hip, steps, warmup):
-    """cfg3 step: conv1 -> maxpool -> conv2, forward + backward (all grads)."""
+    """cfg3 step: conv1 -> maxpool -> conv2, forward + backward: weight and
+    bias gradients of both layers, input gradient of conv2. conv1's input is
+    the image batch, which requires no gradient in the reference's training
+    step (examples/mnist_cuda_cnn.rs:261 sets requires_grad = false, and
+    src/cuda/nn/conv.rs:304 then skips the input gradient); that kernel is
+    timed on its own and reported beside the step."""
     rng = np.random.default_rng(3)
     N, H, W = 128, 28, 28
     x = rng.uniform(0, 1, N * 1 * H * W).astype(np.float32)
@@ -145,7 +150,7 @@ def bench_conv_cfg3(hip, steps, warmup):
         hip.call("nrs_conv2d_backward", gp1.ptr, gw2.ptr, gb2.ptr, dg2.ptr, p1.ptr, dw2.ptr,
                  N, 32, 14, 14, 64, 3, 3, 1, 1)
         hip.call("nrs_maxpool_backward", gy1.ptr, gp1.ptr, am.ptr, N, 32, 28, 28, 2, 2)
-        hip.call("nrs_conv2d_backward", gx.ptr, gw1.ptr, gb1.ptr, gy1.ptr, dx.ptr, dw1.ptr,
+        hip.call("nrs_conv2d_backward", None, gw1.ptr, gb1.ptr, gy1.ptr, dx.ptr, dw1.ptr,
                  N, 1, 28, 28, 32, 3, 3, 1, 1)
 
     def conv_fwd():
@@ -155,7 +160,11 @@ def bench_conv_cfg3(hip, steps, warmup):
     def conv_bwd():
         hip.call("nrs_conv2d_backward", gp1.ptr, gw2.ptr, gb2.ptr, dg2.ptr, p1.ptr, dw2.ptr,
                  N, 32, 14, 14, 64, 3, 3, 1, 1)
-        hip.call("nrs_conv2d_backward", gx.ptr, gw1.ptr, gb1.ptr, gy1.ptr, dx.ptr, dw1.ptr,
+        hip.call("nrs_conv2d_backward", None, gw1.ptr, gb1.ptr, gy1.ptr, dx.ptr, dw1.ptr,
+                 N, 1, 28, 28, 32, 3, 3, 1, 1)
+
+    def conv1_input_grad():
+        hip.call("nrs_conv2d_backward", gx.ptr, None, None, gy1.ptr, dx.ptr, dw1.ptr,
                  N, 1, 28, 28, 32, 3, 3, 1, 1)
 
     for _ in range(warmup):
@@ -168,19 +177,26 @@ def bench_conv_cfg3(hip, steps, warmup):
     ms = (time.perf_counter() - t0) * 1e3 / steps
     fwd_ms = event_ms(hip, conv_fwd, steps, 3)
     bwd_ms = event_ms(hip, conv_bwd, steps, 3)
+    dx1_ms = event_ms(hip, conv1_input_grad, steps, 3)
     # rooflines per layer (implicit-GEMM FLOPs; bytes = each tensor read or
     # written once): forward x, W, b, y; input grad g, W, dx; weight+bias
     # grad g, x, dW, db
-    roof_f = roof_b = 0.0
+    roof_f = roof_b = roof_dx1 = 0.0
     for (ci, co, h) in ((1, 32, 28), (32, 64, 14)):
         P, taps = h * h, ci * 9
         fl = 2.0 * co * N * P * taps
         x_b, y_b, w_b = 4.0 * N * ci * P, 4.0 * N * co * P, 4.0 * co * taps
         roof_f += roofline_us(fl, x_b + w_b + 4 * co + y_b)
-        roof_b += roofline_us(fl, y_b + w_b + x_b) + roofline_us(fl, y_b + x_b + w_b + 4 * co)
+        dx_roof = roofline_us(fl, y_b + w_b + x_b)
+        if ci == 1:
+            roof_dx1 = dx_roof  # the image batch's gradient: not part of the step
+        else:
+            roof_b += dx_roof
+        roof_b += roofline_us(fl, y_b + x_b + w_b + 4 * co)
     return {"ms_per_step": ms, "imgs_per_s": N / (ms / 1e3),
             "fwd_us": fwd_ms * 1e3, "bwd_us": bwd_ms * 1e3,
-            "fwd_roof_us": roof_f, "bwd_roof_us": roof_b}
+            "fwd_roof_us": roof_f, "bwd_roof_us": roof_b,
+            "conv1_input_grad_us": dx1_ms * 1e3, "conv1_input_grad_roof_us": roof_dx1}
 
 
 def bench_mlp_cfg2(hip, steps, warmup):
@@ -521,13 +537,17 @@ def main():
         out["conv2d_fwd_bwd"] = {
             "value": round(c["imgs_per_s"], 1), "unit": "imgs/s",
             "ms_per_step": round(c["ms_per_step"], 4),
-            "config": "cfg3 batch 128 conv1 1->32, maxpool, conv2 32->64, "
-                      "fwd+bwd with input and weight grads",
+            "config": "cfg3 batch 128 conv1 1->32, maxpool, conv2 32->64, fwd+bwd: weight and "
+                      "bias grads of both layers, input grad of conv2 (the image batch requires "
+                      "no grad, as in examples/mnist_cuda_cnn.rs:261)",
             "conv_fwd_us": round(c["fwd_us"], 2), "conv_bwd_us": round(c["bwd_us"], 2),
             "fwd_roofline_us": round(c["fwd_roof_us"], 2),
             "bwd_roofline_us": round(c["bwd_roof_us"], 2),
             "fwd_roofline_frac": round(c["fwd_roof_us"] / c["fwd_us"], 4),
-            "bwd_roofline_frac": round(c["bwd_roof_us"] / c["bwd_us"], 4)}
+            "bwd_roofline_frac": round(c["bwd_roof_us"] / c["bwd_us"], 4),
+            "conv1_input_grad_us": round(c["conv1_input_grad_us"], 2),
+            "conv1_input_grad_roofline_frac": round(
+                c["conv1_input_grad_roof_us"] / c["conv1_input_grad_us"], 4)}
     if not args.no_legs:
         m = bench_mlp_cfg2(hip, args.steps, 5)
         out["mlp_cfg2"] = {"us_per_step": round(m["us_per_step"], 2),
