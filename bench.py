@@ -246,7 +246,8 @@ def bench_attention_cfg4(hip, steps, warmup):
     """cfg4 attention core as one batched call over batch*heads = 256:
     S = Q.K^T / sqrt(32), P = softmax(S), O = P.V, then the backward bmm
     products dP = dO.V^T, dV = P^T.dO, dS = softmax'(P, dP)/sqrt(32),
-    dQ = dS.K, dK = dS^T.Q (fresh outputs). Plus the block's Linear GEMMs
+    dQ = dS.K, dK = dS^T.Q (fresh outputs; each bmm's two gradients in one
+    nrs_bmm_backward call). Plus the block's Linear GEMMs
     (Q/K/V/O projections 4096x256x256 and FFN 256->1024->256, forward and
     both backward products)."""
     rng = np.random.default_rng(4)
@@ -263,21 +264,21 @@ def bench_attention_cfg4(hip, steps, warmup):
         hip.call("nrs_softmax_forward", P.ptr, S.ptr, BH * T, T)
         hip.bmm(hip.NN, o, P, v, BH, T, Dh, T)
 
+    # each bmm's backward computes both of its gradients in one call, as the
+    # reference's bmm backward closure does (src/cuda/graph/bmm.rs:93-131):
+    # O = P.V (NN): dP = dO.V^T, dV = P^T.dO; S = Q.K^T (NT): dQ = dS.K,
+    # dK = dS^T.Q
     def bwd():
-        hip.bmm(hip.NT, dP, do, v, BH, T, T, Dh)
-        hip.bmm(hip.TN, dv, P, do, BH, T, Dh, T)
+        hip.bmm_backward(hip.NN, dP, dv, do, P, v, BH, T, T, Dh)
         hip.call("nrs_softmax_backward", dS.ptr, P.ptr, dP.ptr, BH * T, T, 0.0)
         hip.call("nrs_scale", dS.ptr, dS.ptr, sc, BH * T * T, 0.0)
-        hip.bmm(hip.NN, dq, dS, k, BH, T, Dh, T)
-        hip.bmm(hip.TN, dk, dS, q, BH, T, Dh, T)
+        hip.bmm_backward(hip.NT, dq, dk, dS, q, k, BH, T, Dh, T)
 
     def bmms_only():
         hip.bmm(hip.NT, S, q, k, BH, T, T, Dh)
         hip.bmm(hip.NN, o, P, v, BH, T, Dh, T)
-        hip.bmm(hip.NT, dP, do, v, BH, T, T, Dh)
-        hip.bmm(hip.TN, dv, P, do, BH, T, Dh, T)
-        hip.bmm(hip.NN, dq, dS, k, BH, T, Dh, T)
-        hip.bmm(hip.TN, dk, dS, q, BH, T, Dh, T)
+        hip.bmm_backward(hip.NN, dP, dv, do, P, v, BH, T, T, Dh)
+        hip.bmm_backward(hip.NT, dq, dk, dS, q, k, BH, T, Dh, T)
 
     fwd()
     fwd_us = event_ms(hip, fwd, steps, warmup) * 1e3

@@ -107,6 +107,21 @@ int nrs_gemm_nt_splitk(float *C, const float *A, const float *B,
 int nrs_bmm(int layout, float *C, const float *A, const float *B,
             int64_t batch, int64_t rows, int64_t cols, int64_t inner, float beta);
 
+/* The backward closure of graph bmm (src/cuda/graph/bmm.rs:93-131): the two
+ * gradients of a forward product per item, with G[b] (m x n) the gradient of
+ * its output C[b] (m x n) and A[b] (m x k):
+ *   NN (the reference's bmm, B[b] k x n, C = A . B):
+ *     dA[b] (m x k) = G . B^T + beta*dA      (bmm_grad_a + accumulate_into)
+ *     dB[b] (k x n) = A^T . G + beta*dB      (bmm_grad_b + accumulate_into)
+ *   NT (bmm(A, transpose(B)) without the transpose, B[b] n x k, C = A . B^T):
+ *     dA[b] (m x k) = G . B + beta*dA,   dB[b] (n x k) = G^T . A + beta*dB
+ * Either of dA, dB may be NULL (that gradient is skipped). Items of at most
+ * 128 x 128 x 128 compute both gradients in one launch. dA and dB must not
+ * overlap each other or A, B, G.                                              */
+int nrs_bmm_backward(int layout, float *dA, float *dB, const float *G, const float *A,
+                     const float *B, int64_t batch, int64_t m, int64_t k, int64_t n,
+                     float beta);
+
 /* ---------------------------------------------------------------- conv2d */
 /* The five primitive launches of src/cuda/nn/conv.rs:161-236, same index
  * semantics (columns grouped by sample: col = ni*out_h*out_w + p).           */

@@ -38,6 +38,7 @@ SIGNATURES = {
     "nrs_gemm": [ctypes.c_int, _P, _P, _P, _I, _I, _I, _F, _P, ctypes.c_int],
     "nrs_gemm_nt_splitk": [_P, _P, _P, _I, _I, _I, _F],
     "nrs_bmm": [ctypes.c_int, _P, _P, _P, _I, _I, _I, _I, _F],
+    "nrs_bmm_backward": [ctypes.c_int, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F],
     "nrs_im2col": [_P, _P] + [_I] * 8,
     "nrs_col2out": [_P, _P, _P, _I, _I, _I, _I],
     "nrs_out2mm": [_P, _P, _I, _I, _I, _I],
@@ -169,6 +170,13 @@ def gemm_nt_splitk(C, A, B, rows, cols, inner, beta=0.0):
 
 def bmm(layout, C, A, B, batch, rows, cols, inner, beta=0.0):
     call("nrs_bmm", layout, _ptr(C), _ptr(A), _ptr(B), batch, rows, cols, inner, beta)
+
+
+def bmm_backward(layout, dA, dB, G, A, B, batch, m, k, n, beta=0.0):
+    """Both gradients of C = A . op(B) per item (A m x k, G m x n; op(B) = B
+    [k x n] for NN, B^T with B [n x k] for NT); dA or dB may be None."""
+    call("nrs_bmm_backward", layout, _ptr(dA), _ptr(dB), _ptr(G), _ptr(A), _ptr(B),
+         batch, m, k, n, beta)
 
 
 def sync():

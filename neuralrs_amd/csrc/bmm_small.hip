@@ -59,14 +59,14 @@ __device__ __forceinline__ f32x4 fragment(__amdgpu_buffer_rsrc_t rs, int r, int 
     return v;
 }
 
+// One workgroup `wg` (of batch * wg_per_item) of the product described by a.
 template <bool AK, bool BKC, int G, int JB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-void bmm_small_kernel(SmallArgs a) {
+__device__ __forceinline__ void bmm_small_block(const SmallArgs& a, int wg) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l32 = lane & 31, h = lane >> 5;
-    const int item = blockIdx.x / a.wg_per_item;
-    const int wi = (blockIdx.x - item * a.wg_per_item) * 4 + wave;
+    const int item = wg / a.wg_per_item;
+    const int wi = (wg - item * a.wg_per_item) * 4 + wave;
     if (wi >= a.waves) return;  // wave-uniform; no barriers follow
     const int bm = wi / a.NJ, bn0 = (wi - bm * a.NJ) * JB;
     const int m = 32 * bm + l32;
@@ -125,6 +125,28 @@ void bmm_small_kernel(SmallArgs a) {
     }
 }
 
+template <bool AK, bool BKC, int G, int JB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void bmm_small_kernel(SmallArgs a) {
+    bmm_small_block<AK, BKC, G, JB>(a, blockIdx.x);
+}
+
+// Both gradients of one bmm in one launch: the first product (NT, or NN
+// with BKCA = false) takes workgroups [0, wg_a), the second (TN) the rest.
+// The launch is paid once and the second product's first workgroups start
+// while the first product's last ones drain. (Interleaving the two in
+// proportion to their counts measured slower on attention's gradients:
+// 27.7 vs 26.3 us for both pairs.)
+template <bool BKCA, int GA, int JBA, int GB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void bmm_small_pair_kernel(SmallArgs ga, SmallArgs gb, int wg_a) {
+    const int x = blockIdx.x;
+    if (x < wg_a)  // uniform
+        bmm_small_block<true, BKCA, GA, JBA>(ga, x);
+    else
+        bmm_small_block<false, false, GB, 1>(gb, x - wg_a);
+}
+
 template <bool AK, bool BKC, int JB>
 void* pick_g(int G) {
     return G <= 4   ? reinterpret_cast<void*>(bmm_small_kernel<AK, BKC, 4, JB>)
@@ -136,10 +158,14 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
 
-int bmm_small(const GemmCall& c) {
+namespace {
+
+// Validates a small-item product and fills its kernel arguments (G, JB:
+// k-groups and column blocks per wave); kBmmUnsupported when it does not
+// qualify (anything unusual, including invalid arguments, which gemm_run
+// reports, goes to the general path).
+int small_args(const GemmCall& c, SmallArgs& a, int& G, int& JB) {
     const int64_t M = c.M, N = c.N, K = c.K, batch = c.batch;
-    // anything unusual (including invalid arguments, which gemm_run reports)
-    // goes to the general path
     if (c.layout < NRS_NN || c.layout > NRS_TN || !c.A || !c.B || !c.C || c.amode != OP_DENSE ||
         c.bmode != OP_DENSE || c.nchw_P != 0 || c.epi != NRS_EPI_NONE)
         return kBmmUnsupported;
@@ -152,9 +178,8 @@ int bmm_small(const GemmCall& c) {
     const int MB = (int)((M + 31) / 32), NB = (int)((N + 31) / 32);
     // two column blocks per wave for NT (its A fragments are then loaded
     // once for both): measured 6.9 vs 7.2 us on attention's Q.K^T
-    const int JB = (c.layout == NRS_NT && NB >= 2) ? 2 : 1;
-    const int G = (int)((K + 7) / 8);
-    SmallArgs a;
+    JB = (c.layout == NRS_NT && NB >= 2) ? 2 : 1;
+    G = (int)((K + 7) / 8);
     a.A = c.A;
     a.B = c.B;
     a.C = c.C;
@@ -169,6 +194,36 @@ int bmm_small(const GemmCall& c) {
     a.wg_per_item = (a.waves + 3) / 4;
     a.beta = c.beta;
     if (batch * a.wg_per_item > INT32_MAX) return kBmmUnsupported;
+    return NRS_OK;
+}
+
+int g_index(int G) { return G <= 4 ? 0 : (G <= 8 ? 1 : 2); }
+
+template <bool BKCA, int GA, int JBA>
+void* pick_pair_b(int GB) {
+    switch (g_index(GB)) {
+        case 0: return reinterpret_cast<void*>(bmm_small_pair_kernel<BKCA, GA, JBA, 4>);
+        case 1: return reinterpret_cast<void*>(bmm_small_pair_kernel<BKCA, GA, JBA, 8>);
+        default: return reinterpret_cast<void*>(bmm_small_pair_kernel<BKCA, GA, JBA, 16>);
+    }
+}
+
+template <bool BKCA, int JBA>
+void* pick_pair(int GA, int GB) {
+    switch (g_index(GA)) {
+        case 0: return pick_pair_b<BKCA, 4, JBA>(GB);
+        case 1: return pick_pair_b<BKCA, 8, JBA>(GB);
+        default: return pick_pair_b<BKCA, 16, JBA>(GB);
+    }
+}
+
+}  // namespace
+
+int bmm_small(const GemmCall& c) {
+    SmallArgs a;
+    int G = 0, JB = 1;
+    const int rc = small_args(c, a, G, JB);
+    if (rc) return rc;
     void* fn;
     switch (c.layout) {
         case NRS_NN: fn = pick_g<true, false, 1>(G); break;
@@ -176,8 +231,25 @@ int bmm_small(const GemmCall& c) {
         default: fn = pick_g<false, false, 1>(G); break;
     }
     hipLaunchKernelGGL(reinterpret_cast<void (*)(SmallArgs)>(fn),
-                       dim3((unsigned)(batch * a.wg_per_item)), dim3(256), 0, stream(), a);
+                       dim3((unsigned)(c.batch * a.wg_per_item)), dim3(256), 0, stream(), a);
     NRS_LAUNCH_CHECK("bmm (small items)");
+    return NRS_OK;
+}
+
+int bmm_small_pair(const GemmCall& ga, const GemmCall& gb) {
+    if ((ga.layout != NRS_NT && ga.layout != NRS_NN) || gb.layout != NRS_TN)
+        return kBmmUnsupported;
+    SmallArgs a, b;
+    int GA = 0, JBA = 1, GB = 0, JBB = 1;
+    if (small_args(ga, a, GA, JBA) || small_args(gb, b, GB, JBB)) return kBmmUnsupported;
+    const int64_t wg_a = ga.batch * a.wg_per_item, wg_b = gb.batch * b.wg_per_item;
+    if (wg_a + wg_b > INT32_MAX) return kBmmUnsupported;
+    void* fn = ga.layout == NRS_NN ? pick_pair<false, 1>(GA, GB)
+               : JBA == 2          ? pick_pair<true, 2>(GA, GB)
+                                   : pick_pair<true, 1>(GA, GB);
+    hipLaunchKernelGGL(reinterpret_cast<void (*)(SmallArgs, SmallArgs, int)>(fn),
+                       dim3((unsigned)(wg_a + wg_b)), dim3(256), 0, stream(), a, b, (int)wg_a);
+    NRS_LAUNCH_CHECK("bmm backward (small items)");
     return NRS_OK;
 }
 

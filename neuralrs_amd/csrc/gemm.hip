@@ -252,6 +252,30 @@ int gemm_run(const GemmCall& c) {
 
 }  // namespace nrs
 
+namespace nrs {
+
+// The GemmCall of one bmm product over contiguous items.
+GemmCall bmm_call(int layout, float* C, const float* A, const float* B, int64_t batch,
+                  int64_t rows, int64_t cols, int64_t inner, float beta) {
+    GemmCall c;
+    c.layout = layout;
+    c.C = C;
+    c.A = A;
+    c.B = B;
+    c.M = rows;
+    c.N = cols;
+    c.K = inner;
+    c.batch = batch;
+    c.sA = rows * inner;
+    c.sB = cols * inner;
+    c.sC = rows * cols;
+    c.beta = beta;
+    c.allow_split = false;
+    return c;
+}
+
+}  // namespace nrs
+
 extern "C" {
 
 int nrs_gemm(int layout, float* C, const float* A, const float* B, int64_t rows, int64_t cols,
@@ -289,22 +313,37 @@ int nrs_gemm_nt_splitk(float* C, const float* A, const float* B, int64_t rows, i
 int nrs_bmm(int layout, float* C, const float* A, const float* B, int64_t batch, int64_t rows,
             int64_t cols, int64_t inner, float beta) {
     NRS_REQUIRE_INIT();
-    nrs::GemmCall c;
-    c.layout = layout;
-    c.C = C;
-    c.A = A;
-    c.B = B;
-    c.M = rows;
-    c.N = cols;
-    c.K = inner;
-    c.batch = batch;
-    c.sA = rows * inner;
-    c.sB = cols * inner;
-    c.sC = rows * cols;
-    c.beta = beta;
-    c.allow_split = false;
+    const nrs::GemmCall c = nrs::bmm_call(layout, C, A, B, batch, rows, cols, inner, beta);
     const int rc = nrs::bmm_small(c);
     return rc == nrs::kBmmUnsupported ? nrs::gemm_run(c) : rc;
+}
+
+int nrs_bmm_backward(int layout, float* dA, float* dB, const float* G, const float* A,
+                     const float* B, int64_t batch, int64_t m, int64_t k, int64_t n, float beta) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(layout == NRS_NN || layout == NRS_NT,
+                  "bmm backward: forward layout must be NN or NT, got %d", layout);
+    // forward NN: C = A . B, B [k][n]: dA = G . B^T (NT), dB = A^T . G (TN);
+    // forward NT: C = A . B^T, B [n][k]: dA = G . B (NN), dB = G^T . A (TN)
+    const bool nn = layout == NRS_NN;
+    const nrs::GemmCall ca =
+        nrs::bmm_call(nn ? NRS_NT : NRS_NN, dA, G, B, batch, m, k, n, beta);
+    const nrs::GemmCall cb = nn ? nrs::bmm_call(NRS_TN, dB, A, G, batch, k, n, m, beta)
+                                : nrs::bmm_call(NRS_TN, dB, G, A, batch, n, k, m, beta);
+    if (dA && dB) {
+        // both gradients of small items: one launch
+        const int rc = nrs::bmm_small_pair(ca, cb);
+        if (rc != nrs::kBmmUnsupported) return rc;
+    }
+    if (dA) {
+        const int rc = nrs_bmm(ca.layout, dA, ca.A, ca.B, batch, ca.M, ca.N, ca.K, beta);
+        if (rc) return rc;
+    }
+    if (dB) {
+        const int rc = nrs_bmm(cb.layout, dB, cb.A, cb.B, batch, cb.M, cb.N, cb.K, beta);
+        if (rc) return rc;
+    }
+    return NRS_OK;
 }
 
 }  // extern "C"

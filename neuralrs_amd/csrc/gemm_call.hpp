@@ -55,5 +55,12 @@ int gemm_run(const GemmCall& c);
 // epilogue; returns kBmmUnsupported (launching nothing) for any other call.
 constexpr int kBmmUnsupported = -1;
 int bmm_small(const GemmCall& c);
+// Two gradient products of one bmm (ga: NT or NN, gb: TN) in one launch when
+// both qualify for bmm_small; kBmmUnsupported (launching nothing) otherwise.
+int bmm_small_pair(const GemmCall& ga, const GemmCall& gb);
+
+// The GemmCall of one bmm product over contiguous items (no split-K).
+GemmCall bmm_call(int layout, float* C, const float* A, const float* B, int64_t batch,
+                  int64_t rows, int64_t cols, int64_t inner, float beta);
 
 }  // namespace nrs

@@ -44,6 +44,7 @@ SHAPES = [  # (rows, cols, inner)
     (128, 256, 64), (256, 128, 784), (100, 10, 9), (256, 10, 128), (300, 300, 300),
     (512, 512, 512), (32, 1024, 512), (1, 513, 257), (1000, 3, 2),
     (130, 17, 33), (257, 32, 96),  # at most 32 columns: 128x32 tiles, ragged rows
+    (2048, 2048, 40), (4096, 1024, 72), (2000, 2048, 36),  # large outputs (the last ragged M)
 ]
 
 
@@ -231,6 +232,44 @@ def test_bmm_exact_integers(hip, shape):
     assert np.array_equal(gB.to_host((bt, k, n)),
                           np.matmul(ai.transpose(0, 2, 1), gi).astype(np.float32))
 
+
+@pytest.mark.parametrize("shape", [(256, 128, 128, 32), (256, 128, 32, 128), (3, 36, 20, 12),
+                                   (2, 5, 7, 9), (4, 128, 128, 128), (2, 64, 96, 40)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("beta", [0.0, 0.5])
+@pytest.mark.parametrize("layout", [NN, NT], ids=lambda l: LNAME[l])
+def test_bmm_backward_both_gradients(hip, layout, shape, beta):
+    """nrs_bmm_backward (bmm.rs:93-131): for C = A . op(B) per item, dA =
+    G . op(B)^T + beta*dA and dB = (A^T . G or G^T . A) + beta*dB, both in
+    one launch for small items (the unaligned 5x7x9 items take the
+    two-product path); exact in f32 for these small integers, also one
+    gradient at a time."""
+    bt, m, k, n = shape
+    rng = np.random.default_rng(sum(shape) + int(4 * beta) + 11 * layout)
+    a = int_matrix(rng, (bt, m, k), -3, 3)
+    b = int_matrix(rng, (bt, k, n) if layout == NN else (bt, n, k), -3, 3)
+    g = int_matrix(rng, (bt, m, n), -3, 3)
+    da0 = int_matrix(rng, (bt, m, k), -8, 8)
+    db0 = int_matrix(rng, b.shape, -8, 8)
+    ai, bi, gi = (x.astype(np.int64) for x in (a, b, g))
+    if layout == NN:
+        want_a = np.matmul(gi, bi.transpose(0, 2, 1))
+        want_b = np.matmul(ai.transpose(0, 2, 1), gi)
+    else:
+        want_a = np.matmul(gi, bi)
+        want_b = np.matmul(gi.transpose(0, 2, 1), ai)
+    want_a = (want_a + beta * da0).astype(np.float32)
+    want_b = (want_b + beta * db0).astype(np.float32)
+    dA, dB, dG = (hip.DeviceBuffer.from_host(x) for x in (a, b, g))
+    gA, gB = hip.DeviceBuffer.from_host(da0), hip.DeviceBuffer.from_host(db0)
+    hip.bmm_backward(layout, gA, gB, dG, dA, dB, bt, m, k, n, beta)
+    assert np.array_equal(gA.to_host(da0.shape), want_a)
+    assert np.array_equal(gB.to_host(db0.shape), want_b)
+    gA1, gB1 = hip.DeviceBuffer.from_host(da0), hip.DeviceBuffer.from_host(db0)
+    hip.bmm_backward(layout, gA1, None, dG, dA, dB, bt, m, k, n, beta)
+    hip.bmm_backward(layout, None, gB1, dG, dA, dB, bt, m, k, n, beta)
+    assert np.array_equal(gA1.to_host(da0.shape), want_a)
+    assert np.array_equal(gB1.to_host(db0.shape), want_b)
 
 @pytest.mark.parametrize("shape", [(5, 40, 36, 24), (3, 20, 13, 8), (2, 128, 128, 100),
                                    (7, 1, 4, 4), (3, 128, 64, 128), (6, 32, 32, 32),
