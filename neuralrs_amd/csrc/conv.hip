@@ -856,9 +856,11 @@ int small_wgrad(float* dweight, float* dbias, const float* grad, const float* in
 
 // dinput += the stride-1 input gradient as a slab convolution of the output
 // gradient with the flipped, channel-transposed weights (padding k-1-pad).
+// With `wg`, the weight gradient it describes runs in the same launch when
+// both fit their slab kernels (*wg_done is then set).
 int slab_dgrad(float* dinput, const float* grad, const float* weight, int64_t N, int64_t c_in,
                int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw, int64_t pad,
-               const ConvDims& d) {
+               const ConvDims& d, const SlabWgrad* wg, bool* wg_done) {
     if (c_in > INT32_MAX || c_out > INT32_MAX || in_h > INT32_MAX || in_w > INT32_MAX)
         return kSlabUnsupported;
     SlabConv s;
@@ -879,6 +881,13 @@ int slab_dgrad(float* dinput, const float* grad, const float* weight, int64_t N,
     s.OW = (int)in_w;
     s.flip = true;
     s.beta = 1.0f;
+    if (wg) {
+        const int rc = slab_backward_pair(s, *wg);
+        if (rc != kSlabUnsupported) {
+            *wg_done = rc == NRS_OK;
+            return rc;
+        }
+    }
     return slab_conv(s);
 }
 
@@ -1026,6 +1035,29 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
     NRS_ARG_CHECK(kh < 32768 && kw < 32768 && c_in * in_h * in_w <= INT32_MAX &&
                       c_out * d.out_h * d.out_w <= INT32_MAX && c_out * kh * kw <= INT32_MAX,
                   "conv2d: kernel or image too large");
+    // the slab weight gradient's arguments (it runs beside a slab input
+    // gradient when both fit, else on its own below)
+    nrs::SlabWgrad w;
+    const bool slab_w = dweight && col_h > nrs::kDirectTaps && c_in <= INT32_MAX &&
+                        c_out <= INT32_MAX && in_h <= INT32_MAX && in_w <= INT32_MAX;
+    if (slab_w) {
+        w.x = input;
+        w.g = grad;
+        w.dw = dweight;
+        w.db = dbias;
+        w.N = N;
+        w.C = (int)c_in;
+        w.H = (int)in_h;
+        w.W = (int)in_w;
+        w.M = (int)c_out;
+        w.kh = (int)kh;
+        w.kw = (int)kw;
+        w.stride = (int)stride;
+        w.pad = (int)pad;
+        w.OH = (int)d.out_h;
+        w.OW = (int)d.out_w;
+    }
+    bool wgrad_done = false;
     if (dinput) {
         const int64_t grad_bytes = N * c_out * P * (int64_t)sizeof(float);
         if ((rc = nrs::small_dgrad(dinput, grad, weight, d)) != nrs::kSlabUnsupported) {
@@ -1044,7 +1076,8 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
             NRS_LAUNCH_CHECK("conv2d input gradient (direct)");
         } else if (stride == 1 && pad <= kh - 1 && pad <= kw - 1 &&
                    (rc = slab_dgrad(dinput, grad, weight, N, c_in, in_h, in_w, c_out, kh, kw,
-                                    pad, d)) != nrs::kSlabUnsupported) {
+                                    pad, d, slab_w ? &w : nullptr, &wgrad_done)) !=
+                       nrs::kSlabUnsupported) {
             // dinput += conv(grad, flipped W) with padding k-1-pad, staged in LDS
             if (rc) return rc;
         } else if (stride == 1 && pad <= kh - 1 && pad <= kw - 1 &&
@@ -1083,6 +1116,7 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
             if (rc) return rc;
         }
     }
+    if (wgrad_done) return NRS_OK;
     if ((dweight || dbias) && col_h <= nrs::kDirectTaps) {
         // few taps: both gradients from one pass over the output gradient
         // (conv.rs:314-322 without the cols matrix), on the matrix cores
@@ -1106,26 +1140,9 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
         if ((rc = nrs::few_taps_wgrad(f)) != nrs::kSlabUnsupported) return rc;
         return nrs::small_wgrad(dweight, dbias, grad, input, d);
     }
-    if (dweight && c_in <= INT32_MAX && c_out <= INT32_MAX && in_h <= INT32_MAX &&
-        in_w <= INT32_MAX) {
+    if (slab_w) {
         // input slab and gradient rows staged in LDS, reduction on the matrix
         // cores, per-image partials summed in a fixed order
-        nrs::SlabWgrad w;
-        w.x = input;
-        w.g = grad;
-        w.dw = dweight;
-        w.db = dbias;
-        w.N = N;
-        w.C = (int)c_in;
-        w.H = (int)in_h;
-        w.W = (int)in_w;
-        w.M = (int)c_out;
-        w.kh = (int)kh;
-        w.kw = (int)kw;
-        w.stride = (int)stride;
-        w.pad = (int)pad;
-        w.OH = (int)d.out_h;
-        w.OW = (int)d.out_w;
         rc = nrs::slab_wgrad(w);
         if (rc != nrs::kSlabUnsupported) return rc;
     }

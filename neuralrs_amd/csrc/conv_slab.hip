@@ -26,12 +26,10 @@
 // reference sums channel-major); results agree to f32 rounding.
 #include <algorithm>
 
-#include "conv_slab.hpp"
+#include "conv_slab_wgrad.hpp"
 
 namespace nrs {
 namespace {
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct SlabArgs {
     const float* x;
@@ -64,11 +62,10 @@ struct SlabCfg {
     static constexpr int WB = NSW >= 7 ? 10 : 20;
 };
 
-// Two waves per SIMD: the LDS budget targets two workgroups per CU, and the
-// 256-VGPR cap keeps the accumulators in place in VGPRs.
+// The work of workgroup (bx, by) = (image * bands + band, output-channel
+// block), with 64 * WM * WN threads.
 template <int WM, int WN, int MSW, int NSW>
-__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2)))
-void conv_slab_kernel(SlabArgs a) {
+__device__ __forceinline__ void slab_block(const SlabArgs& a, int bx, int by) {
     using Cfg = SlabCfg<WM, WN, MSW, NSW>;
     extern __shared__ __attribute__((aligned(16))) float lds[];
     // the wave index is uniform; readfirstlane lets the compiler know, so
@@ -79,8 +76,8 @@ void conv_slab_kernel(SlabArgs a) {
     const int q = lane >> 4, l16 = lane & 15;
 
     uint32_t img, bi;
-    fast_divmod(blockIdx.x, a.div_bands, img, bi);
-    const int m0 = blockIdx.y * Cfg::BM;
+    fast_divmod((uint32_t)bx, a.div_bands, img, bi);
+    const int m0 = by * Cfg::BM;
     const int p0 = (int)bi * a.band;
     const int p_end = min(p0 + a.band, a.P);
     const int oy_first = (int)fast_div((uint32_t)p0, a.div_ow);
@@ -136,7 +133,7 @@ void conv_slab_kernel(SlabArgs a) {
         // consecutive lanes read consecutive input columns. Weight block: a
         // straight copy of its packed LDS image.
         const f32x4* wsrc = reinterpret_cast<const f32x4*>(
-            a.wpack + ((int64_t)(c0 / a.CC) * a.nblk + blockIdx.y) * Cfg::BM * a.wrow);
+            a.wpack + ((int64_t)(c0 / a.CC) * a.nblk + by) * Cfg::BM * a.wrow);
         f32x4* wdst = reinterpret_cast<f32x4*>(ws);
         const int rounds = max((a.x_items + Cfg::NT * Cfg::SB - 1) / (Cfg::NT * Cfg::SB),
                                (a.w_items + Cfg::NT * Cfg::WB - 1) / (Cfg::NT * Cfg::WB));
@@ -348,6 +345,35 @@ void conv_slab_kernel(SlabArgs a) {
     }
 }
 
+// Two waves per SIMD: the LDS budget targets two workgroups per CU, and the
+// 256-VGPR cap keeps the accumulators in place in VGPRs.
+template <int WM, int WN, int MSW, int NSW>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2)))
+void conv_slab_kernel(SlabArgs a) {
+    slab_block<WM, WN, MSW, NSW>(a, blockIdx.x, blockIdx.y);
+}
+
+// The input gradient (a flipped slab convolution, d) and the weight
+// gradient (w) of one backward call in one launch: workgroups [0, nw) are
+// the weight gradient's, in its (x, y, z) grid order, the rest the input
+// gradient's. The weight-gradient workgroups are the longer ones and start
+// first; the input-gradient workgroups fill the CU slots beside them and
+// after them, where the weight gradient alone would leave one workgroup
+// slot per CU idle.
+template <int WM, int WN, int MSW, int NSW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void conv_bwd_pair_kernel(WgradArgs w, SlabArgs d, int wgx, int wgy, int nw, int dgx) {
+    static_assert(WM * WN == 4, "both bodies run 256 threads");
+    const int x = blockIdx.x;
+    if (x < nw) {  // uniform
+        const int yz = x / wgx, y = yz % wgy;
+        wgrad_block<kTapw>(w, x - yz * wgx, y, yz / wgy);
+    } else {
+        const int e = x - nw, by = e / dgx;
+        slab_block<WM, WN, MSW, NSW>(d, e - by * dgx, by);
+    }
+}
+
 // Packs the weights of a slab convolution into the LDS image the kernel
 // stages: packed[((chunk * nblk + blk) * BM + m) * wrow + tap * CC + c] =
 // weight (m0 + m, c0 + c, tap), zero outside the tensor and in the row pad,
@@ -420,11 +446,12 @@ SlabPlan plan_slab(const SlabConv& s) {
     return pl;
 }
 
+// Packs the weights (one launch) and fills the kernel arguments and grid.
 template <int WM, int WN, int MSW, int NSW>
-int launch_slab(const SlabConv& s, const SlabPlan& pl) {
+int prepare_slab(const SlabConv& s, const SlabPlan& pl, SlabArgs& a, unsigned& gx,
+                 unsigned& gy) {
     using Cfg = SlabCfg<WM, WN, MSW, NSW>;
     const int64_t P = (int64_t)s.OH * s.OW, taps = (int64_t)s.kh * s.kw;
-    SlabArgs a;
     a.x = s.x;
     a.w = s.w;
     a.bias = s.bias;
@@ -468,44 +495,112 @@ int launch_slab(const SlabConv& s, const SlabPlan& pl) {
     a.div_ow = make_fastdiv((uint32_t)s.OW);
     a.div_psn = make_fastdiv((uint32_t)(pl.slab_rows * pl.slab_w));
     a.div_slab_w = make_fastdiv((uint32_t)pl.slab_w);
+    gx = (unsigned)(s.N * pl.nb);
+    gy = (unsigned)((s.M + Cfg::BM - 1) / Cfg::BM);
+    return NRS_OK;
+}
 
-    auto fn = conv_slab_kernel<WM, WN, MSW, NSW>;
-    static bool attr_set = false;
-    if (!attr_set) {
+// Raises a kernel's dynamic LDS limit to the whole 160 KB, once per process.
+template <typename F>
+int allow_full_lds(F fn, bool& done) {
+    if (!done) {
         NRS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes));
-        attr_set = true;
+        done = true;
     }
-    const unsigned gx = (unsigned)(s.N * pl.nb), gy = (unsigned)((s.M + Cfg::BM - 1) / Cfg::BM);
+    return NRS_OK;
+}
+
+template <int WM, int WN, int MSW, int NSW>
+int launch_slab(const SlabConv& s, const SlabPlan& pl) {
+    using Cfg = SlabCfg<WM, WN, MSW, NSW>;
+    SlabArgs a;
+    unsigned gx = 0, gy = 0;
+    const int rc = prepare_slab<WM, WN, MSW, NSW>(s, pl, a, gx, gy);
+    if (rc) return rc;
+    auto fn = conv_slab_kernel<WM, WN, MSW, NSW>;
+    static bool attr_set = false;
+    if (allow_full_lds(fn, attr_set)) return NRS_ERR_HIP;
     hipLaunchKernelGGL(fn, dim3(gx, gy), dim3(Cfg::NT), pl.lds, stream(), a);
     NRS_LAUNCH_CHECK("conv2d (slab)");
     return NRS_OK;
+}
+
+template <int WM, int WN, int MSW, int NSW>
+int launch_pair(const SlabConv& s, const SlabPlan& pl, const WgradPlan& wp) {
+    SlabArgs a;
+    unsigned gx = 0, gy = 0;
+    const int rc = prepare_slab<WM, WN, MSW, NSW>(s, pl, a, gx, gy);
+    if (rc) return rc;
+    const int64_t nw = (int64_t)wp.gx * wp.gy * wp.gz, total = nw + (int64_t)gx * gy;
+    auto fn = conv_bwd_pair_kernel<WM, WN, MSW, NSW>;
+    static bool attr_set = false;
+    if (allow_full_lds(fn, attr_set)) return NRS_ERR_HIP;
+    hipLaunchKernelGGL(fn, dim3((unsigned)total), dim3(256), std::max(pl.lds, wp.lds), stream(),
+                       wp.a, a, (int)wp.gx, (int)wp.gy, (int)nw, (int)gx);
+    NRS_LAUNCH_CHECK("conv2d backward (slab pair)");
+    return NRS_OK;
+}
+
+// Slab configuration for a convolution: 0, 1, 2 for 64 x 112, 32 x 128 and
+// 16 x 128 tiles (channels x pixels), -1 when none fits. Takes the widest
+// whose LDS lets two workgroups share a CU (one stages while the other
+// computes), else the widest that fits at all.
+int pick_slab(const SlabConv& s, SlabPlan& pl) {
+    const SlabPlan p64 = s.M >= 48 ? plan_slab<4, 1, 1, 7>(s) : SlabPlan{};
+    const SlabPlan p32 = s.M > 16 ? plan_slab<2, 2, 1, 4>(s) : SlabPlan{};
+    const SlabPlan p16 = plan_slab<1, 4, 1, 2>(s);
+    constexpr size_t kHalf = kLdsBytes / 2;
+    const SlabPlan* plans[3] = {&p64, &p32, &p16};
+    for (int k = 0; k < 3; ++k)
+        if (plans[k]->lds && plans[k]->lds <= kHalf) return pl = *plans[k], k;
+    for (int k = 0; k < 3; ++k)
+        if (plans[k]->lds) return pl = *plans[k], k;
+    return -1;
+}
+
+// The shape checks every slab convolution needs before planning.
+bool slab_shape_ok(const SlabConv& s) {
+    if (s.C <= 0 || s.kh <= 0 || s.kw <= 0 || s.stride <= 0) return false;
+    // staged channel chunks must be at least a quarter real channels
+    if (round_up(s.C, 16) > 4 * (int64_t)s.C) return false;
+    return (int64_t)s.C * s.H * s.W <= INT32_MAX && (int64_t)s.OH * s.OW <= INT32_MAX / 2;
 }
 
 }  // namespace
 
 int slab_conv(const SlabConv& s) {
     if (s.N == 0 || s.M == 0 || s.OH == 0 || s.OW == 0) return NRS_OK;
-    if (s.C <= 0 || s.kh <= 0 || s.kw <= 0 || s.stride <= 0) return kSlabUnsupported;
-    // staged channel chunks must be at least a quarter real channels
-    if (round_up(s.C, 16) > 4 * (int64_t)s.C) return kSlabUnsupported;
-    if ((int64_t)s.C * s.H * s.W > INT32_MAX || (int64_t)s.OH * s.OW > INT32_MAX / 2)
+    if (!slab_shape_ok(s)) return kSlabUnsupported;
+    SlabPlan pl;
+    switch (pick_slab(s, pl)) {
+        case 0: return launch_slab<4, 1, 1, 7>(s, pl);
+        case 1: return launch_slab<2, 2, 1, 4>(s, pl);
+        case 2: return launch_slab<1, 4, 1, 2>(s, pl);
+        default: return kSlabUnsupported;
+    }
+}
+
+int slab_backward_pair(const SlabConv& d, const SlabWgrad& w) {
+    if (d.N == 0 || d.M == 0 || d.OH == 0 || d.OW == 0 || !slab_shape_ok(d))
         return kSlabUnsupported;
-    // Tile configurations, widest output-channel block first: 64 x 112,
-    // 32 x 128 and 16 x 128 (channels x pixels). Take the widest whose LDS
-    // lets two workgroups share a CU (one stages while the other computes),
-    // else the widest that fits at all.
-    const SlabPlan p64 = s.M >= 48 ? plan_slab<4, 1, 1, 7>(s) : SlabPlan{};
-    const SlabPlan p32 = s.M > 16 ? plan_slab<2, 2, 1, 4>(s) : SlabPlan{};
-    const SlabPlan p16 = plan_slab<1, 4, 1, 2>(s);
-    constexpr size_t kHalf = kLdsBytes / 2;
-    if (p64.lds && p64.lds <= kHalf) return launch_slab<4, 1, 1, 7>(s, p64);
-    if (p32.lds && p32.lds <= kHalf) return launch_slab<2, 2, 1, 4>(s, p32);
-    if (p16.lds && p16.lds <= kHalf) return launch_slab<1, 4, 1, 2>(s, p16);
-    if (p64.lds) return launch_slab<4, 1, 1, 7>(s, p64);
-    if (p32.lds) return launch_slab<2, 2, 1, 4>(s, p32);
-    if (p16.lds) return launch_slab<1, 4, 1, 2>(s, p16);
-    return kSlabUnsupported;
+    SlabPlan pl;
+    const int cfg = pick_slab(d, pl);
+    if (cfg < 0) return kSlabUnsupported;
+    const int64_t bm = cfg == 0 ? 64 : (cfg == 1 ? 32 : 16);
+    const int64_t d_wgs = d.N * pl.nb * ((d.M + bm - 1) / bm);
+    WgradPlan wp;
+    int rc = plan_slab_wgrad(w, wp);
+    if (rc) return rc;
+    if ((int64_t)wp.gx * wp.gy * wp.gz + d_wgs > INT32_MAX || d.N * pl.nb > INT32_MAX)
+        return kSlabUnsupported;
+    switch (cfg) {
+        case 0: rc = launch_pair<4, 1, 1, 7>(d, pl, wp); break;
+        case 1: rc = launch_pair<2, 2, 1, 4>(d, pl, wp); break;
+        default: rc = launch_pair<1, 4, 1, 2>(d, pl, wp); break;
+    }
+    if (rc) return rc;
+    return slab_wgrad_sum(w, wp);
 }
 
 }  // namespace nrs

@@ -45,6 +45,12 @@ struct SlabWgrad {
 };
 int slab_wgrad(const SlabWgrad& s);
 
+// The stride-1 input gradient d (a slab convolution with flip) and the
+// weight gradient w of one backward call, in one launch of both kernels'
+// workgroups (then the weight gradient's partial sum). Returns
+// kSlabUnsupported (launching nothing) unless both fit their kernels.
+int slab_backward_pair(const SlabConv& d, const SlabWgrad& w);
+
 // Weight and bias gradient of a convolution with c_in*kh*kw <= 15 taps and at
 // most 64 output channels, on the matrix cores (conv_few_taps.hip): dw += and
 // db += (either may be null). Returns kSlabUnsupported (launching nothing)

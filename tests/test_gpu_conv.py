@@ -181,6 +181,26 @@ def test_conv2d_backward_bias_only(hip, orc, shape):
     assert np.array_equal(gB.to_host(), db_ref)
 
 
+@pytest.mark.parametrize("shape", [(4, 16, 32, 12, 12, 3, 3, 1, 1), (1, 160, 20, 5, 5, 3, 3, 1, 1),
+                                   (1, 40, 70, 6, 7, 3, 3, 1, 1)],
+                         ids=["16x128", "64x112", "32x128"])
+def test_conv2d_backward_no_bias_grad(hip, orc, shape):
+    """dbias = NULL with the input and weight gradients in one launch (each
+    slab tile configuration): the weight gradient alone lands in dweight."""
+    n, ci, co, h, w, kh, kw, s, p = shape
+    rng = np.random.default_rng(79)
+    x = int_matrix(rng, (n * ci * h * w,), -3, 3)
+    wt = int_matrix(rng, (co * ci * kh * kw,), -3, 3)
+    oh, ow = orc.conv_out_hw(h, w, kh, kw, s, p)
+    g = int_matrix(rng, (n * co * oh * ow,), -3, 3)
+    di_ref, dw_ref, _ = orc.conv2d_backward(x, wt, g, n, ci, co, h, w, kh, kw, s, p)
+    gI, gW = hip.DeviceBuffer.zeros(x.size), hip.DeviceBuffer.zeros(wt.size)
+    hip.call("nrs_conv2d_backward", gI.ptr, gW.ptr, None, D(hip, g), D(hip, x),
+             D(hip, wt), n, ci, h, w, co, kh, kw, s, p)
+    assert np.array_equal(gI.to_host(), di_ref)
+    assert np.array_equal(gW.to_host(), dw_ref)
+
+
 def test_conv2d_cfg3_layers(hip, orc):
     """cfg3 shapes (batch 128, 1->32 @28x28 and 32->64 @14x14, 3x3 pad 1):
     GPU forward/backward against the restated CPU Conv2d on the same data."""
