@@ -123,6 +123,10 @@ __device__ __forceinline__ void slab_block(const SlabArgs& a, int bx, int by) {
         }
 
     const float* ximg = a.x + (int64_t)img * a.C * HW;
+    // the image as a buffer: a load at kOutOfRange returns zero, so the
+    // padding needs no select after the load (a select would make the
+    // compiler wait for each item's loads before issuing the next item's)
+    const auto rx = buffer_rsrc(ximg, (int64_t)a.C * HW * 4);
     for (int c0 = 0; c0 < a.C; c0 += a.CC) {
         if (c0) __syncthreads();  // the previous chunk's reads are done
         // Staging: each round issues up to Cfg::SB slab items and
@@ -132,8 +136,9 @@ __device__ __forceinline__ void slab_block(const SlabArgs& a, int bx, int by) {
         // Input slab: item = (channel quad, slab pixel), pixels fastest so
         // consecutive lanes read consecutive input columns. Weight block: a
         // straight copy of its packed LDS image.
-        const f32x4* wsrc = reinterpret_cast<const f32x4*>(
-            a.wpack + ((int64_t)(c0 / a.CC) * a.nblk + by) * Cfg::BM * a.wrow);
+        const auto rw = buffer_rsrc(
+            a.wpack + ((int64_t)(c0 / a.CC) * a.nblk + by) * Cfg::BM * a.wrow,
+            (int64_t)a.w_items * 16);
         f32x4* wdst = reinterpret_cast<f32x4*>(ws);
         const int rounds = max((a.x_items + Cfg::NT * Cfg::SB - 1) / (Cfg::NT * Cfg::SB),
                                (a.w_items + Cfg::NT * Cfg::WB - 1) / (Cfg::NT * Cfg::WB));
@@ -157,23 +162,26 @@ __device__ __forceinline__ void slab_block(const SlabArgs& a, int bx, int by) {
                     const bool in =
                         live & ((unsigned)iy < (unsigned)a.H) & ((unsigned)ix < (unsigned)a.W);
                     const int c = c0 + 4 * (int)c4;
-                    const float* src = ximg + (int64_t)c * HW + iy * a.W + ix;
-                    // branch-free: masked lanes load the image's first element
+                    const int off = (c * HW + iy * a.W + ix) * 4;  // bytes
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
                         const bool ok = in & (c + u < a.C);
-                        const float t = *(ok ? src + u * HW : ximg);
-                        v[b][u] = ok ? t : 0.0f;
+                        v[b][u] = buffer_load1(rx, ok ? off + u * HW * 4 : kOutOfRange);
                     }
                     dst[b] = live ? (int)(pos * a.ps + 4 * c4) : -1;
                 }
             }
             if (wrun) {
+                // a load past the block returns zero (those lanes store nothing)
 #pragma unroll
                 for (int b = 0; b < Cfg::WB; ++b)
                     if (wbase + b * Cfg::NT < a.w_items)  // uniform
-                        wv[b] = wsrc[min(wbase + tid + b * Cfg::NT, a.w_items - 1)];
+                        wv[b] = buffer_load4(rw, (wbase + tid + b * Cfg::NT) * 16);
             }
+            // every load before the first LDS store (the scheduler would
+            // otherwise sink some past the stores' waits: a second round
+            // trip)
+            __builtin_amdgcn_sched_barrier(0);
             if (xrun) {
 #pragma unroll
                 for (int b = 0; b < Cfg::SB; ++b)
@@ -187,6 +195,11 @@ __device__ __forceinline__ void slab_block(const SlabArgs& a, int bx, int by) {
                     if (e < a.w_items) wdst[e] = wv[b];
                 }
             }
+            // nothing outstanding at the loop edge: otherwise the compiler
+            // assumes the (conditional) stores may have left loads pending
+            // and waits for all of a round's slab loads before its weight
+            // loads
+            __builtin_amdgcn_s_waitcnt(0);
         }
         __syncthreads();
 
@@ -360,14 +373,14 @@ void conv_slab_kernel(SlabArgs a) {
 // first; the input-gradient workgroups fill the CU slots beside them and
 // after them, where the weight gradient alone would leave one workgroup
 // slot per CU idle.
-template <int WM, int WN, int MSW, int NSW>
+template <int WM, int WN, int MSW, int NSW, bool VEC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void conv_bwd_pair_kernel(WgradArgs w, SlabArgs d, int wgx, int wgy, int nw, int dgx) {
     static_assert(WM * WN == 4, "both bodies run 256 threads");
     const int x = blockIdx.x;
     if (x < nw) {  // uniform
         const int yz = x / wgx, y = yz % wgy;
-        wgrad_block<kTapw>(w, x - yz * wgx, y, yz / wgy);
+        wgrad_block<kTapw, VEC>(w, x - yz * wgx, y, yz / wgy);
     } else {
         const int e = x - nw, by = e / dgx;
         slab_block<WM, WN, MSW, NSW>(d, e - by * dgx, by);
@@ -434,9 +447,10 @@ SlabPlan plan_slab(const SlabConv& s) {
     int64_t CC = round_up(s.C, 16);
     while (CC > 16 && bytes(CC) > kLdsBytes) CC -= 16;
     const int64_t grid_x = s.N * pl.nb, grid_y = (s.M + Cfg::BM - 1) / Cfg::BM;
+    // (the weight block's byte offsets must fit the buffer loads' 31 bits)
     if (bytes(CC) > kLdsBytes || grid_x > INT32_MAX || grid_y > 65535 ||
         pl.slab_rows * pl.slab_w * (CC / 4) > INT32_MAX / 2 ||
-        Cfg::BM * taps * CC > INT32_MAX / 2)
+        Cfg::BM * (taps * CC + 4) > INT32_MAX / 4)
         return SlabPlan{};
     pl.CC = CC;
     // the epilogue's per-wave tiles reuse the same LDS
@@ -533,9 +547,10 @@ int launch_pair(const SlabConv& s, const SlabPlan& pl, const WgradPlan& wp) {
     const int rc = prepare_slab<WM, WN, MSW, NSW>(s, pl, a, gx, gy);
     if (rc) return rc;
     const int64_t nw = (int64_t)wp.gx * wp.gy * wp.gz, total = nw + (int64_t)gx * gy;
-    auto fn = conv_bwd_pair_kernel<WM, WN, MSW, NSW>;
-    static bool attr_set = false;
-    if (allow_full_lds(fn, attr_set)) return NRS_ERR_HIP;
+    auto fn = wp.a.vec_g ? conv_bwd_pair_kernel<WM, WN, MSW, NSW, true>
+                         : conv_bwd_pair_kernel<WM, WN, MSW, NSW, false>;
+    static bool attr_set[2] = {false, false};
+    if (allow_full_lds(fn, attr_set[wp.a.vec_g])) return NRS_ERR_HIP;
     hipLaunchKernelGGL(fn, dim3((unsigned)total), dim3(256), std::max(pl.lds, wp.lds), stream(),
                        wp.a, a, (int)wp.gx, (int)wp.gy, (int)nw, (int)gx);
     NRS_LAUNCH_CHECK("conv2d backward (slab pair)");
@@ -564,7 +579,8 @@ bool slab_shape_ok(const SlabConv& s) {
     if (s.C <= 0 || s.kh <= 0 || s.kw <= 0 || s.stride <= 0) return false;
     // staged channel chunks must be at least a quarter real channels
     if (round_up(s.C, 16) > 4 * (int64_t)s.C) return false;
-    return (int64_t)s.C * s.H * s.W <= INT32_MAX && (int64_t)s.OH * s.OW <= INT32_MAX / 2;
+    // an image's byte offsets fit the buffer loads' 31-bit range
+    return (int64_t)s.C * s.H * s.W <= INT32_MAX / 4 && (int64_t)s.OH * s.OW <= INT32_MAX / 2;
 }
 
 }  // namespace

@@ -7,10 +7,10 @@
 namespace nrs {
 namespace {
 
-template <int TAPW>
+template <int TAPW, bool VEC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void conv_slab_wgrad_kernel(WgradArgs a) {
-    wgrad_block<TAPW>(a, blockIdx.x, blockIdx.y, blockIdx.z);
+    wgrad_block<TAPW, VEC>(a, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // dw[m][c][tap] += sum over slices of part_w[slice][m][tap][c] and
@@ -103,8 +103,8 @@ int plan_slab_wgrad(const SlabWgrad& s, WgradPlan& p) {
     const int64_t nw = (int64_t)s.M * taps * s.C;
     if (slices > INT32_MAX || cparts * ntg > 65535 || mblocks > 65535 ||
         slices * cparts * ntg * mblocks > INT32_MAX ||
-        slices * (nw + s.M) > ((int64_t)1 << 31) || (int64_t)s.C * s.H * s.W > INT32_MAX ||
-        (int64_t)s.M * s.OH * s.OW > INT32_MAX || nw + s.M > INT32_MAX)
+        slices * (nw + s.M) > ((int64_t)1 << 31) || (int64_t)s.C * s.H * s.W > INT32_MAX / 4 ||
+        (int64_t)s.M * s.OH * s.OW > INT32_MAX / 4 || nw + s.M > INT32_MAX)
         return kSlabUnsupported;
 
     float* part = workspace(sizeof(float) * (size_t)(slices * (nw + s.M)), 3);
@@ -164,12 +164,12 @@ int slab_wgrad(const SlabWgrad& s) {
     WgradPlan p;
     const int rc = plan_slab_wgrad(s, p);
     if (rc) return rc;
-    auto fn = conv_slab_wgrad_kernel<kTapw>;
-    static bool attr_set = false;
-    if (!attr_set) {
+    auto fn = p.a.vec_g ? conv_slab_wgrad_kernel<kTapw, true> : conv_slab_wgrad_kernel<kTapw, false>;
+    static bool attr_set[2] = {false, false};
+    if (!attr_set[p.a.vec_g]) {
         NRS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes));
-        attr_set = true;
+        attr_set[p.a.vec_g] = true;
     }
     hipLaunchKernelGGL(fn, dim3(p.gx, p.gy, p.gz), dim3(256), p.lds, stream(), p.a);
     NRS_LAUNCH_CHECK("conv2d weight gradient (slab)");

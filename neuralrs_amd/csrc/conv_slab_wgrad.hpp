@@ -55,8 +55,11 @@ constexpr int kTapw = 9;  // taps per workgroup (a 3x3 kernel in one group)
 
 // The work of workgroup (bx, by, bz) = (slice, channel part * tap groups +
 // tap group, output-channel block); 256 threads, with the LDS bytes of the
-// launch plan below.
-template <int TAPW>
+// launch plan below. VEC (= a.vec_g) stages the gradient rows with 128-bit
+// loads; it is a template parameter so that each form is one straight run
+// of loads (a branch between the two forms made the compiler wait for the
+// loads at the join).
+template <int TAPW, bool VEC>
 __device__ __forceinline__ void wgrad_block(const WgradArgs& a, int bx, int by, int bz) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -89,6 +92,11 @@ __device__ __forceinline__ void wgrad_block(const WgradArgs& a, int bx, int by, 
     const float* gimg = a.g + ((int64_t)img * a.M + m0) * a.OH * a.OW + (int64_t)oy0 * a.OW;
     const int KP4 = a.KP >> 2, g_items = kWgM * KP4;
     const float* ximg = a.x + ((int64_t)img * a.C + c0) * a.H * a.W;
+    // both as buffers: a load at kOutOfRange returns zero, so masked items
+    // need no select after the load (which would make the compiler wait for
+    // each item's load before issuing the next)
+    const auto rg = buffer_rsrc(gimg, (int64_t)kWgM * a.OH * a.OW * 4);
+    const auto rx = buffer_rsrc(ximg, (int64_t)kWgC * a.H * a.W * 4);
     const int x_items = kWgC * srw;
     const int rows_in = (rows_b - 1) * a.stride + a.kh;
     const int rounds = max((g_items + 256 * kWgStageG - 1) / (256 * kWgStageG),
@@ -97,34 +105,29 @@ __device__ __forceinline__ void wgrad_block(const WgradArgs& a, int bx, int by, 
         const int gbase = rd * 256 * kWgStageG, xbase = rd * 256 * kWgStageX;
         f32x4 gv[kWgStageG];
         float xv[kWgStageX];
-        int gdst[kWgStageG], xdst[kWgStageX];
+        int gdst[kWgStageG], xdst[kWgStageX], goff[kWgStageG], glen[kWgStageG], xoff[kWgStageX];
+        // addresses first, then every load of the round in straight-line
+        // code (no per-item branch between two load forms), so a thread
+        // issues them all before its first wait
 #pragma unroll
         for (int b = 0; b < kWgStageG; ++b) {
             gdst[b] = -1;
+            goff[b] = kOutOfRange;
+            glen[b] = 0;
             if (gbase + b * 256 >= g_items) continue;  // uniform
             const int e = gbase + b * 256 + tid;
             uint32_t m, k4;
             fast_divmod((uint32_t)min(e, g_items - 1), a.div_kp4, m, k4);
             const int kk = 4 * (int)k4;
             const bool row = (e < g_items) & (m0 + (int)m < a.M);
-            const float* src = gimg + (int64_t)m * a.OH * a.OW + kk;
-            if (a.vec_g) {
-                const bool ok = row & (kk < PB);
-                gv[b] = *reinterpret_cast<const f32x4*>(ok ? src : gimg);
-                if (!ok) gv[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            } else {
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const bool ok = row & (kk + u < PB);
-                    const float t = *(ok ? src + u : gimg);
-                    gv[b][u] = ok ? t : 0.0f;
-                }
-            }
+            goff[b] = ((int)m * a.OH * a.OW + kk) * 4;  // bytes
+            glen[b] = row ? PB - kk : 0;  // gradient floats from kk on (<= 0: none)
             gdst[b] = e < g_items ? (int)m * a.KPP + kk : -1;
         }
 #pragma unroll
         for (int b = 0; b < kWgStageX; ++b) {
             xdst[b] = -1;
+            xoff[b] = kOutOfRange;
             if (xbase + b * 256 >= x_items) continue;  // uniform
             const int e = xbase + b * 256 + tid;
             uint32_t c, pos, r, col;
@@ -133,16 +136,37 @@ __device__ __forceinline__ void wgrad_block(const WgradArgs& a, int bx, int by, 
             const int iy = iy0 + (int)r, ix = (int)col - a.pad_w;
             const bool ok = (e < x_items) & ((int)r < rows_in) & (c0 + (int)c < a.C) &
                             ((unsigned)iy < (unsigned)a.H) & ((unsigned)ix < (unsigned)a.W);
-            const float t = ximg[ok ? ((int64_t)c * a.H + iy) * a.W + ix : 0];
-            xv[b] = ok ? t : 0.0f;
+            xoff[b] = ok ? (((int)c * a.H + iy) * a.W + ix) * 4 : kOutOfRange;
             xdst[b] = e < x_items ? (int)c * a.CS + (int)pos : -1;
         }
+        if constexpr (VEC) {  // rows of whole float4s
+#pragma unroll
+            for (int b = 0; b < kWgStageG; ++b)
+                if (gbase + b * 256 < g_items)
+                    gv[b] = buffer_load4(rg, glen[b] > 0 ? goff[b] : kOutOfRange);
+        } else {
+#pragma unroll
+            for (int b = 0; b < kWgStageG; ++b)
+                if (gbase + b * 256 < g_items)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        gv[b][u] = buffer_load1(rg, u < glen[b] ? goff[b] + 4 * u : kOutOfRange);
+        }
+#pragma unroll
+        for (int b = 0; b < kWgStageX; ++b)
+            if (xbase + b * 256 < x_items) xv[b] = buffer_load1(rx, xoff[b]);
+        // every load before the first LDS store (the scheduler would
+        // otherwise sink some past the stores' waits: a second round trip)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int b = 0; b < kWgStageG; ++b)
             if (gdst[b] >= 0) *reinterpret_cast<f32x4*>(gs + gdst[b]) = gv[b];
 #pragma unroll
         for (int b = 0; b < kWgStageX; ++b)
             if (xdst[b] >= 0) xs[xdst[b]] = xv[b];
+        // nothing outstanding at the loop edge (else the compiler waits for
+        // the whole previous batch before the next round's first load)
+        __builtin_amdgcn_s_waitcnt(0);
     }
     // slab offset of each band pixel (0 for the padding pixels, whose
     // gradient is zero)
