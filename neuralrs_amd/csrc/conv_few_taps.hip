@@ -32,6 +32,7 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 constexpr int kFewTaps = 15;   // taps per channel (one MFMA column is the bias)
 constexpr int kFewMaxM = 64;   // output channels (four blocks of 16)
 constexpr int kFewImage = 16384;  // staged image floats (64 KB)
+constexpr int kStageX = 4;        // image floats per thread per staging round
 
 struct FewTapsArgs {
     const float* x;
@@ -67,15 +68,29 @@ void wgrad_few_taps_kernel(FewTapsArgs a) {
         }
     }
 
-    // the image with a zero halo of `pad` (rows and columns)
-    const float* img = a.x + (int64_t)n * a.C * a.H * a.W;
+    // the image with a zero halo of `pad` (rows and columns), kStageX items
+    // per thread per round: every load of a round is issued before its
+    // stores (a load at kOutOfRange returns zero, so the halo needs no
+    // select that would make each load wait for the previous)
+    const auto rimg =
+        buffer_rsrc(a.x + (int64_t)n * a.C * a.H * a.W, (int64_t)a.C * a.H * a.W * 4);
     const int plane = a.Hp * a.Wp, xn = a.C * plane;
-    for (int e = tid; e < xn; e += 256) {
-        const int c = e / plane, r = e - c * plane, yy = r / a.Wp, xx = r - yy * a.Wp;
-        const int iy = yy - a.pad, ix = xx - a.pad;
-        const bool ok = ((unsigned)iy < (unsigned)a.H) & ((unsigned)ix < (unsigned)a.W);
-        const float v = img[ok ? (c * a.H + iy) * a.W + ix : 0];
-        xs[e] = ok ? v : 0.0f;
+    for (int e0 = 0; e0 < xn; e0 += 256 * kStageX) {
+        float v[kStageX];
+#pragma unroll
+        for (int k = 0; k < kStageX; ++k) {
+            const int e = e0 + k * 256 + tid;
+            const int c = e / plane, r = e - c * plane, yy = r / a.Wp, xx = r - yy * a.Wp;
+            const int iy = yy - a.pad, ix = xx - a.pad;
+            const bool ok = (e < xn) & ((unsigned)iy < (unsigned)a.H) & ((unsigned)ix < (unsigned)a.W);
+            v[k] = buffer_load1(rimg, ok ? ((c * a.H + iy) * a.W + ix) * 4 : kOutOfRange);
+        }
+#pragma unroll
+        for (int k = 0; k < kStageX; ++k)
+            if (e0 + k * 256 + tid < xn) xs[e0 + k * 256 + tid] = v[k];
+        // nothing outstanding at the loop edge: the compiler would otherwise
+        // wait for the gradient loads above before the first image load
+        __builtin_amdgcn_s_waitcnt(0);
     }
     // this lane's tap: offset in the staged image, or the bias column
     int toff = 0;

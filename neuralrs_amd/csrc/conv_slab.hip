@@ -421,7 +421,7 @@ struct SlabPlan {
 };
 
 template <int WM, int WN, int MSW, int NSW>
-SlabPlan plan_slab(const SlabConv& s) {
+SlabPlan plan_slab(const SlabConv& s, int64_t lds_cap = kLdsBytes) {
     using Cfg = SlabCfg<WM, WN, MSW, NSW>;
     SlabPlan pl;
     const int64_t P = (int64_t)s.OH * s.OW, taps = (int64_t)s.kh * s.kw;
@@ -441,11 +441,12 @@ SlabPlan plan_slab(const SlabConv& s) {
     pl.slab_rows = (out_rows - 1) * s.stride + s.kh;
     pl.slab_w = (int64_t)(s.OW - 1) * s.stride + s.kw;
     // the largest channel chunk (multiple of 16) whose slab and weights fit
+    // in lds_cap bytes
     auto bytes = [&](int64_t cc) {
         return 4 * (pl.slab_rows * pl.slab_w * (cc + 4) + Cfg::BM * (taps * cc + 4));
     };
     int64_t CC = round_up(s.C, 16);
-    while (CC > 16 && bytes(CC) > kLdsBytes) CC -= 16;
+    while (CC > 16 && bytes(CC) > lds_cap) CC -= 16;
     const int64_t grid_x = s.N * pl.nb, grid_y = (s.M + Cfg::BM - 1) / Cfg::BM;
     // (the weight block's byte offsets must fit the buffer loads' 31 bits)
     if (bytes(CC) > kLdsBytes || grid_x > INT32_MAX || grid_y > 65535 ||
@@ -560,12 +561,16 @@ int launch_pair(const SlabConv& s, const SlabPlan& pl, const WgradPlan& wp) {
 // Slab configuration for a convolution: 0, 1, 2 for 64 x 112, 32 x 128 and
 // 16 x 128 tiles (channels x pixels), -1 when none fits. Takes the widest
 // whose LDS lets two workgroups share a CU (one stages while the other
-// computes), else the widest that fits at all.
-int pick_slab(const SlabConv& s, SlabPlan& pl) {
-    const SlabPlan p64 = s.M >= 48 ? plan_slab<4, 1, 1, 7>(s) : SlabPlan{};
-    const SlabPlan p32 = s.M > 16 ? plan_slab<2, 2, 1, 4>(s) : SlabPlan{};
-    const SlabPlan p16 = plan_slab<1, 4, 1, 2>(s);
+// computes), else the widest that fits at all. With `chunked`, a tile may
+// stage its channels in smaller chunks to fit half the LDS: beside the
+// weight gradient's workgroups (one per CU) that keeps the input gradient to
+// one round of wide tiles instead of two rounds of narrow ones.
+int pick_slab(const SlabConv& s, SlabPlan& pl, bool chunked = false) {
     constexpr size_t kHalf = kLdsBytes / 2;
+    const int64_t cap = chunked ? (int64_t)kHalf : kLdsBytes;
+    const SlabPlan p64 = s.M >= 48 ? plan_slab<4, 1, 1, 7>(s, cap) : SlabPlan{};
+    const SlabPlan p32 = s.M > 16 ? plan_slab<2, 2, 1, 4>(s, cap) : SlabPlan{};
+    const SlabPlan p16 = plan_slab<1, 4, 1, 2>(s, cap);
     const SlabPlan* plans[3] = {&p64, &p32, &p16};
     for (int k = 0; k < 3; ++k)
         if (plans[k]->lds && plans[k]->lds <= kHalf) return pl = *plans[k], k;
@@ -601,7 +606,7 @@ int slab_backward_pair(const SlabConv& d, const SlabWgrad& w) {
     if (d.N == 0 || d.M == 0 || d.OH == 0 || d.OW == 0 || !slab_shape_ok(d))
         return kSlabUnsupported;
     SlabPlan pl;
-    const int cfg = pick_slab(d, pl);
+    const int cfg = pick_slab(d, pl, true);
     if (cfg < 0) return kSlabUnsupported;
     const int64_t bm = cfg == 0 ? 64 : (cfg == 1 ? 32 : 16);
     const int64_t d_wgs = d.N * pl.nb * ((d.M + bm - 1) / bm);
