@@ -148,12 +148,26 @@ __global__ __launch_bounds__(256) void conv_fwd_direct_kernel(
         const int j = t % kw, i = (t / kw) % kh, ic = t / (kw * kh);
         tab[threadIdx.x] = make_int2((ic * in_h + i) * in_w + j, i | (j << 16));
     }
-    for (int e = threadIdx.x; e < kDirectOcBlock * WROW; e += blockDim.x) {
-        const int o = e / WROW, t = e - o * WROW;
-        wsh[o][t] = (oc0 + o < oc1 && t < taps) ? weight[(int64_t)(oc0 + o) * taps + t] : 0.0f;
+    // weights and biases: every load issued before any store (zero-returning
+    // buffer loads need no select, which would make each load wait for the
+    // previous one)
+    constexpr int WN = kDirectOcBlock * WROW, WPT = (WN + 255) / 256;
+    const auto rw = buffer_rsrc(weight, (int64_t)c_out * taps * 4);
+    const auto rb = buffer_rsrc(bias ? bias : weight, bias ? (int64_t)c_out * 4 : 0);
+    float wv[WPT];
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+        const int e = threadIdx.x + 256 * k, o = e / WROW, t = e - o * WROW;
+        const bool ok = (e < WN) & (oc0 + o < oc1) & (t < taps);
+        wv[k] = buffer_load1(rw, ok ? ((oc0 + o) * taps + t) * 4 : kOutOfRange);
     }
-    if (threadIdx.x < kDirectOcBlock)
-        bsh[threadIdx.x] = (bias && oc0 + (int)threadIdx.x < oc1) ? bias[oc0 + threadIdx.x] : 0.0f;
+    const int bo = oc0 + (int)threadIdx.x;
+    const bool bok = (threadIdx.x < kDirectOcBlock) & (bo < oc1);
+    const float bv = buffer_load1(rb, bok ? bo * 4 : kOutOfRange);
+#pragma unroll
+    for (int k = 0; k < WPT; ++k)
+        if (threadIdx.x + 256 * k < WN) (&wsh[0][0])[threadIdx.x + 256 * k] = wv[k];
+    if (threadIdx.x < kDirectOcBlock) bsh[threadIdx.x] = bv;
     __syncthreads();
     const int P = (int)div_P.d, total = N * P;
     for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
@@ -309,16 +323,21 @@ __global__ __launch_bounds__(256) void conv_dgrad_small_kernel(
     float* wsh = gt + ((occ * tile + 3) & ~3);
     // the input-gradient values this thread adds to (group 0 writes them),
     // loaded now so the final stores do not wait on a memory round trip
-    float* drow = dinput + (int64_t)n * c_in * HW + (y0 + (live ? (int)yy : 0)) * in_w + x0;
+    // (Zero-returning buffer loads here and below: a select after a load
+    // would make the compiler wait for it before issuing the next.)
+    const int dpix = (y0 + (live ? (int)yy : 0)) * in_w + x0;
+    float* drow = dinput + (int64_t)n * c_in * HW + dpix;
+    const auto rd = buffer_rsrc(dinput + (int64_t)n * c_in * HW, (int64_t)c_in * HW * 4);
     float old[kDgradRun][CIN];
 #pragma unroll
     for (int c = 0; c < CIN; ++c)
 #pragma unroll
         for (int r = 0; r < kDgradRun; ++r) {
             const bool ok = live & (grp == 0) & (c < c_in) & (x0 + r < in_w);
-            const float v = *(ok ? drow + (int64_t)c * HW + r : dinput);
-            old[r][c] = ok ? v : 0.0f;
+            old[r][c] = buffer_load1(rd, ok ? (c * HW + dpix + r) * 4 : kOutOfRange);
         }
+    const auto rw = buffer_rsrc(weight, (int64_t)c_out * c_in * kh * KW * 4);
+    const auto rg = buffer_rsrc(gimg, (int64_t)c_out * P * 4);
     // this thread's staging items e = tid + k*256 over (channel, tile row,
     // column quad): its first item's position, and the advance of 256 items
     // as whole channels, rows and quads, applied with carries (no division
@@ -343,12 +362,11 @@ __global__ __launch_bounds__(256) void conv_dgrad_small_kernel(
             const int ee = min(e, wn - 1);
             const int oi = ee / KW, jj = ee - oi * KW;  // KW is a constant
             const int o = (int)fast_div((uint32_t)oi, div_kh), i = oi - o * kh;
-            const float* w = weight + ((int64_t)(oc0 + o) * c_in * kh + i) * KW + (KW - 1 - jj);
+            const int woff = ((oc0 + o) * c_in * kh + i) * KW + (KW - 1 - jj);
 #pragma unroll
             for (int c = 0; c < CIN; ++c) {
                 const bool ok = (e < wn) & (c < c_in);
-                const float v = *(ok ? w + (int64_t)c * kh * KW : weight);
-                wv[k][c] = ok ? v : 0.0f;
+                wv[k][c] = buffer_load1(rw, ok ? (woff + c * kh * KW) * 4 : kOutOfRange);
             }
         }
         // the chunk's gradient rows: every load of a batch before its stores
@@ -362,13 +380,12 @@ __global__ __launch_bounds__(256) void conv_dgrad_small_kernel(
                 if (b0 + u * 256 < items) {  // uniform
                     const int oy = oy_base + r, ox = ox_base + 4 * c4;
                     const bool row_ok = (ch < nch) & ((unsigned)oy < (unsigned)out_h);
-                    const float* src = gimg + (int64_t)(oc0 + min(ch, nch - 1)) * P + oy * out_w;
+                    const int goff = (oc0 + min(ch, nch - 1)) * P + oy * out_w + ox;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const bool ok = row_ok & ((unsigned)(ox + e) < (unsigned)out_w) &
                                         (4 * c4 + e < gw);
-                        const float g = *(ok ? src + ox + e : gimg);
-                        v[u][e] = ok ? g : 0.0f;
+                        v[u][e] = buffer_load1(rg, ok ? (goff + e) * 4 : kOutOfRange);
                     }
                     if (ch < nch) dst[u] = ch * tile + r * pitch + 4 * c4;
                 }
@@ -383,6 +400,9 @@ __global__ __launch_bounds__(256) void conv_dgrad_small_kernel(
 #pragma unroll
             for (int u = 0; u < kDgradStage; ++u)
                 if (dst[u] >= 0) *reinterpret_cast<f32x4*>(gt + dst[u]) = v[u];
+            // nothing outstanding at the loop edge: the compiler would
+            // otherwise wait for the loads above before the first row load
+            __builtin_amdgcn_s_waitcnt(0);
         }
 #pragma unroll
         for (int k = 0; k < kDgradWStage; ++k) {
@@ -793,8 +813,11 @@ int small_dgrad(float* dinput, const float* grad, const float* weight, const Con
     bands = (d.in_h + band - 1) / band;
     const int64_t tile = (band + d.kh - 1) * pitch, limit = 64 * 1024 / 4;
     const int64_t per_ch = tile + 4 * d.kh * d.kw;  // gradient tile + weights
+    // (byte offsets inside one image and the weights fit the buffer loads'
+    // 31 bits)
     if (per_ch > limit - 3 || d.N * bands > INT32_MAX || d.c_out > INT32_MAX ||
-        d.c_out * d.out_h * d.out_w > INT32_MAX || d.in_h * d.in_w > INT32_MAX)
+        d.c_out * d.out_h * d.out_w > INT32_MAX / 4 || d.c_in * d.in_h * d.in_w > INT32_MAX / 4 ||
+        d.c_out * d.c_in * d.kh * d.kw > INT32_MAX / 4)
         return kSlabUnsupported;
     const int64_t occ = std::min<int64_t>(d.c_out, (limit - 3) / per_ch);
     // channel groups: whole waves of threads per group, enough for the runs
