@@ -280,10 +280,19 @@ def bench_attention_cfg4(hip, steps, warmup):
         hip.bmm_backward(hip.NN, dP, dv, do, P, v, BH, T, T, Dh)
         hip.bmm_backward(hip.NT, dq, dk, dS, q, k, BH, T, Dh, T)
 
+    # the same products with the gradients accumulated into existing
+    # buffers (beta = 1), the form the drop-in backward closure uses
+    def bmms_accumulate():
+        hip.bmm(hip.NT, S, q, k, BH, T, T, Dh)
+        hip.bmm(hip.NN, o, P, v, BH, T, Dh, T)
+        hip.bmm_backward(hip.NN, dP, dv, do, P, v, BH, T, T, Dh, 1.0)
+        hip.bmm_backward(hip.NT, dq, dk, dS, q, k, BH, T, Dh, T, 1.0)
+
     fwd()
     fwd_us = event_ms(hip, fwd, steps, warmup) * 1e3
     bwd_us = event_ms(hip, bwd, steps, warmup) * 1e3
     bmm_us = event_ms(hip, bmms_only, steps, warmup) * 1e3
+    bmm_acc_us = event_ms(hip, bmms_accumulate, steps, warmup) * 1e3
     bmm_roof = 6 * roofline_us(*gemm_roof(T, T, Dh, BH))  # every product moves 25.2 MB
 
     # the block's Linear GEMMs: X[4096,256] through 4 projections and the FFN
@@ -317,6 +326,7 @@ def bench_attention_cfg4(hip, steps, warmup):
     lin_flops = sum(gemm_roof(*s)[0] for s in shapes)
     lin_roof = sum(roofline_us(*gemm_roof(*s)) for s in shapes)
     return {"fwd_us": fwd_us, "bwd_us": bwd_us, "bmm_us": bmm_us, "bmm_roof_us": bmm_roof,
+            "bmm_acc_us": bmm_acc_us,
             "linear_us": lin_us, "linear_tflops": lin_flops / (lin_us * 1e-6) / 1e12,
             "linear_roof_us": lin_roof}
 
@@ -560,6 +570,7 @@ def main():
         out["attention_cfg4"] = {
             "bmm_us": round(at["bmm_us"], 2), "bmm_roofline_us": round(at["bmm_roof_us"], 2),
             "bmm_roofline_frac": round(at["bmm_roof_us"] / at["bmm_us"], 4),
+            "bmm_accumulate_us": round(at["bmm_acc_us"], 2),
             "attn_fwd_us": round(at["fwd_us"], 2), "attn_bwd_us": round(at["bwd_us"], 2),
             "linear_us": round(at["linear_us"], 2), "linear_tflops": round(at["linear_tflops"], 2),
             "linear_roofline_frac": round(at["linear_roof_us"] / at["linear_us"], 4),

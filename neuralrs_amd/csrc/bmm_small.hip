@@ -60,7 +60,11 @@ __device__ __forceinline__ f32x4 fragment(__amdgpu_buffer_rsrc_t rs, int r, int 
 }
 
 // One workgroup `wg` (of batch * wg_per_item) of the product described by a.
-template <bool AK, bool BKC, int G, int JB>
+// ACC (beta != 0): the C values the product adds to are loaded with the
+// fragments, before the MFMA chain, so their wait hides behind it (loading
+// them in the epilogue made every store wait for a round trip, and for the
+// stores before it).
+template <bool AK, bool BKC, int G, int JB, bool ACC>
 __device__ __forceinline__ void bmm_small_block(const SmallArgs& a, int wg) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -81,6 +85,22 @@ __device__ __forceinline__ void bmm_small_block(const SmallArgs& a, int wg) {
         for (int j = 0; j < JB; ++j)
             bf[j][g] = fragment<BKC>(rb, 32 * (bn0 + j) + l32, a.N, a.K, g, h);
     }
+    float* c = a.C + item * a.sC;
+    const int row0 = 32 * bm + 4 * h;
+    f32x16v old[JB];
+    if constexpr (ACC) {
+        const auto rc = buffer_rsrc(c, (int64_t)a.M * a.N * 4);
+#pragma unroll
+        for (int j = 0; j < JB; ++j) {
+            const int n = 32 * (bn0 + j) + l32;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = row0 + 8 * (e >> 2) + (e & 3);
+                old[j][e] = buffer_load1(rc, (row < a.M) & (n < a.N) ? (row * a.N + n) * 4
+                                                                      : kOutOfRange);
+            }
+        }
+    }
     // keep the loads ahead of the MFMA chain (left alone, the scheduler
     // interleaves them to save registers, which costs a round trip each)
     __builtin_amdgcn_sched_barrier(0);
@@ -96,39 +116,22 @@ __device__ __forceinline__ void bmm_small_block(const SmallArgs& a, int wg) {
             for (int p = 0; p < 4; ++p)
                 acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[g][p], bf[j][g][p], acc[j], 0, 0, 0);
     }
-    float* c = a.C + item * a.sC;
-    const int row0 = 32 * bm + 4 * h;
-    if (a.beta == 0.0f) {
 #pragma unroll
-        for (int j = 0; j < JB; ++j) {
-            const int n = 32 * (bn0 + j) + l32;
+    for (int j = 0; j < JB; ++j) {
+        const int n = 32 * (bn0 + j) + l32;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int row = row0 + 8 * (e >> 2) + (e & 3);
-                if (row < a.M && n < a.N)
-                    __builtin_nontemporal_store(acc[j][e], c + (int64_t)row * a.N + n);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < JB; ++j) {
-            const int n = 32 * (bn0 + j) + l32;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int row = row0 + 8 * (e >> 2) + (e & 3);
-                if (row < a.M && n < a.N) {
-                    float* dst = c + (int64_t)row * a.N + n;
-                    __builtin_nontemporal_store(acc[j][e] + a.beta * *dst, dst);
-                }
-            }
+        for (int e = 0; e < 16; ++e) {
+            const int row = row0 + 8 * (e >> 2) + (e & 3);
+            const float v = ACC ? acc[j][e] + a.beta * old[j][e] : acc[j][e];
+            if (row < a.M && n < a.N) __builtin_nontemporal_store(v, c + (int64_t)row * a.N + n);
         }
     }
 }
 
-template <bool AK, bool BKC, int G, int JB>
+template <bool AK, bool BKC, int G, int JB, bool ACC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void bmm_small_kernel(SmallArgs a) {
-    bmm_small_block<AK, BKC, G, JB>(a, blockIdx.x);
+    bmm_small_block<AK, BKC, G, JB, ACC>(a, blockIdx.x);
 }
 
 // Both gradients of one bmm in one launch: the first product (NT, or NN
@@ -137,21 +140,21 @@ void bmm_small_kernel(SmallArgs a) {
 // while the first product's last ones drain. (Interleaving the two in
 // proportion to their counts measured slower on attention's gradients:
 // 27.7 vs 26.3 us for both pairs.)
-template <bool BKCA, int GA, int JBA, int GB>
+template <bool BKCA, int GA, int JBA, int GB, bool ACC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void bmm_small_pair_kernel(SmallArgs ga, SmallArgs gb, int wg_a) {
     const int x = blockIdx.x;
     if (x < wg_a)  // uniform
-        bmm_small_block<true, BKCA, GA, JBA>(ga, x);
+        bmm_small_block<true, BKCA, GA, JBA, ACC>(ga, x);
     else
-        bmm_small_block<false, false, GB, 1>(gb, x - wg_a);
+        bmm_small_block<false, false, GB, 1, ACC>(gb, x - wg_a);
 }
 
-template <bool AK, bool BKC, int JB>
+template <bool AK, bool BKC, int JB, bool ACC>
 void* pick_g(int G) {
-    return G <= 4   ? reinterpret_cast<void*>(bmm_small_kernel<AK, BKC, 4, JB>)
-           : G <= 8 ? reinterpret_cast<void*>(bmm_small_kernel<AK, BKC, 8, JB>)
-                    : reinterpret_cast<void*>(bmm_small_kernel<AK, BKC, 16, JB>);
+    return G <= 4   ? reinterpret_cast<void*>(bmm_small_kernel<AK, BKC, 4, JB, ACC>)
+           : G <= 8 ? reinterpret_cast<void*>(bmm_small_kernel<AK, BKC, 8, JB, ACC>)
+                    : reinterpret_cast<void*>(bmm_small_kernel<AK, BKC, 16, JB, ACC>);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -200,20 +203,23 @@ int small_args(const GemmCall& c, SmallArgs& a, int& G, int& JB) {
 int g_index(int G) { return G <= 4 ? 0 : (G <= 8 ? 1 : 2); }
 
 template <bool BKCA, int GA, int JBA>
-void* pick_pair_b(int GB) {
+void* pick_pair_b(int GB, bool acc) {
     switch (g_index(GB)) {
-        case 0: return reinterpret_cast<void*>(bmm_small_pair_kernel<BKCA, GA, JBA, 4>);
-        case 1: return reinterpret_cast<void*>(bmm_small_pair_kernel<BKCA, GA, JBA, 8>);
-        default: return reinterpret_cast<void*>(bmm_small_pair_kernel<BKCA, GA, JBA, 16>);
+        case 0: return acc ? reinterpret_cast<void*>(bmm_small_pair_kernel<BKCA, GA, JBA, 4, true>)
+                           : reinterpret_cast<void*>(bmm_small_pair_kernel<BKCA, GA, JBA, 4, false>);
+        case 1: return acc ? reinterpret_cast<void*>(bmm_small_pair_kernel<BKCA, GA, JBA, 8, true>)
+                           : reinterpret_cast<void*>(bmm_small_pair_kernel<BKCA, GA, JBA, 8, false>);
+        default: return acc ? reinterpret_cast<void*>(bmm_small_pair_kernel<BKCA, GA, JBA, 16, true>)
+                           : reinterpret_cast<void*>(bmm_small_pair_kernel<BKCA, GA, JBA, 16, false>);
     }
 }
 
 template <bool BKCA, int JBA>
-void* pick_pair(int GA, int GB) {
+void* pick_pair(int GA, int GB, bool acc) {
     switch (g_index(GA)) {
-        case 0: return pick_pair_b<BKCA, 4, JBA>(GB);
-        case 1: return pick_pair_b<BKCA, 8, JBA>(GB);
-        default: return pick_pair_b<BKCA, 16, JBA>(GB);
+        case 0: return pick_pair_b<BKCA, 4, JBA>(GB, acc);
+        case 1: return pick_pair_b<BKCA, 8, JBA>(GB, acc);
+        default: return pick_pair_b<BKCA, 16, JBA>(GB, acc);
     }
 }
 
@@ -224,11 +230,19 @@ int bmm_small(const GemmCall& c) {
     int G = 0, JB = 1;
     const int rc = small_args(c, a, G, JB);
     if (rc) return rc;
+    const bool acc = c.beta != 0.0f;
     void* fn;
     switch (c.layout) {
-        case NRS_NN: fn = pick_g<true, false, 1>(G); break;
-        case NRS_NT: fn = JB == 2 ? pick_g<true, true, 2>(G) : pick_g<true, true, 1>(G); break;
-        default: fn = pick_g<false, false, 1>(G); break;
+        case NRS_NN:
+            fn = acc ? pick_g<true, false, 1, true>(G) : pick_g<true, false, 1, false>(G);
+            break;
+        case NRS_NT:
+            fn = JB == 2 ? (acc ? pick_g<true, true, 2, true>(G) : pick_g<true, true, 2, false>(G))
+                         : (acc ? pick_g<true, true, 1, true>(G) : pick_g<true, true, 1, false>(G));
+            break;
+        default:
+            fn = acc ? pick_g<false, false, 1, true>(G) : pick_g<false, false, 1, false>(G);
+            break;
     }
     hipLaunchKernelGGL(reinterpret_cast<void (*)(SmallArgs)>(fn),
                        dim3((unsigned)(c.batch * a.wg_per_item)), dim3(256), 0, stream(), a);
@@ -237,16 +251,17 @@ int bmm_small(const GemmCall& c) {
 }
 
 int bmm_small_pair(const GemmCall& ga, const GemmCall& gb) {
-    if ((ga.layout != NRS_NT && ga.layout != NRS_NN) || gb.layout != NRS_TN)
+    if ((ga.layout != NRS_NT && ga.layout != NRS_NN) || gb.layout != NRS_TN || ga.beta != gb.beta)
         return kBmmUnsupported;
     SmallArgs a, b;
     int GA = 0, JBA = 1, GB = 0, JBB = 1;
     if (small_args(ga, a, GA, JBA) || small_args(gb, b, GB, JBB)) return kBmmUnsupported;
     const int64_t wg_a = ga.batch * a.wg_per_item, wg_b = gb.batch * b.wg_per_item;
     if (wg_a + wg_b > INT32_MAX) return kBmmUnsupported;
-    void* fn = ga.layout == NRS_NN ? pick_pair<false, 1>(GA, GB)
-               : JBA == 2          ? pick_pair<true, 2>(GA, GB)
-                                   : pick_pair<true, 1>(GA, GB);
+    const bool acc = ga.beta != 0.0f;
+    void* fn = ga.layout == NRS_NN ? pick_pair<false, 1>(GA, GB, acc)
+               : JBA == 2          ? pick_pair<true, 2>(GA, GB, acc)
+                                   : pick_pair<true, 1>(GA, GB, acc);
     hipLaunchKernelGGL(reinterpret_cast<void (*)(SmallArgs, SmallArgs, int)>(fn),
                        dim3((unsigned)(wg_a + wg_b)), dim3(256), 0, stream(), a, b, (int)wg_a);
     NRS_LAUNCH_CHECK("bmm backward (small items)");
