@@ -512,28 +512,45 @@ void gemm_kernel(GemmArgs p) {
             const float bc = (bias_col && colok[j]) ? p.bias[n0 + wn0 + 32 * j + l32] : 0.0f;
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
-                // All 16 old values of the fragment are read before any is
-                // used, so their loads overlap.
-                float old[16];
-                if (beta != 0.0f) {
+                // The fragment's 16 old values and row biases are loaded
+                // before any store, unconditionally from a clamped (always
+                // valid) address: a load inside the store's bounds branch
+                // would be sunk there by the compiler and cost a round trip
+                // per element. Values of lanes that store nothing are unused.
+                float old[16], br[16];
+                if (beta != 0.0f || bias_row) {  // uniform
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int64_t row = row0 + 32 * i + 8 * (r >> 2) + (r & 3);
                         const bool ok = colok[j] & (row < p.M);
-                        old[r] = ok ? out[cbase[j] + row * stride] : 0.0f;
+                        old[r] = beta != 0.0f ? out[ok ? cbase[j] + row * stride : 0] : 0.0f;
+                        br[r] = bias_row ? p.bias[ok ? row : 0] : 0.0f;
                     }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // All 16 results and destinations first, each in registers
+                // of its own (pinned by the empty asm): computed inside each
+                // store's bounds branch they would share temporaries, and a
+                // store's data and address registers cannot be overwritten
+                // before the store has read them, so every store would wait
+                // for the one before it.
+                float v[16];
+                float* dst[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int64_t row = row0 + 32 * i + 8 * (r >> 2) + (r & 3);
+                    v[r] = acc[i][j][r];
+                    if (bias_col) v[r] += bc;
+                    if (bias_row) v[r] += br[r];
+                    if (relu) v[r] = fmaxf(v[r], 0.0f);
+                    if (beta != 0.0f) v[r] = v[r] + beta * old[r];
+                    dst[r] = out + cbase[j] + row * stride;
+                    asm volatile("" : "+v"(v[r]), "+v"(dst[r]));
                 }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int64_t row = row0 + 32 * i + 8 * (r >> 2) + (r & 3);
-                    if (colok[j] && row < p.M) {
-                        float v = acc[i][j][r];
-                        if (bias_col) v += bc;
-                        if (bias_row) v += p.bias[row];
-                        if (relu) v = fmaxf(v, 0.0f);
-                        if (beta != 0.0f) v = v + beta * old[r];
-                        out[cbase[j] + row * stride] = v;
-                    }
+                    if (colok[j] && row < p.M) *dst[r] = v[r];
                 }
             }
         }
