@@ -295,6 +295,22 @@ __device__ __forceinline__ void slab_block(const SlabArgs& a, int bx, int by) {
         // stores are 128-bit and cover whole row segments.
         constexpr int TR = NSW * 16 + 4;   // tile row stride (floats)
         constexpr int TW = MSW * 16 * TR;  // floats per wave
+        const int pw0 = p0 + 16 * wn * NSW, ocw0 = m0 + 16 * wm * MSW;
+        // beta != 0: the values the stores add to, loaded now (before the
+        // tile round trip) and all before any store; loaded beside each
+        // store they would cost a round trip per store
+        f32x4 old[MSW * NSW];
+        if (a.beta != 0.0f) {  // uniform
+            const auto ro = buffer_rsrc(oimg, (int64_t)a.M * a.P * 4);
+#pragma unroll
+            for (int k = 0; k < MSW * NSW; ++k) {
+                const int e = lane + 64 * k;
+                const int row = e / (NSW * 4), c4 = e - row * (NSW * 4);
+                const int oc = ocw0 + row, p = pw0 + 4 * c4;
+                old[k] = buffer_load4(ro, (oc < a.M) & (p < p_end) ? (oc * a.P + p) * 4
+                                                                   : kOutOfRange);
+            }
+        }
         __syncthreads();                   // every wave is done with the operands
         float* tile = lds + wave * TW;
 #pragma unroll
@@ -305,7 +321,8 @@ __device__ __forceinline__ void slab_block(const SlabArgs& a, int bx, int by) {
                 for (int r = 0; r < 4; ++r)
                     tile[(16 * ms + 4 * q + r) * TR + 16 * t + l16] = acc[ms][t][r] + bias[ms][r];
         __syncthreads();
-        const int pw0 = p0 + 16 * wn * NSW, ocw0 = m0 + 16 * wm * MSW;
+        // (P % 4 == 0 and bands of whole float4s: a float4 never straddles
+        // the band's end)
 #pragma unroll
         for (int k = 0; k < MSW * NSW; ++k) {
             const int e = lane + 64 * k;
@@ -313,15 +330,8 @@ __device__ __forceinline__ void slab_block(const SlabArgs& a, int bx, int by) {
             const int oc = ocw0 + row, p = pw0 + 4 * c4;
             if (oc >= a.M || p >= p_end) continue;
             f32x4 v = *reinterpret_cast<const f32x4*>(tile + row * TR + 4 * c4);
-            float* dst = oimg + (int64_t)oc * a.P + p;
-            if (p + 4 <= p_end) {
-                if (a.beta != 0.0f) v = v + a.beta * *reinterpret_cast<const f32x4*>(dst);
-                __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst));
-            } else {
-                for (int u = 0; u < p_end - p; ++u)
-                    __builtin_nontemporal_store(a.beta != 0.0f ? v[u] + a.beta * dst[u] : v[u],
-                                                dst + u);
-            }
+            if (a.beta != 0.0f) v = v + a.beta * old[k];
+            __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(oimg + (int64_t)oc * a.P + p));
         }
         return;
     }
@@ -584,8 +594,9 @@ bool slab_shape_ok(const SlabConv& s) {
     if (s.C <= 0 || s.kh <= 0 || s.kw <= 0 || s.stride <= 0) return false;
     // staged channel chunks must be at least a quarter real channels
     if (round_up(s.C, 16) > 4 * (int64_t)s.C) return false;
-    // an image's byte offsets fit the buffer loads' 31-bit range
-    return (int64_t)s.C * s.H * s.W <= INT32_MAX / 4 && (int64_t)s.OH * s.OW <= INT32_MAX / 2;
+    // an image's byte offsets (input and output) fit the buffer loads' 31-bit
+    // range
+    return (int64_t)s.C * s.H * s.W <= INT32_MAX / 4 && (int64_t)s.M * s.OH * s.OW <= INT32_MAX / 4;
 }
 
 }  // namespace
