@@ -24,6 +24,16 @@ KernelFn pick_vec(bool vec4) {
                 : gemm_kernel<BM, BN, BK, WM_, WN_, AK, BKC, 1, 2, PF, AM, BMD>;
 }
 
+// One load width only (the other variant of some tiles spills).
+template <int BM, int BN, int BK, int WM_, int WN_, int PF, int VEC>
+KernelFn pick_fixed(int layout) {
+    switch (layout) {
+        case NRS_NN: return gemm_kernel<BM, BN, BK, WM_, WN_, true, false, VEC, 2, PF>;
+        case NRS_NT: return gemm_kernel<BM, BN, BK, WM_, WN_, true, true, VEC, 2, PF>;
+        default: return gemm_kernel<BM, BN, BK, WM_, WN_, false, false, VEC, 2, PF>;
+    }
+}
+
 template <int BM, int BN, int BK, int WM_, int WN_, int PF>
 KernelFn pick_layout(int layout, bool vec4) {
     switch (layout) {
@@ -52,18 +62,23 @@ KernelFn pick_conv(int layout, int amode, int bmode, bool vec4) {
 //    GEMMs (83-85% of FP32 MFMA peak at 4096^3 and 8192^3);
 //  * 64x64x32, 4 waves of 32x32, prefetch depth 2: everything mid-sized
 //    (bmm items, conv GEMMs, projections, split-K weight gradients);
-//  * 32x256x32, 4 waves of 32x64: outputs with at most 32 rows;
+//  * 64x128x32, 4 waves of 32x64, prefetch depth 2: dense GEMMs with at
+//    least two of its tiles per CU and K >= 1024 (2048^3: 162 vs 175 us
+//    on 64x64; on fewer tiles or short K the 64x64 tile wins);
+//  * 32x256x32, 4 waves of 32x64, prefetch depth 2 (1 with scalar loads):
+//    outputs with at most 32 rows;
 //  * 32x128x32, 4 waves of 32x32, prefetch depth 2: convolutions whose GEMM
 //    has at most 32 rows (a 64-row tile would double the MFMA work);
 //  * 128x32x32, 4 waves of 32x32, prefetch depth 2: outputs with at most 32
 //    columns, e.g. attention's P.V and its input gradients (d_head 32).
-enum TileId { T256x256 = 0, T64x64, T32x256, T32x128, T128x32, T_COUNT };
+enum TileId { T256x256 = 0, T64x64, T32x256, T32x128, T128x32, T64x128, T_COUNT };
 const TileShape kShapes[T_COUNT] = {
     {256, 256, 32, 512},
     {64, 64, 32, 256},
     {32, 256, 32, 256},
     {32, 128, 32, 256},
     {128, 32, 32, 256},
+    {64, 128, 32, 256},
 };
 
 // `pf` is the register prefetch depth the plan asks for; tiles that have no
@@ -81,7 +96,11 @@ KernelFn kernel_for(int tile, int pf, int layout, bool vec4, int amode, int bmod
         case T64x64:
             return pf == 1 ? pick_layout<64, 64, 32, 2, 2, 1>(layout, vec4)
                            : pick_layout<64, 64, 32, 2, 2, 2>(layout, vec4);
-        case T32x256: return pick_layout<32, 256, 32, 1, 4, 1>(layout, vec4);
+        case T32x256:  // depth 2 with 128-bit loads; its scalar-load variant needs depth 1
+            return vec4 ? pick_fixed<32, 256, 32, 1, 4, 2, 4>(layout)
+                        : pick_fixed<32, 256, 32, 1, 4, 1, 1>(layout);
+        case T64x128:  // planned only with 128-bit loads (the scalar variant spills)
+            return vec4 ? pick_fixed<64, 128, 32, 2, 2, 2, 4>(layout) : nullptr;
         case T128x32:
             return pf == 1 ? pick_layout<128, 32, 32, 4, 1, 1>(layout, vec4)
                            : pick_layout<128, 32, 32, 4, 1, 2>(layout, vec4);
@@ -122,6 +141,8 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool d
             pl.tile = T128x32;
         else if (vec4 && tiles_of(T256x256) >= cus && fill(T256x256) >= 0.85)
             pl.tile = T256x256;
+        else if (vec4 && tiles_of(T64x128) >= 2 * cus && K >= 1024 && fill(T64x128) >= 0.85)
+            pl.tile = T64x128;
     } else if (M <= 32) {  // gathered (convolution) operands: 64x64 or 32x128
         pl.tile = T32x128;
     }
@@ -131,9 +152,13 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool d
     if (force_slices > 0) {
         slices = force_slices;
     } else if (allow_split && batch == 1 && tiles < cus && (2 * tiles <= cus || K >= 2048)) {
-        // About three workgroups per CU, each slice at least two k-tiles, at
-        // most 256 slices (the reduction reads every slice of every output).
-        const int64_t want = std::min<int64_t>(256, cdiv(3 * (int64_t)cus, tiles));
+        // About three workgroups per CU (one for the 32x256 tile, whose
+        // workgroups stream a whole K slice of B: 8 slices of the skinny
+        // 32x8192x8192 GEMM measured 67.8 us against 72.4 us at 24), each
+        // slice at least two k-tiles, at most 256 slices (the reduction reads
+        // every slice of every output).
+        const int64_t per_cu = pl.tile == T32x256 ? 1 : 3;
+        const int64_t want = std::min<int64_t>(256, cdiv(per_cu * (int64_t)cus, tiles));
         const int64_t max_by_k = std::max<int64_t>(1, K / (2 * s.bk));
         slices = (int)std::min<int64_t>(want, max_by_k);
     }

@@ -528,29 +528,26 @@ void gemm_kernel(GemmArgs p) {
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                // All 16 results and destinations first, each in registers
-                // of its own (pinned by the empty asm): computed inside each
-                // store's bounds branch they would share temporaries, and a
-                // store's data and address registers cannot be overwritten
-                // before the store has read them, so every store would wait
-                // for the one before it.
-                float v[16];
-                float* dst[16];
+                // All 16 results first, each in a register of its own
+                // (pinned by the empty asm; they overwrite the old values):
+                // computed inside each store's bounds branch they would share
+                // one temporary, and a store's data register cannot be
+                // overwritten before the store has read it, so every store
+                // would wait for the one before it.
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int64_t row = row0 + 32 * i + 8 * (r >> 2) + (r & 3);
-                    v[r] = acc[i][j][r];
-                    if (bias_col) v[r] += bc;
-                    if (bias_row) v[r] += br[r];
-                    if (relu) v[r] = fmaxf(v[r], 0.0f);
-                    if (beta != 0.0f) v[r] = v[r] + beta * old[r];
-                    dst[r] = out + cbase[j] + row * stride;
-                    asm volatile("" : "+v"(v[r]), "+v"(dst[r]));
+                    float v = acc[i][j][r];
+                    if (bias_col) v += bc;
+                    if (bias_row) v += br[r];
+                    if (relu) v = fmaxf(v, 0.0f);
+                    if (beta != 0.0f) v = v + beta * old[r];
+                    old[r] = v;
+                    asm volatile("" : "+v"(old[r]));
                 }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int64_t row = row0 + 32 * i + 8 * (r >> 2) + (r & 3);
-                    if (colok[j] && row < p.M) *dst[r] = v[r];
+                    if (colok[j] && row < p.M) out[cbase[j] + row * stride] = old[r];
                 }
             }
         }
