@@ -45,6 +45,8 @@ SHAPES = [  # (rows, cols, inner)
     (512, 512, 512), (32, 1024, 512), (1, 513, 257), (1000, 3, 2),
     (130, 17, 33), (257, 32, 96),  # at most 32 columns: 128x32 tiles, ragged rows
     (2048, 2048, 40), (4096, 1024, 72), (2000, 2048, 36),  # large outputs (the last ragged M)
+    (2000, 2100, 1100),  # 64x128 tiles (two per CU, K >= 1024), ragged edges
+    (30, 8200, 1024),    # at most 32 rows: 32x256 tiles over K slices, ragged M and N
 ]
 
 
@@ -111,9 +113,13 @@ def test_gemm_skinny_cfg5(hip, orc):
     assert rel_err(c, c64, ab) <= gemm_tol(k)
 
 
-def test_gemm_beta_bias_relu_epilogues(hip):
+@pytest.mark.parametrize("shape", [(70, 50, 33), (2000, 2100, 1100), (300, 20, 40), (30, 600, 1024),
+                                   (4096, 4096, 64)],
+                         ids=["64x64", "64x128", "128x32", "32x256-splitk", "256x256"])
+def test_gemm_beta_bias_relu_epilogues(hip, shape):
+    """The general epilogue (beta, column bias, row bias + ReLU) on each tile."""
     rng = np.random.default_rng(9)
-    rows, cols, inner = 70, 50, 33
+    rows, cols, inner = shape
     a, b = operands(NN, rows, cols, inner, lambda s: int_matrix(rng, s, -3, 3))
     A, B = logical(NN, a, b)
     prod = (A @ B).astype(np.float32)
