@@ -121,8 +121,8 @@ __global__ __launch_bounds__(256) void flip_weights_kernel(float* __restrict__ w
 // kDirectTaps), e.g. a first layer over grayscale images, where a GEMM tile
 // would be mostly padding and the layer is bound by writing its output. One
 // thread per output pixel: its taps are loaded once (branch-free: clamped
-// index, then zeroed), then it produces a block of up to kDirectOcBlock
-// output channels (blockIdx.y) from wave-uniform weights (scalar loads), so
+// index, then zeroed), then it produces a block of up to `ocb` (<=
+// kDirectOcBlock) output channels (blockIdx.y) from wave-uniform weights, so
 // consecutive lanes store consecutive pixels of each channel plane (with
 // non-temporal stores: the output is not read again here and would evict the
 // input from L2). The sum runs over the taps in (ic, i, j) order. 32-bit
@@ -133,7 +133,7 @@ template <int TAPS>
 __global__ __launch_bounds__(256) void conv_fwd_direct_kernel(
     float* __restrict__ out, const float* __restrict__ input, const float* __restrict__ weight,
     const float* __restrict__ bias, int N, int c_in, int in_h, int in_w, int c_out, int kh, int kw,
-    int stride, int pad, FastDiv div_P, FastDiv div_ow) {
+    int stride, int pad, int ocb, FastDiv div_P, FastDiv div_ow) {
     // tap t = (ic*kh + i)*kw + j: offset inside one image and (i, j); the
     // block's weights (zero past the taps) and biases
     constexpr int WROW = (TAPS + 3) & ~3;  // whole float4s per weight row
@@ -141,8 +141,8 @@ __global__ __launch_bounds__(256) void conv_fwd_direct_kernel(
     __shared__ __attribute__((aligned(16))) float wsh[kDirectOcBlock][WROW];
     __shared__ float bsh[kDirectOcBlock];
     const int taps = c_in * kh * kw;
-    const int oc0 = blockIdx.y * kDirectOcBlock;
-    const int oc1 = min(c_out, oc0 + kDirectOcBlock);
+    const int oc0 = blockIdx.y * ocb;
+    const int oc1 = min(c_out, oc0 + ocb);
     if (threadIdx.x < TAPS) {
         const int t = threadIdx.x < taps ? threadIdx.x : 0;
         const int j = t % kw, i = (t / kw) % kh, ic = t / (kw * kh);
@@ -158,7 +158,7 @@ __global__ __launch_bounds__(256) void conv_fwd_direct_kernel(
 #pragma unroll
     for (int k = 0; k < WPT; ++k) {
         const int e = threadIdx.x + 256 * k, o = e / WROW, t = e - o * WROW;
-        const bool ok = (e < WN) & (oc0 + o < oc1) & (t < taps);
+        const bool ok = (e < WN) & (oc0 + o < oc1) & (t < taps);  // (rows past ocb stay 0)
         wv[k] = buffer_load1(rw, ok ? ((oc0 + o) * taps + t) * 4 : kOutOfRange);
     }
     const int bo = oc0 + (int)threadIdx.x;
@@ -986,11 +986,21 @@ int nrs_conv2d_forward(float* out, const float* input, const float* weight, cons
                             : (taps <= 16 ? nrs::conv_fwd_direct_kernel<16>
                                           : nrs::conv_fwd_direct_kernel<32>);
         const unsigned bx = (unsigned)std::min<int64_t>((N * P + 255) / 256, 65535);
-        const unsigned by = (unsigned)((c_out + nrs::kDirectOcBlock - 1) / nrs::kDirectOcBlock);
+        // output channels per workgroup: halved (down to 8) until there are
+        // about three workgroups per CU, so the output's stores spread evenly
+        // (cfg3 conv1: 392 workgroups of 32 channels left 136 CUs with twice
+        // the work; 784 of 16 channels: 6.7 -> 5.7 us). A smaller block
+        // re-reads the pixel's taps, which hit in L2.
+        int64_t ocb = nrs::kDirectOcBlock;
+        while (ocb > 8 && ocb / 2 >= c_out) ocb /= 2;  // no block wider than the layer
+        auto blocks = [&](int64_t b) { return (int64_t)bx * ((c_out + b - 1) / b); };
+        while (ocb > 8 && blocks(ocb) < 3 * (int64_t)nrs::num_cus() && blocks(ocb / 2) > blocks(ocb))
+            ocb /= 2;
+        const unsigned by = (unsigned)((c_out + ocb - 1) / ocb);
         hipLaunchKernelGGL(fn, dim3(bx, by), dim3(256), 0, nrs::stream(), out, input,
                            weight, bias, (int)N, (int)c_in, (int)in_h, (int)in_w, (int)c_out,
-                           (int)kh, (int)kw, (int)stride, (int)pad, nrs::make_fastdiv((uint32_t)P),
-                           nrs::make_fastdiv((uint32_t)d.out_w));
+                           (int)kh, (int)kw, (int)stride, (int)pad, (int)ocb,
+                           nrs::make_fastdiv((uint32_t)P), nrs::make_fastdiv((uint32_t)d.out_w));
         NRS_LAUNCH_CHECK("conv2d forward (direct)");
         return NRS_OK;
     }
