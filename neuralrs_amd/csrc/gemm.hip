@@ -248,7 +248,8 @@ int gemm_run(const GemmCall& c) {
         NRS_ARG_CHECK(c.nchw_P <= INT32_MAX, "gemm: NCHW plane too large");
         p.div_nchw = make_fastdiv((uint32_t)c.nchw_P);
     }
-    NRS_ARG_CHECK((int64_t)p.tiles_m * p.tiles_n <= INT32_MAX && batch <= 65535,
+    // (the kernel renumbers a split grid by its linear id, tiles * slices)
+    NRS_ARG_CHECK((int64_t)p.tiles_m * p.tiles_n * pl.slices <= INT32_MAX && batch <= 65535,
                   "gemm: grid too large");
 
     KernelFn fn = kernel_for(pl.tile, pl.pf, layout, vec4, c.amode, c.bmode);

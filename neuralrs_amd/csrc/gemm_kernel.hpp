@@ -338,10 +338,28 @@ void gemm_kernel(GemmArgs p) {
     const int wm0 = (wave / WAVES_N) * C_::WM;
     const int wn0 = (wave % WAVES_N) * C_::WN;
 
+    // Split K over a tile count that is not a multiple of 8: the workgroups
+    // are dealt to the 8 XCDs round-robin by linear id, so the tiles of one
+    // K slice would land on different XCDs, each fetching the slice's shared
+    // operand panel into its own L2 (the 64x576 weight gradient over
+    // K = 100352 read its A panel nine times). Renumber so that every XCD
+    // owns whole slices: logical id = (slice, tile), tile fastest, in
+    // contiguous runs per XCD (a bijection on the grid; each slice still
+    // writes its own partial). With a multiple of 8, tile_coords already
+    // gives each XCD a compact block of every slice's tiles, which measured
+    // faster on 256-wide weight gradients than whole slices per XCD.
+    int bid = blockIdx.x, slice = blockIdx.y;
+    if (gridDim.y > 1 && (gridDim.x & 7) != 0) {
+        const int tiles = gridDim.x, total = tiles * gridDim.y;
+        const int lin = blockIdx.x + blockIdx.y * tiles;
+        const int xcd = lin & 7, per = total >> 3, extra = total & 7;
+        const int id = xcd * per + min(xcd, extra) + (lin >> 3);
+        slice = id / tiles;
+        bid = id - slice * tiles;
+    }
     int tm, tn;
-    tile_coords(p, blockIdx.x, tm, tn);
+    tile_coords(p, bid, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-    const int slice = blockIdx.y;
     const int64_t batch = blockIdx.z;
 
     const float* A = p.A + batch * p.sA;

@@ -175,6 +175,26 @@ def test_splitk_nt(hip, orc, shape):
     assert np.array_equal(dC2.to_host((rows, cols)), c)
 
 
+@pytest.mark.parametrize("shape", [(64, 576, 8192), (64, 320, 20000), (30, 100, 30000),
+                                   (128, 256, 12000), (64, 576, 1000)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_splitk_exact_slices_per_xcd(hip, shape):
+    """Split grids whose tile count is not a multiple of 8 (9, 5, 1 tiles) are
+    renumbered so each XCD owns whole K slices; one that is (8 tiles) keeps
+    the per-slice tile order. Small integers make every sum exact, so a slice
+    or tile computed twice or skipped would show as a bit difference."""
+    rows, cols, inner = shape
+    rng = np.random.default_rng(rows * cols + inner)
+    a = int_matrix(rng, (rows, inner), -2, 2)
+    b = int_matrix(rng, (cols, inner), -2, 2)
+    c0 = int_matrix(rng, (rows, cols))
+    dA, dB = hip.DeviceBuffer.from_host(a), hip.DeviceBuffer.from_host(b)
+    dC = hip.DeviceBuffer.from_host(c0)
+    hip.gemm_nt_splitk(dC, dA, dB, rows, cols, inner, 1.0)
+    want = (c0.astype(np.float64) + a.astype(np.float64) @ b.astype(np.float64).T)
+    assert np.array_equal(dC.to_host((rows, cols)), want.astype(np.float32))
+
+
 def test_splitk_cfg5_wgrad_shape(hip, orc):
     """cfg5 split-K wgrad M=64, N=576, K=100352 (NT), f64 on sampled rows."""
     rng = np.random.default_rng(576)
