@@ -114,7 +114,7 @@ def bench_gemm(hip, n, steps, warmup):
             "a": a, "b": b}
 
 
-def bench_conv_cfg3(hip, steps, warmup):
+def bench_conv_cfg3(hip, steps, warmup, closures_only=False):
     """cfg3 step: conv1 -> maxpool -> conv2, forward + backward: weight and
     bias gradients of both layers, input gradient of conv2. conv1's input is
     the image batch, which requires no gradient in the reference's training
@@ -167,6 +167,9 @@ def bench_conv_cfg3(hip, steps, warmup):
         hip.call("nrs_conv2d_backward", gx.ptr, None, None, gy1.ptr, dx.ptr, dw1.ptr,
                  N, 1, 28, 28, 32, 3, 3, 1, 1)
 
+    if closures_only:
+        return {"conv_fwd_cfg3": conv_fwd, "conv_bwd_cfg3": conv_bwd,
+                "conv1_input_grad_cfg3": conv1_input_grad}
     for _ in range(warmup):
         step()
     hip.sync()
@@ -242,7 +245,7 @@ def bench_mlp_cfg2(hip, steps, warmup):
     return {"us_per_step": us, "tflops": flops / (us * 1e-6) / 1e12, "gemm_roof_us": roof}
 
 
-def bench_attention_cfg4(hip, steps, warmup):
+def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
     """cfg4 attention core as one batched call over batch*heads = 256:
     S = Q.K^T / sqrt(32), P = softmax(S), O = P.V, then the backward bmm
     products dP = dO.V^T, dV = P^T.dO, dS = softmax'(P, dP)/sqrt(32),
@@ -288,11 +291,14 @@ def bench_attention_cfg4(hip, steps, warmup):
         hip.bmm_backward(hip.NN, dP, dv, do, P, v, BH, T, T, Dh, 1.0)
         hip.bmm_backward(hip.NT, dq, dk, dS, q, k, BH, T, Dh, T, 1.0)
 
-    fwd()
-    fwd_us = event_ms(hip, fwd, steps, warmup) * 1e3
-    bwd_us = event_ms(hip, bwd, steps, warmup) * 1e3
-    bmm_us = event_ms(hip, bmms_only, steps, warmup) * 1e3
-    bmm_acc_us = event_ms(hip, bmms_accumulate, steps, warmup) * 1e3
+    if closures_only:
+        closures = {"attn_bmm6_cfg4": bmms_only}
+    else:
+        fwd()
+        fwd_us = event_ms(hip, fwd, steps, warmup) * 1e3
+        bwd_us = event_ms(hip, bwd, steps, warmup) * 1e3
+        bmm_us = event_ms(hip, bmms_only, steps, warmup) * 1e3
+        bmm_acc_us = event_ms(hip, bmms_accumulate, steps, warmup) * 1e3
     bmm_roof = 6 * roofline_us(*gemm_roof(T, T, Dh, BH))  # every product moves 25.2 MB
 
     # the block's Linear GEMMs: X[4096,256] through 4 projections and the FFN
@@ -322,6 +328,9 @@ def bench_attention_cfg4(hip, steps, warmup):
     for _ in range(4):
         shapes += [(R, dm, dm), (R, dm, dm), (dm, dm, R)]
     shapes += [(R, ff, dm), (R, dm, ff), (dm, ff, R), (R, dm, ff), (R, ff, dm), (ff, dm, R)]
+    if closures_only:
+        closures["linear_gemms_cfg4"] = linears
+        return closures
     lin_us = event_ms(hip, linears, steps, warmup) * 1e3
     lin_flops = sum(gemm_roof(*s)[0] for s in shapes)
     lin_roof = sum(roofline_us(*gemm_roof(*s)) for s in shapes)
@@ -476,6 +485,46 @@ def profile_pass(hip, n, steps):
     hip.sync()
 
 
+def counters_pass(hip):
+    """Launch sequence for rocprofv3 --pmc over every bench leg: the
+    COPY_BYTES device copy (counter calibration), then each leg's launches
+    twice, the first call warming up, the second the one to read. A 4 KiB
+    device copy goes before each call as a separator, so the dispatch list
+    splits by position: after the calibration copy, segment 2i is leg i's
+    warm-up and segment 2i + 1 its counted call. Prints the leg names, in
+    order, as one JSON line."""
+    src = hip.DeviceBuffer.zeros(COPY_BYTES // 4)
+    dst = hip.DeviceBuffer(COPY_BYTES // 4)
+    mark_a, mark_b = hip.DeviceBuffer.zeros(1024), hip.DeviceBuffer(1024)
+    legs = []
+    rng = np.random.default_rng(5)
+    keep = []
+    for name, layout, m, n, k in (("gemm_nn_4096", hip.NN, 4096, 4096, 4096),
+                                  ("gemm_nn_2048", hip.NN, 2048, 2048, 2048),
+                                  ("gemm_nn_8192", hip.NN, 8192, 8192, 8192),
+                                  ("gemm_skinny_32x8192x8192", hip.NN, 32, 8192, 8192),
+                                  ("gemm_wgrad_nt_64x576x100352", hip.NT, 64, 576, 100352)):
+        a = hip.DeviceBuffer.from_host(rng.uniform(-1, 1, m * k).astype(np.float32))
+        b = hip.DeviceBuffer.from_host(rng.uniform(-1, 1, k * n).astype(np.float32))
+        c = hip.DeviceBuffer(m * n)
+        keep += [a, b, c]
+        if layout == hip.NN:
+            fn = (lambda a=a, b=b, c=c, m=m, n=n, k=k: hip.gemm(hip.NN, c, a, b, m, n, k))
+        else:
+            fn = (lambda a=a, b=b, c=c, m=m, n=n, k=k: hip.gemm_nt_splitk(c, a, b, m, n, k))
+        legs.append((name, fn))
+    legs += list(bench_conv_cfg3(hip, 0, 0, closures_only=True).items())
+    legs += list(bench_attention_cfg4(hip, 0, 0, closures_only=True).items())
+    hip.call("nrs_memcpy_dtod", dst.ptr, src.ptr, COPY_BYTES)
+    hip.sync()
+    for _, fn in legs:
+        for _ in range(2):
+            hip.call("nrs_memcpy_dtod", mark_b.ptr, mark_a.ptr, 4096)
+            fn()
+            hip.sync()
+    print(json.dumps([name for name, _ in legs]))
+
+
 def measured_traffic(n):
     """HBM bytes per launch of the n^3 GEMM from the committed counter
     summary (profiles/gemm_nn_4096_traffic.md), or None."""
@@ -499,6 +548,10 @@ def main():
     ap.add_argument("--no-conv", action="store_true", help="skip the conv2d leg")
     ap.add_argument("--no-legs", action="store_true",
                     help="skip the cfg2 / cfg4 / cfg5 legs (MLP step, attention, GEMM sweep)")
+    ap.add_argument("--counters-pass", action="store_true",
+                    help="only launch every leg twice behind 4 KiB copy separators, after a "
+                         "256 MiB copy calibration, for rocprofv3 --pmc runs; prints the leg "
+                         "names")
     ap.add_argument("--profile-pass", action="store_true",
                     help="only launch a 256 MiB device copy (counter calibration) and then "
                          "--steps GEMMs, for rocprofv3 --pmc runs; prints nothing else")
@@ -514,6 +567,9 @@ def main():
     n = args.size
     if args.profile_pass:
         profile_pass(hip, n, args.steps)
+        return
+    if args.counters_pass:
+        counters_pass(hip)
         return
     g = bench_gemm(hip, n, args.steps, args.warmup)
     flops = 2.0 * n * n * n
