@@ -261,10 +261,11 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
     o, dq, dk, dv = (hip.DeviceBuffer(BH * T * Dh) for _ in range(4))
     sc = 1.0 / np.sqrt(Dh)
 
+    # the scale is fused into the softmax (same bits as nrs_scale followed
+    # by nrs_softmax_forward / nrs_softmax_backward)
     def fwd():
         hip.bmm(hip.NT, S, q, k, BH, T, T, Dh)
-        hip.call("nrs_scale", S.ptr, S.ptr, sc, BH * T * T, 0.0)
-        hip.call("nrs_softmax_forward", P.ptr, S.ptr, BH * T, T)
+        hip.call("nrs_softmax_forward_scaled", P.ptr, S.ptr, BH * T, T, sc)
         hip.bmm(hip.NN, o, P, v, BH, T, Dh, T)
 
     # each bmm's backward computes both of its gradients in one call, as the
@@ -273,8 +274,7 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
     # dK = dS^T.Q
     def bwd():
         hip.bmm_backward(hip.NN, dP, dv, do, P, v, BH, T, T, Dh)
-        hip.call("nrs_softmax_backward", dS.ptr, P.ptr, dP.ptr, BH * T, T, 0.0)
-        hip.call("nrs_scale", dS.ptr, dS.ptr, sc, BH * T * T, 0.0)
+        hip.call("nrs_softmax_backward_scaled", dS.ptr, P.ptr, dP.ptr, BH * T, T, sc, 0.0)
         hip.bmm_backward(hip.NT, dq, dk, dS, q, k, BH, T, Dh, T)
 
     def bmms_only():

@@ -188,6 +188,18 @@ int nrs_softmax_forward(float *out, const float *in, int64_t rows, int64_t width
  * y: gin = y*(grad - sum(y*grad)) + beta*gin.                                */
 int nrs_softmax_backward(float *gin, const float *y, const float *grad, int64_t rows,
                          int64_t width, float beta);
+/* graph::scale then graph::softmax in one pass, the scaled-scores step of
+ * attention and attention_batch (src/cuda/nn/attention.rs:17-18,29-30;
+ * scale.rs:27, softmax.rs:43): out = softmax(scale*x) over the last dim. The
+ * product x*scale is rounded to f32 first, so the bits equal nrs_scale
+ * followed by nrs_softmax_forward.                                           */
+int nrs_softmax_forward_scaled(float *out, const float *in, int64_t rows, int64_t width,
+                               float scale);
+/* The backward of that pair in one pass: softmax_backward followed by
+ * scale_grad, gin = (y*(grad - sum(y*grad)))*scale + beta*gin. With beta 0
+ * the bits equal nrs_softmax_backward followed by nrs_scale.                 */
+int nrs_softmax_backward_scaled(float *gin, const float *y, const float *grad, int64_t rows,
+                                int64_t width, float scale, float beta);
 /* vrelu / relu_grad (src/cuda/graph/relu.rs:16-28): out = max(x, 0);
  * gin = (x > 0 ? grad : 0) + beta*gin.                                       */
 int nrs_relu_forward(float *out, const float *x, int64_t n);

@@ -51,11 +51,11 @@ template <bool KC>
 __device__ __forceinline__ f32x4 fragment(__amdgpu_buffer_rsrc_t rs, int r, int R, int K, int g,
                                           int h) {
     const int k = 8 * g + 4 * h;
-    if (KC) return buffer_load4(rs, (r < R) & (k < K) ? (r * K + k) * 4 : kOutOfRange);
+    if (KC) return buffer_load4(rs, ((r < R) & (k < K)) ? (r * K + k) * 4 : kOutOfRange);
     f32x4 v;
 #pragma unroll
     for (int p = 0; p < 4; ++p)
-        v[p] = buffer_load1(rs, (r < R) & (k + p < K) ? ((k + p) * R + r) * 4 : kOutOfRange);
+        v[p] = buffer_load1(rs, ((r < R) & (k + p < K)) ? ((k + p) * R + r) * 4 : kOutOfRange);
     return v;
 }
 
@@ -96,7 +96,7 @@ __device__ __forceinline__ void bmm_small_block(const SmallArgs& a, int wg) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int row = row0 + 8 * (e >> 2) + (e & 3);
-                old[j][e] = buffer_load1(rc, (row < a.M) & (n < a.N) ? (row * a.N + n) * 4
+                old[j][e] = buffer_load1(rc, ((row < a.M) & (n < a.N)) ? (row * a.N + n) * 4
                                                                       : kOutOfRange);
             }
         }

@@ -54,7 +54,6 @@ void wgrad_few_taps_kernel(FewTapsArgs a) {
 
     // gradient fragments first: [group][block], pixels 16*gi + 4*kq .. +3
     // of channel 16*b + t (zero past P and M through the buffer bounds)
-    const int GPI = (a.P + 15) >> 4;
     const int g0 = (chunk * 4 + wave) * GPW;
     const auto rg = buffer_rsrc(a.g + (int64_t)n * a.M * a.P, (int64_t)a.M * a.P * 4);
     f32x4v ga[GPW][NBLK];
@@ -64,7 +63,7 @@ void wgrad_few_taps_kernel(FewTapsArgs a) {
 #pragma unroll
         for (int b = 0; b < NBLK; ++b) {
             const int oc = 16 * b + t;
-            ga[q][b] = buffer_load4(rg, (p < a.P) & (oc < a.M) ? (oc * a.P + p) * 4 : kOutOfRange);
+            ga[q][b] = buffer_load4(rg, ((p < a.P) & (oc < a.M)) ? (oc * a.P + p) * 4 : kOutOfRange);
         }
     }
 

@@ -307,7 +307,7 @@ __device__ __forceinline__ void slab_block(const SlabArgs& a, int bx, int by) {
                 const int e = lane + 64 * k;
                 const int row = e / (NSW * 4), c4 = e - row * (NSW * 4);
                 const int oc = ocw0 + row, p = pw0 + 4 * c4;
-                old[k] = buffer_load4(ro, (oc < a.M) & (p < p_end) ? (oc * a.P + p) * 4
+                old[k] = buffer_load4(ro, ((oc < a.M) & (p < p_end)) ? (oc * a.P + p) * 4
                                                                    : kOutOfRange);
             }
         }

@@ -68,44 +68,106 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// One wave per row: max, sum of exp(x - max), then exp(x - max) / sum.
+// One wave per row of softmax(scale * x): max, sum of exp(t - max), then
+// exp(t - max) / sum, with t = x * scale rounded to f32 first, as vscale
+// followed by softmax_forward computes it. Lane l takes elements l, l + 64,
+// ... in that order. PER > 0: the row (width <= 64 * PER) stays in registers
+// and is read once. PER = 0: any width, re-read per pass. Both orders of
+// summation are the same, so every form gives the same bits.
+template <int PER>
 __global__ __launch_bounds__(256) void softmax_fwd_kernel(float* __restrict__ out,
                                                           const float* __restrict__ in,
-                                                          int64_t rows, int64_t width) {
+                                                          int64_t rows, int64_t width,
+                                                          float scale) {
+    // x * scale is rounded before the max subtraction, as when vscale runs
+    // first: no multiply-add contraction here
+#pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
     const int64_t waves = (int64_t)gridDim.x * 4;
     for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += waves) {
         const float* x = in + r * width;
-        float m = -INFINITY;
-        for (int64_t f = lane; f < width; f += 64) m = fmaxf(m, x[f]);
-        m = wave_max(m);
-        float s = 0.0f;
-        for (int64_t f = lane; f < width; f += 64) s += expf(x[f] - m);
-        s = wave_sum(s);
         float* y = out + r * width;
-        for (int64_t f = lane; f < width; f += 64) y[f] = expf(x[f] - m) / s;
+        if constexpr (PER > 0) {
+            float v[PER];
+            float m = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = lane + 64 * i;
+                v[i] = f < width ? x[f] * scale : -INFINITY;
+                m = fmaxf(m, v[i]);
+            }
+            m = wave_max(m);
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                v[i] = lane + 64 * i < width ? expf(v[i] - m) : 0.0f;
+                s += v[i];
+            }
+            s = wave_sum(s);
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = lane + 64 * i;
+                if (f < width) y[f] = v[i] / s;
+            }
+        } else {
+            float m = -INFINITY;
+            for (int64_t f = lane; f < width; f += 64) m = fmaxf(m, x[f] * scale);
+            m = wave_max(m);
+            float s = 0.0f;
+            for (int64_t f = lane; f < width; f += 64) s += expf(x[f] * scale - m);
+            s = wave_sum(s);
+            for (int64_t f = lane; f < width; f += 64) y[f] = expf(x[f] * scale - m) / s;
+        }
     }
 }
 
-// gin = y * (g - sum(y * g)) + beta * gin, with y the forward output.
+// gin = (y * (g - sum(y * g))) * scale + beta * gin, with y the forward
+// output: softmax_backward followed by scale_grad in one pass (scale 1 is
+// softmax_backward alone). Same lane order and register forms as above.
+template <int PER>
 __global__ __launch_bounds__(256) void softmax_bwd_kernel(float* __restrict__ gin,
                                                           const float* __restrict__ y,
                                                           const float* __restrict__ g,
                                                           int64_t rows, int64_t width,
-                                                          float beta) {
+                                                          float scale, float beta) {
+#pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
     const int64_t waves = (int64_t)gridDim.x * 4;
     for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += waves) {
         const float* yr = y + r * width;
         const float* gr = g + r * width;
-        float d = 0.0f;
-        for (int64_t f = lane; f < width; f += 64) d += yr[f] * gr[f];
-        d = wave_sum(d);
         float* o = gin + r * width;
-        for (int64_t f = lane; f < width; f += 64) {
-            float v = yr[f] * (gr[f] - d);
-            if (beta != 0.0f) v = v + beta * o[f];
-            o[f] = v;
+        if constexpr (PER > 0) {
+            float yv[PER], gv[PER], ov[PER];
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = lane + 64 * i;
+                const bool in = f < width;
+                yv[i] = in ? yr[f] : 0.0f;
+                gv[i] = in ? gr[f] : 0.0f;
+                ov[i] = (in && beta != 0.0f) ? o[f] : 0.0f;
+                d += yv[i] * gv[i];
+            }
+            d = wave_sum(d);
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = lane + 64 * i;
+                float v = yv[i] * (gv[i] - d);
+                if (scale != 1.0f) v = v * scale;
+                if (beta != 0.0f) v = v + beta * ov[i];
+                if (f < width) o[f] = v;
+            }
+        } else {
+            float d = 0.0f;
+            for (int64_t f = lane; f < width; f += 64) d += yr[f] * gr[f];
+            d = wave_sum(d);
+            for (int64_t f = lane; f < width; f += 64) {
+                float v = yr[f] * (gr[f] - d);
+                if (scale != 1.0f) v = v * scale;
+                if (beta != 0.0f) v = v + beta * o[f];
+                o[f] = v;
+            }
         }
     }
 }
@@ -160,27 +222,47 @@ int nrs_scale(float* out, const float* x, float s, int64_t n, float beta) {
     return NRS_OK;
 }
 
-int nrs_softmax_forward(float* out, const float* in, int64_t rows, int64_t width) {
+int nrs_softmax_forward_scaled(float* out, const float* in, int64_t rows, int64_t width,
+                               float scale) {
     NRS_REQUIRE_INIT();
     NRS_ARG_CHECK(rows >= 0 && width > 0, "softmax: bad shape");
     if (rows == 0) return NRS_OK;
     NRS_ARG_CHECK(out && in, "softmax: null pointer");
-    hipLaunchKernelGGL(nrs::softmax_fwd_kernel, dim3(nrs::rows_grid(rows)), dim3(256), 0,
-                       nrs::stream(), out, in, rows, width);
+    auto fn = width <= 64    ? nrs::softmax_fwd_kernel<1>
+              : width <= 128 ? nrs::softmax_fwd_kernel<2>
+              : width <= 256 ? nrs::softmax_fwd_kernel<4>
+              : width <= 512 ? nrs::softmax_fwd_kernel<8>
+                             : nrs::softmax_fwd_kernel<0>;
+    hipLaunchKernelGGL(fn, dim3(nrs::rows_grid(rows)), dim3(256), 0, nrs::stream(), out, in, rows,
+                       width, scale);
     NRS_LAUNCH_CHECK("softmax forward");
+    return NRS_OK;
+}
+
+int nrs_softmax_forward(float* out, const float* in, int64_t rows, int64_t width) {
+    return nrs_softmax_forward_scaled(out, in, rows, width, 1.0f);
+}
+
+int nrs_softmax_backward_scaled(float* gin, const float* y, const float* grad, int64_t rows,
+                                int64_t width, float scale, float beta) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(rows >= 0 && width > 0, "softmax backward: bad shape");
+    if (rows == 0) return NRS_OK;
+    NRS_ARG_CHECK(gin && y && grad, "softmax backward: null pointer");
+    auto fn = width <= 64    ? nrs::softmax_bwd_kernel<1>
+              : width <= 128 ? nrs::softmax_bwd_kernel<2>
+              : width <= 256 ? nrs::softmax_bwd_kernel<4>
+              : width <= 512 ? nrs::softmax_bwd_kernel<8>
+                             : nrs::softmax_bwd_kernel<0>;
+    hipLaunchKernelGGL(fn, dim3(nrs::rows_grid(rows)), dim3(256), 0, nrs::stream(), gin, y, grad,
+                       rows, width, scale, beta);
+    NRS_LAUNCH_CHECK("softmax backward");
     return NRS_OK;
 }
 
 int nrs_softmax_backward(float* gin, const float* y, const float* grad, int64_t rows,
                          int64_t width, float beta) {
-    NRS_REQUIRE_INIT();
-    NRS_ARG_CHECK(rows >= 0 && width > 0, "softmax backward: bad shape");
-    if (rows == 0) return NRS_OK;
-    NRS_ARG_CHECK(gin && y && grad, "softmax backward: null pointer");
-    hipLaunchKernelGGL(nrs::softmax_bwd_kernel, dim3(nrs::rows_grid(rows)), dim3(256), 0,
-                       nrs::stream(), gin, y, grad, rows, width, beta);
-    NRS_LAUNCH_CHECK("softmax backward");
-    return NRS_OK;
+    return nrs_softmax_backward_scaled(gin, y, grad, rows, width, 1.0f, beta);
 }
 
 int nrs_relu_forward(float* out, const float* x, int64_t n) {

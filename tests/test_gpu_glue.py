@@ -31,8 +31,8 @@ def test_scale_and_accumulate_exact(hip):
     assert np.array_equal(out.to_host(), acc + x * np.float32(0.25))
 
 
-@pytest.mark.parametrize("rows,width", [(4, 5), (1, 1), (7, 63), (5, 65), (3, 1000),
-                                        (32768, 128)])
+@pytest.mark.parametrize("rows,width", [(4, 5), (1, 1), (7, 63), (5, 65), (9, 200), (3, 512),
+                                        (2, 513), (3, 1000), (32768, 128)])
 def test_softmax_fwd_bwd(hip, orc, rows, width):
     rng = np.random.default_rng(rows + width)
     x = (rng.standard_normal(rows * width) * 2).astype(np.float32)
@@ -48,6 +48,44 @@ def test_softmax_fwd_bwd(hip, orc, rows, width):
     ref = acc0.copy()
     orc.softmax_backward(yc, g, ref, width)
     assert np.max(np.abs(gin.to_host() - ref)) < 1e-5 * max(1.0, np.sqrt(width))
+
+
+@pytest.mark.parametrize("rows,width", [(4, 5), (7, 63), (5, 65), (9, 200), (3, 512), (2, 513),
+                                        (3, 1000), (32768, 128)])
+def test_softmax_scaled_is_scale_then_softmax(hip, orc, rows, width):
+    """The fused scaled softmax (forward and backward) gives the same bits as
+    nrs_scale around nrs_softmax_*, as attention composes them, and matches
+    the oracle's softmax of the scaled scores."""
+    rng = np.random.default_rng(rows * width)
+    sc = np.float32(1.0 / np.sqrt(32.0))
+    x = (rng.standard_normal(rows * width) * 4).astype(np.float32)
+    g = rng.standard_normal(rows * width).astype(np.float32)
+    n = x.size
+    # forward: scale then softmax, against the fused call
+    t, y1, y2 = hip.DeviceBuffer(n), hip.DeviceBuffer(n), hip.DeviceBuffer(n)
+    dx = dev(hip, x)
+    hip.call("nrs_scale", t.ptr, dx.ptr, float(sc), n, 0.0)
+    hip.call("nrs_softmax_forward", y1.ptr, t.ptr, rows, width)
+    hip.call("nrs_softmax_forward_scaled", y2.ptr, dx.ptr, rows, width, float(sc))
+    assert np.array_equal(y1.to_host(), y2.to_host())
+    yc = orc.softmax_forward(x * sc, width)
+    assert np.max(np.abs(y2.to_host() - yc)) < 1e-6
+    # backward: softmax_backward then scale_grad, against the fused call
+    dy, dg = dev(hip, yc), dev(hip, g)
+    b1, b2 = hip.DeviceBuffer(n), hip.DeviceBuffer(n)
+    hip.call("nrs_softmax_backward", t.ptr, dy.ptr, dg.ptr, rows, width, 0.0)
+    hip.call("nrs_scale", b1.ptr, t.ptr, float(sc), n, 0.0)
+    hip.call("nrs_softmax_backward_scaled", b2.ptr, dy.ptr, dg.ptr, rows, width, float(sc), 0.0)
+    want = b1.to_host()
+    assert np.array_equal(want, b2.to_host())
+    ref = np.zeros(n, np.float32)
+    orc.softmax_backward(yc, g, ref, width)
+    assert np.max(np.abs(want - ref * sc)) < 1e-5 * max(1.0, np.sqrt(width))
+    # accumulating form: gin += the same gradient
+    acc0 = rng.standard_normal(n).astype(np.float32)
+    b3 = dev(hip, acc0)
+    hip.call("nrs_softmax_backward_scaled", b3.ptr, dy.ptr, dg.ptr, rows, width, float(sc), 1.0)
+    assert np.max(np.abs(b3.to_host() - (acc0 + want))) < 1e-6 * max(1.0, np.abs(acc0).max())
 
 
 def test_relu_fwd_bwd_exact(hip, orc):
