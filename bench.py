@@ -291,14 +291,29 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
         hip.bmm_backward(hip.NN, dP, dv, do, P, v, BH, T, T, Dh, 1.0)
         hip.bmm_backward(hip.NT, dq, dk, dS, q, k, BH, T, Dh, T, 1.0)
 
+    # the heads of the projections [32*128, 8*32] split into [8, 4096, 32]
+    # (q, k, v) and the attention output merged back: one launch each, in
+    # place of the reference's per-head slice_cols / concat_cols loops
+    Rh, Hh = 32 * 128, 8
+    wide = [D(rng.standard_normal(Rh * Hh * Dh).astype(np.float32)) for _ in range(3)]
+    split = [hip.DeviceBuffer(Rh * Hh * Dh) for _ in range(3)]
+    merged = hip.DeviceBuffer(Rh * Hh * Dh)
+
+    def heads():
+        for w_, s_ in zip(wide, split):
+            hip.call("nrs_split_heads", s_.ptr, w_.ptr, Rh, Hh, Dh, 0.0)
+        hip.call("nrs_merge_heads", merged.ptr, split[0].ptr, Rh, Hh, Dh, 0.0)
+
     if closures_only:
-        closures = {"attn_bmm6_cfg4": bmms_only}
+        closures = {"attn_bmm6_cfg4": bmms_only, "heads_split_merge_cfg4": heads}
     else:
         fwd()
         fwd_us = event_ms(hip, fwd, steps, warmup) * 1e3
         bwd_us = event_ms(hip, bwd, steps, warmup) * 1e3
         bmm_us = event_ms(hip, bmms_only, steps, warmup) * 1e3
         bmm_acc_us = event_ms(hip, bmms_accumulate, steps, warmup) * 1e3
+        heads_us = event_ms(hip, heads, steps, warmup) * 1e3
+        heads_roof = roofline_us(0.0, 4 * 8.0 * Rh * Hh * Dh)  # each reads and writes 4 MB
     bmm_roof = 6 * roofline_us(*gemm_roof(T, T, Dh, BH))  # every product moves 25.2 MB
 
     # the block's Linear GEMMs: X[4096,256] through 4 projections and the FFN
@@ -335,7 +350,7 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
     lin_flops = sum(gemm_roof(*s)[0] for s in shapes)
     lin_roof = sum(roofline_us(*gemm_roof(*s)) for s in shapes)
     return {"fwd_us": fwd_us, "bwd_us": bwd_us, "bmm_us": bmm_us, "bmm_roof_us": bmm_roof,
-            "bmm_acc_us": bmm_acc_us,
+            "bmm_acc_us": bmm_acc_us, "heads_us": heads_us, "heads_roof_us": heads_roof,
             "linear_us": lin_us, "linear_tflops": lin_flops / (lin_us * 1e-6) / 1e12,
             "linear_roof_us": lin_roof}
 
@@ -627,6 +642,8 @@ def main():
             "bmm_us": round(at["bmm_us"], 2), "bmm_roofline_us": round(at["bmm_roof_us"], 2),
             "bmm_roofline_frac": round(at["bmm_roof_us"] / at["bmm_us"], 4),
             "bmm_accumulate_us": round(at["bmm_acc_us"], 2),
+            "heads_split3_merge1_us": round(at["heads_us"], 2),
+            "heads_roofline_frac": round(at["heads_roof_us"] / at["heads_us"], 4),
             "attn_fwd_us": round(at["fwd_us"], 2), "attn_bwd_us": round(at["bwd_us"], 2),
             "linear_us": round(at["linear_us"], 2), "linear_tflops": round(at["linear_tflops"], 2),
             "linear_roofline_frac": round(at["linear_roof_us"] / at["linear_us"], 4),

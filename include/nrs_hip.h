@@ -200,6 +200,34 @@ int nrs_softmax_forward_scaled(float *out, const float *in, int64_t rows, int64_
  * the bits equal nrs_softmax_backward followed by nrs_scale.                 */
 int nrs_softmax_backward_scaled(float *gin, const float *y, const float *grad, int64_t rows,
                                 int64_t width, float scale, float beta);
+/* slice_fwd (src/cuda/graph/slice_cols.rs:12-20): out[r][c] = in[r][col_start
+ * + c] for r < rows, c < width, in having total_cols columns.                */
+int nrs_slice_cols(float *out, const float *in, int64_t rows, int64_t total_cols,
+                   int64_t col_start, int64_t width);
+/* slice_bwd + accumulate_into (slice_cols.rs:21-29,66-80): gin[r][col_start +
+ * c] = grad[r][c] + beta*gin[r][col_start + c]; gin's other columns are left
+ * as they are (the reference adds zeros there). beta = 1 is the reference.   */
+int nrs_slice_cols_backward(float *gin, const float *grad, int64_t rows, int64_t total_cols,
+                            int64_t col_start, int64_t width, float beta);
+/* concat_write (src/cuda/graph/concat_cols.rs:12-20), one part:
+ * out[r][col_offset + c] = part[r][c].                                       */
+int nrs_concat_cols(float *out, const float *part, int64_t rows, int64_t total_cols,
+                    int64_t col_offset, int64_t width);
+/* concat_read + accumulate_into (concat_cols.rs:21-29 and its backward
+ * closure): gpart[r][c] = grad[r][col_offset + c] + beta*gpart[r][c].        */
+int nrs_concat_cols_backward(float *gpart, const float *grad, int64_t rows, int64_t total_cols,
+                             int64_t col_offset, int64_t width, float beta);
+/* The per-head slice_cols loop of MultiHeadAttention (src/cuda/nn/
+ * multihead.rs:43-49,72-78) in one launch: out[h][r][c] = in[r][h*width + c]
+ * + beta*out[h][r][c], for heads x rows x width. The heads' rows are then one
+ * batched bmm of heads*batch items. beta = 1 is merge_heads' backward.       */
+int nrs_split_heads(float *out, const float *in, int64_t rows, int64_t heads, int64_t width,
+                    float beta);
+/* Its inverse, the heads' concat_cols (multihead.rs:52,81): out[r][h*width +
+ * c] = in[h][r][c] + beta*out[r][h*width + c]. beta = 1 is split_heads'
+ * backward.                                                                  */
+int nrs_merge_heads(float *out, const float *in, int64_t rows, int64_t heads, int64_t width,
+                    float beta);
 /* vrelu / relu_grad (src/cuda/graph/relu.rs:16-28): out = max(x, 0);
  * gin = (x > 0 ? grad : 0) + beta*gin.                                       */
 int nrs_relu_forward(float *out, const float *x, int64_t n);

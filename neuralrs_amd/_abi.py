@@ -56,6 +56,12 @@ SIGNATURES = {
     "nrs_scale": [_P, _P, _F, _I, _F],
     "nrs_softmax_forward": [_P, _P, _I, _I],
     "nrs_softmax_backward": [_P, _P, _P, _I, _I, _F],
+    "nrs_slice_cols": [_P, _P, _I, _I, _I, _I],
+    "nrs_slice_cols_backward": [_P, _P, _I, _I, _I, _I, _F],
+    "nrs_concat_cols": [_P, _P, _I, _I, _I, _I],
+    "nrs_concat_cols_backward": [_P, _P, _I, _I, _I, _I, _F],
+    "nrs_split_heads": [_P, _P, _I, _I, _I, _F],
+    "nrs_merge_heads": [_P, _P, _I, _I, _I, _F],
     "nrs_softmax_forward_scaled": [_P, _P, _I, _I, _F],
     "nrs_softmax_backward_scaled": [_P, _P, _P, _I, _I, _F, _F],
     "nrs_relu_forward": [_P, _P, _I],

@@ -4,6 +4,10 @@
 //   vscale           src/cuda/graph/scale.rs:10-20       (x * s)
 //   softmax fwd/bwd  src/cuda/graph/softmax.rs:11-35     (last dim)
 //   vrelu/relu_grad  src/cuda/graph/relu.rs:16-28
+//   slice_fwd/bwd    src/cuda/graph/slice_cols.rs:12-29  (column slice)
+//   concat_write/read src/cuda/graph/concat_cols.rs:12-29 (column concat)
+//   and the per-head slice/concat loops of MultiHeadAttention
+//   (src/cuda/nn/multihead.rs:43-52,72-81) as one launch each
 // Every backward entry point takes beta: gin = local + beta * gin, so beta = 1
 // fuses the accumulate_into() the reference launches after each of them
 // (src/cuda/runtime.rs:67-83).
@@ -13,6 +17,8 @@
 
 namespace nrs {
 namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 inline unsigned grid_for(int64_t n) {
     int64_t b = (n + 255) / 256;
@@ -188,12 +194,121 @@ __global__ __launch_bounds__(256) void relu_bwd_kernel(float* gin, const float* 
     }
 }
 
+// dst[h][r][c] = src[h][r][c] + beta * dst[h][r][c] over heads x rows x
+// width, each operand addressed through its own head and row strides
+// (floats). V = 4: 128-bit accesses (width, strides and both base addresses
+// are multiples of 4 floats); V = 1 otherwise.
+struct StridedCopy {
+    float* dst;
+    const float* src;
+    int64_t heads, rows, width;
+    int64_t d_h, d_r, s_h, s_r;
+    float beta;
+};
+
+template <int V>
+__global__ __launch_bounds__(256) void strided_copy_kernel(StridedCopy a) {
+    const int64_t wv = a.width / V, total = a.heads * a.rows * wv;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += step) {
+        const int64_t item = t / wv, c = (t - item * wv) * V;
+        const int64_t h = item / a.rows, r = item - h * a.rows;
+        const float* sp = a.src + h * a.s_h + r * a.s_r + c;
+        float* dp = a.dst + h * a.d_h + r * a.d_r + c;
+        if constexpr (V == 4) {
+            f32x4 v = *reinterpret_cast<const f32x4*>(sp);
+            if (a.beta != 0.0f) v = v + a.beta * *reinterpret_cast<const f32x4*>(dp);
+            *reinterpret_cast<f32x4*>(dp) = v;
+        } else {
+            float v = *sp;
+            if (a.beta != 0.0f) v = v + a.beta * *dp;
+            *dp = v;
+        }
+    }
+}
+
+int strided_copy(const StridedCopy& a, const char* what) {
+    const int64_t n = a.heads * a.rows * a.width;
+    if (n == 0) return NRS_OK;
+    const bool v4 = a.width % 4 == 0 && a.d_h % 4 == 0 && a.d_r % 4 == 0 && a.s_h % 4 == 0 &&
+                    a.s_r % 4 == 0 && ((uintptr_t)a.dst & 15) == 0 && ((uintptr_t)a.src & 15) == 0;
+    if (v4)
+        hipLaunchKernelGGL(strided_copy_kernel<4>, dim3(grid_for(n / 4)), dim3(256), 0, stream(),
+                           a);
+    else
+        hipLaunchKernelGGL(strided_copy_kernel<1>, dim3(grid_for(n)), dim3(256), 0, stream(), a);
+    NRS_LAUNCH_CHECK(what);
+    return NRS_OK;
+}
+
 inline unsigned rows_grid(int64_t rows) {
     return (unsigned)std::max<int64_t>(1, std::min<int64_t>((rows + 3) / 4, 32 * (int64_t)num_cus()));
 }
 
 }  // namespace
 }  // namespace nrs
+
+namespace nrs {
+namespace {
+
+// One column block of a rows x total_cols matrix against a dense rows x width
+// one. into_wide: the block receives (dst = wide + col, row stride
+// total_cols); otherwise the dense matrix does.
+int nrs_slice_cols_backward_impl(float* dst, const float* src, int64_t rows, int64_t total_cols,
+                                 int64_t col, int64_t width, float beta, bool into_wide) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(rows >= 0 && width >= 0 && col >= 0 && total_cols >= 0 &&
+                      col + width <= total_cols,
+                  "column slice: columns [%lld, %lld) outside %lld", (long long)col,
+                  (long long)(col + width), (long long)total_cols);
+    if (rows == 0 || width == 0) return NRS_OK;
+    NRS_ARG_CHECK(dst && src && (const float*)dst != src, "column slice: null or aliased pointer");
+    StridedCopy a{};
+    a.heads = 1;
+    a.rows = rows;
+    a.width = width;
+    a.beta = beta;
+    if (into_wide) {
+        a.dst = dst + col;
+        a.d_r = total_cols;
+        a.src = src;
+        a.s_r = width;
+    } else {
+        a.dst = dst;
+        a.d_r = width;
+        a.src = src + col;
+        a.s_r = total_cols;
+    }
+    return strided_copy(a, into_wide ? "column slice (into the wide matrix)" : "column slice");
+}
+
+// [rows][heads * width] <-> [heads][rows][width]
+int nrs_heads_impl(float* dst, const float* src, int64_t rows, int64_t heads, int64_t width,
+                   float beta, bool split) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(rows >= 0 && heads >= 0 && width >= 0, "heads: negative size");
+    if (rows == 0 || heads == 0 || width == 0) return NRS_OK;
+    NRS_ARG_CHECK(dst && src && (const float*)dst != src, "heads: null or aliased pointer");
+    StridedCopy a{};
+    a.dst = dst;
+    a.src = src;
+    a.heads = heads;
+    a.rows = rows;
+    a.width = width;
+    a.beta = beta;
+    const int64_t dense_h = rows * width, dense_r = width, wide_h = width, wide_r = heads * width;
+    a.d_h = split ? dense_h : wide_h;
+    a.d_r = split ? dense_r : wide_r;
+    a.s_h = split ? wide_h : dense_h;
+    a.s_r = split ? wide_r : dense_r;
+    return strided_copy(a, split ? "split heads" : "merge heads");
+}
+
+}  // namespace
+}  // namespace nrs
+
+using nrs::nrs_heads_impl;
+using nrs::nrs_slice_cols_backward_impl;
 
 extern "C" {
 
@@ -263,6 +378,37 @@ int nrs_softmax_backward_scaled(float* gin, const float* y, const float* grad, i
 int nrs_softmax_backward(float* gin, const float* y, const float* grad, int64_t rows,
                          int64_t width, float beta) {
     return nrs_softmax_backward_scaled(gin, y, grad, rows, width, 1.0f, beta);
+}
+
+int nrs_slice_cols(float* out, const float* in, int64_t rows, int64_t total_cols,
+                   int64_t col_start, int64_t width) {
+    return nrs_slice_cols_backward_impl(out, in, rows, total_cols, col_start, width, 0.0f, false);
+}
+
+int nrs_slice_cols_backward(float* gin, const float* grad, int64_t rows, int64_t total_cols,
+                            int64_t col_start, int64_t width, float beta) {
+    return nrs_slice_cols_backward_impl(gin, grad, rows, total_cols, col_start, width, beta, true);
+}
+
+int nrs_concat_cols(float* out, const float* part, int64_t rows, int64_t total_cols,
+                    int64_t col_offset, int64_t width) {
+    return nrs_slice_cols_backward_impl(out, part, rows, total_cols, col_offset, width, 0.0f, true);
+}
+
+int nrs_concat_cols_backward(float* gpart, const float* grad, int64_t rows, int64_t total_cols,
+                             int64_t col_offset, int64_t width, float beta) {
+    return nrs_slice_cols_backward_impl(gpart, grad, rows, total_cols, col_offset, width, beta,
+                                        false);
+}
+
+int nrs_split_heads(float* out, const float* in, int64_t rows, int64_t heads, int64_t width,
+                    float beta) {
+    return nrs_heads_impl(out, in, rows, heads, width, beta, true);
+}
+
+int nrs_merge_heads(float* out, const float* in, int64_t rows, int64_t heads, int64_t width,
+                    float beta) {
+    return nrs_heads_impl(out, in, rows, heads, width, beta, false);
 }
 
 int nrs_relu_forward(float* out, const float* x, int64_t n) {

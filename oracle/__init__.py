@@ -11,6 +11,7 @@ Parity status per function (see tests/test_oracle.py for the checks):
   graph_bmm_{forward,backward}, graph_add_bias_{forward,backward}, im2col,
   conv2d_im2col, conv2d_forward, conv2d_backward, gpu_im2col, gpu_col2out,
   gpu_out2mm, gpu_col2im, gpu_bias_grad, sum_axis0, maxpool_{forward,backward},
+  slice_cols{,_backward}, concat_cols{,_backward},
   gemm_f64 -- all pinned by the reference's known-answer tests, f64 ground
   truth, invariants and central-difference gradchecks.
   conv2d_backward's weight/bias gradient: the reference folds with a run-time
@@ -83,6 +84,10 @@ def lib():
             "orc_softmax_backward": (None, [f32p, f32p, f32p, I64, I64]),
             "orc_relu_forward": (None, [f32p, f32p, I64]),
             "orc_relu_backward": (None, [f32p, f32p, f32p, I64]),
+            "orc_slice_cols": (None, [f32p, f32p, I64, I64, I64, I64]),
+            "orc_slice_cols_backward": (None, [f32p, f32p, I64, I64, I64, I64]),
+            "orc_concat_part": (None, [f32p, f32p, I64, I64, I64, I64]),
+            "orc_concat_part_backward": (None, [f32p, f32p, I64, I64, I64, I64]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -346,6 +351,37 @@ def softmax_forward(x, width):
 def softmax_backward(y, g, ga, width):
     y = _f32(y).ravel()
     lib().orc_softmax_backward(y, _f32(g).ravel(), ga, y.size // width, width)
+
+
+def slice_cols(a, rows, total_cols, col_start, col_end):
+    out = np.empty(rows * (col_end - col_start), np.float32)
+    lib().orc_slice_cols(_f32(a).ravel(), out, rows, total_cols, col_start, col_end)
+    return out
+
+
+def slice_cols_backward(grad, ga, rows, total_cols, col_start, col_end):
+    lib().orc_slice_cols_backward(_f32(grad).ravel(), ga, rows, total_cols, col_start, col_end)
+
+
+def concat_cols(parts, rows):
+    """parts side by side along the last dim (one orc_concat_part each)."""
+    widths = [np.asarray(p).size // rows for p in parts]
+    total = sum(widths)
+    out = np.empty(rows * total, np.float32)
+    off = 0
+    for p, w in zip(parts, widths):
+        lib().orc_concat_part(_f32(p).ravel(), out, rows, total, off, w)
+        off += w
+    return out
+
+
+def concat_cols_backward(grad, gparts, rows):
+    """gparts[i] += its column block of grad, in place."""
+    widths = [g.size // rows for g in gparts]
+    total, off = sum(widths), 0
+    for gp, w in zip(gparts, widths):
+        lib().orc_concat_part_backward(_f32(grad).ravel(), gp, rows, total, off, w)
+        off += w
 
 
 def relu_forward(x):

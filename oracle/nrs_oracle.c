@@ -570,6 +570,43 @@ EXPORT void orc_transpose_backward(const float *g, float *ga, int64_t batch, int
     }
 }
 
+/* src/autograd/graph/slice_cols.rs:12-31 forward: out[r, c] = a[r, col_start */
+/* + c] for c < col_end - col_start (rows = len / total_cols).                */
+EXPORT void orc_slice_cols(const float *a, float *out, int64_t rows, int64_t total_cols,
+                           int64_t col_start, int64_t col_end) {
+    const int64_t w = col_end - col_start;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < w; ++c) out[r * w + c] = a[r * total_cols + (col_start + c)];
+}
+
+/* src/autograd/graph/slice_cols.rs:36-44 backward:                           */
+/* ga[r, col_start + c] += grad[r, c].                                        */
+EXPORT void orc_slice_cols_backward(const float *grad, float *ga, int64_t rows,
+                                    int64_t total_cols, int64_t col_start, int64_t col_end) {
+    const int64_t w = col_end - col_start;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < w; ++c)
+            ga[r * total_cols + (col_start + c)] = ga[r * total_cols + (col_start + c)] +
+                                                   grad[r * w + c];
+}
+
+/* src/autograd/graph/concat_cols.rs:22-30 forward, one part at col_offset:   */
+/* out[r, col_offset + c] = part[r, c].                                       */
+EXPORT void orc_concat_part(const float *part, float *out, int64_t rows, int64_t total_cols,
+                            int64_t col_offset, int64_t pw) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < pw; ++c) out[r * total_cols + (col_offset + c)] = part[r * pw + c];
+}
+
+/* src/autograd/graph/concat_cols.rs:44-55 backward, one part:                */
+/* gpart[r, c] += grad[r, col_offset + c].                                    */
+EXPORT void orc_concat_part_backward(const float *grad, float *gpart, int64_t rows,
+                                     int64_t total_cols, int64_t col_offset, int64_t pw) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < pw; ++c)
+            gpart[r * pw + c] = gpart[r * pw + c] + grad[r * total_cols + (col_offset + c)];
+}
+
 /* src/autograd/graph/scale.rs:7-33: out = x*s; backward ga += g*s.          */
 EXPORT void orc_scale(const float *x, float *out, float s, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = x[i] * s;

@@ -107,3 +107,114 @@ def test_glue_argument_errors(hip):
         hip.call("nrs_transpose", b.ptr, b.ptr, 1, 2, 2)  # aliased
     with pytest.raises(hip.NrsError):
         hip.call("nrs_softmax_forward", b.ptr, b.ptr, 1, 0)
+
+
+def test_slice_cols_twin(hip, orc):
+    """tests/cuda_manip_test.rs:49-61: slice forward, and its backward
+    accumulated into a zero input gradient, against the CPU op."""
+    from kat import close, formula, kats
+    t = kats()["gpu_twin"]["slice_cols"]
+    rows, total, cs, ce = t["rows"], t["total"], t["cs"], t["ce"]
+    x = formula(t["input"], rows * total)
+    seed = formula(t["seed"], rows * (ce - cs))
+    out = hip.DeviceBuffer(rows * (ce - cs))
+    hip.call("nrs_slice_cols", out.ptr, dev(hip, x).ptr, rows, total, cs, ce - cs)
+    close(out.to_host(), orc.slice_cols(x, rows, total, cs, ce), t["tol"], "slice_cols fwd")
+    ga = hip.DeviceBuffer.zeros(rows * total)
+    hip.call("nrs_slice_cols_backward", ga.ptr, dev(hip, seed).ptr, rows, total, cs, ce - cs, 1.0)
+    ref = np.zeros(rows * total, np.float32)
+    orc.slice_cols_backward(seed, ref, rows, total, cs, ce)
+    close(ga.to_host(), ref, t["tol"], "slice_cols grad")
+
+
+def test_concat_cols_twin(hip, orc):
+    """tests/cuda_manip_test.rs:105-141: three parts side by side, and the
+    gradient split back to each part."""
+    from kat import close, formula, kats
+    t = kats()["gpu_twin"]["concat_cols"]
+    rows, w = t["rows"], t["w"]
+    total = sum(w)
+    parts = [formula(p, rows * pw) for p, pw in zip(t["parts"], w)]
+    seed = formula(t["seed"], rows * total)
+    out = hip.DeviceBuffer(rows * total)
+    off = 0
+    for p, pw in zip(parts, w):
+        hip.call("nrs_concat_cols", out.ptr, dev(hip, p).ptr, rows, total, off, pw)
+        off += pw
+    close(out.to_host(), orc.concat_cols(parts, rows), t["tol"], "concat fwd")
+    refs = [np.zeros(rows * pw, np.float32) for pw in w]
+    orc.concat_cols_backward(seed, refs, rows)
+    dseed, off = dev(hip, seed), 0
+    for i, pw in enumerate(w):
+        gp = hip.DeviceBuffer.zeros(rows * pw)
+        hip.call("nrs_concat_cols_backward", gp.ptr, dseed.ptr, rows, total, off, pw, 1.0)
+        close(gp.to_host(), refs[i], t["tol"], f"concat grad{i}")
+        off += pw
+
+
+@pytest.mark.parametrize("rows,total,cs,w", [(3, 10, 2, 5), (64, 256, 32, 32), (7, 1024, 4, 1000),
+                                             (1, 1, 0, 1), (4096, 256, 224, 32)],
+                         ids=lambda v: str(v))
+def test_slice_concat_exact(hip, orc, rows, total, cs, w):
+    """Copies are exact, and so are beta = 1 sums of small integers: 128-bit
+    (width, offsets multiples of 4) and scalar forms."""
+    rng = np.random.default_rng(rows * total + cs)
+    x = int_matrix(rng, (rows * total,))
+    out = hip.DeviceBuffer(rows * w)
+    hip.call("nrs_slice_cols", out.ptr, dev(hip, x).ptr, rows, total, cs, w)
+    assert np.array_equal(out.to_host(), orc.slice_cols(x, rows, total, cs, cs + w))
+    g, acc = int_matrix(rng, (rows * w,)), int_matrix(rng, (rows * total,))
+    ga = dev(hip, acc)
+    hip.call("nrs_slice_cols_backward", ga.ptr, dev(hip, g).ptr, rows, total, cs, w, 1.0)
+    ref = acc.copy()
+    orc.slice_cols_backward(g, ref, rows, total, cs, cs + w)
+    assert np.array_equal(ga.to_host(), ref)
+    # concat of the slice into a wide buffer leaves the other columns alone
+    wide = dev(hip, acc)
+    hip.call("nrs_concat_cols", wide.ptr, dev(hip, g).ptr, rows, total, cs, w)
+    ref = acc.reshape(rows, total).copy()
+    ref[:, cs:cs + w] = g.reshape(rows, w)
+    assert np.array_equal(wide.to_host(), ref.ravel())
+    gp0 = int_matrix(rng, (rows * w,))
+    gp = dev(hip, gp0)
+    hip.call("nrs_concat_cols_backward", gp.ptr, dev(hip, x).ptr, rows, total, cs, w, 1.0)
+    assert np.array_equal(gp.to_host(), gp0 + x.reshape(rows, total)[:, cs:cs + w].ravel())
+
+
+@pytest.mark.parametrize("rows,heads,width", [(4096, 8, 32), (6, 3, 5), (128, 4, 64)])
+def test_split_merge_heads(hip, orc, rows, heads, width):
+    """split_heads equals the per-head slice_cols loop of MultiHeadAttention,
+    merge_heads its concat_cols; each is the other's backward (beta = 1)."""
+    rng = np.random.default_rng(rows + heads * width)
+    x = int_matrix(rng, (rows * heads * width,))
+    sp = hip.DeviceBuffer(x.size)
+    hip.call("nrs_split_heads", sp.ptr, dev(hip, x).ptr, rows, heads, width, 0.0)
+    want = np.concatenate([orc.slice_cols(x, rows, heads * width, h * width, (h + 1) * width)
+                           for h in range(heads)])
+    got = sp.to_host()
+    assert np.array_equal(got, want)
+    mg = hip.DeviceBuffer(x.size)
+    hip.call("nrs_merge_heads", mg.ptr, sp.ptr, rows, heads, width, 0.0)
+    assert np.array_equal(mg.to_host(), orc.concat_cols(np.split(want, heads), rows))
+    assert np.array_equal(mg.to_host(), x)
+    # accumulating forms
+    acc = int_matrix(rng, (x.size,))
+    a2 = dev(hip, acc)
+    hip.call("nrs_merge_heads", a2.ptr, sp.ptr, rows, heads, width, 1.0)
+    assert np.array_equal(a2.to_host(), acc + x)
+    a3 = dev(hip, acc)
+    hip.call("nrs_split_heads", a3.ptr, dev(hip, x).ptr, rows, heads, width, 1.0)
+    assert np.array_equal(a3.to_host(), acc + want)
+
+
+def test_slice_concat_errors(hip):
+    b = hip.DeviceBuffer(16)
+    with pytest.raises(hip.NrsError):
+        hip.call("nrs_slice_cols", b.ptr, b.ptr, 2, 4, 0, 2)  # aliased
+    c = hip.DeviceBuffer(16)
+    with pytest.raises(hip.NrsError):
+        hip.call("nrs_slice_cols", c.ptr, b.ptr, 2, 4, 3, 2)  # columns past the end
+    with pytest.raises(hip.NrsError):
+        hip.call("nrs_concat_cols_backward", c.ptr, b.ptr, 2, 4, -1, 2, 1.0)
+    with pytest.raises(hip.NrsError):
+        hip.call("nrs_split_heads", c.ptr, c.ptr, 2, 2, 4, 0.0)

@@ -400,3 +400,56 @@ def test_relu_exact_and_mask(orc):
     ga = np.zeros(300, np.float32)
     orc.relu_backward(x, g, ga)
     assert np.array_equal(ga, np.where(x > 0, g, 0).astype(np.float32))
+
+
+def test_slice_concat_known_answers(orc):
+    """tests/slice_concat_test.rs:5-31 and slice_concat_3d_test.rs:6-61."""
+    k = kats()["slice_concat"]
+    a = np.asarray(k["a"], np.float32)
+    rows, total = k["shape"]
+    left = orc.slice_cols(a, rows, total, *k["left"]["cols"])
+    right = orc.slice_cols(a, rows, total, *k["right"]["cols"])
+    assert np.array_equal(left, k["left"]["data"]) and np.array_equal(right, k["right"]["data"])
+    joined = orc.concat_cols([left, right], rows)
+    assert np.array_equal(joined, a)
+    # backward of the round trip with a ones seed: every input column gets 1
+    seed = np.full(rows * total, k["joined_grad_seed"], np.float32)
+    gl, gr = np.zeros_like(left), np.zeros_like(right)
+    orc.concat_cols_backward(seed, [gl, gr], rows)
+    ga = np.zeros_like(a)
+    orc.slice_cols_backward(gl, ga, rows, total, *k["left"]["cols"])
+    orc.slice_cols_backward(gr, ga, rows, total, *k["right"]["cols"])
+    assert np.array_equal(ga, np.full_like(a, k["a_grad"]))
+
+    k3 = kats()["slice_concat_3d"]
+    x = np.arange(16, dtype=np.float32)           # [2, 2, 4]: rows = 4 of the last dim
+    s = orc.slice_cols(x, 4, 4, *k3["slice"]["cols"])
+    assert np.array_equal(s, k3["slice"]["expected"])
+    c = orc.concat_cols([np.asarray(k3["concat"]["a"], np.float32),
+                         np.asarray(k3["concat"]["b"], np.float32)], 4)
+    assert np.array_equal(c, k3["concat"]["expected"])
+    xin = (np.arange(16) * np.float32(k3["roundtrip"]["input_scale"])).astype(np.float32)
+    l3, r3 = orc.slice_cols(xin, 4, 4, 0, 2), orc.slice_cols(xin, 4, 4, 2, 4)
+    assert np.array_equal(orc.concat_cols([l3, r3], 4), xin)
+    g = (np.arange(16) + 1).astype(np.float32)
+    gl3, gr3 = np.zeros(8, np.float32), np.zeros(8, np.float32)
+    orc.concat_cols_backward(g, [gl3, gr3], 4)
+    gin = np.zeros(16, np.float32)
+    orc.slice_cols_backward(gl3, gin, 4, 4, 0, 2)
+    orc.slice_cols_backward(gr3, gin, 4, 4, 2, 4)
+    assert np.array_equal(gin, g)
+
+
+def test_slice_concat_match_numpy_indexing(orc):
+    """The restatement against numpy's column indexing on ragged shapes."""
+    rng = np.random.default_rng(7)
+    for rows, total, cs, ce in ((1, 1, 0, 1), (5, 9, 2, 7), (3, 8, 0, 8), (7, 33, 31, 33)):
+        x = rng.standard_normal(rows * total).astype(np.float32)
+        want = x.reshape(rows, total)[:, cs:ce].ravel()
+        assert np.array_equal(orc.slice_cols(x, rows, total, cs, ce), want)
+        g = rng.standard_normal(rows * (ce - cs)).astype(np.float32)
+        ga = rng.standard_normal(rows * total).astype(np.float32)
+        ref = ga.reshape(rows, total).copy()
+        ref[:, cs:ce] += g.reshape(rows, ce - cs)
+        orc.slice_cols_backward(g, ga, rows, total, cs, ce)
+        assert np.array_equal(ga, ref.ravel())
