@@ -66,9 +66,19 @@ int nrs_set_stream(void *stream);
 void *nrs_get_stream(void);
 /* Message for the last non-zero status (thread-local, valid until the next call). */
 const char *nrs_last_error(void);
-/* Device buffers: replace stream.alloc_zeros / CudaSlice drop (runtime.rs:39-51). */
+/* Device buffers: replace stream.alloc_zeros / CudaSlice drop (runtime.rs:39-51).
+ * A caching allocator: sizes round up to classes (512 B steps to 1 MiB, 2 MiB
+ * steps above); nrs_free returns the block to its class's cache, and the next
+ * nrs_malloc of that class reuses it in library-stream order. nrs_free of a
+ * pointer that is not a live nrs_malloc buffer is an error. Memory is not
+ * zeroed (alloc_zeros = nrs_malloc + nrs_memset_zero).                       */
 int nrs_malloc(void **ptr, size_t bytes);
 int nrs_free(void *ptr);
+/* hipFree every cached idle block (live buffers are untouched); also done by
+ * nrs_shutdown and, once, by an nrs_malloc that runs out of memory.          */
+int nrs_empty_cache(void);
+/* Bytes held by live buffers and by idle cached blocks (class-rounded).     */
+int nrs_memory_stats(size_t *live_bytes, size_t *cached_bytes);
 /* clone_htod / clone_dtoh (runtime.rs:39-63). dtoh synchronises the stream. */
 int nrs_memcpy_htod(void *dst, const void *src, size_t bytes);
 int nrs_memcpy_dtoh(void *dst, const void *src, size_t bytes);

@@ -30,6 +30,8 @@ SIGNATURES = {
     "nrs_last_error": [],
     "nrs_malloc": [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t],
     "nrs_free": [_P],
+    "nrs_empty_cache": [],
+    "nrs_memory_stats": [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
     "nrs_memcpy_htod": [_P, _P, ctypes.c_size_t],
     "nrs_memcpy_dtoh": [_P, _P, ctypes.c_size_t],
     "nrs_memcpy_dtod": [_P, _P, ctypes.c_size_t],
@@ -103,7 +105,8 @@ def check(rc: int, what: str) -> None:
 def call(name: str, *args) -> None:
     """Call an entry point. DeviceBuffer / torch-tensor arguments are passed as
     their device pointers and stay referenced until the launch is enqueued
-    (nrs_free then waits for the device before releasing them)."""
+    (nrs_free caches the block; it is reused only by work enqueued later on
+    the library stream, so queued launches finish with it first)."""
     conv = [_ptr(a) if isinstance(a, DeviceBuffer) or hasattr(a, "data_ptr") else a for a in args]
     check(getattr(load(), name)(*conv), name)
 

@@ -4,6 +4,8 @@
 // residency helpers of src/cuda/runtime.rs:39-124.
 #include <cstdarg>
 #include <cstring>
+#include <unordered_map>
+#include <vector>
 
 #include "nrs_internal.hpp"
 
@@ -22,6 +24,42 @@ struct State {
 
 State g;
 thread_local char g_err[1024] = "";
+
+// Caching allocator behind nrs_malloc / nrs_free. The reference allocates
+// every op's output and gradient with alloc_zeros and frees them on drop
+// (src/cuda/runtime.rs:39-51, e.g. src/cuda/graph/matmul.rs:271,410), so a
+// drop-in pays one allocation per op; hipMalloc costs tens of microseconds and
+// hipFree waits for the device. Blocks are rounded to size classes (512 B
+// steps up to 1 MiB, 2 MiB steps above) and a freed block goes to its class's
+// free list, to be handed out again by the next nrs_malloc of that class.
+// Reuse follows the library stream's order: work enqueued after the reuse
+// runs after every launch that read the block before it was freed.
+constexpr size_t kSmallLimit = size_t(1) << 20, kSmallStep = 512,
+                 kLargeStep = size_t(2) << 20;
+
+struct BlockCache {
+    std::unordered_map<void*, size_t> live;               // pointer -> class bytes
+    std::unordered_map<size_t, std::vector<void*>> idle;  // class bytes -> free blocks
+    size_t live_bytes = 0, idle_bytes = 0;
+};
+BlockCache cache;
+
+size_t size_class(size_t bytes) {
+    if (bytes == 0) bytes = 4;  // a distinct non-null handle for empty tensors
+    const size_t step = bytes <= kSmallLimit ? kSmallStep : kLargeStep;
+    return (bytes + step - 1) / step * step;
+}
+
+// hipFree every idle block (after the stream that freed them has drained).
+int release_idle() {
+    if (cache.idle_bytes == 0) return NRS_OK;
+    NRS_HIP_CHECK(hipStreamSynchronize(g.stream));
+    for (auto& kv : cache.idle)
+        for (void* p : kv.second) NRS_HIP_CHECK(hipFree(p));
+    cache.idle.clear();
+    cache.idle_bytes = 0;
+    return NRS_OK;
+}
 
 // Zero fill in 16-byte units where aligned; a kernel rather than
 // hipMemsetAsync so the call stays correct inside a captured HIP graph.
@@ -121,6 +159,7 @@ int nrs_init(int device) {
 int nrs_shutdown(void) {
     if (!g.init) return NRS_OK;
     NRS_HIP_CHECK(hipStreamSynchronize(g.stream));
+    if (int rc = nrs::release_idle()) return rc;
     for (int s = 0; s < nrs::kSlots; ++s) {
         if (g.ws[s]) NRS_HIP_CHECK(hipFree(g.ws[s]));
         g.ws[s] = nullptr;
@@ -130,6 +169,10 @@ int nrs_shutdown(void) {
 }
 
 int nrs_set_stream(void* stream) {
+    // idle cached blocks may still be read by the old stream's queued work,
+    // which a new stream would not be ordered after
+    if (static_cast<hipStream_t>(stream) != g.stream && nrs::cache.idle_bytes)
+        NRS_HIP_CHECK(hipStreamSynchronize(g.stream));
     g.stream = static_cast<hipStream_t>(stream);
     return NRS_OK;
 }
@@ -142,16 +185,52 @@ int nrs_malloc(void** ptr, size_t bytes) {
     NRS_REQUIRE_INIT();
     NRS_ARG_CHECK(ptr != nullptr, "nrs_malloc: null out-pointer");
     *ptr = nullptr;
-    if (bytes == 0) bytes = 4;  // distinct non-null handle for empty tensors
-    hipError_t e = hipMalloc(ptr, bytes);
-    if (e != hipSuccess)
-        return nrs::set_error(NRS_ERR_ALLOC, "nrs_malloc(%zu): %s", bytes, hipGetErrorString(e));
+    auto& c = nrs::cache;
+    const size_t cls = nrs::size_class(bytes);
+    void* p = nullptr;
+    auto it = c.idle.find(cls);
+    if (it != c.idle.end() && !it->second.empty()) {
+        p = it->second.back();
+        it->second.pop_back();
+        c.idle_bytes -= cls;
+    } else {
+        hipError_t e = hipMalloc(&p, cls);
+        if (e != hipSuccess) {
+            // out of memory with blocks idle in the cache: give them back, retry once
+            (void)hipGetLastError();
+            if (int rc = nrs::release_idle()) return rc;
+            e = hipMalloc(&p, cls);
+        }
+        if (e != hipSuccess)
+            return nrs::set_error(NRS_ERR_ALLOC, "nrs_malloc(%zu): %s", bytes,
+                                  hipGetErrorString(e));
+    }
+    c.live.emplace(p, cls);
+    c.live_bytes += cls;
+    *ptr = p;
     return NRS_OK;
 }
 
 int nrs_free(void* ptr) {
     if (!ptr) return NRS_OK;
-    NRS_HIP_CHECK(hipFree(ptr));
+    auto& c = nrs::cache;
+    auto it = c.live.find(ptr);
+    NRS_ARG_CHECK(it != c.live.end(),
+                  "nrs_free(%p): not a live nrs_malloc buffer (freed twice, or not from "
+                  "nrs_malloc)", ptr);
+    const size_t cls = it->second;
+    c.live.erase(it);
+    c.live_bytes -= cls;
+    c.idle[cls].push_back(ptr);
+    c.idle_bytes += cls;
+    return NRS_OK;
+}
+
+int nrs_empty_cache(void) { return nrs::release_idle(); }
+
+int nrs_memory_stats(size_t* live_bytes, size_t* cached_bytes) {
+    if (live_bytes) *live_bytes = nrs::cache.live_bytes;
+    if (cached_bytes) *cached_bytes = nrs::cache.idle_bytes;
     return NRS_OK;
 }
 
