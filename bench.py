@@ -304,8 +304,23 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
             hip.call("nrs_split_heads", s_.ptr, w_.ptr, Rh, Hh, Dh, 0.0)
         hip.call("nrs_merge_heads", merged.ptr, split[0].ptr, Rh, Hh, Dh, 0.0)
 
+    # the block's LayerNorm over [4096, 256], forward and backward (input,
+    # gamma and beta gradients, accumulated)
+    lx = wide[0]
+    lg, lb = D(np.ones(Hh * Dh, np.float32)), D(np.zeros(Hh * Dh, np.float32))
+    lout, lxn, listd = hip.DeviceBuffer(Rh * Hh * Dh), hip.DeviceBuffer(Rh * Hh * Dh), hip.DeviceBuffer(Rh)
+    ldin = hip.DeviceBuffer.zeros(Rh * Hh * Dh)
+    ldg, ldb = hip.DeviceBuffer.zeros(Hh * Dh), hip.DeviceBuffer.zeros(Hh * Dh)
+
+    def layernorm():
+        hip.call("nrs_layernorm_forward", lout.ptr, lxn.ptr, listd.ptr, lx.ptr, lg.ptr, lb.ptr,
+                 Rh, Hh * Dh, 1e-5)
+        hip.call("nrs_layernorm_backward", ldin.ptr, ldg.ptr, ldb.ptr, split[1].ptr, lg.ptr,
+                 lxn.ptr, listd.ptr, Rh, Hh * Dh, 1.0)
+
     if closures_only:
-        closures = {"attn_bmm6_cfg4": bmms_only, "heads_split_merge_cfg4": heads}
+        closures = {"attn_bmm6_cfg4": bmms_only, "heads_split_merge_cfg4": heads,
+                    "layernorm_cfg4": layernorm}
     else:
         fwd()
         fwd_us = event_ms(hip, fwd, steps, warmup) * 1e3
@@ -314,6 +329,11 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
         bmm_acc_us = event_ms(hip, bmms_accumulate, steps, warmup) * 1e3
         heads_us = event_ms(hip, heads, steps, warmup) * 1e3
         heads_roof = roofline_us(0.0, 4 * 8.0 * Rh * Hh * Dh)  # each reads and writes 4 MB
+        ln_us = event_ms(hip, layernorm, steps, warmup) * 1e3
+        # forward reads x, writes out and x_norm; backward reads grad and
+        # x_norm, writes dinput (+ reads dinput, accumulating); the parameter
+        # sums read grad and x_norm: 9 passes of 4 MB
+        ln_roof = roofline_us(0.0, 9 * 4.0 * Rh * Hh * Dh)
     bmm_roof = 6 * roofline_us(*gemm_roof(T, T, Dh, BH))  # every product moves 25.2 MB
 
     # the block's Linear GEMMs: X[4096,256] through 4 projections and the FFN
@@ -351,6 +371,7 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
     lin_roof = sum(roofline_us(*gemm_roof(*s)) for s in shapes)
     return {"fwd_us": fwd_us, "bwd_us": bwd_us, "bmm_us": bmm_us, "bmm_roof_us": bmm_roof,
             "bmm_acc_us": bmm_acc_us, "heads_us": heads_us, "heads_roof_us": heads_roof,
+            "ln_us": ln_us, "ln_roof_us": ln_roof,
             "linear_us": lin_us, "linear_tflops": lin_flops / (lin_us * 1e-6) / 1e12,
             "linear_roof_us": lin_roof}
 
@@ -644,6 +665,8 @@ def main():
             "bmm_accumulate_us": round(at["bmm_acc_us"], 2),
             "heads_split3_merge1_us": round(at["heads_us"], 2),
             "heads_roofline_frac": round(at["heads_roof_us"] / at["heads_us"], 4),
+            "layernorm_fwd_bwd_us": round(at["ln_us"], 2),
+            "layernorm_roofline_frac": round(at["ln_roof_us"] / at["ln_us"], 4),
             "attn_fwd_us": round(at["fwd_us"], 2), "attn_bwd_us": round(at["bwd_us"], 2),
             "linear_us": round(at["linear_us"], 2), "linear_tflops": round(at["linear_tflops"], 2),
             "linear_roofline_frac": round(at["linear_roof_us"] / at["linear_us"], 4),

@@ -238,6 +238,21 @@ int nrs_split_heads(float *out, const float *in, int64_t rows, int64_t heads, in
  * backward.                                                                  */
 int nrs_merge_heads(float *out, const float *in, int64_t rows, int64_t heads, int64_t width,
                     float beta);
+/* cuda::nn::layernorm forward (src/cuda/nn/normalization.rs:14-40 ln_forward,
+ * 87-120), used by TransformerBlock: per row of `features`, mean, biased var,
+ * inv_std = 1/sqrt(var + eps), x_norm = (x - mean)*inv_std, out = gamma*x_norm
+ * + beta. x_norm [rows*features] and inv_std [rows] are saved for backward.  */
+int nrs_layernorm_forward(float *out, float *x_norm, float *inv_std, const float *in,
+                          const float *gamma, const float *beta, int64_t rows, int64_t features,
+                          float eps);
+/* Its backward (ln_dx, ln_reduce and accumulate_into, normalization.rs:41-80,
+ * 133-160): dxh = grad*gamma; dinput = inv_std*(dxh - mean(dxh) - x_norm*
+ * mean(dxh*x_norm)); dgamma = sum over rows of grad*x_norm; dbeta = sum of
+ * grad; each + acc*old (acc = 1 is the reference's accumulate). Null outputs
+ * are skipped.                                                               */
+int nrs_layernorm_backward(float *dinput, float *dgamma, float *dbeta, const float *grad,
+                           const float *gamma, const float *x_norm, const float *inv_std,
+                           int64_t rows, int64_t features, float acc);
 /* vrelu / relu_grad (src/cuda/graph/relu.rs:16-28): out = max(x, 0);
  * gin = (x > 0 ? grad : 0) + beta*gin.                                       */
 int nrs_relu_forward(float *out, const float *x, int64_t n);

@@ -8,6 +8,7 @@
 //   concat_write/read src/cuda/graph/concat_cols.rs:12-29 (column concat)
 //   and the per-head slice/concat loops of MultiHeadAttention
 //   (src/cuda/nn/multihead.rs:43-52,72-81) as one launch each
+//   layernorm        src/cuda/nn/normalization.rs:14-85  (TransformerBlock)
 // Every backward entry point takes beta: gin = local + beta * gin, so beta = 1
 // fuses the accumulate_into() the reference launches after each of them
 // (src/cuda/runtime.rs:67-83).
@@ -241,6 +242,176 @@ int strided_copy(const StridedCopy& a, const char* what) {
     return NRS_OK;
 }
 
+// LayerNorm forward, one wave per row (src/cuda/nn/normalization.rs:14-40
+// ln_forward, which runs one thread per row): mean, biased variance,
+// inv_std = 1 / sqrt(var + eps), x_norm = (x - mean) * inv_std and
+// out = gamma * x_norm + beta. PER > 0 keeps the row (features <= 64 * PER)
+// in registers; PER = 0 re-reads it.
+template <int PER>
+__global__ __launch_bounds__(256) void layernorm_fwd_kernel(
+    float* __restrict__ out, float* __restrict__ xn_out, float* __restrict__ istd_out,
+    const float* __restrict__ in, const float* __restrict__ gamma,
+    const float* __restrict__ beta, int64_t rows, int64_t F, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t waves = (int64_t)gridDim.x * 4;
+    const float nf = (float)F;
+    for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += waves) {
+        const float* x = in + r * F;
+        float* y = out + r * F;
+        float* xn = xn_out + r * F;
+        if constexpr (PER > 0) {
+            float v[PER];
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = lane + 64 * i;
+                v[i] = f < F ? x[f] : 0.0f;
+                s += v[i];
+            }
+            const float mean = wave_sum(s) / nf;
+            float q = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const float d = lane + 64 * i < F ? v[i] - mean : 0.0f;
+                q += d * d;
+            }
+            const float istd = 1.0f / sqrtf(wave_sum(q) / nf + eps);
+            if (lane == 0) istd_out[r] = istd;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = lane + 64 * i;
+                if (f < F) {
+                    const float t = (v[i] - mean) * istd;
+                    xn[f] = t;
+                    y[f] = gamma[f] * t + beta[f];
+                }
+            }
+        } else {
+            float s = 0.0f;
+            for (int64_t f = lane; f < F; f += 64) s += x[f];
+            const float mean = wave_sum(s) / nf;
+            float q = 0.0f;
+            for (int64_t f = lane; f < F; f += 64) {
+                const float d = x[f] - mean;
+                q += d * d;
+            }
+            const float istd = 1.0f / sqrtf(wave_sum(q) / nf + eps);
+            if (lane == 0) istd_out[r] = istd;
+            for (int64_t f = lane; f < F; f += 64) {
+                const float t = (x[f] - mean) * istd;
+                xn[f] = t;
+                y[f] = gamma[f] * t + beta[f];
+            }
+        }
+    }
+}
+
+// LayerNorm input gradient, one wave per row (normalization.rs:57-80 ln_dx):
+// dxh = grad * gamma, dinput = inv_std * (dxh - sum(dxh)/F - x_norm *
+// sum(dxh * x_norm)/F) + acc * dinput.
+__global__ __launch_bounds__(256) void layernorm_dx_kernel(
+    float* __restrict__ dinput, const float* __restrict__ grad, const float* __restrict__ gamma,
+    const float* __restrict__ x_norm, const float* __restrict__ inv_std, int64_t rows, int64_t F,
+    float acc) {
+    const int lane = threadIdx.x & 63;
+    const int64_t waves = (int64_t)gridDim.x * 4;
+    const float nf = (float)F;
+    for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += waves) {
+        const float* g = grad + r * F;
+        const float* xn = x_norm + r * F;
+        float s1 = 0.0f, s2 = 0.0f;
+        for (int64_t f = lane; f < F; f += 64) {
+            const float d = g[f] * gamma[f];
+            s1 += d;
+            s2 += d * xn[f];
+        }
+        s1 = wave_sum(s1) / nf;
+        s2 = wave_sum(s2) / nf;
+        const float istd = inv_std[r];
+        float* o = dinput + r * F;
+        for (int64_t f = lane; f < F; f += 64) {
+            float v = istd * (g[f] * gamma[f] - s1 - xn[f] * s2);
+            if (acc != 0.0f) v = v + acc * o[f];
+            o[f] = v;
+        }
+    }
+}
+
+// LayerNorm parameter gradients over rows (normalization.rs:41-56 ln_reduce
+// runs one thread per feature over every row). Block (x, c) sums rows
+// [c*kLnRows, (c+1)*kLnRows) of grad * x_norm and grad for 256 features into
+// partial[c], issuing 8 rows' loads before adding any. The combine kernel
+// splits the chunks into kLnGroups contiguous ranges summed in parallel
+// (ascending inside a range) and adds the ranges in order, so the result is
+// deterministic.
+constexpr int kLnRows = 32, kLnGroups = 16;
+
+__global__ __launch_bounds__(256) void layernorm_param_partial_kernel(
+    float* __restrict__ part_g, float* __restrict__ part_b, const float* __restrict__ grad,
+    const float* __restrict__ x_norm, int64_t rows, int64_t F) {
+    const int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (f >= F) return;
+    const int64_t r0 = (int64_t)blockIdx.y * kLnRows;
+    float dg = 0.0f, db = 0.0f;
+    for (int b = 0; b < kLnRows; b += 8) {
+        float gv[8], xv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t r = r0 + b + u;
+            const bool ok = r < rows;
+            gv[u] = ok ? grad[r * F + f] : 0.0f;
+            xv[u] = ok ? x_norm[r * F + f] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            dg += gv[u] * xv[u];
+            db += gv[u];
+        }
+    }
+    part_g[(int64_t)blockIdx.y * F + f] = dg;
+    part_b[(int64_t)blockIdx.y * F + f] = db;
+}
+
+__global__ __launch_bounds__(64 * kLnGroups) void layernorm_param_combine_kernel(
+    float* __restrict__ dgamma, float* __restrict__ dbeta, const float* __restrict__ part_g,
+    const float* __restrict__ part_b, int64_t chunks, int64_t F, float acc) {
+    __shared__ float red[2][kLnGroups][64];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const int64_t f = (int64_t)blockIdx.x * 64 + tx;
+    const int64_t per = (chunks + kLnGroups - 1) / kLnGroups;
+    const int64_t c0 = min(chunks, ty * per), c1 = min(chunks, c0 + per);
+    float dg = 0.0f, db = 0.0f;
+    if (f < F) {
+        for (int64_t c = c0; c < c1; c += 8) {
+            float gv[8], bv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const bool ok = c + u < c1;
+                gv[u] = ok ? part_g[(c + u) * F + f] : 0.0f;
+                bv[u] = ok ? part_b[(c + u) * F + f] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                dg += gv[u];
+                db += bv[u];
+            }
+        }
+    }
+    red[0][ty][tx] = dg;
+    red[1][ty][tx] = db;
+    __syncthreads();
+    if (ty == 0 && f < F) {
+        float sg = red[0][0][tx], sb = red[1][0][tx];
+#pragma unroll
+        for (int y = 1; y < kLnGroups; ++y) {
+            sg += red[0][y][tx];
+            sb += red[1][y][tx];
+        }
+        if (dgamma) dgamma[f] = acc != 0.0f ? sg + acc * dgamma[f] : sg;
+        if (dbeta) dbeta[f] = acc != 0.0f ? sb + acc * dbeta[f] : sb;
+    }
+}
+
 inline unsigned rows_grid(int64_t rows) {
     return (unsigned)std::max<int64_t>(1, std::min<int64_t>((rows + 3) / 4, 32 * (int64_t)num_cus()));
 }
@@ -409,6 +580,57 @@ int nrs_split_heads(float* out, const float* in, int64_t rows, int64_t heads, in
 int nrs_merge_heads(float* out, const float* in, int64_t rows, int64_t heads, int64_t width,
                     float beta) {
     return nrs_heads_impl(out, in, rows, heads, width, beta, false);
+}
+
+int nrs_layernorm_forward(float* out, float* x_norm, float* inv_std, const float* in,
+                          const float* gamma, const float* beta, int64_t rows, int64_t features,
+                          float eps) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(rows >= 0 && features > 0, "layernorm: bad shape");
+    if (rows == 0) return NRS_OK;
+    NRS_ARG_CHECK(out && x_norm && inv_std && in && gamma && beta, "layernorm: null pointer");
+    const int64_t F = features;
+    auto fn = F <= 64    ? nrs::layernorm_fwd_kernel<1>
+              : F <= 128 ? nrs::layernorm_fwd_kernel<2>
+              : F <= 256 ? nrs::layernorm_fwd_kernel<4>
+              : F <= 512 ? nrs::layernorm_fwd_kernel<8>
+                         : nrs::layernorm_fwd_kernel<0>;
+    hipLaunchKernelGGL(fn, dim3(nrs::rows_grid(rows)), dim3(256), 0, nrs::stream(), out, x_norm,
+                       inv_std, in, gamma, beta, rows, F, eps);
+    NRS_LAUNCH_CHECK("layernorm forward");
+    return NRS_OK;
+}
+
+int nrs_layernorm_backward(float* dinput, float* dgamma, float* dbeta, const float* grad,
+                           const float* gamma, const float* x_norm, const float* inv_std,
+                           int64_t rows, int64_t features, float acc) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(rows >= 0 && features > 0, "layernorm backward: bad shape");
+    if (rows == 0) return NRS_OK;
+    NRS_ARG_CHECK(grad && x_norm, "layernorm backward: null pointer");
+    const int64_t F = features;
+    if (dinput) {
+        NRS_ARG_CHECK(gamma && inv_std, "layernorm backward: null gamma or inv_std");
+        hipLaunchKernelGGL(nrs::layernorm_dx_kernel, dim3(nrs::rows_grid(rows)), dim3(256), 0,
+                           nrs::stream(), dinput, grad, gamma, x_norm, inv_std, rows, F, acc);
+        NRS_LAUNCH_CHECK("layernorm backward (input)");
+    }
+    if (dgamma || dbeta) {
+        const int64_t chunks = (rows + nrs::kLnRows - 1) / nrs::kLnRows;
+        const int64_t fb = (F + 255) / 256, fb64 = (F + 63) / 64;
+        NRS_ARG_CHECK(fb64 <= INT32_MAX && chunks <= 65535, "layernorm backward: too large");
+        float* part = nrs::workspace(sizeof(float) * 2 * (size_t)(chunks * F), 0);
+        if (!part) return NRS_ERR_ALLOC;
+        hipLaunchKernelGGL(nrs::layernorm_param_partial_kernel, dim3((unsigned)fb, (unsigned)chunks),
+                           dim3(256), 0, nrs::stream(), part, part + chunks * F, grad, x_norm, rows,
+                           F);
+        NRS_LAUNCH_CHECK("layernorm backward (parameter partials)");
+        hipLaunchKernelGGL(nrs::layernorm_param_combine_kernel, dim3((unsigned)fb64),
+                           dim3(64 * nrs::kLnGroups), 0, nrs::stream(), dgamma, dbeta, part,
+                           part + chunks * F, chunks, F, acc);
+        NRS_LAUNCH_CHECK("layernorm backward (parameters)");
+    }
+    return NRS_OK;
 }
 
 int nrs_relu_forward(float* out, const float* x, int64_t n) {

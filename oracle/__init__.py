@@ -11,7 +11,7 @@ Parity status per function (see tests/test_oracle.py for the checks):
   graph_bmm_{forward,backward}, graph_add_bias_{forward,backward}, im2col,
   conv2d_im2col, conv2d_forward, conv2d_backward, gpu_im2col, gpu_col2out,
   gpu_out2mm, gpu_col2im, gpu_bias_grad, sum_axis0, maxpool_{forward,backward},
-  slice_cols{,_backward}, concat_cols{,_backward},
+  slice_cols{,_backward}, concat_cols{,_backward}, layernorm_{forward,backward},
   gemm_f64 -- all pinned by the reference's known-answer tests, f64 ground
   truth, invariants and central-difference gradchecks.
   conv2d_backward's weight/bias gradient: the reference folds with a run-time
@@ -85,6 +85,8 @@ def lib():
             "orc_relu_forward": (None, [f32p, f32p, I64]),
             "orc_relu_backward": (None, [f32p, f32p, f32p, I64]),
             "orc_slice_cols": (None, [f32p, f32p, I64, I64, I64, I64]),
+            "orc_layernorm_forward": (None, [f32p] * 6 + [I64, I64, ctypes.c_float]),
+            "orc_layernorm_backward": (None, [f32p] * 7 + [I64, I64]),
             "orc_slice_cols_backward": (None, [f32p, f32p, I64, I64, I64, I64]),
             "orc_concat_part": (None, [f32p, f32p, I64, I64, I64, I64]),
             "orc_concat_part_backward": (None, [f32p, f32p, I64, I64, I64, I64]),
@@ -382,6 +384,22 @@ def concat_cols_backward(grad, gparts, rows):
     for gp, w in zip(gparts, widths):
         lib().orc_concat_part_backward(_f32(grad).ravel(), gp, rows, total, off, w)
         off += w
+
+
+def layernorm_forward(x, gamma, beta, rows, features, eps):
+    """(out, x_norm, inv_std) of nn::normalization::LayerNorm's forward."""
+    out = np.empty(rows * features, np.float32)
+    xn = np.empty(rows * features, np.float32)
+    istd = np.empty(rows, np.float32)
+    lib().orc_layernorm_forward(_f32(x).ravel(), _f32(gamma).ravel(), _f32(beta).ravel(), out, xn,
+                                istd, rows, features, float(eps))
+    return out, xn, istd
+
+
+def layernorm_backward(grad, gamma, x_norm, inv_std, din, dgamma, dbeta, rows, features):
+    """Accumulates the backward into din, dgamma, dbeta (float32 arrays)."""
+    lib().orc_layernorm_backward(_f32(grad).ravel(), _f32(gamma).ravel(), _f32(x_norm).ravel(),
+                                 _f32(inv_std).ravel(), din, dgamma, dbeta, rows, features)
 
 
 def relu_forward(x):

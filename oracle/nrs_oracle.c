@@ -607,6 +607,68 @@ EXPORT void orc_concat_part_backward(const float *grad, float *gpart, int64_t ro
             gpart[r * pw + c] = gpart[r * pw + c] + grad[r * total_cols + (col_offset + c)];
 }
 
+/* nn::normalization::LayerNorm (src/nn/normalization.rs:24-56) forward:     */
+/* per row, mean = sum/F and var = sum((x-mean)^2)/F summed left to right,    */
+/* istd = 1/sqrt(var + eps), x_norm = (x - mean)*istd, out = gamma*x_norm +   */
+/* beta. x_norm and inv_std are kept for the backward.                        */
+EXPORT void orc_layernorm_forward(const float *in, const float *gamma, const float *beta,
+                                  float *out, float *x_norm, float *inv_std, int64_t rows,
+                                  int64_t F, float eps) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *x = in + r * F;
+        float s = 0.0f;
+        for (int64_t f = 0; f < F; ++f) s = s + x[f];
+        const float mean = s / (float)F;
+        float q = 0.0f;
+        for (int64_t f = 0; f < F; ++f) {
+            const float d = x[f] - mean;
+            q = q + d * d;
+        }
+        const float var = q / (float)F;
+        const float istd = 1.0f / sqrtf(var + eps);
+        inv_std[r] = istd;
+        for (int64_t f = 0; f < F; ++f) {
+            const float xn = (x[f] - mean) * istd;
+            x_norm[r * F + f] = xn;
+            out[r * F + f] = gamma[f] * xn + beta[f];
+        }
+    }
+}
+
+/* src/nn/normalization.rs:58-97 backward: per row sum1 = sum(dxh), sum2 =    */
+/* sum(dxh*x_norm) with dxh = grad*gamma; din += istd*(dxh - sum1/F -         */
+/* x_norm*sum2/F); dgamma += grad*x_norm and dbeta += grad over rows (the     */
+/* per-call sums are added to the running grads at the end).                  */
+EXPORT void orc_layernorm_backward(const float *grad, const float *gamma, const float *x_norm,
+                                   const float *inv_std, float *din, float *dgamma,
+                                   float *dbeta, int64_t rows, int64_t F) {
+    float *dg = (float *)calloc((size_t)F, sizeof(float));
+    float *db = (float *)calloc((size_t)F, sizeof(float));
+    const float nf = (float)F;
+    for (int64_t r = 0; r < rows; ++r) {
+        const float istd = inv_std[r];
+        float s1 = 0.0f, s2 = 0.0f;
+        for (int64_t f = 0; f < F; ++f) {
+            const float d = grad[r * F + f] * gamma[f];
+            s1 = s1 + d;
+            s2 = s2 + d * x_norm[r * F + f];
+        }
+        for (int64_t f = 0; f < F; ++f) {
+            const int64_t i = r * F + f;
+            const float d = grad[i] * gamma[f];
+            din[i] = din[i] + istd * (d - s1 / nf - x_norm[i] * s2 / nf);
+            dg[f] = dg[f] + grad[i] * x_norm[i];
+            db[f] = db[f] + grad[i];
+        }
+    }
+    for (int64_t f = 0; f < F; ++f) {
+        dgamma[f] = dgamma[f] + dg[f];
+        dbeta[f] = dbeta[f] + db[f];
+    }
+    free(dg);
+    free(db);
+}
+
 /* src/autograd/graph/scale.rs:7-33: out = x*s; backward ga += g*s.          */
 EXPORT void orc_scale(const float *x, float *out, float s, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = x[i] * s;

@@ -218,3 +218,63 @@ def test_slice_concat_errors(hip):
         hip.call("nrs_concat_cols_backward", c.ptr, b.ptr, 2, 4, -1, 2, 1.0)
     with pytest.raises(hip.NrsError):
         hip.call("nrs_split_heads", c.ptr, c.ptr, 2, 2, 4, 0.0)
+
+
+def test_layernorm_twin(hip, orc):
+    """tests/cuda_layers_test.rs:18-62: forward, input grad and gamma/beta
+    grads against the CPU LayerNorm, tol 1e-4."""
+    from kat import close, formula, kats
+    t = kats()["gpu_twin"]["layernorm"]
+    rows, F, eps = t["rows"], t["features"], t["eps"]
+    x, g, b = formula(t["input"], rows * F), formula(t["gamma"], F), formula(t["beta"], F)
+    seed = formula(t["seed"], rows * F)
+    out, xn, istd = hip.DeviceBuffer(rows * F), hip.DeviceBuffer(rows * F), hip.DeviceBuffer(rows)
+    dg_, db_ = dev(hip, g), dev(hip, b)
+    hip.call("nrs_layernorm_forward", out.ptr, xn.ptr, istd.ptr, dev(hip, x).ptr, dg_.ptr,
+             db_.ptr, rows, F, eps)
+    cout, cxn, cistd = orc.layernorm_forward(x, g, b, rows, F, eps)
+    close(out.to_host(), cout, t["tol"], "layernorm fwd")
+    din, dgam, dbet = (hip.DeviceBuffer.zeros(n) for n in (rows * F, F, F))
+    hip.call("nrs_layernorm_backward", din.ptr, dgam.ptr, dbet.ptr, dev(hip, seed).ptr, dg_.ptr,
+             xn.ptr, istd.ptr, rows, F, 1.0)
+    rin, rg, rb = np.zeros(rows * F, np.float32), np.zeros(F, np.float32), np.zeros(F, np.float32)
+    orc.layernorm_backward(seed, g, cxn, cistd, rin, rg, rb, rows, F)
+    close(din.to_host(), rin, t["tol"], "layernorm dinput")
+    close(dgam.to_host(), rg, t["tol"], "layernorm dgamma")
+    close(dbet.to_host(), rb, t["tol"], "layernorm dbeta")
+
+
+@pytest.mark.parametrize("rows,F", [(4096, 256), (5, 64), (3, 65), (70, 512), (9, 600), (1, 1)])
+def test_layernorm_vs_oracle(hip, orc, rows, F):
+    """Register (F <= 512) and re-reading forms, the accumulating backward
+    and skipped outputs, at cfg4's TransformerBlock width and edge widths."""
+    rng = np.random.default_rng(rows * F)
+    eps = 1e-5
+    x = (rng.standard_normal(rows * F) * 3 + 1).astype(np.float32)
+    g, b = rng.standard_normal(F).astype(np.float32), rng.standard_normal(F).astype(np.float32)
+    gr = rng.standard_normal(rows * F).astype(np.float32)
+    out, xn, istd = hip.DeviceBuffer(rows * F), hip.DeviceBuffer(rows * F), hip.DeviceBuffer(rows)
+    dg_ = dev(hip, g)
+    hip.call("nrs_layernorm_forward", out.ptr, xn.ptr, istd.ptr, dev(hip, x).ptr, dg_.ptr,
+             dev(hip, b).ptr, rows, F, eps)
+    cout, cxn, cistd = orc.layernorm_forward(x, g, b, rows, F, eps)
+    scale = 1.0 + np.abs(g).max() + np.abs(b).max()
+    assert np.max(np.abs(out.to_host() - cout)) < 2e-5 * scale
+    assert np.max(np.abs(xn.to_host() - cxn)) < 2e-5
+    assert np.max(np.abs(istd.to_host() - cistd) / cistd) < 1e-5
+    acc_in = rng.standard_normal(rows * F).astype(np.float32)
+    acc_g, acc_b = rng.standard_normal(F).astype(np.float32), rng.standard_normal(F).astype(np.float32)
+    din, dgam, dbet = dev(hip, acc_in), dev(hip, acc_g), dev(hip, acc_b)
+    hip.call("nrs_layernorm_backward", din.ptr, dgam.ptr, dbet.ptr, dev(hip, gr).ptr, dg_.ptr,
+             xn.ptr, istd.ptr, rows, F, 1.0)
+    rin, rg, rb = acc_in.copy(), acc_g.copy(), acc_b.copy()
+    orc.layernorm_backward(gr, g, cxn, cistd, rin, rg, rb, rows, F)
+    assert np.max(np.abs(din.to_host() - rin)) < 1e-4 * (1 + np.abs(rin).max())
+    tol_p = 1e-5 * np.sqrt(rows) * (1 + np.abs(rg).max())
+    assert np.max(np.abs(dgam.to_host() - rg)) < tol_p
+    assert np.max(np.abs(dbet.to_host() - rb)) < 1e-5 * np.sqrt(rows) * (1 + np.abs(rb).max())
+    # parameter gradients only, overwriting (acc 0); the input gradient is skipped
+    d2 = hip.DeviceBuffer(F)
+    hip.call("nrs_layernorm_backward", None, d2.ptr, None, dev(hip, gr).ptr, None, xn.ptr, None,
+             rows, F, 0.0)
+    assert np.max(np.abs(d2.to_host() - (rg - acc_g))) < tol_p

@@ -453,3 +453,53 @@ def test_slice_concat_match_numpy_indexing(orc):
         ref[:, cs:ce] += g.reshape(rows, ce - cs)
         orc.slice_cols_backward(g, ga, rows, total, cs, ce)
         assert np.array_equal(ga, ref.ravel())
+
+
+def test_layernorm_known_answers_and_gradcheck(orc):
+    """nn_layernorm_test.rs / layernorm_3d_test.rs (zero-mean rows with gamma 1,
+    beta 0), gradcheck_layernorm_test.rs (central differences of sum(out^2),
+    h = 1e-3, tol 1e-2), and an f64 restatement of the formula."""
+    k = kats()["layernorm"]
+    eps = k["eps"]
+    for case in k["row_means"]:
+        x = np.asarray(case["input"], np.float32)
+        F = case["features"]
+        rows = x.size // F
+        out, _, _ = orc.layernorm_forward(x, np.ones(F, np.float32), np.zeros(F, np.float32),
+                                          rows, F, eps)
+        assert np.all(np.abs(out.reshape(rows, F).mean(axis=1)) < case["tol"])
+    gc = k["gradcheck"]
+    gamma, beta = np.asarray(gc["gamma"], np.float32), np.asarray(gc["beta"], np.float32)
+    x = np.asarray(gc["input"], np.float32)
+    F = x.size
+
+    def loss(v):
+        return float(np.sum(orc.layernorm_forward(v, gamma, beta, 1, F, eps)[0] ** 2))
+    num = np.array([(loss(x + np.eye(F, dtype=np.float32)[i] * np.float32(gc["h"])) -
+                     loss(x - np.eye(F, dtype=np.float32)[i] * np.float32(gc["h"]))) / (2 * gc["h"])
+                    for i in range(F)])
+    out, xn, istd = orc.layernorm_forward(x, gamma, beta, 1, F, eps)
+    din, dg, db = np.zeros(F, np.float32), np.zeros(F, np.float32), np.zeros(F, np.float32)
+    orc.layernorm_backward(2 * out, gamma, xn, istd, din, dg, db, 1, F)
+    assert np.max(np.abs(num - din)) < gc["tol"]
+    # f64 formula on random rows
+    rng = np.random.default_rng(11)
+    rows, F = 37, 70
+    x = rng.standard_normal(rows * F).astype(np.float32)
+    g, b = rng.standard_normal(F).astype(np.float32), rng.standard_normal(F).astype(np.float32)
+    out, xn, istd = orc.layernorm_forward(x, g, b, rows, F, eps)
+    x64 = x.reshape(rows, F).astype(np.float64)
+    mu, var = x64.mean(axis=1, keepdims=True), x64.var(axis=1, keepdims=True)
+    xn64 = (x64 - mu) / np.sqrt(var + eps)
+    assert np.max(np.abs(out.reshape(rows, F) - (xn64 * g + b))) < 1e-5
+    # backward against the f64 closed form (and dgamma/dbeta column sums)
+    gr = rng.standard_normal(rows * F).astype(np.float32)
+    din, dg, db = np.zeros(rows * F, np.float32), np.zeros(F, np.float32), np.zeros(F, np.float32)
+    orc.layernorm_backward(gr, g, xn, istd, din, dg, db, rows, F)
+    g64 = gr.reshape(rows, F).astype(np.float64)
+    dxh = g64 * g
+    want = (dxh - dxh.mean(axis=1, keepdims=True) -
+            xn64 * (dxh * xn64).mean(axis=1, keepdims=True)) / np.sqrt(var + eps)
+    assert np.max(np.abs(din.reshape(rows, F) - want)) < 1e-4
+    assert np.max(np.abs(dg - (g64 * xn64).sum(axis=0))) < 1e-3
+    assert np.max(np.abs(db - g64.sum(axis=0))) < 1e-4
