@@ -1,6 +1,8 @@
 // Implementation of the C++ host layer (neuralrs.hpp) over the C ABI of
 // libnrs_hip.so. Each op follows the reference op it names: same operand
 // checks and panic messages, same output shape, same gradient flow.
+#include <memory>
+
 #include "neuralrs.hpp"
 
 #include <cmath>
@@ -293,6 +295,84 @@ NodeRef relu(const NodeRef& a) {
     return node;
 }
 
+NodeRef slice_cols(const NodeRef& a, size_t col_start, size_t col_end) {
+    GpuBuffers& ag = gpu_of(a, "cuda slice_cols: input not on GPU");
+    if (a->shape.empty()) throw Panic("cuda slice_cols: scalar input");
+    const size_t total = a->shape.back(), len = product(a->shape);
+    if (col_start > col_end || col_end > total) throw Panic("cuda slice_cols: bad column range");
+    const size_t rows = total ? len / total : 0, w = col_end - col_start;
+    DeviceBuffer out(rows * w, false);
+    check(nrs_slice_cols(out.ptr(), ag.data.ptr(), rows, total, col_start, w),
+          "cuda slice_cols: launch failed");
+    std::vector<size_t> shape = a->shape;
+    shape.back() = w;
+    NodeRef node = make_output(shape, {a}, std::move(out));
+    // slice_bwd into a zero temporary plus accumulate_into, as one pass
+    node->backward_fn = [grad = node->gpu->grad, a, rows, total, col_start,
+                         w](const std::vector<float>&) {
+        check(nrs_slice_cols_backward(gpu_of(a, "backward: parent not on GPU").grad->ptr(),
+                                      grad->ptr(), rows, total, col_start, w, 1.0f),
+              "cuda slice_cols bwd: launch");
+    };
+    return node;
+}
+
+NodeRef concat_cols(const std::vector<NodeRef>& parts) {
+    if (parts.empty()) throw Panic("cuda concat_cols: no parts");
+    std::vector<size_t> widths;
+    size_t total = 0;
+    for (const NodeRef& p : parts) {
+        gpu_of(p, "cuda concat_cols: part not on GPU");
+        if (p->shape.empty()) throw Panic("cuda concat_cols: scalar part");
+        widths.push_back(p->shape.back());
+        total += widths.back();
+    }
+    const size_t rows = widths[0] ? product(parts[0]->shape) / widths[0] : 0;
+    for (size_t i = 0; i < parts.size(); ++i)
+        if (product(parts[i]->shape) != rows * widths[i])
+            throw Panic("cuda concat_cols: parts differ in rows");
+    DeviceBuffer out(rows * total, false);
+    size_t off = 0;
+    for (size_t i = 0; i < parts.size(); ++i) {
+        check(nrs_concat_cols(out.ptr(), gpu_of(parts[i], "").data.ptr(), rows, total, off,
+                              widths[i]),
+              "cuda concat_cols: write launch failed");
+        off += widths[i];
+    }
+    std::vector<size_t> shape = parts[0]->shape;
+    shape.back() = total;
+    NodeRef node = make_output(shape, parts, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, parts, widths, rows,
+                         total](const std::vector<float>&) {
+        size_t off = 0;
+        for (size_t i = 0; i < parts.size(); ++i) {
+            check(nrs_concat_cols_backward(gpu_of(parts[i], "backward: part not on GPU").grad->ptr(),
+                                           grad->ptr(), rows, total, off, widths[i], 1.0f),
+                  "cuda concat_cols bwd: launch");
+            off += widths[i];
+        }
+    };
+    return node;
+}
+
+NodeRef scaled_softmax(const NodeRef& a, float s) {
+    GpuBuffers& ag = gpu_of(a, "cuda softmax: input not on GPU");
+    if (a->shape.empty()) throw Panic("cuda softmax: scalar input");
+    const size_t width = a->shape.back(), len = product(a->shape);
+    const size_t rows = width ? len / width : 0;
+    DeviceBuffer out(len, false);
+    check(nrs_softmax_forward_scaled(out.ptr(), ag.data.ptr(), rows, width, s),
+          "cuda softmax: launch failed");
+    NodeRef node = make_output(a->shape, {a}, std::move(out));
+    const float* y = node->gpu->data.ptr();
+    node->backward_fn = [grad = node->gpu->grad, a, y, rows, width, s](const std::vector<float>&) {
+        check(nrs_softmax_backward_scaled(gpu_of(a, "cuda softmax bwd: input not on GPU").grad->ptr(),
+                                          y, grad->ptr(), rows, width, s, 1.0f),
+              "cuda softmax bwd: launch");
+    };
+    return node;
+}
+
 }  // namespace graph
 
 // ---------------------------------------------------------------------- nn
@@ -371,8 +451,7 @@ NodeRef attention(const NodeRef& q, const NodeRef& k, const NodeRef& v) {
     const float s = 1.0f / std::sqrt(static_cast<float>(q->shape[1]));
     NodeRef kt = graph::transpose(k);
     NodeRef scores = graph::matmul(q, kt);
-    NodeRef scaled = graph::scale(scores, s);
-    NodeRef weights = graph::softmax(scaled);
+    NodeRef weights = graph::scaled_softmax(scores, s);  // scale + softmax, one node
     return graph::matmul(weights, v);
 }
 
@@ -381,9 +460,36 @@ NodeRef attention_batch(const NodeRef& q, const NodeRef& k, const NodeRef& v) {
     const float s = 1.0f / std::sqrt(static_cast<float>(q->shape[2]));
     NodeRef kt = graph::transpose(k);
     NodeRef scores = graph::bmm(q, kt);
-    NodeRef scaled = graph::scale(scores, s);
-    NodeRef weights = graph::softmax(scaled);
+    NodeRef weights = graph::scaled_softmax(scores, s);  // scale + softmax, one node
     return graph::bmm(weights, v);
+}
+
+NodeRef layernorm(const NodeRef& input, const NodeRef& gamma, const NodeRef& beta, float eps) {
+    GpuBuffers& ig = gpu_of(input, "cuda layernorm: input not on GPU");
+    GpuBuffers& gg = gpu_of(gamma, "cuda layernorm: gamma not on GPU");
+    GpuBuffers& bg = gpu_of(beta, "cuda layernorm: beta not on GPU");
+    if (input->shape.empty()) throw Panic("cuda layernorm: scalar input");
+    const size_t F = input->shape.back(), len = product(input->shape);
+    const size_t rows = F ? len / F : 0;
+    if (F == 0 || product(gamma->shape) != F || product(beta->shape) != F)
+        throw Panic("cuda layernorm: gamma/beta length mismatch");
+    DeviceBuffer out(len, false);
+    auto xn = std::make_shared<DeviceBuffer>(len, false);
+    auto istd = std::make_shared<DeviceBuffer>(rows, false);
+    check(nrs_layernorm_forward(out.ptr(), xn->ptr(), istd->ptr(), ig.data.ptr(), gg.data.ptr(),
+                                bg.data.ptr(), rows, F, eps),
+          "cuda layernorm: forward launch failed");
+    NodeRef node = make_output(input->shape, {input, gamma, beta}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, input, gamma, beta, xn, istd, rows,
+                         F](const std::vector<float>&) {
+        GpuBuffers& ig = gpu_of(input, "cuda layernorm bwd: input not on GPU");
+        GpuBuffers& gg = gpu_of(gamma, "cuda layernorm bwd: gamma not on GPU");
+        GpuBuffers& bg = gpu_of(beta, "cuda layernorm bwd: beta not on GPU");
+        check(nrs_layernorm_backward(ig.grad->ptr(), gg.grad->ptr(), bg.grad->ptr(), grad->ptr(),
+                                     gg.data.ptr(), xn->ptr(), istd->ptr(), rows, F, 1.0f),
+              "cuda layernorm bwd: launch");
+    };
+    return node;
 }
 
 }  // namespace nn

@@ -8,9 +8,10 @@
 //   Node / GpuBuffers / backward_graph   src/autograd/node.rs:38-126
 //   runtime::{to_cuda, to_host, set_grad, read_grad, zero_grad, synchronize}
 //                                        src/cuda/runtime.rs:39-124
-//   graph::{matmul, bmm, add, transpose, scale, softmax, relu}
+//   graph::{matmul, bmm, add, transpose, scale, softmax, relu, slice_cols,
+//          concat_cols, scaled_softmax}
 //                                        src/cuda/graph/*.rs
-//   nn::{conv2d, Linear, attention, attention_batch}
+//   nn::{conv2d, Linear, attention, attention_batch, layernorm}
 //                                        src/cuda/nn/{conv,linear,attention}.rs
 // Rc<RefCell<Node>> becomes std::shared_ptr<Node>; a panic ("cuda matmul: lhs
 // not on GPU") becomes a thrown neuralrs::Panic with the same message. Like
@@ -124,6 +125,13 @@ NodeRef scale(const NodeRef& a, float s);
 NodeRef softmax(const NodeRef& a);
 // src/cuda/graph/relu.rs:30-80.
 NodeRef relu(const NodeRef& a);
+// src/cuda/graph/slice_cols.rs:37-86: columns [col_start, col_end) of the last dim.
+NodeRef slice_cols(const NodeRef& a, size_t col_start, size_t col_end);
+// src/cuda/graph/concat_cols.rs:35-95: the parts side by side along the last dim.
+NodeRef concat_cols(const std::vector<NodeRef>& parts);
+// graph::scale then graph::softmax as one node (same values and gradients,
+// one pass each way), as attention applies them (src/cuda/nn/attention.rs:17-18).
+NodeRef scaled_softmax(const NodeRef& a, float s);
 }  // namespace graph
 
 namespace nn {
@@ -144,6 +152,9 @@ struct Linear {
 // src/cuda/nn/attention.rs:10-32: softmax(Q K^T / sqrt(d)) V.
 NodeRef attention(const NodeRef& q, const NodeRef& k, const NodeRef& v);
 NodeRef attention_batch(const NodeRef& q, const NodeRef& k, const NodeRef& v);
+// src/cuda/nn/normalization.rs:87-160: per-row layer norm over the last dim
+// with gamma/beta [features].
+NodeRef layernorm(const NodeRef& input, const NodeRef& gamma, const NodeRef& beta, float eps);
 }  // namespace nn
 
 }  // namespace hip

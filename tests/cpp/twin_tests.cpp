@@ -41,6 +41,14 @@ void orc_softmax_forward(const float*, float*, int64_t, int64_t);
 void orc_softmax_backward(const float*, const float*, float*, int64_t, int64_t);
 void orc_relu_forward(const float*, float*, int64_t);
 void orc_relu_backward(const float*, const float*, float*, int64_t);
+void orc_slice_cols(const float*, float*, int64_t, int64_t, int64_t, int64_t);
+void orc_slice_cols_backward(const float*, float*, int64_t, int64_t, int64_t, int64_t);
+void orc_concat_part(const float*, float*, int64_t, int64_t, int64_t, int64_t);
+void orc_concat_part_backward(const float*, float*, int64_t, int64_t, int64_t, int64_t);
+void orc_layernorm_forward(const float*, const float*, const float*, float*, float*, float*,
+                           int64_t, int64_t, float);
+void orc_layernorm_backward(const float*, const float*, const float*, const float*, float*,
+                            float*, float*, int64_t, int64_t);
 }
 
 using namespace neuralrs;
@@ -427,6 +435,74 @@ struct Case {
     void (*fn)();
 };
 
+// tests/cuda_manip_test.rs:49-61
+void cuda_slice_cols() {
+    const size_t rows = 4, total = 6, cs = 2, ce = 5, sw = ce - cs;
+    const Vec input = formula(rows * total, 13, 0.1f, -0.6f);
+    const Vec seed = formula(rows * sw, 5, 0.1f, 0.3f);
+    Vec cf(rows * sw), cg(rows * total, 0.0f);
+    orc_slice_cols(input.data(), cf.data(), rows, total, cs, ce);
+    orc_slice_cols_backward(seed.data(), cg.data(), rows, total, cs, ce);
+    NodeRef x = resident(input, {rows, total});
+    NodeRef out = hip::graph::slice_cols(x, cs, ce);
+    const Vec gf = gpu::to_host(out);
+    gpu::set_grad(out, seed);
+    backward_graph(out);
+    close(gf, cf, 1e-5f, "slice_cols fwd");
+    close(gpu::read_grad(x), cg, 1e-5f, "slice_cols grad");
+}
+
+// tests/cuda_manip_test.rs:105-141
+void cuda_concat_cols() {
+    const size_t rows = 4, w[3] = {2, 3, 1}, total = 6;
+    const Vec p[3] = {formula(rows * w[0], 7, 0.1f, -0.3f), formula(rows * w[1], 9, 0.1f, -0.4f),
+                      formula(rows * w[2], 5, 0.1f, -0.2f)};
+    const Vec seed = formula(rows * total, 6, 0.1f, 0.2f);
+    Vec cf(rows * total), cg[3];
+    size_t off = 0;
+    for (int i = 0; i < 3; ++i) {
+        orc_concat_part(p[i].data(), cf.data(), rows, total, off, w[i]);
+        cg[i].assign(rows * w[i], 0.0f);
+        orc_concat_part_backward(seed.data(), cg[i].data(), rows, total, off, w[i]);
+        off += w[i];
+    }
+    std::vector<NodeRef> parts;
+    for (int i = 0; i < 3; ++i) parts.push_back(resident(p[i], {rows, w[i]}));
+    NodeRef out = hip::graph::concat_cols(parts);
+    const Vec gf = gpu::to_host(out);
+    gpu::set_grad(out, seed);
+    backward_graph(out);
+    close(gf, cf, 1e-5f, "concat fwd");
+    for (int i = 0; i < 3; ++i)
+        close(gpu::read_grad(parts[i]), cg[i], 1e-5f, "concat grad" + std::to_string(i));
+}
+
+// tests/cuda_layers_test.rs:18-62
+void cuda_layernorm() {
+    const size_t rows = 4, F = 6;
+    const float eps = 1e-5f;
+    const Vec input = formula(rows * F, 13, 0.2f, -1.0f);
+    const Vec gamma = formula(F, 3, 0.3f, 0.5f);
+    const Vec beta = formula(F, 4, 0.1f, -0.2f);
+    const Vec seed = formula(rows * F, 7, 0.1f, 0.2f);
+    Vec cf(rows * F), xn(rows * F), istd(rows), cdin(rows * F, 0.0f), cdg(F, 0.0f), cdb(F, 0.0f);
+    orc_layernorm_forward(input.data(), gamma.data(), beta.data(), cf.data(), xn.data(),
+                          istd.data(), rows, F, eps);
+    orc_layernorm_backward(seed.data(), gamma.data(), xn.data(), istd.data(), cdin.data(),
+                           cdg.data(), cdb.data(), rows, F);
+    NodeRef gx = resident(input, {rows, F});
+    NodeRef gg = resident(gamma, {F});
+    NodeRef gb = resident(beta, {F});
+    NodeRef out = hip::nn::layernorm(gx, gg, gb, eps);
+    const Vec gf = gpu::to_host(out);
+    gpu::set_grad(out, seed);
+    backward_graph(out);
+    close(gf, cf, 1e-4f, "layernorm fwd");
+    close(gpu::read_grad(gx), cdin, 1e-4f, "layernorm dinput");
+    close(gpu::read_grad(gg), cdg, 1e-4f, "layernorm dgamma");
+    close(gpu::read_grad(gb), cdb, 1e-4f, "layernorm dbeta");
+}
+
 const Case kCases[] = {
     {"cuda_resident_matmul_backward", cuda_resident_matmul_backward},
     {"cuda_resident_linear_chain", cuda_resident_linear_chain},
@@ -444,6 +520,9 @@ const Case kCases[] = {
     {"cfg2_mlp_step", cfg2_mlp_step},
     {"cfg3_conv2_layer", cfg3_conv2_layer},
     {"cfg4_attention_heads", cfg4_attention_heads},
+    {"cuda_slice_cols", cuda_slice_cols},
+    {"cuda_concat_cols", cuda_concat_cols},
+    {"cuda_layernorm", cuda_layernorm},
 };
 
 int main(int argc, char** argv) {
