@@ -373,6 +373,21 @@ NodeRef scaled_softmax(const NodeRef& a, float s) {
     return node;
 }
 
+NodeRef reshape(const NodeRef& a, std::vector<size_t> shape) {
+    GpuBuffers& ag = gpu_of(a, "cuda reshape: input not on GPU");
+    const size_t len = product(a->shape);
+    if (product(shape) != len) throw Panic("cuda reshape: element count mismatched");
+    DeviceBuffer out(len, false);
+    check(nrs_memcpy_dtod(out.ptr(), ag.data.ptr(), len * sizeof(float)),
+          "cuda reshape: launch failed");
+    NodeRef node = make_output(std::move(shape), {a}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, a, len](const std::vector<float>&) {
+        check(nrs_accumulate(gpu_of(a, "backward: parent not on GPU").grad->ptr(), grad->ptr(), len),
+              "accumulate launch failed");
+    };
+    return node;
+}
+
 }  // namespace graph
 
 // ---------------------------------------------------------------------- nn
@@ -462,6 +477,39 @@ NodeRef attention_batch(const NodeRef& q, const NodeRef& k, const NodeRef& v) {
     NodeRef scores = graph::bmm(q, kt);
     NodeRef weights = graph::scaled_softmax(scores, s);  // scale + softmax, one node
     return graph::bmm(weights, v);
+}
+
+NodeRef MultiHeadAttention::forward_batch(const NodeRef& x) const {
+    if (x->shape.size() != 3) throw Panic("multihead: x must be [batch, seq, d_model]");
+    const size_t batch = x->shape[0], seq = x->shape[1], d = x->shape[2];
+    if (num_heads == 0 || d_model % num_heads != 0) throw Panic("multihead: d_model % heads != 0");
+    auto proj = [&](const NodeRef& in, const NodeRef& w) {
+        NodeRef flat = graph::reshape(in, {batch * seq, d});
+        return graph::reshape(graph::matmul(flat, w), {batch, seq, d});
+    };
+    NodeRef q = proj(x, w_q), k = proj(x, w_k), v = proj(x, w_v);
+    const size_t d_head = d_model / num_heads;
+    std::vector<NodeRef> heads;
+    for (size_t h = 0; h < num_heads; ++h) {
+        const size_t start = h * d_head, end = start + d_head;
+        heads.push_back(attention_batch(graph::slice_cols(q, start, end),
+                                        graph::slice_cols(k, start, end),
+                                        graph::slice_cols(v, start, end)));
+    }
+    NodeRef concat = graph::concat_cols(heads);
+    NodeRef flat = graph::reshape(concat, {batch * seq, d});
+    return graph::reshape(graph::matmul(flat, w_o), {batch, seq, d});
+}
+
+NodeRef TransformerBlock::forward(const NodeRef& x) const {
+    if (x->shape.size() != 3) throw Panic("transformer block: x must be [batch, seq, d_model]");
+    const size_t batch = x->shape[0], seq = x->shape[1], d = x->shape[2];
+    NodeRef attn_out = mha.forward_batch(x);
+    NodeRef x1 = norm1.forward(graph::add(x, attn_out));
+    NodeRef flat = graph::reshape(x1, {batch * seq, d});
+    NodeRef h = graph::relu(ff1.forward(flat));
+    NodeRef ff_out = graph::reshape(ff2.forward(h), {batch, seq, d});
+    return norm2.forward(graph::add(x1, ff_out));
 }
 
 NodeRef layernorm(const NodeRef& input, const NodeRef& gamma, const NodeRef& beta, float eps) {

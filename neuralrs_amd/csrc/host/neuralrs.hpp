@@ -132,6 +132,9 @@ NodeRef concat_cols(const std::vector<NodeRef>& parts);
 // graph::scale then graph::softmax as one node (same values and gradients,
 // one pass each way), as attention applies them (src/cuda/nn/attention.rs:17-18).
 NodeRef scaled_softmax(const NodeRef& a, float s);
+// src/cuda/graph/reshape.rs:31-70: the same values in a new shape (copied into
+// a new buffer, as the reference does; the gradient is accumulated back).
+NodeRef reshape(const NodeRef& a, std::vector<size_t> shape);
 }  // namespace graph
 
 namespace nn {
@@ -155,6 +158,35 @@ NodeRef attention_batch(const NodeRef& q, const NodeRef& k, const NodeRef& v);
 // src/cuda/nn/normalization.rs:87-160: per-row layer norm over the last dim
 // with gamma/beta [features].
 NodeRef layernorm(const NodeRef& input, const NodeRef& gamma, const NodeRef& beta, float eps);
+
+// src/cuda/nn/normalization.rs (LayerNorm): resident gamma/beta [features].
+struct LayerNorm {
+    NodeRef gamma, beta;
+    float eps;
+    LayerNorm(NodeRef g, NodeRef b, float e) : gamma(std::move(g)), beta(std::move(b)), eps(e) {}
+    NodeRef forward(const NodeRef& x) const { return layernorm(x, gamma, beta, eps); }
+};
+
+// src/cuda/nn/multihead.rs:10-85: projections w_* [d_model, d_model], heads
+// sliced from the projected columns, attention_batch per head, concat, w_o.
+struct MultiHeadAttention {
+    NodeRef w_q, w_k, w_v, w_o;
+    size_t d_model, num_heads;
+    MultiHeadAttention(NodeRef q, NodeRef k, NodeRef v, NodeRef o, size_t d, size_t heads)
+        : w_q(std::move(q)), w_k(std::move(k)), w_v(std::move(v)), w_o(std::move(o)),
+          d_model(d), num_heads(heads) {}
+    NodeRef forward_batch(const NodeRef& x) const;  // [batch, seq, d_model]
+};
+
+// src/cuda/nn/transformer_block.rs:9-45: post-norm block, x + MHA(x) -> norm1
+// -> x1 + ff2(relu(ff1(x1))) -> norm2.
+struct TransformerBlock {
+    MultiHeadAttention mha;
+    LayerNorm norm1, norm2;
+    Linear ff1, ff2;
+    size_t d_model, d_ff;
+    NodeRef forward(const NodeRef& x) const;  // [batch, seq, d_model]
+};
 }  // namespace nn
 
 }  // namespace hip

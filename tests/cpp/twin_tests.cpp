@@ -503,6 +503,139 @@ void cuda_layernorm() {
     close(gpu::read_grad(gb), cdb, 1e-4f, "layernorm dbeta");
 }
 
+// CPU TransformerBlock (src/nn/transformer_block.rs, multihead.rs, attention.rs,
+// normalization.rs) composed from the oracle's CPU ops, forward and backward.
+struct CpuTransformer {
+    Vec out, dx, dwq, dwk, dwv, dwo, dg1, db1, dg2, db2, df1w, df1b, df2w, df2b;
+    CpuTransformer(const Vec& x, const Vec& wq, const Vec& wk, const Vec& wv, const Vec& wo,
+                   const Vec& g1, const Vec& b1, const Vec& g2, const Vec& b2, const Vec& f1w,
+                   const Vec& f1b, const Vec& f2w, const Vec& f2b, const Vec& seed, size_t B,
+                   size_t S, size_t D, size_t H, size_t Fd, float eps) {
+        const size_t R = B * S, dh = D / H;
+        const float s = 1.0f / std::sqrt(static_cast<float>(dh));
+        Vec q(R * D), k(R * D), v(R * D);
+        orc_graph_matmul_forward(x.data(), wq.data(), q.data(), R, D, D);
+        orc_graph_matmul_forward(x.data(), wk.data(), k.data(), R, D, D);
+        orc_graph_matmul_forward(x.data(), wv.data(), v.data(), R, D, D);
+        std::vector<Vec> qh(H, Vec(R * dh)), kh(H, Vec(R * dh)), vh(H, Vec(R * dh)),
+            kt(H, Vec(R * dh)), w(H, Vec(B * S * S)), oh(H, Vec(R * dh));
+        Vec concat(R * D);
+        for (size_t h = 0; h < H; ++h) {
+            orc_slice_cols(q.data(), qh[h].data(), R, D, h * dh, (h + 1) * dh);
+            orc_slice_cols(k.data(), kh[h].data(), R, D, h * dh, (h + 1) * dh);
+            orc_slice_cols(v.data(), vh[h].data(), R, D, h * dh, (h + 1) * dh);
+            Vec scores(B * S * S), scaled(B * S * S);
+            orc_transpose(kh[h].data(), kt[h].data(), B, S, dh);
+            orc_graph_bmm_forward(qh[h].data(), kt[h].data(), scores.data(), B, S, dh, S);
+            orc_scale(scores.data(), scaled.data(), s, B * S * S);
+            orc_softmax_forward(scaled.data(), w[h].data(), B * S, S);
+            orc_graph_bmm_forward(w[h].data(), vh[h].data(), oh[h].data(), B, S, S, dh);
+            orc_concat_part(oh[h].data(), concat.data(), R, D, h * dh, dh);
+        }
+        Vec ao(R * D), x1a(R * D), x1(R * D), xn1(R * D), is1(R);
+        orc_graph_matmul_forward(concat.data(), wo.data(), ao.data(), R, D, D);
+        for (size_t i = 0; i < R * D; ++i) x1a[i] = x[i] + ao[i];
+        orc_layernorm_forward(x1a.data(), g1.data(), b1.data(), x1.data(), xn1.data(), is1.data(),
+                              R, D, eps);
+        Vec h1p(R * Fd), h1(R * Fd), hr(R * Fd), f2p(R * D), f(R * D), x2(R * D), xn2(R * D), is2(R);
+        orc_graph_matmul_forward(x1.data(), f1w.data(), h1p.data(), R, D, Fd);
+        orc_graph_add_bias_forward(h1p.data(), f1b.data(), h1.data(), R, Fd);
+        orc_relu_forward(h1.data(), hr.data(), R * Fd);
+        orc_graph_matmul_forward(hr.data(), f2w.data(), f2p.data(), R, Fd, D);
+        orc_graph_add_bias_forward(f2p.data(), f2b.data(), f.data(), R, D);
+        for (size_t i = 0; i < R * D; ++i) x2[i] = x1[i] + f[i];
+        out.assign(R * D, 0.0f);
+        orc_layernorm_forward(x2.data(), g2.data(), b2.data(), out.data(), xn2.data(), is2.data(),
+                              R, D, eps);
+        // backward
+        auto z = [](size_t n) { return Vec(n, 0.0f); };
+        dx = z(R * D); dwq = z(D * D); dwk = z(D * D); dwv = z(D * D); dwo = z(D * D);
+        dg1 = z(D); db1 = z(D); dg2 = z(D); db2 = z(D);
+        df1w = z(D * Fd); df1b = z(Fd); df2w = z(Fd * D); df2b = z(D);
+        Vec dx2 = z(R * D);
+        orc_layernorm_backward(seed.data(), g2.data(), xn2.data(), is2.data(), dx2.data(),
+                               dg2.data(), db2.data(), R, D);
+        Vec dx1 = dx2, df2p = z(R * D), dhr = z(R * Fd), dh1 = z(R * Fd), dh1p = z(R * Fd);
+        orc_graph_add_bias_backward(dx2.data(), df2p.data(), df2b.data(), R, D);
+        orc_graph_matmul_backward(hr.data(), f2w.data(), df2p.data(), dhr.data(), df2w.data(), R,
+                                  Fd, D);
+        orc_relu_backward(h1.data(), dhr.data(), dh1.data(), R * Fd);
+        orc_graph_add_bias_backward(dh1.data(), dh1p.data(), df1b.data(), R, Fd);
+        orc_graph_matmul_backward(x1.data(), f1w.data(), dh1p.data(), dx1.data(), df1w.data(), R,
+                                  D, Fd);
+        Vec dx1a = z(R * D);
+        orc_layernorm_backward(dx1.data(), g1.data(), xn1.data(), is1.data(), dx1a.data(),
+                               dg1.data(), db1.data(), R, D);
+        for (size_t i = 0; i < R * D; ++i) dx[i] += dx1a[i];
+        Vec dconcat = z(R * D), dq = z(R * D), dk = z(R * D), dv = z(R * D);
+        orc_graph_matmul_backward(concat.data(), wo.data(), dx1a.data(), dconcat.data(),
+                                  dwo.data(), R, D, D);
+        for (size_t h = 0; h < H; ++h) {
+            Vec doh = z(R * dh), dw = z(B * S * S), dvh = z(R * dh), dsc = z(B * S * S),
+                dscores = z(B * S * S), dqh = z(R * dh), dkt = z(R * dh), dkh = z(R * dh);
+            orc_concat_part_backward(dconcat.data(), doh.data(), R, D, h * dh, dh);
+            orc_graph_bmm_backward(w[h].data(), vh[h].data(), doh.data(), dw.data(), dvh.data(), B,
+                                   S, S, dh);
+            orc_softmax_backward(w[h].data(), dw.data(), dsc.data(), B * S, S);
+            orc_scale_backward(dsc.data(), dscores.data(), s, B * S * S);
+            orc_graph_bmm_backward(qh[h].data(), kt[h].data(), dscores.data(), dqh.data(),
+                                   dkt.data(), B, S, dh, S);
+            orc_transpose_backward(dkt.data(), dkh.data(), B, S, dh);
+            orc_slice_cols_backward(dqh.data(), dq.data(), R, D, h * dh, (h + 1) * dh);
+            orc_slice_cols_backward(dkh.data(), dk.data(), R, D, h * dh, (h + 1) * dh);
+            orc_slice_cols_backward(dvh.data(), dv.data(), R, D, h * dh, (h + 1) * dh);
+        }
+        orc_graph_matmul_backward(x.data(), wq.data(), dq.data(), dx.data(), dwq.data(), R, D, D);
+        orc_graph_matmul_backward(x.data(), wk.data(), dk.data(), dx.data(), dwk.data(), R, D, D);
+        orc_graph_matmul_backward(x.data(), wv.data(), dv.data(), dx.data(), dwv.data(), R, D, D);
+    }
+};
+
+// tests/cuda_transformer_test.rs:17-89: the whole block, output, input
+// gradient and all twelve parameter gradients, tol 3e-3.
+void cuda_transformer_block() {
+    const size_t B = 2, S = 3, D = 6, H = 2, Fd = 12;
+    const float eps = 1e-5f;
+    auto mk = [](size_t n, size_t shift) {
+        Vec v(n);
+        for (size_t i = 0; i < n; ++i)
+            v[i] = static_cast<float>(static_cast<int>((i + shift) % 13)) * 0.1f - 0.6f;
+        return v;
+    };
+    const Vec wq = mk(D * D, 1), wk = mk(D * D, 2), wv = mk(D * D, 3), wo = mk(D * D, 4);
+    const Vec g1 = mk(D, 5), b1 = mk(D, 6), g2 = mk(D, 7), b2 = mk(D, 8);
+    const Vec f1w = mk(D * Fd, 9), f1b = mk(Fd, 10), f2w = mk(Fd * D, 11), f2b = mk(D, 12);
+    const Vec x = mk(B * S * D, 20), seed = mk(B * S * D, 30);
+    CpuTransformer c(x, wq, wk, wv, wo, g1, b1, g2, b2, f1w, f1b, f2w, f2b, seed, B, S, D, H, Fd,
+                     eps);
+    NodeRef gwq = resident(wq, {D, D}), gwk = resident(wk, {D, D}), gwv = resident(wv, {D, D}),
+            gwo = resident(wo, {D, D});
+    NodeRef gg1 = resident(g1, {D}), gb1 = resident(b1, {D}), gg2 = resident(g2, {D}),
+            gb2 = resident(b2, {D});
+    NodeRef gf1w = resident(f1w, {D, Fd}), gf1b = resident(f1b, {Fd}),
+            gf2w = resident(f2w, {Fd, D}), gf2b = resident(f2b, {D});
+    hip::nn::TransformerBlock tb{hip::nn::MultiHeadAttention(gwq, gwk, gwv, gwo, D, H),
+                                 hip::nn::LayerNorm(gg1, gb1, eps),
+                                 hip::nn::LayerNorm(gg2, gb2, eps),
+                                 hip::nn::Linear(gf1w, gf1b),
+                                 hip::nn::Linear(gf2w, gf2b),
+                                 D, Fd};
+    NodeRef gx = resident(x, {B, S, D});
+    NodeRef out = tb.forward(gx);
+    const Vec gf = gpu::to_host(out);
+    gpu::set_grad(out, seed);
+    backward_graph(out);
+    close(gf, c.out, 3e-3f, "transformer fwd");
+    const NodeRef params[12] = {gwq, gwk, gwv, gwo, gg1, gb1, gg2, gb2, gf1w, gf1b, gf2w, gf2b};
+    const Vec* want[12] = {&c.dwq, &c.dwk, &c.dwv, &c.dwo, &c.dg1, &c.db1,
+                           &c.dg2, &c.db2, &c.df1w, &c.df1b, &c.df2w, &c.df2b};
+    const char* names[12] = {"w_q", "w_k", "w_v", "w_o", "norm1.gamma", "norm1.beta",
+                             "norm2.gamma", "norm2.beta", "ff1.w", "ff1.b", "ff2.w", "ff2.b"};
+    for (int j = 0; j < 12; ++j)
+        close(gpu::read_grad(params[j]), *want[j], 3e-3f, std::string("transformer d") + names[j]);
+    close(gpu::read_grad(gx), c.dx, 3e-3f, "transformer dx");
+}
+
 const Case kCases[] = {
     {"cuda_resident_matmul_backward", cuda_resident_matmul_backward},
     {"cuda_resident_linear_chain", cuda_resident_linear_chain},
@@ -523,6 +656,7 @@ const Case kCases[] = {
     {"cuda_slice_cols", cuda_slice_cols},
     {"cuda_concat_cols", cuda_concat_cols},
     {"cuda_layernorm", cuda_layernorm},
+    {"cuda_transformer_block", cuda_transformer_block},
 };
 
 int main(int argc, char** argv) {
