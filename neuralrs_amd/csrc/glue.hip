@@ -339,8 +339,9 @@ __global__ __launch_bounds__(256) void layernorm_dx_kernel(
 
 // LayerNorm parameter gradients over rows (normalization.rs:41-56 ln_reduce
 // runs one thread per feature over every row). Block (x, c) sums rows
-// [c*kLnRows, (c+1)*kLnRows) of grad * x_norm and grad for 256 features into
-// partial[c], issuing 8 rows' loads before adding any. The combine kernel
+// [c*rc, (c+1)*rc) of grad * x_norm and grad for 256 features into
+// partial[c], issuing 8 rows' loads before adding any (rc: kLnRows, or a
+// larger multiple of 8 when the rows would need more than 65535 chunks). The combine kernel
 // splits the chunks into kLnGroups contiguous ranges summed in parallel
 // (ascending inside a range) and adds the ranges in order, so the result is
 // deterministic.
@@ -348,12 +349,12 @@ constexpr int kLnRows = 32, kLnGroups = 16;
 
 __global__ __launch_bounds__(256) void layernorm_param_partial_kernel(
     float* __restrict__ part_g, float* __restrict__ part_b, const float* __restrict__ grad,
-    const float* __restrict__ x_norm, int64_t rows, int64_t F) {
+    const float* __restrict__ x_norm, int64_t rows, int64_t F, int64_t rc) {
     const int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (f >= F) return;
-    const int64_t r0 = (int64_t)blockIdx.y * kLnRows;
+    const int64_t r0 = (int64_t)blockIdx.y * rc;
     float dg = 0.0f, db = 0.0f;
-    for (int b = 0; b < kLnRows; b += 8) {
+    for (int64_t b = 0; b < rc; b += 8) {
         float gv[8], xv[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -616,14 +617,16 @@ int nrs_layernorm_backward(float* dinput, float* dgamma, float* dbeta, const flo
         NRS_LAUNCH_CHECK("layernorm backward (input)");
     }
     if (dgamma || dbeta) {
-        const int64_t chunks = (rows + nrs::kLnRows - 1) / nrs::kLnRows;
+        int64_t rc = nrs::kLnRows;
+        if ((rows + rc - 1) / rc > 65535) rc = ((rows + 65534) / 65535 + 7) / 8 * 8;
+        const int64_t chunks = (rows + rc - 1) / rc;
         const int64_t fb = (F + 255) / 256, fb64 = (F + 63) / 64;
         NRS_ARG_CHECK(fb64 <= INT32_MAX && chunks <= 65535, "layernorm backward: too large");
         float* part = nrs::workspace(sizeof(float) * 2 * (size_t)(chunks * F), 0);
         if (!part) return NRS_ERR_ALLOC;
         hipLaunchKernelGGL(nrs::layernorm_param_partial_kernel, dim3((unsigned)fb, (unsigned)chunks),
                            dim3(256), 0, nrs::stream(), part, part + chunks * F, grad, x_norm, rows,
-                           F);
+                           F, rc);
         NRS_LAUNCH_CHECK("layernorm backward (parameter partials)");
         hipLaunchKernelGGL(nrs::layernorm_param_combine_kernel, dim3((unsigned)fb64),
                            dim3(64 * nrs::kLnGroups), 0, nrs::stream(), dgamma, dbeta, part,
