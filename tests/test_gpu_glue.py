@@ -278,3 +278,24 @@ def test_layernorm_vs_oracle(hip, orc, rows, F):
     hip.call("nrs_layernorm_backward", None, d2.ptr, None, dev(hip, gr).ptr, None, xn.ptr, None,
              rows, F, 0.0)
     assert np.max(np.abs(d2.to_host() - (rg - acc_g))) < tol_p
+
+
+def test_layernorm_param_sums_past_two_million_rows(hip):
+    """More rows than 65535 chunks of 32: the chunk height grows. Integer
+    gradients make dbeta an exact sum, so a chunk skipped or counted twice
+    shows; dgamma is checked against f64."""
+    rng = np.random.default_rng(5)
+    rows, F = 2_100_000, 2
+    x = rng.standard_normal(rows * F).astype(np.float32)
+    g = int_matrix(rng, (rows * F,), -3, 3)
+    ones, zeros = np.ones(F, np.float32), np.zeros(F, np.float32)
+    out, xn, istd = hip.DeviceBuffer(rows * F), hip.DeviceBuffer(rows * F), hip.DeviceBuffer(rows)
+    hip.call("nrs_layernorm_forward", out.ptr, xn.ptr, istd.ptr, dev(hip, x).ptr, dev(hip, ones).ptr,
+             dev(hip, zeros).ptr, rows, F, 1e-5)
+    dg, db = hip.DeviceBuffer(F), hip.DeviceBuffer(F)
+    hip.call("nrs_layernorm_backward", None, dg.ptr, db.ptr, dev(hip, g).ptr, None, xn.ptr, None,
+             rows, F, 0.0)
+    g2 = g.reshape(rows, F).astype(np.float64)
+    assert np.array_equal(db.to_host(), g2.sum(axis=0).astype(np.float32))
+    want = (g2 * xn.to_host().reshape(rows, F).astype(np.float64)).sum(axis=0)
+    assert np.max(np.abs(dg.to_host() - want)) < 1e-6 * np.abs(g2).sum(axis=0).max()
