@@ -607,9 +607,19 @@ int nrs_layernorm_backward(float* dinput, float* dgamma, float* dbeta, const flo
                            int64_t rows, int64_t features, float acc) {
     NRS_REQUIRE_INIT();
     NRS_ARG_CHECK(rows >= 0 && features > 0, "layernorm backward: bad shape");
-    if (rows == 0) return NRS_OK;
-    NRS_ARG_CHECK(grad && x_norm, "layernorm backward: null pointer");
     const int64_t F = features;
+    if (rows == 0) {
+        // no rows: the parameter gradients are the empty sums, 0 + acc * old
+        if (dgamma || dbeta) {
+            NRS_ARG_CHECK((F + 63) / 64 <= INT32_MAX, "layernorm backward: too large");
+            hipLaunchKernelGGL(nrs::layernorm_param_combine_kernel, dim3((unsigned)((F + 63) / 64)),
+                               dim3(64 * nrs::kLnGroups), 0, nrs::stream(), dgamma, dbeta,
+                               nullptr, nullptr, int64_t(0), F, acc);
+            NRS_LAUNCH_CHECK("layernorm backward (parameters)");
+        }
+        return NRS_OK;
+    }
+    NRS_ARG_CHECK(grad && x_norm, "layernorm backward: null pointer");
     if (dinput) {
         NRS_ARG_CHECK(gamma && inv_std, "layernorm backward: null gamma or inv_std");
         hipLaunchKernelGGL(nrs::layernorm_dx_kernel, dim3(nrs::rows_grid(rows)), dim3(256), 0,

@@ -169,9 +169,10 @@ int nrs_shutdown(void) {
 }
 
 int nrs_set_stream(void* stream) {
-    // idle cached blocks may still be read by the old stream's queued work,
-    // which a new stream would not be ordered after
-    if (static_cast<hipStream_t>(stream) != g.stream && nrs::cache.idle_bytes)
+    // Work queued on the old stream may still read or write library scratch,
+    // cached blocks and buffers freed since; work on the new stream is not
+    // ordered after it. Drain the old stream before switching.
+    if (static_cast<hipStream_t>(stream) != g.stream && g.init)
         NRS_HIP_CHECK(hipStreamSynchronize(g.stream));
     g.stream = static_cast<hipStream_t>(stream);
     return NRS_OK;

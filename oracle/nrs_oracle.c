@@ -111,37 +111,66 @@ EXPORT void orc_matmul_naive(const float *A, const float *B, float *C,
 
 /* ------------------------------------------------------------------------ */
 /* src/autograd/graph/matmul.rs:17-24  forward: data[i,j] += a[i,t]*b[t,j],  */
-/* t ascending, starting from 0.0.                                           */
+/* t ascending, starting from 0.0. Every output keeps exactly that sequence  */
+/* of roundings; only the loop nest is reordered (a row of accumulators,     */
+/* j innermost), so the bits equal the reference's i-j-t nest while the      */
+/* loop runs at cache speed at the TransformerBlock sizes.                   */
 /* ------------------------------------------------------------------------ */
 EXPORT void orc_graph_matmul_forward(const float *A, const float *B, float *C,
                                      int64_t m, int64_t k, int64_t n) {
-    orc_matmul_naive(A, B, C, m, k, n);
+    for (int64_t i = 0; i < m; ++i) {
+        float *acc = C + i * n;
+        for (int64_t j = 0; j < n; ++j) acc[j] = 0.0f;
+        for (int64_t t = 0; t < k; ++t) {
+            const float a = A[i * k + t];
+            const float *brow = B + t * n;
+            for (int64_t j = 0; j < n; ++j) {
+                float p = a * brow[j];
+                acc[j] = acc[j] + p;
+            }
+        }
+    }
 }
 
 /* src/autograd/graph/matmul.rs:37-63  backward, accumulating into dA, dB:   */
 /*   dA[i,t] += sum_j g[i,j]*b[t,j]  (j ascending, partial sum from 0.0)     */
 /*   dB[t,j] += sum_i a[i,t]*g[i,j]  (i ascending)                          */
+/* Each partial sum sees the reference's terms in the reference's order; the */
+/* nests are reordered so the independent sums advance together (dA over t  */
+/* against a transposed copy of b, dB over whole rows), bits unchanged.     */
 EXPORT void orc_graph_matmul_backward(const float *A, const float *B, const float *G,
                                       float *dA, float *dB,
                                       int64_t m, int64_t k, int64_t n) {
+    float *bt = (float *)malloc(sizeof(float) * (size_t)(k * n > 0 ? k * n : 1));
+    float *acc = (float *)malloc(sizeof(float) * (size_t)(k * n > k ? k * n : (k > 0 ? k : 1)));
+    for (int64_t t = 0; t < k; ++t)
+        for (int64_t j = 0; j < n; ++j) bt[j * k + t] = B[t * n + j];
+    for (int64_t i = 0; i < m; ++i) {
+        for (int64_t t = 0; t < k; ++t) acc[t] = 0.0f;
+        for (int64_t j = 0; j < n; ++j) {
+            const float g = G[i * n + j];
+            const float *bcol = bt + j * k;
+            for (int64_t t = 0; t < k; ++t) {
+                float p = g * bcol[t];
+                acc[t] = acc[t] + p;
+            }
+        }
+        for (int64_t t = 0; t < k; ++t) dA[i * k + t] = dA[i * k + t] + acc[t];
+    }
+    for (int64_t e = 0; e < k * n; ++e) acc[e] = 0.0f;
     for (int64_t i = 0; i < m; ++i)
         for (int64_t t = 0; t < k; ++t) {
-            float g = 0.0f;
+            const float a = A[i * k + t];
+            const float *grow = G + i * n;
+            float *arow = acc + t * n;
             for (int64_t j = 0; j < n; ++j) {
-                float p = G[i * n + j] * B[t * n + j];
-                g = g + p;
+                float p = a * grow[j];
+                arow[j] = arow[j] + p;
             }
-            dA[i * k + t] = dA[i * k + t] + g;
         }
-    for (int64_t t = 0; t < k; ++t)
-        for (int64_t j = 0; j < n; ++j) {
-            float g = 0.0f;
-            for (int64_t i = 0; i < m; ++i) {
-                float p = A[i * k + t] * G[i * n + j];
-                g = g + p;
-            }
-            dB[t * n + j] = dB[t * n + j] + g;
-        }
+    for (int64_t e = 0; e < k * n; ++e) dB[e] = dB[e] + acc[e];
+    free(acc);
+    free(bt);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -47,6 +47,11 @@ SHAPES = [  # (rows, cols, inner)
     (2048, 2048, 40), (4096, 1024, 72), (2000, 2048, 36),  # large outputs (the last ragged M)
     (2000, 2100, 1100),  # 64x128 tiles (two per CU, K >= 1024), ragged edges
     (30, 8200, 1024),    # at most 32 rows: 32x256 tiles over K slices, ragged M and N
+    # cfg4 Linear GEMMs (TransformerBlock, B32 S128 d256 dff1024): Q/K/V/O
+    # projections and the two FFN layers forward (NN) and their input
+    # gradients (NT); the weight gradients over K = 4096 rows (TN, split-K)
+    (4096, 256, 256), (4096, 1024, 256), (4096, 256, 1024),
+    (256, 256, 4096), (256, 1024, 4096), (1024, 256, 4096),
 ]
 
 
@@ -63,7 +68,10 @@ def test_gemm_exact_integers(hip, layout, shape):
 
 @pytest.mark.parametrize("layout", [NN, NT, TN])
 @pytest.mark.parametrize("shape", [(40, 32, 56), (300, 300, 300), (512, 512, 512),
-                                   (256, 128, 784), (1024, 1024, 1024), (32, 2048, 2048)],
+                                   (256, 128, 784), (1024, 1024, 1024), (32, 2048, 2048),
+                                   # cfg4 Linear GEMMs and weight gradients
+                                   (4096, 256, 256), (4096, 1024, 256), (4096, 256, 1024),
+                                   (256, 256, 4096), (256, 1024, 4096), (1024, 256, 4096)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_gemm_f64_tolerance(hip, orc, layout, shape):
     rows, cols, inner = shape
@@ -90,14 +98,16 @@ def test_gemm_cfg1_512_vs_cpu_simd(hip, orc):
     assert rel_err(c, cpu.astype(np.float64), ab) <= 2 * gemm_tol(512)
 
 
-@pytest.mark.parametrize("n", [2048, 4096])
+@pytest.mark.parametrize("n", [2048, 4096, 8192])
 def test_gemm_large_square_sampled_rows(hip, orc, n):
-    """cfg5 squares: f64 check on a sample of rows (every tile row touched)."""
+    """cfg5 squares: f64 check on a sample of rows (every 256-row tile row
+    touched, and the last 40 rows)."""
     rng = np.random.default_rng(n)
     a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
     b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
     c = run_gemm(hip, NN, a, b, n, n, n)
-    rows = np.unique(np.concatenate([np.arange(0, n, 61), np.arange(n - 40, n)]))
+    step = 61 if n <= 4096 else 127
+    rows = np.unique(np.concatenate([np.arange(0, n, step), np.arange(n - 40, n)]))
     c64, ab = orc.gemm_f64("nn", a, b, n, n, n, rowidx=rows)
     assert rel_err(c[rows], c64, ab) <= gemm_tol(n)
 

@@ -299,3 +299,20 @@ def test_layernorm_param_sums_past_two_million_rows(hip):
     assert np.array_equal(db.to_host(), g2.sum(axis=0).astype(np.float32))
     want = (g2 * xn.to_host().reshape(rows, F).astype(np.float64)).sum(axis=0)
     assert np.max(np.abs(dg.to_host() - want)) < 1e-6 * np.abs(g2).sum(axis=0).max()
+
+
+def test_layernorm_backward_zero_rows(hip):
+    """No rows: dgamma and dbeta are the empty sums plus acc * old, as the
+    reference's ln_reduce gives; 0 when overwriting (acc 0), old values kept
+    when accumulating (acc 1). The input gradient has nothing to write."""
+    F = 70
+    old_g = np.arange(F, dtype=np.float32) - 5
+    old_b = np.full(F, np.nan, np.float32)  # never read when overwriting
+    dg, db = dev(hip, old_g), dev(hip, old_b)
+    hip.call("nrs_layernorm_backward", None, dg.ptr, db.ptr, None, None, None, None, 0, F, 0.0)
+    assert np.array_equal(dg.to_host(), np.zeros(F, np.float32))
+    assert np.array_equal(db.to_host(), np.zeros(F, np.float32))
+    dg2, db2 = dev(hip, old_g), dev(hip, old_g * 2)
+    hip.call("nrs_layernorm_backward", None, dg2.ptr, db2.ptr, None, None, None, None, 0, F, 1.0)
+    assert np.array_equal(dg2.to_host(), old_g)
+    assert np.array_equal(db2.to_host(), old_g * 2)

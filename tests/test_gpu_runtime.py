@@ -76,3 +76,69 @@ def test_reused_block_is_ordered_after_queued_reads(hip):
     assert z.ptr == old                        # the same block, reused
     assert np.array_equal(y.to_host(), np.full(n, 6.0, np.float32))
     assert np.array_equal(z.to_host(), np.full(n, -1.0, np.float32))
+
+
+def _hip_runtime():
+    """The HIP runtime libnrs_hip.so is linked against (already mapped into
+    this process once the library is loaded)."""
+    with open("/proc/self/maps") as f:
+        paths = {ln.split()[-1] for ln in f if "libamdhip64.so" in ln}
+    assert paths, "libamdhip64 is not loaded"
+    return ctypes.CDLL(sorted(paths)[0])
+
+
+def _hip_stream():
+    """A new HIP stream at the default priority, as an integer handle."""
+    s = ctypes.c_void_p()
+    assert _hip_runtime().hipStreamCreate(ctypes.byref(s)) == 0
+    return s.value
+
+
+def _int_host(rng, shape, lo=-3, hi=3):
+    return rng.integers(lo, hi + 1, size=shape).astype(np.float32)
+
+
+def test_stream_switch_orders_reuse_after_old_stream(hip):
+    """nrs_set_stream drains the old stream: a block freed while a long GEMM
+    on stream A still reads it, re-allocated and overwritten on stream B,
+    and split-K GEMMs on either stream (sharing, and growing, the library's
+    partials scratch) all give the results of serial execution."""
+    rng = np.random.default_rng(17)
+    n = 4096
+    xa, xb = _int_host(rng, (n, n)), _int_host(rng, (n, n))
+    want = (xa.astype(np.float64) @ xb.astype(np.float64)).astype(np.float32)
+    sa, sb = _hip_stream(), _hip_stream()
+    prev = hip.load().nrs_get_stream()
+    try:
+        dx, dy = hip.DeviceBuffer.from_host(xa), hip.DeviceBuffer.from_host(xb)
+        dc = hip.DeviceBuffer(n * n)
+        hip.call("nrs_set_stream", sa)
+        hip.gemm(hip.NN, dc, dx, dy, n, n, n)       # ~1 ms reading dx on stream A
+        hip.call("nrs_set_stream", sb)
+        old = dx.ptr
+        dx.free()
+        dz = hip.DeviceBuffer(n * n)
+        assert dz.ptr == old                         # the same block, on stream B
+        ones = np.full(n * n, -1.0, np.float32)
+        hip.call("nrs_memcpy_htod", dz.ptr, ones.ctypes.data, ones.nbytes)
+        hip.sync()
+        assert np.array_equal(dc.to_host((n, n)), want)
+
+        # split-K partials: a small plan on A, then a larger one on B (scratch grows)
+        shapes = ((32, 9, 100352), (64, 576, 100352))
+        outs = []
+        for shape, s in zip(shapes, (sa, sb)):
+            rows, cols, inner = shape
+            a, b = _int_host(rng, (rows, inner), -2, 2), _int_host(rng, (cols, inner), -2, 2)
+            hip.call("nrs_set_stream", s)
+            da, db = hip.DeviceBuffer.from_host(a), hip.DeviceBuffer.from_host(b)
+            c = hip.DeviceBuffer(rows * cols)
+            hip.gemm_nt_splitk(c, da, db, rows, cols, inner, 0.0)
+            outs.append((c, da, db, (a.astype(np.float64) @ b.astype(np.float64).T)))
+        hip.sync()
+        for (c, _, _, w), (rows, cols, _) in zip(outs, shapes):
+            assert np.array_equal(c.to_host((rows, cols)), w.astype(np.float32))
+    finally:
+        hip.call("nrs_set_stream", prev)
+        for s in (sa, sb):
+            _hip_runtime().hipStreamDestroy(ctypes.c_void_p(s))

@@ -129,6 +129,55 @@ def test_graph_matmul_backward_exact_and_gradcheck(orc):
     assert np.array_equal(db, db0 + (ai.T @ gi).astype(np.float32))
 
 
+def _literal_graph_matmul(a, b, g, da0, db0):
+    """The reference's loops of src/autograd/graph/matmul.rs:17-63 verbatim in
+    numpy float32 scalars (every product and sum rounded to f32, no fused
+    multiply-add): forward data[i,j] += a[i,t]*b[t,j] over t; dA[i,t] +=
+    sum_j g[i,j]*b[t,j]; dB[t,j] += sum_i a[i,t]*g[i,j]."""
+    f = np.float32
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.zeros((m, n), np.float32)
+    for i in range(m):
+        for j in range(n):
+            s = f(0)
+            for t in range(k):
+                s = f(s + f(a[i, t] * b[t, j]))
+            c[i, j] = s
+    da, db = da0.copy(), db0.copy()
+    for i in range(m):
+        for t in range(k):
+            s = f(0)
+            for j in range(n):
+                s = f(s + f(g[i, j] * b[t, j]))
+            da[i, t] = f(da[i, t] + s)
+    for t in range(k):
+        for j in range(n):
+            s = f(0)
+            for i in range(m):
+                s = f(s + f(a[i, t] * g[i, j]))
+            db[t, j] = f(db[t, j] + s)
+    return c, da, db
+
+
+@pytest.mark.parametrize("m,k,n", [(7, 13, 5), (12, 9, 17), (1, 1, 1)])
+def test_graph_matmul_loop_order_is_bit_exact(orc, m, k, n):
+    """The oracle runs the reference's loops with reordered nests; on random
+    (non-integer) data its bits equal the literal loops', so each output's
+    sequence of roundings is the reference's."""
+    rng = np.random.default_rng(m * 31 + k * 7 + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    g = rng.standard_normal((m, n)).astype(np.float32)
+    da0 = rng.standard_normal((m, k)).astype(np.float32)
+    db0 = rng.standard_normal((k, n)).astype(np.float32)
+    c_ref, da_ref, db_ref = _literal_graph_matmul(a, b, g, da0, db0)
+    assert np.array_equal(orc.graph_matmul_forward(a, b), c_ref)
+    da, db = orc.graph_matmul_backward(a, b, g, da0, db0)
+    assert np.array_equal(da, da_ref)
+    assert np.array_equal(db, db_ref)
+
+
 # ---------------------------------------------------------------- bmm
 def test_bmm_known_answer_and_gradcheck(orc):
     c = K["bmm_forward"]
