@@ -106,6 +106,19 @@ int nrs_gemm(int layout, float *C, const float *A, const float *B,
 int nrs_gemm_nt_splitk(float *C, const float *A, const float *B,
                        int64_t rows, int64_t cols, int64_t inner, float beta);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): nrs_gemm_nt_splitk with the same plan, kernels and bits,
+ * but its split-K partials go to a fixed 14 MiB per-GPU array compiled into
+ * the library (its device address looked up once per device by nrs_init), so
+ * the call allocates nothing. A plan whose partials (slices * rows * cols *
+ * 4 bytes) exceed 14 MiB is rejected with NRS_ERR_ARG; every plan of the
+ * convolution weight-gradient shapes fits (at most 12.7 MB at 64 x 576 over
+ * 100352). All calls on one GPU share the array: calls that overlap on one
+ * GPU (several streams or threads) race and must be serialised by the caller. */
+int nrs_gemm_nt_splitk_noalloc(float *C, const float *A, const float *B,
+                               int64_t rows, int64_t cols, int64_t inner, float beta);
+
 /* ------------------------------------------------------------------- bmm */
 /* bmm_forward / bmm_grad_a / bmm_grad_b (src/cuda/graph/bmm.rs:12-56), per
  * batch item b with the GEMM layouts above and contiguous items:

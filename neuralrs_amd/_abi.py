@@ -39,6 +39,7 @@ SIGNATURES = {
     "nrs_sync": [],
     "nrs_gemm": [ctypes.c_int, _P, _P, _P, _I, _I, _I, _F, _P, ctypes.c_int],
     "nrs_gemm_nt_splitk": [_P, _P, _P, _I, _I, _I, _F],
+    "nrs_gemm_nt_splitk_noalloc": [_P, _P, _P, _I, _I, _I, _F],
     "nrs_bmm": [ctypes.c_int, _P, _P, _P, _I, _I, _I, _I, _F],
     "nrs_bmm_backward": [ctypes.c_int, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F],
     "nrs_im2col": [_P, _P] + [_I] * 8,

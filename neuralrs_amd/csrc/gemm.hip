@@ -258,8 +258,18 @@ int gemm_run(const GemmCall& c) {
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)pl.slices, (unsigned)batch);
     if (pl.slices > 1) {
         NRS_ARG_CHECK(batch == 1, "gemm: split-K with batch > 1 unsupported");
-        float* ws = workspace(sizeof(float) * (size_t)pl.slices * (size_t)M * (size_t)N, 0);
-        if (!ws) return NRS_ERR_ALLOC;
+        const size_t need = sizeof(float) * (size_t)pl.slices * (size_t)M * (size_t)N;
+        float* ws;
+        if (c.partial_buf) {
+            NRS_ARG_CHECK(need <= c.partial_cap,
+                          "gemm: split-K partials of %zu bytes (%d slices of %lld x %lld) exceed "
+                          "the %zu-byte scratch of the no-allocation entry point",
+                          need, pl.slices, (long long)M, (long long)N, c.partial_cap);
+            ws = c.partial_buf;
+        } else {
+            ws = workspace(need, 0);
+            if (!ws) return NRS_ERR_ALLOC;
+        }
         p.partial = ws;
         hipLaunchKernelGGL(fn, grid, dim3(s.threads), 0, stream(), p);
         NRS_LAUNCH_CHECK("gemm (split-K partials)");
@@ -333,6 +343,26 @@ int nrs_gemm_nt_splitk(float* C, const float* A, const float* B, int64_t rows, i
     c.N = cols;
     c.K = inner;
     c.beta = beta;
+    return nrs::gemm_run(c);
+}
+
+int nrs_gemm_nt_splitk_noalloc(float* C, const float* A, const float* B, int64_t rows,
+                               int64_t cols, int64_t inner, float beta) {
+    NRS_REQUIRE_INIT();
+    float* scratch = nrs::noalloc_scratch();
+    NRS_ARG_CHECK(scratch != nullptr, "nrs_gemm_nt_splitk_noalloc: scratch of device %d not set up",
+                  nrs::device());
+    nrs::GemmCall c;
+    c.layout = NRS_NT;
+    c.C = C;
+    c.A = A;
+    c.B = B;
+    c.M = rows;
+    c.N = cols;
+    c.K = inner;
+    c.beta = beta;
+    c.partial_buf = scratch;  // every partial is written before it is read: no clearing
+    c.partial_cap = nrs::kNoAllocScratchBytes;
     return nrs::gemm_run(c);
 }
 

@@ -46,6 +46,11 @@ struct GemmCall {
     int amode = OP_DENSE, bmode = OP_DENSE;
     ConvGeom cg{};
     int64_t gather_bytes = 0;  // bytes of the gathered (non-dense) operand's tensor
+    // Caller-provided split-K partials buffer (no allocation): used instead of
+    // the library's scratch slot when set; a plan whose partials exceed
+    // partial_cap bytes is rejected.
+    float* partial_buf = nullptr;
+    size_t partial_cap = 0;
 };
 
 int gemm_run(const GemmCall& c);

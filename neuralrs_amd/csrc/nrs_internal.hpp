@@ -28,6 +28,12 @@ int set_error(int code, const char* fmt, ...);
 // Returns nullptr (and records an error) when the allocation fails.
 float* workspace(size_t bytes, int slot = 0);
 
+// Scratch of the no-allocation entry points: a file-scope device array of
+// kNoAllocScratchBytes per GPU, its address looked up by nrs_init. Returns
+// nullptr before nrs_init has run on the current device.
+constexpr size_t kNoAllocScratchBytes = size_t(14) << 20;
+float* noalloc_scratch();
+
 // Zero-fills device memory on the library stream with a kernel.
 int zero_fill(void* ptr, size_t bytes);
 

@@ -14,6 +14,14 @@ namespace {
 
 constexpr int kSlots = 5;
 
+// Scratch of the no-allocation entry points: one per GPU, held until the
+// process ends. In host code `scratch` names a host-side stand-in, so it is
+// never passed to a kernel or copy; its device address is looked up once per
+// device in nrs_init (hipGetSymbolAddress) and handed out by noalloc_scratch().
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+float* g_scratch_ptr[kMaxDevices] = {};
+
 struct State {
     bool init = false;
     int device = 0;
@@ -94,6 +102,10 @@ int num_cus() {
 int device() { return g.device; }
 bool initialized() { return g.init; }
 
+float* noalloc_scratch() {
+    return g.device >= 0 && g.device < kMaxDevices ? g_scratch_ptr[g.device] : nullptr;
+}
+
 int set_error(int code, const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
@@ -150,7 +162,17 @@ int nrs_init(int device) {
     NRS_HIP_CHECK(hipGetDeviceCount(&count));
     NRS_ARG_CHECK(device >= 0 && device < count, "nrs_init: device %d out of range (count %d)",
                   device, count);
+    NRS_ARG_CHECK(device < nrs::kMaxDevices, "nrs_init: device %d beyond the %d supported",
+                  device, nrs::kMaxDevices);
     NRS_HIP_CHECK(hipSetDevice(device));
+    if (!nrs::g_scratch_ptr[device]) {
+        // this device's copy of the no-allocation scratch (a symbol lookup,
+        // not an allocation), with the device current
+        void* ptr = nullptr;
+        NRS_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(nrs::scratch)));
+        NRS_ARG_CHECK(ptr != nullptr, "nrs_init: no device address for the scratch array");
+        nrs::g_scratch_ptr[device] = static_cast<float*>(ptr);
+    }
     g.device = device;
     g.init = true;
     return NRS_OK;
