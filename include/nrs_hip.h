@@ -145,6 +145,37 @@ int nrs_bmm_backward(int layout, float *dA, float *dB, const float *G, const flo
                      const float *B, int64_t batch, int64_t m, int64_t k, int64_t n,
                      float beta);
 
+/* ------------------------------------------------- fused attention core */
+/* attention_batch (src/cuda/nn/attention.rs:23-32: bmm(q, transpose(k)),
+ * scale, softmax, bmm with v) for every head of MultiHeadAttention::
+ * forward_batch (src/cuda/nn/multihead.rs:57-85) in one launch, reading and
+ * writing the heads in place: q, k, v and out are row-major [batch*seq, ld]
+ * with head h in columns [h*d_head, (h+1)*d_head), so the per-head
+ * slice_cols / concat_cols copies (multihead.rs:43-52,72-81) disappear; with
+ * heads = 1 and ld = d_head it is attention_batch on [batch, seq, d_head].
+ *   out = softmax(scale * q . k^T) . v   per (batch item, head);
+ *   stats [batch*heads*seq*2] receives, per query row, the softmax in base 2:
+ *   max_j u_j and sum_j 2^(u_j - max) with u = scale * log2(e) * q . k^T; the
+ *   backward recomputes the probabilities from them (the S x S matrix is
+ *   never stored).
+ * The fused path takes seq <= 128 and d_head 16 or 32
+ * (nrs_attention_supported); other shapes are refused with NRS_ERR_ARG and
+ * the caller composes bmm / softmax / bmm instead.                          */
+int nrs_attention_supported(int64_t batch, int64_t heads, int64_t seq, int64_t d_head, int64_t ld);
+int nrs_attention_forward(float *out, float *stats, const float *q, const float *k, const float *v,
+                          int64_t batch, int64_t heads, int64_t seq, int64_t d_head, int64_t ld,
+                          float scale);
+/* Its backward (the closures of bmm.rs:93-131, softmax.rs:23-35 and
+ * scale.rs:10-20 in the order attention composes them), from the forward's
+ * stats: dq = dS . k, dk = dS^T . q, dv = P^T . dout with P recomputed and
+ * dS = (P * (dP - rowsum(P * dP))) * scale, dP = dout . v^T; each gradient
+ * = computed + beta * old (beta = 1 is accumulate_into). Same layouts as the
+ * forward; dq, dk, dv must not overlap each other or the inputs.            */
+int nrs_attention_backward(float *dq, float *dk, float *dv, const float *dout, const float *q,
+                           const float *k, const float *v, const float *stats, int64_t batch,
+                           int64_t heads, int64_t seq, int64_t d_head, int64_t ld, float scale,
+                           float beta);
+
 /* ---------------------------------------------------------------- conv2d */
 /* The five primitive launches of src/cuda/nn/conv.rs:161-236, same index
  * semantics (columns grouped by sample: col = ni*out_h*out_w + p).           */

@@ -42,6 +42,28 @@ NodeRef make_output(std::vector<size_t> shape, std::vector<NodeRef> parents, Dev
     return out;
 }
 
+// The backward closure of a bmm node (bmm.rs:93-131): both gradients
+// accumulated (beta 1) into the parents, in one launch for small items. When
+// a and b are the same node the two gradients go to one buffer, one product
+// after the other.
+void bmm_backward_into(int layout, const NodeRef& a, const NodeRef& b, const float* g,
+                       size_t batch, size_t m, size_t k, size_t n, const char* what) {
+    GpuBuffers& ag = gpu_of(a, "backward: lhs not on GPU");
+    GpuBuffers& bg = gpu_of(b, "backward: rhs not on GPU");
+    if (ag.grad != bg.grad) {
+        check(nrs_bmm_backward(layout, ag.grad->ptr(), bg.grad->ptr(), g, ag.data.ptr(),
+                               bg.data.ptr(), batch, m, k, n, 1.0f),
+              what);
+        return;
+    }
+    check(nrs_bmm_backward(layout, ag.grad->ptr(), nullptr, g, ag.data.ptr(), bg.data.ptr(), batch,
+                           m, k, n, 1.0f),
+          what);
+    check(nrs_bmm_backward(layout, nullptr, bg.grad->ptr(), g, ag.data.ptr(), bg.data.ptr(), batch,
+                           m, k, n, 1.0f),
+          what);
+}
+
 void build_topo(const NodeRef& n, std::unordered_set<const Node*>& visited,
                 std::vector<NodeRef>& topo) {
     if (!visited.insert(n.get()).second) return;
@@ -187,14 +209,7 @@ NodeRef bmm(const NodeRef& a, const NodeRef& b) {
           "cuda bmm: launch failed");
     NodeRef node = make_output({batch, m, n}, {a, b}, std::move(out));
     node->backward_fn = [grad = node->gpu->grad, a, b, batch, m, k, n](const std::vector<float>&) {
-        GpuBuffers& ag = gpu_of(a, "cuda bmm bwd: lhs not on GPU");
-        GpuBuffers& bg = gpu_of(b, "cuda bmm bwd: rhs not on GPU");
-        // bmm_grad_a: da[b] += g[b] . B[b]^T   (bmm.rs:27-41, 95-105)
-        check(nrs_bmm(NRS_NT, ag.grad->ptr(), grad->ptr(), bg.data.ptr(), batch, m, k, n, 1.0f),
-              "cuda bmm bwd: grad_a launch");
-        // bmm_grad_b: db[b] += A[b]^T . g[b]   (bmm.rs:42-56, 109-119)
-        check(nrs_bmm(NRS_TN, bg.grad->ptr(), ag.data.ptr(), grad->ptr(), batch, k, n, m, 1.0f),
-              "cuda bmm bwd: grad_b launch");
+        bmm_backward_into(NRS_NN, a, b, grad->ptr(), batch, m, k, n, "cuda bmm bwd");
     };
     return node;
 }
@@ -461,44 +476,171 @@ NodeRef Linear::forward(const NodeRef& input) const {
     return node;
 }
 
+namespace {
+
+// q . k^T per item without materialising k^T: [b, m, d] x [b, n, d] -> [b, m, n]
+// (or 2-D [m, d] x [n, d] -> [m, n]): the bmm(q, transpose(k)) / matmul(q,
+// transpose(k)) of attention.rs:15,28 as one NT product. Its backward is the
+// bmm closure for that layout: dq += g . k, dk += g^T . q.
+NodeRef bmm_nt(const NodeRef& q, const NodeRef& k) {
+    GpuBuffers& qg = gpu_of(q, "cuda bmm: lhs not on GPU");
+    GpuBuffers& kg = gpu_of(k, "cuda bmm: rhs not on GPU");
+    const bool two_d = q->shape.size() == 2;
+    if (q->shape.size() != k->shape.size() || (!two_d && q->shape.size() != 3))
+        throw Panic("cuda bmm: operands must be 3-D");
+    const size_t batch = two_d ? 1 : q->shape[0];
+    const size_t m = q->shape[two_d ? 0 : 1], d = q->shape.back(), n = k->shape[two_d ? 0 : 1];
+    if (k->shape.back() != d || (!two_d && k->shape[0] != batch))
+        throw Panic("cuda bmm: shape mismatch");
+    DeviceBuffer out(batch * m * n, false);
+    check(nrs_bmm(NRS_NT, out.ptr(), qg.data.ptr(), kg.data.ptr(), batch, m, n, d, 0.0f),
+          "cuda bmm: launch failed");
+    std::vector<size_t> shape = two_d ? std::vector<size_t>{m, n} : std::vector<size_t>{batch, m, n};
+    NodeRef node = make_output(std::move(shape), {q, k}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, q, k, batch, m, d, n](const std::vector<float>&) {
+        bmm_backward_into(NRS_NT, q, k, grad->ptr(), batch, m, d, n, "cuda bmm bwd");
+    };
+    return node;
+}
+
+// [rows, heads * w] -> [heads, rows, w] (given `shape`, e.g. [heads * batch,
+// seq, w]): the per-head slice_cols of MultiHeadAttention (multihead.rs:72-78)
+// in one launch; its backward is merge_heads accumulating into x's gradient.
+NodeRef split_heads(const NodeRef& x, size_t rows, size_t heads, size_t w,
+                    std::vector<size_t> shape) {
+    GpuBuffers& xg = gpu_of(x, "cuda slice_cols: input not on GPU");
+    DeviceBuffer out(rows * heads * w, false);
+    check(nrs_split_heads(out.ptr(), xg.data.ptr(), rows, heads, w, 0.0f),
+          "cuda slice_cols: launch failed");
+    NodeRef node = make_output(std::move(shape), {x}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, x, rows, heads, w](const std::vector<float>&) {
+        check(nrs_merge_heads(gpu_of(x, "backward: parent not on GPU").grad->ptr(), grad->ptr(),
+                              rows, heads, w, 1.0f),
+              "cuda slice_cols bwd: launch");
+    };
+    return node;
+}
+
+// [heads, rows, w] -> [rows, heads * w]: the concat_cols of the heads
+// (multihead.rs:81) in one launch; its backward is split_heads accumulating.
+NodeRef merge_heads(const NodeRef& x, size_t rows, size_t heads, size_t w,
+                    std::vector<size_t> shape) {
+    GpuBuffers& xg = gpu_of(x, "cuda concat_cols: part not on GPU");
+    DeviceBuffer out(rows * heads * w, false);
+    check(nrs_merge_heads(out.ptr(), xg.data.ptr(), rows, heads, w, 0.0f),
+          "cuda concat_cols: write launch failed");
+    NodeRef node = make_output(std::move(shape), {x}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, x, rows, heads, w](const std::vector<float>&) {
+        check(nrs_split_heads(gpu_of(x, "backward: part not on GPU").grad->ptr(), grad->ptr(), rows,
+                              heads, w, 1.0f),
+              "cuda concat_cols bwd: launch");
+    };
+    return node;
+}
+
+// softmax(scale * q . k^T) . v for every (item, head) in one node: q, k, v
+// and the output are [batch * seq, ld] rows (any leading shape of that many
+// elements) with head h in columns [h*dh, (h+1)*dh). Same values as
+// attention_batch per head (attention.rs:23-32); the scores stay on chip and
+// the backward recomputes them from the saved softmax statistics.
+NodeRef fused_attention(const NodeRef& q, const NodeRef& k, const NodeRef& v, size_t batch,
+                        size_t heads, size_t seq, size_t dh, size_t ld, float scale) {
+    GpuBuffers& qg = gpu_of(q, "attention: q not on GPU");
+    GpuBuffers& kg = gpu_of(k, "attention: k not on GPU");
+    GpuBuffers& vg = gpu_of(v, "attention: v not on GPU");
+    const size_t len = product(q->shape);
+    DeviceBuffer out(len, false);
+    auto stats = std::make_shared<DeviceBuffer>(batch * heads * seq * 2, false);
+    check(nrs_attention_forward(out.ptr(), stats->ptr(), qg.data.ptr(), kg.data.ptr(),
+                                vg.data.ptr(), batch, heads, seq, dh, ld, scale),
+          "attention: launch failed");
+    NodeRef node = make_output(q->shape, {q, k, v}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, q, k, v, stats, len, batch, heads, seq, dh, ld,
+                         scale](const std::vector<float>&) {
+        GpuBuffers& qg = gpu_of(q, "attention bwd: q not on GPU");
+        GpuBuffers& kg = gpu_of(k, "attention bwd: k not on GPU");
+        GpuBuffers& vg = gpu_of(v, "attention bwd: v not on GPU");
+        if (qg.grad != kg.grad && kg.grad != vg.grad && qg.grad != vg.grad) {
+            check(nrs_attention_backward(qg.grad->ptr(), kg.grad->ptr(), vg.grad->ptr(),
+                                         grad->ptr(), qg.data.ptr(), kg.data.ptr(), vg.data.ptr(),
+                                         stats->ptr(), batch, heads, seq, dh, ld, scale, 1.0f),
+                  "attention bwd: launch");
+            return;
+        }
+        // q, k or v are one node: the gradients go to temporaries, then add up
+        DeviceBuffer tq(len, true), tk(len, true), tv(len, true);
+        check(nrs_attention_backward(tq.ptr(), tk.ptr(), tv.ptr(), grad->ptr(), qg.data.ptr(),
+                                     kg.data.ptr(), vg.data.ptr(), stats->ptr(), batch, heads, seq,
+                                     dh, ld, scale, 0.0f),
+              "attention bwd: launch");
+        check(nrs_accumulate(qg.grad->ptr(), tq.ptr(), len), "accumulate launch failed");
+        check(nrs_accumulate(kg.grad->ptr(), tk.ptr(), len), "accumulate launch failed");
+        check(nrs_accumulate(vg.grad->ptr(), tv.ptr(), len), "accumulate launch failed");
+    };
+    return node;
+}
+
+}  // namespace
+
 NodeRef attention(const NodeRef& q, const NodeRef& k, const NodeRef& v) {
     if (q->shape.size() != 2) throw Panic("attention: q must be [seq, d]");
-    const float s = 1.0f / std::sqrt(static_cast<float>(q->shape[1]));
-    NodeRef kt = graph::transpose(k);
-    NodeRef scores = graph::matmul(q, kt);
-    NodeRef weights = graph::scaled_softmax(scores, s);  // scale + softmax, one node
+    const size_t seq = q->shape[0], d = q->shape[1];
+    const float s = 1.0f / std::sqrt(static_cast<float>(d));
+    if (k->shape == q->shape && v->shape == q->shape && nrs_attention_supported(1, 1, seq, d, d))
+        return fused_attention(q, k, v, 1, 1, seq, d, d, s);
+    // the composition of attention.rs:15-19 with q . k^T as one NT product and
+    // scale + softmax as one node
+    NodeRef weights = graph::scaled_softmax(bmm_nt(q, k), s);
     return graph::matmul(weights, v);
 }
 
 NodeRef attention_batch(const NodeRef& q, const NodeRef& k, const NodeRef& v) {
     if (q->shape.size() != 3) throw Panic("attention_batch: q must be [batch, seq, d]");
-    const float s = 1.0f / std::sqrt(static_cast<float>(q->shape[2]));
-    NodeRef kt = graph::transpose(k);
-    NodeRef scores = graph::bmm(q, kt);
-    NodeRef weights = graph::scaled_softmax(scores, s);  // scale + softmax, one node
+    const size_t batch = q->shape[0], seq = q->shape[1], d = q->shape[2];
+    const float s = 1.0f / std::sqrt(static_cast<float>(d));
+    if (k->shape == q->shape && v->shape == q->shape &&
+        nrs_attention_supported(batch, 1, seq, d, d))
+        return fused_attention(q, k, v, batch, 1, seq, d, d, s);
+    NodeRef weights = graph::scaled_softmax(bmm_nt(q, k), s);  // attention.rs:28-30
     return graph::bmm(weights, v);
+}
+
+// Shared by forward (batch 1) and forward_batch: the projections of the
+// flattened input, every head's attention at once, the output projection.
+static NodeRef multihead(const MultiHeadAttention& mha, const NodeRef& flat, size_t batch,
+                         size_t seq, size_t d) {
+    if (mha.num_heads == 0 || mha.d_model % mha.num_heads != 0)
+        throw Panic("multihead: d_model % heads != 0");
+    const size_t heads = mha.num_heads, dh = mha.d_model / heads, rows = batch * seq;
+    if (heads * dh != d) throw Panic("multihead: input width is not d_model");
+    NodeRef q = graph::matmul(flat, mha.w_q), k = graph::matmul(flat, mha.w_k),
+            v = graph::matmul(flat, mha.w_v);
+    NodeRef concat;
+    if (nrs_attention_supported(batch, heads, seq, dh, d)) {
+        // heads read and written in place in the [rows, d_model] projections
+        concat = fused_attention(q, k, v, batch, heads, seq, dh, d,
+                                 1.0f / std::sqrt(static_cast<float>(dh)));
+    } else {
+        // the heads as one batch of heads * batch items, one attention_batch
+        const std::vector<size_t> hs{heads * batch, seq, dh};
+        NodeRef att = attention_batch(split_heads(q, rows, heads, dh, hs),
+                                      split_heads(k, rows, heads, dh, hs),
+                                      split_heads(v, rows, heads, dh, hs));
+        concat = merge_heads(att, rows, heads, dh, {rows, d});
+    }
+    return graph::matmul(concat, mha.w_o);
+}
+
+NodeRef MultiHeadAttention::forward(const NodeRef& x) const {
+    if (x->shape.size() != 2) throw Panic("multihead: x must be [seq, d_model]");
+    return multihead(*this, x, 1, x->shape[0], x->shape[1]);
 }
 
 NodeRef MultiHeadAttention::forward_batch(const NodeRef& x) const {
     if (x->shape.size() != 3) throw Panic("multihead: x must be [batch, seq, d_model]");
     const size_t batch = x->shape[0], seq = x->shape[1], d = x->shape[2];
-    if (num_heads == 0 || d_model % num_heads != 0) throw Panic("multihead: d_model % heads != 0");
-    auto proj = [&](const NodeRef& in, const NodeRef& w) {
-        NodeRef flat = graph::reshape(in, {batch * seq, d});
-        return graph::reshape(graph::matmul(flat, w), {batch, seq, d});
-    };
-    NodeRef q = proj(x, w_q), k = proj(x, w_k), v = proj(x, w_v);
-    const size_t d_head = d_model / num_heads;
-    std::vector<NodeRef> heads;
-    for (size_t h = 0; h < num_heads; ++h) {
-        const size_t start = h * d_head, end = start + d_head;
-        heads.push_back(attention_batch(graph::slice_cols(q, start, end),
-                                        graph::slice_cols(k, start, end),
-                                        graph::slice_cols(v, start, end)));
-    }
-    NodeRef concat = graph::concat_cols(heads);
-    NodeRef flat = graph::reshape(concat, {batch * seq, d});
-    return graph::reshape(graph::matmul(flat, w_o), {batch, seq, d});
+    NodeRef out = multihead(*this, graph::reshape(x, {batch * seq, d}), batch, seq, d);
+    return graph::reshape(out, {batch, seq, d});
 }
 
 NodeRef TransformerBlock::forward(const NodeRef& x) const {

@@ -152,7 +152,9 @@ struct Linear {
     NodeRef forward(const NodeRef& input) const;  // [batch,in] -> [batch,out]
 };
 
-// src/cuda/nn/attention.rs:10-32: softmax(Q K^T / sqrt(d)) V.
+// src/cuda/nn/attention.rs:10-32: softmax(Q K^T / sqrt(d)) V. One fused node
+// (scores kept on chip) when q, k, v have one shape, seq <= 128 and d 16 or
+// 32; otherwise Q.K^T as one NT product, scale + softmax, and the last product.
 NodeRef attention(const NodeRef& q, const NodeRef& k, const NodeRef& v);
 NodeRef attention_batch(const NodeRef& q, const NodeRef& k, const NodeRef& v);
 // src/cuda/nn/normalization.rs:87-160: per-row layer norm over the last dim
@@ -167,14 +169,19 @@ struct LayerNorm {
     NodeRef forward(const NodeRef& x) const { return layernorm(x, gamma, beta, eps); }
 };
 
-// src/cuda/nn/multihead.rs:10-85: projections w_* [d_model, d_model], heads
-// sliced from the projected columns, attention_batch per head, concat, w_o.
+// src/cuda/nn/multihead.rs:10-85: projections w_* [d_model, d_model], every
+// head's attention, heads joined, w_o. The reference slices each head out of
+// the projections, runs attention per head and concatenates; here all heads
+// run in one fused attention node that reads and writes them in place (or,
+// for shapes outside the fused path, split/merge-heads nodes around one
+// attention_batch of heads * batch items). Same values and gradients.
 struct MultiHeadAttention {
     NodeRef w_q, w_k, w_v, w_o;
     size_t d_model, num_heads;
     MultiHeadAttention(NodeRef q, NodeRef k, NodeRef v, NodeRef o, size_t d, size_t heads)
         : w_q(std::move(q)), w_k(std::move(k)), w_v(std::move(v)), w_o(std::move(o)),
           d_model(d), num_heads(heads) {}
+    NodeRef forward(const NodeRef& x) const;        // [seq, d_model]
     NodeRef forward_batch(const NodeRef& x) const;  // [batch, seq, d_model]
 };
 

@@ -660,6 +660,112 @@ void cuda_transformer_block() {
     close(gpu::read_grad(gx), c.dx, 3e-3f, "transformer dx");
 }
 
+// CPU MultiHeadAttention::forward_batch (src/nn/multihead.rs composed from
+// the oracle's ops as the reference composes them): projections, per-head
+// slice_cols, attention, concat_cols, output projection; forward and backward.
+struct CpuMultiHead {
+    Vec out, dx, dwq, dwk, dwv, dwo;
+    CpuMultiHead(const Vec& x, const Vec& wq, const Vec& wk, const Vec& wv, const Vec& wo,
+                 const Vec& seed, size_t B, size_t S, size_t D, size_t H) {
+        const size_t R = B * S, dh = D / H;
+        Vec q(R * D), k(R * D), v(R * D), concat(R * D, 0.0f);
+        orc_graph_matmul_forward(x.data(), wq.data(), q.data(), R, D, D);
+        orc_graph_matmul_forward(x.data(), wk.data(), k.data(), R, D, D);
+        orc_graph_matmul_forward(x.data(), wv.data(), v.data(), R, D, D);
+        std::vector<Vec> qh(H, Vec(R * dh)), kh(H, Vec(R * dh)), vh(H, Vec(R * dh));
+        const Vec zero(R * dh, 0.0f);
+        for (size_t h = 0; h < H; ++h) {
+            orc_slice_cols(q.data(), qh[h].data(), R, D, h * dh, (h + 1) * dh);
+            orc_slice_cols(k.data(), kh[h].data(), R, D, h * dh, (h + 1) * dh);
+            orc_slice_cols(v.data(), vh[h].data(), R, D, h * dh, (h + 1) * dh);
+            CpuAttention a(qh[h], kh[h], vh[h], zero, B, S, dh);
+            orc_concat_part(a.out.data(), concat.data(), R, D, h * dh, dh);
+        }
+        out.assign(R * D, 0.0f);
+        orc_graph_matmul_forward(concat.data(), wo.data(), out.data(), R, D, D);
+        Vec dconcat(R * D, 0.0f), dq(R * D, 0.0f), dk(R * D, 0.0f), dv(R * D, 0.0f);
+        dwo.assign(D * D, 0.0f);
+        orc_graph_matmul_backward(concat.data(), wo.data(), seed.data(), dconcat.data(),
+                                  dwo.data(), R, D, D);
+        for (size_t h = 0; h < H; ++h) {
+            Vec doh(R * dh, 0.0f);
+            orc_concat_part_backward(dconcat.data(), doh.data(), R, D, h * dh, dh);
+            CpuAttention a(qh[h], kh[h], vh[h], doh, B, S, dh);
+            orc_slice_cols_backward(a.dq.data(), dq.data(), R, D, h * dh, (h + 1) * dh);
+            orc_slice_cols_backward(a.dk.data(), dk.data(), R, D, h * dh, (h + 1) * dh);
+            orc_slice_cols_backward(a.dv.data(), dv.data(), R, D, h * dh, (h + 1) * dh);
+        }
+        dx.assign(R * D, 0.0f);
+        dwq.assign(D * D, 0.0f);
+        dwk.assign(D * D, 0.0f);
+        dwv.assign(D * D, 0.0f);
+        orc_graph_matmul_backward(x.data(), wq.data(), dq.data(), dx.data(), dwq.data(), R, D, D);
+        orc_graph_matmul_backward(x.data(), wk.data(), dk.data(), dx.data(), dwk.data(), R, D, D);
+        orc_graph_matmul_backward(x.data(), wv.data(), dv.data(), dx.data(), dwv.data(), R, D, D);
+    }
+};
+
+// MultiHeadAttention through the operator surface against the CPU composition:
+// batched (x [B, S, D]) or single-sequence (x [S, D], B = 1).
+void mha_case(size_t B, size_t S, size_t D, size_t H, bool batched, float tol) {
+    const float a = std::sqrt(6.0f / static_cast<float>(2 * D));
+    const Vec wq = uniform(D * D, -a, a), wk = uniform(D * D, -a, a), wv = uniform(D * D, -a, a),
+              wo = uniform(D * D, -a, a);
+    const Vec x = normal(B * S * D, 1.0f), seed = normal(B * S * D, 1.0f);
+    CpuMultiHead c(x, wq, wk, wv, wo, seed, B, S, D, H);
+    NodeRef gwq = resident(wq, {D, D}), gwk = resident(wk, {D, D}), gwv = resident(wv, {D, D}),
+            gwo = resident(wo, {D, D});
+    hip::nn::MultiHeadAttention mha(gwq, gwk, gwv, gwo, D, H);
+    NodeRef gx = batched ? resident(x, {B, S, D}) : resident(x, {S, D});
+    NodeRef out = batched ? mha.forward_batch(gx) : mha.forward(gx);
+    close(gpu::to_host(out), c.out, tol, "mha fwd");
+    gpu::set_grad(out, seed);
+    backward_graph(out);
+    close(gpu::read_grad(gx), c.dx, tol, "mha dx");
+    close(gpu::read_grad(gwq), c.dwq, tol, "mha dw_q");
+    close(gpu::read_grad(gwk), c.dwk, tol, "mha dw_k");
+    close(gpu::read_grad(gwv), c.dwv, tol, "mha dw_v");
+    close(gpu::read_grad(gwo), c.dwo, tol, "mha dw_o");
+}
+
+// single sequence, d_head 16: the fused node with one batch item
+void mha_single_sequence_fused() {
+    reseed(51);
+    mha_case(1, 64, 64, 4, false, 1e-3f);
+}
+
+// d_head 8 (outside the fused path): split-heads, one attention_batch of
+// heads * batch items (Q.K^T as one NT product), merge-heads
+void mha_batch_split_heads() {
+    reseed(52);
+    mha_case(3, 20, 24, 3, true, 1e-3f);
+}
+
+// attention on [seq, d] through the fused node (batch 1, one head)
+void attention_fused_2d() {
+    reseed(53);
+    const size_t S = 50, D = 32, n = S * D;
+    attention_case(1, S, D, false, 1e-3f, normal(n, 1.0f), normal(n, 1.0f), normal(n, 1.0f),
+                   normal(n, 0.1f));
+}
+
+// self-attention with one node as q, k and v: the fused backward's three
+// gradients land in one buffer (through temporaries), dq + dk + dv
+void attention_batch_self() {
+    reseed(54);
+    const size_t B = 4, S = 40, D = 32, n = B * S * D;
+    const Vec x = normal(n, 1.0f), seed = normal(n, 0.1f);
+    CpuAttention cpu(x, x, x, seed, B, S, D);
+    NodeRef gx = resident(x, {B, S, D});
+    NodeRef out = hip::nn::attention_batch(gx, gx, gx);
+    close(gpu::to_host(out), cpu.out, 1e-3f, "self-attention fwd");
+    gpu::set_grad(out, seed);
+    backward_graph(out);
+    Vec want(n);
+    for (size_t i = 0; i < n; ++i) want[i] = cpu.dq[i] + cpu.dk[i] + cpu.dv[i];
+    close(gpu::read_grad(gx), want, 1e-3f, "self-attention dx");
+}
+
 // |gpu - cpu| <= abs_tol + rel * max|cpu| elementwise; prints the largest
 // error against the scale so the margin is on record.
 void close_scaled(const Vec& g, const Vec& c, float abs_tol, float rel, const std::string& what) {
@@ -760,6 +866,10 @@ const Case kCases[] = {
     {"cuda_layernorm", cuda_layernorm},
     {"cuda_transformer_block", cuda_transformer_block},
     {"cfg4_transformer_block", cfg4_transformer_block},
+    {"mha_single_sequence_fused", mha_single_sequence_fused},
+    {"mha_batch_split_heads", mha_batch_split_heads},
+    {"attention_fused_2d", attention_fused_2d},
+    {"attention_batch_self", attention_batch_self},
 };
 
 int main(int argc, char** argv) {
