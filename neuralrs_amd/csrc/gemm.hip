@@ -70,8 +70,13 @@ KernelFn pick_conv(int layout, int amode, int bmode, bool vec4) {
 //  * 32x128x32, 4 waves of 32x32, prefetch depth 2: convolutions whose GEMM
 //    has at most 32 rows (a 64-row tile would double the MFMA work);
 //  * 128x32x32, 4 waves of 32x32, prefetch depth 2: outputs with at most 32
-//    columns, e.g. attention's P.V and its input gradients (d_head 32).
-enum TileId { T256x256 = 0, T64x64, T32x256, T32x128, T128x32, T64x128, T_COUNT };
+//    columns, e.g. attention's P.V and its input gradients (d_head 32);
+//  * 64x64x32 with k-split wave sets (KS = 2: 8 waves, two per 32x32
+//    sub-block, each reducing half of every k-tile), prefetch depth 2: dense
+//    GEMMs with at most two 64x64 tiles per CU and no K split, which would
+//    otherwise run one wave per SIMD (cfg4 projections 4096x256x256:
+//    9.3 -> 8.7 us NT; FFN 4096x256x1024: 29.0 -> 25.1 us NN).
+enum TileId { T256x256 = 0, T64x64, T32x256, T32x128, T128x32, T64x128, T64x64S2, T_COUNT };
 const TileShape kShapes[T_COUNT] = {
     {256, 256, 32, 512},
     {64, 64, 32, 256},
@@ -79,6 +84,7 @@ const TileShape kShapes[T_COUNT] = {
     {32, 128, 32, 256},
     {128, 32, 32, 256},
     {64, 128, 32, 256},
+    {64, 64, 32, 512},
 };
 
 // `pf` is the register prefetch depth the plan asks for; tiles that have no
@@ -104,6 +110,13 @@ KernelFn kernel_for(int tile, int pf, int layout, bool vec4, int amode, int bmod
         case T128x32:
             return pf == 1 ? pick_layout<128, 32, 32, 4, 1, 1>(layout, vec4)
                            : pick_layout<128, 32, 32, 4, 1, 2>(layout, vec4);
+        case T64x64S2:  // planned only with 128-bit loads
+            if (!vec4) return nullptr;
+            switch (layout) {
+                case NRS_NN: return gemm_kernel<64, 64, 32, 2, 2, true, false, 4, 2, 2, OP_DENSE, OP_DENSE, 2>;
+                case NRS_NT: return gemm_kernel<64, 64, 32, 2, 2, true, true, 4, 2, 2, OP_DENSE, OP_DENSE, 2>;
+                default: return gemm_kernel<64, 64, 32, 2, 2, false, false, 4, 2, 2, OP_DENSE, OP_DENSE, 2>;
+            }
         default: return nullptr;
     }
 }
@@ -141,7 +154,7 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool d
             pl.tile = T128x32;
         else if (vec4 && tiles_of(T256x256) >= cus && fill(T256x256) >= 0.85)
             pl.tile = T256x256;
-        else if (vec4 && tiles_of(T64x128) >= 2 * cus && K >= 1024 && fill(T64x128) >= 0.85)
+        else if (vec4 && tiles_of(T64x128) >= 2 * cus && K >= 256 && fill(T64x128) >= 0.85)
             pl.tile = T64x128;
     } else if (M <= 32) {  // gathered (convolution) operands: 64x64 or 32x128
         pl.tile = T32x128;
@@ -151,7 +164,11 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool d
     int slices = 1;
     if (force_slices > 0) {
         slices = force_slices;
-    } else if (allow_split && batch == 1 && tiles < cus && (2 * tiles <= cus || K >= 2048)) {
+    } else if (allow_split && batch == 1 && tiles < cus && (2 * tiles <= cus || K >= 2048) &&
+               K >= 8 * s.bk) {
+        // (a K of fewer than 8 k-tiles is not split: the reduce launch
+        // costs more than the shorter k loop saves, e.g. 256x784 over
+        // K = 128: 12.7 us split in two, 6.1 us whole)
         // About three workgroups per CU (one for the 32x256 tile, whose
         // workgroups stream a whole K slice of B: 8 slices of the skinny
         // 32x8192x8192 GEMM measured 67.8 us against 72.4 us at 24), each
@@ -163,6 +180,10 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool d
         slices = (int)std::min<int64_t>(want, max_by_k);
     }
     if (slices < 1) slices = 1;
+    // Unsplit dense 64x64 grids of at most two tiles per CU: k-split wave sets.
+    if (dense && vec4 && slices == 1 && force_slices <= 0 && pl.tile == T64x64 &&
+        tiles <= 2 * (int64_t)cus && cdiv(K, s.bk) >= 2)
+        pl.tile = T64x64S2;
     int64_t kps = cdiv(cdiv(K, slices), s.bk) * s.bk;
     if (kps <= 0) kps = s.bk;
     slices = (int)std::max<int64_t>(1, cdiv(K, kps));

@@ -90,9 +90,9 @@ __device__ __forceinline__ void tile_coords(const GemmArgs& p, int bid, int& tm,
     tn = in_group / gsize;
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool AK, bool BKC, int VEC>
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool AK, bool BKC, int VEC, int KS = 1>
 struct Cfg {
-    static constexpr int NT = 64 * WAVES_M * WAVES_N;
+    static constexpr int NT = 64 * WAVES_M * WAVES_N * KS;
     static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     static constexpr int FM = WM / 32, FN = WN / 32;
     static constexpr int SA = AK ? (BK + 4) : (BM + 8);
@@ -104,7 +104,7 @@ struct Cfg {
     static constexpr int B_LOADS = BN * BK / (VEC * NT);
     static_assert(FM >= 1 && FN >= 1, "wave tile must be at least 32x32");
     static_assert(FM * 32 * WAVES_M == BM && FN * 32 * WAVES_N == BN, "wave grid");
-    static_assert(BK % 8 == 0, "BK must be a multiple of 8");
+    static_assert(BK % (8 * KS) == 0, "BK must split into groups of 8 per k-split wave set");
     static_assert(A_LOADS >= 1 && B_LOADS >= 1, "tile too small for the thread count");
     static_assert(A_LOADS * VEC * NT == BM * BK && B_LOADS * VEC * NT == BN * BK, "load split");
     static_assert(2 * STAGE * 4 <= 160 * 1024, "LDS budget");
@@ -319,11 +319,16 @@ __device__ __forceinline__ void load_nchw(float (&r)[LOADS][VEC], __amdgpu_buffe
 // latency; the 256x256 tile has enough work per k-tile with PF = 1).
 // AMODE / BMODE: OperandMode of A and B (OP_NCHW needs AK, OP_IM2COL needs
 // !BKC).
+// KS: wave sets splitting each k-tile. KS = 2 runs two waves per output
+// sub-block, each reducing half of every k-tile's groups of 8, and adds the
+// second set's accumulators to the first's through LDS at the end (fixed
+// order): twice the waves per SIMD for tiles that would leave one wave per
+// SIMD waiting on its barrier and LDS reads.
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool AK, bool BKC, int VEC, int WPE,
-          int PF = 1, int AMODE = OP_DENSE, int BMODE = OP_DENSE>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(WPE)))
+          int PF = 1, int AMODE = OP_DENSE, int BMODE = OP_DENSE, int KS = 1>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N * KS) __attribute__((amdgpu_waves_per_eu(WPE)))
 void gemm_kernel(GemmArgs p) {
-    using C_ = Cfg<BM, BN, BK, WAVES_M, WAVES_N, AK, BKC, VEC>;
+    using C_ = Cfg<BM, BN, BK, WAVES_M, WAVES_N, AK, BKC, VEC, KS>;
     static_assert(AMODE != OP_IM2COL && BMODE != OP_NCHW, "unsupported operand mode");
     static_assert(AMODE != OP_NCHW || AK, "OP_NCHW is a reduction-contiguous operand");
     static_assert(BMODE != OP_IM2COL || !BKC, "OP_IM2COL is a k-major operand");
@@ -333,10 +338,12 @@ void gemm_kernel(GemmArgs p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    const int kset = wave / (WAVES_M * WAVES_N);  // k-split wave set
+    const int wv = wave - kset * (WAVES_M * WAVES_N);
     const int h = lane >> 5;
     const int l32 = lane & 31;
-    const int wm0 = (wave / WAVES_N) * C_::WM;
-    const int wn0 = (wave % WAVES_N) * C_::WN;
+    const int wm0 = (wv / WAVES_N) * C_::WM;
+    const int wn0 = (wv % WAVES_N) * C_::WN;
 
     // Split K over a tile count that is not a multiple of 8: the workgroups
     // are dealt to the 8 XCDs round-robin by linear id, so the tiles of one
@@ -416,55 +423,69 @@ void gemm_kernel(GemmArgs p) {
             load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT>(r, B, p.ldb, n0, p.N, k0, kend, tid);
     };
 
-    // The k-tile count is padded to a multiple of PF (padding tiles load as
-    // zeros), and every iteration stores and prefetches unconditionally (the
-    // loads past the end are masked): the loop body is straight-line, so the
-    // compiler can count the loads in flight and wait only for the slot it
-    // stores, PF tiles after issuing it.
+    // Main loop: the body is straight-line (tile t is reduced from LDS, tile
+    // t + 1 goes from its register slot to the other LDS buffer, tile
+    // t + 1 + PF is loaded into the freed slot; loads past the end are
+    // masked), so the compiler can count the loads in flight and wait only
+    // for the slot it stores, PF tiles after issuing it. With kPeel it runs
+    // while tile t + 1 is real and the last tiles go through the tail below,
+    // which loads nothing, stores no padding tile and reduces no padding tile
+    // (a single-tile GEMM would otherwise wait one more memory round trip for
+    // a padding tile before its epilogue).
+    // Wave tiles of at most two accumulators peel the tail; the large tiles
+    // keep one straight-line loop over the k-tile count rounded up to PF
+    // (padding tiles load as zeros): with 128 accumulator registers the
+    // peeled tail costs them spills, and their k loops are long.
+    constexpr bool kPeel = FM * FN <= 2;
     const int ntiles = kend > kbeg ? (int)((kend - kbeg + BK - 1) / BK) : 0;
-    const int nt = (ntiles + PF - 1) / PF * PF;
-    if (nt > 0) {
+    const int nloop = kPeel ? ntiles : (ntiles + PF - 1) / PF * PF;
+    if (ntiles > 0) {
         loadA(ra[0], kbeg);
         loadB(rb[0], kbeg);
         storeA(smem, ra[0], kbeg);
         storeB(smem + C_::A_ELEMS, rb[0], kbeg);
 #pragma unroll
         for (int j = 1; j <= PF; ++j) {
-            const int64_t kj = kbeg + (int64_t)j * BK;
-            loadA(ra[j % PF], kj);
-            loadB(rb[j % PF], kj);
+            if (!kPeel || j < ntiles) {  // uniform
+                const int64_t kj = kbeg + (int64_t)j * BK;
+                loadA(ra[j % PF], kj);
+                loadB(rb[j % PF], kj);
+            }
         }
         __syncthreads();
     }
 
+    auto reduce_tile = [&](int t) {
+        const float* sA = smem + (t & 1) * C_::STAGE;
+        const float* sB = sA + C_::A_ELEMS;
+#pragma unroll
+        for (int gg = 0; gg < BK / 8 / KS; ++gg) {
+            const int g = kset * (BK / 8 / KS) + gg;
+            f32x4 af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                af[i] = read_frag<AK, C_::SA>(sA, wm0 + 32 * i + l32, g, h);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                bf[j] = read_frag<BKC, C_::SB>(sB, wn0 + 32 * j + l32, g, h);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s],
+                                                                        acc[i][j], 0, 0, 0);
+        }
+    };
+
     // The loop is unrolled by PF so every register-slot index is a constant.
-    for (int t0 = 0; t0 < nt; t0 += PF) {
+    int t0 = 0;
+    for (; kPeel ? t0 + PF < ntiles : t0 < nloop; t0 += PF) {
 #pragma unroll
         for (int u = 0; u < PF; ++u) {
             const int t = t0 + u;
-            const float* sA = smem + (t & 1) * C_::STAGE;
-            const float* sB = sA + C_::A_ELEMS;
-#pragma unroll
-            for (int g = 0; g < BK / 8; ++g) {
-                f32x4 af[FM], bf[FN];
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-                    af[i] = read_frag<AK, C_::SA>(sA, wm0 + 32 * i + l32, g, h);
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    bf[j] = read_frag<BKC, C_::SB>(sB, wn0 + 32 * j + l32, g, h);
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-#pragma unroll
-                    for (int i = 0; i < FM; ++i)
-#pragma unroll
-                        for (int j = 0; j < FN; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s],
-                                                                            acc[i][j], 0, 0, 0);
-            }
-            // Tile t+1 goes to the other LDS buffer (after the last tile this
-            // writes a buffer nobody reads), then its slot is refilled with
-            // tile t+1+PF.
+            reduce_tile(t);
             const int slot = (u + 1) % PF;
             float* dA = smem + ((t + 1) & 1) * C_::STAGE;
             const int64_t ks = kbeg + (int64_t)(t + 1) * BK;
@@ -511,6 +532,73 @@ void gemm_kernel(GemmArgs p) {
         }
     }
     const int64_t row0 = m0 + wm0 + 4 * h;  // row of element r = 0 of fragment i = 0
+    const float beta = p.partial ? 0.0f : p.beta;
+    // Small wave tiles load the values an accumulating epilogue adds to
+    // before the last k-tiles are reduced, so that round trip overlaps the
+    // MFMAs instead of following them (clamped, always-valid addresses;
+    // values of lanes that store nothing are unused).
+    constexpr bool kEarlyOld = FM * FN <= 2;
+    float early[kEarlyOld ? FM : 1][kEarlyOld ? FN : 1][16];
+    if constexpr (kEarlyOld) {
+        if (beta != 0.0f && kset == 0) {  // uniform
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int64_t row = row0 + 32 * i + 8 * (r >> 2) + (r & 3);
+                        const bool ok = colok[j] & (row < p.M);
+                        early[i][j][r] = out[ok ? cbase[j] + row * stride : 0];
+                    }
+        }
+    }
+
+    // Tail: the last (at most PF) tiles; only real tiles are stored and reduced.
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+        const int t = t0 + u;
+        if (kPeel && t < ntiles) {  // uniform
+            reduce_tile(t);
+            if (t + 1 < ntiles) {
+                const int slot = (u + 1) % PF;
+                float* dA = smem + ((t + 1) & 1) * C_::STAGE;
+                const int64_t ks = kbeg + (int64_t)(t + 1) * BK;
+                storeA(dA, ra[slot], ks);
+                storeB(dA + C_::A_ELEMS, rb[slot], ks);
+                __syncthreads();
+            }
+        }
+    }
+
+    if constexpr (KS > 1) {
+        // the other wave sets' accumulators, added to set 0's in set order
+        constexpr int WS = WAVES_M * WAVES_N;
+        static_assert((KS - 1) * WS * FM * FN * 16 * 64 <= 2 * C_::STAGE, "k-split LDS space");
+        __syncthreads();  // every wave is done with the staging buffers
+        if (kset > 0) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        smem[((((kset - 1) * WS + wv) * FM + i) * FN + j) * 1024 + r * 64 + lane] =
+                            acc[i][j][r];
+        }
+        __syncthreads();
+        if (kset > 0) return;  // uniform; no barrier follows
+#pragma unroll
+        for (int s2 = 0; s2 < KS - 1; ++s2)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        acc[i][j][r] += smem[(((s2 * WS + wv) * FM + i) * FN + j) * 1024 + r * 64 + lane];
+    }
+
     if (plain && full) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
@@ -524,7 +612,6 @@ void gemm_kernel(GemmArgs p) {
         const bool bias_col = !p.partial && (p.epi & NRS_EPI_BIAS_COL);
         const bool bias_row = !p.partial && (p.epi & NRS_EPI_BIAS_ROW);
         const bool relu = !p.partial && (p.epi & NRS_EPI_RELU);
-        const float beta = p.partial ? 0.0f : p.beta;
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const float bc = (bias_col && colok[j]) ? p.bias[n0 + wn0 + 32 * j + l32] : 0.0f;
@@ -541,7 +628,10 @@ void gemm_kernel(GemmArgs p) {
                     for (int r = 0; r < 16; ++r) {
                         const int64_t row = row0 + 32 * i + 8 * (r >> 2) + (r & 3);
                         const bool ok = colok[j] & (row < p.M);
-                        old[r] = beta != 0.0f ? out[ok ? cbase[j] + row * stride : 0] : 0.0f;
+                        if constexpr (kEarlyOld)
+                            old[r] = beta != 0.0f ? early[i][j][r] : 0.0f;
+                        else
+                            old[r] = beta != 0.0f ? out[ok ? cbase[j] + row * stride : 0] : 0.0f;
                         br[r] = bias_row ? p.bias[ok ? row : 0] : 0.0f;
                     }
                     __builtin_amdgcn_sched_barrier(0);

@@ -1,0 +1,202 @@
+// Step timings from C++ (no Python between launches), printed as one JSON
+// object for bench.py:
+//   block: the cfg4 TransformerBlock (B32 S128 d256 h8 dff1024) forward and
+//          backward through the C++ operator surface (libnrs_host.so), the
+//          path a drop-in caller takes: nn::TransformerBlock::forward,
+//          set_grad, backward_graph, zero_grad of the parameters;
+//   mlp:   the cfg2 MLP training step (784 -> 128 -> ReLU -> 10, batch 256,
+//          softmax cross-entropy gradient) issued through the C ABI, timed
+//          eagerly and as a replayed HIP graph of the same launches.
+// Usage: bench_host {block|mlp} [steps] [warmup]
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "neuralrs.hpp"
+#include "nrs_hip.h"
+
+using namespace neuralrs;
+using Vec = std::vector<float>;
+namespace gpu = neuralrs::hip::runtime;
+
+namespace {
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        std::fprintf(stderr, "%s: %s\n", what, hipGetErrorString(e));
+        std::exit(2);
+    }
+}
+
+void nrs_check(int rc, const char* what) {
+    if (rc != NRS_OK) {
+        std::fprintf(stderr, "%s: %s\n", what, nrs_last_error());
+        std::exit(2);
+    }
+}
+
+std::mt19937_64 rng(7);
+
+Vec normal(size_t n, float std) {
+    std::normal_distribution<float> d(0.0f, std);
+    Vec v(n);
+    for (float& x : v) x = d(rng);
+    return v;
+}
+
+Vec uniform(size_t n, float lo, float hi) {
+    std::uniform_real_distribution<float> d(lo, hi);
+    Vec v(n);
+    for (float& x : v) x = d(rng);
+    return v;
+}
+
+NodeRef resident(const Vec& v, std::vector<size_t> shape) {
+    NodeRef n = Node::create(v, std::move(shape));
+    gpu::to_cuda(n);
+    return n;
+}
+
+// GPU time of `steps` calls of fn on the library stream (HIP events) and the
+// host wall time of the same loop, after `warmup` calls.
+template <class F>
+void time_steps(F&& fn, int steps, int warmup, double& gpu_us, double& wall_us) {
+    for (int i = 0; i < warmup; ++i) fn();
+    nrs_check(nrs_sync(), "sync");
+    hipStream_t s = static_cast<hipStream_t>(nrs_get_stream());
+    hipEvent_t e0, e1;
+    hip_check(hipEventCreate(&e0), "event");
+    hip_check(hipEventCreate(&e1), "event");
+    const auto t0 = std::chrono::steady_clock::now();
+    hip_check(hipEventRecord(e0, s), "record");
+    for (int i = 0; i < steps; ++i) fn();
+    hip_check(hipEventRecord(e1, s), "record");
+    hip_check(hipEventSynchronize(e1), "event sync");
+    const auto t1 = std::chrono::steady_clock::now();
+    float ms = 0.0f;
+    hip_check(hipEventElapsedTime(&ms, e0, e1), "elapsed");
+    gpu_us = 1e3 * ms / steps;
+    wall_us = std::chrono::duration<double, std::micro>(t1 - t0).count() / steps;
+    hip_check(hipEventDestroy(e0), "event");
+    hip_check(hipEventDestroy(e1), "event");
+}
+
+int bench_block(int steps, int warmup) {
+    const size_t B = 32, S = 128, D = 256, H = 8, F = 1024;
+    const float xa = std::sqrt(6.0f / (2 * D)), fa = std::sqrt(6.0f / (D + F));
+    NodeRef wq = resident(uniform(D * D, -xa, xa), {D, D}), wk = resident(uniform(D * D, -xa, xa), {D, D});
+    NodeRef wv = resident(uniform(D * D, -xa, xa), {D, D}), wo = resident(uniform(D * D, -xa, xa), {D, D});
+    NodeRef g1 = resident(Vec(D, 1.0f), {D}), b1 = resident(Vec(D, 0.0f), {D});
+    NodeRef g2 = resident(Vec(D, 1.0f), {D}), b2 = resident(Vec(D, 0.0f), {D});
+    NodeRef f1w = resident(uniform(D * F, -fa, fa), {D, F}), f1b = resident(Vec(F, 0.0f), {F});
+    NodeRef f2w = resident(uniform(F * D, -fa, fa), {F, D}), f2b = resident(Vec(D, 0.0f), {D});
+    hip::nn::TransformerBlock tb{hip::nn::MultiHeadAttention(wq, wk, wv, wo, D, H),
+                                 hip::nn::LayerNorm(g1, b1, 1e-5f), hip::nn::LayerNorm(g2, b2, 1e-5f),
+                                 hip::nn::Linear(f1w, f1b), hip::nn::Linear(f2w, f2b), D, F};
+    NodeRef x = resident(normal(B * S * D, 1.0f), {B, S, D});
+    const std::vector<NodeRef> params{wq, wk, wv, wo, g1, b1, g2, b2, f1w, f1b, f2w, f2b};
+    // upstream gradient: a resident buffer copied into the output's gradient
+    // on the device (set_grad's host copy would synchronise every step)
+    DeviceBuffer seed = DeviceBuffer::from_host(normal(B * S * D, 1.0f));
+    auto step = [&] {
+        NodeRef out = tb.forward(x);
+        nrs_check(nrs_memcpy_dtod(out->gpu->grad->ptr(), seed.ptr(), seed.len() * sizeof(float)),
+                  "seed");
+        backward_graph(out);
+        gpu::zero_grad(params);
+        x->gpu->grad->zero();
+    };
+    double gpu_us = 0, wall_us = 0;
+    time_steps(step, steps, warmup, gpu_us, wall_us);
+    // forward alone
+    double f_gpu = 0, f_wall = 0;
+    time_steps([&] { NodeRef out = tb.forward(x); }, steps, warmup, f_gpu, f_wall);
+    const double flops_fwd = 2.0 * B * S * (4.0 * D * D + 2.0 * D * F) + 2.0 * 2.0 * B * H * S * S * (D / H);
+    std::printf("{\"workload\": \"cfg4 TransformerBlock B32 S128 d256 h8 dff1024 through libnrs_host.so\", "
+                "\"step_gpu_us\": %.2f, \"step_wall_us\": %.2f, \"fwd_gpu_us\": %.2f, "
+                "\"fwd_wall_us\": %.2f, \"gemm_flop_per_step\": %.6e, \"steps\": %d}\n",
+                gpu_us, wall_us, f_gpu, f_wall, 3.0 * flops_fwd, steps);
+    return 0;
+}
+
+int bench_mlp(int steps, int warmup) {
+    const int64_t Bn = 256, I = 784, Hd = 128, O = 10;
+    DeviceBuffer x = DeviceBuffer::from_host(normal(Bn * I, 1.0f));
+    DeviceBuffer w1 = DeviceBuffer::from_host(normal(I * Hd, std::sqrt(2.0f / I)));
+    DeviceBuffer w2 = DeviceBuffer::from_host(normal(Hd * O, std::sqrt(2.0f / Hd)));
+    DeviceBuffer b1(Hd, true), b2(O, true);
+    Vec t(Bn * O, 0.0f);
+    std::uniform_int_distribution<int> cls(0, O - 1);
+    for (int64_t r = 0; r < Bn; ++r) t[r * O + cls(rng)] = -1.0f;
+    DeviceBuffer negt = DeviceBuffer::from_host(t);
+    DeviceBuffer h(Bn * Hd, false), a(Bn * Hd, false), z(Bn * O, false), sm(Bn * O, false),
+        gz(Bn * O, false), ga(Bn * Hd, false), gh(Bn * Hd, false), gx(Bn * I, false);
+    DeviceBuffer gw1(I * Hd, true), gw2(Hd * O, true), gb1(Hd, true), gb2(O, true);
+    // the same thirteen launches as the reference's step: Linear, ReLU,
+    // Linear, softmax cross-entropy gradient (softmax - onehot) / batch, then
+    // the backward of each layer (dW and db accumulated, dh, dx)
+    auto step = [&] {
+        nrs_check(nrs_gemm(NRS_NN, h.ptr(), x.ptr(), w1.ptr(), Bn, Hd, I, 0.0f, b1.ptr(), NRS_EPI_BIAS_COL), "l1");
+        nrs_check(nrs_relu_forward(a.ptr(), h.ptr(), Bn * Hd), "relu");
+        nrs_check(nrs_gemm(NRS_NN, z.ptr(), a.ptr(), w2.ptr(), Bn, O, Hd, 0.0f, b2.ptr(), NRS_EPI_BIAS_COL), "l2");
+        nrs_check(nrs_softmax_forward(sm.ptr(), z.ptr(), Bn, O), "softmax");
+        nrs_check(nrs_vadd(gz.ptr(), sm.ptr(), negt.ptr(), Bn * O), "ce");
+        nrs_check(nrs_scale(gz.ptr(), gz.ptr(), 1.0f / Bn, Bn * O, 0.0f), "ce scale");
+        nrs_check(nrs_gemm(NRS_TN, gw2.ptr(), a.ptr(), gz.ptr(), Hd, O, Bn, 1.0f, nullptr, 0), "dw2");
+        nrs_check(nrs_sum_axis0(gb2.ptr(), gz.ptr(), Bn, O, 1.0f), "db2");
+        nrs_check(nrs_gemm(NRS_NT, ga.ptr(), gz.ptr(), w2.ptr(), Bn, Hd, O, 0.0f, nullptr, 0), "da");
+        nrs_check(nrs_relu_backward(gh.ptr(), ga.ptr(), h.ptr(), Bn * Hd, 0.0f), "relu bwd");
+        nrs_check(nrs_gemm(NRS_TN, gw1.ptr(), x.ptr(), gh.ptr(), I, Hd, Bn, 1.0f, nullptr, 0), "dw1");
+        nrs_check(nrs_sum_axis0(gb1.ptr(), gh.ptr(), Bn, Hd, 1.0f), "db1");
+        nrs_check(nrs_gemm(NRS_NT, gx.ptr(), gh.ptr(), w1.ptr(), Bn, I, Hd, 0.0f, nullptr, 0), "dx");
+    };
+    double gpu_us = 0, wall_us = 0;
+    time_steps(step, steps, warmup, gpu_us, wall_us);
+    // the same step captured once into a HIP graph and replayed (every
+    // launch above is capture-safe once the split-K scratch has grown)
+    hipStream_t cap;
+    hip_check(hipStreamCreate(&cap), "stream");
+    void* prev = nrs_get_stream();
+    nrs_check(nrs_set_stream(cap), "set stream");
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    hip_check(hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal), "begin capture");
+    step();
+    hip_check(hipStreamEndCapture(cap, &graph), "end capture");
+    hip_check(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "instantiate");
+    double g_gpu = 0, g_wall = 0;
+    time_steps([&] { hip_check(hipGraphLaunch(exec, cap), "graph launch"); }, steps, warmup, g_gpu, g_wall);
+    hip_check(hipStreamSynchronize(cap), "sync");
+    nrs_check(nrs_set_stream(prev), "set stream");
+    hip_check(hipGraphExecDestroy(exec), "destroy");
+    hip_check(hipGraphDestroy(graph), "destroy");
+    hip_check(hipStreamDestroy(cap), "destroy");
+    std::printf("{\"workload\": \"cfg2 MLP step 784-128-10 batch 256 through the C ABI\", "
+                "\"launches\": 13, \"eager_gpu_us\": %.2f, \"eager_wall_us\": %.2f, "
+                "\"graph_gpu_us\": %.2f, \"graph_wall_us\": %.2f, \"steps\": %d}\n",
+                gpu_us, wall_us, g_gpu, g_wall, steps);
+    return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    if (argc < 2) {
+        std::fprintf(stderr, "usage: %s {block|mlp} [steps] [warmup]\n", argv[0]);
+        return 2;
+    }
+    const int steps = argc > 2 ? std::atoi(argv[2]) : 20;
+    const int warmup = argc > 3 ? std::atoi(argv[3]) : 5;
+    nrs_check(nrs_init(0), "init");
+    if (!std::strcmp(argv[1], "block")) return bench_block(steps, warmup);
+    if (!std::strcmp(argv[1], "mlp")) return bench_mlp(steps, warmup);
+    std::fprintf(stderr, "unknown workload %s\n", argv[1]);
+    return 2;
+}

@@ -52,6 +52,8 @@ SHAPES = [  # (rows, cols, inner)
     # gradients (NT); the weight gradients over K = 4096 rows (TN, split-K)
     (4096, 256, 256), (4096, 1024, 256), (4096, 256, 1024),
     (256, 256, 4096), (256, 1024, 4096), (1024, 256, 4096),
+    # k-split wave sets (64x64 tiles, 8 waves) with ragged edges
+    (1000, 260, 200), (4000, 300, 96),
 ]
 
 
@@ -124,8 +126,8 @@ def test_gemm_skinny_cfg5(hip, orc):
 
 
 @pytest.mark.parametrize("shape", [(70, 50, 33), (2000, 2100, 1100), (300, 20, 40), (30, 600, 1024),
-                                   (4096, 4096, 64)],
-                         ids=["64x64", "64x128", "128x32", "32x256-splitk", "256x256"])
+                                   (4096, 4096, 64), (1000, 260, 200)],
+                         ids=["64x64", "64x128", "128x32", "32x256-splitk", "256x256", "64x64-ksplit"])
 def test_gemm_beta_bias_relu_epilogues(hip, shape):
     """The general epilogue (beta, column bias, row bias + ReLU) on each tile."""
     rng = np.random.default_rng(9)
