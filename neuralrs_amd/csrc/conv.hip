@@ -1023,6 +1023,9 @@ int nrs_conv2d_forward(float* out, const float* input, const float* weight, cons
         s.OH = (int)d.out_h;
         s.OW = (int)d.out_w;
         if (c_out <= INT32_MAX && d.out_h <= INT32_MAX && d.out_w <= INT32_MAX) {
+            // small 3x3 images: the whole image resident in LDS
+            rc = nrs::img_conv(s);
+            if (rc != nrs::kSlabUnsupported) return rc;
             rc = nrs::slab_conv(s);
             if (rc != nrs::kSlabUnsupported) return rc;
         }

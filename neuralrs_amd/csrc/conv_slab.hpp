@@ -31,6 +31,13 @@ struct SlabConv {
 constexpr int kSlabUnsupported = -1;
 int slab_conv(const SlabConv& s);
 
+// The same convolution for 3x3 stride-1 layers whose whole padded image
+// (rows of at most 16 floats) and weight block fit LDS, with a channel count
+// that is a multiple of 16 (conv_img.hip): one staging round per workgroup,
+// weights in their natural order (no packing launch). kSlabUnsupported
+// (launching nothing) for other shapes.
+int img_conv(const SlabConv& s);
+
 // Weight gradient dw[m][c][i][j] += sum g[n,m,oy,ox] * x[n,c,oy*s-pad+i,ox*s-pad+j]
 // and, when db is given, bias gradient db[m] += sum g[n,m,oy,ox], with
 // per-image partial sums added in a fixed order. dw is required; returns

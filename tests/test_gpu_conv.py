@@ -41,6 +41,12 @@ CONV_SHAPES = [  # (n, c_in, c_out, h, w, kh, kw, stride, pad)
     (2, 1, 48, 20, 20, 1, 1, 1, 0),  # three channel blocks, one tap
     (2, 1, 5, 9, 12, 3, 5, 1, 2),    # 15 taps: the bias column is the last MFMA column
     (2, 3, 17, 12, 12, 2, 2, 2, 0),  # three input channels, stride 2
+    # image-resident 3x3 kernels (channels a multiple of 16, padded rows <= 16)
+    (3, 32, 64, 14, 14, 3, 3, 1, 1),  # cfg3 conv2 geometry
+    (2, 48, 20, 9, 7, 3, 3, 1, 1),    # ragged second output-channel block
+    (2, 32, 40, 14, 14, 3, 3, 1, 0),  # pad 0
+    (2, 16, 8, 10, 10, 3, 3, 1, 2),   # pad 2
+    (2, 16, 32, 12, 12, 3, 3, 1, 0),  # input gradient at pad 2
 ]
 ids = ["x".join(map(str, s)) for s in CONV_SHAPES]
 
