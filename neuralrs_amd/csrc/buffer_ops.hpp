@@ -5,6 +5,7 @@
 
 namespace nrs {
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -23,6 +24,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float* base,
 
 __device__ __forceinline__ float buffer_load1(__amdgpu_buffer_rsrc_t r, int byte_off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
+}
+
+__device__ __forceinline__ f32x2 buffer_load2(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 0));
 }
 
 __device__ __forceinline__ f32x4 buffer_load4(__amdgpu_buffer_rsrc_t r, int byte_off) {

@@ -202,6 +202,84 @@ __global__ __launch_bounds__(256) void conv_fwd_direct_kernel(
     }
 }
 
+// The same direct convolution for "same"-padded 3x3 stride-1 layers with
+// CIN <= 3 input channels and rows of a multiple of 4 pixels: one thread per
+// quad of 4 consecutive output pixels of one row and QOC output channels, so
+// each channel leaves as one 128-bit store per lane (a wave writes 1 KiB of a
+// channel plane per store). The quad's 3*CIN input row segments of 6 floats
+// are read as an aligned 128-bit load plus its two neighbours, issued before
+// the weights are staged, so the input and weight round trips overlap. Same
+// sum order as conv_fwd_direct_kernel: taps in (ic, i, j) order from zero,
+// then + bias.
+constexpr int kQuadOc = 8;
+
+template <int CIN>
+__global__ __launch_bounds__(256) void conv_fwd_quad_kernel(
+    float* __restrict__ out, const float* __restrict__ input, const float* __restrict__ weight,
+    const float* __restrict__ bias, int N, int H, int W, int c_out, FastDiv div_qimg,
+    FastDiv div_qrow) {
+    constexpr int ROWS = 3 * CIN, TAPS = 9 * CIN;
+    __shared__ __attribute__((aligned(16))) float wsh[kQuadOc][TAPS];
+    __shared__ float bsh[kQuadOc];
+    const int tid = threadIdx.x;
+    const int P = H * W, oc0 = blockIdx.y * kQuadOc;
+    const int64_t quads = (int64_t)N * (P >> 2);
+    const int g = blockIdx.x * 256 + tid;
+    const bool valid = g < quads;
+    uint32_t n, qq, oy, qx;
+    fast_divmod((uint32_t)(valid ? g : 0), div_qimg, n, qq);
+    fast_divmod(qq, div_qrow, oy, qx);
+    const int ox = 4 * (int)qx;
+    // input row segments: columns ox-1 .. ox+4 of rows oy-1 .. oy+1
+    const auto rx = buffer_rsrc(input, (int64_t)N * CIN * P * 4);
+    float seg[ROWS][6];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        const int ic = r / 3, iy = (int)oy + r % 3 - 1;
+        const bool rok = valid & ((unsigned)iy < (unsigned)H);
+        const int base = (((int)n * CIN + ic) * H + iy) * W + ox;
+        const f32x4 mid = buffer_load4(rx, rok ? base * 4 : kOutOfRange);
+        seg[r][0] = buffer_load1(rx, rok & (ox > 0) ? (base - 1) * 4 : kOutOfRange);
+        seg[r][5] = buffer_load1(rx, rok & (ox + 4 < W) ? (base + 4) * 4 : kOutOfRange);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) seg[r][1 + u] = mid[u];
+    }
+    // this block's weights (zero past c_out) and biases
+    constexpr int WN = kQuadOc * TAPS, WPT = (WN + 255) / 256;
+    const auto rw = buffer_rsrc(weight, (int64_t)c_out * TAPS * 4);
+    const auto rb = buffer_rsrc(bias ? bias : weight, bias ? (int64_t)c_out * 4 : 0);
+    float wv[WPT];
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+        const int e = tid + 256 * k;
+        wv[k] = buffer_load1(rw, e < WN ? (oc0 * TAPS + e) * 4 : kOutOfRange);
+    }
+    const float bv = buffer_load1(rb, tid < kQuadOc ? (oc0 + tid) * 4 : kOutOfRange);
+#pragma unroll
+    for (int k = 0; k < WPT; ++k)
+        if (tid + 256 * k < WN) (&wsh[0][0])[tid + 256 * k] = wv[k];
+    if (tid < kQuadOc) bsh[tid] = bv;
+    __syncthreads();
+    if (!valid) return;
+    float* o = out + ((int64_t)n * c_out + oc0) * P + (int)oy * W + ox;
+    const int noc = min(kQuadOc, c_out - oc0);
+#pragma unroll
+    for (int oc = 0; oc < kQuadOc; ++oc) {
+        if (oc >= noc) break;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const float w = wsh[oc][r * 3 + j];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) acc[u] += w * seg[r][u + j];
+            }
+        const float b = bsh[oc];
+        __builtin_nontemporal_store(acc + b, reinterpret_cast<f32x4*>(o + (int64_t)oc * P));
+    }
+}
+
 // Direct input gradient for c_in <= kDirectCin (any stride): one thread per
 // input pixel accumulates, for its c_in channels, every (oc, i, j) whose
 // window covers it, with weights (c_out*c_in*kh*kw <= kDirectWeights) from
@@ -980,8 +1058,25 @@ int nrs_conv2d_forward(float* out, const float* input, const float* weight, cons
                     d.out_h, d.out_w, P};
     if (c_in * kh * kw <= nrs::kDirectTaps && c_out <= 65535 &&
         N * std::max(c_in * in_h * in_w, c_out * P) <= INT32_MAX) {
-        // few taps per output: direct convolution, one thread per pixel
         const int64_t taps = c_in * kh * kw;
+        if (kh == 3 && kw == 3 && stride == 1 && pad == 1 && c_in <= 3 && in_w % 4 == 0 &&
+            ((uintptr_t)out & 15) == 0 && ((uintptr_t)input & 15) == 0 &&
+            N * c_in * in_h * in_w <= INT32_MAX / 4) {
+            // "same" 3x3 over rows of whole quads: four pixels per thread
+            const int64_t quads = N * P / 4;
+            auto fn = c_in == 1 ? nrs::conv_fwd_quad_kernel<1>
+                                : (c_in == 2 ? nrs::conv_fwd_quad_kernel<2>
+                                             : nrs::conv_fwd_quad_kernel<3>);
+            hipLaunchKernelGGL(fn, dim3((unsigned)((quads + 255) / 256),
+                                        (unsigned)((c_out + nrs::kQuadOc - 1) / nrs::kQuadOc)),
+                               dim3(256), 0, nrs::stream(), out, input, weight, bias, (int)N,
+                               (int)in_h, (int)in_w, (int)c_out,
+                               nrs::make_fastdiv((uint32_t)(P / 4)),
+                               nrs::make_fastdiv((uint32_t)(in_w / 4)));
+            NRS_LAUNCH_CHECK("conv2d forward (direct, pixel quads)");
+            return NRS_OK;
+        }
+        // few taps per output: direct convolution, one thread per pixel
         auto fn = taps <= 9 ? nrs::conv_fwd_direct_kernel<9>
                             : (taps <= 16 ? nrs::conv_fwd_direct_kernel<16>
                                           : nrs::conv_fwd_direct_kernel<32>);

@@ -5,13 +5,14 @@
 // flipped, channel-transposed weights).
 //
 // One workgroup owns one image and MB output channels. It stages, once:
-//   * the whole zero-padded image, channel planes [C][R][PW] (R = H + 2*pad
-//     rows, PW >= W + 2*pad columns), read as contiguous 128-bit loads and
-//     scattered into the zeroed planes;
+//   * the whole zero-padded image as rows of 16 floats, channel planes of
+//     R = H + 2*PAD rows. Each thread copies whole rows: the source row is
+//     read with 64-bit loads (32-bit for odd widths) and written with the
+//     halo zeros as four 128-bit LDS stores, so no zero-fill pass, no barrier
+//     before the copy and no per-element index arithmetic;
 //   * the block's weights in their natural order [MB][C*9] (+4 pad per row),
 //     or flipped and transposed for the input gradient;
-// then reduces K = C*9 entirely from LDS. No weight repacking launch and no
-// per-item index arithmetic beyond the row copy.
+// then reduces K = C*9 entirely from LDS.
 //
 // Reduction order: k = c*9 + tap, the weights' own order. Lane quarter q
 // (lanes 16q..16q+15) takes the channels [q*C/4, (q+1)*C/4), so at step s
@@ -19,11 +20,13 @@
 //   * A (weights, rows = output channels): four consecutive steps are four
 //     consecutive floats of the lane's weight row: one 128-bit LDS read per
 //     four MFMAs;
-//   * B (image, columns = output pixels): step s reads plane q*C/4 + s/9 at
-//     tap (s%9)/3, s%3 from the lane's pixel: within a group of four
-//     channels the 36 offsets are compile-time constants (immediate offsets
-//     of the LDS reads).
-// Lane l's accumulator holds D[m = 4*(l/16) + r][pixel = 16*tile + l%16].
+//   * B (image, columns = output pixels): a pixel tile is one output row
+//     (lane = column; lanes past the row's width compute values that are
+//     never stored), so step s reads plane q*C/4 + s/9 at a compile-time
+//     offset (s%9)/3 rows and s%3 columns from the lane's pixel. The
+//     quarters' planes start 16 floats apart modulo 64, so the 64 lanes of a
+//     read hit 64 different banks.
+// Lane l's accumulator holds D[m = 4*(l/16) + r][column l%16 of its row].
 #include <algorithm>
 
 #include "buffer_ops.hpp"
@@ -33,31 +36,31 @@
 namespace nrs {
 namespace {
 
+constexpr int kImgRow = 16;   // floats per staged row (padded width <= 16)
+constexpr int kImgRpt = 4;    // staged rows per thread per round
+
 struct ImgArgs {
     const float* x;     // NCHW [N][C][H][W]
     const float* w;     // [M][C][3][3], or [C][M][3][3] with FLIP
     const float* bias;  // [M] or null
     float* out;         // NCHW [N][M][OH][OW]
-    int C, H, W, M, pad, OH, OW, P;
-    int R, plane;       // staged rows (H + 2*pad) and floats per staged plane (>= R * PW)
-    int tiles;          // pixel tiles of 16 per image
+    int C, H, W, M, OH, OW, P;
+    int R;              // staged rows per plane (H + 2*PAD)
+    int plane;          // floats per staged plane (>= R*16 + 2, a multiple of 4)
+    int qpitch;         // floats per lane quarter's C/4 planes (16 mod 64)
     int wrow;           // floats per staged weight row (C*9 + 4)
     int vec_out;        // 128-bit output stores (P % 4 == 0, 16-byte aligned output)
     float beta;
-    FastDiv div_ow, div_hw, div_w;
+    FastDiv div_r;      // staged rows per plane
+    FastDiv div_cq;     // channels per lane quarter
+    FastDiv div_wq;     // forward: float4s per weight row (C*9/4)
+    FastDiv div_p4;     // float4s per output channel plane
 };
 
-template <int PW>
-__device__ __forceinline__ int tap_off(int tap) {
-    return (tap / 3) * PW + tap % 3;
-}
-
-// MB output channels (OB = MB/16 blocks) per workgroup of 4 waves: wave w
-// takes channel block w % OB and the pixel tiles w / OB + k * (4 / OB),
-// k < NSW.
-template <int PW, int MB, int NSW, bool FLIP>
+template <int PAD, int MB, int NSW, bool FLIP>
 __global__ __launch_bounds__(256) void conv_img_kernel(ImgArgs a) {
     constexpr int OB = MB / 16, TSTEP = 4 / OB;
+    constexpr int SEG = kImgRow - 2 * PAD;  // source floats loaded per staged row
     static_assert(MB == 16 || MB == 32, "16 or 32 output channels per workgroup");
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -66,15 +69,15 @@ __global__ __launch_bounds__(256) void conv_img_kernel(ImgArgs a) {
     const int img = blockIdx.x, m0 = blockIdx.y * MB;
     const int C = a.C, CQ = C >> 2;  // channels per lane quarter (multiple of 4)
     float* xs = lds;
-    float* ws = lds + C * a.plane;
+    float* ws = lds + 4 * a.qpitch;
 
-    // ---- staging: the image and the weight block. A round issues all of its
-    // loads before its first LDS store, so the common shapes pay one memory
-    // round trip.
+    // ---- staging: the image rows, then the weight block. A round issues
+    // all of its loads before its first LDS store, so the common shapes pay
+    // one memory round trip.
     {
         const float* ximg = a.x + (int64_t)img * C * a.H * a.W;
-        const int HW = a.H * a.W, nimg = C * HW;  // floats of this image
-        const auto rx = buffer_rsrc(ximg, (int64_t)nimg * 4);
+        const auto rx = buffer_rsrc(ximg, (int64_t)C * a.H * a.W * 4);
+        const bool pairs = ((a.W & 1) == 0) && ((((uintptr_t)ximg) & 7) == 0);
         constexpr int WB = FLIP ? 4 : 9;  // weight items per thread in the first round
         const int wq = MB * (C * 9 / 4);  // forward: float4s of the [MB][C*9] block
         const int wpairs = MB * C;        // input gradient: (m, c) pairs of 9 taps
@@ -86,13 +89,17 @@ __global__ __launch_bounds__(256) void conv_img_kernel(ImgArgs a) {
             if constexpr (!FLIP) {
                 const float* wsrc = a.w + (int64_t)m0 * C * 9;
                 const auto rw = buffer_rsrc(wsrc, (int64_t)max(0, min(MB, a.M - m0)) * C * 9 * 4);
-                const int per_row = C * 9 / 4;
 #pragma unroll
                 for (int b = 0; b < WB; ++b) {
                     const int e = w0 + b * 256 + tid;
-                    const int m = e / per_row, k4 = e - m * per_row;
                     wv[b] = buffer_load4(rw, e < wq ? e * 16 : kOutOfRange);
-                    wd[b] = e < wq ? m * a.wrow + 4 * k4 : -1;
+                }
+#pragma unroll
+                for (int b = 0; b < WB; ++b) {
+                    const int e = w0 + b * 256 + tid;
+                    // row m = e / (C*9/4): staged at m*wrow + 4*(e - m*C*9/4)
+                    const int m = (int)fast_div((uint32_t)e, a.div_wq);
+                    wd[b] = e < wq ? 4 * e + 4 * m : -1;
                 }
             } else {
                 const auto rw = buffer_rsrc(a.w, (int64_t)C * a.M * 9 * 4);
@@ -122,67 +129,59 @@ __global__ __launch_bounds__(256) void conv_img_kernel(ImgArgs a) {
                 }
             }
         };
-        // The image is contiguous: it is read as 128-bit loads (XV per
-        // thread per round, the weights in the first round too) and scattered
-        // into the zeroed, padded planes; the last nimg % 4 floats are read
-        // one by one.
-        constexpr int XV = 8;
-        const int n4 = nimg >> 2;
-        const bool aligned = (((uintptr_t)ximg) & 15) == 0;
-        for (int r0 = 0; r0 == 0 || r0 < n4; r0 += XV * 256) {
-            f32x4 v[XV];
+        // staged row `row` = c*R + y holds source row y - PAD of channel c
+        // (zeros outside the image) at columns PAD .. PAD+W-1; loads past the
+        // row's W floats are masked to the buffer's zero
+        const int nrows = C * a.R;
+        for (int r0 = 0; r0 < nrows; r0 += 256 * kImgRpt) {
+            float v[kImgRpt][SEG];
 #pragma unroll
-            for (int b = 0; b < XV; ++b) {
-                const int e = r0 + b * 256 + tid;
-                if (aligned) {
-                    v[b] = buffer_load4(rx, e < n4 ? e * 16 : kOutOfRange);
+            for (int i = 0; i < kImgRpt; ++i) {
+                if (r0 + i * 256 >= nrows) break;  // uniform
+                const int row = r0 + i * 256 + tid;
+                const uint32_t c = fast_div((uint32_t)row, a.div_r);
+                const int y = row - (int)c * a.R - PAD;
+                const bool ok = (row < nrows) & ((unsigned)y < (unsigned)a.H);
+                const int src = ((int)c * a.H + y) * a.W;
+                if (pairs) {
+#pragma unroll
+                    for (int k = 0; k < SEG / 2; ++k) {
+                        const f32x2 t =
+                            buffer_load2(rx, (ok & (2 * k < a.W)) ? (src + 2 * k) * 4 : kOutOfRange);
+                        v[i][2 * k] = t[0];
+                        v[i][2 * k + 1] = t[1];
+                    }
                 } else {
 #pragma unroll
-                    for (int u = 0; u < 4; ++u)
-                        v[b][u] = buffer_load1(rx, e < n4 ? (4 * e + u) * 4 : kOutOfRange);
+                    for (int k = 0; k < SEG; ++k)
+                        v[i][k] = buffer_load1(rx, (ok & (k < a.W)) ? (src + k) * 4 : kOutOfRange);
                 }
             }
             f32x4 wv[FLIP ? 1 : WB];
             float wf[FLIP ? WB : 1][9];
             int wd[WB];
-            float tail = 0.0f;
-            if (r0 == 0) {
-                load_weights(0, wv, wf, wd);
-                if (tid < (nimg & 3)) tail = buffer_load1(rx, (4 * n4 + tid) * 4);
-                // zero the planes (halo included) while the loads fly
-                f32x4* z = reinterpret_cast<f32x4*>(xs);
-                for (int e = tid; e < (C * a.plane) / 4; e += 256) z[e] = f32x4{0.f, 0.f, 0.f, 0.f};
-                for (int e = (C * a.plane) / 4 * 4 + tid; e < C * a.plane; e += 256) xs[e] = 0.0f;
-                __syncthreads();
-            }
+            if (r0 == 0) load_weights(0, wv, wf, wd);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int b = 0; b < XV; ++b) {
-                const int e = r0 + b * 256 + tid;
-                if (e >= n4) continue;
-                uint32_t c, rem, r, col;
-                fast_divmod((uint32_t)(4 * e), a.div_hw, c, rem);
-                fast_divmod(rem, a.div_w, r, col);
+            for (int i = 0; i < kImgRpt; ++i) {
+                if (r0 + i * 256 >= nrows) break;  // uniform
+                const int row = r0 + i * 256 + tid;
+                if (row >= nrows) continue;
+                const uint32_t c = fast_div((uint32_t)row, a.div_r);
+                const int y = row - (int)c * a.R;
+                uint32_t qq, cl;
+                fast_divmod(c, a.div_cq, qq, cl);
+                float* dst = xs + (int)qq * a.qpitch + (int)cl * a.plane + y * kImgRow;
+                // columns PAD .. PAD+SEG-1 carry the loaded floats (zero past
+                // W), the rest is halo
+                float r[kImgRow];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    xs[(int)c * a.plane + ((int)r + a.pad) * PW + (int)col + a.pad] = v[b][u];
-                    if (++col == (uint32_t)a.W) {
-                        col = 0;
-                        if (++r == (uint32_t)a.H) {
-                            r = 0;
-                            ++c;
-                        }
-                    }
-                }
+                for (int j = 0; j < kImgRow; ++j) r[j] = (j >= PAD && j < PAD + SEG) ? v[i][j - PAD] : 0.0f;
+#pragma unroll
+                for (int j = 0; j < kImgRow; j += 4)
+                    *reinterpret_cast<f32x4*>(dst + j) = f32x4{r[j], r[j + 1], r[j + 2], r[j + 3]};
             }
-            if (r0 == 0) {
-                store_weights(wv, wf, wd);
-                if (tid < (nimg & 3)) {
-                    const int e = 4 * n4 + tid;
-                    const int c = e / HW, rem = e - c * HW, r = rem / a.W, col = rem - r * a.W;
-                    xs[c * a.plane + (r + a.pad) * PW + col + a.pad] = tail;
-                }
-            }
+            if (r0 == 0) store_weights(wv, wf, wd);
             __builtin_amdgcn_s_waitcnt(0);
         }
         const int witems = FLIP ? wpairs : wq;
@@ -205,15 +204,13 @@ __global__ __launch_bounds__(256) void conv_img_kernel(ImgArgs a) {
         const int m = m0 + 16 * ob + 4 * q + r;
         bias[r] = (a.bias && m < a.M) ? a.bias[m] : 0.0f;
     }
-    // per-tile LDS offset of this lane's pixel window (quarter's first plane)
+    // per-tile LDS offset of this lane's pixel (quarter's first plane); tiles
+    // past the last output row repeat it (their results are not stored)
     int pb[NSW];
 #pragma unroll
     for (int k = 0; k < NSW; ++k) {
-        const int t = t0 + k * TSTEP;
-        const int p = min(16 * t + l16, a.P - 1);  // masked pixels read pixel P-1
-        uint32_t oy, ox;
-        fast_divmod((uint32_t)p, a.div_ow, oy, ox);
-        pb[k] = (q * CQ) * a.plane + (int)oy * PW + (int)ox;
+        const int oy = min(t0 + k * TSTEP, a.OH - 1);
+        pb[k] = q * a.qpitch + oy * kImgRow + l16;
     }
     __syncthreads();
 
@@ -231,7 +228,7 @@ __global__ __launch_bounds__(256) void conv_img_kernel(ImgArgs a) {
         for (int k = 0; k < NSW; ++k)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                bf[k][r] = xs[pb[k] + cbase + (r / 9) * a.plane + tap_off<PW>(r % 9)];
+                bf[k][r] = xs[pb[k] + cbase + (r / 9) * a.plane + ((r % 9) / 3) * kImgRow + r % 3];
 #pragma unroll
         for (int u = 0; u < 9; ++u) {
             f32x4 an;
@@ -243,7 +240,8 @@ __global__ __launch_bounds__(256) void conv_img_kernel(ImgArgs a) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int s = 4 * (u + 1) + r;
-                        bn[k][r] = xs[pb[k] + cbase + (s / 9) * a.plane + tap_off<PW>(s % 9)];
+                        bn[k][r] =
+                            xs[pb[k] + cbase + (s / 9) * a.plane + ((s % 9) / 3) * kImgRow + s % 3];
                     }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -277,21 +275,26 @@ __global__ __launch_bounds__(256) void conv_img_kernel(ImgArgs a) {
 #pragma unroll
         for (int u = 0; u < OV; ++u) {
             const int e = u * 256 + tid;
-            const int m = e / max(P4, 1), p4 = e - m * P4;
+            const int m = (int)fast_div((uint32_t)e, a.div_p4), p4 = e - m * P4;
             old[u] = (m < mvalid) ? *reinterpret_cast<const f32x4*>(oimg + (int64_t)(m0 + m) * a.P + 4 * p4)
                                   : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
     }
     __syncthreads();  // every wave is done with the image planes
     float* ot = lds;  // [MB][P]
+    if (l16 < a.OW) {
 #pragma unroll
-    for (int k = 0; k < NSW; ++k)
+        for (int k = 0; k < NSW; ++k) {
+            const int oy = t0 + k * TSTEP;
+            if (oy < a.OH) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int p = 16 * (t0 + k * TSTEP) + l16;
-            const int m = 16 * ob + 4 * q + r;
-            if (p < a.P) ot[m * a.P + p] = acc[k][r] + bias[r];
+                for (int r = 0; r < 4; ++r) {
+                    const int m = 16 * ob + 4 * q + r;
+                    ot[m * a.P + oy * a.OW + l16] = acc[k][r] + bias[r];
+                }
+            }
         }
+    }
     __syncthreads();
     if (vec) {
         const int total = mvalid * P4;
@@ -300,7 +303,7 @@ __global__ __launch_bounds__(256) void conv_img_kernel(ImgArgs a) {
             for (int u = 0; u < OV; ++u) {
                 const int e = u0 + u * 256 + tid;
                 if (e >= total) continue;
-                const int m = e / P4, p4 = e - m * P4;
+                const int m = (int)fast_div((uint32_t)e, a.div_p4), p4 = e - m * P4;
                 f32x4 v = *reinterpret_cast<const f32x4*>(ot + m * a.P + 4 * p4);
                 if (a.beta != 0.0f) {
                     const f32x4 o = u0 == 0 ? old[u]
@@ -326,9 +329,9 @@ __global__ __launch_bounds__(256) void conv_img_kernel(ImgArgs a) {
 
 constexpr int kImgLdsBytes = 160 * 1024;
 
-template <int PW, int MB, int NSW, bool FLIP>
+template <int PAD, int MB, int NSW, bool FLIP>
 int launch_img(const ImgArgs& a, int64_t N, size_t lds) {
-    auto fn = conv_img_kernel<PW, MB, NSW, FLIP>;
+    auto fn = conv_img_kernel<PAD, MB, NSW, FLIP>;
     static bool attr_set = false;
     if (!attr_set) {
         NRS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -341,34 +344,42 @@ int launch_img(const ImgArgs& a, int64_t N, size_t lds) {
     return NRS_OK;
 }
 
+template <int PAD, bool FLIP>
+int launch_img_pad(const ImgArgs& a, int64_t N, size_t lds, int MB, int NSW) {
+    if (MB == 32) return NSW == 7 ? launch_img<PAD, 32, 7, FLIP>(a, N, lds)
+                                  : launch_img<PAD, 32, 4, FLIP>(a, N, lds);
+    return NSW == 7 ? launch_img<PAD, 16, 7, FLIP>(a, N, lds)
+                    : launch_img<PAD, 16, 4, FLIP>(a, N, lds);
+}
+
 }  // namespace
 
 int img_conv(const SlabConv& s) {
     // 3x3, stride 1, channel count a multiple of 16, rows of at most 16
-    // staged floats, a handful of 16-pixel tiles per wave
+    // staged floats, a handful of output rows per wave
     if (s.kh != 3 || s.kw != 3 || s.stride != 1 || s.pad_h != s.pad_w || s.pad_h > 2 ||
         s.C % 16 != 0 || s.C <= 0 || s.M <= 0 || s.N <= 0 || s.N > 65535)
         return kSlabUnsupported;
     const int pad = s.pad_h;
     const int R = s.H + 2 * pad, Wp = s.W + 2 * pad;
-    if (Wp > 16 || s.OH != R - 2 || s.OW != Wp - 2) return kSlabUnsupported;
-    constexpr int PW = 16;
-    const int P = s.OH * s.OW, tiles = (P + 15) / 16;
+    if (Wp > kImgRow || s.OH != R - 2 || s.OW != Wp - 2 || s.OH < 1 || s.OW < 1)
+        return kSlabUnsupported;
+    const int P = s.OH * s.OW;
     // 32 output channels per workgroup when that leaves at least one
     // workgroup per CU, else 16
     const int MB = (s.M % 32 == 0 && s.N * (s.M / 32) >= num_cus()) ? 32 : 16;
-    const int per_wave = (tiles + (4 / (MB / 16)) - 1) / (4 / (MB / 16));
+    const int per_wave = (s.OH + (4 / (MB / 16)) - 1) / (4 / (MB / 16));
     const int NSW = per_wave <= 4 ? 4 : (per_wave <= 7 ? 7 : 0);
     if (NSW == 0) return kSlabUnsupported;
-    // plane pitch: the four lane quarters read four channel planes at once;
-    // a pitch with quarters * planes = 16 (mod 64) floats puts them on
-    // different LDS banks
+    // planes of R rows (+2 floats read by the lanes past the last column of
+    // the last row); the four lane quarters' plane blocks start 16 floats
+    // apart modulo 64 so a quarter-per-16-banks read has no conflicts
     const int CQ = s.C / 4;
-    int plane = R * PW;
-    while ((CQ * plane) % 64 != 16) ++plane;
+    const int plane = (R * kImgRow + 2 + 3) / 4 * 4;
+    const int qpitch = CQ * plane + (((16 - CQ * plane) % 64) + 64) % 64;
     const int wrow = s.C * 9 + 4;
     // (the epilogue's [MB][P] output tile reuses the image planes)
-    const size_t lds = 4 * std::max((size_t)s.C * plane + (size_t)MB * wrow, (size_t)MB * P);
+    const size_t lds = 4 * std::max((size_t)4 * qpitch + (size_t)MB * wrow, (size_t)MB * P);
     if (lds > kImgLdsBytes) return kSlabUnsupported;
     ImgArgs a;
     a.x = s.x;
@@ -379,29 +390,27 @@ int img_conv(const SlabConv& s) {
     a.H = s.H;
     a.W = s.W;
     a.M = s.M;
-    a.pad = pad;
     a.OH = s.OH;
     a.OW = s.OW;
     a.P = P;
     a.R = R;
     a.plane = plane;
-    a.tiles = tiles;
+    a.qpitch = qpitch;
     a.wrow = wrow;
     a.beta = s.beta;
     a.vec_out = (P % 4 == 0 && ((uintptr_t)s.out & 15) == 0) ? 1 : 0;
-    a.div_ow = make_fastdiv((uint32_t)s.OW);
-    a.div_hw = make_fastdiv((uint32_t)(s.H * s.W));
-    a.div_w = make_fastdiv((uint32_t)s.W);
-    if (s.flip) {
-        if (MB == 32) return NSW == 7 ? launch_img<PW, 32, 7, true>(a, s.N, lds)
-                                      : launch_img<PW, 32, 4, true>(a, s.N, lds);
-        return NSW == 7 ? launch_img<PW, 16, 7, true>(a, s.N, lds)
-                        : launch_img<PW, 16, 4, true>(a, s.N, lds);
+    a.div_r = make_fastdiv((uint32_t)R);
+    a.div_cq = make_fastdiv((uint32_t)CQ);
+    a.div_wq = make_fastdiv((uint32_t)(s.C * 9 / 4));
+    a.div_p4 = make_fastdiv((uint32_t)std::max(1, P / 4));
+    switch (pad) {
+        case 0: return s.flip ? launch_img_pad<0, true>(a, s.N, lds, MB, NSW)
+                              : launch_img_pad<0, false>(a, s.N, lds, MB, NSW);
+        case 1: return s.flip ? launch_img_pad<1, true>(a, s.N, lds, MB, NSW)
+                              : launch_img_pad<1, false>(a, s.N, lds, MB, NSW);
+        default: return s.flip ? launch_img_pad<2, true>(a, s.N, lds, MB, NSW)
+                               : launch_img_pad<2, false>(a, s.N, lds, MB, NSW);
     }
-    if (MB == 32) return NSW == 7 ? launch_img<PW, 32, 7, false>(a, s.N, lds)
-                                  : launch_img<PW, 32, 4, false>(a, s.N, lds);
-    return NSW == 7 ? launch_img<PW, 16, 7, false>(a, s.N, lds)
-                    : launch_img<PW, 16, 4, false>(a, s.N, lds);
 }
 
 }  // namespace nrs

@@ -41,6 +41,9 @@ CONV_SHAPES = [  # (n, c_in, c_out, h, w, kh, kw, stride, pad)
     (2, 1, 48, 20, 20, 1, 1, 1, 0),  # three channel blocks, one tap
     (2, 1, 5, 9, 12, 3, 5, 1, 2),    # 15 taps: the bias column is the last MFMA column
     (2, 3, 17, 12, 12, 2, 2, 2, 0),  # three input channels, stride 2
+    # "same" 3x3 over rows of whole pixel quads (direct forward, 4 pixels per thread)
+    (2, 2, 13, 6, 12, 3, 3, 1, 1),    # two input channels, ragged output-channel block
+    (3, 1, 9, 5, 4, 3, 3, 1, 1),      # one quad per row: both row edges in one quad
     # image-resident 3x3 kernels (channels a multiple of 16, padded rows <= 16)
     (3, 32, 64, 14, 14, 3, 3, 1, 1),  # cfg3 conv2 geometry
     (2, 48, 20, 9, 7, 3, 3, 1, 1),    # ragged second output-channel block
