@@ -983,11 +983,17 @@ int slab_dgrad(float* dinput, const float* grad, const float* weight, int64_t N,
     s.flip = true;
     s.beta = 1.0f;
     if (wg) {
+        // with the weight gradient: both in one launch
         const int rc = slab_backward_pair(s, *wg);
         if (rc != kSlabUnsupported) {
             *wg_done = rc == NRS_OK;
             return rc;
         }
+    } else {
+        // small 3x3 images: the whole gradient image resident in LDS, the
+        // weights flipped while they are staged (no packing launch)
+        const int rc = img_conv(s);
+        if (rc != kSlabUnsupported) return rc;
     }
     return slab_conv(s);
 }

@@ -172,6 +172,29 @@ def test_conv2d_backward_without_input_grad(hip, orc):
     assert np.array_equal(gB.to_host(), db_ref)
 
 
+@pytest.mark.parametrize("shape", [
+    (3, 32, 64, 14, 14, 3, 3, 1, 1),  # cfg3 conv2 geometry
+    (2, 20, 32, 9, 7, 3, 3, 1, 1),    # ragged input-channel block
+    (2, 16, 32, 12, 12, 3, 3, 1, 0),  # the flipped convolution pads by 2
+    (2, 8, 16, 10, 10, 3, 3, 1, 2),   # ... and by 0
+], ids=["cfg3-conv2", "ragged", "pad0", "pad2"])
+def test_conv2d_backward_input_grad_only(hip, orc, shape):
+    """dweight = dbias = NULL: the input gradient alone (the image-resident
+    flipped convolution for these shapes), accumulated into dinput."""
+    n, ci, co, h, w, kh, kw, s, p = shape
+    rng = np.random.default_rng(80 + sum(shape))
+    x = int_matrix(rng, (n * ci * h * w,), -3, 3)
+    wt = int_matrix(rng, (co * ci * kh * kw,), -3, 3)
+    oh, ow = orc.conv_out_hw(h, w, kh, kw, s, p)
+    g = int_matrix(rng, (n * co * oh * ow,), -3, 3)
+    di_ref, _, _ = orc.conv2d_backward(x, wt, g, n, ci, co, h, w, kh, kw, s, p)
+    gi0 = int_matrix(rng, (x.size,))
+    gI = D(hip, gi0)
+    hip.call("nrs_conv2d_backward", gI.ptr, None, None, D(hip, g), D(hip, x),
+             D(hip, wt), n, ci, h, w, co, kh, kw, s, p)
+    assert np.array_equal(gI.to_host(), gi0 + di_ref)
+
+
 @pytest.mark.parametrize("shape", [(2, 1, 4, 6, 6, 3, 3, 1, 1), (2, 6, 5, 9, 9, 3, 3, 1, 1)],
                          ids=["few-taps", "gemm"])
 def test_conv2d_backward_bias_only(hip, orc, shape):
