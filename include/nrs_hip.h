@@ -238,6 +238,16 @@ int nrs_scale(float *out, const float *x, float s, int64_t n, float beta);
 /* softmax_forward (src/cuda/graph/softmax.rs:11-22): softmax over the last
  * dim of rows x width, max-subtracted.                                       */
 int nrs_softmax_forward(float *out, const float *in, int64_t rows, int64_t width);
+/* Cross-entropy of raw logits [batch, classes] against a one-hot target of
+ * the same shape (src/cuda/loss/cross_entropy.rs:18-36, ce_forward): row_loss
+ * [batch] gets sum_c -t*(l - logsumexp(l)) per row; the batch mean is the
+ * caller's host-side sum / batch (cross_entropy.rs:74-88).                  */
+int nrs_cross_entropy_forward(float *row_loss, const float *logits, const float *target,
+                              int64_t batch, int64_t classes);
+/* The fused seed of cross_entropy_backward (cross_entropy.rs:39-58,100-127):
+ * grad = (softmax(logits) - target) / batch, written (not accumulated).     */
+int nrs_cross_entropy_backward(float *grad, const float *logits, const float *target,
+                               int64_t batch, int64_t classes);
 /* softmax_backward (src/cuda/graph/softmax.rs:23-35), from the forward output
  * y: gin = y*(grad - sum(y*grad)) + beta*gin.                                */
 int nrs_softmax_backward(float *gin, const float *y, const float *grad, int64_t rows,

@@ -61,6 +61,8 @@ SIGNATURES = {
     "nrs_transpose": [_P, _P, _I, _I, _I],
     "nrs_scale": [_P, _P, _F, _I, _F],
     "nrs_softmax_forward": [_P, _P, _I, _I],
+    "nrs_cross_entropy_forward": [_P, _P, _P, _I, _I],
+    "nrs_cross_entropy_backward": [_P, _P, _P, _I, _I],
     "nrs_softmax_backward": [_P, _P, _P, _I, _I, _F],
     "nrs_slice_cols": [_P, _P, _I, _I, _I, _I],
     "nrs_slice_cols_backward": [_P, _P, _I, _I, _I, _I, _F],

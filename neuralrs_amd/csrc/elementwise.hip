@@ -52,6 +52,47 @@ __global__ __launch_bounds__(256) void bias_add_kernel(float* out, const float* 
         out[i] = a[i] + bias[i % cols];
 }
 
+// out[chunk][c] = sum_{r in chunk} in[r, c] (+ beta * out[c] for a single
+// chunk) for chunks of `chunk_rows` rows (blockIdx.y): a workgroup owns 64
+// columns of one chunk and splits its rows into 16 contiguous groups, one
+// wave each; a lane issues its group's loads 16 at a time, and the group
+// sums are added in group order (deterministic).
+constexpr int kColGroups = 16, kColBatch = 16, kColSingleRows = kColGroups * 4 * kColBatch;
+constexpr int kColChunkRows = kColGroups * kColBatch;
+
+__global__ __launch_bounds__(64 * kColGroups) void colsum_single_kernel(float* __restrict__ out,
+                                                                       const float* __restrict__ in,
+                                                                       int64_t rows, int64_t cols,
+                                                                       int64_t chunk_rows, float beta) {
+    __shared__ float red[kColGroups][64];
+    const int x = threadIdx.x & 63, y = threadIdx.x >> 6;
+    const int64_t c = (int64_t)blockIdx.x * 64 + x;
+    const int64_t first = (int64_t)blockIdx.y * chunk_rows;
+    in += first * cols;
+    out += (int64_t)blockIdx.y * cols;
+    rows = min(chunk_rows, rows - first);
+    const int64_t per = (rows + kColGroups - 1) / kColGroups;
+    const int64_t r0 = min(rows, y * per), r1 = min(rows, r0 + per);
+    const int64_t cc = c < cols ? c : cols - 1;  // clamped: always a valid address
+    float v = 0.0f;
+    for (int64_t rb = r0; rb < r1; rb += kColBatch) {
+        float t[kColBatch];
+#pragma unroll
+        for (int u = 0; u < kColBatch; ++u) t[u] = in[min(rb + u, r1 - 1) * cols + cc];
+#pragma unroll
+        for (int u = 0; u < kColBatch; ++u)
+            if (rb + u < r1) v += t[u];
+    }
+    red[y][x] = v;
+    __syncthreads();
+    if (y != 0 || c >= cols) return;
+    float r = red[0][x];
+#pragma unroll
+    for (int g = 1; g < kColGroups; ++g) r += red[g][x];
+    if (beta != 0.0f) r = r + beta * out[c];
+    out[c] = r;
+}
+
 // partial[chunk, c] = sum_{r in chunk} in[r, c], r ascending.
 __global__ __launch_bounds__(256) void colsum_partial_kernel(float* __restrict__ partial,
                                                              const float* __restrict__ in,
@@ -244,6 +285,29 @@ int nrs_sum_axis0(float* out, const float* in, int64_t rows, int64_t cols, float
     NRS_ARG_CHECK(rows >= 0 && cols >= 0, "sum_axis0: negative size");
     if (cols == 0) return NRS_OK;
     NRS_ARG_CHECK(out && (in || rows == 0), "sum_axis0: null pointer");
+    const unsigned cb = (unsigned)((cols + 63) / 64);
+    if (rows <= nrs::kColSingleRows) {
+        // short columns (a Linear's bias gradient over a batch): one launch
+        hipLaunchKernelGGL(nrs::colsum_single_kernel, dim3(cb), dim3(64 * nrs::kColGroups), 0,
+                           nrs::stream(), out, in, rows, cols, std::max<int64_t>(rows, 1), beta);
+        NRS_LAUNCH_CHECK("sum_axis0");
+        return NRS_OK;
+    }
+    if (rows <= (int64_t)nrs::kColChunkRows * nrs::kColSingleRows && rows <= 65535ll * nrs::kColChunkRows) {
+        // chunks of 256 rows summed side by side, then the chunk sums (at
+        // most kColSingleRows of them) in chunk order
+        const int64_t chunks = (rows + nrs::kColChunkRows - 1) / nrs::kColChunkRows;
+        float* part = nrs::workspace(sizeof(float) * (size_t)(chunks * cols), 3);
+        if (!part) return NRS_ERR_ALLOC;
+        hipLaunchKernelGGL(nrs::colsum_single_kernel, dim3(cb, (unsigned)chunks),
+                           dim3(64 * nrs::kColGroups), 0, nrs::stream(), part, in, rows, cols,
+                           (int64_t)nrs::kColChunkRows, 0.0f);
+        NRS_LAUNCH_CHECK("sum_axis0 (chunks)");
+        hipLaunchKernelGGL(nrs::colsum_single_kernel, dim3(cb), dim3(64 * nrs::kColGroups), 0,
+                           nrs::stream(), out, part, chunks, cols, chunks, beta);
+        NRS_LAUNCH_CHECK("sum_axis0");
+        return NRS_OK;
+    }
     const int64_t col_blocks = (cols + 255) / 256;
     // Row chunks so that ~2 workgroups per CU run, each chunk >= 64 rows.
     int64_t chunks = std::max<int64_t>(1, (2 * (int64_t)nrs::num_cus()) / col_blocks);

@@ -476,11 +476,60 @@ int nrs_heads_impl(float* dst, const float* src, int64_t rows, int64_t heads, in
     return strided_copy(a, split ? "split heads" : "merge heads");
 }
 
+// Cross-entropy of raw logits against a target (one-hot rows), one thread
+// per row as the reference's kernels (src/cuda/loss/cross_entropy.rs:18-58):
+// the row max folded from its first logit, the sum of expf(l - max) in class
+// order; GRAD: out[row] = (softmax - target) * (1 / batch), the fused seed of
+// cross_entropy_backward; else out[row] = sum_c -t_c * (l_c - log_sum_exp).
+template <bool GRAD>
+__global__ __launch_bounds__(256) void cross_entropy_kernel(float* __restrict__ out,
+                                                            const float* __restrict__ logits,
+                                                            const float* __restrict__ target,
+                                                            int64_t batch, int64_t classes) {
+    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= batch) return;
+    const float* l = logits + b * classes;
+    const float* t = target + b * classes;
+    float mx = l[0];
+    for (int64_t c = 1; c < classes; ++c) mx = fmaxf(mx, l[c]);
+    float sum = 0.0f;
+    for (int64_t c = 0; c < classes; ++c) sum += expf(l[c] - mx);
+    if constexpr (GRAD) {
+        const float inv_batch = 1.0f / (float)batch;
+        float* g = out + b * classes;
+        for (int64_t c = 0; c < classes; ++c) g[c] = (expf(l[c] - mx) / sum - t[c]) * inv_batch;
+    } else {
+        const float lse = logf(sum) + mx;
+        float loss = 0.0f;
+        for (int64_t c = 0; c < classes; ++c) loss += -t[c] * (l[c] - lse);
+        out[b] = loss;
+    }
+}
+
+int cross_entropy_launch(bool grad, float* out, const float* logits, const float* target,
+                         int64_t batch, int64_t classes) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(batch >= 0 && classes > 0, "cross_entropy: bad shape");
+    if (batch == 0) return NRS_OK;
+    NRS_ARG_CHECK(out && logits && target, "cross_entropy: null pointer");
+    NRS_ARG_CHECK((batch + 255) / 256 <= INT32_MAX, "cross_entropy: batch too large");
+    const dim3 grid((unsigned)((batch + 255) / 256));
+    if (grad)
+        hipLaunchKernelGGL(cross_entropy_kernel<true>, grid, dim3(256), 0, stream(), out, logits,
+                           target, batch, classes);
+    else
+        hipLaunchKernelGGL(cross_entropy_kernel<false>, grid, dim3(256), 0, stream(), out, logits,
+                           target, batch, classes);
+    NRS_LAUNCH_CHECK(grad ? "cross_entropy backward" : "cross_entropy forward");
+    return NRS_OK;
+}
+
 }  // namespace
 }  // namespace nrs
 
 using nrs::nrs_heads_impl;
 using nrs::nrs_slice_cols_backward_impl;
+using nrs::cross_entropy_launch;
 
 extern "C" {
 
@@ -528,6 +577,16 @@ int nrs_softmax_forward_scaled(float* out, const float* in, int64_t rows, int64_
 
 int nrs_softmax_forward(float* out, const float* in, int64_t rows, int64_t width) {
     return nrs_softmax_forward_scaled(out, in, rows, width, 1.0f);
+}
+
+int nrs_cross_entropy_forward(float* row_loss, const float* logits, const float* target,
+                              int64_t batch, int64_t classes) {
+    return cross_entropy_launch(false, row_loss, logits, target, batch, classes);
+}
+
+int nrs_cross_entropy_backward(float* grad, const float* logits, const float* target,
+                               int64_t batch, int64_t classes) {
+    return cross_entropy_launch(true, grad, logits, target, batch, classes);
 }
 
 int nrs_softmax_backward_scaled(float* gin, const float* y, const float* grad, int64_t rows,

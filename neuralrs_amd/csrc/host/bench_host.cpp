@@ -5,7 +5,7 @@
 //          path a drop-in caller takes: nn::TransformerBlock::forward,
 //          set_grad, backward_graph, zero_grad of the parameters;
 //   mlp:   the cfg2 MLP training step (784 -> 128 -> ReLU -> 10, batch 256,
-//          softmax cross-entropy gradient) issued through the C ABI, timed
+//          fused cross-entropy gradient) issued through the C ABI, timed
 //          eagerly and as a replayed HIP graph of the same launches.
 // Usage: bench_host {block|mlp} [steps] [warmup]
 #include <hip/hip_runtime.h>
@@ -134,25 +134,25 @@ int bench_mlp(int steps, int warmup) {
     DeviceBuffer b1(Hd, true), b2(O, true);
     Vec t(Bn * O, 0.0f);
     std::uniform_int_distribution<int> cls(0, O - 1);
-    for (int64_t r = 0; r < Bn; ++r) t[r * O + cls(rng)] = -1.0f;
-    DeviceBuffer negt = DeviceBuffer::from_host(t);
-    DeviceBuffer h(Bn * Hd, false), a(Bn * Hd, false), z(Bn * O, false), sm(Bn * O, false),
-        gz(Bn * O, false), ga(Bn * Hd, false), gh(Bn * Hd, false), gx(Bn * I, false);
+    for (int64_t r = 0; r < Bn; ++r) t[r * O + cls(rng)] = 1.0f;
+    DeviceBuffer onehot = DeviceBuffer::from_host(t);
+    DeviceBuffer a(Bn * Hd, false), z(Bn * O, false), gz(Bn * O, false), ga(Bn * Hd, false),
+        gh(Bn * Hd, false), gx(Bn * I, false);
     DeviceBuffer gw1(I * Hd, true), gw2(Hd * O, true), gb1(Hd, true), gb2(O, true);
-    // the same thirteen launches as the reference's step: Linear, ReLU,
-    // Linear, softmax cross-entropy gradient (softmax - onehot) / batch, then
-    // the backward of each layer (dW and db accumulated, dh, dx)
+    // the reference's step (Linear, ReLU, Linear, the fused cross-entropy
+    // seed (softmax - onehot) / batch, then each layer's backward: dW and db
+    // accumulated, dh, dx) in ten launches: bias and ReLU ride the first
+    // GEMM's epilogue, and the ReLU backward masks by the activation (a > 0
+    // exactly where the pre-activation is)
     auto step = [&] {
-        nrs_check(nrs_gemm(NRS_NN, h.ptr(), x.ptr(), w1.ptr(), Bn, Hd, I, 0.0f, b1.ptr(), NRS_EPI_BIAS_COL), "l1");
-        nrs_check(nrs_relu_forward(a.ptr(), h.ptr(), Bn * Hd), "relu");
+        nrs_check(nrs_gemm(NRS_NN, a.ptr(), x.ptr(), w1.ptr(), Bn, Hd, I, 0.0f, b1.ptr(),
+                           NRS_EPI_BIAS_COL | NRS_EPI_RELU), "l1+relu");
         nrs_check(nrs_gemm(NRS_NN, z.ptr(), a.ptr(), w2.ptr(), Bn, O, Hd, 0.0f, b2.ptr(), NRS_EPI_BIAS_COL), "l2");
-        nrs_check(nrs_softmax_forward(sm.ptr(), z.ptr(), Bn, O), "softmax");
-        nrs_check(nrs_vadd(gz.ptr(), sm.ptr(), negt.ptr(), Bn * O), "ce");
-        nrs_check(nrs_scale(gz.ptr(), gz.ptr(), 1.0f / Bn, Bn * O, 0.0f), "ce scale");
+        nrs_check(nrs_cross_entropy_backward(gz.ptr(), z.ptr(), onehot.ptr(), Bn, O), "ce");
         nrs_check(nrs_gemm(NRS_TN, gw2.ptr(), a.ptr(), gz.ptr(), Hd, O, Bn, 1.0f, nullptr, 0), "dw2");
         nrs_check(nrs_sum_axis0(gb2.ptr(), gz.ptr(), Bn, O, 1.0f), "db2");
         nrs_check(nrs_gemm(NRS_NT, ga.ptr(), gz.ptr(), w2.ptr(), Bn, Hd, O, 0.0f, nullptr, 0), "da");
-        nrs_check(nrs_relu_backward(gh.ptr(), ga.ptr(), h.ptr(), Bn * Hd, 0.0f), "relu bwd");
+        nrs_check(nrs_relu_backward(gh.ptr(), ga.ptr(), a.ptr(), Bn * Hd, 0.0f), "relu bwd");
         nrs_check(nrs_gemm(NRS_TN, gw1.ptr(), x.ptr(), gh.ptr(), I, Hd, Bn, 1.0f, nullptr, 0), "dw1");
         nrs_check(nrs_sum_axis0(gb1.ptr(), gh.ptr(), Bn, Hd, 1.0f), "db1");
         nrs_check(nrs_gemm(NRS_NT, gx.ptr(), gh.ptr(), w1.ptr(), Bn, I, Hd, 0.0f, nullptr, 0), "dx");
@@ -179,7 +179,7 @@ int bench_mlp(int steps, int warmup) {
     hip_check(hipGraphDestroy(graph), "destroy");
     hip_check(hipStreamDestroy(cap), "destroy");
     std::printf("{\"workload\": \"cfg2 MLP step 784-128-10 batch 256 through the C ABI\", "
-                "\"launches\": 13, \"eager_gpu_us\": %.2f, \"eager_wall_us\": %.2f, "
+                "\"launches\": 10, \"eager_gpu_us\": %.2f, \"eager_wall_us\": %.2f, "
                 "\"graph_gpu_us\": %.2f, \"graph_wall_us\": %.2f, \"steps\": %d}\n",
                 gpu_us, wall_us, g_gpu, g_wall, steps);
     return 0;

@@ -405,6 +405,40 @@ NodeRef reshape(const NodeRef& a, std::vector<size_t> shape) {
 
 }  // namespace graph
 
+// -------------------------------------------------------------------- loss
+namespace loss {
+namespace {
+// (batch, classes) of the logits (src/cuda/loss/cross_entropy.rs:62-67)
+std::pair<size_t, size_t> batch_classes(const NodeRef& n) {
+    if (n->shape.size() == 2) return {n->shape[0], n->shape[1]};
+    if (n->shape.empty()) throw Panic("cuda ce: scalar logits");
+    return {1, n->shape[0]};
+}
+}  // namespace
+
+float cross_entropy(const NodeRef& pred, const NodeRef& target) {
+    const auto [batch, classes] = batch_classes(pred);
+    GpuBuffers& p = gpu_of(pred, "cuda ce: logits not on GPU");
+    GpuBuffers& t = gpu_of(target, "cuda ce: target not on GPU");
+    DeviceBuffer row_loss(batch, true);
+    check(nrs_cross_entropy_forward(row_loss.ptr(), p.data.ptr(), t.data.ptr(), batch, classes),
+          "cuda ce: forward launch failed");
+    const std::vector<float> host = row_loss.to_host();
+    float total = 0.0f;
+    for (float v : host) total += v;
+    return total / (float)batch;
+}
+
+void cross_entropy_backward(const NodeRef& pred, const NodeRef& target) {
+    const auto [batch, classes] = batch_classes(pred);
+    GpuBuffers& p = gpu_of(pred, "cuda ce: logits not on GPU");
+    GpuBuffers& t = gpu_of(target, "cuda ce: target not on GPU");
+    check(nrs_cross_entropy_backward(p.grad->ptr(), p.data.ptr(), t.data.ptr(), batch, classes),
+          "cuda ce: backward launch failed");
+}
+
+}  // namespace loss
+
 // ---------------------------------------------------------------------- nn
 namespace nn {
 

@@ -137,6 +137,17 @@ NodeRef scaled_softmax(const NodeRef& a, float s);
 NodeRef reshape(const NodeRef& a, std::vector<size_t> shape);
 }  // namespace graph
 
+namespace loss {
+// src/cuda/loss/cross_entropy.rs:74-91: cross-entropy of resident logits
+// ([batch, classes], or [classes] as one row) against a resident one-hot
+// target, averaged over the batch (per-row losses on the device, summed on
+// the host in row order).
+float cross_entropy(const NodeRef& pred, const NodeRef& target);
+// src/cuda/loss/cross_entropy.rs:100-127: writes (softmax - target) / batch
+// into the logits' gradient; backward_graph then propagates it.
+void cross_entropy_backward(const NodeRef& pred, const NodeRef& target);
+}  // namespace loss
+
 namespace nn {
 // src/cuda/nn/conv.rs:244-328: input [N,c_in,H,W], weight [c_out,c_in,kh,kw],
 // bias [c_out] -> [N,c_out,oh,ow]. The input gradient is skipped when

@@ -83,6 +83,8 @@ def lib():
             "orc_softmax_forward": (None, [f32p, f32p, I64, I64]),
             "orc_softmax_backward": (None, [f32p, f32p, f32p, I64, I64]),
             "orc_relu_forward": (None, [f32p, f32p, I64]),
+            "orc_cross_entropy_loss": (ctypes.c_float, [f32p, f32p, I64, I64]),
+            "orc_cross_entropy_grad": (None, [f32p, f32p, f32p, I64, I64]),
             "orc_relu_backward": (None, [f32p, f32p, f32p, I64]),
             "orc_slice_cols": (None, [f32p, f32p, I64, I64, I64, I64]),
             "orc_layernorm_forward": (None, [f32p] * 6 + [I64, I64, ctypes.c_float]),
@@ -400,6 +402,20 @@ def layernorm_backward(grad, gamma, x_norm, inv_std, din, dgamma, dbeta, rows, f
     """Accumulates the backward into din, dgamma, dbeta (float32 arrays)."""
     lib().orc_layernorm_backward(_f32(grad).ravel(), _f32(gamma).ravel(), _f32(x_norm).ravel(),
                                  _f32(inv_std).ravel(), din, dgamma, dbeta, rows, features)
+
+
+def cross_entropy_loss(logits, target, classes):
+    """CrossEntropyLoss::forward (src/nn/loss.rs:49-75): batch-mean loss."""
+    logits, target = _f32(logits).ravel(), _f32(target).ravel()
+    return float(lib().orc_cross_entropy_loss(logits, target, logits.size // classes, classes))
+
+
+def cross_entropy_grad(logits, target, classes):
+    """CrossEntropyLoss::backward's seed (src/nn/loss.rs:77-106): (softmax - t) / batch."""
+    logits, target = _f32(logits).ravel(), _f32(target).ravel()
+    out = np.empty_like(logits)
+    lib().orc_cross_entropy_grad(logits, target, out, logits.size // classes, classes)
+    return out
 
 
 def relu_forward(x):

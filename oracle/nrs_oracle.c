@@ -736,6 +736,45 @@ EXPORT void orc_softmax_backward(const float *y, const float *g, float *ga, int6
     }
 }
 
+/* src/nn/loss.rs:49-75 (CrossEntropyLoss::forward): per row, max folded    */
+/* from -inf with f32::max, sum_exp = sum of exp(x - max) in class order,    */
+/* log_sum_exp = ln(sum_exp) + max; total += -t * (x - log_sum_exp) over     */
+/* rows then classes; returns total / batch.                                 */
+EXPORT float orc_cross_entropy_loss(const float *logits, const float *target, int64_t batch,
+                                    int64_t classes) {
+    float total = 0.0f;
+    for (int64_t b = 0; b < batch; ++b) {
+        const float *row = logits + b * classes;
+        float mx = -INFINITY;
+        for (int64_t c = 0; c < classes; ++c) mx = fmaxf(mx, row[c]);
+        float sum_exp = 0.0f;
+        for (int64_t c = 0; c < classes; ++c) sum_exp = sum_exp + expf(row[c] - mx);
+        const float lse = logf(sum_exp) + mx;
+        for (int64_t c = 0; c < classes; ++c) {
+            const float log_softmax = row[c] - lse;
+            total = total + (-target[b * classes + c]) * log_softmax;
+        }
+    }
+    return total / (float)batch;
+}
+
+/* src/nn/loss.rs:77-106 (CrossEntropyLoss::backward): exps = exp(x - max),  */
+/* sum in class order, grad = (exps / sum - t) / batch (assigned).           */
+EXPORT void orc_cross_entropy_grad(const float *logits, const float *target, float *grad,
+                                   int64_t batch, int64_t classes) {
+    for (int64_t b = 0; b < batch; ++b) {
+        const float *row = logits + b * classes;
+        float mx = -INFINITY;
+        for (int64_t c = 0; c < classes; ++c) mx = fmaxf(mx, row[c]);
+        float sum = 0.0f;
+        for (int64_t c = 0; c < classes; ++c) sum = sum + expf(row[c] - mx);
+        for (int64_t c = 0; c < classes; ++c) {
+            const float softmax_c = expf(row[c] - mx) / sum;
+            grad[b * classes + c] = (softmax_c - target[b * classes + c]) / (float)batch;
+        }
+    }
+}
+
 /* src/autograd/graph/relu.rs:10-45: out = x > 0 ? x : 0; ga += x > 0 ? g : 0. */
 EXPORT void orc_relu_forward(const float *x, float *out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = x[i] > 0.0f ? x[i] : 0.0f;

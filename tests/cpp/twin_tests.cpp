@@ -41,6 +41,8 @@ void orc_scale_backward(const float*, float*, float, int64_t);
 void orc_softmax_forward(const float*, float*, int64_t, int64_t);
 void orc_softmax_backward(const float*, const float*, float*, int64_t, int64_t);
 void orc_relu_forward(const float*, float*, int64_t);
+float orc_cross_entropy_loss(const float*, const float*, int64_t, int64_t);
+void orc_cross_entropy_grad(const float*, const float*, float*, int64_t, int64_t);
 void orc_relu_backward(const float*, const float*, float*, int64_t);
 void orc_slice_cols(const float*, float*, int64_t, int64_t, int64_t, int64_t);
 void orc_slice_cols_backward(const float*, float*, int64_t, int64_t, int64_t, int64_t);
@@ -161,6 +163,36 @@ void cuda_resident_linear_chain() {
     gpu::set_grad(gy, seed);
     backward_graph(gy);
     close(gy_data, y, 1e-3f, "fwd");
+    close(gpu::read_grad(gx), dx, 1e-3f, "x.grad");
+    close(gpu::read_grad(gw), dw, 1e-3f, "w.grad");
+    close(gpu::read_grad(gb), db, 1e-3f, "bias.grad");
+}
+
+// tests/cuda_ce_test.rs:10-58: cross-entropy of add(matmul(x, w), bias)
+// against one-hot rows, loss and gradients through the Linear
+void cuda_cross_entropy_through_linear() {
+    const size_t batch = 16, in_f = 24, classes = 10;
+    Vec x = formula(batch * in_f, 17, 0.1f, -0.8f), w = formula(in_f * classes, 13, 0.05f, -0.3f);
+    Vec bias = formula(classes, 5, 0.2f, -0.4f), target(batch * classes, 0.0f);
+    for (size_t b = 0; b < batch; ++b) target[b * classes + b % classes] = 1.0f;
+    Vec mm(batch * classes), logits(batch * classes), seed(batch * classes);
+    Vec dmm(batch * classes, 0.0f), db(classes, 0.0f), dx(batch * in_f, 0.0f), dw(in_f * classes, 0.0f);
+    orc_graph_matmul_forward(x.data(), w.data(), mm.data(), batch, in_f, classes);
+    orc_graph_add_bias_forward(mm.data(), bias.data(), logits.data(), batch, classes);
+    const float cpu_loss = orc_cross_entropy_loss(logits.data(), target.data(), batch, classes);
+    orc_cross_entropy_grad(logits.data(), target.data(), seed.data(), batch, classes);
+    orc_graph_add_bias_backward(seed.data(), dmm.data(), db.data(), batch, classes);
+    orc_graph_matmul_backward(x.data(), w.data(), dmm.data(), dx.data(), dw.data(), batch, in_f, classes);
+
+    NodeRef gx = resident(x, {batch, in_f}), gw = resident(w, {in_f, classes});
+    NodeRef gb = resident(bias, {classes}), gt = resident(target, {batch, classes});
+    NodeRef glogits = hip::graph::add(hip::graph::matmul(gx, gw), gb);
+    const float gpu_loss = hip::loss::cross_entropy(glogits, gt);
+    hip::loss::cross_entropy_backward(glogits, gt);
+    backward_graph(glogits);
+    if (!(std::fabs(gpu_loss - cpu_loss) < 1e-3f))
+        throw std::runtime_error("ce loss: gpu " + std::to_string(gpu_loss) + " cpu " +
+                                 std::to_string(cpu_loss));
     close(gpu::read_grad(gx), dx, 1e-3f, "x.grad");
     close(gpu::read_grad(gw), dw, 1e-3f, "w.grad");
     close(gpu::read_grad(gb), db, 1e-3f, "bias.grad");
@@ -848,6 +880,7 @@ const Case kCases[] = {
     {"cuda_resident_matmul_backward", cuda_resident_matmul_backward},
     {"cuda_resident_linear_chain", cuda_resident_linear_chain},
     {"cuda_linear", cuda_linear},
+    {"cuda_cross_entropy_through_linear", cuda_cross_entropy_through_linear},
     {"cuda_conv2d_forward", cuda_conv2d_forward},
     {"cuda_conv2d_backward", cuda_conv2d_backward},
     {"cuda_conv2d_backward_stride2", cuda_conv2d_backward_stride2},

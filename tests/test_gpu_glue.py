@@ -101,6 +101,29 @@ def test_relu_fwd_bwd_exact(hip, orc):
     assert np.array_equal(gin.to_host(), ref)
 
 
+@pytest.mark.parametrize("batch,classes", [(256, 10), (16, 10), (7, 1), (33, 100), (1, 3)])
+def test_cross_entropy_vs_oracle(hip, orc, batch, classes):
+    """nrs_cross_entropy_forward / _backward (src/cuda/loss/cross_entropy.rs:
+    18-58) against the oracle's CrossEntropyLoss (src/nn/loss.rs:49-106) on
+    one-hot rows: the batch-mean loss (the row losses summed on the host) and
+    the written seed (softmax - t) / batch, over an old gradient."""
+    rng = np.random.default_rng(batch * 1000 + classes)
+    x = (rng.standard_normal((batch, classes)) * 4).astype(np.float32)
+    t = np.zeros((batch, classes), np.float32)
+    t[np.arange(batch), rng.integers(0, classes, batch)] = 1.0
+    dx, dt = hip.DeviceBuffer.from_host(x), hip.DeviceBuffer.from_host(t)
+    rows = hip.DeviceBuffer(batch)
+    hip.call("nrs_cross_entropy_forward", rows, dx, dt, batch, classes)
+    loss = float(np.float32(rows.to_host().astype(np.float32).sum(dtype=np.float32)) / np.float32(batch))
+    want = orc.cross_entropy_loss(x, t, classes)
+    assert abs(loss - want) <= 1e-5 * max(1.0, abs(want)), (loss, want)
+    g = hip.DeviceBuffer.from_host(rng.standard_normal(batch * classes).astype(np.float32))
+    hip.call("nrs_cross_entropy_backward", g, dx, dt, batch, classes)
+    gw = orc.cross_entropy_grad(x, t, classes)
+    err = np.abs(g.to_host() - gw).max()
+    assert err <= 2e-7 + 1e-6 / batch, err
+
+
 def test_glue_argument_errors(hip):
     b = hip.DeviceBuffer(4)
     with pytest.raises(hip.NrsError):

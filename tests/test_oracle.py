@@ -441,6 +441,43 @@ def test_softmax_backward_gradcheck(orc):
     assert np.max(np.abs(ga - num)) < 1e-2
 
 
+def test_cross_entropy_closed_form_and_gradcheck(orc):
+    """CrossEntropyLoss (src/nn/loss.rs:49-106) pinned without the reference:
+    with one-hot targets the loss is the batch mean of -log softmax at the
+    target class (float64 log-sum-exp); the gradient equals central
+    differences of the oracle's own loss, each row of it sums to zero, and
+    it equals (softmax - t) / batch through the separately pinned softmax.
+    A dropped max shift, a wrong sign or a missing / batch fails one of them."""
+    rng = np.random.default_rng(23)
+    for batch, classes in [(1, 1), (5, 10), (16, 10), (3, 7)]:
+        x = (rng.standard_normal((batch, classes)) * 3).astype(np.float32)
+        cls = rng.integers(0, classes, batch)
+        t = np.zeros((batch, classes), np.float32)
+        t[np.arange(batch), cls] = 1.0
+        x64 = x.astype(np.float64)
+        m = x64.max(axis=1, keepdims=True)
+        lse = np.log(np.exp(x64 - m).sum(axis=1)) + m[:, 0]
+        want = np.mean(lse - x64[np.arange(batch), cls])
+        loss = orc.cross_entropy_loss(x, t, classes)
+        assert abs(loss - want) <= 1e-5 * max(1.0, abs(want))
+        # huge logits stay finite (the max shift)
+        assert np.isfinite(orc.cross_entropy_loss(x + np.float32(90.0), t, classes))
+        g = orc.cross_entropy_grad(x, t, classes).reshape(batch, classes)
+        assert np.max(np.abs(g.sum(axis=1))) <= 1e-6
+        sm = orc.softmax_forward(x, classes).reshape(batch, classes)
+        assert np.max(np.abs(g - (sm - t) / batch)) <= 1e-6
+        h = 1e-2
+        num = np.zeros((batch, classes))
+        for i in range(batch):
+            for c in range(classes):
+                xp, xm = x.copy(), x.copy()
+                xp[i, c] += h
+                xm[i, c] -= h
+                num[i, c] = (orc.cross_entropy_loss(xp, t, classes) -
+                             orc.cross_entropy_loss(xm, t, classes)) / (2 * h)
+        assert np.max(np.abs(g - num)) < 2e-3
+
+
 def test_relu_exact_and_mask(orc):
     rng = np.random.default_rng(9)
     x = int_matrix(rng, (300,))
