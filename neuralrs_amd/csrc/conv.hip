@@ -239,8 +239,8 @@ __global__ __launch_bounds__(256) void conv_fwd_quad_kernel(
         const bool rok = valid & ((unsigned)iy < (unsigned)H);
         const int base = (((int)n * CIN + ic) * H + iy) * W + ox;
         const f32x4 mid = buffer_load4(rx, rok ? base * 4 : kOutOfRange);
-        seg[r][0] = buffer_load1(rx, rok & (ox > 0) ? (base - 1) * 4 : kOutOfRange);
-        seg[r][5] = buffer_load1(rx, rok & (ox + 4 < W) ? (base + 4) * 4 : kOutOfRange);
+        seg[r][0] = buffer_load1(rx, (rok & (ox > 0)) ? (base - 1) * 4 : kOutOfRange);
+        seg[r][5] = buffer_load1(rx, (rok & (ox + 4 < W)) ? (base + 4) * 4 : kOutOfRange);
 #pragma unroll
         for (int u = 0; u < 4; ++u) seg[r][1 + u] = mid[u];
     }
@@ -353,6 +353,131 @@ __global__ __launch_bounds__(256) void conv_dgrad_direct_kernel(
                 if (beta != 0.0f) v = v + beta * *dst;
                 *dst = v;
             }
+    }
+}
+
+// The stride-1 input gradient of a "same" 3x3 layer with CIN <= 4 input
+// channels and rows of a multiple of 4 pixels (conv.rs:304-312 without the
+// dcols matrix). A workgroup owns one image and a band of `band` input rows;
+// a thread owns a quad of 4 pixels of one row in one of `groups` output-
+// channel groups. Per chunk of kQuadDgradOc output channels the block stages
+// the gradient rows the band's windows touch (band + 2 rows of `pitch`
+// floats: the row at columns 4 .. 4+W-1 and zero around it, each row copied
+// as 128-bit loads and stores) and the chunk's weights; a thread then reads,
+// per (oc, i), its six gradient values as one 128-bit and two 32-bit LDS
+// reads and forms
+//   dinput[c, y, x] += grad[oc, y + 1 - i, x + 1 - j] * W[oc, c, i, j]
+// for its 4 pixels, over (oc, i, j) in order. The groups' sums are added in
+// group order, then to the old dinput.
+constexpr int kQuadDgradOc = 32, kQuadDgradStage = 12;
+
+template <int CIN>
+__global__ __launch_bounds__(256) void conv_dgrad_quad_kernel(
+    float* __restrict__ dinput, const float* __restrict__ grad, const float* __restrict__ weight,
+    int c_in, int H, int W, int c_out, int band, int bands, int pitch, int groups, int qpg,
+    FastDiv div_qrow, FastDiv div_slots, FastDiv div_pq) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const int tid = threadIdx.x;
+    const int n = blockIdx.x / bands, y0 = (blockIdx.x - n * bands) * band;
+    const int rows = min(band, H - y0);
+    const int rrows = band + 2, tile = rrows * pitch, HW = H * W;
+    float* gt = lds;                                       // [oc][rrows][pitch]
+    float* wsh = lds + kQuadDgradOc * tile;                // [oc][CIN][9]
+    float* red = wsh + kQuadDgradOc * CIN * 9;             // [groups][qpg][CIN][4]
+    // this thread's quad and channel group
+    const int grp = tid / qpg, q = tid - grp * qpg;
+    uint32_t yy, qx;
+    fast_divmod((uint32_t)q, div_qrow, yy, qx);
+    const bool live = grp < groups && (int)yy < rows;
+    const int x0 = 4 * (int)qx;
+    const float* gimg = grad + (int64_t)n * c_out * HW;
+    const auto rg = buffer_rsrc(gimg, (int64_t)c_out * HW * 4);
+    const auto rw = buffer_rsrc(weight, (int64_t)c_out * c_in * 9 * 4);
+    float acc[CIN][4] = {};
+    const int slots = rrows * (pitch >> 2);  // float4 slots per channel tile
+    for (int oc0 = 0; oc0 < c_out; oc0 += kQuadDgradOc) {
+        const int nch = min(kQuadDgradOc, c_out - oc0);
+        if (oc0) __syncthreads();
+        // stage: float4 slot e of channel tile ch holds columns 4*k .. 4*k+3
+        // of tile row r, i.e. gradient row y0 - 1 + r, columns 4*k - 4 ..;
+        // a round issues all its loads (and, first, the chunk's weights
+        // [o][c][tap], zero past c_in and c_out) before any LDS store
+        constexpr int WPT = (kQuadDgradOc * CIN * 9 + 255) / 256;
+        for (int e0 = 0; e0 < nch * slots; e0 += 256 * kQuadDgradStage) {
+            float wv[WPT];
+            if (e0 == 0) {
+#pragma unroll
+                for (int k = 0; k < WPT; ++k) {
+                    const int e = tid + 256 * k;
+                    const int o = e / (CIN * 9), rem = e - o * CIN * 9, c = rem / 9, t = rem - c * 9;
+                    const bool ok = (o < nch) & (c < c_in) & (e < kQuadDgradOc * CIN * 9);
+                    wv[k] = buffer_load1(rw, ok ? (((oc0 + o) * c_in + c) * 9 + t) * 4 : kOutOfRange);
+                }
+            }
+            f32x4 v[kQuadDgradStage];
+            int dst[kQuadDgradStage];
+#pragma unroll
+            for (int u = 0; u < kQuadDgradStage; ++u) {
+                const int e = e0 + u * 256 + tid;
+                uint32_t ch, sl, r, k;
+                fast_divmod((uint32_t)e, div_slots, ch, sl);
+                fast_divmod(sl, div_pq, r, k);
+                const int gy = y0 - 1 + (int)r, gx = 4 * (int)k - 4;
+                const bool ok = (e < nch * slots) & ((unsigned)gy < (unsigned)H) & (gx >= 0) & (gx < W);
+                v[u] = buffer_load4(rg, ok ? (((oc0 + (int)ch) * H + gy) * W + gx) * 4 : kOutOfRange);
+                dst[u] = e < nch * slots ? (int)ch * tile + (int)r * pitch + 4 * (int)k : -1;
+            }
+            if (e0 == 0) {
+#pragma unroll
+                for (int k = 0; k < WPT; ++k)
+                    if (tid + 256 * k < kQuadDgradOc * CIN * 9) wsh[tid + 256 * k] = wv[k];
+            }
+#pragma unroll
+            for (int u = 0; u < kQuadDgradStage; ++u)
+                if (dst[u] >= 0) *reinterpret_cast<f32x4*>(gt + dst[u]) = v[u];
+        }
+        __syncthreads();
+        if (live) {
+            for (int o = grp; o < nch; o += groups) {
+                const float* gr0 = gt + o * tile + x0 + 4;
+                const float* wo = wsh + o * CIN * 9;
+#pragma unroll
+                for (int i = 0; i < 3; ++i) {
+                    // gradient row y + 1 - i = tile row (yy + 2 - i)
+                    const float* gr = gr0 + ((int)yy + 2 - i) * pitch;
+                    const f32x4 mid = *reinterpret_cast<const f32x4*>(gr);
+                    const float gv[6] = {gr[-1], mid[0], mid[1], mid[2], mid[3], gr[4]};
+#pragma unroll
+                    for (int j = 0; j < 3; ++j)
+#pragma unroll
+                        for (int c = 0; c < CIN; ++c) {
+                            const float w = wo[c * 9 + i * 3 + j];
+                            // pixel x0 + u reads column x0 + u + 1 - j
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) acc[c][u] += gv[u + 2 - j] * w;
+                        }
+                }
+            }
+        }
+    }
+    // the groups' sums in group order, then + old dinput
+    __syncthreads();
+    if (live) {
+#pragma unroll
+        for (int c = 0; c < CIN; ++c)
+            *reinterpret_cast<f32x4*>(red + ((grp * qpg + q) * CIN + c) * 4) =
+                f32x4{acc[c][0], acc[c][1], acc[c][2], acc[c][3]};
+    }
+    __syncthreads();
+    if (grp != 0 || !live) return;
+    float* drow = dinput + (int64_t)n * c_in * HW + (y0 + (int)yy) * W + x0;
+#pragma unroll
+    for (int c = 0; c < CIN; ++c) {
+        if (c >= c_in) break;
+        f32x4 r = *reinterpret_cast<const f32x4*>(red + (q * CIN + c) * 4);
+        for (int g2 = 1; g2 < groups; ++g2) r += *reinterpret_cast<const f32x4*>(red + ((g2 * qpg + q) * CIN + c) * 4);
+        f32x4* d = reinterpret_cast<f32x4*>(drow + (int64_t)c * HW);
+        *d = r + *d;
     }
 }
 
@@ -879,8 +1004,43 @@ int launch_out2mm(float* mm, const float* grad, const ConvDims& d) {
 // dinput += the stride-1 input gradient of a layer with c_in <= kDirectCin
 // and a kernel width the row kernel is built for, gathered from LDS;
 // kSlabUnsupported when it does not apply or its tiles do not fit.
+int quad_dgrad(float* dinput, const float* grad, const float* weight, const ConvDims& d) {
+    if (d.stride != 1 || d.c_in > 4 || d.kh != 3 || d.kw != 3 || d.pad != 1 || d.in_w % 4 ||
+        d.in_w > 64 || d.out_h != d.in_h || d.out_w != d.in_w || ((uintptr_t)dinput & 15) ||
+        ((uintptr_t)grad & 15) || d.c_out * d.in_h * d.in_w > INT32_MAX / 4 ||
+        d.c_in * d.in_h * d.in_w > INT32_MAX / 4)
+        return kSlabUnsupported;
+    const int W4 = (int)d.in_w / 4;
+    // bands of rows so that about two workgroups per CU run, whose quads
+    // fill at most 256 threads
+    int64_t bands = std::max<int64_t>(1, std::min<int64_t>(d.in_h, (2 * num_cus() + d.N - 1) / d.N));
+    int64_t band = (d.in_h + bands - 1) / bands;
+    band = std::max<int64_t>(1, std::min<int64_t>(band, 256 / W4));
+    bands = (d.in_h + band - 1) / band;
+    if (d.N * bands > INT32_MAX) return kSlabUnsupported;
+    const int qpg = (int)(band * W4);  // quads per band
+    int groups = 4;
+    while (groups > 1 && groups * qpg > 256) groups /= 2;
+    if (qpg > 256) return kSlabUnsupported;
+    const int pitch = (int)d.in_w + 8;  // 4 zero columns either side
+    const int rrows = (int)band + 2, CIN = d.c_in == 1 ? 1 : 4;
+    const size_t lds = sizeof(float) * ((size_t)kQuadDgradOc * rrows * pitch +
+                                        (size_t)kQuadDgradOc * CIN * 9 + (size_t)groups * qpg * CIN * 4);
+    if (lds > 64 * 1024) return kSlabUnsupported;
+    auto fn = CIN == 1 ? conv_dgrad_quad_kernel<1> : conv_dgrad_quad_kernel<4>;
+    hipLaunchKernelGGL(fn, dim3((unsigned)(d.N * bands)), dim3(256), lds, stream(), dinput, grad,
+                       weight, (int)d.c_in, (int)d.in_h, (int)d.in_w, (int)d.c_out, (int)band,
+                       (int)bands, pitch, groups, qpg, make_fastdiv((uint32_t)W4),
+                       make_fastdiv((uint32_t)(rrows * (pitch / 4))),
+                       make_fastdiv((uint32_t)(pitch / 4)));
+    NRS_LAUNCH_CHECK("conv2d input gradient (pixel quads)");
+    return NRS_OK;
+}
+
 int small_dgrad(float* dinput, const float* grad, const float* weight, const ConvDims& d) {
     if (d.stride != 1 || d.c_in > kDirectCin) return kSlabUnsupported;
+    const int rq = quad_dgrad(dinput, grad, weight, d);
+    if (rq != kSlabUnsupported) return rq;
     const int64_t ngx = (d.in_w + kDgradRun - 1) / kDgradRun;
     if (ngx > 256) return kSlabUnsupported;
     // row pitch: the runs' windows, whole float4s
