@@ -204,8 +204,12 @@ def bench_conv_cfg3(hip, steps, warmup, closures_only=False):
 
 def bench_mlp_cfg2(hip, steps, warmup):
     """cfg2 training step: x[256,784] -> Linear(784,128) -> ReLU ->
-    Linear(128,10) -> softmax cross-entropy gradient (softmax - onehot)/256 ->
-    backward (dW, db of both layers, dh, dx)."""
+    Linear(128,10) -> cross-entropy seed (softmax - onehot)/256 (the fused
+    ce_backward of src/cuda/loss/cross_entropy.rs:39-58) -> backward (dW, db
+    of both layers, dh, dx), in ten launches: bias and ReLU in the first
+    GEMM's epilogue, the ReLU backward masked by the activation (a > 0
+    exactly where the pre-activation is). Issued from Python here; the same
+    step issued from C++ (eagerly and as a HIP graph) is host_step()."""
     rng = np.random.default_rng(2)
     B, I, Hd, O = 256, 784, 128, 10
     D = hip.DeviceBuffer.from_host
@@ -215,34 +219,58 @@ def bench_mlp_cfg2(hip, steps, warmup):
     b1, b2 = hip.DeviceBuffer.zeros(Hd), hip.DeviceBuffer.zeros(O)
     t = np.zeros((B, O), np.float32)
     t[np.arange(B), rng.integers(0, O, B)] = 1.0
-    negt = D(-t)
-    h, a, z, sm, gz = (hip.DeviceBuffer(B * Hd), hip.DeviceBuffer(B * Hd), hip.DeviceBuffer(B * O),
-                       hip.DeviceBuffer(B * O), hip.DeviceBuffer(B * O))
+    onehot = D(t)
+    a, z, gz = hip.DeviceBuffer(B * Hd), hip.DeviceBuffer(B * O), hip.DeviceBuffer(B * O)
     ga, gh, gx = hip.DeviceBuffer(B * Hd), hip.DeviceBuffer(B * Hd), hip.DeviceBuffer(B * I)
     gw1, gw2 = hip.DeviceBuffer.zeros(I * Hd), hip.DeviceBuffer.zeros(Hd * O)
     gb1, gb2 = hip.DeviceBuffer.zeros(Hd), hip.DeviceBuffer.zeros(O)
 
     def step():
-        hip.gemm(hip.NN, h, x, w1, B, Hd, I, 0.0, b1, hip.EPI_BIAS_COL)
-        hip.call("nrs_relu_forward", a.ptr, h.ptr, B * Hd)
+        hip.gemm(hip.NN, a, x, w1, B, Hd, I, 0.0, b1, hip.EPI_BIAS_COL | hip.EPI_RELU)
         hip.gemm(hip.NN, z, a, w2, B, O, Hd, 0.0, b2, hip.EPI_BIAS_COL)
-        hip.call("nrs_softmax_forward", sm.ptr, z.ptr, B, O)
-        hip.call("nrs_vadd", gz.ptr, sm.ptr, negt.ptr, B * O)
-        hip.call("nrs_scale", gz.ptr, gz.ptr, 1.0 / B, B * O, 0.0)
+        hip.call("nrs_cross_entropy_backward", gz.ptr, z.ptr, onehot.ptr, B, O)
         hip.gemm(hip.TN, gw2, a, gz, Hd, O, B, 1.0)
         hip.call("nrs_sum_axis0", gb2.ptr, gz.ptr, B, O, 1.0)
         hip.gemm(hip.NT, ga, gz, w2, B, Hd, O)
-        hip.call("nrs_relu_backward", gh.ptr, ga.ptr, h.ptr, B * Hd, 0.0)
+        hip.call("nrs_relu_backward", gh.ptr, ga.ptr, a.ptr, B * Hd, 0.0)
         hip.gemm(hip.TN, gw1, x, gh, I, Hd, B, 1.0)
         hip.call("nrs_sum_axis0", gb1.ptr, gh.ptr, B, Hd, 1.0)
         hip.gemm(hip.NT, gx, gh, w1, B, I, Hd)
 
     us = event_ms(hip, step, steps, warmup) * 1e3
+    return {"us_per_step": us, "gemm_roof_us": mlp_gemm_roof_us()}
+
+
+def mlp_gemm_roof_us():
+    """Roofline time of cfg2's six GEMMs (each max(FLOP, bytes) bound)."""
+    B, I, Hd, O = 256, 784, 128, 10
     roof = 0.0
     for (m, n, k) in ((B, Hd, I), (B, O, Hd), (Hd, O, B), (B, Hd, O), (I, Hd, B), (B, I, Hd)):
         roof += roofline_us(*gemm_roof(m, n, k))
-    flops = 3 * (2.0 * B * I * Hd + 2.0 * B * Hd * O)
-    return {"us_per_step": us, "tflops": flops / (us * 1e-6) / 1e12, "gemm_roof_us": roof}
+    return roof
+
+
+def host_step(kind, steps, warmup):
+    """Runs neuralrs_amd/bench_host (C++, no Python between launches) for
+    `kind` ("mlp": the cfg2 step through the C ABI, eager and replayed as a
+    HIP graph; "block": the cfg4 TransformerBlock forward + backward through
+    the C++ operator surface) in a child process and returns its JSON, or
+    None when the binary is missing or fails."""
+    import subprocess
+    exe = os.path.join(ROOT, "neuralrs_amd", "bench_host")
+    if not os.path.exists(exe):
+        return None
+    try:
+        proc = subprocess.run([exe, kind, str(steps), str(warmup)], capture_output=True,
+                              text=True, timeout=300)
+    except subprocess.TimeoutExpired:
+        return None
+    if proc.returncode != 0:
+        return None
+    for line in reversed(proc.stdout.splitlines()):
+        if line.startswith("{"):
+            return json.loads(line)
+    return None
 
 
 def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
@@ -291,6 +319,21 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
         hip.bmm_backward(hip.NN, dP, dv, do, P, v, BH, T, T, Dh, 1.0)
         hip.bmm_backward(hip.NT, dq, dk, dS, q, k, BH, T, Dh, T, 1.0)
 
+    # the fused attention core (nrs_attention_forward / _backward): every
+    # head's softmax(scale Q.K^T).V in one launch, heads read and written in
+    # place in the projections' [32*128, 256] rows, scores kept on chip
+    Bf, Hf, ldf = 32, 8, 8 * Dh
+    fq, fk, fv, fdo = (D(rng.standard_normal(Bf * T * ldf).astype(np.float32)) for _ in range(4))
+    fo, fst = hip.DeviceBuffer(Bf * T * ldf), hip.DeviceBuffer(Bf * Hf * T * 2)
+    fdq, fdk, fdv = (hip.DeviceBuffer(Bf * T * ldf) for _ in range(3))
+
+    def fused_fwd():
+        hip.call("nrs_attention_forward", fo, fst, fq, fk, fv, Bf, Hf, T, Dh, ldf, sc)
+
+    def fused_bwd():
+        hip.call("nrs_attention_backward", fdq, fdk, fdv, fdo, fq, fk, fv, fst, Bf, Hf, T, Dh,
+                 ldf, sc, 0.0)
+
     # the heads of the projections [32*128, 8*32] split into [8, 4096, 32]
     # (q, k, v) and the attention output merged back: one launch each, in
     # place of the reference's per-head slice_cols / concat_cols loops
@@ -320,13 +363,17 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
 
     if closures_only:
         closures = {"attn_bmm6_cfg4": bmms_only, "heads_split_merge_cfg4": heads,
-                    "layernorm_cfg4": layernorm}
+                    "layernorm_cfg4": layernorm, "attn_fused_fwd_cfg4": fused_fwd,
+                    "attn_fused_bwd_cfg4": fused_bwd}
     else:
         fwd()
         fwd_us = event_ms(hip, fwd, steps, warmup) * 1e3
         bwd_us = event_ms(hip, bwd, steps, warmup) * 1e3
         bmm_us = event_ms(hip, bmms_only, steps, warmup) * 1e3
         bmm_acc_us = event_ms(hip, bmms_accumulate, steps, warmup) * 1e3
+        fused_fwd()
+        ffwd_us = event_ms(hip, fused_fwd, steps, warmup) * 1e3
+        fbwd_us = event_ms(hip, fused_bwd, steps, warmup) * 1e3
         heads_us = event_ms(hip, heads, steps, warmup) * 1e3
         heads_roof = roofline_us(0.0, 4 * 8.0 * Rh * Hh * Dh)  # each reads and writes 4 MB
         ln_us = event_ms(hip, layernorm, steps, warmup) * 1e3
@@ -335,6 +382,11 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
         # sums read grad and x_norm: 9 passes of 4 MB
         ln_roof = roofline_us(0.0, 9 * 4.0 * Rh * Hh * Dh)
     bmm_roof = 6 * roofline_us(*gemm_roof(T, T, Dh, BH))  # every product moves 25.2 MB
+    # the fused core's bound: the six products' FLOP at MFMA peak (forward
+    # 2, backward 4; its HBM traffic, Q/K/V/dO in and O/dQ/dK/dV out, 32 MB,
+    # takes less at 8 TB/s); the backward's recomputation of the scores is
+    # extra work, not counted
+    fused_roof = 6 * 2.0 * BH * T * T * Dh / (PEAK_FP32_MFMA_TFLOPS * 1e12) * 1e6
 
     # the block's Linear GEMMs: X[4096,256] through 4 projections and the FFN
     R, dm, ff = 32 * 128, 256, 1024
@@ -370,6 +422,7 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
     lin_flops = sum(gemm_roof(*s)[0] for s in shapes)
     lin_roof = sum(roofline_us(*gemm_roof(*s)) for s in shapes)
     return {"fwd_us": fwd_us, "bwd_us": bwd_us, "bmm_us": bmm_us, "bmm_roof_us": bmm_roof,
+            "fused_fwd_us": ffwd_us, "fused_bwd_us": fbwd_us, "fused_roof_us": fused_roof,
             "bmm_acc_us": bmm_acc_us, "heads_us": heads_us, "heads_roof_us": heads_roof,
             "ln_us": ln_us, "ln_roof_us": ln_roof,
             "linear_us": lin_us, "linear_tflops": lin_flops / (lin_us * 1e-6) / 1e12,
@@ -448,9 +501,10 @@ def cpu_baseline_gemm(a, b, target_s=10.0):
 
 def cpu_baseline_extra():
     """BASELINE's CPU plan beside the GEMM baseline: host CPU model, the
-    oracle's matmul_simd at 512^3 (cfg1) on all threads and on one, and the
-    cfg3 conv layers forward + backward (C restatement of nn::conv::Conv2d,
-    OpenMP over images) on a bounded 16-image sample, in imgs/s."""
+    oracle's matmul_simd at 512^3 (cfg1) on all threads and on one, the cfg3
+    conv layers forward + backward (C restatement of nn::conv::Conv2d,
+    OpenMP over images) on a bounded 16-image sample, in imgs/s, and cfg2's
+    six MLP GEMMs on the restated CPU autograd matmul, in us per step."""
     import oracle
     model = "unknown"
     try:
@@ -495,6 +549,32 @@ def cpu_baseline_extra():
         reps += 1
     dt = (time.perf_counter() - t0) / reps
     out["conv_cfg3_imgs_per_s"] = round(n / dt, 1)
+    # cfg2's six MLP GEMMs on the reference's CPU autograd matmul (forward
+    # and backward loops of autograd/graph/matmul.rs, single-threaded as
+    # there), on the same shapes as the GPU step
+    B, I, Hd, O = 256, 784, 128, 10
+    xm = rng.standard_normal((B, I)).astype(np.float32)
+    w1m = (rng.standard_normal((I, Hd)) * np.sqrt(2.0 / I)).astype(np.float32)
+    w2m = (rng.standard_normal((Hd, O)) * np.sqrt(2.0 / Hd)).astype(np.float32)
+    gz = (rng.standard_normal((B, O)) / B).astype(np.float32)
+    gh = rng.standard_normal((B, Hd)).astype(np.float32)
+
+    def mlp_gemms():
+        h = oracle.graph_matmul_forward(xm, w1m)
+        oracle.graph_matmul_forward(h, w2m)
+        oracle.graph_matmul_backward(h, w2m, gz)
+        oracle.graph_matmul_backward(xm, w1m, gh)
+
+    mlp_gemms()
+    mreps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 3.0:
+        mlp_gemms()
+        mreps += 1
+    mdt = (time.perf_counter() - t0) / mreps
+    out["mlp_cfg2_gemms_us_per_step"] = round(mdt * 1e6, 1)
+    out["mlp_cfg2_sample"] = (f"cfg2's 6 GEMMs (x.W1, h.W2 and their backward products, "
+                              f"156.1 MFLOP) on the C restatement of autograd/graph/matmul.rs, "
+                              f"1 thread, {mreps} reps, {mdt * 1e3:.1f} ms each")
     out["conv_cfg3_sample"] = (f"{n} images of cfg3 (conv1 1->32 @28x28, conv2 32->64 @14x14, "
                                f"forward + backward with input, weight and bias grads), "
                                f"{reps} reps, {dt * 1e3:.1f} ms each")
@@ -653,11 +733,30 @@ def main():
                 c["conv1_input_grad_roof_us"] / c["conv1_input_grad_us"], 4)}
     if not args.no_legs:
         m = bench_mlp_cfg2(hip, args.steps, 5)
-        out["mlp_cfg2"] = {"us_per_step": round(m["us_per_step"], 2),
-                           "tflops": round(m["tflops"], 3),
+        hm = host_step("mlp", 200, 20)
+        out["mlp_cfg2"] = {"python_us_per_step": round(m["us_per_step"], 2),
                            "gemm_roofline_us": round(m["gemm_roof_us"], 3),
-                           "config": "cfg2 Linear 784->128, ReLU, Linear 128->10, batch 256, "
-                                     "softmax-CE grad, fwd+bwd incl. dx"}
+                           "launches": 10,
+                           "config": "cfg2 Linear 784->128 (+bias, ReLU epilogue), Linear 128->10, "
+                                     "batch 256, fused CE grad, fwd+bwd incl. dx and both bias "
+                                     "grads"}
+        if hm:
+            out["mlp_cfg2"].update({
+                "us_per_step": round(hm["eager_gpu_us"], 2),
+                "graph_us_per_step": round(hm["graph_gpu_us"], 2),
+                "gemm_roofline_frac": round(m["gemm_roof_us"] / hm["eager_gpu_us"], 4),
+                "timing": "C++ issue (neuralrs_amd/bench_host mlp), HIP events on the stream"})
+        hb = host_step("block", 50, 10)
+        if hb:
+            gemm_roof = hb["gemm_flop_per_step"] / (PEAK_FP32_MFMA_TFLOPS * 1e12) * 1e6
+            out["transformer_block_cfg4"] = {
+                "step_us": round(hb["step_gpu_us"], 2), "fwd_us": round(hb["fwd_gpu_us"], 2),
+                "gemm_flop_per_step": hb["gemm_flop_per_step"],
+                "gemm_roofline_us": round(gemm_roof, 2),
+                "gemm_roofline_frac": round(gemm_roof / hb["step_gpu_us"], 4),
+                "config": "cfg4 TransformerBlock B32 S128 d256 h8 dff1024 forward + backward "
+                          "through the C++ operator surface (libnrs_host.so), from C++",
+                "timing": "neuralrs_amd/bench_host block, HIP events on the stream"}
         at = bench_attention_cfg4(hip, args.steps, 5)
         out["attention_cfg4"] = {
             "bmm_us": round(at["bmm_us"], 2), "bmm_roofline_us": round(at["bmm_roof_us"], 2),
@@ -668,10 +767,15 @@ def main():
             "layernorm_fwd_bwd_us": round(at["ln_us"], 2),
             "layernorm_roofline_frac": round(at["ln_roof_us"] / at["ln_us"], 4),
             "attn_fwd_us": round(at["fwd_us"], 2), "attn_bwd_us": round(at["bwd_us"], 2),
+            "fused_fwd_us": round(at["fused_fwd_us"], 2),
+            "fused_bwd_us": round(at["fused_bwd_us"], 2),
+            "fused_roofline_us": round(at["fused_roof_us"], 2),
+            "fused_roofline_frac": round(at["fused_roof_us"] / (at["fused_fwd_us"] + at["fused_bwd_us"]), 4),
             "linear_us": round(at["linear_us"], 2), "linear_tflops": round(at["linear_tflops"], 2),
             "linear_roofline_frac": round(at["linear_roof_us"] / at["linear_us"], 4),
-            "config": "cfg4 batch 32 x 8 heads, seq 128, d_head 32: 6 bmm (QK^T, PV and the 4 "
-                      "backward products) + 4 proj and 2 FFN Linear GEMMs fwd+bwd"}
+            "config": "cfg4 batch 32 x 8 heads, seq 128, d_head 32: the fused attention core "
+                      "(fused_*), the same core as 6 bmm (QK^T, PV and the 4 backward products) "
+                      "+ softmax launches (attn_*, bmm_*), 4 proj and 2 FFN Linear GEMMs fwd+bwd"}
         out["gemm_sweep_cfg5"] = bench_sweep_cfg5(hip, args.steps)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_gemm(g["a"], g["b"])
