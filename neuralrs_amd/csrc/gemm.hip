@@ -174,9 +174,13 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool d
         // 32x8192x8192 GEMM measured 67.8 us against 72.4 us at 24), each
         // slice at least two k-tiles, at most 256 slices (the reduction reads
         // every slice of every output).
+        // Grids of 16 or more tiles keep at least 8 k-tiles per slice: their
+        // partials are big, and a 3-k-tile slice is all latency (the cfg4
+        // weight gradient 256x256 over K = 4096: 43 slices 19.4 us, 16
+        // slices 14.9 us).
         const int64_t per_cu = pl.tile == T32x256 ? 1 : 3;
         const int64_t want = std::min<int64_t>(256, cdiv(per_cu * (int64_t)cus, tiles));
-        const int64_t max_by_k = std::max<int64_t>(1, K / (2 * s.bk));
+        const int64_t max_by_k = std::max<int64_t>(1, K / ((tiles >= 16 ? 8 : 2) * s.bk));
         slices = (int)std::min<int64_t>(want, max_by_k);
     }
     if (slices < 1) slices = 1;
