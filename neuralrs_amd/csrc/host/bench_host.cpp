@@ -107,7 +107,7 @@ int bench_block(int steps, int warmup) {
     DeviceBuffer seed = DeviceBuffer::from_host(normal(B * S * D, 1.0f));
     auto step = [&] {
         NodeRef out = tb.forward(x);
-        nrs_check(nrs_memcpy_dtod(out->gpu->grad->ptr(), seed.ptr(), seed.len() * sizeof(float)),
+        nrs_check(nrs_memcpy_dtod(out->gpu->grad->write_target(), seed.ptr(), seed.len() * sizeof(float)),
                   "seed");
         backward_graph(out);
         gpu::zero_grad(params);

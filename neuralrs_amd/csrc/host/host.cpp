@@ -6,6 +6,7 @@
 #include "neuralrs.hpp"
 
 #include <cmath>
+#include <initializer_list>
 #include <unordered_set>
 
 #include "nrs_hip.h"
@@ -42,22 +43,51 @@ NodeRef make_output(std::vector<size_t> shape, std::vector<NodeRef> parents, Dev
     return out;
 }
 
+// accumulate_into (src/cuda/runtime.rs): dst += src over len elements. A
+// destination that is still a pending zero takes a copy instead.
+void accumulate_into(DeviceBuffer& dst, const float* src, size_t len) {
+    if (dst.pending_zero()) {
+        check(nrs_memcpy_dtod(dst.write_target(), src, len * sizeof(float)),
+              "accumulate copy failed");
+        return;
+    }
+    check(nrs_accumulate(dst.ptr(), src, len), "accumulate launch failed");
+}
+
+// The one beta of a launch that stores value + beta * old into several
+// distinct buffers: 0 when all of them are pending zeros, else 1 (any pending
+// zero among them is cleared first).
+float joint_beta(std::initializer_list<DeviceBuffer*> bufs) {
+    bool all_pending = true;
+    for (DeviceBuffer* b : bufs) all_pending = all_pending && b->pending_zero();
+    for (DeviceBuffer* b : bufs) {
+        if (all_pending)
+            b->write_target();
+        else
+            b->ptr();
+    }
+    return all_pending ? 0.0f : 1.0f;
+}
+
 // The backward closure of a bmm node (bmm.rs:93-131): both gradients
-// accumulated (beta 1) into the parents, in one launch for small items. When
-// a and b are the same node the two gradients go to one buffer, one product
-// after the other.
+// accumulated into the parents, in one launch for small items. When a and b
+// are the same node the two gradients go to one buffer, one product after the
+// other.
 void bmm_backward_into(int layout, const NodeRef& a, const NodeRef& b, const float* g,
                        size_t batch, size_t m, size_t k, size_t n, const char* what) {
     GpuBuffers& ag = gpu_of(a, "backward: lhs not on GPU");
     GpuBuffers& bg = gpu_of(b, "backward: rhs not on GPU");
     if (ag.grad != bg.grad) {
-        check(nrs_bmm_backward(layout, ag.grad->ptr(), bg.grad->ptr(), g, ag.data.ptr(),
-                               bg.data.ptr(), batch, m, k, n, 1.0f),
+        const float beta = joint_beta({ag.grad.get(), bg.grad.get()});
+        check(nrs_bmm_backward(layout, ag.grad->write_target(), bg.grad->write_target(), g,
+                               ag.data.ptr(), bg.data.ptr(), batch, m, k, n, beta),
               what);
         return;
     }
-    check(nrs_bmm_backward(layout, ag.grad->ptr(), nullptr, g, ag.data.ptr(), bg.data.ptr(), batch,
-                           m, k, n, 1.0f),
+    float beta = 1.0f;
+    float* da = ag.grad->acc_target(beta);
+    check(nrs_bmm_backward(layout, da, nullptr, g, ag.data.ptr(), bg.data.ptr(), batch, m, k, n,
+                           beta),
           what);
     check(nrs_bmm_backward(layout, nullptr, bg.grad->ptr(), g, ag.data.ptr(), bg.data.ptr(), batch,
                            m, k, n, 1.0f),
@@ -74,11 +104,15 @@ void build_topo(const NodeRef& n, std::unordered_set<const Node*>& visited,
 }  // namespace
 
 // ------------------------------------------------------------ DeviceBuffer
-DeviceBuffer::DeviceBuffer(size_t len, bool zero) : len_(len) {
+DeviceBuffer::DeviceBuffer(size_t len, bool zero) : len_(len), pending_zero_(zero) {
     void* p = nullptr;
     check(nrs_malloc(&p, len * sizeof(float)), "device alloc failed");
     ptr_ = static_cast<float*>(p);
-    if (zero) check(nrs_memset_zero(ptr_, len * sizeof(float)), "device memset failed");
+}
+
+void DeviceBuffer::clear_now() const {
+    check(nrs_memset_zero(ptr_, len_ * sizeof(float)), "device memset failed");
+    pending_zero_ = false;
 }
 
 DeviceBuffer DeviceBuffer::from_host(const std::vector<float>& v) {
@@ -91,9 +125,11 @@ DeviceBuffer::~DeviceBuffer() {
     if (ptr_) nrs_free(ptr_);
 }
 
-DeviceBuffer::DeviceBuffer(DeviceBuffer&& o) noexcept : ptr_(o.ptr_), len_(o.len_) {
+DeviceBuffer::DeviceBuffer(DeviceBuffer&& o) noexcept
+    : ptr_(o.ptr_), len_(o.len_), pending_zero_(o.pending_zero_) {
     o.ptr_ = nullptr;
     o.len_ = 0;
+    o.pending_zero_ = false;
 }
 
 DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
@@ -101,19 +137,25 @@ DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
         if (ptr_) nrs_free(ptr_);
         ptr_ = o.ptr_;
         len_ = o.len_;
+        pending_zero_ = o.pending_zero_;
         o.ptr_ = nullptr;
         o.len_ = 0;
+        o.pending_zero_ = false;
     }
     return *this;
 }
 
 std::vector<float> DeviceBuffer::to_host() const {
     std::vector<float> v(len_);
+    if (pending_zero_) {
+        check(nrs_sync(), "synchronize failed");
+        return v;
+    }
     check(nrs_memcpy_dtoh(v.data(), ptr_, len_ * sizeof(float)), "dtoh failed");
     return v;
 }
 
-void DeviceBuffer::zero() { check(nrs_memset_zero(ptr_, len_ * sizeof(float)), "memset failed"); }
+void DeviceBuffer::zero() { pending_zero_ = true; }
 
 // -------------------------------------------------------------------- Node
 NodeRef Node::create(std::vector<float> data, std::vector<size_t> shape) {
@@ -186,12 +228,15 @@ NodeRef matmul(const NodeRef& a, const NodeRef& b) {
     node->backward_fn = [grad = node->gpu->grad, a, b, m, k, n](const std::vector<float>&) {
         GpuBuffers& ag = gpu_of(a, "cuda matmul bwd: lhs not on GPU");
         GpuBuffers& bg = gpu_of(b, "cuda matmul bwd: rhs not on GPU");
+        float beta = 1.0f;
         // dA += dC . B^T   (matmul_nt, then accumulate_into: matmul.rs:418-423)
-        check(nrs_gemm(NRS_NT, ag.grad->ptr(), grad->ptr(), bg.data.ptr(), m, k, n, 1.0f, nullptr,
+        float* da = ag.grad->acc_target(beta);
+        check(nrs_gemm(NRS_NT, da, grad->ptr(), bg.data.ptr(), m, k, n, beta, nullptr,
                        NRS_EPI_NONE),
               "cuda matmul bwd: launch failed");
         // dB += A^T . dC   (matmul_tn, then accumulate_into: matmul.rs:425-431)
-        check(nrs_gemm(NRS_TN, bg.grad->ptr(), ag.data.ptr(), grad->ptr(), k, n, m, 1.0f, nullptr,
+        float* db = bg.grad->acc_target(beta);
+        check(nrs_gemm(NRS_TN, db, ag.data.ptr(), grad->ptr(), k, n, m, beta, nullptr,
                        NRS_EPI_NONE),
               "cuda matmul bwd: launch failed");
     };
@@ -231,13 +276,15 @@ NodeRef add(const NodeRef& a, const NodeRef& b) {
     const size_t rows = broadcast ? a->shape[0] : 0, cols = broadcast ? a->shape[1] : 0;
     node->backward_fn = [grad = node->gpu->grad, a, b, len, broadcast, rows,
                          cols](const std::vector<float>&) {
-        check(nrs_accumulate(gpu_of(a, "backward: parent not on GPU").grad->ptr(), grad->ptr(), len),
-              "accumulate launch failed");
-        float* bgrad = gpu_of(b, "backward: parent not on GPU").grad->ptr();
-        if (broadcast)  // bias gradient: column sums (add.rs:91-100, reduce.rs:28-43)
-            check(nrs_sum_axis0(bgrad, grad->ptr(), rows, cols, 1.0f), "sum_axis0 launch failed");
-        else
-            check(nrs_accumulate(bgrad, grad->ptr(), len), "accumulate launch failed");
+        accumulate_into(*gpu_of(a, "backward: parent not on GPU").grad, grad->ptr(), len);
+        DeviceBuffer& bgrad = *gpu_of(b, "backward: parent not on GPU").grad;
+        if (broadcast) {  // bias gradient: column sums (add.rs:91-100, reduce.rs:28-43)
+            float beta = 1.0f;
+            float* db = bgrad.acc_target(beta);
+            check(nrs_sum_axis0(db, grad->ptr(), rows, cols, beta), "sum_axis0 launch failed");
+        } else {
+            accumulate_into(bgrad, grad->ptr(), len);
+        }
     };
     return node;
 }
@@ -256,10 +303,15 @@ NodeRef transpose(const NodeRef& a) {
     NodeRef node = make_output(shape, {a}, std::move(out));
     node->backward_fn = [grad = node->gpu->grad, a, batch, rows, cols, len](const std::vector<float>&) {
         // the gradient is [.., cols, rows]: transpose back, then accumulate (transpose.rs:53-69)
+        DeviceBuffer& agrad = *gpu_of(a, "backward: parent not on GPU").grad;
+        if (agrad.pending_zero()) {  // nothing to add to: transpose straight into it
+            check(nrs_transpose(agrad.write_target(), grad->ptr(), batch, cols, rows),
+                  "cuda transpose bwd: launch");
+            return;
+        }
         DeviceBuffer tmp(len, false);
         check(nrs_transpose(tmp.ptr(), grad->ptr(), batch, cols, rows), "cuda transpose bwd: launch");
-        check(nrs_accumulate(gpu_of(a, "backward: parent not on GPU").grad->ptr(), tmp.ptr(), len),
-              "accumulate launch failed");
+        accumulate_into(agrad, tmp.ptr(), len);
     };
     return node;
 }
@@ -271,8 +323,9 @@ NodeRef scale(const NodeRef& a, float s) {
     check(nrs_scale(out.ptr(), ag.data.ptr(), s, len, 0.0f), "cuda scale: launch failed");
     NodeRef node = make_output(a->shape, {a}, std::move(out));
     node->backward_fn = [grad = node->gpu->grad, a, s, len](const std::vector<float>&) {
-        check(nrs_scale(gpu_of(a, "backward: parent not on GPU").grad->ptr(), grad->ptr(), s, len, 1.0f),
-              "cuda scale bwd: launch");
+        float beta = 1.0f;
+        float* ga = gpu_of(a, "backward: parent not on GPU").grad->acc_target(beta);
+        check(nrs_scale(ga, grad->ptr(), s, len, beta), "cuda scale bwd: launch");
     };
     return node;
 }
@@ -289,8 +342,9 @@ NodeRef softmax(const NodeRef& a) {
     // alive whenever the closure runs.
     const float* y = node->gpu->data.ptr();
     node->backward_fn = [grad = node->gpu->grad, a, y, rows, width](const std::vector<float>&) {
-        check(nrs_softmax_backward(gpu_of(a, "cuda softmax bwd: input not on GPU").grad->ptr(), y,
-                                   grad->ptr(), rows, width, 1.0f),
+        float beta = 1.0f;
+        float* ga = gpu_of(a, "cuda softmax bwd: input not on GPU").grad->acc_target(beta);
+        check(nrs_softmax_backward(ga, y, grad->ptr(), rows, width, beta),
               "cuda softmax bwd: launch");
     };
     return node;
@@ -304,7 +358,9 @@ NodeRef relu(const NodeRef& a) {
     NodeRef node = make_output(a->shape, {a}, std::move(out));
     node->backward_fn = [grad = node->gpu->grad, a, len](const std::vector<float>&) {
         GpuBuffers& g = gpu_of(a, "cuda relu bwd: input not on GPU");
-        check(nrs_relu_backward(g.grad->ptr(), grad->ptr(), g.data.ptr(), len, 1.0f),
+        float beta = 1.0f;
+        float* ga = g.grad->acc_target(beta);
+        check(nrs_relu_backward(ga, grad->ptr(), g.data.ptr(), len, beta),
               "cuda relu bwd: launch");
     };
     return node;
@@ -381,8 +437,9 @@ NodeRef scaled_softmax(const NodeRef& a, float s) {
     NodeRef node = make_output(a->shape, {a}, std::move(out));
     const float* y = node->gpu->data.ptr();
     node->backward_fn = [grad = node->gpu->grad, a, y, rows, width, s](const std::vector<float>&) {
-        check(nrs_softmax_backward_scaled(gpu_of(a, "cuda softmax bwd: input not on GPU").grad->ptr(),
-                                          y, grad->ptr(), rows, width, s, 1.0f),
+        float beta = 1.0f;
+        float* ga = gpu_of(a, "cuda softmax bwd: input not on GPU").grad->acc_target(beta);
+        check(nrs_softmax_backward_scaled(ga, y, grad->ptr(), rows, width, s, beta),
               "cuda softmax bwd: launch");
     };
     return node;
@@ -397,8 +454,7 @@ NodeRef reshape(const NodeRef& a, std::vector<size_t> shape) {
           "cuda reshape: launch failed");
     NodeRef node = make_output(std::move(shape), {a}, std::move(out));
     node->backward_fn = [grad = node->gpu->grad, a, len](const std::vector<float>&) {
-        check(nrs_accumulate(gpu_of(a, "backward: parent not on GPU").grad->ptr(), grad->ptr(), len),
-              "accumulate launch failed");
+        accumulate_into(*gpu_of(a, "backward: parent not on GPU").grad, grad->ptr(), len);
     };
     return node;
 }
@@ -420,7 +476,7 @@ float cross_entropy(const NodeRef& pred, const NodeRef& target) {
     const auto [batch, classes] = batch_classes(pred);
     GpuBuffers& p = gpu_of(pred, "cuda ce: logits not on GPU");
     GpuBuffers& t = gpu_of(target, "cuda ce: target not on GPU");
-    DeviceBuffer row_loss(batch, true);
+    DeviceBuffer row_loss(batch, false);
     check(nrs_cross_entropy_forward(row_loss.ptr(), p.data.ptr(), t.data.ptr(), batch, classes),
           "cuda ce: forward launch failed");
     const std::vector<float> host = row_loss.to_host();
@@ -433,7 +489,8 @@ void cross_entropy_backward(const NodeRef& pred, const NodeRef& target) {
     const auto [batch, classes] = batch_classes(pred);
     GpuBuffers& p = gpu_of(pred, "cuda ce: logits not on GPU");
     GpuBuffers& t = gpu_of(target, "cuda ce: target not on GPU");
-    check(nrs_cross_entropy_backward(p.grad->ptr(), p.data.ptr(), t.data.ptr(), batch, classes),
+    check(nrs_cross_entropy_backward(p.grad->write_target(), p.data.ptr(), t.data.ptr(), batch,
+                                     classes),
           "cuda ce: backward launch failed");
 }
 
@@ -498,14 +555,17 @@ NodeRef Linear::forward(const NodeRef& input) const {
         GpuBuffers& xg = gpu_of(x, "cuda matmul bwd: lhs not on GPU");
         GpuBuffers& wg = gpu_of(w, "cuda matmul bwd: rhs not on GPU");
         GpuBuffers& bg = gpu_of(b, "backward: parent not on GPU");
-        check(nrs_gemm(NRS_NT, xg.grad->ptr(), grad->ptr(), wg.data.ptr(), batch, in_f, out_f, 1.0f,
-                       nullptr, NRS_EPI_NONE),
+        float beta = 1.0f;
+        float* dx = xg.grad->acc_target(beta);
+        check(nrs_gemm(NRS_NT, dx, grad->ptr(), wg.data.ptr(), batch, in_f, out_f, beta, nullptr,
+                       NRS_EPI_NONE),
               "cuda linear bwd: dx launch");
-        check(nrs_gemm(NRS_TN, wg.grad->ptr(), xg.data.ptr(), grad->ptr(), in_f, out_f, batch, 1.0f,
-                       nullptr, NRS_EPI_NONE),
+        float* dw = wg.grad->acc_target(beta);
+        check(nrs_gemm(NRS_TN, dw, xg.data.ptr(), grad->ptr(), in_f, out_f, batch, beta, nullptr,
+                       NRS_EPI_NONE),
               "cuda linear bwd: dw launch");
-        check(nrs_sum_axis0(bg.grad->ptr(), grad->ptr(), batch, out_f, 1.0f),
-              "cuda linear bwd: bias launch");
+        float* db = bg.grad->acc_target(beta);
+        check(nrs_sum_axis0(db, grad->ptr(), batch, out_f, beta), "cuda linear bwd: bias launch");
     };
     return node;
 }
@@ -548,8 +608,9 @@ NodeRef split_heads(const NodeRef& x, size_t rows, size_t heads, size_t w,
           "cuda slice_cols: launch failed");
     NodeRef node = make_output(std::move(shape), {x}, std::move(out));
     node->backward_fn = [grad = node->gpu->grad, x, rows, heads, w](const std::vector<float>&) {
-        check(nrs_merge_heads(gpu_of(x, "backward: parent not on GPU").grad->ptr(), grad->ptr(),
-                              rows, heads, w, 1.0f),
+        float beta = 1.0f;
+        float* gx = gpu_of(x, "backward: parent not on GPU").grad->acc_target(beta);
+        check(nrs_merge_heads(gx, grad->ptr(), rows, heads, w, beta),
               "cuda slice_cols bwd: launch");
     };
     return node;
@@ -565,8 +626,9 @@ NodeRef merge_heads(const NodeRef& x, size_t rows, size_t heads, size_t w,
           "cuda concat_cols: write launch failed");
     NodeRef node = make_output(std::move(shape), {x}, std::move(out));
     node->backward_fn = [grad = node->gpu->grad, x, rows, heads, w](const std::vector<float>&) {
-        check(nrs_split_heads(gpu_of(x, "backward: part not on GPU").grad->ptr(), grad->ptr(), rows,
-                              heads, w, 1.0f),
+        float beta = 1.0f;
+        float* gx = gpu_of(x, "backward: part not on GPU").grad->acc_target(beta);
+        check(nrs_split_heads(gx, grad->ptr(), rows, heads, w, beta),
               "cuda concat_cols bwd: launch");
     };
     return node;
@@ -595,21 +657,23 @@ NodeRef fused_attention(const NodeRef& q, const NodeRef& k, const NodeRef& v, si
         GpuBuffers& kg = gpu_of(k, "attention bwd: k not on GPU");
         GpuBuffers& vg = gpu_of(v, "attention bwd: v not on GPU");
         if (qg.grad != kg.grad && kg.grad != vg.grad && qg.grad != vg.grad) {
-            check(nrs_attention_backward(qg.grad->ptr(), kg.grad->ptr(), vg.grad->ptr(),
-                                         grad->ptr(), qg.data.ptr(), kg.data.ptr(), vg.data.ptr(),
-                                         stats->ptr(), batch, heads, seq, dh, ld, scale, 1.0f),
+            const float beta = joint_beta({qg.grad.get(), kg.grad.get(), vg.grad.get()});
+            check(nrs_attention_backward(qg.grad->write_target(), kg.grad->write_target(),
+                                         vg.grad->write_target(), grad->ptr(), qg.data.ptr(),
+                                         kg.data.ptr(), vg.data.ptr(), stats->ptr(), batch, heads,
+                                         seq, dh, ld, scale, beta),
                   "attention bwd: launch");
             return;
         }
         // q, k or v are one node: the gradients go to temporaries, then add up
-        DeviceBuffer tq(len, true), tk(len, true), tv(len, true);
+        DeviceBuffer tq(len, false), tk(len, false), tv(len, false);
         check(nrs_attention_backward(tq.ptr(), tk.ptr(), tv.ptr(), grad->ptr(), qg.data.ptr(),
                                      kg.data.ptr(), vg.data.ptr(), stats->ptr(), batch, heads, seq,
                                      dh, ld, scale, 0.0f),
               "attention bwd: launch");
-        check(nrs_accumulate(qg.grad->ptr(), tq.ptr(), len), "accumulate launch failed");
-        check(nrs_accumulate(kg.grad->ptr(), tk.ptr(), len), "accumulate launch failed");
-        check(nrs_accumulate(vg.grad->ptr(), tv.ptr(), len), "accumulate launch failed");
+        accumulate_into(*qg.grad, tq.ptr(), len);
+        accumulate_into(*kg.grad, tk.ptr(), len);
+        accumulate_into(*vg.grad, tv.ptr(), len);
     };
     return node;
 }
@@ -709,8 +773,12 @@ NodeRef layernorm(const NodeRef& input, const NodeRef& gamma, const NodeRef& bet
         GpuBuffers& ig = gpu_of(input, "cuda layernorm bwd: input not on GPU");
         GpuBuffers& gg = gpu_of(gamma, "cuda layernorm bwd: gamma not on GPU");
         GpuBuffers& bg = gpu_of(beta, "cuda layernorm bwd: beta not on GPU");
+        // one beta for the three gradients, unless gamma and beta are one node
+        const bool distinct = ig.grad != gg.grad && ig.grad != bg.grad && gg.grad != bg.grad;
+        const float acc =
+            distinct ? joint_beta({ig.grad.get(), gg.grad.get(), bg.grad.get()}) : 1.0f;
         check(nrs_layernorm_backward(ig.grad->ptr(), gg.grad->ptr(), bg.grad->ptr(), grad->ptr(),
-                                     gg.data.ptr(), xn->ptr(), istd->ptr(), rows, F, 1.0f),
+                                     gg.data.ptr(), xn->ptr(), istd->ptr(), rows, F, acc),
               "cuda layernorm bwd: launch");
     };
     return node;

@@ -43,6 +43,14 @@ struct Panic : std::runtime_error {
 enum class Device { CPU, GPU };
 
 // Owning f32 device allocation: the reference's CudaSlice<f32>.
+//
+// A zeroed buffer (alloc_zeros, memset_zeros) is zero in value at once but its
+// memory is cleared only when first needed: ptr() clears it first, while a
+// kernel that writes every element as value + beta * old takes the pointer
+// from acc_target(), which hands out beta 0 instead of clearing (and a kernel
+// that overwrites every element takes write_target()). Gradient buffers are
+// created zeroed and their first contribution is usually such a kernel, so a
+// backward pass mostly skips the clearing launches.
 class DeviceBuffer {
 public:
     DeviceBuffer() = default;
@@ -54,14 +62,35 @@ public:
     DeviceBuffer(const DeviceBuffer&) = delete;
     DeviceBuffer& operator=(const DeviceBuffer&) = delete;
 
-    float* ptr() const { return ptr_; }
+    // Device memory holding the buffer's value (a pending zero is cleared
+    // first).
+    float* ptr() const {
+        if (pending_zero_) clear_now();
+        return ptr_;
+    }
+    // For a launch that stores value + beta * old in every element: sets
+    // beta (0 while the buffer is a pending zero, else 1) and returns memory
+    // that holds the buffer's value once the launch is enqueued.
+    float* acc_target(float& beta) {
+        beta = pending_zero_ ? 0.0f : 1.0f;
+        pending_zero_ = false;
+        return ptr_;
+    }
+    // For a launch that overwrites every element without reading it.
+    float* write_target() {
+        pending_zero_ = false;
+        return ptr_;
+    }
+    bool pending_zero() const { return pending_zero_; }
     size_t len() const { return len_; }
     std::vector<float> to_host() const;  // stream.clone_dtoh (synchronises)
     void zero();                          // stream.memset_zeros
 
 private:
+    void clear_now() const;
     float* ptr_ = nullptr;
     size_t len_ = 0;
+    mutable bool pending_zero_ = false;
 };
 
 // src/autograd/node.rs:49-53: device data plus a shared, swappable gradient.

@@ -798,6 +798,59 @@ void attention_batch_self() {
     close(gpu::read_grad(gx), want, 1e-3f, "self-attention dx");
 }
 
+// Gradients over several backward passes (src/autograd/node.rs:113-151
+// accumulates into every parent): parents used twice (w in matmul(w, w), h in
+// relu(h) and add(r, h)) collect both contributions, a second graph over the
+// same leaves adds to their gradients, zero_grad makes them read zero, and a
+// third pass starts again from zero.
+void grads_accumulate_and_zero() {
+    const size_t m = 24, k = 16;
+    const Vec x = formula(m * k, 11, 0.1f, -0.5f), w = formula(k * k, 7, 0.08f, -0.25f);
+    const Vec seed = formula(k * m, 5, 0.2f, -0.4f);
+    Vec p(k * k), h(m * k), r(m * k), s(m * k), t(k * m), u(k * m);
+    orc_graph_matmul_forward(w.data(), w.data(), p.data(), k, k, k);
+    orc_graph_matmul_forward(x.data(), p.data(), h.data(), m, k, k);
+    orc_relu_forward(h.data(), r.data(), m * k);
+    for (size_t i = 0; i < m * k; ++i) s[i] = r[i] + h[i];
+    orc_transpose(s.data(), t.data(), 1, m, k);
+    orc_scale(t.data(), u.data(), 0.5f, k * m);
+    Vec dt(k * m, 0.0f), ds(m * k, 0.0f), dh(m * k, 0.0f), dp(k * k, 0.0f), dx(m * k, 0.0f),
+        dw(k * k, 0.0f);
+    orc_scale_backward(seed.data(), dt.data(), 0.5f, k * m);
+    orc_transpose_backward(dt.data(), ds.data(), 1, m, k);
+    for (size_t i = 0; i < m * k; ++i) dh[i] += ds[i];      // add: dh += ds (dr = ds)
+    orc_relu_backward(h.data(), ds.data(), dh.data(), m * k);  // relu: dh += relu'(h) dr
+    orc_graph_matmul_backward(x.data(), p.data(), dh.data(), dx.data(), dp.data(), m, k, k);
+    orc_graph_matmul_backward(w.data(), w.data(), dp.data(), dw.data(), dw.data(), k, k, k);
+
+    NodeRef gx = resident(x, {m, k}), gw = resident(w, {k, k});
+    auto pass = [&] {
+        NodeRef gp = hip::graph::matmul(gw, gw);
+        NodeRef gh = hip::graph::matmul(gx, gp);
+        NodeRef gs = hip::graph::add(hip::graph::relu(gh), gh);
+        NodeRef out =
+            hip::graph::reshape(hip::graph::scale(hip::graph::transpose(gs), 0.5f), {k * m});
+        gpu::set_grad(out, seed);
+        backward_graph(out);
+        return gpu::to_host(out);
+    };
+    close(pass(), u, 1e-3f, "pass 1 fwd");
+    close(gpu::read_grad(gx), dx, 1e-3f, "pass 1 x.grad");
+    close(gpu::read_grad(gw), dw, 1e-3f, "pass 1 w.grad");
+    pass();
+    Vec dx2(dx), dw2(dw);
+    for (float& v : dx2) v *= 2.0f;
+    for (float& v : dw2) v *= 2.0f;
+    close(gpu::read_grad(gx), dx2, 2e-3f, "pass 2 x.grad");
+    close(gpu::read_grad(gw), dw2, 2e-3f, "pass 2 w.grad");
+    gpu::zero_grad({gx, gw});
+    close(gpu::read_grad(gx), Vec(m * k, 0.0f), 1e-30f, "zeroed x.grad");
+    close(gpu::read_grad(gw), Vec(k * k, 0.0f), 1e-30f, "zeroed w.grad");
+    pass();
+    close(gpu::read_grad(gx), dx, 1e-3f, "pass 3 x.grad");
+    close(gpu::read_grad(gw), dw, 1e-3f, "pass 3 w.grad");
+}
+
 // |gpu - cpu| <= abs_tol + rel * max|cpu| elementwise; prints the largest
 // error against the scale so the margin is on record.
 void close_scaled(const Vec& g, const Vec& c, float abs_tol, float rel, const std::string& what) {
@@ -903,6 +956,7 @@ const Case kCases[] = {
     {"mha_batch_split_heads", mha_batch_split_heads},
     {"attention_fused_2d", attention_fused_2d},
     {"attention_batch_self", attention_batch_self},
+    {"grads_accumulate_and_zero", grads_accumulate_and_zero},
 };
 
 int main(int argc, char** argv) {
