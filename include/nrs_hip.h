@@ -98,6 +98,30 @@ int nrs_gemm(int layout, float *C, const float *A, const float *B,
              int64_t rows, int64_t cols, int64_t inner,
              float beta, const float *bias, int epilogue);
 
+/* Several mm calls in one launch: the two gradient products of a matmul
+ * node's backward closure (src/cuda/graph/matmul.rs:418-431: matmul_nt for dA
+ * and matmul_tn for dB, each followed by accumulate_into) or the projections
+ * of one input (src/cuda/nn/multihead.rs:64-66, three matmuls of x). Each
+ * descriptor means exactly nrs_gemm with its fields; at most
+ * NRS_GEMM_GROUP_MAX of them. When every call is dense, 16-byte aligned with
+ * rows of whole float4s and no output overlaps another call's output or
+ * operands, their workgroups share one grid (one problem's load latency,
+ * barriers and epilogue overlap another's matrix-core work); otherwise the
+ * calls run one after another in the order given. Results equal nrs_gemm's to
+ * the GEMM tolerance (the tiling, hence the summation order, may differ).   */
+#define NRS_GEMM_GROUP_MAX 4
+typedef struct nrs_gemm_desc {
+    int layout;
+    float *C;
+    const float *A;
+    const float *B;
+    int64_t rows, cols, inner;
+    float beta;
+    const float *bias;
+    int epilogue;
+} nrs_gemm_desc;
+int nrs_gemm_group(const nrs_gemm_desc *descs, int count);
+
 /* mm_nt_splitk(a, b, rows, cols, inner) (src/cuda/graph/matmul.rs:354-379):
  * C = A[rows,inner] . B[cols,inner]^T + beta*C for skinny outputs with a huge
  * inner dimension. The inner dimension is split across workgroups; partial

@@ -21,6 +21,16 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int64
 _F = ctypes.c_float
 
+GEMM_GROUP_MAX = 4
+
+
+class GemmDesc(ctypes.Structure):
+    """nrs_gemm_desc (include/nrs_hip.h): one nrs_gemm call of a group."""
+    _fields_ = [("layout", ctypes.c_int), ("C", _P), ("A", _P), ("B", _P),
+                ("rows", _I), ("cols", _I), ("inner", _I), ("beta", _F),
+                ("bias", _P), ("epilogue", ctypes.c_int)]
+
+
 # name -> argtypes (all return int status unless listed in _RET)
 SIGNATURES = {
     "nrs_init": [ctypes.c_int],
@@ -38,6 +48,7 @@ SIGNATURES = {
     "nrs_memset_zero": [_P, ctypes.c_size_t],
     "nrs_sync": [],
     "nrs_gemm": [ctypes.c_int, _P, _P, _P, _I, _I, _I, _F, _P, ctypes.c_int],
+    "nrs_gemm_group": [ctypes.POINTER(GemmDesc), ctypes.c_int],
     "nrs_gemm_nt_splitk": [_P, _P, _P, _I, _I, _I, _F],
     "nrs_gemm_nt_splitk_noalloc": [_P, _P, _P, _I, _I, _I, _F],
     "nrs_bmm": [ctypes.c_int, _P, _P, _P, _I, _I, _I, _I, _F],
@@ -181,6 +192,20 @@ class DeviceBuffer:
 def gemm(layout, C, A, B, rows, cols, inner, beta=0.0, bias=None, epilogue=EPI_NONE):
     call("nrs_gemm", layout, _ptr(C), _ptr(A), _ptr(B), rows, cols, inner, beta, _ptr(bias),
          epilogue)
+
+
+def gemm_group(calls):
+    """Several gemm calls in one nrs_gemm_group launch; each call is a tuple
+    (layout, C, A, B, rows, cols, inner[, beta[, bias[, epilogue]]])."""
+    descs = (GemmDesc * max(1, len(calls)))()
+    for d, c in zip(descs, calls):
+        layout, C, A, B, rows, cols, inner = c[:7]
+        beta = c[7] if len(c) > 7 else 0.0
+        bias = c[8] if len(c) > 8 else None
+        epi = c[9] if len(c) > 9 else EPI_NONE
+        d.layout, d.C, d.A, d.B = layout, _ptr(C), _ptr(A), _ptr(B)
+        d.rows, d.cols, d.inner, d.beta, d.bias, d.epilogue = rows, cols, inner, beta, _ptr(bias), epi
+    call("nrs_gemm_group", descs, len(calls))
 
 
 def gemm_nt_splitk(C, A, B, rows, cols, inner, beta=0.0):

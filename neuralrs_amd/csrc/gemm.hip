@@ -201,12 +201,19 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool d
 
 }  // namespace
 
-int gemm_run(const GemmCall& c) {
-    const int layout = c.layout;
+namespace {
+
+// Argument checks shared by every GEMM entry; `empty` is set for a call with
+// nothing to compute (a zero output dimension or batch).
+int check_call(const GemmCall& c, bool& empty) {
     const int64_t M = c.M, N = c.N, K = c.K, batch = c.batch;
-    NRS_ARG_CHECK(layout >= NRS_NN && layout <= NRS_TN, "gemm: unknown layout %d", layout);
+    empty = false;
+    NRS_ARG_CHECK(c.layout >= NRS_NN && c.layout <= NRS_TN, "gemm: unknown layout %d", c.layout);
     NRS_ARG_CHECK(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "gemm: negative size");
-    if (M == 0 || N == 0 || batch == 0) return NRS_OK;
+    if (M == 0 || N == 0 || batch == 0) {
+        empty = true;
+        return NRS_OK;
+    }
     NRS_ARG_CHECK(c.C != nullptr, "gemm: null C");
     NRS_ARG_CHECK(K == 0 || (c.A != nullptr && c.B != nullptr), "gemm: null operand");
     NRS_ARG_CHECK(!(c.epi & (NRS_EPI_BIAS_COL | NRS_EPI_BIAS_ROW)) || c.bias != nullptr,
@@ -215,13 +222,17 @@ int gemm_run(const GemmCall& c) {
     const bool dense = c.amode == OP_DENSE && c.bmode == OP_DENSE;
     NRS_ARG_CHECK(dense || (c.gather_bytes > 0 && c.gather_bytes <= 0x80000000ll),
                   "gemm: gathered operand must be 1 B .. 2 GiB");
+    return NRS_OK;
+}
 
+// 128-bit loads need 16-byte aligned rows of both operands (k-slices are
+// multiples of BK, hence of 4). Bounds are checked per vector, so the guarded
+// dimension must be a multiple of 4.
+bool vec4_loads(const GemmCall& c) {
+    const int layout = c.layout;
+    const int64_t M = c.M, N = c.N, K = c.K, batch = c.batch;
     const int64_t lda = (layout == NRS_TN) ? M : K;
     const int64_t ldb = (layout == NRS_NT) ? K : N;
-
-    // 128-bit loads need 16-byte aligned rows of both operands (k-slices
-    // are multiples of BK, hence of 4). Bounds are checked per vector, so the
-    // guarded dimension must be a multiple of 4.
     bool a_vec, b_vec;
     if (c.amode == OP_NCHW)  // four columns never straddle an image
         a_vec = aligned16(c.A) && c.cg.P % 4 == 0 && K % 4 == 0;
@@ -233,13 +244,13 @@ int gemm_run(const GemmCall& c) {
     else
         b_vec = aligned16(c.B) && ldb % 4 == 0 && (c.sB % 4 == 0 || batch == 1) &&
                 (layout == NRS_NT ? K % 4 == 0 : N % 4 == 0);
-    const bool vec4 = a_vec && b_vec;
+    return a_vec && b_vec;
+}
 
-    Plan pl = plan_gemm(M, N, K, batch, vec4, dense, c.allow_split && c.nchw_P == 0,
-                        c.force_slices);
-    const TileShape& s = kShapes[pl.tile];
-
-    GemmArgs p{};
+// Kernel arguments of call c on tile shape s with plan pl (partial unset).
+int make_args(GemmArgs& p, const GemmCall& c, const TileShape& s, const Plan& pl) {
+    const int64_t M = c.M, N = c.N, K = c.K;
+    p = GemmArgs{};
     p.A = c.A;
     p.B = c.B;
     p.C = c.C;
@@ -247,8 +258,8 @@ int gemm_run(const GemmCall& c) {
     p.M = M;
     p.N = N;
     p.K = K;
-    p.lda = lda;
-    p.ldb = ldb;
+    p.lda = (c.layout == NRS_TN) ? M : K;
+    p.ldb = (c.layout == NRS_NT) ? K : N;
     p.ldc = N;
     p.sA = c.sA;
     p.sB = c.sB;
@@ -262,7 +273,7 @@ int gemm_run(const GemmCall& c) {
     p.k_per_slice = pl.k_per_slice;
     p.cg = c.cg;
     p.gather_bytes = c.gather_bytes;
-    if (!dense) {
+    if (c.amode != OP_DENSE || c.bmode != OP_DENSE) {
         NRS_ARG_CHECK(c.cg.P >= 1 && c.cg.P <= INT32_MAX && c.cg.ow >= 1 && c.cg.ow <= INT32_MAX &&
                           K <= INT32_MAX,
                       "gemm: convolution geometry out of range");
@@ -274,8 +285,35 @@ int gemm_run(const GemmCall& c) {
         p.div_nchw = make_fastdiv((uint32_t)c.nchw_P);
     }
     // (the kernel renumbers a split grid by its linear id, tiles * slices)
-    NRS_ARG_CHECK((int64_t)p.tiles_m * p.tiles_n * pl.slices <= INT32_MAX && batch <= 65535,
+    NRS_ARG_CHECK((int64_t)p.tiles_m * p.tiles_n * pl.slices <= INT32_MAX && c.batch <= 65535,
                   "gemm: grid too large");
+    return NRS_OK;
+}
+
+void launch_reduce(GemmArgs p, int slices) {
+    const int64_t total = p.M * p.N;
+    unsigned blocks = (unsigned)std::min<int64_t>(cdiv(total, 64), 4 * (int64_t)num_cus());
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(64 * kSplitGroups), 0, stream(), p,
+                       slices);
+}
+
+}  // namespace
+
+int gemm_run(const GemmCall& c) {
+    bool empty;
+    const int rc = check_call(c, empty);
+    if (rc != NRS_OK || empty) return rc;
+    const int layout = c.layout;
+    const int64_t M = c.M, N = c.N, K = c.K, batch = c.batch;
+    const bool dense = c.amode == OP_DENSE && c.bmode == OP_DENSE;
+    const bool vec4 = vec4_loads(c);
+
+    Plan pl = plan_gemm(M, N, K, batch, vec4, dense, c.allow_split && c.nchw_P == 0,
+                        c.force_slices);
+    const TileShape& s = kShapes[pl.tile];
+    GemmArgs p;
+    const int arc = make_args(p, c, s, pl);
+    if (arc != NRS_OK) return arc;
 
     KernelFn fn = kernel_for(pl.tile, pl.pf, layout, vec4, c.amode, c.bmode);
     NRS_ARG_CHECK(fn != nullptr, "gemm: no kernel for layout %d with operand modes %d/%d", layout,
@@ -298,16 +336,127 @@ int gemm_run(const GemmCall& c) {
         p.partial = ws;
         hipLaunchKernelGGL(fn, grid, dim3(s.threads), 0, stream(), p);
         NRS_LAUNCH_CHECK("gemm (split-K partials)");
-        const int64_t total = M * N;
-        unsigned blocks = (unsigned)std::min<int64_t>(cdiv(total, 64), 4 * (int64_t)num_cus());
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(64 * kSplitGroups), 0,
-                           stream(), p, pl.slices);
+        launch_reduce(p, pl.slices);
         NRS_LAUNCH_CHECK("gemm (split-K reduce)");
     } else {
         p.partial = nullptr;
         hipLaunchKernelGGL(fn, grid, dim3(s.threads), 0, stream(), p);
         NRS_LAUNCH_CHECK("gemm");
     }
+    return NRS_OK;
+}
+
+namespace {
+
+bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
+    const char* x = static_cast<const char*>(a);
+    const char* y = static_cast<const char*>(b);
+    return x < y + bbytes && y < x + abytes;
+}
+
+// The group kernel's tile: 64x64x32, 2x2 waves of 32x32, prefetch depth 2,
+// compiled for up to four waves per SIMD so that several problems'
+// workgroups share a CU.
+constexpr int kGroupBM = 64, kGroupBN = 64, kGroupBK = 32, kGroupThreads = 256;
+static_assert(kGroupMax == NRS_GEMM_GROUP_MAX, "group size of the kernel and the C ABI");
+
+}  // namespace
+
+int gemm_group_run(const GemmCall* calls, int count) {
+    NRS_ARG_CHECK(count >= 0 && (count == 0 || calls != nullptr), "gemm group: bad count");
+    // Checks first, so that an invalid call launches nothing.
+    bool grouped = count >= 2 && count <= kGroupMax;
+    int live = 0;
+    for (int i = 0; i < count; ++i) {
+        bool empty;
+        const int rc = check_call(calls[i], empty);
+        if (rc != NRS_OK) return rc;
+        if (empty) continue;
+        ++live;
+        const GemmCall& c = calls[i];
+        grouped = grouped && c.amode == OP_DENSE && c.bmode == OP_DENSE && c.batch == 1 &&
+                  c.nchw_P == 0 && c.partial_buf == nullptr && c.force_slices == 0 &&
+                  c.K > 0 && vec4_loads(c);
+    }
+    // An output overlapping another call's operand or output would make the
+    // result depend on the order the problems run in: such groups run one
+    // call after another, in the order given.
+    for (int i = 0; grouped && i < count; ++i) {
+        const GemmCall& ci = calls[i];
+        if (ci.M == 0 || ci.N == 0) continue;
+        const size_t cb = sizeof(float) * (size_t)(ci.M * ci.N);
+        for (int j = 0; grouped && j < count; ++j) {
+            const GemmCall& cj = calls[j];
+            if (j == i || cj.M == 0 || cj.N == 0) continue;
+            const size_t ab = sizeof(float) * (size_t)(cj.M * cj.K);
+            const size_t bb = sizeof(float) * (size_t)(cj.K * cj.N);
+            if (overlaps(ci.C, cb, cj.C, sizeof(float) * (size_t)(cj.M * cj.N)) ||
+                overlaps(ci.C, cb, cj.A, ab) || overlaps(ci.C, cb, cj.B, bb))
+                grouped = false;
+        }
+    }
+    if (!grouped || live < 2) {
+        for (int i = 0; i < count; ++i) {
+            const int rc = gemm_run(calls[i]);
+            if (rc != NRS_OK) return rc;
+        }
+        return NRS_OK;
+    }
+
+    const int cus = num_cus();
+    const TileShape s{kGroupBM, kGroupBN, kGroupBK, kGroupThreads};
+    GemmGroupArgs g{};
+    size_t partial_floats = 0;
+    int next = 0;
+    int64_t total_wgs = 0;
+    for (int i = 0; i < count; ++i) {
+        const GemmCall& c = calls[i];
+        if (c.M == 0 || c.N == 0) continue;
+        const int64_t tiles = cdiv(c.M, s.bm) * cdiv(c.N, s.bn);
+        // A problem of few tiles over a long K is split so that it brings
+        // about one workgroup per CU (at least 8 k-tiles per slice, 2 for a
+        // grid under 16 tiles), like a launch of its own would.
+        int64_t slices = 1;
+        if (tiles * 2 <= cus && c.K >= 8 * s.bk) {
+            const int64_t want = std::min<int64_t>(256, cdiv(cus, tiles));
+            const int64_t max_by_k = std::max<int64_t>(1, c.K / ((tiles >= 16 ? 8 : 2) * s.bk));
+            slices = std::max<int64_t>(1, std::min(want, max_by_k));
+        }
+        Plan pl{T64x64, 1, c.K, 2};
+        int64_t kps = cdiv(cdiv(c.K, slices), s.bk) * s.bk;
+        slices = std::max<int64_t>(1, cdiv(c.K, kps));
+        pl.slices = (int)slices;
+        pl.k_per_slice = kps;
+        GemmArgs& p = g.prob[next];
+        const int rc = make_args(p, c, s, pl);
+        if (rc != NRS_OK) return rc;
+        total_wgs = (total_wgs + 7) / 8 * 8;
+        g.first[next] = (int)total_wgs;
+        g.layout[next] = c.layout;
+        g.slices[next] = (int)slices;
+        total_wgs += tiles * slices;
+        if (slices > 1) partial_floats += (size_t)slices * (size_t)(c.M * c.N);
+        ++next;
+    }
+    g.count = next;
+    NRS_ARG_CHECK(total_wgs <= INT32_MAX, "gemm group: grid too large");
+    if (partial_floats > 0) {
+        float* ws = workspace(sizeof(float) * partial_floats, 0);
+        if (!ws) return NRS_ERR_ALLOC;
+        for (int q = 0; q < g.count; ++q)
+            if (g.slices[q] > 1) {
+                g.prob[q].partial = ws;
+                ws += (size_t)g.slices[q] * (size_t)(g.prob[q].M * g.prob[q].N);
+            }
+    }
+    hipLaunchKernelGGL((gemm_group_kernel<kGroupBM, kGroupBN, kGroupBK, 2, 2, 4, 2>),
+                       dim3((unsigned)total_wgs), dim3(kGroupThreads), 0, stream(), g);
+    NRS_LAUNCH_CHECK("gemm group");
+    for (int q = 0; q < g.count; ++q)
+        if (g.slices[q] > 1) {
+            launch_reduce(g.prob[q], g.slices[q]);
+            NRS_LAUNCH_CHECK("gemm group (split-K reduce)");
+        }
     return NRS_OK;
 }
 
@@ -354,6 +503,29 @@ int nrs_gemm(int layout, float* C, const float* A, const float* B, int64_t rows,
     c.bias = bias;
     c.epi = epilogue;
     return nrs::gemm_run(c);
+}
+
+int nrs_gemm_group(const nrs_gemm_desc* descs, int count) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(count >= 0 && count <= NRS_GEMM_GROUP_MAX,
+                  "gemm group: %d calls (at most %d)", count, NRS_GEMM_GROUP_MAX);
+    NRS_ARG_CHECK(count == 0 || descs != nullptr, "gemm group: null descriptors");
+    nrs::GemmCall calls[NRS_GEMM_GROUP_MAX];
+    for (int i = 0; i < count; ++i) {
+        const nrs_gemm_desc& d = descs[i];
+        nrs::GemmCall& c = calls[i];
+        c.layout = d.layout;
+        c.C = d.C;
+        c.A = d.A;
+        c.B = d.B;
+        c.M = d.rows;
+        c.N = d.cols;
+        c.K = d.inner;
+        c.beta = d.beta;
+        c.bias = d.bias;
+        c.epi = d.epilogue;
+    }
+    return nrs::gemm_group_run(calls, count);
 }
 
 int nrs_gemm_nt_splitk(float* C, const float* A, const float* B, int64_t rows, int64_t cols,

@@ -54,6 +54,9 @@ struct GemmCall {
 };
 
 int gemm_run(const GemmCall& c);
+// Up to kGroupMax dense calls in one launch of the group kernel when they
+// qualify (see nrs_gemm_group), else gemm_run on each in order.
+int gemm_group_run(const GemmCall* calls, int count);
 
 // Batched products of small dense items (M, N, K <= 128, 16-byte aligned
 // items, K or the transposed operand's rows in whole float4s), without

@@ -312,7 +312,8 @@ __device__ __forceinline__ void load_nchw(float (&r)[LOADS][VEC], __amdgpu_buffe
     }
 }
 
-// WPE: minimum waves per SIMD the register allocation must allow.
+// Template parameters of gemm_block / gemm_kernel:
+// WPE (kernels): minimum waves per SIMD the register allocation must allow.
 // PF: prefetch depth. Global loads for k-tile j go into register slot j % PF
 // and are issued PF tiles before tile j is stored to LDS, so each load has
 // PF tiles of MFMA work to land in (small tiles need PF > 1 to cover HBM
@@ -324,16 +325,19 @@ __device__ __forceinline__ void load_nchw(float (&r)[LOADS][VEC], __amdgpu_buffe
 // second set's accumulators to the first's through LDS at the end (fixed
 // order): twice the waves per SIMD for tiles that would leave one wave per
 // SIMD waiting on its barrier and LDS reads.
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool AK, bool BKC, int VEC, int WPE,
-          int PF = 1, int AMODE = OP_DENSE, int BMODE = OP_DENSE, int KS = 1>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N * KS) __attribute__((amdgpu_waves_per_eu(WPE)))
-void gemm_kernel(GemmArgs p) {
+//
+// gemm_block computes output tile `bid` (of tiles_m x tiles_n) over K slice
+// `slice` of batch item `batch`, staging through `smem` (2 * STAGE floats);
+// gemm_kernel runs one GEMM per launch, gemm_group_kernel several.
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool AK, bool BKC, int VEC, int PF,
+          int AMODE, int BMODE, int KS>
+__device__ __forceinline__ void gemm_block(const GemmArgs& p, float* smem, int bid, int slice,
+                                           int64_t batch) {
     using C_ = Cfg<BM, BN, BK, WAVES_M, WAVES_N, AK, BKC, VEC, KS>;
     static_assert(AMODE != OP_IM2COL && BMODE != OP_NCHW, "unsupported operand mode");
     static_assert(AMODE != OP_NCHW || AK, "OP_NCHW is a reduction-contiguous operand");
     static_assert(BMODE != OP_IM2COL || !BKC, "OP_IM2COL is a k-major operand");
     constexpr int FM = C_::FM, FN = C_::FN, NT = C_::NT;
-    __shared__ __attribute__((aligned(16))) float smem[2 * C_::STAGE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -345,29 +349,9 @@ void gemm_kernel(GemmArgs p) {
     const int wm0 = (wv / WAVES_N) * C_::WM;
     const int wn0 = (wv % WAVES_N) * C_::WN;
 
-    // Split K over a tile count that is not a multiple of 8: the workgroups
-    // are dealt to the 8 XCDs round-robin by linear id, so the tiles of one
-    // K slice would land on different XCDs, each fetching the slice's shared
-    // operand panel into its own L2 (the 64x576 weight gradient over
-    // K = 100352 read its A panel nine times). Renumber so that every XCD
-    // owns whole slices: logical id = (slice, tile), tile fastest, in
-    // contiguous runs per XCD (a bijection on the grid; each slice still
-    // writes its own partial). With a multiple of 8, tile_coords already
-    // gives each XCD a compact block of every slice's tiles, which measured
-    // faster on 256-wide weight gradients than whole slices per XCD.
-    int bid = blockIdx.x, slice = blockIdx.y;
-    if (gridDim.y > 1 && (gridDim.x & 7) != 0) {
-        const int tiles = gridDim.x, total = tiles * gridDim.y;
-        const int lin = blockIdx.x + blockIdx.y * tiles;
-        const int xcd = lin & 7, per = total >> 3, extra = total & 7;
-        const int id = xcd * per + min(xcd, extra) + (lin >> 3);
-        slice = id / tiles;
-        bid = id - slice * tiles;
-    }
     int tm, tn;
     tile_coords(p, bid, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-    const int64_t batch = blockIdx.z;
 
     const float* A = p.A + batch * p.sA;
     const float* B = p.B + batch * p.sB;
@@ -659,6 +643,95 @@ void gemm_kernel(GemmArgs p) {
                 }
             }
         }
+    }
+}
+
+// Split K over a tile count that is not a multiple of 8: the workgroups are
+// dealt to the 8 XCDs round-robin by linear id, so the tiles of one K slice
+// would land on different XCDs, each fetching the slice's shared operand panel
+// into its own L2 (the 64x576 weight gradient over K = 100352 read its A panel
+// nine times). Renumber so that every XCD owns whole slices: logical id =
+// (slice, tile), tile fastest, in contiguous runs per XCD (a bijection on the
+// grid; each slice still writes its own partial). With a multiple of 8,
+// tile_coords already gives each XCD a compact block of every slice's tiles,
+// which measured faster on 256-wide weight gradients than whole slices per
+// XCD. `lin` is the workgroup's linear id, its low three bits its XCD.
+__device__ __forceinline__ void split_coords(int lin, int tiles, int slices, int& bid, int& slice) {
+    if (slices > 1 && (tiles & 7) != 0) {
+        const int total = tiles * slices;
+        const int xcd = lin & 7, per = total >> 3, extra = total & 7;
+        const int id = xcd * per + min(xcd, extra) + (lin >> 3);
+        slice = id / tiles;
+        bid = id - slice * tiles;
+    } else {
+        slice = lin / tiles;
+        bid = lin - slice * tiles;
+    }
+}
+
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool AK, bool BKC, int VEC, int WPE,
+          int PF = 1, int AMODE = OP_DENSE, int BMODE = OP_DENSE, int KS = 1>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N * KS) __attribute__((amdgpu_waves_per_eu(WPE)))
+void gemm_kernel(GemmArgs p) {
+    using C_ = Cfg<BM, BN, BK, WAVES_M, WAVES_N, AK, BKC, VEC, KS>;
+    __shared__ __attribute__((aligned(16))) float smem[2 * C_::STAGE];
+    int bid = blockIdx.x, slice = blockIdx.y;
+    if (gridDim.y > 1 && (gridDim.x & 7) != 0)
+        split_coords(blockIdx.x + blockIdx.y * gridDim.x, gridDim.x, gridDim.y, bid, slice);
+    gemm_block<BM, BN, BK, WAVES_M, WAVES_N, AK, BKC, VEC, PF, AMODE, BMODE, KS>(p, smem, bid, slice,
+                                                                                 blockIdx.z);
+}
+
+// Several independent dense GEMMs in one launch (the products of one
+// backward step, or projections of one input): problem q owns workgroups
+// [first[q], first[q] + tiles_q * slices[q]) of a 1-D grid, each range
+// starting at a multiple of 8 so that a workgroup's XCD is its id within the
+// problem modulo 8, as in a launch of its own (ids past a problem's range,
+// the padding up to the next multiple of 8, exit at once). The problems'
+// workgroups share the CUs, so one problem's load latency, barriers and
+// epilogue overlap another's MFMAs; one launch per GEMM leaves each CU a
+// single workgroup of small tiles whose waves all stall at the same points.
+constexpr int kGroupMax = 4;
+struct GemmGroupArgs {
+    GemmArgs prob[kGroupMax];
+    int first[kGroupMax];   // first workgroup id of each problem, ascending
+    int layout[kGroupMax];  // NRS_NN / NRS_NT / NRS_TN
+    int slices[kGroupMax];  // K slices (partials to prob[q].partial when > 1)
+    int count;
+};
+
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int WPE, int PF>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(WPE)))
+void gemm_group_kernel(GemmGroupArgs g) {
+    constexpr int kNN = 2 * Cfg<BM, BN, BK, WAVES_M, WAVES_N, true, false, 4>::STAGE;
+    constexpr int kNT = 2 * Cfg<BM, BN, BK, WAVES_M, WAVES_N, true, true, 4>::STAGE;
+    constexpr int kTN = 2 * Cfg<BM, BN, BK, WAVES_M, WAVES_N, false, false, 4>::STAGE;
+    constexpr int kMax = kNN > kNT ? (kNN > kTN ? kNN : kTN) : (kNT > kTN ? kNT : kTN);
+    __shared__ __attribute__((aligned(16))) float smem[kMax];
+    const int b = blockIdx.x;
+    int q = 0;
+#pragma unroll
+    for (int i = 1; i < kGroupMax; ++i)
+        if (i < g.count && b >= g.first[i]) q = i;
+    const GemmArgs& p = g.prob[q];
+    const int tiles = p.tiles_m * p.tiles_n, slices = g.slices[q];
+    const int lin = b - g.first[q];
+    if (lin >= tiles * slices) return;  // uniform: padding up to the next problem
+    int bid, slice;
+    split_coords(lin, tiles, slices, bid, slice);
+    switch (g.layout[q]) {
+        case NRS_NN:
+            gemm_block<BM, BN, BK, WAVES_M, WAVES_N, true, false, 4, PF, OP_DENSE, OP_DENSE, 1>(
+                p, smem, bid, slice, 0);
+            break;
+        case NRS_NT:
+            gemm_block<BM, BN, BK, WAVES_M, WAVES_N, true, true, 4, PF, OP_DENSE, OP_DENSE, 1>(
+                p, smem, bid, slice, 0);
+            break;
+        default:
+            gemm_block<BM, BN, BK, WAVES_M, WAVES_N, false, false, 4, PF, OP_DENSE, OP_DENSE, 1>(
+                p, smem, bid, slice, 0);
+            break;
     }
 }
 

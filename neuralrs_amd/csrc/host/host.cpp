@@ -94,6 +94,40 @@ void bmm_backward_into(int layout, const NodeRef& a, const NodeRef& b, const flo
           what);
 }
 
+// The backward closure of a matmul node (matmul.rs:418-431): dA += dC . B^T
+// (matmul_nt) and dB += A^T . dC (matmul_tn), each followed by
+// accumulate_into, as one grouped launch. When a and b are the same node the
+// two products go to one buffer, one after the other.
+void matmul_backward_into(const NodeRef& a, const NodeRef& b, const float* g, size_t m, size_t k,
+                          size_t n, const char* what) {
+    GpuBuffers& ag = gpu_of(a, "cuda matmul bwd: lhs not on GPU");
+    GpuBuffers& bg = gpu_of(b, "cuda matmul bwd: rhs not on GPU");
+    float ba = 1.0f, bb = 1.0f;
+    float* da = ag.grad->acc_target(ba);
+    if (ag.grad == bg.grad) {
+        check(nrs_gemm(NRS_NT, da, g, bg.data.ptr(), m, k, n, ba, nullptr, NRS_EPI_NONE), what);
+        check(nrs_gemm(NRS_TN, bg.grad->ptr(), ag.data.ptr(), g, k, n, m, 1.0f, nullptr,
+                       NRS_EPI_NONE),
+              what);
+        return;
+    }
+    float* db = bg.grad->acc_target(bb);
+    const nrs_gemm_desc d[2] = {
+        {NRS_NT, da, g, bg.data.ptr(), (int64_t)m, (int64_t)k, (int64_t)n, ba, nullptr,
+         NRS_EPI_NONE},
+        {NRS_TN, db, ag.data.ptr(), g, (int64_t)k, (int64_t)n, (int64_t)m, bb, nullptr,
+         NRS_EPI_NONE}};
+    check(nrs_gemm_group(d, 2), what);
+}
+
+// Gives a matmul output node (a [m, k] . b [k, n]) its backward closure.
+void set_matmul_backward(const NodeRef& node, const NodeRef& a, const NodeRef& b, size_t m,
+                         size_t k, size_t n) {
+    node->backward_fn = [grad = node->gpu->grad, a, b, m, k, n](const std::vector<float>&) {
+        matmul_backward_into(a, b, grad->ptr(), m, k, n, "cuda matmul bwd: launch failed");
+    };
+}
+
 void build_topo(const NodeRef& n, std::unordered_set<const Node*>& visited,
                 std::vector<NodeRef>& topo) {
     if (!visited.insert(n.get()).second) return;
@@ -225,21 +259,7 @@ NodeRef matmul(const NodeRef& a, const NodeRef& b) {
                    NRS_EPI_NONE),
           "cuda matmul: launch failed");
     NodeRef node = make_output({m, n}, {a, b}, std::move(out));
-    node->backward_fn = [grad = node->gpu->grad, a, b, m, k, n](const std::vector<float>&) {
-        GpuBuffers& ag = gpu_of(a, "cuda matmul bwd: lhs not on GPU");
-        GpuBuffers& bg = gpu_of(b, "cuda matmul bwd: rhs not on GPU");
-        float beta = 1.0f;
-        // dA += dC . B^T   (matmul_nt, then accumulate_into: matmul.rs:418-423)
-        float* da = ag.grad->acc_target(beta);
-        check(nrs_gemm(NRS_NT, da, grad->ptr(), bg.data.ptr(), m, k, n, beta, nullptr,
-                       NRS_EPI_NONE),
-              "cuda matmul bwd: launch failed");
-        // dB += A^T . dC   (matmul_tn, then accumulate_into: matmul.rs:425-431)
-        float* db = bg.grad->acc_target(beta);
-        check(nrs_gemm(NRS_TN, db, ag.data.ptr(), grad->ptr(), k, n, m, beta, nullptr,
-                       NRS_EPI_NONE),
-              "cuda matmul bwd: launch failed");
-    };
+    set_matmul_backward(node, a, b, m, k, n);
     return node;
 }
 
@@ -552,18 +572,10 @@ NodeRef Linear::forward(const NodeRef& input) const {
     NodeRef node = make_output({batch, out_f}, {x, w, b}, std::move(out));
     node->backward_fn = [grad = node->gpu->grad, x, w, b, batch, in_f,
                          out_f](const std::vector<float>&) {
-        GpuBuffers& xg = gpu_of(x, "cuda matmul bwd: lhs not on GPU");
-        GpuBuffers& wg = gpu_of(w, "cuda matmul bwd: rhs not on GPU");
         GpuBuffers& bg = gpu_of(b, "backward: parent not on GPU");
+        // dx += g . W^T and dW += x^T . g in one grouped launch, then the bias
+        matmul_backward_into(x, w, grad->ptr(), batch, in_f, out_f, "cuda linear bwd: launch");
         float beta = 1.0f;
-        float* dx = xg.grad->acc_target(beta);
-        check(nrs_gemm(NRS_NT, dx, grad->ptr(), wg.data.ptr(), batch, in_f, out_f, beta, nullptr,
-                       NRS_EPI_NONE),
-              "cuda linear bwd: dx launch");
-        float* dw = wg.grad->acc_target(beta);
-        check(nrs_gemm(NRS_TN, dw, xg.data.ptr(), grad->ptr(), in_f, out_f, batch, beta, nullptr,
-                       NRS_EPI_NONE),
-              "cuda linear bwd: dw launch");
         float* db = bg.grad->acc_target(beta);
         check(nrs_sum_axis0(db, grad->ptr(), batch, out_f, beta), "cuda linear bwd: bias launch");
     };
@@ -571,6 +583,36 @@ NodeRef Linear::forward(const NodeRef& input) const {
 }
 
 namespace {
+
+// x . w for each of several weights, in one grouped launch: the Q, K and V
+// projections of one input (multihead.rs:64-66). Each result is a node of
+// its own with graph::matmul's checks, output and backward closure.
+std::vector<NodeRef> matmul_shared_lhs(const NodeRef& x, const std::vector<NodeRef>& ws) {
+    GpuBuffers& xg = gpu_of(x, "cuda matmul: lhs not on GPU");
+    if (x->shape.size() != 2) throw Panic("cuda matmul: operands must be 2-D");
+    if (ws.empty() || ws.size() > NRS_GEMM_GROUP_MAX) throw Panic("cuda matmul: bad group");
+    const size_t m = x->shape[0], k = x->shape[1];
+    std::vector<DeviceBuffer> outs;
+    std::vector<nrs_gemm_desc> d;
+    for (const NodeRef& w : ws) {
+        GpuBuffers& wg = gpu_of(w, "cuda matmul: rhs not on GPU");
+        if (w->shape.size() != 2) throw Panic("cuda matmul: operands must be 2-D");
+        if (w->shape[0] != k) throw Panic("cuda matmul: inner dims mismatch");
+        const size_t n = w->shape[1];
+        outs.emplace_back(m * n, false);
+        d.push_back({NRS_NN, outs.back().ptr(), xg.data.ptr(), wg.data.ptr(), (int64_t)m,
+                     (int64_t)n, (int64_t)k, 0.0f, nullptr, NRS_EPI_NONE});
+    }
+    check(nrs_gemm_group(d.data(), (int)d.size()), "cuda matmul: launch failed");
+    std::vector<NodeRef> nodes;
+    for (size_t i = 0; i < ws.size(); ++i) {
+        const size_t n = ws[i]->shape[1];
+        NodeRef node = make_output({m, n}, {x, ws[i]}, std::move(outs[i]));
+        set_matmul_backward(node, x, ws[i], m, k, n);
+        nodes.push_back(std::move(node));
+    }
+    return nodes;
+}
 
 // q . k^T per item without materialising k^T: [b, m, d] x [b, n, d] -> [b, m, n]
 // (or 2-D [m, d] x [n, d] -> [m, n]): the bmm(q, transpose(k)) / matmul(q,
@@ -711,8 +753,8 @@ static NodeRef multihead(const MultiHeadAttention& mha, const NodeRef& flat, siz
         throw Panic("multihead: d_model % heads != 0");
     const size_t heads = mha.num_heads, dh = mha.d_model / heads, rows = batch * seq;
     if (heads * dh != d) throw Panic("multihead: input width is not d_model");
-    NodeRef q = graph::matmul(flat, mha.w_q), k = graph::matmul(flat, mha.w_k),
-            v = graph::matmul(flat, mha.w_v);
+    const std::vector<NodeRef> qkv = matmul_shared_lhs(flat, {mha.w_q, mha.w_k, mha.w_v});
+    const NodeRef &q = qkv[0], &k = qkv[1], &v = qkv[2];
     NodeRef concat;
     if (nrs_attention_supported(batch, heads, seq, dh, d)) {
         // heads read and written in place in the [rows, d_model] projections

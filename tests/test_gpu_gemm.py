@@ -166,6 +166,93 @@ def test_gemm_errors_raise(hip):
         hip.gemm(NN, dC, dC, dC, 2, 2, 1, 0.0, None, 1)  # bias flag, null bias
 
 
+# ------------------------------------------------------------- grouped GEMMs
+def group_case(hip, rng, specs, make):
+    """Device operands, outputs and expected results for nrs_gemm_group:
+    specs are (layout, rows, cols, inner, beta, epilogue) tuples."""
+    calls, want, outs = [], [], []
+    for layout, rows, cols, inner, beta, epi in specs:
+        a, b = operands(layout, rows, cols, inner, make)
+        A, B = logical(layout, a, b)
+        c0 = make((rows, cols))
+        bias = make((cols,)) if epi & 1 else (make((rows,)) if epi & 2 else None)
+        v = A @ B
+        if epi & 1:
+            v = v + bias[None, :]
+        if epi & 2:
+            v = v + bias[:, None]
+        if epi & 4:
+            v = np.maximum(v, 0)
+        want.append((v + beta * c0).astype(np.float32))
+        dC = hip.DeviceBuffer.from_host(c0)
+        outs.append((dC, rows, cols))
+        calls.append((layout, dC, hip.DeviceBuffer.from_host(a), hip.DeviceBuffer.from_host(b),
+                      rows, cols, inner, beta,
+                      hip.DeviceBuffer.from_host(bias) if bias is not None else None, epi))
+    return calls, want, outs
+
+
+GROUPS = {
+    # a Linear's backward: dX (NT) and dW (TN, K split) of the cfg4 projection
+    "proj_bwd": [(NT, 4096, 256, 256, 1.0, 0), (TN, 256, 256, 4096, 0.0, 0)],
+    # the FFN backward pair, dW over K = 4096 into 64 tiles
+    "ffn_bwd": [(NT, 4096, 1024, 256, 0.0, 0), (TN, 1024, 256, 4096, 1.0, 0)],
+    # three projections of one input (Q, K, V) and a fourth with bias + ReLU
+    "four_nn": [(NN, 512, 256, 256, 0.0, 0), (NN, 512, 256, 256, 0.0, 0),
+                (NN, 512, 256, 256, 0.0, 0), (NN, 300, 68, 36, 0.0, 1 | 4)],
+    # ragged edges, a row-bias epilogue, a short split
+    "ragged": [(NN, 130, 68, 40, 1.0, 2), (TN, 60, 36, 3000, 0.0, 0), (NT, 100, 12, 8, 0.0, 0)],
+}
+
+
+@pytest.mark.parametrize("name", list(GROUPS))
+def test_gemm_group_exact_integers(hip, name):
+    """Every call of a group gives nrs_gemm's exact result (small integers:
+    any tiling and summation order is exact)."""
+    rng = np.random.default_rng(len(name))
+    calls, want, outs = group_case(hip, rng, GROUPS[name], lambda s: int_matrix(rng, s, -3, 3))
+    hip.gemm_group(calls)
+    for (dC, rows, cols), w, spec in zip(outs, want, GROUPS[name]):
+        assert np.array_equal(dC.to_host((rows, cols)), w), spec
+
+
+def test_gemm_group_f64_tolerance(hip, orc):
+    """The cfg4 projection backward pair on U(-1, 1) data against f64."""
+    rng = np.random.default_rng(4)
+    specs = [(NT, 4096, 256, 256), (TN, 256, 256, 4096)]
+    calls, refs = [], []
+    for layout, rows, cols, inner in specs:
+        a, b = operands(layout, rows, cols, inner, lambda s: rng.uniform(-1, 1, s).astype(np.float32))
+        dC = hip.DeviceBuffer(rows * cols)
+        calls.append((layout, dC, hip.DeviceBuffer.from_host(a), hip.DeviceBuffer.from_host(b),
+                      rows, cols, inner))
+        refs.append((dC, rows, cols, inner) + orc.gemm_f64(LNAME[layout], a, b, rows, cols, inner))
+    hip.gemm_group(calls)
+    for dC, rows, cols, inner, c64, ab in refs:
+        assert rel_err(dC.to_host((rows, cols)), c64, ab) <= gemm_tol(inner)
+
+
+def test_gemm_group_overlap_runs_in_order(hip):
+    """Two calls into one output (the second accumulating) cannot share a
+    grid: they run one after the other, as two nrs_gemm calls would."""
+    rng = np.random.default_rng(5)
+    a1, b1 = int_matrix(rng, (64, 32)), int_matrix(rng, (32, 48))
+    a2, b2 = int_matrix(rng, (64, 16)), int_matrix(rng, (16, 48))
+    dC = hip.DeviceBuffer(64 * 48)
+    d = [hip.DeviceBuffer.from_host(x) for x in (a1, b1, a2, b2)]
+    hip.gemm_group([(NN, dC, d[0], d[1], 64, 48, 32, 0.0), (NN, dC, d[2], d[3], 64, 48, 16, 1.0)])
+    assert np.array_equal(dC.to_host((64, 48)), a1 @ b1 + a2 @ b2)
+
+
+def test_gemm_group_errors(hip):
+    dC = hip.DeviceBuffer(4)
+    with pytest.raises(hip.NrsError):  # more calls than a group holds
+        hip.gemm_group([(NN, dC, dC, dC, 2, 2, 1)] * (hip.GEMM_GROUP_MAX + 1))
+    with pytest.raises(hip.NrsError):  # an invalid call launches nothing
+        hip.gemm_group([(NN, dC, dC, dC, 2, 2, 1), (7, dC, dC, dC, 2, 2, 1)])
+    hip.gemm_group([])  # nothing to do
+
+
 # ------------------------------------------------------------------ split-K
 @pytest.mark.parametrize("shape", [(32, 9, 100352), (64, 288, 25088), (5, 7, 3000), (3, 2, 1)],
                          ids=lambda s: "x".join(map(str, s)))
