@@ -206,10 +206,11 @@ def bench_mlp_cfg2(hip, steps, warmup):
     """cfg2 training step: x[256,784] -> Linear(784,128) -> ReLU ->
     Linear(128,10) -> cross-entropy seed (softmax - onehot)/256 (the fused
     ce_backward of src/cuda/loss/cross_entropy.rs:39-58) -> backward (dW, db
-    of both layers, dh, dx), in ten launches: bias and ReLU in the first
+    of both layers, dh, dx), in nine launches: bias and ReLU in the first
     GEMM's epilogue, the ReLU backward masked by the activation (a > 0
-    exactly where the pre-activation is). Issued from Python here; the same
-    step issued from C++ (eagerly and as a HIP graph) is host_step()."""
+    exactly where the pre-activation is), the first layer's weight and input
+    gradients in one grouped launch. Issued from Python here; the same step
+    issued from C++ (eagerly and as a HIP graph) is host_step()."""
     rng = np.random.default_rng(2)
     B, I, Hd, O = 256, 784, 128, 10
     D = hip.DeviceBuffer.from_host
@@ -233,9 +234,8 @@ def bench_mlp_cfg2(hip, steps, warmup):
         hip.call("nrs_sum_axis0", gb2.ptr, gz.ptr, B, O, 1.0)
         hip.gemm(hip.NT, ga, gz, w2, B, Hd, O)
         hip.call("nrs_relu_backward", gh.ptr, ga.ptr, a.ptr, B * Hd, 0.0)
-        hip.gemm(hip.TN, gw1, x, gh, I, Hd, B, 1.0)
+        hip.gemm_group([(hip.TN, gw1, x, gh, I, Hd, B, 1.0), (hip.NT, gx, gh, w1, B, I, Hd)])
         hip.call("nrs_sum_axis0", gb1.ptr, gh.ptr, B, Hd, 1.0)
-        hip.gemm(hip.NT, gx, gh, w1, B, I, Hd)
 
     us = event_ms(hip, step, steps, warmup) * 1e3
     return {"us_per_step": us, "gemm_roof_us": mlp_gemm_roof_us()}
@@ -388,29 +388,34 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
     # extra work, not counted
     fused_roof = 6 * 2.0 * BH * T * T * Dh / (PEAK_FP32_MFMA_TFLOPS * 1e12) * 1e6
 
-    # the block's Linear GEMMs: X[4096,256] through 4 projections and the FFN
+    # the block's Linear GEMMs: X[4096,256] through 4 projections and the FFN,
+    # launched as the operator surface launches them: the Q, K, V projections
+    # of one input as one grouped launch, each layer's input and weight
+    # gradients (dX = dY.W^T, dW = X^T.dY) as one grouped launch
     R, dm, ff = 32 * 128, 256, 1024
     X = D(rng.standard_normal(R * dm).astype(np.float32))
     H = D(rng.standard_normal(R * ff).astype(np.float32))
-    Wp = D((rng.standard_normal(dm * dm) * np.sqrt(1.0 / dm)).astype(np.float32))
+    Wp = [D((rng.standard_normal(dm * dm) * np.sqrt(1.0 / dm)).astype(np.float32))
+          for _ in range(4)]
     W1 = D((rng.standard_normal(dm * ff) * np.sqrt(1.0 / dm)).astype(np.float32))
     W2 = D((rng.standard_normal(ff * dm) * np.sqrt(1.0 / ff)).astype(np.float32))
+    Yp = [hip.DeviceBuffer(R * dm) for _ in range(4)]
     Yd, Yf, gXd, gXf = (hip.DeviceBuffer(R * dm), hip.DeviceBuffer(R * ff),
                         hip.DeviceBuffer(R * dm), hip.DeviceBuffer(R * ff))
-    gWp, gW1, gW2 = hip.DeviceBuffer(dm * dm), hip.DeviceBuffer(dm * ff), hip.DeviceBuffer(ff * dm)
+    gWp = [hip.DeviceBuffer(dm * dm) for _ in range(4)]
+    gW1, gW2 = hip.DeviceBuffer(dm * ff), hip.DeviceBuffer(ff * dm)
     shapes = []
 
     def linears():
-        for _ in range(4):  # projections: Y = X.Wp, dX = dY.Wp^T, dW = X^T.dY
-            hip.gemm(hip.NN, Yd, X, Wp, R, dm, dm)
-            hip.gemm(hip.NT, gXd, Yd, Wp, R, dm, dm)
-            hip.gemm(hip.TN, gWp, X, Yd, dm, dm, R)
+        hip.gemm_group([(hip.NN, Yp[i], X, Wp[i], R, dm, dm) for i in range(3)])  # Q, K, V
+        hip.gemm(hip.NN, Yp[3], X, Wp[3], R, dm, dm)                              # output proj
         hip.gemm(hip.NN, Yf, X, W1, R, ff, dm)
-        hip.gemm(hip.NT, gXd, Yf, W1, R, dm, ff)
-        hip.gemm(hip.TN, gW1, X, Yf, dm, ff, R)
         hip.gemm(hip.NN, Yd, H, W2, R, dm, ff)
-        hip.gemm(hip.NT, gXf, Yd, W2, R, ff, dm)
-        hip.gemm(hip.TN, gW2, H, Yd, ff, dm, R)
+        for i in range(4):
+            hip.gemm_group([(hip.NT, gXd, Yp[i], Wp[i], R, dm, dm),
+                            (hip.TN, gWp[i], X, Yp[i], dm, dm, R)])
+        hip.gemm_group([(hip.NT, gXd, Yf, W1, R, dm, ff), (hip.TN, gW1, X, Yf, dm, ff, R)])
+        hip.gemm_group([(hip.NT, gXf, Yd, W2, R, ff, dm), (hip.TN, gW2, H, Yd, ff, dm, R)])
 
     for _ in range(4):
         shapes += [(R, dm, dm), (R, dm, dm), (dm, dm, R)]
@@ -736,7 +741,7 @@ def main():
         hm = host_step("mlp", 200, 20)
         out["mlp_cfg2"] = {"python_us_per_step": round(m["us_per_step"], 2),
                            "gemm_roofline_us": round(m["gemm_roof_us"], 3),
-                           "launches": 10,
+                           "launches": 9,
                            "config": "cfg2 Linear 784->128 (+bias, ReLU epilogue), Linear 128->10, "
                                      "batch 256, fused CE grad, fwd+bwd incl. dx and both bias "
                                      "grads"}
