@@ -125,11 +125,12 @@ __device__ __forceinline__ void tile_pos(int q, int64_t mn0, int64_t k0, int64_t
 
 // Loads the k-tile [k0, k0+BK) of one dense operand into registers.
 // KC: reduction dim contiguous (X[mn*ld + k]); else X[k*ld + mn].
-// Out-of-range elements read the operand's first element instead; store_tile
-// replaces them by zero. The loads stay unconditional and their values are
-// not touched until the LDS store, so the compiler waits only for the oldest
-// prefetch slot.
-template <int BMN, int BK, bool KC, int VEC, int LOADS, int NT>
+// With CHECK, out-of-range elements read the operand's first element
+// instead, and store_tile replaces them by zero; without it (tiles known to
+// lie inside the operand) the address is used as is. The loads stay
+// unconditional and their values are not touched until the LDS store, so the
+// compiler waits only for the oldest prefetch slot.
+template <int BMN, int BK, bool KC, int VEC, int LOADS, int NT, bool CHECK = true>
 __device__ __forceinline__ void load_tile(float (&r)[LOADS][VEC], const float* X, int64_t ld,
                                           int64_t mn0, int64_t MN, int64_t k0, int64_t kend,
                                           int tid) {
@@ -137,8 +138,8 @@ __device__ __forceinline__ void load_tile(float (&r)[LOADS][VEC], const float* X
     for (int i = 0; i < LOADS; ++i) {
         int64_t mn, k;
         tile_pos<BMN, BK, KC, VEC>(tid + i * NT, mn0, k0, mn, k);
-        const bool ok = (mn < MN) & (k < kend);
-        const float* src = ok ? (KC ? X + mn * ld + k : X + k * ld + mn) : X;
+        const float* src = KC ? X + mn * ld + k : X + k * ld + mn;
+        if constexpr (CHECK) src = ((mn < MN) & (k < kend)) ? src : X;
         if constexpr (VEC == 4) {
             const f32x4 v = *reinterpret_cast<const f32x4*>(src);
             r[i][0] = v[0];
@@ -325,14 +326,19 @@ __device__ __forceinline__ void load_nchw(float (&r)[LOADS][VEC], __amdgpu_buffe
 // second set's accumulators to the first's through LDS at the end (fixed
 // order): twice the waves per SIMD for tiles that would leave one wave per
 // SIMD waiting on its barrier and LDS reads.
+// INTERIOR (gemm_tile): the whole output tile lies inside C and the K slice
+// is a whole number of k-tiles, so dense operands load and store without
+// per-element bounds selects.
 //
-// gemm_block computes output tile `bid` (of tiles_m x tiles_n) over K slice
-// `slice` of batch item `batch`, staging through `smem` (2 * STAGE floats);
-// gemm_kernel runs one GEMM per launch, gemm_group_kernel several.
+// gemm_tile computes the output tile at (m0, n0) over K range [kbeg, kend)
+// of batch item `batch` (partials: slice `slice`), staging through `smem`
+// (2 * STAGE floats); gemm_block finds the tile of workgroup `bid` and picks
+// the interior or the bounds-checked form; gemm_kernel runs one GEMM per
+// launch, gemm_group_kernel several.
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool AK, bool BKC, int VEC, int PF,
-          int AMODE, int BMODE, int KS>
-__device__ __forceinline__ void gemm_block(const GemmArgs& p, float* smem, int bid, int slice,
-                                           int64_t batch) {
+          int AMODE, int BMODE, int KS, bool INTERIOR>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& p, float* smem, int64_t m0, int64_t n0,
+                                          int64_t kbeg, int64_t kend, int slice, int64_t batch) {
     using C_ = Cfg<BM, BN, BK, WAVES_M, WAVES_N, AK, BKC, VEC, KS>;
     static_assert(AMODE != OP_IM2COL && BMODE != OP_NCHW, "unsupported operand mode");
     static_assert(AMODE != OP_NCHW || AK, "OP_NCHW is a reduction-contiguous operand");
@@ -349,14 +355,8 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& p, float* smem, int b
     const int wm0 = (wv / WAVES_N) * C_::WM;
     const int wn0 = (wv % WAVES_N) * C_::WN;
 
-    int tm, tn;
-    tile_coords(p, bid, tm, tn);
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-
     const float* A = p.A + batch * p.sA;
     const float* B = p.B + batch * p.sB;
-    const int64_t kbeg = (int64_t)slice * p.k_per_slice;
-    const int64_t kend = min(p.K, kbeg + p.k_per_slice);
 
     f32x16 acc[FM][FN];
 #pragma unroll
@@ -381,37 +381,11 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& p, float* smem, int b
         }
     }
     const __amdgpu_buffer_rsrc_t gather = buffer_rsrc(AMODE == OP_NCHW ? A : B, p.gather_bytes);
-    auto loadA = [&](float (&r)[C_::A_LOADS][VEC], int64_t k0) {
-        if constexpr (AMODE == OP_NCHW)
-            load_nchw<BM, BK, VEC, C_::A_LOADS, NT>(r, gather, p.cg.div_P, m0, p.M, k0, kend, tid);
-        else
-            load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(r, A, p.lda, m0, p.M, k0, kend, tid);
-    };
-    const uint32_t a_bits = tile_mn_bits<BM, BK, AK, VEC, C_::A_LOADS, NT>(m0, p.M, tid);
-    const uint32_t b_bits = tile_mn_bits<BN, BK, BKC, VEC, C_::B_LOADS, NT>(n0, p.N, tid);
-    auto storeA = [&](float* dst, const float (&r)[C_::A_LOADS][VEC], int64_t k0) {
-        store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT, AMODE == OP_DENSE>(dst, r, tid, a_bits,
-                                                                               kend - k0);
-    };
-    auto storeB = [&](float* dst, const float (&r)[C_::B_LOADS][VEC], int64_t k0) {
-        if constexpr (BMODE == OP_IM2COL)
-            store_im2col<BN, BK, VEC, C_::B_LOADS, C_::SB, NT>(dst, r, tid);
-        else
-            store_tile<BN, BK, BKC, VEC, C_::B_LOADS, C_::SB, NT, true>(dst, r, tid, b_bits,
-                                                                         kend - k0);
-    };
-    auto loadB = [&](float (&r)[C_::B_LOADS][VEC], int64_t k0) {
-        if constexpr (BMODE == OP_IM2COL)
-            load_im2col<BN, BK, VEC, C_::B_LOADS, NT>(r, gather, p.cg, icol, ktab, k0, kend, tid);
-        else
-            load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT>(r, B, p.ldb, n0, p.N, k0, kend, tid);
-    };
-
     // Main loop: the body is straight-line (tile t is reduced from LDS, tile
     // t + 1 goes from its register slot to the other LDS buffer, tile
     // t + 1 + PF is loaded into the freed slot; loads past the end are
-    // masked), so the compiler can count the loads in flight and wait only
-    // for the slot it stores, PF tiles after issuing it. With kPeel it runs
+    // masked or skipped), so the compiler can count the loads in flight and
+    // wait only for the slot it stores, PF tiles after issuing it. With kPeel it runs
     // while tile t + 1 is real and the last tiles go through the tail below,
     // which loads nothing, stores no padding tile and reduces no padding tile
     // (a single-tile GEMM would otherwise wait one more memory round trip for
@@ -421,6 +395,46 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& p, float* smem, int b
     // (padding tiles load as zeros): with 128 accumulator registers the
     // peeled tail costs them spills, and their k loops are long.
     constexpr bool kPeel = FM * FN <= 2;
+    // Loads past the slice's end are skipped (not clamped) where no padding
+    // tile is reduced: with kPeel, or with one tile in flight.
+    constexpr bool kSkipPast = kPeel || PF == 1;
+    static_assert(!INTERIOR || (kSkipPast && AMODE == OP_DENSE && BMODE == OP_DENSE),
+                  "interior tiles skip the loads past the end");
+    auto loadA = [&](float (&r)[C_::A_LOADS][VEC], int64_t k0) {
+        if constexpr (AMODE == OP_NCHW)
+            load_nchw<BM, BK, VEC, C_::A_LOADS, NT>(r, gather, p.cg.div_P, m0, p.M, k0, kend, tid);
+        else if constexpr (INTERIOR)
+            load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT, false>(r, A, p.lda, m0, p.M, k0, kend, tid);
+        else
+            load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(r, A, p.lda, m0, p.M, k0, kend, tid);
+    };
+    const uint32_t a_bits = tile_mn_bits<BM, BK, AK, VEC, C_::A_LOADS, NT>(m0, p.M, tid);
+    const uint32_t b_bits = tile_mn_bits<BN, BK, BKC, VEC, C_::B_LOADS, NT>(n0, p.N, tid);
+    auto storeA = [&](float* dst, const float (&r)[C_::A_LOADS][VEC], int64_t k0) {
+        if constexpr (INTERIOR)
+            store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT, false>(dst, r, tid, a_bits, BK);
+        else
+            store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT, AMODE == OP_DENSE>(
+                dst, r, tid, a_bits, kend - k0);
+    };
+    auto storeB = [&](float* dst, const float (&r)[C_::B_LOADS][VEC], int64_t k0) {
+        if constexpr (BMODE == OP_IM2COL)
+            store_im2col<BN, BK, VEC, C_::B_LOADS, C_::SB, NT>(dst, r, tid);
+        else if constexpr (INTERIOR)
+            store_tile<BN, BK, BKC, VEC, C_::B_LOADS, C_::SB, NT, false>(dst, r, tid, b_bits, BK);
+        else
+            store_tile<BN, BK, BKC, VEC, C_::B_LOADS, C_::SB, NT, true>(dst, r, tid, b_bits,
+                                                                         kend - k0);
+    };
+    auto loadB = [&](float (&r)[C_::B_LOADS][VEC], int64_t k0) {
+        if constexpr (BMODE == OP_IM2COL)
+            load_im2col<BN, BK, VEC, C_::B_LOADS, NT>(r, gather, p.cg, icol, ktab, k0, kend, tid);
+        else if constexpr (INTERIOR)
+            load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT, false>(r, B, p.ldb, n0, p.N, k0, kend, tid);
+        else
+            load_tile<BN, BK, BKC, VEC, C_::B_LOADS, NT>(r, B, p.ldb, n0, p.N, k0, kend, tid);
+    };
+
     const int ntiles = kend > kbeg ? (int)((kend - kbeg + BK - 1) / BK) : 0;
     const int nloop = kPeel ? ntiles : (ntiles + PF - 1) / PF * PF;
     if (ntiles > 0) {
@@ -430,7 +444,7 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& p, float* smem, int b
         storeB(smem + C_::A_ELEMS, rb[0], kbeg);
 #pragma unroll
         for (int j = 1; j <= PF; ++j) {
-            if (!kPeel || j < ntiles) {  // uniform
+            if ((!kPeel && !kSkipPast) || j < ntiles) {  // uniform
                 const int64_t kj = kbeg + (int64_t)j * BK;
                 loadA(ra[j % PF], kj);
                 loadB(rb[j % PF], kj);
@@ -476,8 +490,10 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& p, float* smem, int b
             storeA(dA, ra[slot], ks);
             storeB(dA + C_::A_ELEMS, rb[slot], ks);
             const int64_t kn = kbeg + (int64_t)(t + 1 + PF) * BK;
-            loadA(ra[slot], kn);
-            loadB(rb[slot], kn);
+            if (!kSkipPast || kn < kend) {  // uniform
+                loadA(ra[slot], kn);
+                loadB(rb[slot], kn);
+            }
             __syncthreads();
         }
     }
@@ -644,6 +660,29 @@ __device__ __forceinline__ void gemm_block(const GemmArgs& p, float* smem, int b
             }
         }
     }
+}
+
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool AK, bool BKC, int VEC, int PF,
+          int AMODE, int BMODE, int KS>
+__device__ __forceinline__ void gemm_block(const GemmArgs& p, float* smem, int bid, int slice,
+                                           int64_t batch) {
+    using C_ = Cfg<BM, BN, BK, WAVES_M, WAVES_N, AK, BKC, VEC, KS>;
+    int tm, tn;
+    tile_coords(p, bid, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t kbeg = (int64_t)slice * p.k_per_slice;
+    const int64_t kend = min(p.K, kbeg + p.k_per_slice);
+    constexpr bool kInteriorForm =
+        AMODE == OP_DENSE && BMODE == OP_DENSE && (C_::FM * C_::FN <= 2 || PF == 1);
+    if constexpr (kInteriorForm) {
+        if (m0 + BM <= p.M && n0 + BN <= p.N && (kend - kbeg) % BK == 0) {  // uniform
+            gemm_tile<BM, BN, BK, WAVES_M, WAVES_N, AK, BKC, VEC, PF, AMODE, BMODE, KS, true>(
+                p, smem, m0, n0, kbeg, kend, slice, batch);
+            return;
+        }
+    }
+    gemm_tile<BM, BN, BK, WAVES_M, WAVES_N, AK, BKC, VEC, PF, AMODE, BMODE, KS, false>(
+        p, smem, m0, n0, kbeg, kend, slice, batch);
 }
 
 // Split K over a tile count that is not a multiple of 8: the workgroups are
