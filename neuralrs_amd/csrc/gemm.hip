@@ -62,9 +62,12 @@ KernelFn pick_conv(int layout, int amode, int bmode, bool vec4) {
 //    GEMMs (83-85% of FP32 MFMA peak at 4096^3 and 8192^3);
 //  * 64x64x32, 4 waves of 32x32, prefetch depth 2: everything mid-sized
 //    (bmm items, conv GEMMs, projections, split-K weight gradients);
-//  * 64x128x32, 4 waves of 32x64, prefetch depth 2: dense GEMMs with at
-//    least two of its tiles per CU and K >= 1024 (2048^3: 162 vs 175 us
-//    on 64x64; on fewer tiles or short K the 64x64 tile wins);
+//  * 128x128x32, 8 waves of 64x32, prefetch depth 2: dense GEMMs with one
+//    to three of its tiles per CU (2048^3: 132 vs 150 us on 64x128; the cfg4
+//    FFN 4096x1024x256: 24.6 vs 24.9 us);
+//  * 64x128x32, 4 waves of 32x64, prefetch depth 2: grids of at least two
+//    of its tiles per CU and K >= 256 whose 128x128 grid would be mostly
+//    padding (2048^3 ran 162 us on it against 175 us on 64x64);
 //  * 32x256x32, 4 waves of 32x64, prefetch depth 2 (1 with scalar loads):
 //    outputs with at most 32 rows;
 //  * 32x128x32, 4 waves of 32x32, prefetch depth 2: convolutions whose GEMM
@@ -76,7 +79,7 @@ KernelFn pick_conv(int layout, int amode, int bmode, bool vec4) {
 //    GEMMs with at most two 64x64 tiles per CU and no K split, which would
 //    otherwise run one wave per SIMD (cfg4 projections 4096x256x256:
 //    9.3 -> 8.7 us NT; FFN 4096x256x1024: 29.0 -> 25.1 us NN).
-enum TileId { T256x256 = 0, T64x64, T32x256, T32x128, T128x32, T64x128, T64x64S2, T_COUNT };
+enum TileId { T256x256 = 0, T64x64, T32x256, T32x128, T128x32, T64x128, T64x64S2, T128x128, T_COUNT };
 const TileShape kShapes[T_COUNT] = {
     {256, 256, 32, 512},
     {64, 64, 32, 256},
@@ -85,6 +88,7 @@ const TileShape kShapes[T_COUNT] = {
     {128, 32, 32, 256},
     {64, 128, 32, 256},
     {64, 64, 32, 512},
+    {128, 128, 32, 512},
 };
 
 // `pf` is the register prefetch depth the plan asks for; tiles that have no
@@ -110,6 +114,8 @@ KernelFn kernel_for(int tile, int pf, int layout, bool vec4, int amode, int bmod
         case T128x32:
             return pf == 1 ? pick_layout<128, 32, 32, 4, 1, 1>(layout, vec4)
                            : pick_layout<128, 32, 32, 4, 1, 2>(layout, vec4);
+        case T128x128:  // planned only with 128-bit loads
+            return vec4 ? pick_fixed<128, 128, 32, 2, 4, 2, 4>(layout) : nullptr;
         case T64x64S2:  // planned only with 128-bit loads
             if (!vec4) return nullptr;
             switch (layout) {
@@ -154,6 +160,8 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t batch, bool vec4, bool d
             pl.tile = T128x32;
         else if (vec4 && tiles_of(T256x256) >= cus && fill(T256x256) >= 0.85)
             pl.tile = T256x256;
+        else if (vec4 && tiles_of(T128x128) >= cus && fill(T128x128) >= 0.85)
+            pl.tile = T128x128;
         else if (vec4 && tiles_of(T64x128) >= 2 * cus && K >= 256 && fill(T64x128) >= 0.85)
             pl.tile = T64x128;
     } else if (M <= 32) {  // gathered (convolution) operands: 64x64 or 32x128

@@ -45,7 +45,7 @@ SHAPES = [  # (rows, cols, inner)
     (512, 512, 512), (32, 1024, 512), (1, 513, 257), (1000, 3, 2),
     (130, 17, 33), (257, 32, 96),  # at most 32 columns: 128x32 tiles, ragged rows
     (2048, 2048, 40), (4096, 1024, 72), (2000, 2048, 36),  # large outputs (the last ragged M)
-    (2000, 2100, 1100),  # 64x128 tiles (two per CU, K >= 1024), ragged edges
+    (2000, 2100, 1100),  # 128x128 tiles (one per CU), ragged edges
     (30, 8200, 1024),    # at most 32 rows: 32x256 tiles over K slices, ragged M and N
     # cfg4 Linear GEMMs (TransformerBlock, B32 S128 d256 dff1024): Q/K/V/O
     # projections and the two FFN layers forward (NN) and their input
@@ -127,7 +127,7 @@ def test_gemm_skinny_cfg5(hip, orc):
 
 @pytest.mark.parametrize("shape", [(70, 50, 33), (2000, 2100, 1100), (300, 20, 40), (30, 600, 1024),
                                    (4096, 4096, 64), (1000, 260, 200)],
-                         ids=["64x64", "64x128", "128x32", "32x256-splitk", "256x256", "64x64-ksplit"])
+                         ids=["64x64", "128x128", "128x32", "32x256-splitk", "256x256", "64x64-ksplit"])
 def test_gemm_beta_bias_relu_epilogues(hip, shape):
     """The general epilogue (beta, column bias, row bias + ReLU) on each tile."""
     rng = np.random.default_rng(9)
