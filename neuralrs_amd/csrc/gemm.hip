@@ -386,8 +386,8 @@ int gemm_group_run(const GemmCall* calls, int count) {
                   c.nchw_P == 0 && c.partial_buf == nullptr && c.force_slices == 0 &&
                   c.K > 0 && vec4_loads(c);
     }
-    // An output overlapping another call's operand or output would make the
-    // result depend on the order the problems run in: such groups run one
+    // An output overlapping another call's operand, bias or output would make
+    // the result depend on the order the problems run in: such groups run one
     // call after another, in the order given.
     for (int i = 0; grouped && i < count; ++i) {
         const GemmCall& ci = calls[i];
@@ -398,8 +398,13 @@ int gemm_group_run(const GemmCall* calls, int count) {
             if (j == i || cj.M == 0 || cj.N == 0) continue;
             const size_t ab = sizeof(float) * (size_t)(cj.M * cj.K);
             const size_t bb = sizeof(float) * (size_t)(cj.K * cj.N);
+            const int64_t bias_n = std::max<int64_t>((cj.epi & NRS_EPI_BIAS_COL) ? cj.N : 0,
+                                                     (cj.epi & NRS_EPI_BIAS_ROW) ? cj.M : 0);
+            const size_t biasb = sizeof(float) * (size_t)bias_n;
             if (overlaps(ci.C, cb, cj.C, sizeof(float) * (size_t)(cj.M * cj.N)) ||
-                overlaps(ci.C, cb, cj.A, ab) || overlaps(ci.C, cb, cj.B, bb))
+                overlaps(ci.C, cb, cj.A, ab) || overlaps(ci.C, cb, cj.B, bb) ||
+                ((cj.epi & (NRS_EPI_BIAS_COL | NRS_EPI_BIAS_ROW)) &&
+                 overlaps(ci.C, cb, cj.bias, biasb)))
                 grouped = false;
         }
     }

@@ -244,6 +244,19 @@ def test_gemm_group_overlap_runs_in_order(hip):
     assert np.array_equal(dC.to_host((64, 48)), a1 @ b1 + a2 @ b2)
 
 
+def test_gemm_group_output_over_bias_runs_in_order(hip):
+    """A call whose output is another call's bias: the second call reads the
+    first one's result, as two nrs_gemm calls in that order would."""
+    rng = np.random.default_rng(6)
+    a1, b1 = int_matrix(rng, (1, 24)), int_matrix(rng, (24, 32))
+    a2, b2 = int_matrix(rng, (40, 16)), int_matrix(rng, (16, 32))
+    d = [hip.DeviceBuffer.from_host(x) for x in (a1, b1, a2, b2)]
+    bias, out = hip.DeviceBuffer(32), hip.DeviceBuffer(40 * 32)
+    hip.gemm_group([(NN, bias, d[0], d[1], 1, 32, 24, 0.0),
+                    (NN, out, d[2], d[3], 40, 32, 16, 0.0, bias, 1)])
+    assert np.array_equal(out.to_host((40, 32)), a2 @ b2 + (a1 @ b1)[0][None, :])
+
+
 def test_gemm_group_errors(hip):
     dC = hip.DeviceBuffer(4)
     with pytest.raises(hip.NrsError):  # more calls than a group holds

@@ -142,3 +142,24 @@ def test_stream_switch_orders_reuse_after_old_stream(hip):
         hip.call("nrs_set_stream", prev)
         for s in (sa, sb):
             _hip_runtime().hipStreamDestroy(ctypes.c_void_p(s))
+
+
+@pytest.mark.parametrize("nbytes,src_off,dst_off", [(16, 0, 0), (4096 * 256 * 4, 0, 0),
+                                                    (1000 * 4, 0, 0), (36, 4, 0), (64, 0, 8),
+                                                    (7, 1, 3)])
+def test_memcpy_dtod_aligned_and_ragged(hip, nbytes, src_off, dst_off):
+    """nrs_memcpy_dtod copies exactly `bytes` bytes: the 16-byte copy kernel
+    for aligned whole units, the runtime copy otherwise; bytes around the
+    destination range stay untouched."""
+    rng = np.random.default_rng(nbytes + src_off)
+    src = rng.integers(0, 256, nbytes + 64, dtype=np.uint8)
+    dst0 = rng.integers(0, 256, nbytes + 64, dtype=np.uint8)
+    dsrc = hip.DeviceBuffer.from_host(src.view(np.float32) if src.size % 4 == 0 else
+                                      np.pad(src, (0, (-src.size) % 4)).view(np.float32))
+    ddst = hip.DeviceBuffer.from_host(dst0.view(np.float32) if dst0.size % 4 == 0 else
+                                      np.pad(dst0, (0, (-dst0.size) % 4)).view(np.float32))
+    hip.call("nrs_memcpy_dtod", ddst.ptr + dst_off, dsrc.ptr + src_off, nbytes)
+    got = ddst.to_host().view(np.uint8)[: dst0.size]
+    want = dst0.copy()
+    want[dst_off:dst_off + nbytes] = src[src_off:src_off + nbytes]
+    assert np.array_equal(got, want)
