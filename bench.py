@@ -206,11 +206,11 @@ def bench_mlp_cfg2(hip, steps, warmup):
     """cfg2 training step: x[256,784] -> Linear(784,128) -> ReLU ->
     Linear(128,10) -> cross-entropy seed (softmax - onehot)/256 (the fused
     ce_backward of src/cuda/loss/cross_entropy.rs:39-58) -> backward (dW, db
-    of both layers, dh, dx), in nine launches: bias and ReLU in the first
+    of both layers, dh, dx), in six library calls: bias and ReLU in the first
     GEMM's epilogue, the ReLU backward masked by the activation (a > 0
-    exactly where the pre-activation is), the first layer's weight and input
-    gradients in one grouped launch. Issued from Python here; the same step
-    issued from C++ (eagerly and as a HIP graph) is host_step()."""
+    exactly where the pre-activation is), each layer's weight, bias and input
+    gradients in one nrs_linear_backward. Issued from Python here; the same
+    step issued from C++ (eagerly and as a HIP graph) is host_step()."""
     rng = np.random.default_rng(2)
     B, I, Hd, O = 256, 784, 128, 10
     D = hip.DeviceBuffer.from_host
@@ -230,12 +230,9 @@ def bench_mlp_cfg2(hip, steps, warmup):
         hip.gemm(hip.NN, a, x, w1, B, Hd, I, 0.0, b1, hip.EPI_BIAS_COL | hip.EPI_RELU)
         hip.gemm(hip.NN, z, a, w2, B, O, Hd, 0.0, b2, hip.EPI_BIAS_COL)
         hip.call("nrs_cross_entropy_backward", gz.ptr, z.ptr, onehot.ptr, B, O)
-        hip.gemm(hip.TN, gw2, a, gz, Hd, O, B, 1.0)
-        hip.call("nrs_sum_axis0", gb2.ptr, gz.ptr, B, O, 1.0)
-        hip.gemm(hip.NT, ga, gz, w2, B, Hd, O)
+        hip.call("nrs_linear_backward", ga, gw2, gb2, gz, a, w2, B, Hd, O, 0.0, 1.0, 1.0)
         hip.call("nrs_relu_backward", gh.ptr, ga.ptr, a.ptr, B * Hd, 0.0)
-        hip.gemm_group([(hip.TN, gw1, x, gh, I, Hd, B, 1.0), (hip.NT, gx, gh, w1, B, I, Hd)])
-        hip.call("nrs_sum_axis0", gb1.ptr, gh.ptr, B, Hd, 1.0)
+        hip.call("nrs_linear_backward", gx, gw1, gb1, gh, x, w1, B, I, Hd, 0.0, 1.0, 1.0)
 
     us = event_ms(hip, step, steps, warmup) * 1e3
     return {"us_per_step": us, "gemm_roof_us": mlp_gemm_roof_us()}
@@ -741,7 +738,7 @@ def main():
         hm = host_step("mlp", 200, 20)
         out["mlp_cfg2"] = {"python_us_per_step": round(m["us_per_step"], 2),
                            "gemm_roofline_us": round(m["gemm_roof_us"], 3),
-                           "launches": 9,
+                           "library_calls": 6,
                            "config": "cfg2 Linear 784->128 (+bias, ReLU epilogue), Linear 128->10, "
                                      "batch 256, fused CE grad, fwd+bwd incl. dx and both bias "
                                      "grads"}

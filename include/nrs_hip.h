@@ -122,6 +122,24 @@ typedef struct nrs_gemm_desc {
 } nrs_gemm_desc;
 int nrs_gemm_group(const nrs_gemm_desc *descs, int count);
 
+/* The backward of Linear::forward = add(matmul(x, W), bias) (src/cuda/nn/
+ * linear.rs:22-25; the closures of src/cuda/graph/matmul.rs:418-431 and
+ * src/cuda/graph/add.rs:91-100), grad [batch, out_f], x [batch, in_f],
+ * W [in_f, out_f]:
+ *   dW = x^T . grad + beta_w * dW          (matmul_tn + accumulate_into)
+ *   db = sum over rows of grad + beta_b*db (sum_axis0 + accumulate_into)
+ *   dx = grad . W^T + beta_x * dx          (matmul_nt + accumulate_into)
+ * in one grouped launch (plus a split-K reduce when the weight gradient is
+ * split): db is computed as an extra output row of the weight-gradient
+ * product whose x^T row is all ones, so it needs no column-sum launch, where
+ * that row costs no extra tile row (in_f not a multiple of 64) or the
+ * product is small (else the column sums follow as one nrs_sum_axis0). dx
+ * and db may be NULL (not computed); dW may not. Results are within the GEMM
+ * tolerance of the separate calls (db sums in the product's order).       */
+int nrs_linear_backward(float *dx, float *dw, float *db, const float *grad,
+                        const float *x, const float *w, int64_t batch, int64_t in_f,
+                        int64_t out_f, float beta_x, float beta_w, float beta_b);
+
 /* mm_nt_splitk(a, b, rows, cols, inner) (src/cuda/graph/matmul.rs:354-379):
  * C = A[rows,inner] . B[cols,inner]^T + beta*C for skinny outputs with a huge
  * inner dimension. The inner dimension is split across workgroups; partial

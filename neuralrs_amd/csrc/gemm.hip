@@ -230,6 +230,9 @@ int check_call(const GemmCall& c, bool& empty) {
     const bool dense = c.amode == OP_DENSE && c.bmode == OP_DENSE;
     NRS_ARG_CHECK(dense || (c.gather_bytes > 0 && c.gather_bytes <= 0x80000000ll),
                   "gemm: gathered operand must be 1 B .. 2 GiB");
+    NRS_ARG_CHECK(!c.sum_row || (dense && batch == 1 && c.nchw_P == 0 && c.epi == NRS_EPI_NONE &&
+                                 M < INT32_MAX),
+                  "gemm: a row of sums needs a dense, unbatched GEMM without epilogue");
     return NRS_OK;
 }
 
@@ -272,7 +275,10 @@ int make_args(GemmArgs& p, const GemmCall& c, const TileShape& s, const Plan& pl
     p.sA = c.sA;
     p.sB = c.sB;
     p.sC = c.sC;
-    p.tiles_m = (int)cdiv(M, s.bm);
+    p.mrows = M + (c.sum_row ? 1 : 0);
+    p.sum_row = c.sum_row;
+    p.sum_beta = c.sum_beta;
+    p.tiles_m = (int)cdiv(p.mrows, s.bm);
     p.tiles_n = (int)cdiv(N, s.bn);
     p.group_m = 8;
     p.beta = c.beta;
@@ -299,7 +305,7 @@ int make_args(GemmArgs& p, const GemmCall& c, const TileShape& s, const Plan& pl
 }
 
 void launch_reduce(GemmArgs p, int slices) {
-    const int64_t total = p.M * p.N;
+    const int64_t total = p.mrows * p.N;
     unsigned blocks = (unsigned)std::min<int64_t>(cdiv(total, 64), 4 * (int64_t)num_cus());
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(64 * kSplitGroups), 0, stream(), p,
                        slices);
@@ -316,8 +322,8 @@ int gemm_run(const GemmCall& c) {
     const bool dense = c.amode == OP_DENSE && c.bmode == OP_DENSE;
     const bool vec4 = vec4_loads(c);
 
-    Plan pl = plan_gemm(M, N, K, batch, vec4, dense, c.allow_split && c.nchw_P == 0,
-                        c.force_slices);
+    Plan pl = plan_gemm(M + (c.sum_row ? 1 : 0), N, K, batch, vec4, dense,
+                        c.allow_split && c.nchw_P == 0, c.force_slices);
     const TileShape& s = kShapes[pl.tile];
     GemmArgs p;
     const int arc = make_args(p, c, s, pl);
@@ -329,7 +335,7 @@ int gemm_run(const GemmCall& c) {
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)pl.slices, (unsigned)batch);
     if (pl.slices > 1) {
         NRS_ARG_CHECK(batch == 1, "gemm: split-K with batch > 1 unsupported");
-        const size_t need = sizeof(float) * (size_t)pl.slices * (size_t)M * (size_t)N;
+        const size_t need = sizeof(float) * (size_t)pl.slices * (size_t)p.mrows * (size_t)N;
         float* ws;
         if (c.partial_buf) {
             NRS_ARG_CHECK(need <= c.partial_cap,
@@ -389,23 +395,35 @@ int gemm_group_run(const GemmCall* calls, int count) {
     // An output overlapping another call's operand, bias or output would make
     // the result depend on the order the problems run in: such groups run one
     // call after another, in the order given.
+    struct Range {
+        const void* p;
+        size_t bytes;
+    };
+    auto ranges = [](const GemmCall& c, bool outputs_only, Range (&r)[5]) {
+        int n = 0;
+        r[n++] = {c.C, sizeof(float) * (size_t)(c.M * c.N)};
+        if (c.sum_row) r[n++] = {c.sum_row, sizeof(float) * (size_t)c.N};
+        if (outputs_only) return n;
+        r[n++] = {c.A, sizeof(float) * (size_t)(c.M * c.K)};
+        r[n++] = {c.B, sizeof(float) * (size_t)(c.K * c.N)};
+        if (c.epi & (NRS_EPI_BIAS_COL | NRS_EPI_BIAS_ROW))
+            r[n++] = {c.bias, sizeof(float) * (size_t)std::max<int64_t>(
+                                  (c.epi & NRS_EPI_BIAS_COL) ? c.N : 0,
+                                  (c.epi & NRS_EPI_BIAS_ROW) ? c.M : 0)};
+        return n;
+    };
     for (int i = 0; grouped && i < count; ++i) {
         const GemmCall& ci = calls[i];
         if (ci.M == 0 || ci.N == 0) continue;
-        const size_t cb = sizeof(float) * (size_t)(ci.M * ci.N);
+        Range out[5], other[5];
+        const int no = ranges(ci, true, out);
         for (int j = 0; grouped && j < count; ++j) {
             const GemmCall& cj = calls[j];
             if (j == i || cj.M == 0 || cj.N == 0) continue;
-            const size_t ab = sizeof(float) * (size_t)(cj.M * cj.K);
-            const size_t bb = sizeof(float) * (size_t)(cj.K * cj.N);
-            const int64_t bias_n = std::max<int64_t>((cj.epi & NRS_EPI_BIAS_COL) ? cj.N : 0,
-                                                     (cj.epi & NRS_EPI_BIAS_ROW) ? cj.M : 0);
-            const size_t biasb = sizeof(float) * (size_t)bias_n;
-            if (overlaps(ci.C, cb, cj.C, sizeof(float) * (size_t)(cj.M * cj.N)) ||
-                overlaps(ci.C, cb, cj.A, ab) || overlaps(ci.C, cb, cj.B, bb) ||
-                ((cj.epi & (NRS_EPI_BIAS_COL | NRS_EPI_BIAS_ROW)) &&
-                 overlaps(ci.C, cb, cj.bias, biasb)))
-                grouped = false;
+            const int nj = ranges(cj, false, other);
+            for (int a = 0; a < no; ++a)
+                for (int b = 0; b < nj; ++b)
+                    if (overlaps(out[a].p, out[a].bytes, other[b].p, other[b].bytes)) grouped = false;
         }
     }
     if (!grouped || live < 2) {
@@ -431,7 +449,7 @@ int gemm_group_run(const GemmCall* calls, int count) {
     for (int i = 0; i < count; ++i) {
         const GemmCall& c = calls[i];
         if (c.M == 0 || c.N == 0) continue;
-        const int64_t tiles = cdiv(c.M, s.bm) * cdiv(c.N, s.bn);
+        const int64_t tiles = cdiv(c.M + (c.sum_row ? 1 : 0), s.bm) * cdiv(c.N, s.bn);
         int64_t slices = 1;
         if (tiles * 2 <= cus && c.K >= 8 * s.bk) {
             const int64_t want = std::min<int64_t>(256, cdiv(cus, tiles));
@@ -452,7 +470,7 @@ int gemm_group_run(const GemmCall* calls, int count) {
     for (int oi = 0; oi < live_n; ++oi) {
         const GemmCall& c = calls[order[oi]];
         const Plan& pl = plans[order[oi]];
-        const int64_t tiles = cdiv(c.M, s.bm) * cdiv(c.N, s.bn);
+        const int64_t tiles = cdiv(c.M + (c.sum_row ? 1 : 0), s.bm) * cdiv(c.N, s.bn);
         GemmArgs& p = g.prob[next];
         const int rc = make_args(p, c, s, pl);
         if (rc != NRS_OK) return rc;
@@ -461,7 +479,7 @@ int gemm_group_run(const GemmCall* calls, int count) {
         g.layout[next] = c.layout;
         g.slices[next] = pl.slices;
         total_wgs += tiles * pl.slices;
-        if (pl.slices > 1) partial_floats += (size_t)pl.slices * (size_t)(c.M * c.N);
+        if (pl.slices > 1) partial_floats += (size_t)pl.slices * (size_t)(p.mrows * c.N);
         ++next;
     }
     g.count = next;
@@ -472,7 +490,7 @@ int gemm_group_run(const GemmCall* calls, int count) {
         for (int q = 0; q < g.count; ++q)
             if (g.slices[q] > 1) {
                 g.prob[q].partial = ws;
-                ws += (size_t)g.slices[q] * (size_t)(g.prob[q].M * g.prob[q].N);
+                ws += (size_t)g.slices[q] * (size_t)(g.prob[q].mrows * g.prob[q].N);
             }
     }
     hipLaunchKernelGGL((gemm_group_kernel<kGroupBM, kGroupBN, kGroupBK, 2, 2, 4, 2>),
@@ -552,6 +570,55 @@ int nrs_gemm_group(const nrs_gemm_desc* descs, int count) {
         c.epi = d.epilogue;
     }
     return nrs::gemm_group_run(calls, count);
+}
+
+int nrs_linear_backward(float* dx, float* dw, float* db, const float* grad, const float* x,
+                        const float* w, int64_t batch, int64_t in_f, int64_t out_f, float beta_x,
+                        float beta_w, float beta_b) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(batch >= 0 && in_f >= 0 && out_f >= 0, "linear backward: negative size");
+    NRS_ARG_CHECK(dw != nullptr, "linear backward: null weight gradient");
+    if (in_f == 0 && db) {  // no weight rows to carry the row of sums
+        const int rc = nrs_sum_axis0(db, grad, batch, out_f, beta_b);
+        if (rc != NRS_OK || !dx) return rc;
+        db = nullptr;
+    }
+    // The row of sums rides the weight-gradient product when it costs no
+    // extra tile row (in_f not a multiple of 64) or the product is small;
+    // else (the cfg4 FFN's 256 x 1024 weight gradient: 80 tiles in place of
+    // 64) the column sums are a launch of their own after the group.
+    float* db_after = nullptr;
+    if (db && in_f % 64 == 0 && in_f * out_f > 65536) {
+        db_after = db;
+        db = nullptr;
+    }
+    nrs::GemmCall calls[2];
+    int n = 0;
+    nrs::GemmCall& cw = calls[n++];  // dW = x^T . grad, db = column sums of grad
+    cw.layout = NRS_TN;
+    cw.C = dw;
+    cw.A = x;
+    cw.B = grad;
+    cw.M = in_f;
+    cw.N = out_f;
+    cw.K = batch;
+    cw.beta = beta_w;
+    cw.sum_row = db;
+    cw.sum_beta = beta_b;
+    if (dx) {  // dx = grad . W^T
+        nrs::GemmCall& cx = calls[n++];
+        cx.layout = NRS_NT;
+        cx.C = dx;
+        cx.A = grad;
+        cx.B = w;
+        cx.M = batch;
+        cx.N = in_f;
+        cx.K = out_f;
+        cx.beta = beta_x;
+    }
+    const int rc = nrs::gemm_group_run(calls, n);
+    if (rc != NRS_OK || !db_after) return rc;
+    return nrs_sum_axis0(db_after, grad, batch, out_f, beta_b);
 }
 
 int nrs_gemm_nt_splitk(float* C, const float* A, const float* B, int64_t rows, int64_t cols,

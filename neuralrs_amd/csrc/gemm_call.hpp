@@ -51,6 +51,12 @@ struct GemmCall {
     // partial_cap bytes is rejected.
     float* partial_buf = nullptr;
     size_t partial_cap = 0;
+    // Row of sums (dense, batch 1, no epilogue): non-null also computes
+    // sum_row[c] = sum_k op(B)[k][c] + sum_beta * sum_row[c] as an extra
+    // output row whose A row is all ones (a Linear's bias gradient beside
+    // its weight gradient).
+    float* sum_row = nullptr;
+    float sum_beta = 0.0f;
 };
 
 int gemm_run(const GemmCall& c);

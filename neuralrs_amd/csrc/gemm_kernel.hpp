@@ -53,6 +53,12 @@ struct GemmArgs {
     ConvGeom cg;         // operand geometry for the implicit-GEMM operand modes
     int64_t gather_bytes;  // size of the gathered operand's tensor (<= 2 GiB)
     FastDiv div_nchw;      // divider for nchw_P
+    // Row of sums: non-null adds output row M, whose A row is all ones, so it
+    // holds sum_k op(B)[k][col]; it goes to sum_row[col] (+ sum_beta * old)
+    // instead of C (split-K partials carry it as their row M).
+    float* sum_row;
+    float sum_beta;
+    int64_t mrows;  // rows of the product: M, or M + 1 with a row of sums
 };
 
 
@@ -167,13 +173,27 @@ __device__ __forceinline__ uint32_t tile_mn_bits(int64_t mn0, int64_t MN, int ti
     return bits;
 }
 
+// Bit i set: load i of this thread starts at row (column) `one` of the
+// operand: the row of ones of a row-of-sums product.
+template <int BMN, int BK, bool KC, int VEC, int LOADS, int NT>
+__device__ __forceinline__ uint32_t tile_one_bits(int64_t mn0, int64_t one, int tid) {
+    uint32_t bits = 0;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        int64_t mn, k;
+        tile_pos<BMN, BK, KC, VEC>(tid + i * NT, mn0, 0, mn, k);
+        bits |= (uint32_t)(mn == one) << i;
+    }
+    return bits;
+}
+
 // Stores a k-tile to LDS. MASK: zero the elements load_tile read out of
 // range (dense operands; gathered operands arrive already zero-filled):
 // load i is in range iff bit i of mn_bits is set and its k offset inside the
 // tile is below krem = kend - k0.
 template <int BMN, int BK, bool KC, int VEC, int LOADS, int S, int NT, bool MASK>
 __device__ __forceinline__ void store_tile(float* s, const float (&r)[LOADS][VEC], int tid,
-                                           uint32_t mn_bits, int64_t krem) {
+                                           uint32_t mn_bits, int64_t krem, uint32_t one_bits = 0) {
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
         const int q = tid + i * NT;
@@ -186,12 +206,19 @@ __device__ __forceinline__ void store_tile(float* s, const float (&r)[LOADS][VEC
             kofs = q / (BMN / VEC);
         }
         bool ok = true;
-        if constexpr (MASK) ok = ((mn_bits >> i) & 1u) & (kofs < krem);
+        float one = 0.0f;  // the row of ones (row of sums) in place of zeros
+        if constexpr (MASK) {
+            ok = ((mn_bits >> i) & 1u) & (kofs < krem);
+            one = (((one_bits >> i) & 1u) & (kofs < krem)) ? 1.0f : 0.0f;
+        }
         if constexpr (VEC == 4) {
+            // a vector along mn starts at the ones row (M % 4 == 0); along k
+            // it lies wholly in the row
             *reinterpret_cast<f32x4*>(s + off) =
-                ok ? f32x4{r[i][0], r[i][1], r[i][2], r[i][3]} : f32x4{0.f, 0.f, 0.f, 0.f};
+                ok ? f32x4{r[i][0], r[i][1], r[i][2], r[i][3]}
+                   : (KC ? f32x4{one, one, one, one} : f32x4{one, 0.f, 0.f, 0.f});
         } else {
-            s[off] = ok ? r[i][0] : 0.0f;
+            s[off] = ok ? r[i][0] : one;
         }
     }
 }
@@ -409,13 +436,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, float* smem, int64_
             load_tile<BM, BK, AK, VEC, C_::A_LOADS, NT>(r, A, p.lda, m0, p.M, k0, kend, tid);
     };
     const uint32_t a_bits = tile_mn_bits<BM, BK, AK, VEC, C_::A_LOADS, NT>(m0, p.M, tid);
+    const uint32_t a_ones =
+        p.sum_row ? tile_one_bits<BM, BK, AK, VEC, C_::A_LOADS, NT>(m0, p.M, tid) : 0u;
     const uint32_t b_bits = tile_mn_bits<BN, BK, BKC, VEC, C_::B_LOADS, NT>(n0, p.N, tid);
     auto storeA = [&](float* dst, const float (&r)[C_::A_LOADS][VEC], int64_t k0) {
         if constexpr (INTERIOR)
             store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT, false>(dst, r, tid, a_bits, BK);
         else
             store_tile<BM, BK, AK, VEC, C_::A_LOADS, C_::SA, NT, AMODE == OP_DENSE>(
-                dst, r, tid, a_bits, kend - k0);
+                dst, r, tid, a_bits, kend - k0, a_ones);
     };
     auto storeB = [&](float* dst, const float (&r)[C_::B_LOADS][VEC], int64_t k0) {
         if constexpr (BMODE == OP_IM2COL)
@@ -511,7 +540,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, float* smem, int64_
     float* out;
     int64_t stride;
     if (p.partial) {
-        out = p.partial + (int64_t)slice * p.M * p.N;
+        out = p.partial + (int64_t)slice * p.mrows * p.N;
         stride = p.N;
     } else {
         out = p.C + batch * p.sC;
@@ -657,6 +686,22 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, float* smem, int64_
                     const int64_t row = row0 + 32 * i + 8 * (r >> 2) + (r & 3);
                     if (colok[j] && row < p.M) out[cbase[j] + row * stride] = old[r];
                 }
+                if (p.sum_row) {  // uniform; the row of sums, raw
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int64_t row = row0 + 32 * i + 8 * (r >> 2) + (r & 3);
+                        if (colok[j] && row == p.M) {
+                            if (p.partial) {
+                                out[cbase[j] + row * stride] = acc[i][j][r];
+                            } else {
+                                float* sr = p.sum_row + cbase[j];
+                                float v = acc[i][j][r];
+                                if (p.sum_beta != 0.0f) v = v + p.sum_beta * *sr;
+                                *sr = v;
+                            }
+                        }
+                    }
+                }
             }
         }
     }
@@ -784,7 +829,7 @@ constexpr int kSplitGroups = 16;
 __global__ __launch_bounds__(64 * kSplitGroups) void splitk_reduce_kernel(GemmArgs p,
                                                                          int slices) {
     __shared__ float red[kSplitGroups][64];
-    const int64_t total = p.M * p.N;
+    const int64_t total = p.mrows * p.N;
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     const int per = (slices + kSplitGroups - 1) / kSplitGroups;
     const int s0 = min(slices, ty * per), s1 = min(slices, s0 + per);
@@ -800,7 +845,13 @@ __global__ __launch_bounds__(64 * kSplitGroups) void splitk_reduce_kernel(GemmAr
 #pragma unroll
             for (int y = 1; y < kSplitGroups; ++y) r += red[y][tx];
             const int64_t row = e / p.N;
-            epilogue_store(p, p.C, row, e - row * p.N, r);
+            if (row < p.M) {
+                epilogue_store(p, p.C, row, e - row * p.N, r);
+            } else {  // the row of sums
+                float* sr = p.sum_row + (e - row * p.N);
+                if (p.sum_beta != 0.0f) r = r + p.sum_beta * *sr;
+                *sr = r;
+            }
         }
         __syncthreads();
     }

@@ -141,24 +141,23 @@ int bench_mlp(int steps, int warmup) {
     DeviceBuffer gw1(I * Hd, true), gw2(Hd * O, true), gb1(Hd, true), gb2(O, true);
     // the reference's step (Linear, ReLU, Linear, the fused cross-entropy
     // seed (softmax - onehot) / batch, then each layer's backward: dW and db
-    // accumulated, dh, dx) in nine launches: bias and ReLU ride the first
-    // GEMM's epilogue, the ReLU backward masks by the activation (a > 0
-    // exactly where the pre-activation is), and the first layer's weight and
-    // input gradients share one grouped launch
+    // accumulated, dh, dx): bias and ReLU ride the first GEMM's epilogue,
+    // the ReLU backward masks by the activation (a > 0 exactly where the
+    // pre-activation is), and each layer's backward is one nrs_linear_backward
+    // (weight, bias and input gradients; the bias gradient an extra row of
+    // the weight-gradient product)
     auto step = [&] {
         nrs_check(nrs_gemm(NRS_NN, a.ptr(), x.ptr(), w1.ptr(), Bn, Hd, I, 0.0f, b1.ptr(),
                            NRS_EPI_BIAS_COL | NRS_EPI_RELU), "l1+relu");
         nrs_check(nrs_gemm(NRS_NN, z.ptr(), a.ptr(), w2.ptr(), Bn, O, Hd, 0.0f, b2.ptr(), NRS_EPI_BIAS_COL), "l2");
         nrs_check(nrs_cross_entropy_backward(gz.ptr(), z.ptr(), onehot.ptr(), Bn, O), "ce");
-        nrs_check(nrs_gemm(NRS_TN, gw2.ptr(), a.ptr(), gz.ptr(), Hd, O, Bn, 1.0f, nullptr, 0), "dw2");
-        nrs_check(nrs_sum_axis0(gb2.ptr(), gz.ptr(), Bn, O, 1.0f), "db2");
-        nrs_check(nrs_gemm(NRS_NT, ga.ptr(), gz.ptr(), w2.ptr(), Bn, Hd, O, 0.0f, nullptr, 0), "da");
+        // layer 2: dW2 (+=), db2 (+=) and dA (=), then the ReLU mask
+        nrs_check(nrs_linear_backward(ga.ptr(), gw2.ptr(), gb2.ptr(), gz.ptr(), a.ptr(), w2.ptr(),
+                                      Bn, Hd, O, 0.0f, 1.0f, 1.0f), "layer 2 bwd");
         nrs_check(nrs_relu_backward(gh.ptr(), ga.ptr(), a.ptr(), Bn * Hd, 0.0f), "relu bwd");
-        const nrs_gemm_desc l1_grads[2] = {
-            {NRS_TN, gw1.ptr(), x.ptr(), gh.ptr(), I, Hd, Bn, 1.0f, nullptr, 0},   // dW1
-            {NRS_NT, gx.ptr(), gh.ptr(), w1.ptr(), Bn, I, Hd, 0.0f, nullptr, 0}};  // dx
-        nrs_check(nrs_gemm_group(l1_grads, 2), "dw1 + dx");
-        nrs_check(nrs_sum_axis0(gb1.ptr(), gh.ptr(), Bn, Hd, 1.0f), "db1");
+        // layer 1: dW1 (+=), db1 (+=) and dx (=)
+        nrs_check(nrs_linear_backward(gx.ptr(), gw1.ptr(), gb1.ptr(), gh.ptr(), x.ptr(), w1.ptr(),
+                                      Bn, I, Hd, 0.0f, 1.0f, 1.0f), "layer 1 bwd");
     };
     double gpu_us = 0, wall_us = 0;
     time_steps(step, steps, warmup, gpu_us, wall_us);
@@ -182,7 +181,7 @@ int bench_mlp(int steps, int warmup) {
     hip_check(hipGraphDestroy(graph), "destroy");
     hip_check(hipStreamDestroy(cap), "destroy");
     std::printf("{\"workload\": \"cfg2 MLP step 784-128-10 batch 256 through the C ABI\", "
-                "\"launches\": 9, \"eager_gpu_us\": %.2f, \"eager_wall_us\": %.2f, "
+                "\"calls\": 6, \"eager_gpu_us\": %.2f, \"eager_wall_us\": %.2f, "
                 "\"graph_gpu_us\": %.2f, \"graph_wall_us\": %.2f, \"steps\": %d}\n",
                 gpu_us, wall_us, g_gpu, g_wall, steps);
     return 0;

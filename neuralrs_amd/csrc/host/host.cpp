@@ -572,12 +572,27 @@ NodeRef Linear::forward(const NodeRef& input) const {
     NodeRef node = make_output({batch, out_f}, {x, w, b}, std::move(out));
     node->backward_fn = [grad = node->gpu->grad, x, w, b, batch, in_f,
                          out_f](const std::vector<float>&) {
+        GpuBuffers& xg = gpu_of(x, "cuda matmul bwd: lhs not on GPU");
+        GpuBuffers& wg = gpu_of(w, "cuda matmul bwd: rhs not on GPU");
         GpuBuffers& bg = gpu_of(b, "backward: parent not on GPU");
-        // dx += g . W^T and dW += x^T . g in one grouped launch, then the bias
-        matmul_backward_into(x, w, grad->ptr(), batch, in_f, out_f, "cuda linear bwd: launch");
-        float beta = 1.0f;
-        float* db = bg.grad->acc_target(beta);
-        check(nrs_sum_axis0(db, grad->ptr(), batch, out_f, beta), "cuda linear bwd: bias launch");
+        if (xg.grad == wg.grad || xg.grad == bg.grad || wg.grad == bg.grad) {
+            // parents sharing a gradient: the products one after the other
+            matmul_backward_into(x, w, grad->ptr(), batch, in_f, out_f, "cuda linear bwd: launch");
+            float beta = 1.0f;
+            float* db = bg.grad->acc_target(beta);
+            check(nrs_sum_axis0(db, grad->ptr(), batch, out_f, beta),
+                  "cuda linear bwd: bias launch");
+            return;
+        }
+        // dx += g . W^T, dW += x^T . g and db += column sums of g, one
+        // grouped launch (the bias gradient rides the weight gradient)
+        float bx = 1.0f, bw = 1.0f, bb = 1.0f;
+        float* dx = xg.grad->acc_target(bx);
+        float* dw = wg.grad->acc_target(bw);
+        float* db = bg.grad->acc_target(bb);
+        check(nrs_linear_backward(dx, dw, db, grad->ptr(), xg.data.ptr(), wg.data.ptr(), batch,
+                                  in_f, out_f, bx, bw, bb),
+              "cuda linear bwd: launch");
     };
     return node;
 }

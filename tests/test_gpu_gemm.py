@@ -257,6 +257,58 @@ def test_gemm_group_output_over_bias_runs_in_order(hip):
     assert np.array_equal(out.to_host((40, 32)), a2 @ b2 + (a1 @ b1)[0][None, :])
 
 
+# ------------------------------------------------- Linear backward (fused)
+@pytest.mark.parametrize("batch,in_f,out_f", [(4096, 256, 1024), (4096, 1024, 256), (4096, 256, 256),
+                                              (256, 784, 128), (256, 128, 10), (37, 30, 9),
+                                              (5, 4, 8), (300, 64, 7), (1, 1, 1)],
+                         ids=lambda v: str(v))
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+def test_linear_backward_exact_integers(hip, batch, in_f, out_f, beta):
+    """dW, db (the extra row of the weight-gradient product) and dx of one
+    nrs_linear_backward against the reference's three products (exact on
+    small integers): split and unsplit weight gradients, 128-bit and scalar
+    operands, grouped and one-after-another launches."""
+    rng = np.random.default_rng(batch * 31 + in_f * 7 + out_f)
+    g, x = int_matrix(rng, (batch, out_f), -3, 3), int_matrix(rng, (batch, in_f), -3, 3)
+    w = int_matrix(rng, (in_f, out_f), -3, 3)
+    dx0, dw0, db0 = (int_matrix(rng, s, -3, 3) for s in ((batch, in_f), (in_f, out_f), (out_f,)))
+    D = hip.DeviceBuffer.from_host
+    ddx, ddw, ddb = D(dx0), D(dw0), D(db0)
+    hip.call("nrs_linear_backward", ddx, ddw, ddb, D(g), D(x), D(w), batch, in_f, out_f,
+             beta, beta, beta)
+    assert np.array_equal(ddw.to_host((in_f, out_f)), x.T @ g + beta * dw0)
+    assert np.array_equal(ddb.to_host(), g.sum(axis=0) + beta * db0)
+    assert np.array_equal(ddx.to_host((batch, in_f)), g @ w.T + beta * dx0)
+
+
+def test_linear_backward_optional_outputs_and_empty(hip):
+    """dx and db may be NULL; no input features (db still the column sums);
+    no rows (dW = beta dW, db = beta db)."""
+    rng = np.random.default_rng(11)
+    D = hip.DeviceBuffer.from_host
+    g, x, w = int_matrix(rng, (64, 32)), int_matrix(rng, (64, 48)), int_matrix(rng, (48, 32))
+    ddw = hip.DeviceBuffer(48 * 32)
+    hip.call("nrs_linear_backward", None, ddw, None, D(g), D(x), D(w), 64, 48, 32, 0.0, 0.0, 0.0)
+    assert np.array_equal(ddw.to_host((48, 32)), x.T @ g)
+    ddb = hip.DeviceBuffer(32)
+    hip.call("nrs_linear_backward", None, ddw, ddb, D(g), D(x), D(w), 64, 48, 32, 0.0, 1.0, 0.0)
+    assert np.array_equal(ddb.to_host(), g.sum(axis=0))
+    assert np.array_equal(ddw.to_host((48, 32)), 2 * (x.T @ g))
+    # no input features: only the bias gradient has elements
+    dummy = hip.DeviceBuffer(4)
+    ddb2 = D(np.ones(32, np.float32))
+    hip.call("nrs_linear_backward", dummy, dummy, ddb2, D(g), dummy, dummy, 64, 0, 32, 0.0, 0.0, 1.0)
+    assert np.array_equal(ddb2.to_host(), g.sum(axis=0) + 1)
+    # no rows: the empty sums plus beta * old
+    dw0, db0 = int_matrix(rng, (48, 32)), int_matrix(rng, (32,))
+    ddw0, ddb0 = D(dw0), D(db0)
+    hip.call("nrs_linear_backward", None, ddw0, ddb0, dummy, dummy, dummy, 0, 48, 32, 0.0, 1.0, 0.5)
+    assert np.array_equal(ddw0.to_host((48, 32)), dw0)
+    assert np.array_equal(ddb0.to_host(), 0.5 * db0)
+    with pytest.raises(hip.NrsError):  # the weight gradient is required
+        hip.call("nrs_linear_backward", None, None, ddb0, D(g), D(x), D(w), 64, 48, 32, 0.0, 0.0, 0.0)
+
+
 def test_gemm_group_errors(hip):
     dC = hip.DeviceBuffer(4)
     with pytest.raises(hip.NrsError):  # more calls than a group holds
