@@ -341,6 +341,13 @@ int nrs_merge_heads(float *out, const float *in, int64_t rows, int64_t heads, in
 int nrs_layernorm_forward(float *out, float *x_norm, float *inv_std, const float *in,
                           const float *gamma, const float *beta, int64_t rows, int64_t features,
                           float eps);
+/* The same LayerNorm of in + in2, the residual add before each norm of
+ * TransformerBlock::forward (src/cuda/nn/transformer_block.rs:32-33, 41-42: add then
+ * norm) in one pass: the sum is rounded to f32 as the add computes it and is
+ * not written out. in2 may be NULL (nrs_layernorm_forward).                  */
+int nrs_add_layernorm_forward(float *out, float *x_norm, float *inv_std, const float *in,
+                              const float *in2, const float *gamma, const float *beta,
+                              int64_t rows, int64_t features, float eps);
 /* Its backward (ln_dx, ln_reduce and accumulate_into, normalization.rs:41-80,
  * 133-160): dxh = grad*gamma; dinput = inv_std*(dxh - mean(dxh) - x_norm*
  * mean(dxh*x_norm)); dgamma = sum over rows of grad*x_norm; dbeta = sum of

@@ -82,6 +82,7 @@ SIGNATURES = {
     "nrs_concat_cols_backward": [_P, _P, _I, _I, _I, _I, _F],
     "nrs_split_heads": [_P, _P, _I, _I, _I, _F],
     "nrs_layernorm_forward": [_P, _P, _P, _P, _P, _P, _I, _I, _F],
+    "nrs_add_layernorm_forward": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _F],
     "nrs_layernorm_backward": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _F],
     "nrs_merge_heads": [_P, _P, _I, _I, _I, _F],
     "nrs_softmax_forward_scaled": [_P, _P, _I, _I, _F],

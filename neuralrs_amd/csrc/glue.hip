@@ -246,17 +246,21 @@ int strided_copy(const StridedCopy& a, const char* what) {
 // ln_forward, which runs one thread per row): mean, biased variance,
 // inv_std = 1 / sqrt(var + eps), x_norm = (x - mean) * inv_std and
 // out = gamma * x_norm + beta. PER > 0 keeps the row (features <= 64 * PER)
-// in registers; PER = 0 re-reads it.
+// in registers; PER = 0 re-reads it. A non-null `in2` normalises in + in2
+// (the sum rounded to f32 as the residual add computes it) without writing
+// the sum out.
 template <int PER>
 __global__ __launch_bounds__(256) void layernorm_fwd_kernel(
     float* __restrict__ out, float* __restrict__ xn_out, float* __restrict__ istd_out,
-    const float* __restrict__ in, const float* __restrict__ gamma,
+    const float* __restrict__ in, const float* __restrict__ in2, const float* __restrict__ gamma,
     const float* __restrict__ beta, int64_t rows, int64_t F, float eps) {
     const int lane = threadIdx.x & 63;
     const int64_t waves = (int64_t)gridDim.x * 4;
     const float nf = (float)F;
     for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += waves) {
         const float* x = in + r * F;
+        const float* x2 = in2 ? in2 + r * F : nullptr;
+        auto at = [&](int64_t f) { return x2 ? x[f] + x2[f] : x[f]; };
         float* y = out + r * F;
         float* xn = xn_out + r * F;
         if constexpr (PER > 0) {
@@ -265,7 +269,7 @@ __global__ __launch_bounds__(256) void layernorm_fwd_kernel(
 #pragma unroll
             for (int i = 0; i < PER; ++i) {
                 const int f = lane + 64 * i;
-                v[i] = f < F ? x[f] : 0.0f;
+                v[i] = f < F ? at(f) : 0.0f;
                 s += v[i];
             }
             const float mean = wave_sum(s) / nf;
@@ -288,17 +292,17 @@ __global__ __launch_bounds__(256) void layernorm_fwd_kernel(
             }
         } else {
             float s = 0.0f;
-            for (int64_t f = lane; f < F; f += 64) s += x[f];
+            for (int64_t f = lane; f < F; f += 64) s += at(f);
             const float mean = wave_sum(s) / nf;
             float q = 0.0f;
             for (int64_t f = lane; f < F; f += 64) {
-                const float d = x[f] - mean;
+                const float d = at(f) - mean;
                 q += d * d;
             }
             const float istd = 1.0f / sqrtf(wave_sum(q) / nf + eps);
             if (lane == 0) istd_out[r] = istd;
             for (int64_t f = lane; f < F; f += 64) {
-                const float t = (x[f] - mean) * istd;
+                const float t = (at(f) - mean) * istd;
                 xn[f] = t;
                 y[f] = gamma[f] * t + beta[f];
             }
@@ -642,9 +646,9 @@ int nrs_merge_heads(float* out, const float* in, int64_t rows, int64_t heads, in
     return nrs_heads_impl(out, in, rows, heads, width, beta, false);
 }
 
-int nrs_layernorm_forward(float* out, float* x_norm, float* inv_std, const float* in,
-                          const float* gamma, const float* beta, int64_t rows, int64_t features,
-                          float eps) {
+int nrs_add_layernorm_forward(float* out, float* x_norm, float* inv_std, const float* in,
+                              const float* in2, const float* gamma, const float* beta,
+                              int64_t rows, int64_t features, float eps) {
     NRS_REQUIRE_INIT();
     NRS_ARG_CHECK(rows >= 0 && features > 0, "layernorm: bad shape");
     if (rows == 0) return NRS_OK;
@@ -656,9 +660,16 @@ int nrs_layernorm_forward(float* out, float* x_norm, float* inv_std, const float
               : F <= 512 ? nrs::layernorm_fwd_kernel<8>
                          : nrs::layernorm_fwd_kernel<0>;
     hipLaunchKernelGGL(fn, dim3(nrs::rows_grid(rows)), dim3(256), 0, nrs::stream(), out, x_norm,
-                       inv_std, in, gamma, beta, rows, F, eps);
+                       inv_std, in, in2, gamma, beta, rows, F, eps);
     NRS_LAUNCH_CHECK("layernorm forward");
     return NRS_OK;
+}
+
+int nrs_layernorm_forward(float* out, float* x_norm, float* inv_std, const float* in,
+                          const float* gamma, const float* beta, int64_t rows, int64_t features,
+                          float eps) {
+    return nrs_add_layernorm_forward(out, x_norm, inv_std, in, nullptr, gamma, beta, rows,
+                                     features, eps);
 }
 
 int nrs_layernorm_backward(float* dinput, float* dgamma, float* dbeta, const float* grad,

@@ -554,48 +554,74 @@ NodeRef conv2d(const NodeRef& input, const NodeRef& weight, const NodeRef& bias,
     return node;
 }
 
-NodeRef Linear::forward(const NodeRef& input) const {
+namespace {
+
+// The backward of a Linear node (its matmul closure and the bias's
+// sum_axis0, linear.rs:22-25) given the gradient g of its output.
+void linear_backward_into(const NodeRef& x, const NodeRef& w, const NodeRef& b, const float* g,
+                          size_t batch, size_t in_f, size_t out_f) {
+    GpuBuffers& xg = gpu_of(x, "cuda matmul bwd: lhs not on GPU");
+    GpuBuffers& wg = gpu_of(w, "cuda matmul bwd: rhs not on GPU");
+    GpuBuffers& bg = gpu_of(b, "backward: parent not on GPU");
+    if (xg.grad == wg.grad || xg.grad == bg.grad || wg.grad == bg.grad) {
+        // parents sharing a gradient: the products one after the other
+        matmul_backward_into(x, w, g, batch, in_f, out_f, "cuda linear bwd: launch");
+        float beta = 1.0f;
+        float* db = bg.grad->acc_target(beta);
+        check(nrs_sum_axis0(db, g, batch, out_f, beta), "cuda linear bwd: bias launch");
+        return;
+    }
+    // dx += g . W^T, dW += x^T . g and db += column sums of g, one grouped
+    // launch (the bias gradient rides the weight gradient)
+    float bx = 1.0f, bw = 1.0f, bb = 1.0f;
+    float* dx = xg.grad->acc_target(bx);
+    float* dw = wg.grad->acc_target(bw);
+    float* db = bg.grad->acc_target(bb);
+    check(nrs_linear_backward(dx, dw, db, g, xg.data.ptr(), wg.data.ptr(), batch, in_f, out_f, bx,
+                              bw, bb),
+          "cuda linear bwd: launch");
+}
+
+// x . W + bias, optionally followed by ReLU in the same GEMM epilogue.
+NodeRef linear_node(const Linear& l, const NodeRef& input, bool relu) {
     GpuBuffers& xg = gpu_of(input, "cuda matmul: lhs not on GPU");
-    GpuBuffers& wg = gpu_of(weights, "cuda matmul: rhs not on GPU");
-    GpuBuffers& bg = gpu_of(bias, "cuda add: rhs not on GPU");
-    if (input->shape.size() != 2 || weights->shape.size() != 2)
+    GpuBuffers& wg = gpu_of(l.weights, "cuda matmul: rhs not on GPU");
+    GpuBuffers& bg = gpu_of(l.bias, "cuda add: rhs not on GPU");
+    if (input->shape.size() != 2 || l.weights->shape.size() != 2)
         throw Panic("cuda matmul: operands must be 2-D");
-    const size_t batch = input->shape[0], in_f = input->shape[1], out_f = weights->shape[1];
-    if (weights->shape[0] != in_f) throw Panic("cuda matmul: inner dims mismatch");
-    if (product(bias->shape) != out_f) throw Panic("cuda add: bias length mismatch");
+    const size_t batch = input->shape[0], in_f = input->shape[1], out_f = l.weights->shape[1];
+    if (l.weights->shape[0] != in_f) throw Panic("cuda matmul: inner dims mismatch");
+    if (product(l.bias->shape) != out_f) throw Panic("cuda add: bias length mismatch");
     // x . W + bias in one GEMM: bias added in the epilogue (matmul + add).
     DeviceBuffer out(batch * out_f, false);
     check(nrs_gemm(NRS_NN, out.ptr(), xg.data.ptr(), wg.data.ptr(), batch, out_f, in_f, 0.0f,
-                   bg.data.ptr(), NRS_EPI_BIAS_COL),
+                   bg.data.ptr(), NRS_EPI_BIAS_COL | (relu ? NRS_EPI_RELU : 0)),
           "cuda linear: launch failed");
-    NodeRef x = input, w = weights, b = bias;
+    NodeRef x = input, w = l.weights, b = l.bias;
     NodeRef node = make_output({batch, out_f}, {x, w, b}, std::move(out));
-    node->backward_fn = [grad = node->gpu->grad, x, w, b, batch, in_f,
+    if (!relu) {
+        node->backward_fn = [grad = node->gpu->grad, x, w, b, batch, in_f,
+                             out_f](const std::vector<float>&) {
+            linear_backward_into(x, w, b, grad->ptr(), batch, in_f, out_f);
+        };
+        return node;
+    }
+    // relu.rs:30-45 masks by the pre-activation; the output is positive
+    // exactly where it is, so the mask is read from the node's own output
+    const float* y = node->gpu->data.ptr();
+    node->backward_fn = [grad = node->gpu->grad, x, w, b, y, batch, in_f,
                          out_f](const std::vector<float>&) {
-        GpuBuffers& xg = gpu_of(x, "cuda matmul bwd: lhs not on GPU");
-        GpuBuffers& wg = gpu_of(w, "cuda matmul bwd: rhs not on GPU");
-        GpuBuffers& bg = gpu_of(b, "backward: parent not on GPU");
-        if (xg.grad == wg.grad || xg.grad == bg.grad || wg.grad == bg.grad) {
-            // parents sharing a gradient: the products one after the other
-            matmul_backward_into(x, w, grad->ptr(), batch, in_f, out_f, "cuda linear bwd: launch");
-            float beta = 1.0f;
-            float* db = bg.grad->acc_target(beta);
-            check(nrs_sum_axis0(db, grad->ptr(), batch, out_f, beta),
-                  "cuda linear bwd: bias launch");
-            return;
-        }
-        // dx += g . W^T, dW += x^T . g and db += column sums of g, one
-        // grouped launch (the bias gradient rides the weight gradient)
-        float bx = 1.0f, bw = 1.0f, bb = 1.0f;
-        float* dx = xg.grad->acc_target(bx);
-        float* dw = wg.grad->acc_target(bw);
-        float* db = bg.grad->acc_target(bb);
-        check(nrs_linear_backward(dx, dw, db, grad->ptr(), xg.data.ptr(), wg.data.ptr(), batch,
-                                  in_f, out_f, bx, bw, bb),
-              "cuda linear bwd: launch");
+        DeviceBuffer gm(batch * out_f, false);
+        check(nrs_relu_backward(gm.ptr(), grad->ptr(), y, batch * out_f, 0.0f),
+              "cuda relu bwd: launch");
+        linear_backward_into(x, w, b, gm.ptr(), batch, in_f, out_f);
     };
     return node;
 }
+
+}  // namespace
+
+NodeRef Linear::forward(const NodeRef& input) const { return linear_node(*this, input, false); }
 
 namespace {
 
@@ -798,15 +824,83 @@ NodeRef MultiHeadAttention::forward_batch(const NodeRef& x) const {
     return graph::reshape(out, {batch, seq, d});
 }
 
+namespace {
+
+// norm(add(a, b)) as one node: the residual add and the LayerNorm of
+// transformer_block.rs:32-33, 41-42, with the sum never written out. The
+// add node is internal to the block, so no graph node a caller can reach is
+// lost. Its backward is the LayerNorm's, whose input gradient goes to both
+// a and b (add.rs's backward): straight into a's gradient when that is a
+// pending zero (then copied or added into b's), else through a temporary.
+NodeRef add_layernorm(const NodeRef& a, const NodeRef& b, const LayerNorm& norm) {
+    GpuBuffers& ag = gpu_of(a, "cuda add: lhs not on GPU");
+    GpuBuffers& bgb = gpu_of(b, "cuda add: rhs not on GPU");
+    GpuBuffers& gg = gpu_of(norm.gamma, "cuda layernorm: gamma not on GPU");
+    GpuBuffers& betag = gpu_of(norm.beta, "cuda layernorm: beta not on GPU");
+    if (product(b->shape) != product(a->shape)) throw Panic("cuda add: shape mismatch");
+    if (a->shape.empty()) throw Panic("cuda layernorm: scalar input");
+    const size_t F = a->shape.back(), len = product(a->shape);
+    const size_t rows = F ? len / F : 0;
+    if (F == 0 || product(norm.gamma->shape) != F || product(norm.beta->shape) != F)
+        throw Panic("cuda layernorm: gamma/beta length mismatch");
+    DeviceBuffer out(len, false);
+    auto xn = std::make_shared<DeviceBuffer>(len, false);
+    auto istd = std::make_shared<DeviceBuffer>(rows, false);
+    check(nrs_add_layernorm_forward(out.ptr(), xn->ptr(), istd->ptr(), ag.data.ptr(),
+                                    bgb.data.ptr(), gg.data.ptr(), betag.data.ptr(), rows, F,
+                                    norm.eps),
+          "cuda layernorm: forward launch failed");
+    NodeRef gamma = norm.gamma, beta = norm.beta;
+    NodeRef node = make_output(a->shape, {a, b, gamma, beta}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, a, b, gamma, beta, xn, istd, rows, F,
+                         len](const std::vector<float>&) {
+        GpuBuffers& ag = gpu_of(a, "cuda layernorm bwd: input not on GPU");
+        GpuBuffers& bgb = gpu_of(b, "cuda layernorm bwd: input not on GPU");
+        GpuBuffers& gg = gpu_of(gamma, "cuda layernorm bwd: gamma not on GPU");
+        GpuBuffers& betag = gpu_of(beta, "cuda layernorm bwd: beta not on GPU");
+        const bool distinct = ag.grad != bgb.grad && ag.grad != gg.grad &&
+                              ag.grad != betag.grad && bgb.grad != gg.grad &&
+                              bgb.grad != betag.grad && gg.grad != betag.grad;
+        if (distinct && ag.grad->pending_zero()) {
+            // a's gradient becomes exactly the input gradient
+            const float acc = joint_beta({ag.grad.get(), gg.grad.get(), betag.grad.get()});
+            check(nrs_layernorm_backward(ag.grad->ptr(), gg.grad->ptr(), betag.grad->ptr(),
+                                         grad->ptr(), gg.data.ptr(), xn->ptr(), istd->ptr(), rows,
+                                         F, acc),
+                  "cuda layernorm bwd: launch");
+            accumulate_into(*bgb.grad, ag.grad->ptr(), len);
+            return;
+        }
+        DeviceBuffer tmp(len, false);
+        check(nrs_layernorm_backward(tmp.ptr(), nullptr, nullptr, grad->ptr(), gg.data.ptr(),
+                                     xn->ptr(), istd->ptr(), rows, F, 0.0f),
+              "cuda layernorm bwd: launch");
+        const float accp =
+            gg.grad != betag.grad ? joint_beta({gg.grad.get(), betag.grad.get()}) : 1.0f;
+        check(nrs_layernorm_backward(nullptr, gg.grad->ptr(), betag.grad->ptr(), grad->ptr(),
+                                     gg.data.ptr(), xn->ptr(), istd->ptr(), rows, F, accp),
+              "cuda layernorm bwd: launch");
+        accumulate_into(*ag.grad, tmp.ptr(), len);
+        accumulate_into(*bgb.grad, tmp.ptr(), len);
+    };
+    return node;
+}
+
+}  // namespace
+
 NodeRef TransformerBlock::forward(const NodeRef& x) const {
     if (x->shape.size() != 3) throw Panic("transformer block: x must be [batch, seq, d_model]");
     const size_t batch = x->shape[0], seq = x->shape[1], d = x->shape[2];
     NodeRef attn_out = mha.forward_batch(x);
-    NodeRef x1 = norm1.forward(graph::add(x, attn_out));
+    // norm1(add(x, attn_out)) and norm2(add(x1, ff_out)) each as one node,
+    // relu(ff1(x1)) as one node with ReLU in the GEMM epilogue: the sums and
+    // the pre-activation are internal to the block, so no node a caller can
+    // reach is lost
+    NodeRef x1 = add_layernorm(x, attn_out, norm1);
     NodeRef flat = graph::reshape(x1, {batch * seq, d});
-    NodeRef h = graph::relu(ff1.forward(flat));
+    NodeRef h = linear_node(ff1, flat, true);
     NodeRef ff_out = graph::reshape(ff2.forward(h), {batch, seq, d});
-    return norm2.forward(graph::add(x1, ff_out));
+    return add_layernorm(x1, ff_out, norm2);
 }
 
 NodeRef layernorm(const NodeRef& input, const NodeRef& gamma, const NodeRef& beta, float eps) {

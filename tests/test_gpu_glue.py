@@ -339,3 +339,24 @@ def test_layernorm_backward_zero_rows(hip):
     hip.call("nrs_layernorm_backward", None, dg2.ptr, db2.ptr, None, None, None, None, 0, F, 1.0)
     assert np.array_equal(dg2.to_host(), old_g)
     assert np.array_equal(db2.to_host(), old_g * 2)
+
+
+@pytest.mark.parametrize("rows,F", [(4096, 256), (3, 65), (70, 512), (9, 600)])
+def test_add_layernorm_matches_add_then_layernorm(hip, rows, F):
+    """The fused residual add + LayerNorm gives the bits of nrs_vadd followed
+    by nrs_layernorm_forward (register and re-reading forms)."""
+    rng = np.random.default_rng(rows + F)
+    a, b = (rng.standard_normal(rows * F).astype(np.float32) for _ in range(2))
+    g, be = rng.standard_normal(F).astype(np.float32), rng.standard_normal(F).astype(np.float32)
+    da, db_, dg, dbe = dev(hip, a), dev(hip, b), dev(hip, g), dev(hip, be)
+    s = hip.DeviceBuffer(rows * F)
+    hip.call("nrs_vadd", s.ptr, da.ptr, db_.ptr, rows * F)
+    outs = [[hip.DeviceBuffer(rows * F), hip.DeviceBuffer(rows * F), hip.DeviceBuffer(rows)]
+            for _ in range(2)]
+    o, xn, istd = outs[0]
+    hip.call("nrs_layernorm_forward", o.ptr, xn.ptr, istd.ptr, s.ptr, dg.ptr, dbe.ptr, rows, F, 1e-5)
+    o2, xn2, istd2 = outs[1]
+    hip.call("nrs_add_layernorm_forward", o2.ptr, xn2.ptr, istd2.ptr, da.ptr, db_.ptr, dg.ptr,
+             dbe.ptr, rows, F, 1e-5)
+    for x, y in zip(outs[0], outs[1]):
+        assert np.array_equal(x.to_host(), y.to_host())
