@@ -356,6 +356,15 @@ int nrs_add_layernorm_forward(float *out, float *x_norm, float *inv_std, const f
 int nrs_layernorm_backward(float *dinput, float *dgamma, float *dbeta, const float *grad,
                            const float *gamma, const float *x_norm, const float *inv_std,
                            int64_t rows, int64_t features, float acc);
+/* The backward of norm(a + b) (transformer_block.rs:32-33, 41-42; the add's
+ * backward, src/cuda/graph/add.rs:41-110, hands the input gradient to both a
+ * and b): the input gradient of nrs_layernorm_backward stored to da (+ beta_a
+ * * old) and, when db is not NULL, to db (+ beta_b * old) in the same pass;
+ * the parameter gradients take beta_params. db needs da.                     */
+int nrs_add_layernorm_backward(float *da, float *db, float *dgamma, float *dbeta,
+                               const float *grad, const float *gamma, const float *x_norm,
+                               const float *inv_std, int64_t rows, int64_t features, float beta_a,
+                               float beta_b, float beta_params);
 /* vrelu / relu_grad (src/cuda/graph/relu.rs:16-28): out = max(x, 0);
  * gin = (x > 0 ? grad : 0) + beta*gin.                                       */
 int nrs_relu_forward(float *out, const float *x, int64_t n);

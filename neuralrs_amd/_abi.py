@@ -84,6 +84,7 @@ SIGNATURES = {
     "nrs_layernorm_forward": [_P, _P, _P, _P, _P, _P, _I, _I, _F],
     "nrs_add_layernorm_forward": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _F],
     "nrs_layernorm_backward": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _F],
+    "nrs_add_layernorm_backward": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _F, _F],
     "nrs_merge_heads": [_P, _P, _I, _I, _I, _F],
     "nrs_softmax_forward_scaled": [_P, _P, _I, _I, _F],
     "nrs_softmax_backward_scaled": [_P, _P, _P, _I, _I, _F, _F],

@@ -313,10 +313,12 @@ __global__ __launch_bounds__(256) void layernorm_fwd_kernel(
 // LayerNorm input gradient, one wave per row (normalization.rs:57-80 ln_dx):
 // dxh = grad * gamma, dinput = inv_std * (dxh - sum(dxh)/F - x_norm *
 // sum(dxh * x_norm)/F) + acc * dinput.
+// dinput = dx + acc * dinput and, when dinput2 is set, dinput2 = dx + acc2 *
+// dinput2 (the input gradient of norm(a + b) goes to both a and b).
 __global__ __launch_bounds__(256) void layernorm_dx_kernel(
-    float* __restrict__ dinput, const float* __restrict__ grad, const float* __restrict__ gamma,
-    const float* __restrict__ x_norm, const float* __restrict__ inv_std, int64_t rows, int64_t F,
-    float acc) {
+    float* __restrict__ dinput, float* __restrict__ dinput2, const float* __restrict__ grad,
+    const float* __restrict__ gamma, const float* __restrict__ x_norm,
+    const float* __restrict__ inv_std, int64_t rows, int64_t F, float acc, float acc2) {
     const int lane = threadIdx.x & 63;
     const int64_t waves = (int64_t)gridDim.x * 4;
     const float nf = (float)F;
@@ -333,10 +335,11 @@ __global__ __launch_bounds__(256) void layernorm_dx_kernel(
         s2 = wave_sum(s2) / nf;
         const float istd = inv_std[r];
         float* o = dinput + r * F;
+        float* o2 = dinput2 ? dinput2 + r * F : nullptr;
         for (int64_t f = lane; f < F; f += 64) {
-            float v = istd * (g[f] * gamma[f] - s1 - xn[f] * s2);
-            if (acc != 0.0f) v = v + acc * o[f];
-            o[f] = v;
+            const float dx = istd * (g[f] * gamma[f] - s1 - xn[f] * s2);
+            o[f] = acc != 0.0f ? dx + acc * o[f] : dx;
+            if (o2) o2[f] = acc2 != 0.0f ? dx + acc2 * o2[f] : dx;
         }
     }
 }
@@ -675,7 +678,19 @@ int nrs_layernorm_forward(float* out, float* x_norm, float* inv_std, const float
 int nrs_layernorm_backward(float* dinput, float* dgamma, float* dbeta, const float* grad,
                            const float* gamma, const float* x_norm, const float* inv_std,
                            int64_t rows, int64_t features, float acc) {
+    return nrs_add_layernorm_backward(dinput, nullptr, dgamma, dbeta, grad, gamma, x_norm, inv_std,
+                                      rows, features, acc, 0.0f, acc);
+}
+
+int nrs_add_layernorm_backward(float* da, float* db, float* dgamma, float* dbeta, const float* grad,
+                               const float* gamma, const float* x_norm, const float* inv_std,
+                               int64_t rows, int64_t features, float beta_a, float beta_b,
+                               float beta_params) {
     NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(db == nullptr || da != nullptr, "layernorm backward: second input gradient "
+                                                  "without the first");
+    float* dinput = da;
+    const float acc = beta_params;
     NRS_ARG_CHECK(rows >= 0 && features > 0, "layernorm backward: bad shape");
     const int64_t F = features;
     if (rows == 0) {
@@ -693,7 +708,8 @@ int nrs_layernorm_backward(float* dinput, float* dgamma, float* dbeta, const flo
     if (dinput) {
         NRS_ARG_CHECK(gamma && inv_std, "layernorm backward: null gamma or inv_std");
         hipLaunchKernelGGL(nrs::layernorm_dx_kernel, dim3(nrs::rows_grid(rows)), dim3(256), 0,
-                           nrs::stream(), dinput, grad, gamma, x_norm, inv_std, rows, F, acc);
+                           nrs::stream(), dinput, db, grad, gamma, x_norm, inv_std, rows, F,
+                           beta_a, beta_b);
         NRS_LAUNCH_CHECK("layernorm backward (input)");
     }
     if (dgamma || dbeta) {

@@ -155,26 +155,37 @@ DeviceBuffer DeviceBuffer::from_host(const std::vector<float>& v) {
     return b;
 }
 
+DeviceBuffer DeviceBuffer::view_of(const DeviceBuffer& src) {
+    DeviceBuffer v;
+    v.ptr_ = src.ptr();  // a pending zero is cleared: the view reads memory
+    v.len_ = src.len_;
+    v.owned_ = false;
+    return v;
+}
+
 DeviceBuffer::~DeviceBuffer() {
-    if (ptr_) nrs_free(ptr_);
+    if (ptr_ && owned_) nrs_free(ptr_);
 }
 
 DeviceBuffer::DeviceBuffer(DeviceBuffer&& o) noexcept
-    : ptr_(o.ptr_), len_(o.len_), pending_zero_(o.pending_zero_) {
+    : ptr_(o.ptr_), len_(o.len_), pending_zero_(o.pending_zero_), owned_(o.owned_) {
     o.ptr_ = nullptr;
     o.len_ = 0;
     o.pending_zero_ = false;
+    o.owned_ = true;
 }
 
 DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
     if (this != &o) {
-        if (ptr_) nrs_free(ptr_);
+        if (ptr_ && owned_) nrs_free(ptr_);
         ptr_ = o.ptr_;
         len_ = o.len_;
         pending_zero_ = o.pending_zero_;
+        owned_ = o.owned_;
         o.ptr_ = nullptr;
         o.len_ = 0;
         o.pending_zero_ = false;
+        o.owned_ = true;
     }
     return *this;
 }
@@ -786,6 +797,24 @@ NodeRef attention_batch(const NodeRef& q, const NodeRef& k, const NodeRef& v) {
     return graph::bmm(weights, v);
 }
 
+// `a` in another shape without a copy: the node shares a's device memory and
+// its gradient, so its consumers' gradients land in a's gradient directly and
+// it has no backward of its own. Only for reshapes internal to a composite
+// node (the flattening inside MultiHeadAttention and TransformerBlock), which
+// no caller can reach: graph::reshape copies, as the reference does
+// (src/cuda/graph/reshape.rs:31-70), and keeps the two gradients apart.
+static NodeRef reshape_view(const NodeRef& a, std::vector<size_t> shape) {
+    GpuBuffers& ag = gpu_of(a, "cuda reshape: input not on GPU");
+    if (product(shape) != product(a->shape)) throw Panic("cuda reshape: element count mismatched");
+    NodeRef out = std::make_shared<Node>();
+    out->shape = std::move(shape);
+    out->parents = {a};
+    out->gpu = std::make_unique<GpuBuffers>();
+    out->gpu->data = DeviceBuffer::view_of(ag.data);
+    out->gpu->grad = ag.grad;
+    return out;
+}
+
 // Shared by forward (batch 1) and forward_batch: the projections of the
 // flattened input, every head's attention at once, the output projection.
 static NodeRef multihead(const MultiHeadAttention& mha, const NodeRef& flat, size_t batch,
@@ -820,7 +849,7 @@ NodeRef MultiHeadAttention::forward(const NodeRef& x) const {
 NodeRef MultiHeadAttention::forward_batch(const NodeRef& x) const {
     if (x->shape.size() != 3) throw Panic("multihead: x must be [batch, seq, d_model]");
     const size_t batch = x->shape[0], seq = x->shape[1], d = x->shape[2];
-    NodeRef out = multihead(*this, graph::reshape(x, {batch * seq, d}), batch, seq, d);
+    NodeRef out = multihead(*this, reshape_view(x, {batch * seq, d}), batch, seq, d);
     return graph::reshape(out, {batch, seq, d});
 }
 
@@ -830,8 +859,9 @@ namespace {
 // transformer_block.rs:32-33, 41-42, with the sum never written out. The
 // add node is internal to the block, so no graph node a caller can reach is
 // lost. Its backward is the LayerNorm's, whose input gradient goes to both
-// a and b (add.rs's backward): straight into a's gradient when that is a
-// pending zero (then copied or added into b's), else through a temporary.
+// a and b (add.rs's backward): stored to or added into both gradients by one
+// launch when the four gradients are distinct buffers, else through a
+// temporary.
 NodeRef add_layernorm(const NodeRef& a, const NodeRef& b, const LayerNorm& norm) {
     GpuBuffers& ag = gpu_of(a, "cuda add: lhs not on GPU");
     GpuBuffers& bgb = gpu_of(b, "cuda add: rhs not on GPU");
@@ -861,14 +891,18 @@ NodeRef add_layernorm(const NodeRef& a, const NodeRef& b, const LayerNorm& norm)
         const bool distinct = ag.grad != bgb.grad && ag.grad != gg.grad &&
                               ag.grad != betag.grad && bgb.grad != gg.grad &&
                               bgb.grad != betag.grad && gg.grad != betag.grad;
-        if (distinct && ag.grad->pending_zero()) {
-            // a's gradient becomes exactly the input gradient
-            const float acc = joint_beta({ag.grad.get(), gg.grad.get(), betag.grad.get()});
-            check(nrs_layernorm_backward(ag.grad->ptr(), gg.grad->ptr(), betag.grad->ptr(),
-                                         grad->ptr(), gg.data.ptr(), xn->ptr(), istd->ptr(), rows,
-                                         F, acc),
+        if (distinct) {
+            // the input gradient stored to (or added into) both a's and b's
+            // gradients in one pass
+            float beta_a = 1.0f, beta_b = 1.0f;
+            float* da = ag.grad->acc_target(beta_a);
+            float* db = bgb.grad->acc_target(beta_b);
+            const float acc = gg.grad != betag.grad ? joint_beta({gg.grad.get(), betag.grad.get()})
+                                                    : 1.0f;
+            check(nrs_add_layernorm_backward(da, db, gg.grad->ptr(), betag.grad->ptr(), grad->ptr(),
+                                             gg.data.ptr(), xn->ptr(), istd->ptr(), rows, F,
+                                             beta_a, beta_b, acc),
                   "cuda layernorm bwd: launch");
-            accumulate_into(*bgb.grad, ag.grad->ptr(), len);
             return;
         }
         DeviceBuffer tmp(len, false);
@@ -891,15 +925,16 @@ NodeRef add_layernorm(const NodeRef& a, const NodeRef& b, const LayerNorm& norm)
 NodeRef TransformerBlock::forward(const NodeRef& x) const {
     if (x->shape.size() != 3) throw Panic("transformer block: x must be [batch, seq, d_model]");
     const size_t batch = x->shape[0], seq = x->shape[1], d = x->shape[2];
-    NodeRef attn_out = mha.forward_batch(x);
-    // norm1(add(x, attn_out)) and norm2(add(x1, ff_out)) each as one node,
-    // relu(ff1(x1)) as one node with ReLU in the GEMM epilogue: the sums and
-    // the pre-activation are internal to the block, so no node a caller can
-    // reach is lost
+    if (d != mha.d_model) throw Panic("multihead: input width is not d_model");
+    // mha.forward_batch(x) without its reshapes: the attention output stays
+    // [batch*seq, d] (add_layernorm takes it as is); norm1(add(x, attn_out))
+    // and norm2(add(x1, ff_out)) each as one node, relu(ff1(x1)) as one node
+    // with ReLU in the GEMM epilogue. The reshapes, sums and pre-activation
+    // are internal to the block, so no node a caller can reach is lost.
+    NodeRef attn_out = multihead(mha, reshape_view(x, {batch * seq, d}), batch, seq, d);
     NodeRef x1 = add_layernorm(x, attn_out, norm1);
-    NodeRef flat = graph::reshape(x1, {batch * seq, d});
-    NodeRef h = linear_node(ff1, flat, true);
-    NodeRef ff_out = graph::reshape(ff2.forward(h), {batch, seq, d});
+    NodeRef h = linear_node(ff1, reshape_view(x1, {batch * seq, d}), true);
+    NodeRef ff_out = ff2.forward(h);
     return add_layernorm(x1, ff_out, norm2);
 }
 

@@ -56,6 +56,10 @@ public:
     DeviceBuffer() = default;
     explicit DeviceBuffer(size_t len, bool zero = true);  // stream.alloc_zeros
     static DeviceBuffer from_host(const std::vector<float>& v);  // stream.clone_htod
+    // The memory of `src` without owning it (not freed by this buffer): the
+    // data of a node internal to a composite op that shows another node's
+    // values in another shape. `src` must outlive the view.
+    static DeviceBuffer view_of(const DeviceBuffer& src);
     ~DeviceBuffer();
     DeviceBuffer(DeviceBuffer&& o) noexcept;
     DeviceBuffer& operator=(DeviceBuffer&& o) noexcept;
@@ -91,6 +95,7 @@ private:
     float* ptr_ = nullptr;
     size_t len_ = 0;
     mutable bool pending_zero_ = false;
+    bool owned_ = true;
 };
 
 // src/autograd/node.rs:49-53: device data plus a shared, swappable gradient.

@@ -360,3 +360,46 @@ def test_add_layernorm_matches_add_then_layernorm(hip, rows, F):
              dbe.ptr, rows, F, 1e-5)
     for x, y in zip(outs[0], outs[1]):
         assert np.array_equal(x.to_host(), y.to_host())
+
+
+@pytest.mark.parametrize("rows,F", [(4096, 256), (3, 65), (70, 512)])
+@pytest.mark.parametrize("betas", [(0.0, 0.0, 0.0), (1.0, 0.0, 1.0), (0.0, 1.0, 0.0), (1.0, 1.0, 1.0)])
+def test_add_layernorm_backward_two_outputs(hip, rows, F, betas):
+    """nrs_add_layernorm_backward gives a's and b's gradients the bits of
+    nrs_layernorm_backward's input gradient (each with its own beta) and the
+    parameter gradients its bits, in one pass."""
+    beta_a, beta_b, beta_p = betas
+    rng = np.random.default_rng(rows * 7 + F)
+    x = rng.standard_normal(rows * F).astype(np.float32)
+    g, be = rng.standard_normal(F).astype(np.float32), rng.standard_normal(F).astype(np.float32)
+    gr = rng.standard_normal(rows * F).astype(np.float32)
+    old_a, old_b = (rng.standard_normal(rows * F).astype(np.float32) for _ in range(2))
+    old_g, old_be = (rng.standard_normal(F).astype(np.float32) for _ in range(2))
+    o, xn, istd = hip.DeviceBuffer(rows * F), hip.DeviceBuffer(rows * F), hip.DeviceBuffer(rows)
+    dg_ = dev(hip, g)
+    hip.call("nrs_layernorm_forward", o.ptr, xn.ptr, istd.ptr, dev(hip, x).ptr, dg_.ptr,
+             dev(hip, be).ptr, rows, F, 1e-5)
+    dgr = dev(hip, gr)
+    # reference: the single-output backward, once per beta
+    ra, rb = dev(hip, old_a), dev(hip, old_b)
+    rg, rbe = dev(hip, old_g), dev(hip, old_be)
+    hip.call("nrs_layernorm_backward", ra.ptr, None, None, dgr.ptr, dg_.ptr, xn.ptr, istd.ptr,
+             rows, F, beta_a)
+    hip.call("nrs_layernorm_backward", rb.ptr, None, None, dgr.ptr, dg_.ptr, xn.ptr, istd.ptr,
+             rows, F, beta_b)
+    hip.call("nrs_layernorm_backward", None, rg.ptr, rbe.ptr, dgr.ptr, dg_.ptr, xn.ptr, istd.ptr,
+             rows, F, beta_p)
+    da, db_ = dev(hip, old_a), dev(hip, old_b)
+    dgam, dbet = dev(hip, old_g), dev(hip, old_be)
+    print(f"add_layernorm_backward rows {rows} F {F} betas {betas}", flush=True)
+    hip.call("nrs_add_layernorm_backward", da.ptr, db_.ptr, dgam.ptr, dbet.ptr, dgr.ptr, dg_.ptr,
+             xn.ptr, istd.ptr, rows, F, beta_a, beta_b, beta_p)
+    for got, want in ((da, ra), (db_, rb), (dgam, rg), (dbet, rbe)):
+        assert np.array_equal(got.to_host(), want.to_host())
+
+
+def test_add_layernorm_backward_second_output_needs_first(hip):
+    buf = hip.DeviceBuffer(16)
+    with pytest.raises(hip.NrsError):
+        hip.call("nrs_add_layernorm_backward", None, buf.ptr, None, None, buf.ptr, buf.ptr,
+                 buf.ptr, buf.ptr, 4, 4, 0.0, 0.0, 0.0)
