@@ -206,11 +206,13 @@ def bench_mlp_cfg2(hip, steps, warmup):
     """cfg2 training step: x[256,784] -> Linear(784,128) -> ReLU ->
     Linear(128,10) -> cross-entropy seed (softmax - onehot)/256 (the fused
     ce_backward of src/cuda/loss/cross_entropy.rs:39-58) -> backward (dW, db
-    of both layers, dh, dx), in six library calls: bias and ReLU in the first
-    GEMM's epilogue, the ReLU backward masked by the activation (a > 0
-    exactly where the pre-activation is), each layer's weight, bias and input
-    gradients in one nrs_linear_backward. Issued from Python here; the same
-    step issued from C++ (eagerly and as a HIP graph) is host_step()."""
+    of both layers, dh, dx), in four library calls of one launch each: bias
+    and ReLU in the first GEMM's epilogue, the seed in the second's
+    (nrs_linear_cross_entropy), layer 2's backward with the ReLU backward in
+    its input gradient's epilogue (nrs_linear_backward_relu, masked by the
+    activation: a > 0 exactly where the pre-activation is), layer 1's
+    backward (nrs_linear_backward). Issued from Python here; the same step
+    issued from C++ (eagerly and as a HIP graph) is host_step()."""
     rng = np.random.default_rng(2)
     B, I, Hd, O = 256, 784, 128, 10
     D = hip.DeviceBuffer.from_host
@@ -222,16 +224,14 @@ def bench_mlp_cfg2(hip, steps, warmup):
     t[np.arange(B), rng.integers(0, O, B)] = 1.0
     onehot = D(t)
     a, z, gz = hip.DeviceBuffer(B * Hd), hip.DeviceBuffer(B * O), hip.DeviceBuffer(B * O)
-    ga, gh, gx = hip.DeviceBuffer(B * Hd), hip.DeviceBuffer(B * Hd), hip.DeviceBuffer(B * I)
+    gh, gx = hip.DeviceBuffer(B * Hd), hip.DeviceBuffer(B * I)
     gw1, gw2 = hip.DeviceBuffer.zeros(I * Hd), hip.DeviceBuffer.zeros(Hd * O)
     gb1, gb2 = hip.DeviceBuffer.zeros(Hd), hip.DeviceBuffer.zeros(O)
 
     def step():
         hip.gemm(hip.NN, a, x, w1, B, Hd, I, 0.0, b1, hip.EPI_BIAS_COL | hip.EPI_RELU)
-        hip.gemm(hip.NN, z, a, w2, B, O, Hd, 0.0, b2, hip.EPI_BIAS_COL)
-        hip.call("nrs_cross_entropy_backward", gz.ptr, z.ptr, onehot.ptr, B, O)
-        hip.call("nrs_linear_backward", ga, gw2, gb2, gz, a, w2, B, Hd, O, 0.0, 1.0, 1.0)
-        hip.call("nrs_relu_backward", gh.ptr, ga.ptr, a.ptr, B * Hd, 0.0)
+        hip.call("nrs_linear_cross_entropy", z, gz, a, w2, b2, onehot, B, Hd, O)
+        hip.call("nrs_linear_backward_relu", gh, gw2, gb2, gz, a, w2, a, B, Hd, O, 0.0, 1.0, 1.0)
         hip.call("nrs_linear_backward", gx, gw1, gb1, gh, x, w1, B, I, Hd, 0.0, 1.0, 1.0)
 
     us = event_ms(hip, step, steps, warmup) * 1e3
@@ -738,10 +738,11 @@ def main():
         hm = host_step("mlp", 200, 20)
         out["mlp_cfg2"] = {"python_us_per_step": round(m["us_per_step"], 2),
                            "gemm_roofline_us": round(m["gemm_roof_us"], 3),
-                           "library_calls": 6,
-                           "config": "cfg2 Linear 784->128 (+bias, ReLU epilogue), Linear 128->10, "
-                                     "batch 256, fused CE grad, fwd+bwd incl. dx and both bias "
-                                     "grads"}
+                           "library_calls": 4,
+                           "config": "cfg2 Linear 784->128 (+bias, ReLU epilogue), Linear 128->10 "
+                                     "(+bias, fused CE seed epilogue), batch 256, fwd+bwd incl. "
+                                     "dx and both bias grads (ReLU backward in layer 2's dx "
+                                     "epilogue)"}
         if hm:
             out["mlp_cfg2"].update({
                 "us_per_step": round(hm["eager_gpu_us"], 2),

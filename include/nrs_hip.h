@@ -140,6 +140,34 @@ int nrs_linear_backward(float *dx, float *dw, float *db, const float *grad,
                         const float *x, const float *w, int64_t batch, int64_t in_f,
                         int64_t out_f, float beta_x, float beta_w, float beta_b);
 
+/* nrs_linear_backward of a Linear whose input is the output of a ReLU, with
+ * the ReLU's backward (relu_grad, src/cuda/graph/relu.rs:16-28: the gradient
+ * passes where the ReLU input is > 0) applied to dx:
+ *   dx = (grad . W^T) * (mask > 0) + beta_x * dx
+ * mask is the ReLU's input or its output [batch, in_f] (both are > 0 at the
+ * same places), so dx is the gradient of the ReLU's INPUT, and the gradient
+ * of the ReLU's output is never materialised. dW and db as in
+ * nrs_linear_backward. One launch when both products are short (the mask
+ * rides the input-gradient product's epilogue); else the products, then one
+ * nrs_relu_backward pass. mask may be NULL only when dx is.               */
+int nrs_linear_backward_relu(float *dx, float *dw, float *db, const float *grad,
+                             const float *x, const float *w, const float *mask,
+                             int64_t batch, int64_t in_f, int64_t out_f,
+                             float beta_x, float beta_w, float beta_b);
+
+/* The last Linear of a classifier followed by the fused cross-entropy seed:
+ * Linear::forward (src/cuda/nn/linear.rs:22-25, matmul + bias add) then
+ * cross_entropy_backward (src/cuda/loss/cross_entropy.rs:39-58):
+ *   logits = x . W + bias                       [batch, classes]
+ *   grad   = (softmax(logits) - target) / batch [batch, classes]
+ * with the seed computed as ce_backward computes it (row max folded from
+ * class 0, sum of expf(l - max) in class order). bias may be NULL. One launch
+ * for at most 16 classes; else nrs_gemm then nrs_cross_entropy_backward.
+ * logits, grad and target must not overlap.                               */
+int nrs_linear_cross_entropy(float *logits, float *grad, const float *x, const float *w,
+                             const float *bias, const float *target, int64_t batch,
+                             int64_t in_f, int64_t classes);
+
 /* mm_nt_splitk(a, b, rows, cols, inner) (src/cuda/graph/matmul.rs:354-379):
  * C = A[rows,inner] . B[cols,inner]^T + beta*C for skinny outputs with a huge
  * inner dimension. The inner dimension is split across workgroups; partial

@@ -50,6 +50,8 @@ SIGNATURES = {
     "nrs_gemm": [ctypes.c_int, _P, _P, _P, _I, _I, _I, _F, _P, ctypes.c_int],
     "nrs_gemm_group": [ctypes.POINTER(GemmDesc), ctypes.c_int],
     "nrs_linear_backward": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _F, _F],
+    "nrs_linear_backward_relu": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _F, _F],
+    "nrs_linear_cross_entropy": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
     "nrs_gemm_nt_splitk": [_P, _P, _P, _I, _I, _I, _F],
     "nrs_gemm_nt_splitk_noalloc": [_P, _P, _P, _I, _I, _I, _F],
     "nrs_bmm": [ctypes.c_int, _P, _P, _P, _I, _I, _I, _I, _F],

@@ -4,6 +4,7 @@
 #include <algorithm>
 
 #include "gemm_kernel.hpp"
+#include "gemm_wsplit.hpp"
 
 namespace nrs {
 
@@ -319,6 +320,9 @@ int gemm_run(const GemmCall& c) {
     if (rc != NRS_OK || empty) return rc;
     const int layout = c.layout;
     const int64_t M = c.M, N = c.N, K = c.K, batch = c.batch;
+    // few output tiles over a reduction of at most a few rounds: one launch
+    // of the short-GEMM kernel, no split-K partials or reduce launch
+    if (wsplit_eligible(c, true)) return wsplit_run(&c, 1, nullptr);
     const bool dense = c.amode == OP_DENSE && c.bmode == OP_DENSE;
     const bool vec4 = vec4_loads(c);
 
@@ -368,6 +372,48 @@ bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
     return x < y + bbytes && y < x + abytes;
 }
 
+}  // namespace
+
+// True when no call's outputs (C, the row of sums) overlap another call's
+// outputs or operands (A, B, bias, and extra[j] of call j when given), so the
+// calls may run in any order or together.
+bool outputs_independent(const GemmCall* calls, int count, const OperandRange* extra) {
+    struct Range {
+        const void* p;
+        size_t bytes;
+    };
+    auto ranges = [&](int idx, bool outputs_only, Range (&r)[6]) {
+        const GemmCall& c = calls[idx];
+        int n = 0;
+        r[n++] = {c.C, sizeof(float) * (size_t)(c.M * c.N)};
+        if (c.sum_row) r[n++] = {c.sum_row, sizeof(float) * (size_t)c.N};
+        if (outputs_only) return n;
+        r[n++] = {c.A, sizeof(float) * (size_t)(c.M * c.K)};
+        r[n++] = {c.B, sizeof(float) * (size_t)(c.K * c.N)};
+        if (c.epi & (NRS_EPI_BIAS_COL | NRS_EPI_BIAS_ROW))
+            r[n++] = {c.bias, sizeof(float) * (size_t)std::max<int64_t>(
+                                  (c.epi & NRS_EPI_BIAS_COL) ? c.N : 0,
+                                  (c.epi & NRS_EPI_BIAS_ROW) ? c.M : 0)};
+        if (extra && extra[idx].p) r[n++] = {extra[idx].p, extra[idx].bytes};
+        return n;
+    };
+    for (int i = 0; i < count; ++i) {
+        if (calls[i].M == 0 || calls[i].N == 0) continue;
+        Range out[6], other[6];
+        const int no = ranges(i, true, out);
+        for (int j = 0; j < count; ++j) {
+            if (j == i || calls[j].M == 0 || calls[j].N == 0) continue;
+            const int nj = ranges(j, false, other);
+            for (int a = 0; a < no; ++a)
+                for (int b = 0; b < nj; ++b)
+                    if (overlaps(out[a].p, out[a].bytes, other[b].p, other[b].bytes)) return false;
+        }
+    }
+    return true;
+}
+
+namespace {
+
 // The group kernel's tile: 64x64x32, 2x2 waves of 32x32, prefetch depth 2,
 // compiled for up to four waves per SIMD so that several problems'
 // workgroups share a CU.
@@ -380,6 +426,8 @@ int gemm_group_run(const GemmCall* calls, int count) {
     NRS_ARG_CHECK(count >= 0 && (count == 0 || calls != nullptr), "gemm group: bad count");
     // Checks first, so that an invalid call launches nothing.
     bool grouped = count >= 2 && count <= kGroupMax;
+    bool short_group = grouped;  // every live call fits the short-GEMM kernel
+    bool is_live[kGroupMax] = {};
     int live = 0;
     for (int i = 0; i < count; ++i) {
         bool empty;
@@ -387,44 +435,24 @@ int gemm_group_run(const GemmCall* calls, int count) {
         if (rc != NRS_OK) return rc;
         if (empty) continue;
         ++live;
+        if (i < kGroupMax) is_live[i] = true;
         const GemmCall& c = calls[i];
         grouped = grouped && c.amode == OP_DENSE && c.bmode == OP_DENSE && c.batch == 1 &&
                   c.nchw_P == 0 && c.partial_buf == nullptr && c.force_slices == 0 &&
                   c.K > 0 && vec4_loads(c);
+        short_group = short_group && wsplit_eligible(c, true);
     }
     // An output overlapping another call's operand, bias or output would make
     // the result depend on the order the problems run in: such groups run one
     // call after another, in the order given.
-    struct Range {
-        const void* p;
-        size_t bytes;
-    };
-    auto ranges = [](const GemmCall& c, bool outputs_only, Range (&r)[5]) {
+    if ((grouped || short_group) && !outputs_independent(calls, count, nullptr))
+        grouped = short_group = false;
+    if (short_group && live >= 2) {
+        GemmCall live_calls[kGroupMax];
         int n = 0;
-        r[n++] = {c.C, sizeof(float) * (size_t)(c.M * c.N)};
-        if (c.sum_row) r[n++] = {c.sum_row, sizeof(float) * (size_t)c.N};
-        if (outputs_only) return n;
-        r[n++] = {c.A, sizeof(float) * (size_t)(c.M * c.K)};
-        r[n++] = {c.B, sizeof(float) * (size_t)(c.K * c.N)};
-        if (c.epi & (NRS_EPI_BIAS_COL | NRS_EPI_BIAS_ROW))
-            r[n++] = {c.bias, sizeof(float) * (size_t)std::max<int64_t>(
-                                  (c.epi & NRS_EPI_BIAS_COL) ? c.N : 0,
-                                  (c.epi & NRS_EPI_BIAS_ROW) ? c.M : 0)};
-        return n;
-    };
-    for (int i = 0; grouped && i < count; ++i) {
-        const GemmCall& ci = calls[i];
-        if (ci.M == 0 || ci.N == 0) continue;
-        Range out[5], other[5];
-        const int no = ranges(ci, true, out);
-        for (int j = 0; grouped && j < count; ++j) {
-            const GemmCall& cj = calls[j];
-            if (j == i || cj.M == 0 || cj.N == 0) continue;
-            const int nj = ranges(cj, false, other);
-            for (int a = 0; a < no; ++a)
-                for (int b = 0; b < nj; ++b)
-                    if (overlaps(out[a].p, out[a].bytes, other[b].p, other[b].bytes)) grouped = false;
-        }
+        for (int i = 0; i < count; ++i)
+            if (is_live[i]) live_calls[n++] = calls[i];
+        return wsplit_run(live_calls, n, nullptr);
     }
     if (!grouped || live < 2) {
         for (int i = 0; i < count; ++i) {
@@ -530,6 +558,90 @@ GemmCall bmm_call(int layout, float* C, const float* A, const float* B, int64_t 
 
 }  // namespace nrs
 
+namespace nrs {
+
+// nrs_linear_backward, with the input gradient masked (v = 0 where
+// mask <= 0) when mask is non-null.
+int linear_backward(float* dx, float* dw, float* db, const float* grad, const float* x,
+                    const float* w, const float* mask, int64_t batch, int64_t in_f, int64_t out_f,
+                    float beta_x, float beta_w, float beta_b) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(batch >= 0 && in_f >= 0 && out_f >= 0, "linear backward: negative size");
+    NRS_ARG_CHECK(dw != nullptr, "linear backward: null weight gradient");
+    if (in_f == 0 && db) {  // no weight rows to carry the row of sums
+        const int rc = nrs_sum_axis0(db, grad, batch, out_f, beta_b);
+        if (rc != NRS_OK || !dx) return rc;
+        db = nullptr;
+    }
+    // The row of sums rides the weight-gradient product when it costs no
+    // extra tile row (in_f not a multiple of 64) or the product is small;
+    // else (the cfg4 FFN's 256 x 1024 weight gradient: 80 tiles in place of
+    // 64) the column sums are a launch of their own after the group.
+    float* db_after = nullptr;
+    if (db && in_f % 64 == 0 && in_f * out_f > 65536) {
+        db_after = db;
+        db = nullptr;
+    }
+    nrs::GemmCall calls[2];
+    int n = 0;
+    nrs::GemmCall& cw = calls[n++];  // dW = x^T . grad, db = column sums of grad
+    cw.layout = NRS_TN;
+    cw.C = dw;
+    cw.A = x;
+    cw.B = grad;
+    cw.M = in_f;
+    cw.N = out_f;
+    cw.K = batch;
+    cw.beta = beta_w;
+    cw.sum_row = db;
+    cw.sum_beta = beta_b;
+    if (dx) {  // dx = grad . W^T
+        nrs::GemmCall& cx = calls[n++];
+        cx.layout = NRS_NT;
+        cx.C = dx;
+        cx.A = grad;
+        cx.B = w;
+        cx.M = batch;
+        cx.N = in_f;
+        cx.K = out_f;
+        cx.beta = beta_x;
+    }
+    if (mask && batch > 0 && in_f > 0) {
+        // dx masked in the product's epilogue when both products fit one
+        // short-GEMM launch; else dx goes through library scratch (slot 1)
+        // and nrs_relu_backward applies the mask
+        bool fits = true;
+        for (int i = 0; i < n; ++i) {
+            bool empty;
+            const int crc = check_call(calls[i], empty);
+            if (crc != NRS_OK) return crc;
+            fits = fits && !empty && wsplit_eligible(calls[i], true);
+        }
+        const OperandRange extra[2] = {{nullptr, 0},
+                                       {mask, sizeof(float) * (size_t)(batch * in_f)}};
+        if (fits && outputs_independent(calls, n, extra)) {
+            WsExtra ex[2];
+            ex[1].mask = mask;
+            const int rc = wsplit_run(calls, n, ex);
+            if (rc != NRS_OK || !db_after) return rc;
+            return nrs_sum_axis0(db_after, grad, batch, out_f, beta_b);
+        }
+        float* tmp = workspace(sizeof(float) * (size_t)(batch * in_f), 1);
+        if (!tmp) return NRS_ERR_ALLOC;
+        calls[1].C = tmp;
+        calls[1].beta = 0.0f;
+        int rc = gemm_group_run(calls, n);
+        if (rc == NRS_OK) rc = nrs_relu_backward(dx, tmp, mask, batch * in_f, beta_x);
+        if (rc != NRS_OK || !db_after) return rc;
+        return nrs_sum_axis0(db_after, grad, batch, out_f, beta_b);
+    }
+    const int rc = nrs::gemm_group_run(calls, n);
+    if (rc != NRS_OK || !db_after) return rc;
+    return nrs_sum_axis0(db_after, grad, batch, out_f, beta_b);
+}
+
+}  // namespace nrs
+
 extern "C" {
 
 int nrs_gemm(int layout, float* C, const float* A, const float* B, int64_t rows, int64_t cols,
@@ -575,50 +687,58 @@ int nrs_gemm_group(const nrs_gemm_desc* descs, int count) {
 int nrs_linear_backward(float* dx, float* dw, float* db, const float* grad, const float* x,
                         const float* w, int64_t batch, int64_t in_f, int64_t out_f, float beta_x,
                         float beta_w, float beta_b) {
+    return nrs::linear_backward(dx, dw, db, grad, x, w, nullptr, batch, in_f, out_f, beta_x,
+                                beta_w, beta_b);
+}
+
+int nrs_linear_backward_relu(float* dx, float* dw, float* db, const float* grad, const float* x,
+                             const float* w, const float* mask, int64_t batch, int64_t in_f,
+                             int64_t out_f, float beta_x, float beta_w, float beta_b) {
     NRS_REQUIRE_INIT();
-    NRS_ARG_CHECK(batch >= 0 && in_f >= 0 && out_f >= 0, "linear backward: negative size");
-    NRS_ARG_CHECK(dw != nullptr, "linear backward: null weight gradient");
-    if (in_f == 0 && db) {  // no weight rows to carry the row of sums
-        const int rc = nrs_sum_axis0(db, grad, batch, out_f, beta_b);
-        if (rc != NRS_OK || !dx) return rc;
-        db = nullptr;
+    NRS_ARG_CHECK(!dx || mask, "linear backward relu: null mask");
+    return nrs::linear_backward(dx, dw, db, grad, x, w, dx ? mask : nullptr, batch, in_f, out_f,
+                                beta_x, beta_w, beta_b);
+}
+
+int nrs_linear_cross_entropy(float* logits, float* grad, const float* x, const float* w,
+                             const float* bias, const float* target, int64_t batch, int64_t in_f,
+                             int64_t classes) {
+    NRS_REQUIRE_INIT();
+    NRS_ARG_CHECK(batch >= 0 && in_f >= 0 && classes >= 1, "linear cross_entropy: bad shape");
+    if (batch == 0) return NRS_OK;
+    NRS_ARG_CHECK(logits && grad && target && (in_f == 0 || (x && w)),
+                  "linear cross_entropy: null pointer");
+    const size_t out_bytes = sizeof(float) * (size_t)(batch * classes);
+    NRS_ARG_CHECK(!nrs::overlaps(logits, out_bytes, grad, out_bytes) &&
+                      !nrs::overlaps(grad, out_bytes, target, out_bytes),
+                  "linear cross_entropy: logits, grad and target must not overlap");
+    nrs::GemmCall c;
+    c.layout = NRS_NN;
+    c.C = logits;
+    c.A = x;
+    c.B = w;
+    c.M = batch;
+    c.N = classes;
+    c.K = in_f;
+    c.bias = bias;
+    c.epi = bias ? NRS_EPI_BIAS_COL : NRS_EPI_NONE;
+    bool empty;
+    const int rc = nrs::check_call(c, empty);
+    if (rc != NRS_OK) return rc;
+    nrs::OperandRange seed_out{grad, out_bytes};
+    if (classes <= 16 && nrs::wsplit_eligible(c, false) &&
+        nrs::outputs_independent(&c, 1, nullptr) &&
+        !nrs::overlaps(grad, out_bytes, x, sizeof(float) * (size_t)(batch * in_f)) &&
+        !nrs::overlaps(grad, out_bytes, w, sizeof(float) * (size_t)(in_f * classes))) {
+        (void)seed_out;
+        nrs::WsExtra e;
+        e.ce_grad = grad;
+        e.ce_target = target;
+        return nrs::wsplit_run(&c, 1, &e);
     }
-    // The row of sums rides the weight-gradient product when it costs no
-    // extra tile row (in_f not a multiple of 64) or the product is small;
-    // else (the cfg4 FFN's 256 x 1024 weight gradient: 80 tiles in place of
-    // 64) the column sums are a launch of their own after the group.
-    float* db_after = nullptr;
-    if (db && in_f % 64 == 0 && in_f * out_f > 65536) {
-        db_after = db;
-        db = nullptr;
-    }
-    nrs::GemmCall calls[2];
-    int n = 0;
-    nrs::GemmCall& cw = calls[n++];  // dW = x^T . grad, db = column sums of grad
-    cw.layout = NRS_TN;
-    cw.C = dw;
-    cw.A = x;
-    cw.B = grad;
-    cw.M = in_f;
-    cw.N = out_f;
-    cw.K = batch;
-    cw.beta = beta_w;
-    cw.sum_row = db;
-    cw.sum_beta = beta_b;
-    if (dx) {  // dx = grad . W^T
-        nrs::GemmCall& cx = calls[n++];
-        cx.layout = NRS_NT;
-        cx.C = dx;
-        cx.A = grad;
-        cx.B = w;
-        cx.M = batch;
-        cx.N = in_f;
-        cx.K = out_f;
-        cx.beta = beta_x;
-    }
-    const int rc = nrs::gemm_group_run(calls, n);
-    if (rc != NRS_OK || !db_after) return rc;
-    return nrs_sum_axis0(db_after, grad, batch, out_f, beta_b);
+    const int grc = nrs::gemm_run(c);
+    if (grc != NRS_OK) return grc;
+    return nrs_cross_entropy_backward(grad, logits, target, batch, classes);
 }
 
 int nrs_gemm_nt_splitk(float* C, const float* A, const float* B, int64_t rows, int64_t cols,

@@ -64,6 +64,15 @@ int gemm_run(const GemmCall& c);
 // qualify (see nrs_gemm_group), else gemm_run on each in order.
 int gemm_group_run(const GemmCall* calls, int count);
 
+// A further operand of a call (e.g. an epilogue's mask) for the overlap check.
+struct OperandRange {
+    const void* p;
+    size_t bytes;
+};
+// True when no call's outputs (C, row of sums) overlap another call's outputs
+// or operands (A, B, bias, extra[j] of call j when extra is non-null).
+bool outputs_independent(const GemmCall* calls, int count, const OperandRange* extra);
+
 // Batched products of small dense items (M, N, K <= 128, 16-byte aligned
 // items, K or the transposed operand's rows in whole float4s), without
 // epilogue; returns kBmmUnsupported (launching nothing) for any other call.

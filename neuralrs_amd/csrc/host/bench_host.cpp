@@ -136,26 +136,24 @@ int bench_mlp(int steps, int warmup) {
     std::uniform_int_distribution<int> cls(0, O - 1);
     for (int64_t r = 0; r < Bn; ++r) t[r * O + cls(rng)] = 1.0f;
     DeviceBuffer onehot = DeviceBuffer::from_host(t);
-    DeviceBuffer a(Bn * Hd, false), z(Bn * O, false), gz(Bn * O, false), ga(Bn * Hd, false),
+    DeviceBuffer a(Bn * Hd, false), z(Bn * O, false), gz(Bn * O, false),
         gh(Bn * Hd, false), gx(Bn * I, false);
     DeviceBuffer gw1(I * Hd, true), gw2(Hd * O, true), gb1(Hd, true), gb2(O, true);
     // the reference's step (Linear, ReLU, Linear, the fused cross-entropy
     // seed (softmax - onehot) / batch, then each layer's backward: dW and db
-    // accumulated, dh, dx): bias and ReLU ride the first GEMM's epilogue,
-    // the ReLU backward masks by the activation (a > 0 exactly where the
-    // pre-activation is), and each layer's backward is one nrs_linear_backward
-    // (weight, bias and input gradients; the bias gradient an extra row of
-    // the weight-gradient product)
+    // accumulated, dx written) in four library calls: layer 1 with bias and
+    // ReLU in the product's epilogue; layer 2 with the seed in its epilogue;
+    // layer 2's backward with the ReLU backward applied to its input
+    // gradient (the mask is the ReLU output: a > 0 exactly where the
+    // pre-activation is); layer 1's backward. Each is one launch.
     auto step = [&] {
         nrs_check(nrs_gemm(NRS_NN, a.ptr(), x.ptr(), w1.ptr(), Bn, Hd, I, 0.0f, b1.ptr(),
                            NRS_EPI_BIAS_COL | NRS_EPI_RELU), "l1+relu");
-        nrs_check(nrs_gemm(NRS_NN, z.ptr(), a.ptr(), w2.ptr(), Bn, O, Hd, 0.0f, b2.ptr(), NRS_EPI_BIAS_COL), "l2");
-        nrs_check(nrs_cross_entropy_backward(gz.ptr(), z.ptr(), onehot.ptr(), Bn, O), "ce");
-        // layer 2: dW2 (+=), db2 (+=) and dA (=), then the ReLU mask
-        nrs_check(nrs_linear_backward(ga.ptr(), gw2.ptr(), gb2.ptr(), gz.ptr(), a.ptr(), w2.ptr(),
-                                      Bn, Hd, O, 0.0f, 1.0f, 1.0f), "layer 2 bwd");
-        nrs_check(nrs_relu_backward(gh.ptr(), ga.ptr(), a.ptr(), Bn * Hd, 0.0f), "relu bwd");
-        // layer 1: dW1 (+=), db1 (+=) and dx (=)
+        nrs_check(nrs_linear_cross_entropy(z.ptr(), gz.ptr(), a.ptr(), w2.ptr(), b2.ptr(),
+                                           onehot.ptr(), Bn, Hd, O), "l2+ce");
+        nrs_check(nrs_linear_backward_relu(gh.ptr(), gw2.ptr(), gb2.ptr(), gz.ptr(), a.ptr(),
+                                           w2.ptr(), a.ptr(), Bn, Hd, O, 0.0f, 1.0f, 1.0f),
+                  "layer 2 bwd + relu bwd");
         nrs_check(nrs_linear_backward(gx.ptr(), gw1.ptr(), gb1.ptr(), gh.ptr(), x.ptr(), w1.ptr(),
                                       Bn, I, Hd, 0.0f, 1.0f, 1.0f), "layer 1 bwd");
     };
@@ -181,7 +179,7 @@ int bench_mlp(int steps, int warmup) {
     hip_check(hipGraphDestroy(graph), "destroy");
     hip_check(hipStreamDestroy(cap), "destroy");
     std::printf("{\"workload\": \"cfg2 MLP step 784-128-10 batch 256 through the C ABI\", "
-                "\"calls\": 6, \"eager_gpu_us\": %.2f, \"eager_wall_us\": %.2f, "
+                "\"calls\": 4, \"eager_gpu_us\": %.2f, \"eager_wall_us\": %.2f, "
                 "\"graph_gpu_us\": %.2f, \"graph_wall_us\": %.2f, \"steps\": %d}\n",
                 gpu_us, wall_us, g_gpu, g_wall, steps);
     return 0;

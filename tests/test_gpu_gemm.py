@@ -481,3 +481,136 @@ def test_bmm_small_items_accumulate(hip, layout, shape):
     dA, dB, dC = (hip.DeviceBuffer.from_host(x) for x in (a, b, c0))
     hip.bmm(layout, dC, dA, dB, bt, m, n, k, 0.5)
     assert np.array_equal(dC.to_host((bt, m, n)), want)
+
+
+# ------------------------------------------- short GEMMs and fused Linear heads
+SHORT_SHAPES = [  # outputs of few 64x64 tiles: one launch, K split over waves
+    (16, 16, 4), (15, 17, 3), (1, 1, 2000), (33, 47, 1500), (100, 7, 2048), (2, 300, 1029),
+    (256, 128, 784), (256, 10, 128), (128, 10, 256), (256, 128, 10), (784, 128, 256),
+    (256, 784, 128), (129, 65, 513),
+]
+
+
+@pytest.mark.parametrize("layout", [NN, NT, TN])
+@pytest.mark.parametrize("shape", SHORT_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("offset", [0, 1], ids=["aligned", "offset"])
+def test_short_gemm_exact_integers(hip, layout, shape, offset):
+    """Short GEMMs (K split over the waves of one workgroup, one or several
+    rounds): bit-exact on small integers, with 16-byte aligned operands
+    (128-bit loads where k is contiguous) and with every operand one float
+    past alignment (32-bit loads); beta = 1 accumulates."""
+    rows, cols, inner = shape
+    rng = np.random.default_rng(rows * 131 + cols * 17 + inner + layout)
+    a, b = operands(layout, rows, cols, inner, lambda s: int_matrix(rng, s, -3, 3))
+    A, B = logical(layout, a, b)
+    c0 = int_matrix(rng, (rows, cols), -3, 3)
+
+    def placed(x):
+        buf = hip.DeviceBuffer.from_host(np.concatenate([np.zeros(offset, np.float32), x.ravel()]))
+        return buf, buf.ptr + 4 * offset
+
+    (bA, pA), (bB, pB), (bC, pC) = placed(a), placed(b), placed(c0)
+    hip.gemm(layout, pC, pA, pB, rows, cols, inner, 1.0)
+    got = bC.to_host()[offset:].reshape(rows, cols)
+    assert np.array_equal(got, (A @ B).astype(np.float32) + c0), f"{LNAME[layout]} {shape}"
+
+
+@pytest.mark.parametrize("shape", [(100, 30, 50), (16, 16, 1), (70, 33, 1300)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_short_gemm_epilogues(hip, shape):
+    """Column bias, row bias + ReLU and beta on the short-GEMM path."""
+    rng = np.random.default_rng(19)
+    rows, cols, inner = shape
+    a, b = operands(NN, rows, cols, inner, lambda s: int_matrix(rng, s, -3, 3))
+    A, B = logical(NN, a, b)
+    prod = (A @ B).astype(np.float32)
+    c0, bc, br = int_matrix(rng, (rows, cols)), int_matrix(rng, (cols,)), int_matrix(rng, (rows,))
+    assert np.array_equal(run_gemm(hip, NN, a, b, rows, cols, inner, 1.0, c0), c0 + prod)
+    assert np.array_equal(run_gemm(hip, NN, a, b, rows, cols, inner, 0.0, None, bc, 1 | 4),
+                          np.maximum(prod + bc[None, :], 0))
+    assert np.array_equal(run_gemm(hip, NN, a, b, rows, cols, inner, 0.0, None, br, 2),
+                          prod + br[:, None])
+
+
+@pytest.mark.parametrize("batch,in_f,out_f", [(256, 128, 10), (256, 784, 128), (37, 30, 9),
+                                              (3, 5, 2), (4096, 256, 256), (300, 1000, 64)],
+                         ids=lambda v: str(v))
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+def test_linear_backward_relu_exact_integers(hip, orc, batch, in_f, out_f, beta):
+    """nrs_linear_backward_relu: dW, db as nrs_linear_backward, and
+    dx = (g . W^T) * (mask > 0) + beta dx, the Linear's input gradient passed
+    through the preceding ReLU's backward (the oracle's relu_backward,
+    src/autograd/graph/relu.rs), exact on small integers; the masked product
+    rides the short-GEMM epilogue, or (4096 x 256 x 256) the tiled products
+    followed by one ReLU-backward pass."""
+    rng = np.random.default_rng(batch + 7 * in_f + out_f)
+    g, x = int_matrix(rng, (batch, out_f), -3, 3), int_matrix(rng, (batch, in_f), -3, 3)
+    w = int_matrix(rng, (in_f, out_f), -3, 3)
+    mask = int_matrix(rng, (batch, in_f), -2, 2)  # ReLU input: negative, zero and positive
+    dx0, dw0, db0 = (int_matrix(rng, s, -3, 3) for s in ((batch, in_f), (in_f, out_f), (out_f,)))
+    D = hip.DeviceBuffer.from_host
+    ddx, ddw, ddb = D(dx0), D(dw0), D(db0)
+    hip.call("nrs_linear_backward_relu", ddx, ddw, ddb, D(g), D(x), D(w), D(mask), batch, in_f,
+             out_f, beta, beta, beta)
+    dh = (g @ w.T).astype(np.float32)
+    want_dx = np.zeros_like(dh)
+    orc.relu_backward(mask.ravel(), dh.ravel(), want_dx.reshape(-1))
+    assert np.array_equal(ddx.to_host((batch, in_f)), want_dx + beta * dx0)
+    assert np.array_equal(ddw.to_host((in_f, out_f)), x.T @ g + beta * dw0)
+    assert np.array_equal(ddb.to_host(), g.sum(axis=0) + beta * db0)
+
+
+def test_linear_backward_relu_matches_composition(hip):
+    """Same bits as nrs_linear_backward followed by nrs_relu_backward (random
+    f32 data, the cfg2 hidden layer)."""
+    rng = np.random.default_rng(5)
+    batch, in_f, out_f = 256, 128, 10
+    g = (rng.standard_normal((batch, out_f)) * 0.1).astype(np.float32)
+    h = np.maximum(rng.standard_normal((batch, in_f)), 0).astype(np.float32)
+    w = rng.standard_normal((in_f, out_f)).astype(np.float32)
+    D = hip.DeviceBuffer.from_host
+    dg, dh, dw_ = D(g), D(h), D(w)
+    fx, fw, fb = hip.DeviceBuffer(batch * in_f), hip.DeviceBuffer(in_f * out_f), hip.DeviceBuffer(out_f)
+    hip.call("nrs_linear_backward_relu", fx, fw, fb, dg, dh, dw_, dh, batch, in_f, out_f, 0.0, 0.0, 0.0)
+    cx, cw, cb = hip.DeviceBuffer(batch * in_f), hip.DeviceBuffer(in_f * out_f), hip.DeviceBuffer(out_f)
+    hip.call("nrs_linear_backward", cx, cw, cb, dg, dh, dw_, batch, in_f, out_f, 0.0, 0.0, 0.0)
+    hip.call("nrs_relu_backward", cx, cx, dh, batch * in_f, 0.0)
+    for f, c in ((fx, cx), (fw, cw), (fb, cb)):
+        assert np.array_equal(f.to_host(), c.to_host())
+
+
+@pytest.mark.parametrize("batch,in_f,classes", [(256, 128, 10), (37, 20, 16), (5, 9, 3),
+                                                (1000, 64, 10), (64, 32, 40), (3, 1, 1)],
+                         ids=lambda v: str(v))
+def test_linear_cross_entropy(hip, orc, batch, in_f, classes):
+    """nrs_linear_cross_entropy: logits = x . W + b (exact on small integers)
+    and the seed (softmax - t) / batch with the same bits as
+    nrs_cross_entropy_backward on those logits, within the CE test's bound of
+    the oracle's CrossEntropyLoss gradient; one launch up to 16 classes, the
+    GEMM and the seed kernel beyond (40 classes)."""
+    rng = np.random.default_rng(batch * 3 + classes)
+    x, w = int_matrix(rng, (batch, in_f), -2, 2), int_matrix(rng, (in_f, classes), -2, 2)
+    x, w = x * np.float32(0.25), w * np.float32(0.25)  # exact products, moderate logits
+    bias = int_matrix(rng, (classes,), -2, 2)
+    t = np.zeros((batch, classes), np.float32)
+    t[np.arange(batch), rng.integers(0, classes, batch)] = 1.0
+    D = hip.DeviceBuffer.from_host
+    dx, dw, db, dt = D(x), D(w), D(bias), D(t)
+    logits, grad = hip.DeviceBuffer(batch * classes), hip.DeviceBuffer(batch * classes)
+    hip.call("nrs_linear_cross_entropy", logits, grad, dx, dw, db, dt, batch, in_f, classes)
+    lg = logits.to_host((batch, classes))
+    assert np.array_equal(lg, (x @ w).astype(np.float32) + bias[None, :])
+    seed = hip.DeviceBuffer(batch * classes)
+    hip.call("nrs_cross_entropy_backward", seed, logits, dt, batch, classes)
+    assert np.array_equal(grad.to_host(), seed.to_host())
+    gw = orc.cross_entropy_grad(lg, t, classes)
+    assert np.abs(grad.to_host() - gw).max() <= 2e-7 + 1e-6 / batch
+
+
+def test_linear_cross_entropy_errors(hip):
+    buf = hip.DeviceBuffer(64)
+    with pytest.raises(hip.NrsError):  # the seed would overwrite the logits
+        hip.call("nrs_linear_cross_entropy", buf, buf, buf, buf, None, buf, 4, 2, 3)
+    with pytest.raises(hip.NrsError):
+        hip.call("nrs_linear_backward_relu", buf, buf, None, buf, buf, buf, None, 4, 2, 3,
+                 0.0, 0.0, 0.0)
