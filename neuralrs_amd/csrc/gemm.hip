@@ -307,6 +307,12 @@ int make_args(GemmArgs& p, const GemmCall& c, const TileShape& s, const Plan& pl
 
 void launch_reduce(GemmArgs p, int slices) {
     const int64_t total = p.mrows * p.N;
+    if (p.N % 4 == 0 && p.nchw_P == 0 && p.ldc == p.N && aligned16(p.C) && aligned16(p.partial)) {
+        const unsigned blocks =
+            (unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(total / 4, 256), 8 * (int64_t)num_cus()));
+        hipLaunchKernelGGL(splitk_reduce4_kernel, dim3(blocks), dim3(256), 0, stream(), p, slices);
+        return;
+    }
     unsigned blocks = (unsigned)std::min<int64_t>(cdiv(total, 64), 4 * (int64_t)num_cus());
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(64 * kSplitGroups), 0, stream(), p,
                        slices);

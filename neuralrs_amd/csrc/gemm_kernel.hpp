@@ -857,4 +857,56 @@ __global__ __launch_bounds__(64 * kSplitGroups) void splitk_reduce_kernel(GemmAr
     }
 }
 
+// The same sum for row-major outputs of whole float4s (N % 4 == 0, C and the
+// partials 16-byte aligned): a thread owns four consecutive outputs and adds
+// the slices in slice order with 128-bit loads, eight (then four) slices'
+// loads in flight at a time; no LDS, no barrier. Row-major epilogue only.
+__global__ __launch_bounds__(256) void splitk_reduce4_kernel(GemmArgs p, int slices) {
+    const int64_t total = p.mrows * p.N, total4 = total >> 2;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total4;
+         i += (int64_t)gridDim.x * 256) {
+        const f32x4* src = reinterpret_cast<const f32x4*>(p.partial) + i;
+        const int64_t stride4 = total4;
+        f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        int s = 0;
+        for (; s + 8 <= slices; s += 8) {
+            f32x4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = src[(int64_t)(s + j) * stride4];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc = acc + v[j];
+        }
+        if (s + 4 <= slices) {
+            f32x4 v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = src[(int64_t)(s + j) * stride4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = acc + v[j];
+            s += 4;
+        }
+        for (; s < slices; ++s) acc = acc + src[(int64_t)s * stride4];
+        const int64_t e = i << 2, row = e / p.N, col = e - row * p.N;
+        if (row < p.M) {
+            if (p.epi & NRS_EPI_BIAS_COL)
+                acc = acc + f32x4{p.bias[col], p.bias[col + 1], p.bias[col + 2], p.bias[col + 3]};
+            if (p.epi & NRS_EPI_BIAS_ROW) acc = acc + p.bias[row];
+            if (p.epi & NRS_EPI_RELU) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[j] = fmaxf(acc[j], 0.0f);
+            }
+            f32x4* dst = reinterpret_cast<f32x4*>(p.C + row * p.ldc + col);
+            if (p.beta != 0.0f) acc = acc + p.beta * *dst;
+            *dst = acc;
+        } else {  // the row of sums
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float r = acc[j];
+                float* sr = p.sum_row + col + j;
+                if (p.sum_beta != 0.0f) r = r + p.sum_beta * *sr;
+                *sr = r;
+            }
+        }
+    }
+}
+
 }  // namespace nrs
