@@ -231,6 +231,8 @@ int check_call(const GemmCall& c, bool& empty) {
     const bool dense = c.amode == OP_DENSE && c.bmode == OP_DENSE;
     NRS_ARG_CHECK(dense || (c.gather_bytes > 0 && c.gather_bytes <= 0x80000000ll),
                   "gemm: gathered operand must be 1 B .. 2 GiB");
+    NRS_ARG_CHECK(!c.mask || (dense && batch == 1 && c.nchw_P == 0),
+                  "gemm: a mask needs a dense, unbatched, row-major GEMM");
     NRS_ARG_CHECK(!c.sum_row || (dense && batch == 1 && c.nchw_P == 0 && c.epi == NRS_EPI_NONE &&
                                  M < INT32_MAX),
                   "gemm: a row of sums needs a dense, unbatched GEMM without epilogue");
@@ -279,6 +281,7 @@ int make_args(GemmArgs& p, const GemmCall& c, const TileShape& s, const Plan& pl
     p.mrows = M + (c.sum_row ? 1 : 0);
     p.sum_row = c.sum_row;
     p.sum_beta = c.sum_beta;
+    p.mask = c.mask;
     p.tiles_m = (int)cdiv(p.mrows, s.bm);
     p.tiles_n = (int)cdiv(N, s.bn);
     p.group_m = 8;
@@ -388,7 +391,7 @@ bool outputs_independent(const GemmCall* calls, int count, const OperandRange* e
         const void* p;
         size_t bytes;
     };
-    auto ranges = [&](int idx, bool outputs_only, Range (&r)[6]) {
+    auto ranges = [&](int idx, bool outputs_only, Range (&r)[7]) {
         const GemmCall& c = calls[idx];
         int n = 0;
         r[n++] = {c.C, sizeof(float) * (size_t)(c.M * c.N)};
@@ -400,12 +403,13 @@ bool outputs_independent(const GemmCall* calls, int count, const OperandRange* e
             r[n++] = {c.bias, sizeof(float) * (size_t)std::max<int64_t>(
                                   (c.epi & NRS_EPI_BIAS_COL) ? c.N : 0,
                                   (c.epi & NRS_EPI_BIAS_ROW) ? c.M : 0)};
+        if (c.mask) r[n++] = {c.mask, sizeof(float) * (size_t)(c.M * c.N)};
         if (extra && extra[idx].p) r[n++] = {extra[idx].p, extra[idx].bytes};
         return n;
     };
     for (int i = 0; i < count; ++i) {
         if (calls[i].M == 0 || calls[i].N == 0) continue;
-        Range out[6], other[6];
+        Range out[7], other[7];
         const int no = ranges(i, true, out);
         for (int j = 0; j < count; ++j) {
             if (j == i || calls[j].M == 0 || calls[j].N == 0) continue;
@@ -611,35 +615,7 @@ int linear_backward(float* dx, float* dw, float* db, const float* grad, const fl
         cx.N = in_f;
         cx.K = out_f;
         cx.beta = beta_x;
-    }
-    if (mask && batch > 0 && in_f > 0) {
-        // dx masked in the product's epilogue when both products fit one
-        // short-GEMM launch; else dx goes through library scratch (slot 1)
-        // and nrs_relu_backward applies the mask
-        bool fits = true;
-        for (int i = 0; i < n; ++i) {
-            bool empty;
-            const int crc = check_call(calls[i], empty);
-            if (crc != NRS_OK) return crc;
-            fits = fits && !empty && wsplit_eligible(calls[i], true);
-        }
-        const OperandRange extra[2] = {{nullptr, 0},
-                                       {mask, sizeof(float) * (size_t)(batch * in_f)}};
-        if (fits && outputs_independent(calls, n, extra)) {
-            WsExtra ex[2];
-            ex[1].mask = mask;
-            const int rc = wsplit_run(calls, n, ex);
-            if (rc != NRS_OK || !db_after) return rc;
-            return nrs_sum_axis0(db_after, grad, batch, out_f, beta_b);
-        }
-        float* tmp = workspace(sizeof(float) * (size_t)(batch * in_f), 1);
-        if (!tmp) return NRS_ERR_ALLOC;
-        calls[1].C = tmp;
-        calls[1].beta = 0.0f;
-        int rc = gemm_group_run(calls, n);
-        if (rc == NRS_OK) rc = nrs_relu_backward(dx, tmp, mask, batch * in_f, beta_x);
-        if (rc != NRS_OK || !db_after) return rc;
-        return nrs_sum_axis0(db_after, grad, batch, out_f, beta_b);
+        cx.mask = mask;
     }
     const int rc = nrs::gemm_group_run(calls, n);
     if (rc != NRS_OK || !db_after) return rc;

@@ -57,6 +57,9 @@ struct GemmCall {
     // its weight gradient).
     float* sum_row = nullptr;
     float sum_beta = 0.0f;
+    // ReLU-backward mask (dense, unbatched, row-major C): output elements
+    // whose mask[row][col] is not > 0 are 0 before beta * old is added.
+    const float* mask = nullptr;
 };
 
 int gemm_run(const GemmCall& c);

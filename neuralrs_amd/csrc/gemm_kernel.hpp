@@ -59,6 +59,8 @@ struct GemmArgs {
     float* sum_row;
     float sum_beta;
     int64_t mrows;  // rows of the product: M, or M + 1 with a row of sums
+    // non-null: row-major [M][ldc]; v = 0 where mask <= 0 (before beta)
+    const float* mask;
 };
 
 
@@ -76,6 +78,7 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs& p, float* C, int6
         idx = ((int64_t)img * p.M + row) * p.nchw_P + pc;
     } else {
         idx = row * p.ldc + col;
+        if (p.mask && !(p.mask[idx] > 0.0f)) v = 0.0f;
     }
     if (p.beta != 0.0f) v = v + p.beta * C[idx];
     C[idx] = v;
@@ -536,7 +539,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, float* smem, int64_
     // ReLU, beta) and the bounds tests are uniform per workgroup and hoisted
     // out of the element loop.
     const bool full = (m0 + BM <= p.M) && (n0 + BN <= p.N);
-    const bool plain = p.partial != nullptr || (p.epi == NRS_EPI_NONE && p.beta == 0.0f);
+    const bool plain =
+        p.partial != nullptr || (p.epi == NRS_EPI_NONE && p.beta == 0.0f && p.mask == nullptr);
     float* out;
     int64_t stride;
     if (p.partial) {
@@ -641,6 +645,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, float* smem, int64_
         const bool bias_col = !p.partial && (p.epi & NRS_EPI_BIAS_COL);
         const bool bias_row = !p.partial && (p.epi & NRS_EPI_BIAS_ROW);
         const bool relu = !p.partial && (p.epi & NRS_EPI_RELU);
+        const float* mask = p.partial ? nullptr : p.mask;  // row-major C only
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const float bc = (bias_col && colok[j]) ? p.bias[n0 + wn0 + 32 * j + l32] : 0.0f;
@@ -652,7 +657,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, float* smem, int64_
                 // would be sunk there by the compiler and cost a round trip
                 // per element. Values of lanes that store nothing are unused.
                 float old[16], br[16];
-                if (beta != 0.0f || bias_row) {  // uniform
+                bool live[16];
+                if (beta != 0.0f || bias_row || mask) {  // uniform
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int64_t row = row0 + 32 * i + 8 * (r >> 2) + (r & 3);
@@ -662,6 +668,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, float* smem, int64_
                         else
                             old[r] = beta != 0.0f ? out[ok ? cbase[j] + row * stride : 0] : 0.0f;
                         br[r] = bias_row ? p.bias[ok ? row : 0] : 0.0f;
+                        live[r] = mask ? mask[ok ? cbase[j] + row * stride : 0] > 0.0f : true;
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
@@ -677,6 +684,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, float* smem, int64_
                     if (bias_col) v += bc;
                     if (bias_row) v += br[r];
                     if (relu) v = fmaxf(v, 0.0f);
+                    if (mask && !live[r]) v = 0.0f;
                     if (beta != 0.0f) v = v + beta * old[r];
                     old[r] = v;
                     asm volatile("" : "+v"(old[r]));
@@ -893,6 +901,11 @@ __global__ __launch_bounds__(256) void splitk_reduce4_kernel(GemmArgs p, int sli
             if (p.epi & NRS_EPI_RELU) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[j] = fmaxf(acc[j], 0.0f);
+            }
+            if (p.mask) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (!(p.mask[row * p.ldc + col + j] > 0.0f)) acc[j] = 0.0f;
             }
             f32x4* dst = reinterpret_cast<f32x4*>(p.C + row * p.ldc + col);
             if (p.beta != 0.0f) acc = acc + p.beta * *dst;

@@ -266,8 +266,8 @@ int wsplit_run(const GemmCall* calls, int count, const WsExtra* extra) {
                                       : (b_vec ? WS_NT_AS_BV : WS_NT_AS_BS);
         p.beta = c.beta;
         p.epi = c.epi;
-        if (extra && extra[i].mask) {
-            p.mask = extra[i].mask;
+        if (c.mask) {
+            p.mask = c.mask;
             p.epi |= kWsMask;
         }
         if (extra && extra[i].ce_grad) {

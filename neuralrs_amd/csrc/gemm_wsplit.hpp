@@ -31,10 +31,9 @@ struct WsArgs {
     int count;
 };
 
-// Epilogue operands beyond GemmCall's: a ReLU mask for the product, or the
-// cross-entropy seed's output and target (N <= 16, no beta, no row of sums).
+// Epilogue operands beyond GemmCall's: the cross-entropy seed's output and
+// target (N <= 16, no beta, no row of sums).
 struct WsExtra {
-    const float* mask = nullptr;
     float* ce_grad = nullptr;
     const float* ce_target = nullptr;
 };

@@ -568,15 +568,22 @@ NodeRef conv2d(const NodeRef& input, const NodeRef& weight, const NodeRef& bias,
 namespace {
 
 // The backward of a Linear node (its matmul closure and the bias's
-// sum_axis0, linear.rs:22-25) given the gradient g of its output.
+// sum_axis0, linear.rs:22-25) given the gradient g of its output. With
+// `mask` (the input x is a ReLU output whose gradient only ever receives
+// masked contributions, see linear_node), the input gradient is masked by
+// x > 0 in the same launch: relu_grad (relu.rs:30-45) of the ReLU's output
+// gradient, i.e. the gradient of the ReLU's input.
 void linear_backward_into(const NodeRef& x, const NodeRef& w, const NodeRef& b, const float* g,
-                          size_t batch, size_t in_f, size_t out_f) {
+                          size_t batch, size_t in_f, size_t out_f, const float* mask = nullptr) {
     GpuBuffers& xg = gpu_of(x, "cuda matmul bwd: lhs not on GPU");
     GpuBuffers& wg = gpu_of(w, "cuda matmul bwd: rhs not on GPU");
     GpuBuffers& bg = gpu_of(b, "backward: parent not on GPU");
     if (xg.grad == wg.grad || xg.grad == bg.grad || wg.grad == bg.grad) {
         // parents sharing a gradient: the products one after the other
         matmul_backward_into(x, w, g, batch, in_f, out_f, "cuda linear bwd: launch");
+        if (mask)  // every contribution to x's gradient is masked: mask the sum
+            check(nrs_relu_backward(xg.grad->ptr(), xg.grad->ptr(), mask, batch * in_f, 0.0f),
+                  "cuda relu bwd: launch");
         float beta = 1.0f;
         float* db = bg.grad->acc_target(beta);
         check(nrs_sum_axis0(db, g, batch, out_f, beta), "cuda linear bwd: bias launch");
@@ -588,13 +595,27 @@ void linear_backward_into(const NodeRef& x, const NodeRef& w, const NodeRef& b, 
     float* dx = xg.grad->acc_target(bx);
     float* dw = wg.grad->acc_target(bw);
     float* db = bg.grad->acc_target(bb);
-    check(nrs_linear_backward(dx, dw, db, g, xg.data.ptr(), wg.data.ptr(), batch, in_f, out_f, bx,
-                              bw, bb),
+    check(mask ? nrs_linear_backward_relu(dx, dw, db, g, xg.data.ptr(), wg.data.ptr(), mask, batch,
+                                          in_f, out_f, bx, bw, bb)
+               : nrs_linear_backward(dx, dw, db, g, xg.data.ptr(), wg.data.ptr(), batch, in_f,
+                                     out_f, bx, bw, bb),
           "cuda linear bwd: launch");
 }
 
-// x . W + bias, optionally followed by ReLU in the same GEMM epilogue.
-NodeRef linear_node(const Linear& l, const NodeRef& input, bool relu) {
+// How a Linear node meets a ReLU:
+//   kPlain      x . W + bias;
+//   kReluOut    relu(x . W + bias), ReLU in the GEMM epilogue; the node's
+//               backward masks its output gradient by the output (> 0
+//               exactly where the pre-activation is);
+//   kReluOutPre the same node whose only consumer is a kReluIn Linear: the
+//               gradient arrives masked, so the backward uses it as is;
+//   kReluIn     x . W + bias whose input x is a kReluOutPre node: its
+//               backward writes x's gradient masked by x > 0 in the
+//               input-gradient product's epilogue (nrs_linear_backward_relu).
+enum class ReluLink { kPlain, kReluOut, kReluOutPre, kReluIn };
+
+NodeRef linear_node(const Linear& l, const NodeRef& input, ReluLink link) {
+    const bool relu = link == ReluLink::kReluOut || link == ReluLink::kReluOutPre;
     GpuBuffers& xg = gpu_of(input, "cuda matmul: lhs not on GPU");
     GpuBuffers& wg = gpu_of(l.weights, "cuda matmul: rhs not on GPU");
     GpuBuffers& bg = gpu_of(l.bias, "cuda add: rhs not on GPU");
@@ -611,6 +632,14 @@ NodeRef linear_node(const Linear& l, const NodeRef& input, bool relu) {
     NodeRef x = input, w = l.weights, b = l.bias;
     NodeRef node = make_output({batch, out_f}, {x, w, b}, std::move(out));
     if (!relu) {
+        const float* mask = link == ReluLink::kReluIn ? xg.data.ptr() : nullptr;
+        node->backward_fn = [grad = node->gpu->grad, x, w, b, batch, in_f, out_f,
+                             mask](const std::vector<float>&) {
+            linear_backward_into(x, w, b, grad->ptr(), batch, in_f, out_f, mask);
+        };
+        return node;
+    }
+    if (link == ReluLink::kReluOutPre) {
         node->backward_fn = [grad = node->gpu->grad, x, w, b, batch, in_f,
                              out_f](const std::vector<float>&) {
             linear_backward_into(x, w, b, grad->ptr(), batch, in_f, out_f);
@@ -632,7 +661,9 @@ NodeRef linear_node(const Linear& l, const NodeRef& input, bool relu) {
 
 }  // namespace
 
-NodeRef Linear::forward(const NodeRef& input) const { return linear_node(*this, input, false); }
+NodeRef Linear::forward(const NodeRef& input) const {
+    return linear_node(*this, input, ReluLink::kPlain);
+}
 
 namespace {
 
@@ -933,8 +964,10 @@ NodeRef TransformerBlock::forward(const NodeRef& x) const {
     // are internal to the block, so no node a caller can reach is lost.
     NodeRef attn_out = multihead(mha, reshape_view(x, {batch * seq, d}), batch, seq, d);
     NodeRef x1 = add_layernorm(x, attn_out, norm1);
-    NodeRef h = linear_node(ff1, reshape_view(x1, {batch * seq, d}), true);
-    NodeRef ff_out = ff2.forward(h);
+    // h is internal and ff2 its only consumer: ff2's backward writes h's
+    // gradient already masked by the ReLU, and h's backward uses it as is
+    NodeRef h = linear_node(ff1, reshape_view(x1, {batch * seq, d}), ReluLink::kReluOutPre);
+    NodeRef ff_out = linear_node(ff2, h, ReluLink::kReluIn);
     return add_layernorm(x1, ff_out, norm2);
 }
 

@@ -533,7 +533,8 @@ def test_short_gemm_epilogues(hip, shape):
 
 
 @pytest.mark.parametrize("batch,in_f,out_f", [(256, 128, 10), (256, 784, 128), (37, 30, 9),
-                                              (3, 5, 2), (4096, 256, 256), (300, 1000, 64)],
+                                              (3, 5, 2), (4096, 256, 256), (300, 1000, 64),
+                                              (4096, 1024, 256), (64, 64, 4096)],
                          ids=lambda v: str(v))
 @pytest.mark.parametrize("beta", [0.0, 1.0])
 def test_linear_backward_relu_exact_integers(hip, orc, batch, in_f, out_f, beta):
@@ -541,8 +542,9 @@ def test_linear_backward_relu_exact_integers(hip, orc, batch, in_f, out_f, beta)
     dx = (g . W^T) * (mask > 0) + beta dx, the Linear's input gradient passed
     through the preceding ReLU's backward (the oracle's relu_backward,
     src/autograd/graph/relu.rs), exact on small integers; the masked product
-    rides the short-GEMM epilogue, or (4096 x 256 x 256) the tiled products
-    followed by one ReLU-backward pass."""
+    rides the short-GEMM epilogue or the tiled kernels' epilogue (grouped
+    launches; 64 x 64 over K = 4096: a split input gradient whose reduce
+    applies the mask)."""
     rng = np.random.default_rng(batch + 7 * in_f + out_f)
     g, x = int_matrix(rng, (batch, out_f), -3, 3), int_matrix(rng, (batch, in_f), -3, 3)
     w = int_matrix(rng, (in_f, out_f), -3, 3)
