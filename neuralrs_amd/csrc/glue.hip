@@ -380,6 +380,100 @@ __global__ __launch_bounds__(256) void layernorm_param_partial_kernel(
     part_b[(int64_t)blockIdx.y * F + f] = db;
 }
 
+// Input gradient (when dinput is set) and parameter partials (when part_g
+// is set) in one pass, F <= 64 * PER; every LayerNorm backward of such a
+// width runs this kernel, so each gradient has the same bits whichever
+// others a call asks for: block c
+// owns rows [c*rc, (c+1)*rc); wave w takes row pairs r0 + 2w + 8k, +1 (both
+// rows' loads issued before either is used), writes each row's input
+// gradient exactly as layernorm_dx_kernel does, and sums grad * x_norm and
+// grad over its rows in row order; the four waves' sums are added in wave
+// order into partial[c] for layernorm_param_combine_kernel. grad and x_norm
+// are read once for both gradients.
+template <int PER>
+__global__ __launch_bounds__(256) void layernorm_bwd_fused_kernel(
+    float* __restrict__ dinput, float* __restrict__ dinput2, float* __restrict__ part_g,
+    float* __restrict__ part_b, const float* __restrict__ grad, const float* __restrict__ gamma,
+    const float* __restrict__ x_norm, const float* __restrict__ inv_std, int64_t rows, int64_t F,
+    int64_t rc, float acc, float acc2) {
+    __shared__ float red[2][4][64 * PER];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t r0 = (int64_t)blockIdx.x * rc, r1 = min(rows, r0 + rc);
+    const float nf = (float)F;
+    float gm[PER], pg[PER], pb[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int f = lane + 64 * i;
+        // gamma is only needed (and may be null) without an input gradient
+        gm[i] = (dinput != nullptr && f < F) ? gamma[f] : 0.0f;
+        pg[i] = 0.0f;
+        pb[i] = 0.0f;
+    }
+    for (int64_t rb = r0 + 2 * w; rb < r1; rb += 8) {
+        const bool two = rb + 1 < r1;  // wave-uniform
+        float g[2][PER], xn[2][PER];
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = lane + 64 * i;
+                const bool ok = f < F && (q == 0 || two);
+                const int64_t at = ok ? (rb + q) * F + f : 0;
+                g[q][i] = ok ? grad[at] : 0.0f;
+                xn[q][i] = ok ? x_norm[at] : 0.0f;
+            }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            if (q == 1 && !two) break;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                pg[i] += g[q][i] * xn[q][i];
+                pb[i] += g[q][i];
+            }
+            if (!dinput) continue;  // parameter gradients only
+            const int64_t r = rb + q;
+            float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const float d = g[q][i] * gm[i];
+                s1 += d;
+                s2 += d * xn[q][i];
+            }
+            s1 = wave_sum(s1) / nf;
+            s2 = wave_sum(s2) / nf;
+            const float istd = inv_std[r];
+            float* o = dinput + r * F;
+            float* o2 = dinput2 ? dinput2 + r * F : nullptr;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = lane + 64 * i;
+                if (f < F) {
+                    const float dx = istd * (g[q][i] * gm[i] - s1 - xn[q][i] * s2);
+                    o[f] = acc != 0.0f ? dx + acc * o[f] : dx;
+                    if (o2) o2[f] = acc2 != 0.0f ? dx + acc2 * o2[f] : dx;
+                }
+            }
+        }
+    }
+    if (!part_g) return;  // input gradient only (uniform)
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        red[0][w][lane + 64 * i] = pg[i];
+        red[1][w][lane + 64 * i] = pb[i];
+    }
+    __syncthreads();
+    for (int f = threadIdx.x; f < F; f += 256) {
+        float sg = red[0][0][f], sb = red[1][0][f];
+#pragma unroll
+        for (int y = 1; y < 4; ++y) {
+            sg += red[0][y][f];
+            sb += red[1][y][f];
+        }
+        part_g[(int64_t)blockIdx.x * F + f] = sg;
+        part_b[(int64_t)blockIdx.x * F + f] = sb;
+    }
+}
+
 __global__ __launch_bounds__(64 * kLnGroups) void layernorm_param_combine_kernel(
     float* __restrict__ dgamma, float* __restrict__ dbeta, const float* __restrict__ part_g,
     const float* __restrict__ part_b, int64_t chunks, int64_t F, float acc) {
@@ -705,6 +799,34 @@ int nrs_add_layernorm_backward(float* da, float* db, float* dgamma, float* dbeta
         return NRS_OK;
     }
     NRS_ARG_CHECK(grad && x_norm, "layernorm backward: null pointer");
+    if ((dinput || dgamma || dbeta) && F <= 512) {
+        // the input gradient and the parameter partials from one pass over
+        // grad and x_norm, then the chunk partials combined
+        NRS_ARG_CHECK(!dinput || (gamma && inv_std), "layernorm backward: null gamma or inv_std");
+        int64_t rc = 8;
+        if ((rows + rc - 1) / rc > INT32_MAX / 2) rc = ((rows + INT32_MAX / 2 - 1) / (INT32_MAX / 2) + 7) / 8 * 8;
+        const int64_t chunks = (rows + rc - 1) / rc;
+        const bool params = dgamma || dbeta;
+        float* part = nullptr;
+        if (params) {
+            part = nrs::workspace(sizeof(float) * 2 * (size_t)(chunks * F), 0);
+            if (!part) return NRS_ERR_ALLOC;
+        }
+        auto fn = F <= 64    ? nrs::layernorm_bwd_fused_kernel<1>
+                  : F <= 128 ? nrs::layernorm_bwd_fused_kernel<2>
+                  : F <= 256 ? nrs::layernorm_bwd_fused_kernel<4>
+                             : nrs::layernorm_bwd_fused_kernel<8>;
+        hipLaunchKernelGGL(fn, dim3((unsigned)chunks), dim3(256), 0, nrs::stream(), dinput, db,
+                           part, params ? part + chunks * F : nullptr, grad, gamma, x_norm,
+                           inv_std, rows, F, rc, beta_a, beta_b);
+        NRS_LAUNCH_CHECK("layernorm backward (input and parameter partials)");
+        if (!params) return NRS_OK;
+        hipLaunchKernelGGL(nrs::layernorm_param_combine_kernel, dim3((unsigned)((F + 63) / 64)),
+                           dim3(64 * nrs::kLnGroups), 0, nrs::stream(), dgamma, dbeta, part,
+                           part + chunks * F, chunks, F, acc);
+        NRS_LAUNCH_CHECK("layernorm backward (parameters)");
+        return NRS_OK;
+    }
     if (dinput) {
         NRS_ARG_CHECK(gamma && inv_std, "layernorm backward: null gamma or inv_std");
         hipLaunchKernelGGL(nrs::layernorm_dx_kernel, dim3(nrs::rows_grid(rows)), dim3(256), 0,
