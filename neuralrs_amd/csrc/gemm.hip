@@ -4,6 +4,7 @@
 #include <algorithm>
 
 #include "gemm_kernel.hpp"
+#include "gemm_skinny.hpp"
 #include "gemm_wsplit.hpp"
 
 namespace nrs {
@@ -308,6 +309,14 @@ int make_args(GemmArgs& p, const GemmCall& c, const TileShape& s, const Plan& pl
     return NRS_OK;
 }
 
+void launch_reduce(GemmArgs p, int slices);
+
+}  // namespace
+
+void launch_splitk_reduce(GemmArgs p, int slices) { launch_reduce(p, slices); }
+
+namespace {
+
 void launch_reduce(GemmArgs p, int slices) {
     const int64_t total = p.mrows * p.N;
     if (p.N % 4 == 0 && p.nchw_P == 0 && p.ldc == p.N && aligned16(p.C) && aligned16(p.partial)) {
@@ -332,6 +341,8 @@ int gemm_run(const GemmCall& c) {
     // few output tiles over a reduction of at most a few rounds: one launch
     // of the short-GEMM kernel, no split-K partials or reduce launch
     if (wsplit_eligible(c, true)) return wsplit_run(&c, 1, nullptr);
+    // at most 32 rows over a long B: B streamed into registers
+    if (skinny_eligible(c)) return skinny_run(c);
     const bool dense = c.amode == OP_DENSE && c.bmode == OP_DENSE;
     const bool vec4 = vec4_loads(c);
 

@@ -616,3 +616,26 @@ def test_linear_cross_entropy_errors(hip):
     with pytest.raises(hip.NrsError):
         hip.call("nrs_linear_backward_relu", buf, buf, None, buf, buf, buf, None, 4, 2, 3,
                  0.0, 0.0, 0.0)
+
+
+@pytest.mark.parametrize("layout", [NN, TN])
+@pytest.mark.parametrize("shape", [(32, 8192, 2048), (17, 1024, 300), (1, 4096, 1000),
+                                   (30, 8200, 1024), (32, 1152, 8200)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_skinny_gemm_exact_integers(hip, layout, shape):
+    """At most 32 rows over B [K][N] streamed into registers (one K slice per
+    strip or split-K partials and the reduce): exact on small integers, with
+    beta = 1 and with a column bias + ReLU epilogue; ragged N (8200 = 64
+    strips + 8 columns), K not a multiple of the 8-k group (300, 1000, 8200)."""
+    rows, cols, inner = shape
+    if layout == NN and inner % 4:
+        pytest.skip("NN takes 128-bit A rows: K % 4 == 0")
+    rng = np.random.default_rng(rows * 3 + cols + inner + layout)
+    a, b = operands(layout, rows, cols, inner, lambda s: int_matrix(rng, s, -2, 2))
+    A, B = logical(layout, a, b)
+    prod = (A @ B).astype(np.float32)
+    c0 = int_matrix(rng, (rows, cols), -3, 3)
+    assert np.array_equal(run_gemm(hip, layout, a, b, rows, cols, inner, 1.0, c0), c0 + prod)
+    bc = int_matrix(rng, (cols,), -3, 3)
+    assert np.array_equal(run_gemm(hip, layout, a, b, rows, cols, inner, 0.0, None, bc, 1 | 4),
+                          np.maximum(prod + bc[None, :], 0))
