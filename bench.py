@@ -202,7 +202,7 @@ def bench_conv_cfg3(hip, steps, warmup, closures_only=False):
             "conv1_input_grad_us": dx1_ms * 1e3, "conv1_input_grad_roof_us": roof_dx1}
 
 
-def bench_mlp_cfg2(hip, steps, warmup):
+def bench_mlp_cfg2(hip, steps, warmup, closures_only=False):
     """cfg2 training step: x[256,784] -> Linear(784,128) -> ReLU ->
     Linear(128,10) -> cross-entropy seed (softmax - onehot)/256 (the fused
     ce_backward of src/cuda/loss/cross_entropy.rs:39-58) -> backward (dW, db
@@ -234,6 +234,8 @@ def bench_mlp_cfg2(hip, steps, warmup):
         hip.call("nrs_linear_backward_relu", gh, gw2, gb2, gz, a, w2, a, B, Hd, O, 0.0, 1.0, 1.0)
         hip.call("nrs_linear_backward", gx, gw1, gb1, gh, x, w1, B, I, Hd, 0.0, 1.0, 1.0)
 
+    if closures_only:
+        return {"mlp_step_cfg2": step}
     us = event_ms(hip, step, steps, warmup) * 1e3
     return {"us_per_step": us, "gemm_roof_us": mlp_gemm_roof_us()}
 
@@ -633,6 +635,7 @@ def counters_pass(hip):
         legs.append((name, fn))
     legs += list(bench_conv_cfg3(hip, 0, 0, closures_only=True).items())
     legs += list(bench_attention_cfg4(hip, 0, 0, closures_only=True).items())
+    legs += list(bench_mlp_cfg2(hip, 0, 0, closures_only=True).items())
     hip.call("nrs_memcpy_dtod", dst.ptr, src.ptr, COPY_BYTES)
     hip.sync()
     for _, fn in legs:
