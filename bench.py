@@ -140,11 +140,25 @@ def bench_conv_cfg3(hip, steps, warmup, closures_only=False):
     gw1, gw2 = hip.DeviceBuffer.zeros(w1.size), hip.DeviceBuffer.zeros(w2.size)
     gb1, gb2 = hip.DeviceBuffer.zeros(32), hip.DeviceBuffer.zeros(64)
 
+    # conv1 -> maxpool as one node each way: conv1's output only feeds the
+    # pooling, so the fused forward never writes it and the fused backward
+    # expands the pooled gradient while loading (nrs_conv2d_maxpool_forward /
+    # nrs_maxpool_conv2d_backward); the unfused sequence is step_unfused
     def step():
+        hip.call("nrs_conv2d_maxpool_forward", p1.ptr, am.ptr, None, dx.ptr, dw1.ptr, db1.ptr,
+                 N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2)
+        hip.call("nrs_conv2d_forward", y2.ptr, p1.ptr, dw2.ptr, db2.ptr, N, 32, 14, 14, 64, 3, 3, 1, 1)
+        # backward (zero_grad of the pooled activation's grad, then accumulate)
+        hip.call("nrs_memset_zero", gp1.ptr, gp1.nbytes)
+        hip.call("nrs_conv2d_backward", gp1.ptr, gw2.ptr, gb2.ptr, dg2.ptr, p1.ptr, dw2.ptr,
+                 N, 32, 14, 14, 64, 3, 3, 1, 1)
+        hip.call("nrs_maxpool_conv2d_backward", None, gw1.ptr, gb1.ptr, gp1.ptr, am.ptr, dx.ptr,
+                 dw1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2)
+
+    def step_unfused():
         hip.call("nrs_conv2d_forward", y1.ptr, dx.ptr, dw1.ptr, db1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1)
         hip.call("nrs_maxpool_forward", p1.ptr, am.ptr, y1.ptr, N, 32, 28, 28, 2, 2)
         hip.call("nrs_conv2d_forward", y2.ptr, p1.ptr, dw2.ptr, db2.ptr, N, 32, 14, 14, 64, 3, 3, 1, 1)
-        # backward (zero_grad of the activation grads, then accumulate)
         hip.call("nrs_memset_zero", gp1.ptr, gp1.nbytes)
         hip.call("nrs_memset_zero", gy1.ptr, gy1.nbytes)
         hip.call("nrs_conv2d_backward", gp1.ptr, gw2.ptr, gb2.ptr, dg2.ptr, p1.ptr, dw2.ptr,
@@ -167,17 +181,31 @@ def bench_conv_cfg3(hip, steps, warmup, closures_only=False):
         hip.call("nrs_conv2d_backward", gx.ptr, None, None, gy1.ptr, dx.ptr, dw1.ptr,
                  N, 1, 28, 28, 32, 3, 3, 1, 1)
 
+    def conv1_pool_fwd():
+        hip.call("nrs_conv2d_maxpool_forward", p1.ptr, am.ptr, None, dx.ptr, dw1.ptr, db1.ptr,
+                 N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2)
+
+    def conv1_pool_bwd():
+        hip.call("nrs_maxpool_conv2d_backward", None, gw1.ptr, gb1.ptr, gp1.ptr, am.ptr, dx.ptr,
+                 dw1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2)
+
     if closures_only:
         return {"conv_fwd_cfg3": conv_fwd, "conv_bwd_cfg3": conv_bwd,
-                "conv1_input_grad_cfg3": conv1_input_grad}
-    for _ in range(warmup):
-        step()
-    hip.sync()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    hip.sync()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
+                "conv1_input_grad_cfg3": conv1_input_grad,
+                "conv1_maxpool_fwd_cfg3": conv1_pool_fwd, "maxpool_conv1_bwd_cfg3": conv1_pool_bwd}
+
+    def wall_ms(fn):
+        for _ in range(warmup):
+            fn()
+        hip.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        hip.sync()
+        return (time.perf_counter() - t0) * 1e3 / steps
+
+    ms_unfused = wall_ms(step_unfused)
+    ms = wall_ms(step)
     fwd_ms = event_ms(hip, conv_fwd, steps, 3)
     bwd_ms = event_ms(hip, conv_bwd, steps, 3)
     dx1_ms = event_ms(hip, conv1_input_grad, steps, 3)
@@ -196,7 +224,9 @@ def bench_conv_cfg3(hip, steps, warmup, closures_only=False):
         else:
             roof_b += dx_roof
         roof_b += roofline_us(fl, y_b + x_b + w_b + 4 * co)
-    return {"ms_per_step": ms, "imgs_per_s": N / (ms / 1e3),
+    return {"ms_per_step": ms, "imgs_per_s": N / (ms / 1e3), "ms_per_step_unfused": ms_unfused,
+            "conv1_pool_fwd_us": event_ms(hip, conv1_pool_fwd, steps, 3) * 1e3,
+            "pool_conv1_bwd_us": event_ms(hip, conv1_pool_bwd, steps, 3) * 1e3,
             "fwd_us": fwd_ms * 1e3, "bwd_us": bwd_ms * 1e3,
             "fwd_roof_us": roof_f, "bwd_roof_us": roof_b,
             "conv1_input_grad_us": dx1_ms * 1e3, "conv1_input_grad_roof_us": roof_dx1}
@@ -725,9 +755,15 @@ def main():
         out["conv2d_fwd_bwd"] = {
             "value": round(c["imgs_per_s"], 1), "unit": "imgs/s",
             "ms_per_step": round(c["ms_per_step"], 4),
+            "ms_per_step_unfused": round(c["ms_per_step_unfused"], 4),
             "config": "cfg3 batch 128 conv1 1->32, maxpool, conv2 32->64, fwd+bwd: weight and "
                       "bias grads of both layers, input grad of conv2 (the image batch requires "
-                      "no grad, as in examples/mnist_cuda_cnn.rs:261)",
+                      "no grad, as in examples/mnist_cuda_cnn.rs:261); conv1 and the maxpool "
+                      "as one node each way (nrs_conv2d_maxpool_forward / "
+                      "nrs_maxpool_conv2d_backward), the two ops separately in "
+                      "ms_per_step_unfused",
+            "conv1_maxpool_fwd_us": round(c["conv1_pool_fwd_us"], 2),
+            "maxpool_conv1_bwd_us": round(c["pool_conv1_bwd_us"], 2),
             "conv_fwd_us": round(c["fwd_us"], 2), "conv_bwd_us": round(c["bwd_us"], 2),
             "fwd_roofline_us": round(c["fwd_roof_us"], 2),
             "bwd_roofline_us": round(c["bwd_roof_us"], 2),

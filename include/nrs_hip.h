@@ -277,6 +277,35 @@ int nrs_conv2d_backward(float *dinput, float *dweight, float *dbias,
                         int64_t c_out, int64_t kh, int64_t kw, int64_t stride,
                         int64_t pad);
 
+/* nn::conv2d followed by max pooling (src/cuda/nn/conv.rs:244-277, then
+ * src/cuda/nn/maxpool.rs:18-46 on the conv output) in one call: pooled
+ * [N, c_out, oh/k', ow/k'] and argmax as nrs_maxpool_forward gives them for
+ * the conv output (flat indices into [N, c_out, oh, ow], first maximum wins).
+ * out receives the conv output when non-NULL; a CNN whose conv output only
+ * feeds the pooling passes NULL and the conv output is never written. One
+ * launch for "same" 3x3 stride-1 layers with c_in <= 3, width % 4 == 0, even
+ * height and 2x2 stride-2 pooling (the conv values have the bits of
+ * nrs_conv2d_forward's); any other shape runs the two ops (the conv output
+ * in library scratch when out is NULL).                                     */
+int nrs_conv2d_maxpool_forward(float *pooled, int32_t *argmax, float *out, const float *input,
+                               const float *weight, const float *bias, int64_t N, int64_t c_in,
+                               int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
+                               int64_t stride, int64_t pad, int64_t pool_k, int64_t pool_stride);
+/* The backward closures of that pair: nrs_conv2d_backward (accumulating
+ * dinput, dweight, dbias; any may be NULL) with the conv output's gradient
+ * taken as maxpool_backward of grad_pooled into zeros
+ * (src/cuda/nn/maxpool.rs:48-66), which is never written when dinput is NULL
+ * and the layer has few taps (<= 32 per output channel, 2x2 stride-2
+ * pooling, width % 4 == 0): the weight and bias gradients then read the
+ * pooled gradient and argmax and expand them while loading, one launch plus
+ * the slice sum. Otherwise the unpooled gradient goes through library
+ * scratch and the two backward calls.                                       */
+int nrs_maxpool_conv2d_backward(float *dinput, float *dweight, float *dbias,
+                                const float *grad_pooled, const int32_t *argmax,
+                                const float *input, const float *weight, int64_t N, int64_t c_in,
+                                int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
+                                int64_t stride, int64_t pad, int64_t pool_k, int64_t pool_stride);
+
 /* ------------------------------------------------------ gradient plumbing */
 /* accumulate (src/cuda/runtime.rs:13-19): acc[i] += src[i].                  */
 int nrs_accumulate(float *acc, const float *src, int64_t n);

@@ -280,6 +280,108 @@ __global__ __launch_bounds__(256) void conv_fwd_quad_kernel(
     }
 }
 
+// Forward of a "same" 3x3 layer followed by 2x2 max pooling of stride 2: the
+// conv2d then MaxPool2d of a CNN (src/cuda/nn/conv.rs:244-277,
+// src/cuda/nn/maxpool.rs:18-46) in one pass. A thread owns a 4-wide, 2-tall
+// block of the conv output, i.e. two pooled outputs, for 8 output channels;
+// its input is 4 rows of 6 floats per input channel. Each conv value is
+// computed as conv_fwd_quad_kernel computes it (same products in the same
+// order, then + bias); each 2x2 window keeps the first maximum in scan order
+// and records the conv output's flat element index, as maxpool_forward does.
+// The conv output is written only when out is set; the pooled values and
+// indices leave as 64-bit stores.
+template <int CIN>
+__global__ __launch_bounds__(256) void conv_fwd_pool_quad_kernel(
+    float* __restrict__ pooled, int32_t* __restrict__ argmax, float* __restrict__ out,
+    const float* __restrict__ input, const float* __restrict__ weight,
+    const float* __restrict__ bias, int N, int H, int W, int c_out, FastDiv div_bimg,
+    FastDiv div_brow) {
+    constexpr int ROWS = 4 * CIN, TAPS = 9 * CIN;
+    __shared__ __attribute__((aligned(16))) float wsh[kQuadOc][TAPS];
+    __shared__ float bsh[kQuadOc];
+    const int tid = threadIdx.x;
+    const int P = H * W, PW = W >> 1, PP = (H >> 1) * PW, oc0 = blockIdx.y * kQuadOc;
+    const int64_t blocks = (int64_t)N * (H >> 1) * (W >> 2);
+    const int g = blockIdx.x * 256 + tid;
+    const bool valid = g < blocks;
+    uint32_t n, qq, py, qx;
+    fast_divmod((uint32_t)(valid ? g : 0), div_bimg, n, qq);
+    fast_divmod(qq, div_brow, py, qx);
+    const int oy = 2 * (int)py, ox = 4 * (int)qx;
+    // input row segments: columns ox-1 .. ox+4 of rows oy-1 .. oy+2
+    const auto rx = buffer_rsrc(input, (int64_t)N * CIN * P * 4);
+    float seg[ROWS][6];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        const int ic = r / 4, iy = oy + r % 4 - 1;
+        const bool rok = valid & ((unsigned)iy < (unsigned)H);
+        const int base = (((int)n * CIN + ic) * H + iy) * W + ox;
+        const f32x4 mid = buffer_load4(rx, rok ? base * 4 : kOutOfRange);
+        seg[r][0] = buffer_load1(rx, (rok & (ox > 0)) ? (base - 1) * 4 : kOutOfRange);
+        seg[r][5] = buffer_load1(rx, (rok & (ox + 4 < W)) ? (base + 4) * 4 : kOutOfRange);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) seg[r][1 + u] = mid[u];
+    }
+    constexpr int WN = kQuadOc * TAPS, WPT = (WN + 255) / 256;
+    const auto rw = buffer_rsrc(weight, (int64_t)c_out * TAPS * 4);
+    const auto rb = buffer_rsrc(bias ? bias : weight, bias ? (int64_t)c_out * 4 : 0);
+    float wv[WPT];
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+        const int e = tid + 256 * k;
+        wv[k] = buffer_load1(rw, e < WN ? (oc0 * TAPS + e) * 4 : kOutOfRange);
+    }
+    const float bv = buffer_load1(rb, tid < kQuadOc ? (oc0 + tid) * 4 : kOutOfRange);
+#pragma unroll
+    for (int k = 0; k < WPT; ++k)
+        if (tid + 256 * k < WN) (&wsh[0][0])[tid + 256 * k] = wv[k];
+    if (tid < kQuadOc) bsh[tid] = bv;
+    __syncthreads();
+    if (!valid) return;
+    const int noc = min(kQuadOc, c_out - oc0);
+#pragma unroll
+    for (int oc = 0; oc < kQuadOc; ++oc) {
+        if (oc >= noc) break;
+        f32x4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ic = 0; ic < CIN; ++ic)
+#pragma unroll
+            for (int i = 0; i < 3; ++i)
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    const float w = wsh[oc][(ic * 3 + i) * 3 + j];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        a0[u] += w * seg[ic * 4 + i][u + j];
+                        a1[u] += w * seg[ic * 4 + i + 1][u + j];
+                    }
+                }
+        const float b = bsh[oc];
+        const f32x4 v0 = a0 + b, v1 = a1 + b;
+        const int plane = ((int)n * c_out + oc0 + oc) * P;
+        const int e00 = plane + oy * W + ox;  // flat index of (oy, ox)
+        f32x2 pv;
+        int32_t pi[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {  // windows of columns 2h, 2h + 1
+            float best = v0[2 * h];
+            int bi = e00 + 2 * h;
+            if (v0[2 * h + 1] > best) { best = v0[2 * h + 1]; bi = e00 + 2 * h + 1; }
+            if (v1[2 * h] > best) { best = v1[2 * h]; bi = e00 + W + 2 * h; }
+            if (v1[2 * h + 1] > best) { best = v1[2 * h + 1]; bi = e00 + W + 2 * h + 1; }
+            pv[h] = best;
+            pi[h] = bi;
+        }
+        const int64_t po = ((int64_t)n * c_out + oc0 + oc) * PP + (int)py * PW + 2 * (int)qx;
+        *reinterpret_cast<f32x2*>(pooled + po) = pv;
+        *reinterpret_cast<int2*>(argmax + po) = make_int2(pi[0], pi[1]);
+        if (out) {
+            __builtin_nontemporal_store(v0, reinterpret_cast<f32x4*>(out + e00));
+            __builtin_nontemporal_store(v1, reinterpret_cast<f32x4*>(out + e00 + W));
+        }
+    }
+}
+
 // Direct input gradient for c_in <= kDirectCin (any stride): one thread per
 // input pixel accumulates, for its c_in channels, every (oc, i, j) whose
 // window covers it, with weights (c_out*c_in*kh*kw <= kDirectWeights) from
@@ -1206,6 +1308,104 @@ int nrs_conv2d_bias_grad(float* dbias, const float* grad, int64_t N, int64_t c_o
     NRS_REQUIRE_INIT();
     NRS_ARG_CHECK(N >= 0 && c_out >= 0 && out_h >= 0 && out_w >= 0, "bias_grad: negative size");
     return nrs::bias_grad_launch(dbias, grad, N, c_out, out_h * out_w, beta);
+}
+
+int nrs_conv2d_maxpool_forward(float* pooled, int32_t* argmax, float* out, const float* input,
+                               const float* weight, const float* bias, int64_t N, int64_t c_in,
+                               int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
+                               int64_t stride, int64_t pad, int64_t pool_k, int64_t pool_stride) {
+    NRS_REQUIRE_INIT();
+    nrs::ConvDims d;
+    int rc = nrs::conv_dims(d, N, c_in, in_h, in_w, c_out, kh, kw, stride, pad);
+    if (rc) return rc;
+    NRS_ARG_CHECK(pool_k > 0 && pool_stride > 0 && d.out_h >= pool_k && d.out_w >= pool_k,
+                  "conv2d maxpool: bad window");
+    NRS_ARG_CHECK(N * c_out * d.out_h * d.out_w <= INT32_MAX,
+                  "conv2d maxpool: conv output too large for int32 argmax");
+    if (c_out == 0 || N == 0) return NRS_OK;
+    NRS_ARG_CHECK(pooled && argmax && input && weight, "conv2d maxpool: null pointer");
+    auto a8 = [](const void* q) { return ((uintptr_t)q & 7) == 0; };
+    if (kh == 3 && kw == 3 && stride == 1 && pad == 1 && c_in <= 3 && in_w % 4 == 0 &&
+        in_h % 2 == 0 && pool_k == 2 && pool_stride == 2 && c_out <= 65535 &&
+        ((uintptr_t)input & 15) == 0 && (!out || ((uintptr_t)out & 15) == 0) && a8(pooled) &&
+        a8(argmax) && N * c_in * in_h * in_w <= INT32_MAX / 4 &&
+        N * std::max(c_in, c_out) * in_h * in_w <= INT32_MAX) {
+        const int64_t blocks = N * (in_h / 2) * (in_w / 4);
+        auto fn = c_in == 1 ? nrs::conv_fwd_pool_quad_kernel<1>
+                            : (c_in == 2 ? nrs::conv_fwd_pool_quad_kernel<2>
+                                         : nrs::conv_fwd_pool_quad_kernel<3>);
+        hipLaunchKernelGGL(fn, dim3((unsigned)((blocks + 255) / 256),
+                                    (unsigned)((c_out + nrs::kQuadOc - 1) / nrs::kQuadOc)),
+                           dim3(256), 0, nrs::stream(), pooled, argmax, out, input, weight, bias,
+                           (int)N, (int)in_h, (int)in_w, (int)c_out,
+                           nrs::make_fastdiv((uint32_t)((in_h / 2) * (in_w / 4))),
+                           nrs::make_fastdiv((uint32_t)(in_w / 4)));
+        NRS_LAUNCH_CHECK("conv2d + maxpool forward (pixel blocks)");
+        return NRS_OK;
+    }
+    // any other shape: the conv output (the caller's, else library scratch),
+    // then the pooling
+    float* y = out;
+    if (!y) {
+        y = nrs::workspace(sizeof(float) * (size_t)(N * c_out * d.out_h * d.out_w), 5);
+        if (!y) return NRS_ERR_ALLOC;
+    }
+    rc = nrs_conv2d_forward(y, input, weight, bias, N, c_in, in_h, in_w, c_out, kh, kw, stride, pad);
+    if (rc) return rc;
+    return nrs_maxpool_forward(pooled, argmax, y, N, c_out, d.out_h, d.out_w, pool_k, pool_stride);
+}
+
+int nrs_maxpool_conv2d_backward(float* dinput, float* dweight, float* dbias,
+                                const float* grad_pooled, const int32_t* argmax,
+                                const float* input, const float* weight, int64_t N, int64_t c_in,
+                                int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
+                                int64_t stride, int64_t pad, int64_t pool_k,
+                                int64_t pool_stride) {
+    NRS_REQUIRE_INIT();
+    nrs::ConvDims d;
+    int rc = nrs::conv_dims(d, N, c_in, in_h, in_w, c_out, kh, kw, stride, pad);
+    if (rc) return rc;
+    NRS_ARG_CHECK(pool_k > 0 && pool_stride > 0 && d.out_h >= pool_k && d.out_w >= pool_k,
+                  "maxpool conv2d backward: bad window");
+    const int64_t conv_elems = N * c_out * d.out_h * d.out_w;
+    NRS_ARG_CHECK(conv_elems <= INT32_MAX,
+                  "maxpool conv2d backward: conv output too large for int32 argmax");
+    if (c_out == 0 || N == 0 || (!dinput && !dweight && !dbias)) return NRS_OK;
+    NRS_ARG_CHECK(grad_pooled && argmax && input && weight, "maxpool conv2d backward: null pointer");
+    if (!dinput && pool_k == 2 && pool_stride == 2 && c_in * kh * kw <= nrs::kDirectTaps &&
+        c_out <= INT32_MAX) {
+        // weight and bias gradients with the pooled gradient expanded while
+        // it is loaded
+        nrs::FewTapsWgrad f;
+        f.x = input;
+        f.g = nullptr;
+        f.gp = grad_pooled;
+        f.am = argmax;
+        f.dw = dweight;
+        f.db = dbias;
+        f.N = N;
+        f.C = (int)c_in;
+        f.H = (int)in_h;
+        f.W = (int)in_w;
+        f.M = (int)c_out;
+        f.kh = (int)kh;
+        f.kw = (int)kw;
+        f.stride = (int)stride;
+        f.pad = (int)pad;
+        f.OH = (int)d.out_h;
+        f.OW = (int)d.out_w;
+        if ((rc = nrs::few_taps_wgrad(f)) != nrs::kSlabUnsupported) return rc;
+    }
+    // any other case: the conv output's gradient in library scratch (the
+    // pooling's backward into zeros), then the conv backward
+    float* g = nrs::workspace(sizeof(float) * (size_t)conv_elems, 5);
+    if (!g) return NRS_ERR_ALLOC;
+    if ((rc = nrs::zero_fill(g, sizeof(float) * (size_t)conv_elems))) return rc;
+    rc = nrs_maxpool_backward(g, grad_pooled, argmax, N, c_out, d.out_h, d.out_w, pool_k,
+                              pool_stride);
+    if (rc) return rc;
+    return nrs_conv2d_backward(dinput, dweight, dbias, g, input, weight, N, c_in, in_h, in_w,
+                               c_out, kh, kw, stride, pad);
 }
 
 int nrs_conv2d_forward(float* out, const float* input, const float* weight, const float* bias,

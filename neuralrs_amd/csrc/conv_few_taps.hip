@@ -13,6 +13,10 @@
 // output gradient per channel block feeds four MFMAs. The input image is
 // staged in LDS with a zero halo, so a tap reads x_t(p) branch-free.
 //
+// UNPOOL: the output gradient is the 2x2 max-pool backward of a pooled
+// gradient, expanded while loading (the conv output's gradient is never
+// written).
+//
 // A workgroup (4 waves) owns one image and `4*GPW` groups of 16 pixels.
 // A wave issues all its gradient loads at once (one memory round trip) and
 // then runs its MFMA chain over its pixel groups in order. The four waves'
@@ -37,13 +41,15 @@ constexpr int kStageX = 4;        // image floats per thread per staging round
 struct FewTapsArgs {
     const float* x;
     const float* g;
+    const float* gp;     // UNPOOL: pooled gradient [N][M][OH/2][OW/2]
+    const int32_t* am;   // UNPOOL: its argmax (flat conv-output indices)
     float* pw;  // [slices][M][taps]
     float* pb;  // [slices][M]
-    int C, H, W, M, kh, kw, stride, pad, OW, P, Hp, Wp, taps, chunks;
+    int C, H, W, M, kh, kw, stride, pad, OH, OW, P, Hp, Wp, taps, chunks;
     FastDiv div_ow;
 };
 
-template <int NBLK, int GPW>
+template <int NBLK, int GPW, bool UNPOOL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void wgrad_few_taps_kernel(FewTapsArgs a) {
     extern __shared__ __attribute__((aligned(16))) float xs[];  // [C][Hp][Wp]
@@ -55,16 +61,61 @@ void wgrad_few_taps_kernel(FewTapsArgs a) {
     // gradient fragments first: [group][block], pixels 16*gi + 4*kq .. +3
     // of channel 16*b + t (zero past P and M through the buffer bounds)
     const int g0 = (chunk * 4 + wave) * GPW;
-    const auto rg = buffer_rsrc(a.g + (int64_t)n * a.M * a.P, (int64_t)a.M * a.P * 4);
     f32x4v ga[GPW][NBLK];
+    if constexpr (!UNPOOL) {
+        const auto rg = buffer_rsrc(a.g + (int64_t)n * a.M * a.P, (int64_t)a.M * a.P * 4);
 #pragma unroll
-    for (int q = 0; q < GPW; ++q) {
-        const int p = 16 * (g0 + q) + 4 * kq;
+        for (int q = 0; q < GPW; ++q) {
+            const int p = 16 * (g0 + q) + 4 * kq;
 #pragma unroll
-        for (int b = 0; b < NBLK; ++b) {
-            const int oc = 16 * b + t;
-            ga[q][b] = buffer_load4(rg, ((p < a.P) & (oc < a.M)) ? (oc * a.P + p) * 4 : kOutOfRange);
+            for (int b = 0; b < NBLK; ++b) {
+                const int oc = 16 * b + t;
+                ga[q][b] =
+                    buffer_load4(rg, ((p < a.P) & (oc < a.M)) ? (oc * a.P + p) * 4 : kOutOfRange);
+            }
         }
+    } else {
+        // pixels p .. p+3 (one row: OW % 4 == 0) lie in pooled columns
+        // x/2 and x/2 + 1 of pooled row y/2: two pooled values and two
+        // indices per quad, 64-bit loads; the quad's values are the pooled
+        // value where the index names the pixel, else 0
+        const int PP = (a.OH >> 1) * (a.OW >> 1);
+        const auto rp = buffer_rsrc(a.gp + (int64_t)n * a.M * PP, (int64_t)a.M * PP * 4);
+        const auto ri = buffer_rsrc(reinterpret_cast<const float*>(a.am) + (int64_t)n * a.M * PP,
+                                    (int64_t)a.M * PP * 4);
+        f32x2 gv[GPW][NBLK], iv[GPW][NBLK];
+        int qy[GPW], qx[GPW];
+#pragma unroll
+        for (int q = 0; q < GPW; ++q) {
+            const int p = 16 * (g0 + q) + 4 * kq;
+            uint32_t y, x;
+            fast_divmod((uint32_t)min(p, a.P - 1), a.div_ow, y, x);
+            qy[q] = (int)y;
+            qx[q] = (int)x;
+            const int pw = (int)(y >> 1) * (a.OW >> 1) + (int)(x >> 1);
+#pragma unroll
+            for (int b = 0; b < NBLK; ++b) {
+                const int oc = 16 * b + t;
+                const bool ok = (p < a.P) & (oc < a.M);
+                gv[q][b] = buffer_load2(rp, ok ? (oc * PP + pw) * 4 : kOutOfRange);
+                iv[q][b] = buffer_load2(ri, ok ? (oc * PP + pw) * 4 : kOutOfRange);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < GPW; ++q)
+#pragma unroll
+            for (int b = 0; b < NBLK; ++b) {
+                const int oc = 16 * b + t;
+                const int e0 = ((n * a.M + oc) * a.OH + qy[q]) * a.OW + qx[q];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    // the element first, then its bits (a bit_cast of the
+                    // vector element expression read element 0 for every u)
+                    const float raw = u < 2 ? iv[q][b].x : iv[q][b].y;
+                    const int idx = __builtin_bit_cast(int, raw);
+                    ga[q][b][u] = idx == e0 + u ? (u < 2 ? gv[q][b].x : gv[q][b].y) : 0.0f;
+                }
+            }
     }
 
     // the image with a zero halo of `pad` (rows and columns), kStageX items
@@ -149,14 +200,20 @@ void wgrad_few_taps_kernel(FewTapsArgs a) {
     }
 }
 
-template <int NBLK>
+template <int NBLK, bool UNPOOL>
 void* pick_gpw(int gpw) {
     switch (gpw) {
-        case 1: return reinterpret_cast<void*>(wgrad_few_taps_kernel<NBLK, 1>);
-        case 2: return reinterpret_cast<void*>(wgrad_few_taps_kernel<NBLK, 2>);
-        case 4: return reinterpret_cast<void*>(wgrad_few_taps_kernel<NBLK, 4>);
-        default: return reinterpret_cast<void*>(wgrad_few_taps_kernel<NBLK, 8>);
+        case 1: return reinterpret_cast<void*>(wgrad_few_taps_kernel<NBLK, 1, UNPOOL>);
+        case 2: return reinterpret_cast<void*>(wgrad_few_taps_kernel<NBLK, 2, UNPOOL>);
+        case 4: return reinterpret_cast<void*>(wgrad_few_taps_kernel<NBLK, 4, UNPOOL>);
+        default: return reinterpret_cast<void*>(wgrad_few_taps_kernel<NBLK, 8, UNPOOL>);
     }
+}
+
+template <bool UNPOOL>
+void* pick_kernel(int nblk, int gpw) {
+    return nblk == 1 ? pick_gpw<1, UNPOOL>(gpw)
+                     : (nblk == 2 ? pick_gpw<2, UNPOOL>(gpw) : pick_gpw<4, UNPOOL>(gpw));
 }
 
 }  // namespace
@@ -168,6 +225,10 @@ int few_taps_wgrad(const FewTapsWgrad& s) {
     if (taps > kFewTaps || s.M > kFewMaxM || s.M < 1 || P % 4 || P < 1 || s.N < 1 ||
         (int64_t)s.C * Hp * Wp > kFewImage || (int64_t)s.M * P > INT32_MAX / 4 ||
         (int64_t)(s.OH - 1) * s.stride + s.kh > Hp || (int64_t)(s.OW - 1) * s.stride + s.kw > Wp)
+        return kSlabUnsupported;
+    const bool unpool = s.g == nullptr;
+    if (unpool && (!s.gp || !s.am || s.OH % 2 || s.OW % 4 || ((uintptr_t)s.gp & 7) ||
+                   ((uintptr_t)s.am & 7) || s.N * s.M * P > INT32_MAX))
         return kSlabUnsupported;
     const int nblk = s.M <= 16 ? 1 : (s.M <= 32 ? 2 : 4);  // channel blocks instantiated
     const int64_t gpi = (P + 15) / 16;
@@ -184,6 +245,8 @@ int few_taps_wgrad(const FewTapsWgrad& s) {
     FewTapsArgs a;
     a.x = s.x;
     a.g = s.g;
+    a.gp = s.gp;
+    a.am = s.am;
     a.pw = pw;
     a.pb = pb;
     a.C = s.C;
@@ -194,6 +257,7 @@ int few_taps_wgrad(const FewTapsWgrad& s) {
     a.kw = s.kw;
     a.stride = s.stride;
     a.pad = s.pad;
+    a.OH = s.OH;
     a.OW = s.OW;
     a.P = (int)P;
     a.Hp = Hp;
@@ -203,7 +267,7 @@ int few_taps_wgrad(const FewTapsWgrad& s) {
     a.div_ow = make_fastdiv((uint32_t)s.OW);
     const size_t lds =
         sizeof(float) * (size_t)std::max<int64_t>((int64_t)s.C * Hp * Wp, 4 * nblk * 16 * 17);
-    void* fn = nblk == 1 ? pick_gpw<1>(gpw) : (nblk == 2 ? pick_gpw<2>(gpw) : pick_gpw<4>(gpw));
+    void* fn = unpool ? pick_kernel<true>(nblk, gpw) : pick_kernel<false>(nblk, gpw);
     hipLaunchKernelGGL(reinterpret_cast<void (*)(FewTapsArgs)>(fn), dim3((unsigned)slices),
                        dim3(256), lds, stream(), a);
     NRS_LAUNCH_CHECK("conv2d weight gradient (few taps)");

@@ -69,6 +69,11 @@ struct FewTapsWgrad {
     float* db = nullptr;       // [M] or null
     int64_t N = 0;
     int C = 0, H = 0, W = 0, M = 0, kh = 0, kw = 0, stride = 1, pad = 0, OH = 0, OW = 0;
+    // g absent: the output gradient is the 2x2 (stride 2) max-pool backward of
+    // gp [N][M][OH/2][OW/2] with argmax am (flat indices of the conv output),
+    // expanded on the fly: g[e] = gp[w] where am[w] == e, else 0
+    const float* gp = nullptr;
+    const int32_t* am = nullptr;
 };
 int few_taps_wgrad(const FewTapsWgrad& s);
 

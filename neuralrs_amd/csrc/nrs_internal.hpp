@@ -24,7 +24,9 @@ int set_error(int code, const char* fmt, ...);
 
 // Library-owned scratch, grown lazily, one buffer per slot:
 //   0 split-K partials, 1 im2col / dcols columns, 2 conv grad in GEMM layout,
-//   3 reduction partials, 4 conv weights packed for LDS staging.
+//   3 reduction partials, 4 conv weights packed for LDS staging, 5 the conv
+//   output or its gradient around a fused pooling (not used by the conv
+//   entry points themselves, which the fused ones call).
 // Returns nullptr (and records an error) when the allocation fails.
 float* workspace(size_t bytes, int slot = 0);
 

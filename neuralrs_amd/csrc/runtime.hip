@@ -12,7 +12,7 @@
 namespace nrs {
 namespace {
 
-constexpr int kSlots = 5;
+constexpr int kSlots = 6;
 
 // Scratch of the no-allocation entry points: one per GPU, held until the
 // process ends. In host code `scratch` names a host-side stand-in, so it is

@@ -316,3 +316,98 @@ def test_maxpool_bit_exact(hip, orc, dims):
     di = D(hip, d0)
     hip.call("nrs_maxpool_backward", di.ptr, D(hip, g), am.ptr, n, c, h, w, k, s)
     assert np.array_equal(di.to_host(), orc.maxpool_backward(g, am_ref, x.size, d0))
+
+
+# ------------------------------------------------ conv2d + maxpool, fused
+POOL_SHAPES = [  # (n, c_in, c_out, h, w, kh, kw, stride, pad, pool_k, pool_stride)
+    (128, 1, 32, 28, 28, 3, 3, 1, 1, 2, 2),   # cfg3 conv1 -> maxpool: the fused kernels
+    (3, 3, 20, 8, 12, 3, 3, 1, 1, 2, 2),      # 3 input channels, ragged channel block
+    (2, 2, 9, 6, 4, 3, 3, 1, 1, 2, 2),
+    (2, 4, 6, 8, 8, 3, 3, 1, 1, 2, 2),        # 4 input channels: forward runs the two ops
+    (2, 1, 5, 7, 9, 3, 3, 1, 1, 2, 2),        # odd sizes: the two ops (and a partial window)
+    (2, 2, 4, 9, 9, 3, 3, 1, 1, 3, 3),        # 3x3 pooling
+    (2, 3, 4, 8, 8, 5, 5, 1, 2, 2, 2),        # 5x5 conv
+]
+
+
+def _pool_ref(hip, x, w, b, shape, floats):
+    n, ci, co, h, wd, kh, kw, s, p, pk, ps = shape
+    D = hip.DeviceBuffer.from_host
+    oh, ow = (h + 2 * p - kh) // s + 1, (wd + 2 * p - kw) // s + 1
+    ph, pw = (oh - pk) // ps + 1, (ow - pk) // ps + 1
+    y = hip.DeviceBuffer(n * co * oh * ow)
+    hip.call("nrs_conv2d_forward", y, D(x), D(w), D(b), n, ci, h, wd, co, kh, kw, s, p)
+    pooled, am = hip.DeviceBuffer(n * co * ph * pw), hip.DeviceBuffer(n * co * ph * pw, np.int32)
+    hip.call("nrs_maxpool_forward", pooled, am, y, n, co, oh, ow, pk, ps)
+    return y.to_host(), pooled.to_host(), am.to_host(), (oh, ow, ph, pw)
+
+
+@pytest.mark.parametrize("shape", POOL_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("floats", [False, True], ids=["ints", "floats"])
+def test_conv2d_maxpool_forward_matches_the_two_ops(hip, shape, floats):
+    """nrs_conv2d_maxpool_forward gives the pooled values, argmax and (when
+    asked) conv output of nrs_conv2d_forward then nrs_maxpool_forward, bit for
+    bit (small integers, with ties the first maximum wins; and f32 data)."""
+    n, ci, co, h, wd, kh, kw, s, p, pk, ps = shape
+    rng = np.random.default_rng(n * 100 + ci * 10 + co)
+    if floats:
+        x = rng.standard_normal(n * ci * h * wd).astype(np.float32)
+        w = (rng.standard_normal(co * ci * kh * kw) * 0.3).astype(np.float32)
+        b = rng.standard_normal(co).astype(np.float32)
+    else:
+        x = int_matrix(rng, (n * ci * h * wd,), -2, 2)
+        w = int_matrix(rng, (co * ci * kh * kw,), -2, 2)
+        b = int_matrix(rng, (co,), -2, 2)
+    y_ref, pool_ref, am_ref, (oh, ow, ph, pw) = _pool_ref(hip, x, w, b, shape, floats)
+    D = hip.DeviceBuffer.from_host
+    for with_out in (False, True):
+        pooled, am = hip.DeviceBuffer(n * co * ph * pw), hip.DeviceBuffer(n * co * ph * pw, np.int32)
+        y = hip.DeviceBuffer(n * co * oh * ow) if with_out else None
+        print(f"conv2d maxpool forward {shape} floats={floats} out={with_out}", flush=True)
+        hip.call("nrs_conv2d_maxpool_forward", pooled, am, y, D(x), D(w), D(b), n, ci, h, wd, co,
+                 kh, kw, s, p, pk, ps)
+        assert np.array_equal(pooled.to_host(), pool_ref)
+        assert np.array_equal(am.to_host(), am_ref)
+        if with_out:
+            assert np.array_equal(y.to_host(), y_ref)
+
+
+@pytest.mark.parametrize("shape", POOL_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("with_dx", [False, True], ids=["w_b", "x_w_b"])
+def test_maxpool_conv2d_backward_matches_the_two_ops(hip, orc, shape, with_dx):
+    """nrs_maxpool_conv2d_backward (weight and bias gradients, and the input
+    gradient when asked) equals maxpool_backward into zeros followed by
+    nrs_conv2d_backward, bit for bit, accumulating over old values; the
+    weight-only form of cfg3 conv1 expands the pooled gradient while loading.
+    Also checked against the oracle's maxpool and conv2d backward on small
+    integers."""
+    n, ci, co, h, wd, kh, kw, s, p, pk, ps = shape
+    rng = np.random.default_rng(n * 7 + ci * 3 + co)
+    x = int_matrix(rng, (n * ci * h * wd,), -2, 2)
+    w = int_matrix(rng, (co * ci * kh * kw,), -2, 2)
+    b = np.zeros(co, np.float32)
+    _, _, am, (oh, ow, ph, pw) = _pool_ref(hip, x, w, b, shape, False)
+    gp = int_matrix(rng, (n * co * ph * pw,), -3, 3)
+    D = hip.DeviceBuffer.from_host
+    old_x, old_w, old_b = (int_matrix(rng, (m,), -3, 3) for m in (x.size, w.size, co))
+    # the two ops
+    dam = hip.DeviceBuffer.from_host(am, np.int32)
+    g = hip.DeviceBuffer.zeros(n * co * oh * ow)
+    hip.call("nrs_maxpool_backward", g, D(gp), dam, n, co, oh, ow, pk, ps)
+    rx, rw, rb = D(old_x), D(old_w), D(old_b)
+    hip.call("nrs_conv2d_backward", rx if with_dx else None, rw, rb, g, D(x), D(w), n, ci, h, wd,
+             co, kh, kw, s, p)
+    fx, fw, fb = D(old_x), D(old_w), D(old_b)
+    print(f"maxpool conv2d backward {shape} dx={with_dx}", flush=True)
+    hip.call("nrs_maxpool_conv2d_backward", fx if with_dx else None, fw, fb, D(gp), dam, D(x),
+             D(w), n, ci, h, wd, co, kh, kw, s, p, pk, ps)
+    assert np.array_equal(fw.to_host(), rw.to_host())
+    assert np.array_equal(fb.to_host(), rb.to_host())
+    if with_dx:
+        assert np.array_equal(fx.to_host(), rx.to_host())
+    # the oracle: maxpool backward into zeros, then Conv2d's backward
+    g_ref = orc.maxpool_backward(gp, am, n * co * oh * ow)
+    _, dw_ref, db_ref = orc.conv2d_backward(x, w, g_ref, n, ci, co, h, wd, kh, kw, s, p)
+    assert np.array_equal(fw.to_host(), dw_ref.ravel() + old_w)
+    assert np.array_equal(fb.to_host(), db_ref.ravel() + old_b)
+    assert np.any(dw_ref != 0)  # the pooled gradient reached the weights
