@@ -143,15 +143,16 @@ def bench_conv_cfg3(hip, steps, warmup, closures_only=False):
     # conv1 -> maxpool as one node each way: conv1's output only feeds the
     # pooling, so the fused forward never writes it and the fused backward
     # expands the pooled gradient while loading (nrs_conv2d_maxpool_forward /
-    # nrs_maxpool_conv2d_backward); the unfused sequence is step_unfused
+    # nrs_maxpool_conv2d_backward); the op-by-op sequence, with its zeroing
+    # launches, is step_unfused
     def step():
         hip.call("nrs_conv2d_maxpool_forward", p1.ptr, am.ptr, None, dx.ptr, dw1.ptr, db1.ptr,
                  N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2)
         hip.call("nrs_conv2d_forward", y2.ptr, p1.ptr, dw2.ptr, db2.ptr, N, 32, 14, 14, 64, 3, 3, 1, 1)
-        # backward (zero_grad of the pooled activation's grad, then accumulate)
-        hip.call("nrs_memset_zero", gp1.ptr, gp1.nbytes)
-        hip.call("nrs_conv2d_backward", gp1.ptr, gw2.ptr, gb2.ptr, dg2.ptr, p1.ptr, dw2.ptr,
-                 N, 32, 14, 14, 64, 3, 3, 1, 1)
+        # backward: the pooled activation's gradient is written (beta 0: its
+        # zero_grad and first accumulate_into in one), the parameters' add up
+        hip.call("nrs_conv2d_backward_beta", gp1.ptr, gw2.ptr, gb2.ptr, dg2.ptr, p1.ptr, dw2.ptr,
+                 N, 32, 14, 14, 64, 3, 3, 1, 1, 0.0)
         hip.call("nrs_maxpool_conv2d_backward", None, gw1.ptr, gb1.ptr, gp1.ptr, am.ptr, dx.ptr,
                  dw1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2)
 

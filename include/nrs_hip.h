@@ -277,6 +277,17 @@ int nrs_conv2d_backward(float *dinput, float *dweight, float *dbias,
                         int64_t c_out, int64_t kh, int64_t kw, int64_t stride,
                         int64_t pad);
 
+/* nrs_conv2d_backward with dinput = its gradient + beta_input * dinput: 1 is
+ * nrs_conv2d_backward's accumulation (the backward closure's accumulate_into,
+ * src/cuda/nn/conv.rs:298-312); 0 writes the gradient without reading dinput
+ * (a gradient buffer that was just zeroed needs no zeroing launch). dweight
+ * and dbias accumulate as in nrs_conv2d_backward.                          */
+int nrs_conv2d_backward_beta(float *dinput, float *dweight, float *dbias,
+                             const float *grad, const float *input, const float *weight,
+                             int64_t N, int64_t c_in, int64_t in_h, int64_t in_w,
+                             int64_t c_out, int64_t kh, int64_t kw, int64_t stride,
+                             int64_t pad, float beta_input);
+
 /* nn::conv2d followed by max pooling (src/cuda/nn/conv.rs:244-277, then
  * src/cuda/nn/maxpool.rs:18-46 on the conv output) in one call: pooled
  * [N, c_out, oh/k', ow/k'] and argmax as nrs_maxpool_forward gives them for

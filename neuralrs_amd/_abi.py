@@ -66,6 +66,7 @@ SIGNATURES = {
     "nrs_conv2d_bias_grad": [_P, _P, _I, _I, _I, _I, _F],
     "nrs_conv2d_forward": [_P, _P, _P, _P] + [_I] * 9,
     "nrs_conv2d_backward": [_P, _P, _P, _P, _P, _P] + [_I] * 9,
+    "nrs_conv2d_backward_beta": [_P, _P, _P, _P, _P, _P] + [_I] * 9 + [_F],
     "nrs_conv2d_maxpool_forward": [_P, _P, _P, _P, _P, _P] + [_I] * 11,
     "nrs_maxpool_conv2d_backward": [_P, _P, _P, _P, _P, _P, _P] + [_I] * 11,
     "nrs_accumulate": [_P, _P, _I],

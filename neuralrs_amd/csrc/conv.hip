@@ -1106,7 +1106,16 @@ int launch_out2mm(float* mm, const float* grad, const ConvDims& d) {
 // dinput += the stride-1 input gradient of a layer with c_in <= kDirectCin
 // and a kernel width the row kernel is built for, gathered from LDS;
 // kSlabUnsupported when it does not apply or its tiles do not fit.
-int quad_dgrad(float* dinput, const float* grad, const float* weight, const ConvDims& d) {
+// dinput = beta * dinput ahead of a kernel that only accumulates (beta 0:
+// a fill, nothing read).
+int prescale_grad(float* dinput, int64_t n, float beta) {
+    if (beta == 1.0f) return NRS_OK;
+    if (beta == 0.0f) return zero_fill(dinput, sizeof(float) * (size_t)n);
+    return nrs_scale(dinput, dinput, beta, n, 0.0f);
+}
+
+int quad_dgrad(float* dinput, const float* grad, const float* weight, const ConvDims& d,
+               float beta) {
     if (d.stride != 1 || d.c_in > 4 || d.kh != 3 || d.kw != 3 || d.pad != 1 || d.in_w % 4 ||
         d.in_w > 64 || d.out_h != d.in_h || d.out_w != d.in_w || ((uintptr_t)dinput & 15) ||
         ((uintptr_t)grad & 15) || d.c_out * d.in_h * d.in_w > INT32_MAX / 4 ||
@@ -1130,6 +1139,7 @@ int quad_dgrad(float* dinput, const float* grad, const float* weight, const Conv
                                         (size_t)kQuadDgradOc * CIN * 9 + (size_t)groups * qpg * CIN * 4);
     if (lds > 64 * 1024) return kSlabUnsupported;
     auto fn = CIN == 1 ? conv_dgrad_quad_kernel<1> : conv_dgrad_quad_kernel<4>;
+    if (int rc = prescale_grad(dinput, d.N * d.c_in * d.in_h * d.in_w, beta)) return rc;
     hipLaunchKernelGGL(fn, dim3((unsigned)(d.N * bands)), dim3(256), lds, stream(), dinput, grad,
                        weight, (int)d.c_in, (int)d.in_h, (int)d.in_w, (int)d.c_out, (int)band,
                        (int)bands, pitch, groups, qpg, make_fastdiv((uint32_t)W4),
@@ -1139,9 +1149,10 @@ int quad_dgrad(float* dinput, const float* grad, const float* weight, const Conv
     return NRS_OK;
 }
 
-int small_dgrad(float* dinput, const float* grad, const float* weight, const ConvDims& d) {
+int small_dgrad(float* dinput, const float* grad, const float* weight, const ConvDims& d,
+                float beta) {
     if (d.stride != 1 || d.c_in > kDirectCin) return kSlabUnsupported;
-    const int rq = quad_dgrad(dinput, grad, weight, d);
+    const int rq = quad_dgrad(dinput, grad, weight, d, beta);
     if (rq != kSlabUnsupported) return rq;
     const int64_t ngx = (d.in_w + kDgradRun - 1) / kDgradRun;
     if (ngx > 256) return kSlabUnsupported;
@@ -1179,6 +1190,7 @@ int small_dgrad(float* dinput, const float* grad, const float* weight, const Con
         case 7: fn = c1 ? conv_dgrad_small_kernel<7, 1> : conv_dgrad_small_kernel<7, 4>; break;
         default: return kSlabUnsupported;
     }
+    if (int rc = prescale_grad(dinput, d.N * d.c_in * d.in_h * d.in_w, beta)) return rc;
     hipLaunchKernelGGL(fn, dim3((unsigned)(d.N * bands)), dim3(256), lds, stream(), dinput, grad,
                        weight, (int)d.c_in, (int)d.in_h, (int)d.in_w, (int)d.c_out, (int)d.kh,
                        (int)d.pad, (int)d.out_h, (int)d.out_w, (int)band, (int)bands, (int)occ,
@@ -1223,7 +1235,7 @@ int small_wgrad(float* dweight, float* dbias, const float* grad, const float* in
 // both fit their slab kernels (*wg_done is then set).
 int slab_dgrad(float* dinput, const float* grad, const float* weight, int64_t N, int64_t c_in,
                int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw, int64_t pad,
-               const ConvDims& d, const SlabWgrad* wg, bool* wg_done) {
+               const ConvDims& d, const SlabWgrad* wg, bool* wg_done, float beta) {
     if (c_in > INT32_MAX || c_out > INT32_MAX || in_h > INT32_MAX || in_w > INT32_MAX)
         return kSlabUnsupported;
     SlabConv s;
@@ -1243,7 +1255,7 @@ int slab_dgrad(float* dinput, const float* grad, const float* weight, int64_t N,
     s.OH = (int)in_h;
     s.OW = (int)in_w;
     s.flip = true;
-    s.beta = 1.0f;
+    s.beta = beta;
     if (wg) {
         // with the weight gradient: both in one launch
         const int rc = slab_backward_pair(s, *wg);
@@ -1523,6 +1535,14 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
                         const float* input, const float* weight, int64_t N, int64_t c_in,
                         int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
                         int64_t stride, int64_t pad) {
+    return nrs_conv2d_backward_beta(dinput, dweight, dbias, grad, input, weight, N, c_in, in_h,
+                                    in_w, c_out, kh, kw, stride, pad, 1.0f);
+}
+
+int nrs_conv2d_backward_beta(float* dinput, float* dweight, float* dbias, const float* grad,
+                             const float* input, const float* weight, int64_t N, int64_t c_in,
+                             int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
+                             int64_t stride, int64_t pad, float beta_input) {
     NRS_REQUIRE_INIT();
     nrs::ConvDims d;
     int rc = nrs::conv_dims(d, N, c_in, in_h, in_w, c_out, kh, kw, stride, pad);
@@ -1557,7 +1577,7 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
     bool wgrad_done = false;
     if (dinput) {
         const int64_t grad_bytes = N * c_out * P * (int64_t)sizeof(float);
-        if ((rc = nrs::small_dgrad(dinput, grad, weight, d)) != nrs::kSlabUnsupported) {
+        if ((rc = nrs::small_dgrad(dinput, grad, weight, d, beta_input)) != nrs::kSlabUnsupported) {
             // a handful of input channels, stride 1: gather from LDS
             if (rc) return rc;
         } else if (c_in <= nrs::kDirectCin && c_out * c_in * kh * kw <= nrs::kDirectWeights &&
@@ -1569,11 +1589,11 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
                                (int)in_h, (int)in_w, (int)c_out, (int)kh, (int)kw,
                                nrs::make_fastdiv((uint32_t)stride), (int)pad, (int)d.out_h,
                                (int)d.out_w, nrs::make_fastdiv((uint32_t)(in_h * in_w)),
-                               nrs::make_fastdiv((uint32_t)in_w), 1.0f);
+                               nrs::make_fastdiv((uint32_t)in_w), beta_input);
             NRS_LAUNCH_CHECK("conv2d input gradient (direct)");
         } else if (stride == 1 && pad <= kh - 1 && pad <= kw - 1 &&
                    (rc = slab_dgrad(dinput, grad, weight, N, c_in, in_h, in_w, c_out, kh, kw,
-                                    pad, d, slab_w ? &w : nullptr, &wgrad_done)) !=
+                                    pad, d, slab_w ? &w : nullptr, &wgrad_done, beta_input)) !=
                        nrs::kSlabUnsupported) {
             // dinput += conv(grad, flipped W) with padding k-1-pad, staged in LDS
             if (rc) return rc;
@@ -1589,7 +1609,7 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
             NRS_LAUNCH_CHECK("conv2d flip weights");
             nrs::ConvGeom g{c_out, d.out_h, d.out_w, (int)kh, (int)kw, 1, (int)(kh - 1 - pad),
                             (int)(kw - 1 - pad), in_h, in_w, in_h * in_w};
-            rc = nrs::implicit_conv(dinput, grad, wf, nullptr, N, c_in, g, 1.0f);
+            rc = nrs::implicit_conv(dinput, grad, wf, nullptr, N, c_in, g, beta_input);
             if (rc) return rc;
         } else {
             // dcols[col_h, N*P] = W^T . G ; dinput += col2im(dcols)   (conv.rs:304-312)
@@ -1609,7 +1629,7 @@ int nrs_conv2d_backward(float* dinput, float* dweight, float* dbias, const float
             c.K = c_out;
             rc = nrs::gemm_run(c);
             if (rc) return rc;
-            rc = nrs::launch_col2im(dinput, cols, d, 1.0f);
+            rc = nrs::launch_col2im(dinput, cols, d, beta_input);
             if (rc) return rc;
         }
     }

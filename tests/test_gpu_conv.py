@@ -411,3 +411,36 @@ def test_maxpool_conv2d_backward_matches_the_two_ops(hip, orc, shape, with_dx):
     assert np.array_equal(fw.to_host(), dw_ref.ravel() + old_w)
     assert np.array_equal(fb.to_host(), db_ref.ravel() + old_b)
     assert np.any(dw_ref != 0)  # the pooled gradient reached the weights
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 4, 8, 8, 3, 3, 1, 1), (3, 1, 32, 28, 28, 3, 3, 1, 1),
+                                   (2, 32, 64, 14, 14, 3, 3, 1, 1), (2, 6, 5, 9, 9, 3, 3, 1, 1),
+                                   (1, 8, 3, 7, 7, 3, 3, 2, 1), (2, 2, 3, 6, 6, 2, 2, 1, 2),
+                                   (1, 40, 70, 6, 7, 3, 3, 1, 1)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("beta", [0.0, 0.5, 1.0])
+@pytest.mark.parametrize("with_w", [False, True], ids=["dx", "dx_dw_db"])
+def test_conv2d_backward_beta(hip, orc, shape, beta, with_w):
+    """nrs_conv2d_backward_beta: dinput = its gradient + beta * dinput on every
+    input-gradient path (pixel quads, direct, slab and the slab pair with the
+    weight gradient, implicit GEMM, col2im); beta 0 over NaN shows that the
+    old values are not read. Weight and bias gradients accumulate."""
+    n, ci, co, h, w, kh, kw, s, p = shape
+    rng = np.random.default_rng(n + ci + co + h)
+    x = int_matrix(rng, (n * ci * h * w,), -2, 2)
+    wt = int_matrix(rng, (co * ci * kh * kw,), -2, 2)
+    oh, ow = (h + 2 * p - kh) // s + 1, (w + 2 * p - kw) // s + 1
+    g = int_matrix(rng, (n * co * oh * ow,), -2, 2)
+    di_ref, dw_ref, db_ref = orc.conv2d_backward(x, wt, g, n, ci, co, h, w, kh, kw, s, p)
+    old = int_matrix(rng, (x.size,), -3, 3) if beta else np.full(x.size, np.nan, np.float32)
+    ow0, ob0 = int_matrix(rng, (wt.size,), -3, 3), int_matrix(rng, (co,), -3, 3)
+    D = hip.DeviceBuffer.from_host
+    ddi, ddw, ddb = D(old), D(ow0), D(ob0)
+    print(f"conv2d backward beta {shape} beta={beta} w={with_w}", flush=True)
+    hip.call("nrs_conv2d_backward_beta", ddi, ddw if with_w else None, ddb if with_w else None,
+             D(g), D(x), D(wt), n, ci, h, w, co, kh, kw, s, p, beta)
+    want = di_ref.ravel() + (beta * old if beta else 0)
+    assert np.array_equal(ddi.to_host(), want)
+    if with_w:
+        assert np.array_equal(ddw.to_host(), dw_ref.ravel() + ow0)
+        assert np.array_equal(ddb.to_host(), db_ref.ravel() + ob0)
