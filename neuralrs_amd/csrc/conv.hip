@@ -1258,15 +1258,22 @@ int slab_dgrad(float* dinput, const float* grad, const float* weight, int64_t N,
     s.beta = beta;
     if (wg) {
         // with the weight gradient: both in one launch
-        const int rc = slab_backward_pair(s, *wg);
+        int rc = pipe_backward(&s, *wg);
+        if (rc != kSlabUnsupported) {
+            *wg_done = rc == NRS_OK;
+            return rc;
+        }
+        rc = slab_backward_pair(s, *wg);
         if (rc != kSlabUnsupported) {
             *wg_done = rc == NRS_OK;
             return rc;
         }
     } else {
-        // small 3x3 images: the whole gradient image resident in LDS, the
-        // weights flipped while they are staged (no packing launch)
-        const int rc = img_conv(s);
+        // small 3x3 images: the gradient image resident in LDS, the weights
+        // flipped while they are staged (no packing launch)
+        int rc = pipe_conv(s);
+        if (rc != kSlabUnsupported) return rc;
+        rc = img_conv(s);
         if (rc != kSlabUnsupported) return rc;
     }
     return slab_conv(s);
@@ -1497,6 +1504,8 @@ int nrs_conv2d_forward(float* out, const float* input, const float* weight, cons
         s.OW = (int)d.out_w;
         if (c_out <= INT32_MAX && d.out_h <= INT32_MAX && d.out_w <= INT32_MAX) {
             // small 3x3 images: the whole image resident in LDS
+            rc = nrs::pipe_conv(s);
+            if (rc != nrs::kSlabUnsupported) return rc;
             rc = nrs::img_conv(s);
             if (rc != nrs::kSlabUnsupported) return rc;
             rc = nrs::slab_conv(s);
@@ -1659,7 +1668,9 @@ int nrs_conv2d_backward_beta(float* dinput, float* dweight, float* dbias, const 
     }
     if (slab_w) {
         // input slab and gradient rows staged in LDS, reduction on the matrix
-        // cores, per-image partials summed in a fixed order
+        // cores, per-slice partials summed in a fixed order
+        rc = nrs::pipe_backward(nullptr, w);
+        if (rc != nrs::kSlabUnsupported) return rc;
         rc = nrs::slab_wgrad(w);
         if (rc != nrs::kSlabUnsupported) return rc;
     }

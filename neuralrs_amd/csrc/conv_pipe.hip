@@ -1,0 +1,531 @@
+// Chunk-pipelined image-resident convolution for small "same" 3x3 layers
+// (stride 1, pad 1, images of at most 14x14), on the f32 matrix cores
+// (v_mfma_f32_16x16x4f32). One kernel body serves
+//   * the forward of nn::conv2d (src/cuda/nn/conv.rs:266-277),
+//   * its input gradient (conv.rs:304-312), read as a forward convolution of
+//     the output gradient with the flipped, channel-transposed weights,
+//   * its weight and bias gradient (conv.rs:314-322),
+// and the backward runs both gradients' workgroups in one launch.
+//
+// Output workgroups ("D" blocks: forward or input gradient) own one image
+// and 32 output channels. The reduction K = C*9 is walked in chunks of 16
+// input channels, double-buffered in LDS: while the matrix cores reduce
+// chunk j, the loads of chunk j+1 are in flight into registers, and they are
+// written to the other buffer afterwards. A chunk is
+//   * 16 zero-padded image planes of 16 rows x 16 floats (+4, so a plane is
+//     4 floats past a multiple of 64 banks), each thread copying one row;
+//   * the block's 32 weight rows of the chunk's 16 channels x 9 taps: a
+//     straight 128-bit copy in the forward; in the input gradient the taps of
+//     w[oc][c] are reversed and (oc, c) transposed while they are staged.
+// Wave w owns output-channel block w & 1 (A rows) and output rows
+// (w >> 1) * 7 .. +6 (one B tile per row: lane = column, so every tap offset
+// is an immediate). Lane quarter q takes chunk channels 4q .. 4q+3, whose
+// planes start 16 banks apart, so a B read of 64 lanes hits 64 banks.
+//
+// Weight-gradient workgroups ("W" blocks) own two consecutive images (a K
+// slice), 16 input channels (N: channel x tap) and 64 output channels (M).
+// K is the image's pixels: lane quarter q takes pixels 4s + q at step s, so
+// the four quarters read four neighbouring pixels of their channel's plane
+// (planes 4 banks apart: conflict-free). The gradient rows are staged
+// de-interleaved by quarter ([oc][q][s]), so four steps of A are one 128-bit
+// read. The bias gradient is the same A values summed on the vector ALU.
+// Each slice writes [M][9][C] partials that wgrad_partial_sum adds in slice
+// order (deterministic).
+#include <algorithm>
+
+#include "buffer_ops.hpp"
+#include "conv_slab.hpp"
+#include "fastdiv.hpp"
+
+namespace nrs {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPRow = 16;                       // floats per staged image row
+constexpr int kPPlane = 260;                    // floats per staged plane (16 x 16 + 4)
+constexpr int kPCC = 16;                        // channels per chunk / per W block
+constexpr int kPImg = kPCC * kPPlane;           // a chunk's 16 staged planes
+constexpr int kPMB = 32;                        // output channels per D block
+constexpr int kPWrow = 148;                     // floats per staged weight row (144 + 4)
+constexpr int kPDBuf = kPImg + kPMB * kPWrow;   // floats per D chunk buffer
+constexpr int kPWM = 64;                        // output channels per W block
+constexpr int kPGrow = 52;                      // floats per (oc, quarter) gradient row
+constexpr int kPGs = kPWM * 4 * kPGrow;         // staged gradient floats per image
+constexpr int kPWBuf = kPGs + kPImg;            // floats per W image buffer
+constexpr int kPImgs = 2;                       // images per W block (K slice)
+constexpr int kPMaxSide = 14;                   // largest image side (16 with the halo)
+
+struct PipeArgs {
+    // D blocks: out[n][m][y][x] = sum_{c,tap} Wt(m, c, tap) img[n][c][y+dy-1][x+dx-1]
+    //           (+ bias[m]) + beta * out
+    const float* dimg;   // [N][dC][H][W]
+    const float* dw;     // forward: [dM][dC][3][3]; input gradient: [dC][dM][3][3]
+    const float* dbias;  // [dM] or null
+    float* dout;         // [N][dM][H][W]
+    int dC, dM, nd;      // reduction channels, output channels, D blocks
+    float beta;
+    // W blocks: part_w[slice][m][tap][c] = sum over the slice's pixels of
+    //           g[n][m][y][x] * x[n][c][y+dy-1][x+dx-1]; part_b[slice][m] = sum g
+    const float* wx;     // [N][wC][H][W]
+    const float* wg;     // [N][wM][H][W]
+    float* part_w;
+    float* part_b;       // or null
+    int wC, wM, nw;      // input channels, output channels, W blocks
+    int N, H, W, P;
+};
+
+// Tap t of a 3x3 window as an offset in a staged plane.
+__device__ constexpr int tap_off(int t) { return (t / 3) * kPRow + t % 3; }
+
+// One padded image row (16 floats: halo, W values, zeros) for staging:
+// thread -> (plane p = tid >> 4, padded row y = tid & 15); loads of channel
+// `ch` of the image behind `r`, zero outside.
+struct RowStage {
+    f32x2 v[kPMaxSide / 2];
+    __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t r, int ch, int y, int H, int W) {
+        const bool ok = (y >= 1) & (y <= H);
+        const int src = (ch * H + y - 1) * W;
+#pragma unroll
+        for (int k = 0; k < kPMaxSide / 2; ++k)
+            v[k] = buffer_load2(r, (ok & (2 * k < W)) ? (src + 2 * k) * 4 : kOutOfRange);
+    }
+    __device__ __forceinline__ void store(float* dst) const {
+        *reinterpret_cast<f32x4*>(dst) = f32x4{0.0f, v[0][0], v[0][1], v[1][0]};
+        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{v[1][1], v[2][0], v[2][1], v[3][0]};
+        *reinterpret_cast<f32x4*>(dst + 8) = f32x4{v[3][1], v[4][0], v[4][1], v[5][0]};
+        *reinterpret_cast<f32x4*>(dst + 12) = f32x4{v[5][1], v[6][0], v[6][1], 0.0f};
+    }
+};
+
+// ---- D blocks -------------------------------------------------------------
+
+constexpr int kPWItems = kPMB * kPCC * 9 / 4;            // weight float4s per chunk (1152)
+constexpr int kPWSlots = (kPWItems + 255) / 256;         // per thread (5, the last partial)
+
+template <bool FLIP>
+struct WeightStage {
+    f32x4 v[kPWSlots];
+    // chunk j's weights of output channels m0 .. m0+31
+    __device__ __forceinline__ void issue(const PipeArgs& a, __amdgpu_buffer_rsrc_t r, int j, int m0,
+                                          int tid) {
+#pragma unroll
+        for (int i = 0; i < kPWSlots; ++i) {
+            const int e = tid + 256 * i;
+            int src;
+            if constexpr (!FLIP) {
+                // row m: the chunk's 144 floats w[m0+m][16j .. 16j+15][0..8]
+                const int m = e / 36, f = e - 36 * m;
+                src = ((m0 + m) * a.dC + kPCC * j) * 9 + 4 * f;
+            } else {
+                // oc = 16j + o: the 288 floats w[oc][m0 .. m0+31][0..8]
+                const int o = e / 72, f = e - 72 * o;
+                src = ((kPCC * j + o) * a.dM + m0) * 9 + 4 * f;
+            }
+            v[i] = buffer_load4(r, e < kPWItems ? src * 4 : kOutOfRange);
+        }
+    }
+    __device__ __forceinline__ void store(float* ws, int tid) const {
+#pragma unroll
+        for (int i = 0; i < kPWSlots; ++i) {
+            const int e = tid + 256 * i;
+            if (e >= kPWItems) continue;
+            if constexpr (!FLIP) {
+                const int m = e / 36, f = e - 36 * m;
+                *reinterpret_cast<f32x4*>(ws + m * kPWrow + 4 * f) = v[i];
+            } else {
+                // element u of the item is w[oc][m0 + c][tap] with 4f + u = 9c + tap;
+                // staged at row c, column 9*o + 8 - tap
+                const int o = e / 72, f = e - 72 * o;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int k = 4 * f + u;
+                    const int c = (k * 7282) >> 16;  // k / 9 for k < 32768
+                    const int tap = k - 9 * c;
+                    ws[c * kPWrow + 9 * o + 8 - tap] = v[i][u];
+                }
+            }
+        }
+    }
+};
+
+template <bool FLIP>
+__device__ __forceinline__ void pipe_d_block(const PipeArgs& a, int bid, float* lds) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane >> 4, l16 = lane & 15;
+    const int mblocks = a.dM / kPMB;
+    const int img = bid / mblocks, m0 = (bid - img * mblocks) * kPMB;
+    const int H = a.H, W = a.W, P = a.P, nch = a.dC / kPCC;
+
+    const auto rimg = buffer_rsrc(a.dimg + (int64_t)img * a.dC * P, (int64_t)a.dC * P * 4);
+    const auto rw = buffer_rsrc(a.dw, (int64_t)a.dC * a.dM * 9 * 4);
+    const int sp = tid >> 4, sy = tid & 15;
+    RowStage rs;
+    WeightStage<FLIP> wst;
+
+    // chunk 0 staged, chunk 1's loads in flight
+    rs.issue(rimg, sp, sy, H, W);
+    wst.issue(a, rw, 0, m0, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    rs.store(lds + sp * kPPlane + sy * kPRow);
+    wst.store(lds + kPImg, tid);
+    if (nch > 1) {
+        rs.issue(rimg, kPCC + sp, sy, H, W);
+        wst.issue(a, rw, 1, m0, tid);
+    }
+    __syncthreads();
+
+    const int mb = wave & 1, row0 = (wave >> 1) * 7;
+    int boff[7];
+#pragma unroll
+    for (int t = 0; t < 7; ++t) boff[t] = 4 * q * kPPlane + min(row0 + t, H - 1) * kPRow + l16;
+    const int aoff = kPImg + (mb * 16 + l16) * kPWrow + 36 * q;
+    f32x4 acc[7];
+#pragma unroll
+    for (int t = 0; t < 7; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int j = 0; j < nch; ++j) {
+        const float* cb = lds + (j & 1) * kPDBuf;
+        // 36 steps: step s of quarter q is channel 4q + s/9, tap s%9. The B
+        // values of step s+1 are read while step s's MFMAs run.
+        f32x4 av = *reinterpret_cast<const f32x4*>(cb + aoff);
+        float bv[7];
+#pragma unroll
+        for (int t = 0; t < 7; ++t) bv[t] = cb[boff[t]];
+        // The schedule is pinned per step: the next step's reads go one
+        // after each of this step's MFMAs, so the wave issues them while the
+        // matrix core is busy. Left alone, the compiler sinks every read to
+        // just before its MFMA and the LDS latency shows; issued as a block
+        // between MFMA groups, they leave the matrix core idle.
+#pragma unroll
+        for (int s = 0; s < 36; ++s) {
+            float bn[7];
+            f32x4 an = av;
+            if (s + 1 < 36) {
+                const int off = ((s + 1) / 9) * kPPlane + tap_off((s + 1) % 9);
+#pragma unroll
+                for (int t = 0; t < 7; ++t) bn[t] = cb[boff[t] + off];
+                if ((s + 1) % 4 == 0) an = *reinterpret_cast<const f32x4*>(cb + aoff + s + 1);
+            }
+#pragma unroll
+            for (int t = 0; t < 7; ++t)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s & 3], bv[t], acc[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 7; ++t) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 1 < 36) {
+#pragma unroll
+                for (int t = 0; t < 7; ++t) bv[t] = bn[t];
+                av = an;
+            }
+        }
+        if (j + 1 < nch) {
+            // the other buffer was last read by chunk j-1, which every wave
+            // finished before the previous barrier
+            float* nb = lds + ((j + 1) & 1) * kPDBuf;
+            rs.store(nb + sp * kPPlane + sy * kPRow);
+            wst.store(nb + kPImg, tid);
+            if (j + 2 < nch) {
+                rs.issue(rimg, kPCC * (j + 2) + sp, sy, H, W);
+                wst.issue(a, rw, j + 2, m0, tid);
+            }
+            __syncthreads();
+        }
+    }
+
+    // epilogue: lane holds D[m = 4q + r][column l16] of each row tile
+    float* oimg = a.dout + ((int64_t)img * a.dM + m0 + mb * 16 + 4 * q) * P;
+    float bias[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bias[r] = a.dbias ? a.dbias[m0 + mb * 16 + 4 * q + r] : 0.0f;
+    const bool colok = l16 < W;
+    if (a.beta != 0.0f) {
+        float old[7][4];
+#pragma unroll
+        for (int t = 0; t < 7; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int oy = row0 + t;
+                old[t][r] = (colok & (oy < H)) ? oimg[r * P + oy * W + l16] : 0.0f;
+            }
+#pragma unroll
+        for (int t = 0; t < 7; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int oy = row0 + t;
+                if (colok & (oy < H)) oimg[r * P + oy * W + l16] = acc[t][r] + bias[r] + a.beta * old[t][r];
+            }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 7; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int oy = row0 + t;
+                if (colok & (oy < H)) oimg[r * P + oy * W + l16] = acc[t][r] + bias[r];
+            }
+    }
+}
+
+// ---- W blocks -------------------------------------------------------------
+
+constexpr int kPGItems = kPWM * kPGrow / 4 * 4;    // gradient float4 slots per image (64 x 52)
+constexpr int kPGSlots = kPGItems / 256;           // 13 per thread
+
+struct GradStage {
+    f32x4 v[kPGSlots];
+    // item e = (oc, s'): g[n][m0 + oc][4s' .. 4s'+3], zero for s' >= P/4
+    __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t r, int img, int m0, int M, int P,
+                                          int tid) {
+        const int S4 = P >> 2;
+#pragma unroll
+        for (int i = 0; i < kPGSlots; ++i) {
+            const int e = tid + 256 * i;
+            const int oc = e / kPGrow, s = e - kPGrow * oc;
+            const int src = ((img * M + m0 + oc) * P + 4 * s) * 4;
+            v[i] = buffer_load4(r, s < S4 ? src : kOutOfRange);
+        }
+    }
+    // staged de-interleaved: gs[oc][q][s'] = g[oc][4s' + q]
+    __device__ __forceinline__ void store(float* gs, int tid) const {
+#pragma unroll
+        for (int i = 0; i < kPGSlots; ++i) {
+            const int e = tid + 256 * i;
+            const int oc = e / kPGrow, s = e - kPGrow * oc;
+            float* d = gs + oc * 4 * kPGrow + s;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) d[u * kPGrow] = v[i][u];
+        }
+    }
+};
+
+__device__ __forceinline__ void pipe_w_block(const PipeArgs& a, int bid, float* lds) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane >> 4, l16 = lane & 15;
+    const int cblocks = a.wC / kPCC, mblocks = a.wM / kPWM;
+    const int cblk = bid % cblocks, rest = bid / cblocks;
+    const int mblk = rest % mblocks, slice = rest / mblocks;
+    const int c0 = cblk * kPCC, m0 = mblk * kPWM;
+    const int img0 = slice * kPImgs, nimg = min(kPImgs, a.N - img0);
+    const int H = a.H, W = a.W, P = a.P;
+
+    // the slice's images as buffers (loads past the last image return zero)
+    const auto rg = buffer_rsrc(a.wg, (int64_t)a.N * a.wM * P * 4);
+    const auto rx = buffer_rsrc(a.wx + (int64_t)c0 * P, ((int64_t)a.N * a.wC - c0) * P * 4);
+    const int sp = tid >> 4, sy = tid & 15;
+    RowStage rs;
+    GradStage gst;
+    // input plane of channel c0 + sp of image n: plane n * wC + sp in rx
+    rs.issue(rx, img0 * a.wC + sp, sy, H, W);
+    gst.issue(rg, img0, m0, a.wM, P, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    rs.store(lds + kPGs + sp * kPPlane + sy * kPRow);
+    gst.store(lds, tid);
+    if (nimg > 1) {
+        rs.issue(rx, (img0 + 1) * a.wC + sp, sy, H, W);
+        gst.issue(rg, img0 + 1, m0, a.wM, P, tid);
+    }
+    // staged-plane offset of pixel 4s + q (clamped to the last pixel, whose
+    // gradient rows are zero past the image): table [q][s]
+    if (tid < 4 * kPGrow) {
+        const int tq = tid / kPGrow, ts = tid - kPGrow * tq;
+        const int p = min(4 * ts + tq, P - 1), y = p / W;
+        reinterpret_cast<int*>(lds + 2 * kPWBuf)[tid] = y * kPRow + (p - y * W);
+    }
+    __syncthreads();
+
+    const int gb = (16 * wave + l16) * 4 * kPGrow + q * kPGrow;
+    const int xb = kPGs + l16 * kPPlane;
+    const int* ptab = reinterpret_cast<const int*>(lds + 2 * kPWBuf) + q * kPGrow;
+    const int G = (P >> 2) >> 2, T = (P >> 2) & 3;  // whole groups of four steps, tail steps
+    f32x4 acc[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float bsum = 0.0f;
+
+    // One step: this step's nine MFMAs (A = av_u, B = bv), with the next
+    // step's nine B reads (at pixel offset pnext) placed one after each MFMA,
+    // so the wave issues them while the matrix core is busy.
+    auto step = [&](float av_u, float (&bv)[9], int pnext, const float* cb) {
+        float bn[9];
+#pragma unroll
+        for (int t = 0; t < 9; ++t) bn[t] = cb[xb + pnext + tap_off(t)];
+#pragma unroll
+        for (int t = 0; t < 9; ++t)
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av_u, bv[t], acc[t], 0, 0, 0);
+        bsum += av_u;
+#pragma unroll
+        for (int t = 0; t < 9; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < 9; ++t) bv[t] = bn[t];
+    };
+
+    for (int i = 0; i < nimg; ++i) {
+        const float* cb = lds + (i & 1) * kPWBuf;
+        // step s of quarter q is pixel 4s + q; its offset in a staged plane
+        // comes from the table, four steps per 128-bit read
+        i32x4 pc = *reinterpret_cast<const i32x4*>(ptab);
+        f32x4 av = *reinterpret_cast<const f32x4*>(cb + gb);
+        float bv[9];
+#pragma unroll
+        for (int t = 0; t < 9; ++t) bv[t] = cb[xb + pc[0] + tap_off(t)];
+        for (int g = 0; g < G; ++g) {
+            const int gn = min(g + 1, kPGrow / 4 - 1);
+            const f32x4 an = *reinterpret_cast<const f32x4*>(cb + gb + 4 * gn);
+            const i32x4 pn = *reinterpret_cast<const i32x4*>(ptab + 4 * gn);
+            step(av[0], bv, pc[1], cb);
+            step(av[1], bv, pc[2], cb);
+            step(av[2], bv, pc[3], cb);
+            step(av[3], bv, pn[0], cb);
+            av = an;
+            pc = pn;
+        }
+        // the last P/4 % 4 steps
+        if (T > 0) step(av[0], bv, pc[1], cb);
+        if (T > 1) step(av[1], bv, pc[2], cb);
+        if (T > 2) step(av[2], bv, pc[3], cb);
+        if (i + 1 < nimg) {
+            float* nb = lds + ((i + 1) & 1) * kPWBuf;
+            rs.store(nb + kPGs + sp * kPPlane + sy * kPRow);
+            gst.store(nb, tid);
+            if (i + 2 < nimg) {
+                rs.issue(rx, (img0 + i + 2) * a.wC + sp, sy, H, W);
+                gst.issue(rg, img0 + i + 2, m0, a.wM, P, tid);
+            }
+            __syncthreads();
+        }
+    }
+
+    // partials: lane holds D[oc = 4q + r][channel l16] of each tap
+    const int c = c0 + l16;
+#pragma unroll
+    for (int t = 0; t < 9; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 16 * wave + 4 * q + r;
+            a.part_w[(((int64_t)slice * a.wM + m) * 9 + t) * a.wC + c] = acc[t][r];
+        }
+    if (a.part_b && cblk == 0) {
+        bsum += __shfl_xor(bsum, 16);
+        bsum += __shfl_xor(bsum, 32);
+        if (q == 0) a.part_b[(int64_t)slice * a.wM + m0 + 16 * wave + l16] = bsum;
+    }
+}
+
+// W blocks first (ids [0, nw)), then D blocks.
+template <bool FLIP, bool HAS_W>
+__global__ __launch_bounds__(256) void conv_pipe_kernel(PipeArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const int bid = blockIdx.x;
+    if constexpr (HAS_W) {
+        if (bid < a.nw) {
+            pipe_w_block(a, bid, lds);
+            return;
+        }
+        pipe_d_block<FLIP>(a, bid - a.nw, lds);
+    } else {
+        pipe_d_block<FLIP>(a, bid, lds);
+    }
+}
+
+constexpr int kPipeLdsMax = 160 * 1024;
+
+template <bool FLIP, bool HAS_W>
+int launch_pipe(const PipeArgs& a) {
+    auto fn = conv_pipe_kernel<FLIP, HAS_W>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        NRS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, kPipeLdsMax));
+        attr_set = true;
+    }
+    // W blocks: two image buffers and the pixel-offset table
+    const size_t lds = sizeof(float) * (size_t)(a.nw > 0 ? std::max(2 * kPWBuf + 4 * kPGrow, 2 * kPDBuf)
+                                                         : 2 * kPDBuf);
+    hipLaunchKernelGGL(fn, dim3((unsigned)(a.nw + a.nd)), dim3(256), lds, stream(), a);
+    NRS_LAUNCH_CHECK("conv2d (chunk-pipelined)");
+    return NRS_OK;
+}
+
+// The shapes the kernel takes: "same" 3x3 stride 1 over images of at most
+// 14x14 with an even width of at least 4 and whole pixel quads.
+bool pipe_geometry(int kh, int kw, int stride, int pad_h, int pad_w, int H, int W, int OH, int OW) {
+    return kh == 3 && kw == 3 && stride == 1 && pad_h == 1 && pad_w == 1 && OH == H && OW == W &&
+           H >= 1 && H <= kPMaxSide && W >= 4 && W <= kPMaxSide && W % 2 == 0 && (H * W) % 4 == 0;
+}
+
+}  // namespace
+
+int pipe_conv(const SlabConv& s) {
+    if (!pipe_geometry(s.kh, s.kw, s.stride, s.pad_h, s.pad_w, s.H, s.W, s.OH, s.OW) ||
+        s.C % kPCC != 0 || s.C <= 0 || s.M % kPMB != 0 || s.M <= 0 || s.N <= 0 ||
+        s.N * (s.M / kPMB) > 0x7fffffff || s.N * (int64_t)std::max(s.C, s.M) * s.H * s.W > 0x1fffffff ||
+        ((uintptr_t)s.x & 7) != 0)
+        return kSlabUnsupported;
+    PipeArgs a{};
+    a.dimg = s.x;
+    a.dw = s.w;
+    a.dbias = s.bias;
+    a.dout = s.out;
+    a.dC = s.C;
+    a.dM = s.M;
+    a.nd = (int)(s.N * (s.M / kPMB));
+    a.beta = s.beta;
+    a.N = (int)s.N;
+    a.H = s.H;
+    a.W = s.W;
+    a.P = s.H * s.W;
+    return s.flip ? launch_pipe<true, false>(a) : launch_pipe<false, false>(a);
+}
+
+int pipe_backward(const SlabConv* d, const SlabWgrad& w) {
+    if (!pipe_geometry(w.kh, w.kw, w.stride, w.pad, w.pad, w.H, w.W, w.OH, w.OW) || !w.dw ||
+        w.C % kPMB != 0 || w.C <= 0 || w.M % kPWM != 0 || w.M <= 0 || w.N <= 0 ||
+        w.N * (int64_t)std::max(w.C, w.M) * w.H * w.W > 0x1fffffff || ((uintptr_t)w.x & 7) != 0 ||
+        ((uintptr_t)w.g & 15) != 0)
+        return kSlabUnsupported;
+    if (d && (d->x != w.g || d->C != w.M || d->M != w.C || !d->flip)) return kSlabUnsupported;
+    const int P = w.H * w.W;
+    const int64_t slices = (w.N + kPImgs - 1) / kPImgs;
+    const int64_t nw = slices * (w.C / kPCC) * (w.M / kPWM);
+    const int64_t nd = d ? w.N * (w.C / kPMB) : 0;
+    if (nw + nd > 0x7fffffff) return kSlabUnsupported;
+    const int64_t npw = (int64_t)w.M * 9 * w.C;
+    float* part = workspace(sizeof(float) * (size_t)(slices * (npw + w.M)), 3);
+    if (!part) return NRS_ERR_ALLOC;
+    PipeArgs a{};
+    if (d) {
+        a.dimg = d->x;
+        a.dw = d->w;
+        a.dout = d->out;
+        a.dC = d->C;
+        a.dM = d->M;
+        a.beta = d->beta;
+    }
+    a.nd = (int)nd;
+    a.wx = w.x;
+    a.wg = w.g;
+    a.part_w = part;
+    a.part_b = w.db ? part + slices * npw : nullptr;
+    a.wC = w.C;
+    a.wM = w.M;
+    a.nw = (int)nw;
+    a.N = (int)w.N;
+    a.H = w.H;
+    a.W = w.W;
+    a.P = P;
+    int rc = launch_pipe<true, true>(a);
+    if (rc) return rc;
+    return wgrad_partial_sum(w.dw, w.db, part, a.part_b, (int)slices, w.M, w.C, 9);
+}
+
+}  // namespace nrs

@@ -38,6 +38,12 @@ int slab_conv(const SlabConv& s);
 // (launching nothing) for other shapes.
 int img_conv(const SlabConv& s);
 
+// The same convolution, chunk-pipelined (conv_pipe.hip), for "same" 3x3
+// stride-1 layers over images of at most 14x14 (even width >= 4, whole pixel
+// quads) with C % 16 == 0 and M % 32 == 0; kSlabUnsupported (launching
+// nothing) for other shapes.
+int pipe_conv(const SlabConv& s);
+
 // Weight gradient dw[m][c][i][j] += sum g[n,m,oy,ox] * x[n,c,oy*s-pad+i,ox*s-pad+j]
 // and, when db is given, bias gradient db[m] += sum g[n,m,oy,ox], with
 // per-image partial sums added in a fixed order. dw is required; returns
@@ -57,6 +63,13 @@ int slab_wgrad(const SlabWgrad& s);
 // workgroups (then the weight gradient's partial sum). Returns
 // kSlabUnsupported (launching nothing) unless both fit their kernels.
 int slab_backward_pair(const SlabConv& d, const SlabWgrad& w);
+
+// The backward of a "same" 3x3 stride-1 layer in one chunk-pipelined launch
+// (conv_pipe.hip): the weight and bias gradient w (dw required) and, when d
+// is given, the input gradient d (a flipped convolution of w.g), then the
+// weight gradient's partial sum. Needs pipe_conv's geometry, C % 32 == 0 and
+// M % 64 == 0; returns kSlabUnsupported (launching nothing) otherwise.
+int pipe_backward(const SlabConv* d, const SlabWgrad& w);
 
 // Weight and bias gradient of a convolution with c_in*kh*kw <= 15 taps and at
 // most 64 output channels, on the matrix cores (conv_few_taps.hip): dw += and

@@ -50,6 +50,12 @@ CONV_SHAPES = [  # (n, c_in, c_out, h, w, kh, kw, stride, pad)
     (2, 32, 40, 14, 14, 3, 3, 1, 0),  # pad 0
     (2, 16, 8, 10, 10, 3, 3, 1, 2),   # pad 2
     (2, 16, 32, 12, 12, 3, 3, 1, 0),  # input gradient at pad 2
+    # chunk-pipelined "same" 3x3 kernels (images <= 14x14, even width, whole quads)
+    (2, 64, 64, 14, 12, 3, 3, 1, 1),  # two input-gradient blocks, four weight-gradient channel blocks
+    (5, 32, 128, 8, 6, 3, 3, 1, 1),   # two weight-gradient channel blocks, odd batch (a 1-image slice)
+    (2, 96, 64, 10, 10, 3, 3, 1, 1),  # three output blocks each way, six forward chunks
+    (3, 16, 64, 4, 4, 3, 3, 1, 1),    # forward only (16 input channels), one row tile per wave
+    (1, 32, 64, 2, 8, 3, 3, 1, 1),    # two rows: most row tiles clamped
 ]
 ids = ["x".join(map(str, s)) for s in CONV_SHAPES]
 
