@@ -212,9 +212,13 @@ __global__ __launch_bounds__(256) void conv_fwd_direct_kernel(
 // sum order as conv_fwd_direct_kernel: taps in (ic, i, j) order from zero,
 // then + bias.
 constexpr int kQuadOc = 8;
+// Threads per workgroup of the pixel-quad forward: one wave, so the grid
+// spreads evenly over the CUs (cfg3 conv1: 1568 workgroups, ~6 per CU; in
+// workgroups of 256 threads, 392 of them left 136 CUs with twice the work).
+constexpr int kQuadThreads = 64;
 
 template <int CIN>
-__global__ __launch_bounds__(256) void conv_fwd_quad_kernel(
+__global__ __launch_bounds__(kQuadThreads) void conv_fwd_quad_kernel(
     float* __restrict__ out, const float* __restrict__ input, const float* __restrict__ weight,
     const float* __restrict__ bias, int N, int H, int W, int c_out, FastDiv div_qimg,
     FastDiv div_qrow) {
@@ -224,7 +228,7 @@ __global__ __launch_bounds__(256) void conv_fwd_quad_kernel(
     const int tid = threadIdx.x;
     const int P = H * W, oc0 = blockIdx.y * kQuadOc;
     const int64_t quads = (int64_t)N * (P >> 2);
-    const int g = blockIdx.x * 256 + tid;
+    const int g = blockIdx.x * kQuadThreads + tid;
     const bool valid = g < quads;
     uint32_t n, qq, oy, qx;
     fast_divmod((uint32_t)(valid ? g : 0), div_qimg, n, qq);
@@ -245,19 +249,19 @@ __global__ __launch_bounds__(256) void conv_fwd_quad_kernel(
         for (int u = 0; u < 4; ++u) seg[r][1 + u] = mid[u];
     }
     // this block's weights (zero past c_out) and biases
-    constexpr int WN = kQuadOc * TAPS, WPT = (WN + 255) / 256;
+    constexpr int WN = kQuadOc * TAPS, WPT = (WN + kQuadThreads - 1) / kQuadThreads;
     const auto rw = buffer_rsrc(weight, (int64_t)c_out * TAPS * 4);
     const auto rb = buffer_rsrc(bias ? bias : weight, bias ? (int64_t)c_out * 4 : 0);
     float wv[WPT];
 #pragma unroll
     for (int k = 0; k < WPT; ++k) {
-        const int e = tid + 256 * k;
+        const int e = tid + kQuadThreads * k;
         wv[k] = buffer_load1(rw, e < WN ? (oc0 * TAPS + e) * 4 : kOutOfRange);
     }
     const float bv = buffer_load1(rb, tid < kQuadOc ? (oc0 + tid) * 4 : kOutOfRange);
 #pragma unroll
     for (int k = 0; k < WPT; ++k)
-        if (tid + 256 * k < WN) (&wsh[0][0])[tid + 256 * k] = wv[k];
+        if (tid + kQuadThreads * k < WN) (&wsh[0][0])[tid + kQuadThreads * k] = wv[k];
     if (tid < kQuadOc) bsh[tid] = bv;
     __syncthreads();
     if (!valid) return;
@@ -1452,9 +1456,9 @@ int nrs_conv2d_forward(float* out, const float* input, const float* weight, cons
             auto fn = c_in == 1 ? nrs::conv_fwd_quad_kernel<1>
                                 : (c_in == 2 ? nrs::conv_fwd_quad_kernel<2>
                                              : nrs::conv_fwd_quad_kernel<3>);
-            hipLaunchKernelGGL(fn, dim3((unsigned)((quads + 255) / 256),
+            hipLaunchKernelGGL(fn, dim3((unsigned)((quads + nrs::kQuadThreads - 1) / nrs::kQuadThreads),
                                         (unsigned)((c_out + nrs::kQuadOc - 1) / nrs::kQuadOc)),
-                               dim3(256), 0, nrs::stream(), out, input, weight, bias, (int)N,
+                               dim3(nrs::kQuadThreads), 0, nrs::stream(), out, input, weight, bias, (int)N,
                                (int)in_h, (int)in_w, (int)c_out,
                                nrs::make_fastdiv((uint32_t)(P / 4)),
                                nrs::make_fastdiv((uint32_t)(in_w / 4)));

@@ -181,6 +181,9 @@ __device__ __forceinline__ void pipe_d_block(const PipeArgs& a, int bid, float* 
 #pragma unroll
     for (int t = 0; t < 7; ++t) boff[t] = 4 * q * kPPlane + min(row0 + t, H - 1) * kPRow + l16;
     const int aoff = kPImg + (mb * 16 + l16) * kPWrow + 36 * q;
+    float bias[4];  // loaded now, used in the epilogue
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bias[r] = a.dbias ? a.dbias[m0 + mb * 16 + 4 * q + r] : 0.0f;
     f32x4 acc[7];
 #pragma unroll
     for (int t = 0; t < 7; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -238,36 +241,46 @@ __device__ __forceinline__ void pipe_d_block(const PipeArgs& a, int bid, float* 
         }
     }
 
-    // epilogue: lane holds D[m = 4q + r][column l16] of each row tile
-    float* oimg = a.dout + ((int64_t)img * a.dM + m0 + mb * 16 + 4 * q) * P;
-    float bias[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) bias[r] = a.dbias ? a.dbias[m0 + mb * 16 + 4 * q + r] : 0.0f;
-    const bool colok = l16 < W;
+    // epilogue: lane holds D[m = 4q + r][column l16] of each row tile. The
+    // block's [32][P] output goes through the chunk buffer the last chunk did
+    // not use (every wave finished reading it before the last barrier), so it
+    // leaves as 128-bit stores of contiguous channel rows; + bias on the way
+    // in, + beta * old on the way out (old values loaded before the round trip).
+    float* ot = lds + (nch & 1) * kPDBuf;
+    float* oimg = a.dout + ((int64_t)img * a.dM + m0) * P;
+    const int P4 = P >> 2, total = kPMB * P4;
+    constexpr int kOV = (kPMB * kPMaxSide * kPMaxSide / 4 + 255) / 256;  // float4s per thread
+    // e / P4 as a multiply-shift: exact for e < 2^11, P4 <= 49
+    const uint32_t p4inv = ((1u << 20) + P4 - 1) / P4;
+    f32x4 old[kOV];
     if (a.beta != 0.0f) {
-        float old[7][4];
 #pragma unroll
-        for (int t = 0; t < 7; ++t)
+        for (int u = 0; u < kOV; ++u) {
+            const int e = tid + 256 * u;
+            const int m = (int)(((uint32_t)e * p4inv) >> 20), p4 = e - m * P4;
+            old[u] = e < total ? *reinterpret_cast<const f32x4*>(oimg + (int64_t)m * P + 4 * p4)
+                               : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    if (l16 < W) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int oy = row0 + t;
-                old[t][r] = (colok & (oy < H)) ? oimg[r * P + oy * W + l16] : 0.0f;
+        for (int t = 0; t < 7; ++t) {
+            const int oy = row0 + t;
+            if (oy < H) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ot[(mb * 16 + 4 * q + r) * P + oy * W + l16] = acc[t][r] + bias[r];
             }
+        }
+    }
+    __syncthreads();
 #pragma unroll
-        for (int t = 0; t < 7; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int oy = row0 + t;
-                if (colok & (oy < H)) oimg[r * P + oy * W + l16] = acc[t][r] + bias[r] + a.beta * old[t][r];
-            }
-    } else {
-#pragma unroll
-        for (int t = 0; t < 7; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int oy = row0 + t;
-                if (colok & (oy < H)) oimg[r * P + oy * W + l16] = acc[t][r] + bias[r];
-            }
+    for (int u = 0; u < kOV; ++u) {
+        const int e = tid + 256 * u;
+        if (e >= total) continue;
+        const int m = (int)(((uint32_t)e * p4inv) >> 20), p4 = e - m * P4;
+        f32x4 v = *reinterpret_cast<const f32x4*>(ot + m * P + 4 * p4);
+        if (a.beta != 0.0f) v = v + a.beta * old[u];
+        *reinterpret_cast<f32x4*>(oimg + (int64_t)m * P + 4 * p4) = v;
     }
 }
 
@@ -469,7 +482,7 @@ int pipe_conv(const SlabConv& s) {
     if (!pipe_geometry(s.kh, s.kw, s.stride, s.pad_h, s.pad_w, s.H, s.W, s.OH, s.OW) ||
         s.C % kPCC != 0 || s.C <= 0 || s.M % kPMB != 0 || s.M <= 0 || s.N <= 0 ||
         s.N * (s.M / kPMB) > 0x7fffffff || s.N * (int64_t)std::max(s.C, s.M) * s.H * s.W > 0x1fffffff ||
-        ((uintptr_t)s.x & 7) != 0)
+        ((uintptr_t)s.x & 7) != 0 || ((uintptr_t)s.out & 15) != 0)
         return kSlabUnsupported;
     PipeArgs a{};
     a.dimg = s.x;
@@ -493,7 +506,8 @@ int pipe_backward(const SlabConv* d, const SlabWgrad& w) {
         w.N * (int64_t)std::max(w.C, w.M) * w.H * w.W > 0x1fffffff || ((uintptr_t)w.x & 7) != 0 ||
         ((uintptr_t)w.g & 15) != 0)
         return kSlabUnsupported;
-    if (d && (d->x != w.g || d->C != w.M || d->M != w.C || !d->flip)) return kSlabUnsupported;
+    if (d && (d->x != w.g || d->C != w.M || d->M != w.C || !d->flip || ((uintptr_t)d->out & 15) != 0))
+        return kSlabUnsupported;
     const int P = w.H * w.W;
     const int64_t slices = (w.N + kPImgs - 1) / kPImgs;
     const int64_t nw = slices * (w.C / kPCC) * (w.M / kPWM);
