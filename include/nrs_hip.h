@@ -287,6 +287,17 @@ int nrs_conv2d_backward_beta(float *dinput, float *dweight, float *dbias,
                              int64_t N, int64_t c_in, int64_t in_h, int64_t in_w,
                              int64_t c_out, int64_t kh, int64_t kw, int64_t stride,
                              int64_t pad, float beta_input);
+/* nrs_conv2d_backward_beta whose weight and bias gradients are likewise
+ * dweight = gradient + beta_params * dweight (and dbias): 1 accumulates as
+ * the reference does (conv.rs:314-322 into accumulate_into); 0 writes them
+ * without reading the old values, for gradients that were just zeroed
+ * (runtime.rs:108-117 zero_grad) and so need no clearing launch. Same
+ * kernels and sums as nrs_conv2d_backward; no counterpart in the reference. */
+int nrs_conv2d_backward_ex(float *dinput, float *dweight, float *dbias,
+                           const float *grad, const float *input, const float *weight,
+                           int64_t N, int64_t c_in, int64_t in_h, int64_t in_w,
+                           int64_t c_out, int64_t kh, int64_t kw, int64_t stride,
+                           int64_t pad, float beta_input, float beta_params);
 
 /* nn::conv2d followed by max pooling (src/cuda/nn/conv.rs:244-277, then
  * src/cuda/nn/maxpool.rs:18-46 on the conv output) in one call: pooled
@@ -316,6 +327,30 @@ int nrs_maxpool_conv2d_backward(float *dinput, float *dweight, float *dbias,
                                 const float *input, const float *weight, int64_t N, int64_t c_in,
                                 int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
                                 int64_t stride, int64_t pad, int64_t pool_k, int64_t pool_stride);
+
+/* The same two calls with a ReLU between the conv and the pooling, the
+ * reference CNN's maxpool2d(relu(conv2d(..)), 2, 2)
+ * (examples/mnist_cuda_cnn.rs:125,127; src/cuda/graph/relu.rs:16-28 between
+ * conv.rs:244-277 and maxpool.rs:18-46): pooled and argmax are the pooling of
+ * relu(conv output), first maximum wins (windows of zeros keep their first
+ * element); out, when non-NULL, receives the conv output before the ReLU.
+ * The backward's relu_grad test (conv value > 0) is taken from the pooled
+ * value at each window's argmax, which is that conv value's ReLU: pass the
+ * forward's pooled output. Same single-launch shapes as above. dinput
+ * accumulates; dweight and dbias take beta_params as nrs_conv2d_backward_ex
+ * does (1 accumulates).                                                     */
+int nrs_conv2d_relu_maxpool_forward(float *pooled, int32_t *argmax, float *out,
+                                    const float *input, const float *weight, const float *bias,
+                                    int64_t N, int64_t c_in, int64_t in_h, int64_t in_w,
+                                    int64_t c_out, int64_t kh, int64_t kw, int64_t stride,
+                                    int64_t pad, int64_t pool_k, int64_t pool_stride);
+int nrs_maxpool_relu_conv2d_backward(float *dinput, float *dweight, float *dbias,
+                                     const float *grad_pooled, const int32_t *argmax,
+                                     const float *pooled, const float *input, const float *weight,
+                                     int64_t N, int64_t c_in, int64_t in_h, int64_t in_w,
+                                     int64_t c_out, int64_t kh, int64_t kw, int64_t stride,
+                                     int64_t pad, int64_t pool_k, int64_t pool_stride,
+                                     float beta_params);
 
 /* ------------------------------------------------------ gradient plumbing */
 /* accumulate (src/cuda/runtime.rs:13-19): acc[i] += src[i].                  */

@@ -67,8 +67,11 @@ SIGNATURES = {
     "nrs_conv2d_forward": [_P, _P, _P, _P] + [_I] * 9,
     "nrs_conv2d_backward": [_P, _P, _P, _P, _P, _P] + [_I] * 9,
     "nrs_conv2d_backward_beta": [_P, _P, _P, _P, _P, _P] + [_I] * 9 + [_F],
+    "nrs_conv2d_backward_ex": [_P, _P, _P, _P, _P, _P] + [_I] * 9 + [_F, _F],
     "nrs_conv2d_maxpool_forward": [_P, _P, _P, _P, _P, _P] + [_I] * 11,
     "nrs_maxpool_conv2d_backward": [_P, _P, _P, _P, _P, _P, _P] + [_I] * 11,
+    "nrs_conv2d_relu_maxpool_forward": [_P, _P, _P, _P, _P, _P] + [_I] * 11,
+    "nrs_maxpool_relu_conv2d_backward": [_P, _P, _P, _P, _P, _P, _P, _P] + [_I] * 11 + [_F],
     "nrs_accumulate": [_P, _P, _I],
     "nrs_vadd": [_P, _P, _P, _I],
     "nrs_bias_add": [_P, _P, _P, _I, _I],

@@ -295,10 +295,10 @@ __global__ __launch_bounds__(kQuadThreads) void conv_fwd_quad_kernel(
 // The conv output is written only when out is set; the pooled values and
 // indices leave as 64-bit stores.
 template <int CIN>
-__global__ __launch_bounds__(256) void conv_fwd_pool_quad_kernel(
+__global__ __launch_bounds__(kQuadThreads) void conv_fwd_pool_quad_kernel(
     float* __restrict__ pooled, int32_t* __restrict__ argmax, float* __restrict__ out,
     const float* __restrict__ input, const float* __restrict__ weight,
-    const float* __restrict__ bias, int N, int H, int W, int c_out, FastDiv div_bimg,
+    const float* __restrict__ bias, int N, int H, int W, int c_out, int relu, FastDiv div_bimg,
     FastDiv div_brow) {
     constexpr int ROWS = 4 * CIN, TAPS = 9 * CIN;
     __shared__ __attribute__((aligned(16))) float wsh[kQuadOc][TAPS];
@@ -306,7 +306,7 @@ __global__ __launch_bounds__(256) void conv_fwd_pool_quad_kernel(
     const int tid = threadIdx.x;
     const int P = H * W, PW = W >> 1, PP = (H >> 1) * PW, oc0 = blockIdx.y * kQuadOc;
     const int64_t blocks = (int64_t)N * (H >> 1) * (W >> 2);
-    const int g = blockIdx.x * 256 + tid;
+    const int g = blockIdx.x * kQuadThreads + tid;
     const bool valid = g < blocks;
     uint32_t n, qq, py, qx;
     fast_divmod((uint32_t)(valid ? g : 0), div_bimg, n, qq);
@@ -326,19 +326,19 @@ __global__ __launch_bounds__(256) void conv_fwd_pool_quad_kernel(
 #pragma unroll
         for (int u = 0; u < 4; ++u) seg[r][1 + u] = mid[u];
     }
-    constexpr int WN = kQuadOc * TAPS, WPT = (WN + 255) / 256;
+    constexpr int WN = kQuadOc * TAPS, WPT = (WN + kQuadThreads - 1) / kQuadThreads;
     const auto rw = buffer_rsrc(weight, (int64_t)c_out * TAPS * 4);
     const auto rb = buffer_rsrc(bias ? bias : weight, bias ? (int64_t)c_out * 4 : 0);
     float wv[WPT];
 #pragma unroll
     for (int k = 0; k < WPT; ++k) {
-        const int e = tid + 256 * k;
+        const int e = tid + kQuadThreads * k;
         wv[k] = buffer_load1(rw, e < WN ? (oc0 * TAPS + e) * 4 : kOutOfRange);
     }
     const float bv = buffer_load1(rb, tid < kQuadOc ? (oc0 + tid) * 4 : kOutOfRange);
 #pragma unroll
     for (int k = 0; k < WPT; ++k)
-        if (tid + 256 * k < WN) (&wsh[0][0])[tid + 256 * k] = wv[k];
+        if (tid + kQuadThreads * k < WN) (&wsh[0][0])[tid + kQuadThreads * k] = wv[k];
     if (tid < kQuadOc) bsh[tid] = bv;
     __syncthreads();
     if (!valid) return;
@@ -364,15 +364,25 @@ __global__ __launch_bounds__(256) void conv_fwd_pool_quad_kernel(
         const f32x4 v0 = a0 + b, v1 = a1 + b;
         const int plane = ((int)n * c_out + oc0 + oc) * P;
         const int e00 = plane + oy * W + ox;  // flat index of (oy, ox)
+        // the pooled values: of relu(conv) when a ReLU sits between the two
+        // (vrelu's x > 0 ? x : 0), else of the conv values
+        f32x4 r0 = v0, r1 = v1;
+        if (relu) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                r0[u] = v0[u] > 0.0f ? v0[u] : 0.0f;
+                r1[u] = v1[u] > 0.0f ? v1[u] : 0.0f;
+            }
+        }
         f32x2 pv;
         int32_t pi[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {  // windows of columns 2h, 2h + 1
-            float best = v0[2 * h];
+            float best = r0[2 * h];
             int bi = e00 + 2 * h;
-            if (v0[2 * h + 1] > best) { best = v0[2 * h + 1]; bi = e00 + 2 * h + 1; }
-            if (v1[2 * h] > best) { best = v1[2 * h]; bi = e00 + W + 2 * h; }
-            if (v1[2 * h + 1] > best) { best = v1[2 * h + 1]; bi = e00 + W + 2 * h + 1; }
+            if (r0[2 * h + 1] > best) { best = r0[2 * h + 1]; bi = e00 + 2 * h + 1; }
+            if (r1[2 * h] > best) { best = r1[2 * h]; bi = e00 + W + 2 * h; }
+            if (r1[2 * h + 1] > best) { best = r1[2 * h + 1]; bi = e00 + W + 2 * h + 1; }
             pv[h] = best;
             pi[h] = bi;
         }
@@ -1207,7 +1217,7 @@ int small_dgrad(float* dinput, const float* grad, const float* weight, const Con
 // dweight += and dbias += (either may be null) for a layer with c_in*kh*kw <=
 // kDirectTaps: per-image sums, then a fixed-order sum over the images.
 int small_wgrad(float* dweight, float* dbias, const float* grad, const float* input,
-                const ConvDims& d) {
+                const ConvDims& d, float beta) {
     const int64_t taps = d.c_in * d.kh * d.kw, P = d.out_h * d.out_w;
     if (d.N * P == 0) return NRS_OK;
     const int ocw = taps <= 9 ? 4 : (taps <= 16 ? 2 : 1);
@@ -1230,7 +1240,7 @@ int small_wgrad(float* dweight, float* dbias, const float* grad, const float* in
     NRS_LAUNCH_CHECK("conv2d weight gradient (small)");
     // the per-image partials are [n][oc][taps]: the slab layout with one
     // channel of `taps` taps; weights and bias summed in one launch
-    return wgrad_partial_sum(dweight, dbias, pw, pb, (int)d.N, (int)d.c_out, 1, (int)taps);
+    return wgrad_partial_sum(dweight, dbias, pw, pb, (int)d.N, (int)d.c_out, 1, (int)taps, beta);
 }
 
 // dinput += the stride-1 input gradient as a slab convolution of the output
@@ -1333,10 +1343,16 @@ int nrs_conv2d_bias_grad(float* dbias, const float* grad, int64_t N, int64_t c_o
     return nrs::bias_grad_launch(dbias, grad, N, c_out, out_h * out_w, beta);
 }
 
-int nrs_conv2d_maxpool_forward(float* pooled, int32_t* argmax, float* out, const float* input,
-                               const float* weight, const float* bias, int64_t N, int64_t c_in,
-                               int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
-                               int64_t stride, int64_t pad, int64_t pool_k, int64_t pool_stride) {
+}  // extern "C"
+
+namespace nrs {
+namespace {
+
+// conv2d (+ ReLU when relu) + max pooling, the forward of both fused entry points.
+int conv_pool_forward(float* pooled, int32_t* argmax, float* out, const float* input,
+                      const float* weight, const float* bias, int64_t N, int64_t c_in, int64_t in_h,
+                      int64_t in_w, int64_t c_out, int64_t kh, int64_t kw, int64_t stride,
+                      int64_t pad, int64_t pool_k, int64_t pool_stride, bool relu) {
     NRS_REQUIRE_INIT();
     nrs::ConvDims d;
     int rc = nrs::conv_dims(d, N, c_in, in_h, in_w, c_out, kh, kw, stride, pad);
@@ -1357,33 +1373,42 @@ int nrs_conv2d_maxpool_forward(float* pooled, int32_t* argmax, float* out, const
         auto fn = c_in == 1 ? nrs::conv_fwd_pool_quad_kernel<1>
                             : (c_in == 2 ? nrs::conv_fwd_pool_quad_kernel<2>
                                          : nrs::conv_fwd_pool_quad_kernel<3>);
-        hipLaunchKernelGGL(fn, dim3((unsigned)((blocks + 255) / 256),
+        hipLaunchKernelGGL(fn, dim3((unsigned)((blocks + nrs::kQuadThreads - 1) / nrs::kQuadThreads),
                                     (unsigned)((c_out + nrs::kQuadOc - 1) / nrs::kQuadOc)),
-                           dim3(256), 0, nrs::stream(), pooled, argmax, out, input, weight, bias,
-                           (int)N, (int)in_h, (int)in_w, (int)c_out,
+                           dim3(nrs::kQuadThreads), 0, nrs::stream(), pooled, argmax, out, input,
+                           weight, bias, (int)N, (int)in_h, (int)in_w, (int)c_out, relu ? 1 : 0,
                            nrs::make_fastdiv((uint32_t)((in_h / 2) * (in_w / 4))),
                            nrs::make_fastdiv((uint32_t)(in_w / 4)));
         NRS_LAUNCH_CHECK("conv2d + maxpool forward (pixel blocks)");
         return NRS_OK;
     }
     // any other shape: the conv output (the caller's, else library scratch),
-    // then the pooling
+    // its ReLU (in scratch), then the pooling
+    const int64_t conv_elems = N * c_out * d.out_h * d.out_w;
     float* y = out;
     if (!y) {
-        y = nrs::workspace(sizeof(float) * (size_t)(N * c_out * d.out_h * d.out_w), 5);
+        y = nrs::workspace(sizeof(float) * (size_t)conv_elems, 5);
         if (!y) return NRS_ERR_ALLOC;
     }
     rc = nrs_conv2d_forward(y, input, weight, bias, N, c_in, in_h, in_w, c_out, kh, kw, stride, pad);
     if (rc) return rc;
-    return nrs_maxpool_forward(pooled, argmax, y, N, c_out, d.out_h, d.out_w, pool_k, pool_stride);
+    const float* a = y;
+    if (relu) {
+        float* r = out ? nrs::workspace(sizeof(float) * (size_t)conv_elems, 5) : y;
+        if (!r) return NRS_ERR_ALLOC;
+        if ((rc = nrs_relu_forward(r, y, conv_elems))) return rc;
+        a = r;
+    }
+    return nrs_maxpool_forward(pooled, argmax, a, N, c_out, d.out_h, d.out_w, pool_k, pool_stride);
 }
 
-int nrs_maxpool_conv2d_backward(float* dinput, float* dweight, float* dbias,
-                                const float* grad_pooled, const int32_t* argmax,
-                                const float* input, const float* weight, int64_t N, int64_t c_in,
-                                int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
-                                int64_t stride, int64_t pad, int64_t pool_k,
-                                int64_t pool_stride) {
+// The backward of max pooling (over a ReLU of the conv output when pooled is
+// given: its values gate each window's gradient) then the conv backward.
+int pool_conv_backward(float* dinput, float* dweight, float* dbias, const float* grad_pooled,
+                       const int32_t* argmax, const float* pooled, const float* input,
+                       const float* weight, int64_t N, int64_t c_in, int64_t in_h, int64_t in_w,
+                       int64_t c_out, int64_t kh, int64_t kw, int64_t stride, int64_t pad,
+                       int64_t pool_k, int64_t pool_stride, float beta_params) {
     NRS_REQUIRE_INIT();
     nrs::ConvDims d;
     int rc = nrs::conv_dims(d, N, c_in, in_h, in_w, c_out, kh, kw, stride, pad);
@@ -1404,6 +1429,8 @@ int nrs_maxpool_conv2d_backward(float* dinput, float* dweight, float* dbias,
         f.g = nullptr;
         f.gp = grad_pooled;
         f.am = argmax;
+        f.pv = pooled;
+        f.beta = beta_params;
         f.dw = dweight;
         f.db = dbias;
         f.N = N;
@@ -1419,6 +1446,16 @@ int nrs_maxpool_conv2d_backward(float* dinput, float* dweight, float* dbias,
         f.OW = (int)d.out_w;
         if ((rc = nrs::few_taps_wgrad(f)) != nrs::kSlabUnsupported) return rc;
     }
+    if (pooled) {
+        // the ReLU's gate applied to the pooled gradient: a window passes its
+        // gradient only when its pooled value is > 0
+        const int64_t np = N * c_out * ((d.out_h - pool_k) / pool_stride + 1) *
+                           ((d.out_w - pool_k) / pool_stride + 1);
+        float* gm = nrs::workspace(sizeof(float) * (size_t)std::max<int64_t>(1, np), 6);
+        if (!gm) return NRS_ERR_ALLOC;
+        if ((rc = nrs_relu_backward(gm, grad_pooled, pooled, np, 0.0f))) return rc;
+        grad_pooled = gm;
+    }
     // any other case: the conv output's gradient in library scratch (the
     // pooling's backward into zeros), then the conv backward
     float* g = nrs::workspace(sizeof(float) * (size_t)conv_elems, 5);
@@ -1427,8 +1464,54 @@ int nrs_maxpool_conv2d_backward(float* dinput, float* dweight, float* dbias,
     rc = nrs_maxpool_backward(g, grad_pooled, argmax, N, c_out, d.out_h, d.out_w, pool_k,
                               pool_stride);
     if (rc) return rc;
-    return nrs_conv2d_backward(dinput, dweight, dbias, g, input, weight, N, c_in, in_h, in_w,
-                               c_out, kh, kw, stride, pad);
+    return nrs_conv2d_backward_ex(dinput, dweight, dbias, g, input, weight, N, c_in, in_h, in_w,
+                                  c_out, kh, kw, stride, pad, 1.0f, beta_params);
+}
+
+}  // namespace
+}  // namespace nrs
+
+extern "C" {
+
+int nrs_conv2d_maxpool_forward(float* pooled, int32_t* argmax, float* out, const float* input,
+                               const float* weight, const float* bias, int64_t N, int64_t c_in,
+                               int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
+                               int64_t stride, int64_t pad, int64_t pool_k, int64_t pool_stride) {
+    return nrs::conv_pool_forward(pooled, argmax, out, input, weight, bias, N, c_in, in_h, in_w,
+                                  c_out, kh, kw, stride, pad, pool_k, pool_stride, false);
+}
+
+int nrs_conv2d_relu_maxpool_forward(float* pooled, int32_t* argmax, float* out,
+                                    const float* input, const float* weight, const float* bias,
+                                    int64_t N, int64_t c_in, int64_t in_h, int64_t in_w,
+                                    int64_t c_out, int64_t kh, int64_t kw, int64_t stride,
+                                    int64_t pad, int64_t pool_k, int64_t pool_stride) {
+    return nrs::conv_pool_forward(pooled, argmax, out, input, weight, bias, N, c_in, in_h, in_w,
+                                  c_out, kh, kw, stride, pad, pool_k, pool_stride, true);
+}
+
+int nrs_maxpool_conv2d_backward(float* dinput, float* dweight, float* dbias,
+                                const float* grad_pooled, const int32_t* argmax,
+                                const float* input, const float* weight, int64_t N, int64_t c_in,
+                                int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
+                                int64_t stride, int64_t pad, int64_t pool_k,
+                                int64_t pool_stride) {
+    return nrs::pool_conv_backward(dinput, dweight, dbias, grad_pooled, argmax, nullptr, input,
+                                   weight, N, c_in, in_h, in_w, c_out, kh, kw, stride, pad, pool_k,
+                                   pool_stride, 1.0f);
+}
+
+int nrs_maxpool_relu_conv2d_backward(float* dinput, float* dweight, float* dbias,
+                                     const float* grad_pooled, const int32_t* argmax,
+                                     const float* pooled, const float* input, const float* weight,
+                                     int64_t N, int64_t c_in, int64_t in_h, int64_t in_w,
+                                     int64_t c_out, int64_t kh, int64_t kw, int64_t stride,
+                                     int64_t pad, int64_t pool_k, int64_t pool_stride,
+                                     float beta_params) {
+    NRS_ARG_CHECK(pooled || N * c_out == 0, "maxpool relu conv2d backward: null pooled values");
+    return nrs::pool_conv_backward(dinput, dweight, dbias, grad_pooled, argmax, pooled, input,
+                                   weight, N, c_in, in_h, in_w, c_out, kh, kw, stride, pad, pool_k,
+                                   pool_stride, beta_params);
 }
 
 int nrs_conv2d_forward(float* out, const float* input, const float* weight, const float* bias,
@@ -1556,6 +1639,14 @@ int nrs_conv2d_backward_beta(float* dinput, float* dweight, float* dbias, const 
                              const float* input, const float* weight, int64_t N, int64_t c_in,
                              int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
                              int64_t stride, int64_t pad, float beta_input) {
+    return nrs_conv2d_backward_ex(dinput, dweight, dbias, grad, input, weight, N, c_in, in_h, in_w,
+                                  c_out, kh, kw, stride, pad, beta_input, 1.0f);
+}
+
+int nrs_conv2d_backward_ex(float* dinput, float* dweight, float* dbias, const float* grad,
+                           const float* input, const float* weight, int64_t N, int64_t c_in,
+                           int64_t in_h, int64_t in_w, int64_t c_out, int64_t kh, int64_t kw,
+                           int64_t stride, int64_t pad, float beta_input, float beta_params) {
     NRS_REQUIRE_INIT();
     nrs::ConvDims d;
     int rc = nrs::conv_dims(d, N, c_in, in_h, in_w, c_out, kh, kw, stride, pad);
@@ -1586,6 +1677,7 @@ int nrs_conv2d_backward_beta(float* dinput, float* dweight, float* dbias, const 
         w.pad = (int)pad;
         w.OH = (int)d.out_h;
         w.OW = (int)d.out_w;
+        w.beta = beta_params;
     }
     bool wgrad_done = false;
     if (dinput) {
@@ -1667,8 +1759,9 @@ int nrs_conv2d_backward_beta(float* dinput, float* dweight, float* dbias, const 
         f.pad = (int)pad;
         f.OH = (int)d.out_h;
         f.OW = (int)d.out_w;
+        f.beta = beta_params;
         if ((rc = nrs::few_taps_wgrad(f)) != nrs::kSlabUnsupported) return rc;
-        return nrs::small_wgrad(dweight, dbias, grad, input, d);
+        return nrs::small_wgrad(dweight, dbias, grad, input, d, beta_params);
     }
     if (slab_w) {
         // input slab and gradient rows staged in LDS, reduction on the matrix
@@ -1692,7 +1785,7 @@ int nrs_conv2d_backward_beta(float* dinput, float* dweight, float* dbias, const 
         c.M = c_out;
         c.N = col_h;
         c.K = width;
-        c.beta = 1.0f;
+        c.beta = beta_params;
         const int64_t grad_bytes = N * c_out * P * (int64_t)sizeof(float);
         if (grad_bytes <= nrs::kMaxGatherBytes) {
             c.A = grad;
@@ -1711,7 +1804,7 @@ int nrs_conv2d_backward_beta(float* dinput, float* dweight, float* dbias, const 
         if (rc) return rc;
     }
     if (dbias) {
-        rc = nrs::bias_grad_launch(dbias, grad, N, c_out, P, 1.0f);  // conv.rs:322
+        rc = nrs::bias_grad_launch(dbias, grad, N, c_out, P, beta_params);  // conv.rs:322
         if (rc) return rc;
     }
     return NRS_OK;

@@ -43,6 +43,7 @@ struct FewTapsArgs {
     const float* g;
     const float* gp;     // UNPOOL: pooled gradient [N][M][OH/2][OW/2]
     const int32_t* am;   // UNPOOL: its argmax (flat conv-output indices)
+    const float* pv;     // UNPOOL with a ReLU between conv and pool: the pooled values (or null)
     float* pw;  // [slices][M][taps]
     float* pb;  // [slices][M]
     int C, H, W, M, kh, kw, stride, pad, OH, OW, P, Hp, Wp, taps, chunks;
@@ -83,7 +84,13 @@ void wgrad_few_taps_kernel(FewTapsArgs a) {
         const auto rp = buffer_rsrc(a.gp + (int64_t)n * a.M * PP, (int64_t)a.M * PP * 4);
         const auto ri = buffer_rsrc(reinterpret_cast<const float*>(a.am) + (int64_t)n * a.M * PP,
                                     (int64_t)a.M * PP * 4);
-        f32x2 gv[GPW][NBLK], iv[GPW][NBLK];
+        // with a ReLU between the conv and the pooling, a window's gradient
+        // passes only where its pooled value (the ReLU of the conv value at
+        // the index) is > 0, relu_grad's test on the conv value
+        const bool relu = a.pv != nullptr;
+        const auto rv = buffer_rsrc(relu ? a.pv + (int64_t)n * a.M * PP : a.gp,
+                                    relu ? (int64_t)a.M * PP * 4 : 0);
+        f32x2 gv[GPW][NBLK], iv[GPW][NBLK], vv[GPW][NBLK];
         int qy[GPW], qx[GPW];
 #pragma unroll
         for (int q = 0; q < GPW; ++q) {
@@ -99,6 +106,7 @@ void wgrad_few_taps_kernel(FewTapsArgs a) {
                 const bool ok = (p < a.P) & (oc < a.M);
                 gv[q][b] = buffer_load2(rp, ok ? (oc * PP + pw) * 4 : kOutOfRange);
                 iv[q][b] = buffer_load2(ri, ok ? (oc * PP + pw) * 4 : kOutOfRange);
+                vv[q][b] = buffer_load2(rv, (ok & relu) ? (oc * PP + pw) * 4 : kOutOfRange);
             }
         }
 #pragma unroll
@@ -113,7 +121,9 @@ void wgrad_few_taps_kernel(FewTapsArgs a) {
                     // vector element expression read element 0 for every u)
                     const float raw = u < 2 ? iv[q][b].x : iv[q][b].y;
                     const int idx = __builtin_bit_cast(int, raw);
-                    ga[q][b][u] = idx == e0 + u ? (u < 2 ? gv[q][b].x : gv[q][b].y) : 0.0f;
+                    const float pval = u < 2 ? vv[q][b].x : vv[q][b].y;
+                    const bool pass = (idx == e0 + u) & (!relu | (pval > 0.0f));
+                    ga[q][b][u] = pass ? (u < 2 ? gv[q][b].x : gv[q][b].y) : 0.0f;
                 }
             }
     }
@@ -228,7 +238,7 @@ int few_taps_wgrad(const FewTapsWgrad& s) {
         return kSlabUnsupported;
     const bool unpool = s.g == nullptr;
     if (unpool && (!s.gp || !s.am || s.OH % 2 || s.OW % 4 || ((uintptr_t)s.gp & 7) ||
-                   ((uintptr_t)s.am & 7) || s.N * s.M * P > INT32_MAX))
+                   ((uintptr_t)s.am & 7) || ((uintptr_t)s.pv & 7) || s.N * s.M * P > INT32_MAX))
         return kSlabUnsupported;
     const int nblk = s.M <= 16 ? 1 : (s.M <= 32 ? 2 : 4);  // channel blocks instantiated
     const int64_t gpi = (P + 15) / 16;
@@ -247,6 +257,7 @@ int few_taps_wgrad(const FewTapsWgrad& s) {
     a.g = s.g;
     a.gp = s.gp;
     a.am = s.am;
+    a.pv = s.pv;
     a.pw = pw;
     a.pb = pb;
     a.C = s.C;
@@ -271,7 +282,7 @@ int few_taps_wgrad(const FewTapsWgrad& s) {
     hipLaunchKernelGGL(reinterpret_cast<void (*)(FewTapsArgs)>(fn), dim3((unsigned)slices),
                        dim3(256), lds, stream(), a);
     NRS_LAUNCH_CHECK("conv2d weight gradient (few taps)");
-    return wgrad_partial_sum(s.dw, s.db, pw, pb, (int)slices, s.M, 1, taps);
+    return wgrad_partial_sum(s.dw, s.db, pw, pb, (int)slices, s.M, 1, taps, s.beta);
 }
 
 }  // namespace nrs

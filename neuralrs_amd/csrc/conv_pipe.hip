@@ -539,7 +539,7 @@ int pipe_backward(const SlabConv* d, const SlabWgrad& w) {
     a.P = P;
     int rc = launch_pipe<true, true>(a);
     if (rc) return rc;
-    return wgrad_partial_sum(w.dw, w.db, part, a.part_b, (int)slices, w.M, w.C, 9);
+    return wgrad_partial_sum(w.dw, w.db, part, a.part_b, (int)slices, w.M, w.C, 9, w.beta);
 }
 
 }  // namespace nrs

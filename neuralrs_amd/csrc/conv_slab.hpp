@@ -55,6 +55,7 @@ struct SlabWgrad {
     float* db = nullptr;       // [M] or null
     int64_t N = 0;
     int C = 0, H = 0, W = 0, M = 0, kh = 0, kw = 0, stride = 1, pad = 0, OH = 0, OW = 0;
+    float beta = 1.0f;  // dw = gradient + beta * dw (likewise db); 0 reads nothing
 };
 int slab_wgrad(const SlabWgrad& s);
 
@@ -87,13 +88,18 @@ struct FewTapsWgrad {
     // expanded on the fly: g[e] = gp[w] where am[w] == e, else 0
     const float* gp = nullptr;
     const int32_t* am = nullptr;
+    // with a ReLU between the conv and the pooling: the pooled values, whose
+    // sign gates each window's gradient (null: no ReLU)
+    const float* pv = nullptr;
+    float beta = 1.0f;  // dw = gradient + beta * dw (likewise db); 0 reads nothing
 };
 int few_taps_wgrad(const FewTapsWgrad& s);
 
-// dw[m][c][tap] += sum over slices of part_w[slice][m][tap][c] (when dw is
-// given) and db[m] += sum over slices of part_b[slice][m] (when db is given),
-// the slices added in a fixed order; one launch.
+// dw[m][c][tap] = sum over slices of part_w[slice][m][tap][c] + beta * dw
+// (when dw is given) and db[m] = sum over slices of part_b[slice][m] +
+// beta * db (when db is given), the slices added in a fixed order; one
+// launch. beta 0 reads neither.
 int wgrad_partial_sum(float* dw, float* db, const float* part_w, const float* part_b, int slices,
-                      int M, int C, int taps);
+                      int M, int C, int taps, float beta = 1.0f);
 
 }  // namespace nrs

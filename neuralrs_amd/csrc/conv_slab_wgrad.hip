@@ -24,7 +24,7 @@ constexpr int kSumGroups = 16, kSumBatch = 32;
 
 __global__ __launch_bounds__(64 * kSumGroups) void wgrad_sum_kernel(
     float* __restrict__ dw, float* __restrict__ db, const float* __restrict__ part_w,
-    const float* __restrict__ part_b, int slices, int M, int C, int taps) {
+    const float* __restrict__ part_b, int slices, int M, int C, int taps, float beta) {
     __shared__ float red[kSumGroups][64];
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     const int nw = dw ? M * taps * C : 0, total = nw + (db ? M : 0);
@@ -67,7 +67,8 @@ __global__ __launch_bounds__(64 * kSumGroups) void wgrad_sum_kernel(
             } else {
                 dst = db + (e - nw);
             }
-            *dst = r + *dst;
+            // beta 0 writes without reading the old gradient
+            *dst = beta != 0.0f ? r + beta * *dst : r;
         }
         __syncthreads();
     }
@@ -157,7 +158,7 @@ int plan_slab_wgrad(const SlabWgrad& s, WgradPlan& p) {
 int slab_wgrad_sum(const SlabWgrad& s, const WgradPlan& p) {
     // dW and (when requested) dB from the partials
     return wgrad_partial_sum(s.dw, s.db, p.a.part_w, p.a.part_w + (int64_t)p.slices * p.nw,
-                             p.slices, s.M, s.C, p.a.taps);
+                             p.slices, s.M, s.C, p.a.taps, s.beta);
 }
 
 int slab_wgrad(const SlabWgrad& s) {
@@ -177,12 +178,12 @@ int slab_wgrad(const SlabWgrad& s) {
 }
 
 int wgrad_partial_sum(float* dw, float* db, const float* part_w, const float* part_b, int slices,
-                      int M, int C, int taps) {
+                      int M, int C, int taps, float beta) {
     const int64_t total = (dw ? (int64_t)M * taps * C : 0) + (db ? M : 0);
     if (total == 0) return NRS_OK;
     hipLaunchKernelGGL(wgrad_sum_kernel, dim3((unsigned)((total + 63) / 64)),
                        dim3(64 * kSumGroups), 0, stream(), dw, db, part_w, part_b, slices, M, C,
-                       taps);
+                       taps, beta);
     NRS_LAUNCH_CHECK("conv2d weight gradient (sum)");
     return NRS_OK;
 }

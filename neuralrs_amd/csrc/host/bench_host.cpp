@@ -6,8 +6,13 @@
 //          set_grad, backward_graph, zero_grad of the parameters;
 //   mlp:   the cfg2 MLP training step (784 -> 128 -> ReLU -> 10, batch 256,
 //          fused cross-entropy gradient) issued through the C ABI, timed
-//          eagerly and as a replayed HIP graph of the same launches.
-// Usage: bench_host {block|mlp} [steps] [warmup]
+//          eagerly and as a replayed HIP graph of the same launches;
+//   cnn:   the cfg3 step (batch 128: conv1 1->32 3x3 p1 -> ReLU -> 2x2 max
+//          pool -> conv2 32->64 3x3 p1, forward and backward, the image
+//          batch requiring no gradient) through the C++ operator surface, as
+//          the reference CNN builds it (maxpool2d(relu(conv2d(..)))), op by
+//          op and with conv1 + ReLU + pool as one conv2d_maxpool node.
+// Usage: bench_host {block|mlp|cnn} [steps] [warmup]
 #include <hip/hip_runtime.h>
 
 #include <chrono>
@@ -126,6 +131,37 @@ int bench_block(int steps, int warmup) {
     return 0;
 }
 
+int bench_cnn(int steps, int warmup) {
+    const size_t N = 128, H = 28, W = 28, C1 = 32, C2 = 64;
+    NodeRef x = resident(uniform(N * H * W, 0.0f, 1.0f), {N, 1, H, W});
+    x->requires_grad = false;  // examples/mnist_cuda_cnn.rs:261
+    NodeRef w1 = resident(normal(C1 * 9, std::sqrt(2.0f / 9.0f)), {C1, 1, 3, 3});
+    NodeRef b1 = resident(Vec(C1, 0.0f), {C1});
+    NodeRef w2 = resident(normal(C2 * C1 * 9, std::sqrt(2.0f / 288.0f)), {C2, C1, 3, 3});
+    NodeRef b2 = resident(Vec(C2, 0.0f), {C2});
+    const std::vector<NodeRef> params{w1, b1, w2, b2};
+    DeviceBuffer seed = DeviceBuffer::from_host(normal(N * C2 * 14 * 14, 1.0f));
+    auto run = [&](bool fused) {
+        NodeRef p1 = fused ? hip::nn::conv2d_maxpool(x, w1, b1, 1, 1, true, 2, 2)
+                           : hip::nn::maxpool2d(hip::graph::relu(hip::nn::conv2d(x, w1, b1, 1, 1)),
+                                                2, 2);
+        NodeRef out = hip::nn::conv2d(p1, w2, b2, 1, 1);
+        nrs_check(nrs_memcpy_dtod(out->gpu->grad->write_target(), seed.ptr(), seed.len() * sizeof(float)),
+                  "seed");
+        backward_graph(out);
+        gpu::zero_grad(params);
+    };
+    double f_gpu = 0, f_wall = 0, u_gpu = 0, u_wall = 0;
+    time_steps([&] { run(true); }, steps, warmup, f_gpu, f_wall);
+    time_steps([&] { run(false); }, steps, warmup, u_gpu, u_wall);
+    std::printf("{\"workload\": \"cfg3 CNN step batch 128 (conv1 -> ReLU -> 2x2 maxpool -> conv2, "
+                "fwd + bwd) through libnrs_host.so\", \"step_gpu_us\": %.2f, \"step_wall_us\": %.2f, "
+                "\"imgs_per_s\": %.1f, \"unfused_step_gpu_us\": %.2f, \"unfused_step_wall_us\": %.2f, "
+                "\"steps\": %d}\n",
+                f_gpu, f_wall, N / (f_gpu * 1e-6), u_gpu, u_wall, steps);
+    return 0;
+}
+
 int bench_mlp(int steps, int warmup) {
     const int64_t Bn = 256, I = 784, Hd = 128, O = 10;
     DeviceBuffer x = DeviceBuffer::from_host(normal(Bn * I, 1.0f));
@@ -189,7 +225,7 @@ int bench_mlp(int steps, int warmup) {
 
 int main(int argc, char** argv) {
     if (argc < 2) {
-        std::fprintf(stderr, "usage: %s {block|mlp} [steps] [warmup]\n", argv[0]);
+        std::fprintf(stderr, "usage: %s {block|mlp|cnn} [steps] [warmup]\n", argv[0]);
         return 2;
     }
     const int steps = argc > 2 ? std::atoi(argv[2]) : 20;
@@ -197,6 +233,7 @@ int main(int argc, char** argv) {
     nrs_check(nrs_init(0), "init");
     if (!std::strcmp(argv[1], "block")) return bench_block(steps, warmup);
     if (!std::strcmp(argv[1], "mlp")) return bench_mlp(steps, warmup);
+    if (!std::strcmp(argv[1], "cnn")) return bench_cnn(steps, warmup);
     std::fprintf(stderr, "unknown workload %s\n", argv[1]);
     return 2;
 }

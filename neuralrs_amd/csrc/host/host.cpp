@@ -1,6 +1,7 @@
 // Implementation of the C++ host layer (neuralrs.hpp) over the C ABI of
 // libnrs_hip.so. Each op follows the reference op it names: same operand
 // checks and panic messages, same output shape, same gradient flow.
+#include <algorithm>
 #include <memory>
 
 #include "neuralrs.hpp"
@@ -15,8 +16,29 @@ namespace neuralrs {
 
 namespace {
 
-void check(int rc, const char* what) {
+// Buffers handed out by acc_target / write_target since the last launch
+// check: their memory holds a value only once that launch is enqueued.
+std::vector<DeviceBuffer*>& taken_pending() {
+    static std::vector<DeviceBuffer*> v;
+    return v;
+}
+
+// A library call that allocates, copies or clears: the launch of an op is
+// checked by check(), which settles the buffers taken for it.
+void check_raw(int rc, const char* what) {
     if (rc != NRS_OK) throw Panic(std::string(what) + ": " + nrs_last_error());
+}
+
+// The launch of an op: on success the buffers taken for it hold its result;
+// on failure nothing was enqueued, so they are pending zeros again.
+void check(int rc, const char* what) {
+    std::vector<DeviceBuffer*>& t = taken_pending();
+    if (rc != NRS_OK) {
+        for (DeviceBuffer* b : t) b->zero();
+        t.clear();
+        throw Panic(std::string(what) + ": " + nrs_last_error());
+    }
+    t.clear();
 }
 
 size_t product(const std::vector<size_t>& s) {
@@ -138,20 +160,22 @@ void build_topo(const NodeRef& n, std::unordered_set<const Node*>& visited,
 }  // namespace
 
 // ------------------------------------------------------------ DeviceBuffer
+void note_pending_taken(DeviceBuffer* b) { taken_pending().push_back(b); }
+
 DeviceBuffer::DeviceBuffer(size_t len, bool zero) : len_(len), pending_zero_(zero) {
     void* p = nullptr;
-    check(nrs_malloc(&p, len * sizeof(float)), "device alloc failed");
+    check_raw(nrs_malloc(&p, len * sizeof(float)), "device alloc failed");
     ptr_ = static_cast<float*>(p);
 }
 
 void DeviceBuffer::clear_now() const {
-    check(nrs_memset_zero(ptr_, len_ * sizeof(float)), "device memset failed");
+    check_raw(nrs_memset_zero(ptr_, len_ * sizeof(float)), "device memset failed");
     pending_zero_ = false;
 }
 
 DeviceBuffer DeviceBuffer::from_host(const std::vector<float>& v) {
     DeviceBuffer b(v.size(), false);
-    check(nrs_memcpy_htod(b.ptr_, v.data(), v.size() * sizeof(float)), "htod failed");
+    check_raw(nrs_memcpy_htod(b.ptr_, v.data(), v.size() * sizeof(float)), "htod failed");
     return b;
 }
 
@@ -164,6 +188,8 @@ DeviceBuffer DeviceBuffer::view_of(const DeviceBuffer& src) {
 }
 
 DeviceBuffer::~DeviceBuffer() {
+    std::vector<DeviceBuffer*>& t = taken_pending();
+    t.erase(std::remove(t.begin(), t.end(), this), t.end());
     if (ptr_ && owned_) nrs_free(ptr_);
 }
 
@@ -193,10 +219,10 @@ DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
 std::vector<float> DeviceBuffer::to_host() const {
     std::vector<float> v(len_);
     if (pending_zero_) {
-        check(nrs_sync(), "synchronize failed");
+        check_raw(nrs_sync(), "synchronize failed");
         return v;
     }
-    check(nrs_memcpy_dtoh(v.data(), ptr_, len_ * sizeof(float)), "dtoh failed");
+    check_raw(nrs_memcpy_dtoh(v.data(), ptr_, len_ * sizeof(float)), "dtoh failed");
     return v;
 }
 
@@ -556,11 +582,105 @@ NodeRef conv2d(const NodeRef& input, const NodeRef& weight, const NodeRef& bias,
         GpuBuffers& ig = gpu_of(input, "conv2d bwd: input not on GPU");
         GpuBuffers& wg = gpu_of(weight, "conv2d bwd: weight not on GPU");
         GpuBuffers& bg = gpu_of(bias, "conv2d bwd: bias not on GPU");
-        float* dinput = input->requires_grad ? ig.grad->ptr() : nullptr;  // conv.rs:304
-        check(nrs_conv2d_backward(dinput, wg.grad->ptr(), bg.grad->ptr(), grad->ptr(),
-                                  ig.data.ptr(), wg.data.ptr(), n, c_in, in_h, in_w, c_out, kh, kw,
-                                  stride, pad),
+        // the input gradient is written when it is still a pending zero
+        // (beta 0), else added; conv.rs:304 skips it for an input that
+        // requires no gradient
+        float beta = 1.0f;
+        float* dinput = input->requires_grad ? ig.grad->acc_target(beta) : nullptr;
+        // the parameter gradients likewise: written when both are pending
+        // zeros (after zero_grad), else added
+        const float beta_p = joint_beta({wg.grad.get(), bg.grad.get()});
+        check(nrs_conv2d_backward_ex(dinput, wg.grad->write_target(), bg.grad->write_target(),
+                                     grad->ptr(), ig.data.ptr(), wg.data.ptr(), n, c_in, in_h,
+                                     in_w, c_out, kh, kw, stride, pad, beta, beta_p),
               "cuda conv2d bwd: launch failed");
+    };
+    return node;
+}
+
+NodeRef maxpool2d(const NodeRef& input, size_t kernel, size_t stride) {
+    GpuBuffers& ig = gpu_of(input, "cuda maxpool: input not on GPU");
+    if (input->shape.size() != 4) throw Panic("cuda maxpool: input must be 4-D");
+    const size_t n = input->shape[0], c = input->shape[1], in_h = input->shape[2],
+                 in_w = input->shape[3];
+    if (kernel == 0 || stride == 0 || in_h < kernel || in_w < kernel)
+        throw Panic("cuda maxpool: bad window");
+    const size_t out_h = (in_h - kernel) / stride + 1, out_w = (in_w - kernel) / stride + 1;
+    const size_t total = n * c * out_h * out_w;
+    DeviceBuffer out(total, false);
+    // the winners' flat input indices (int32, same element size as f32)
+    auto argmax = std::make_shared<DeviceBuffer>(total, false);
+    check(nrs_maxpool_forward(out.ptr(), reinterpret_cast<int32_t*>(argmax->write_target()),
+                              ig.data.ptr(), n, c, in_h, in_w, kernel, stride),
+          "cuda maxpool: forward launch failed");
+    NodeRef node = make_output({n, c, out_h, out_w}, {input}, std::move(out));
+    node->backward_fn = [grad = node->gpu->grad, input, argmax, n, c, in_h, in_w, kernel,
+                         stride](const std::vector<float>&) {
+        GpuBuffers& ig = gpu_of(input, "cuda maxpool bwd: input not on GPU");
+        check(nrs_maxpool_backward(ig.grad->ptr(), grad->ptr(),
+                                   reinterpret_cast<const int32_t*>(argmax->ptr()), n, c, in_h,
+                                   in_w, kernel, stride),
+              "cuda maxpool bwd: launch failed");
+    };
+    return node;
+}
+
+NodeRef conv2d_maxpool(const NodeRef& input, const NodeRef& weight, const NodeRef& bias,
+                       size_t stride, size_t pad, bool relu, size_t pool_k, size_t pool_stride) {
+    GpuBuffers& ig = gpu_of(input, "cuda conv2d: input not on GPU");
+    GpuBuffers& wg = gpu_of(weight, "cuda conv2d: weight not on GPU");
+    GpuBuffers& bg = gpu_of(bias, "cuda conv2d: bias not on GPU");
+    if (input->shape.size() != 4 || weight->shape.size() != 4)
+        throw Panic("cuda conv2d: input and weight must be 4-D");
+    const size_t n = input->shape[0], c_in = input->shape[1], in_h = input->shape[2],
+                 in_w = input->shape[3];
+    const size_t c_out = weight->shape[0], kh = weight->shape[2], kw = weight->shape[3];
+    if (weight->shape[1] != c_in) throw Panic("cuda conv2d: channel mismatch");
+    if (product(bias->shape) != c_out) throw Panic("cuda conv2d: bias length mismatch");
+    if (stride == 0 || in_h + 2 * pad < kh || in_w + 2 * pad < kw)
+        throw Panic("cuda conv2d: bad stride/padding for the kernel size");
+    const size_t out_h = (in_h + 2 * pad - kh) / stride + 1;
+    const size_t out_w = (in_w + 2 * pad - kw) / stride + 1;
+    if (pool_k == 0 || pool_stride == 0 || out_h < pool_k || out_w < pool_k)
+        throw Panic("cuda maxpool: bad window");
+    const size_t ph = (out_h - pool_k) / pool_stride + 1, pw = (out_w - pool_k) / pool_stride + 1;
+    const size_t total = n * c_out * ph * pw;
+    DeviceBuffer pooled(total, false);
+    auto argmax = std::make_shared<DeviceBuffer>(total, false);
+    int32_t* am = reinterpret_cast<int32_t*>(argmax->write_target());
+    check(relu ? nrs_conv2d_relu_maxpool_forward(pooled.ptr(), am, nullptr, ig.data.ptr(),
+                                                 wg.data.ptr(), bg.data.ptr(), n, c_in, in_h, in_w,
+                                                 c_out, kh, kw, stride, pad, pool_k, pool_stride)
+               : nrs_conv2d_maxpool_forward(pooled.ptr(), am, nullptr, ig.data.ptr(),
+                                            wg.data.ptr(), bg.data.ptr(), n, c_in, in_h, in_w,
+                                            c_out, kh, kw, stride, pad, pool_k, pool_stride),
+          "cuda conv2d maxpool: launch failed");
+    NodeRef node = make_output({n, c_out, ph, pw}, {input, weight, bias}, std::move(pooled));
+    Node* self = node.get();
+    node->backward_fn = [grad = node->gpu->grad, self, input, weight, bias, argmax, relu, n, c_in,
+                         in_h, in_w, c_out, kh, kw, stride, pad, pool_k,
+                         pool_stride](const std::vector<float>&) {
+        GpuBuffers& ig = gpu_of(input, "conv2d bwd: input not on GPU");
+        GpuBuffers& wg = gpu_of(weight, "conv2d bwd: weight not on GPU");
+        GpuBuffers& bg = gpu_of(bias, "conv2d bwd: bias not on GPU");
+        float* dinput = input->requires_grad ? ig.grad->ptr() : nullptr;  // conv.rs:304
+        const int32_t* am = reinterpret_cast<const int32_t*>(argmax->ptr());
+        // the ReLU's gate reads the node's own pooled values (its data); the
+        // parameter gradients are written when both are pending zeros
+        if (relu) {
+            const float beta_p = joint_beta({wg.grad.get(), bg.grad.get()});
+            check(nrs_maxpool_relu_conv2d_backward(
+                      dinput, wg.grad->write_target(), bg.grad->write_target(), grad->ptr(), am,
+                      self->gpu->data.ptr(), ig.data.ptr(), wg.data.ptr(), n, c_in, in_h, in_w,
+                      c_out, kh, kw, stride, pad, pool_k, pool_stride, beta_p),
+                  "cuda conv2d bwd: launch failed");
+        } else {
+            check(nrs_maxpool_conv2d_backward(dinput, wg.grad->ptr(), bg.grad->ptr(), grad->ptr(),
+                                              am, ig.data.ptr(), wg.data.ptr(), n, c_in, in_h,
+                                              in_w, c_out, kh, kw, stride, pad, pool_k,
+                                              pool_stride),
+                  "cuda conv2d bwd: launch failed");
+        }
     };
     return node;
 }
@@ -870,6 +990,14 @@ static NodeRef multihead(const MultiHeadAttention& mha, const NodeRef& flat, siz
         concat = merge_heads(att, rows, heads, dh, {rows, d});
     }
     return graph::matmul(concat, mha.w_o);
+}
+
+NodeRef SelfAttention::forward(const NodeRef& x) const {
+    // self_attention.rs:31-36: q, k, v = x . w_q, x . w_k, x . w_v (one grouped
+    // launch, three matmul nodes), then attention
+    if (x->shape.size() != 2) throw Panic("self attention: x must be [seq, d_model]");
+    const std::vector<NodeRef> qkv = matmul_shared_lhs(x, {w_q, w_k, w_v});
+    return attention(qkv[0], qkv[1], qkv[2]);
 }
 
 NodeRef MultiHeadAttention::forward(const NodeRef& x) const {

@@ -11,8 +11,9 @@
 //   graph::{matmul, bmm, add, transpose, scale, softmax, relu, slice_cols,
 //          concat_cols, scaled_softmax}
 //                                        src/cuda/graph/*.rs
-//   nn::{conv2d, Linear, attention, attention_batch, layernorm}
-//                                        src/cuda/nn/{conv,linear,attention}.rs
+//   nn::{conv2d, maxpool2d, Linear, attention, attention_batch, layernorm,
+//        SelfAttention, MultiHeadAttention, TransformerBlock}
+//                                        src/cuda/nn/*.rs
 // Rc<RefCell<Node>> becomes std::shared_ptr<Node>; a panic ("cuda matmul: lhs
 // not on GPU") becomes a thrown neuralrs::Panic with the same message. Like
 // the reference it is single-threaded, device 0, one stream.
@@ -51,6 +52,12 @@ enum class Device { CPU, GPU };
 // that overwrites every element takes write_target()). Gradient buffers are
 // created zeroed and their first contribution is usually such a kernel, so a
 // backward pass mostly skips the clearing launches.
+class DeviceBuffer;
+// Records that `b` stopped being a pending zero for a launch that is about to
+// be enqueued: a failed launch (a thrown Panic) makes it a pending zero again,
+// since nothing was written to its memory.
+void note_pending_taken(DeviceBuffer* b);
+
 class DeviceBuffer {
 public:
     DeviceBuffer() = default;
@@ -77,12 +84,12 @@ public:
     // that holds the buffer's value once the launch is enqueued.
     float* acc_target(float& beta) {
         beta = pending_zero_ ? 0.0f : 1.0f;
-        pending_zero_ = false;
+        take_pending();
         return ptr_;
     }
     // For a launch that overwrites every element without reading it.
     float* write_target() {
-        pending_zero_ = false;
+        take_pending();
         return ptr_;
     }
     bool pending_zero() const { return pending_zero_; }
@@ -91,6 +98,12 @@ public:
     void zero();                          // stream.memset_zeros
 
 private:
+    void take_pending() {
+        if (pending_zero_) {
+            pending_zero_ = false;
+            note_pending_taken(this);
+        }
+    }
     void clear_now() const;
     float* ptr_ = nullptr;
     size_t len_ = 0;
@@ -189,6 +202,20 @@ namespace nn {
 NodeRef conv2d(const NodeRef& input, const NodeRef& weight, const NodeRef& bias, size_t stride,
                size_t pad);
 
+// src/cuda/nn/maxpool.rs:60-66: kernel x kernel windows with `stride`, no
+// padding, on [N,C,H,W]; the backward adds each window's gradient to its
+// first maximum.
+NodeRef maxpool2d(const NodeRef& input, size_t kernel, size_t stride);
+
+// maxpool2d(conv2d(input, weight, bias, stride, pad), pool_k, pool_stride),
+// or with relu maxpool2d(relu(conv2d(..)), ..) as the reference CNN builds it
+// (examples/mnist_cuda_cnn.rs:125,127), as one node for a conv output that
+// only feeds the pooling: same values and gradients, and the conv output and
+// its ReLU are never materialised on the fused shapes ("same" 3x3 stride 1
+// over c_in <= 3 channels with 2x2 stride-2 pooling: one launch each way).
+NodeRef conv2d_maxpool(const NodeRef& input, const NodeRef& weight, const NodeRef& bias,
+                       size_t stride, size_t pad, bool relu, size_t pool_k, size_t pool_stride);
+
 // src/cuda/nn/linear.rs:11-26: weights [in,out], bias [out].
 struct Linear {
     NodeRef weights;
@@ -205,6 +232,18 @@ NodeRef attention_batch(const NodeRef& q, const NodeRef& k, const NodeRef& v);
 // src/cuda/nn/normalization.rs:87-160: per-row layer norm over the last dim
 // with gamma/beta [features].
 NodeRef layernorm(const NodeRef& input, const NodeRef& gamma, const NodeRef& beta, float eps);
+
+// src/cuda/nn/self_attention.rs:10-37: single-head self-attention over
+// resident projections w_q, w_k, w_v [d_model, d_k]: x [seq, d_model] ->
+// attention(x w_q, x w_k, x w_v) [seq, d_k] (the three projections of one
+// input share one grouped launch).
+struct SelfAttention {
+    NodeRef w_q, w_k, w_v;
+    size_t d_model, d_k;
+    SelfAttention(NodeRef q, NodeRef k, NodeRef v, size_t d, size_t dk)
+        : w_q(std::move(q)), w_k(std::move(k)), w_v(std::move(v)), d_model(d), d_k(dk) {}
+    NodeRef forward(const NodeRef& x) const;
+};
 
 // src/cuda/nn/normalization.rs (LayerNorm): resident gamma/beta [features].
 struct LayerNorm {

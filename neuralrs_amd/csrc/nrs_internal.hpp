@@ -26,7 +26,8 @@ int set_error(int code, const char* fmt, ...);
 //   0 split-K partials, 1 im2col / dcols columns, 2 conv grad in GEMM layout,
 //   3 reduction partials, 4 conv weights packed for LDS staging, 5 the conv
 //   output or its gradient around a fused pooling (not used by the conv
-//   entry points themselves, which the fused ones call).
+//   entry points themselves, which the fused ones call), 6 the pooled
+//   gradient masked by a ReLU between conv and pooling.
 // Returns nullptr (and records an error) when the allocation fails.
 float* workspace(size_t bytes, int slot = 0);
 

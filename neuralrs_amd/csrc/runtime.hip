@@ -12,7 +12,7 @@
 namespace nrs {
 namespace {
 
-constexpr int kSlots = 6;
+constexpr int kSlots = 7;
 
 // Scratch of the no-allocation entry points: one per GPU, held until the
 // process ends. In host code `scratch` names a host-side stand-in, so it is

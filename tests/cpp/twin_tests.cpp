@@ -44,6 +44,9 @@ void orc_relu_forward(const float*, float*, int64_t);
 float orc_cross_entropy_loss(const float*, const float*, int64_t, int64_t);
 void orc_cross_entropy_grad(const float*, const float*, float*, int64_t, int64_t);
 void orc_relu_backward(const float*, const float*, float*, int64_t);
+void orc_maxpool_forward(const float*, float*, int32_t*, int64_t, int64_t, int64_t, int64_t, int64_t,
+                         int64_t);
+void orc_maxpool_backward(const float*, const int32_t*, float*, int64_t);
 void orc_slice_cols(const float*, float*, int64_t, int64_t, int64_t, int64_t);
 void orc_slice_cols_backward(const float*, float*, int64_t, int64_t, int64_t, int64_t);
 void orc_concat_part(const float*, float*, int64_t, int64_t, int64_t, int64_t);
@@ -929,6 +932,153 @@ void cfg4_transformer_block() {
     close_scaled(gpu::read_grad(gx), c.dx, 3e-3f, rel, "cfg4 block dx");
 }
 
+// tests/cuda_assembly_test.rs:86-131: single-head self-attention, seq 4,
+// d_model 6, d_k 4, formula inputs, tol 1e-3 (the CPU side: the three
+// projections and attention composed from the oracle's ops).
+void cuda_self_attention() {
+    const size_t S = 4, D = 6, DK = 4;
+    const Vec x = formula(S * D, 11, 0.1f, -0.5f), wq = formula(D * DK, 13, 0.1f, -0.6f),
+              wk = formula(D * DK, 9, 0.1f, -0.4f), wv = formula(D * DK, 7, 0.1f, -0.3f),
+              seed = formula(S * DK, 6, 0.1f, 0.2f);
+    Vec q(S * DK), k(S * DK), v(S * DK);
+    orc_graph_matmul_forward(x.data(), wq.data(), q.data(), S, D, DK);
+    orc_graph_matmul_forward(x.data(), wk.data(), k.data(), S, D, DK);
+    orc_graph_matmul_forward(x.data(), wv.data(), v.data(), S, D, DK);
+    CpuAttention a(q, k, v, seed, 1, S, DK);
+    Vec cdx(S * D, 0.0f), cdq(D * DK, 0.0f), cdk(D * DK, 0.0f), cdv(D * DK, 0.0f);
+    orc_graph_matmul_backward(x.data(), wq.data(), a.dq.data(), cdx.data(), cdq.data(), S, D, DK);
+    orc_graph_matmul_backward(x.data(), wk.data(), a.dk.data(), cdx.data(), cdk.data(), S, D, DK);
+    orc_graph_matmul_backward(x.data(), wv.data(), a.dv.data(), cdx.data(), cdv.data(), S, D, DK);
+
+    NodeRef gwq = resident(wq, {D, DK}), gwk = resident(wk, {D, DK}), gwv = resident(wv, {D, DK});
+    hip::nn::SelfAttention sa(gwq, gwk, gwv, D, DK);
+    NodeRef gx = resident(x, {S, D});
+    NodeRef gout = sa.forward(gx);
+    const Vec gf = gpu::to_host(gout);
+    gpu::set_grad(gout, seed);
+    backward_graph(gout);
+    close(gf, a.out, 1e-3f, "self_attn fwd");
+    close(gpu::read_grad(gwq), cdq, 1e-3f, "self_attn dw_q");
+    close(gpu::read_grad(gwk), cdk, 1e-3f, "self_attn dw_k");
+    close(gpu::read_grad(gwv), cdv, 1e-3f, "self_attn dw_v");
+    close(gpu::read_grad(gx), cdx, 1e-3f, "self_attn dx");
+}
+
+// tests/cuda_assembly_test.rs:133-182: MultiHeadAttention on one sequence,
+// seq 4, d_model 6, 2 heads (d_head 3), formula inputs, tol 1e-3.
+void cuda_multihead() {
+    const size_t S = 4, D = 6, H = 2;
+    const Vec x = formula(S * D, 11, 0.1f, -0.5f), wq = formula(D * D, 13, 0.1f, -0.6f),
+              wk = formula(D * D, 9, 0.1f, -0.4f), wv = formula(D * D, 7, 0.1f, -0.3f),
+              wo = formula(D * D, 5, 0.1f, -0.2f), seed = formula(S * D, 6, 0.1f, 0.2f);
+    CpuMultiHead c(x, wq, wk, wv, wo, seed, 1, S, D, H);
+    NodeRef gwq = resident(wq, {D, D}), gwk = resident(wk, {D, D}), gwv = resident(wv, {D, D}),
+            gwo = resident(wo, {D, D});
+    hip::nn::MultiHeadAttention mha(gwq, gwk, gwv, gwo, D, H);
+    NodeRef gx = resident(x, {S, D});
+    NodeRef gout = mha.forward(gx);
+    const Vec gf = gpu::to_host(gout);
+    gpu::set_grad(gout, seed);
+    backward_graph(gout);
+    close(gf, c.out, 1e-3f, "mha fwd");
+    close(gpu::read_grad(gwq), c.dwq, 1e-3f, "mha dw_q");
+    close(gpu::read_grad(gwk), c.dwk, 1e-3f, "mha dw_k");
+    close(gpu::read_grad(gwv), c.dwv, 1e-3f, "mha dw_v");
+    close(gpu::read_grad(gwo), c.dwo, 1e-3f, "mha dw_o");
+    close(gpu::read_grad(gx), c.dx, 1e-3f, "mha dx");
+}
+
+// tests/cuda_maxpool_test.rs:9-39: maxpool2d against the CPU MaxPool2d
+// (restated by the oracle), forward 1e-5, input gradient 1e-4.
+void maxpool_case(size_t n, size_t c, size_t in_h, size_t in_w, size_t k, size_t stride) {
+    const size_t in_len = n * c * in_h * in_w;
+    Vec input(in_len);
+    for (size_t i = 0; i < in_len; ++i)
+        input[i] = static_cast<float>(static_cast<int>((i * 31 + 7) % 97)) * 0.05f - 2.0f;
+    const size_t oh = (in_h - k) / stride + 1, ow = (in_w - k) / stride + 1, out_len = n * c * oh * ow;
+    Vec cout(out_len), cig(in_len, 0.0f);
+    std::vector<int32_t> am(out_len);
+    orc_maxpool_forward(input.data(), cout.data(), am.data(), n, c, in_h, in_w, k, stride);
+    const Vec seed = formula(out_len, 7, 0.2f, 0.1f);
+    orc_maxpool_backward(seed.data(), am.data(), cig.data(), out_len);
+    NodeRef gi = resident(input, {n, c, in_h, in_w});
+    NodeRef gout = hip::nn::maxpool2d(gi, k, stride);
+    if (gout->shape != std::vector<size_t>{n, c, oh, ow}) throw Failure("maxpool: output shape");
+    close(gpu::to_host(gout), cout, 1e-5f, "maxpool fwd");
+    gpu::set_grad(gout, seed);
+    backward_graph(gout);
+    close(gpu::read_grad(gi), cig, 1e-4f, "maxpool input.grad");
+}
+void cuda_maxpool_non_overlapping() { maxpool_case(2, 3, 8, 8, 2, 2); }
+void cuda_maxpool_overlapping() { maxpool_case(2, 3, 7, 7, 3, 1); }
+
+// cfg3 end to end at batch 128 through the operator surface, as the reference
+// CNN builds it (examples/mnist_cuda_cnn.rs:125: maxpool2d(relu(conv2d(..)))):
+// conv1 1->32 3x3 p1 -> ReLU -> 2x2 maxpool -> conv2 32->64 3x3 p1, forward
+// and backward (the image batch requires no gradient, as at
+// mnist_cuda_cnn.rs:261), against the oracle's Conv2d, ReLU and max pooling
+// composed the same way. Run twice on the GPU: op by op (conv2d, relu,
+// maxpool2d nodes) and with the first three as one conv2d_maxpool node; the
+// two must agree bit for bit except where a conv output lands exactly on a
+// ReLU or pooling tie, which the integer check of the GPU tests covers.
+void cfg3_cnn_step() {
+    reseed(33);
+    const size_t N = 128, H = 28, W = 28, C1 = 32, C2 = 64, PH = 14, PW = 14;
+    const Vec x = uniform(N * H * W, 0.0f, 1.0f);
+    const Vec w1 = normal(C1 * 9, std::sqrt(2.0f / 9.0f)), b1 = normal(C1, 0.1f);
+    const Vec w2 = normal(C2 * C1 * 9, std::sqrt(2.0f / 288.0f)), b2 = normal(C2, 0.1f);
+    const Vec seed = normal(N * C2 * PH * PW, 1.0f);
+    // CPU composition
+    Vec y1(N * C1 * H * W), a1(N * C1 * H * W), p1(N * C1 * PH * PW), y2(N * C2 * PH * PW);
+    std::vector<int32_t> am(N * C1 * PH * PW);
+    orc_conv2d_forward(x.data(), w1.data(), b1.data(), y1.data(), N, 1, C1, H, W, 3, 3, 1, 1);
+    orc_relu_forward(y1.data(), a1.data(), y1.size());
+    orc_maxpool_forward(a1.data(), p1.data(), am.data(), N, C1, H, W, 2, 2);
+    orc_conv2d_forward(p1.data(), w2.data(), b2.data(), y2.data(), N, C1, C2, PH, PW, 3, 3, 1, 1);
+    Vec dp1(p1.size(), 0.0f), dw2(w2.size(), 0.0f), db2(C2, 0.0f), da1(a1.size(), 0.0f),
+        dy1(y1.size(), 0.0f), dx(x.size(), 0.0f), dw1(w1.size(), 0.0f), db1(C1, 0.0f);
+    orc_conv2d_backward(p1.data(), w2.data(), seed.data(), dp1.data(), dw2.data(), db2.data(), N,
+                        C1, C2, PH, PW, 3, 3, 1, 1);
+    orc_maxpool_backward(dp1.data(), am.data(), da1.data(), dp1.size());
+    orc_relu_backward(y1.data(), da1.data(), dy1.data(), y1.size());
+    orc_conv2d_backward(x.data(), w1.data(), dy1.data(), dx.data(), dw1.data(), db1.data(), N, 1,
+                        C1, H, W, 3, 3, 1, 1);
+    Vec fused_out, fused_dw1, fused_db1, fused_dw2, fused_db2;
+    for (int fused = 0; fused < 2; ++fused) {
+        const char* tag = fused ? "cfg3 cnn (fused conv1+relu+pool)" : "cfg3 cnn (op by op)";
+        NodeRef gx = resident(x, {N, 1, H, W});
+        gx->requires_grad = false;
+        NodeRef gw1 = resident(w1, {C1, 1, 3, 3}), gb1 = resident(b1, {C1});
+        NodeRef gw2 = resident(w2, {C2, C1, 3, 3}), gb2 = resident(b2, {C2});
+        NodeRef pooled = fused ? hip::nn::conv2d_maxpool(gx, gw1, gb1, 1, 1, true, 2, 2)
+                               : hip::nn::maxpool2d(
+                                     hip::graph::relu(hip::nn::conv2d(gx, gw1, gb1, 1, 1)), 2, 2);
+        close(gpu::to_host(pooled), p1, 1e-4f, std::string(tag) + " pooled");
+        NodeRef out = hip::nn::conv2d(pooled, gw2, gb2, 1, 1);
+        const Vec gout = gpu::to_host(out);
+        close_scaled(gout, y2, 1e-4f, 1e-5f, std::string(tag) + " fwd");
+        gpu::set_grad(out, seed);
+        backward_graph(out);
+        const Vec gdw1 = gpu::read_grad(gw1), gdb1 = gpu::read_grad(gb1),
+                  gdw2 = gpu::read_grad(gw2), gdb2 = gpu::read_grad(gb2);
+        // the parameter gradients sum N * 196 (conv2) or N * 784 (conv1)
+        // terms: an absolute floor plus a relative bar on their scale
+        close_scaled(gdw2, dw2, 1e-3f, 1e-5f, std::string(tag) + " conv2 weight.grad");
+        close_scaled(gdb2, db2, 1e-3f, 1e-5f, std::string(tag) + " conv2 bias.grad");
+        close_scaled(gdw1, dw1, 1e-3f, 1e-5f, std::string(tag) + " conv1 weight.grad");
+        close_scaled(gdb1, db1, 1e-3f, 1e-5f, std::string(tag) + " conv1 bias.grad");
+        if (fused) {
+            close(gout, fused_out, 1e-5f, "cfg3 cnn fused vs op by op fwd");
+            close_scaled(gdw1, fused_dw1, 1e-4f, 1e-6f, "cfg3 cnn fused vs op by op conv1 weight.grad");
+            close_scaled(gdb1, fused_db1, 1e-4f, 1e-6f, "cfg3 cnn fused vs op by op conv1 bias.grad");
+        } else {
+            fused_out = gout;
+            fused_dw1 = gdw1;
+            fused_db1 = gdb1;
+        }
+    }
+}
+
 const Case kCases[] = {
     {"cuda_resident_matmul_backward", cuda_resident_matmul_backward},
     {"cuda_resident_linear_chain", cuda_resident_linear_chain},
@@ -957,6 +1107,11 @@ const Case kCases[] = {
     {"attention_fused_2d", attention_fused_2d},
     {"attention_batch_self", attention_batch_self},
     {"grads_accumulate_and_zero", grads_accumulate_and_zero},
+    {"cuda_self_attention", cuda_self_attention},
+    {"cuda_multihead", cuda_multihead},
+    {"cuda_maxpool_non_overlapping", cuda_maxpool_non_overlapping},
+    {"cuda_maxpool_overlapping", cuda_maxpool_overlapping},
+    {"cfg3_cnn_step", cfg3_cnn_step},
 };
 
 int main(int argc, char** argv) {

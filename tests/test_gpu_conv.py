@@ -336,24 +336,32 @@ POOL_SHAPES = [  # (n, c_in, c_out, h, w, kh, kw, stride, pad, pool_k, pool_stri
 ]
 
 
-def _pool_ref(hip, x, w, b, shape, floats):
+def _pool_ref(hip, x, w, b, shape, floats, relu=False):
     n, ci, co, h, wd, kh, kw, s, p, pk, ps = shape
     D = hip.DeviceBuffer.from_host
     oh, ow = (h + 2 * p - kh) // s + 1, (wd + 2 * p - kw) // s + 1
     ph, pw = (oh - pk) // ps + 1, (ow - pk) // ps + 1
     y = hip.DeviceBuffer(n * co * oh * ow)
     hip.call("nrs_conv2d_forward", y, D(x), D(w), D(b), n, ci, h, wd, co, kh, kw, s, p)
+    a = y
+    if relu:
+        a = hip.DeviceBuffer(n * co * oh * ow)
+        hip.call("nrs_relu_forward", a, y, n * co * oh * ow)
     pooled, am = hip.DeviceBuffer(n * co * ph * pw), hip.DeviceBuffer(n * co * ph * pw, np.int32)
-    hip.call("nrs_maxpool_forward", pooled, am, y, n, co, oh, ow, pk, ps)
+    hip.call("nrs_maxpool_forward", pooled, am, a, n, co, oh, ow, pk, ps)
     return y.to_host(), pooled.to_host(), am.to_host(), (oh, ow, ph, pw)
 
 
 @pytest.mark.parametrize("shape", POOL_SHAPES, ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("floats", [False, True], ids=["ints", "floats"])
-def test_conv2d_maxpool_forward_matches_the_two_ops(hip, shape, floats):
-    """nrs_conv2d_maxpool_forward gives the pooled values, argmax and (when
-    asked) conv output of nrs_conv2d_forward then nrs_maxpool_forward, bit for
-    bit (small integers, with ties the first maximum wins; and f32 data)."""
+@pytest.mark.parametrize("relu", [False, True], ids=["pool", "relu_pool"])
+def test_conv2d_maxpool_forward_matches_the_two_ops(hip, orc, shape, floats, relu):
+    """nrs_conv2d_maxpool_forward (nrs_conv2d_relu_maxpool_forward with relu)
+    gives the pooled values, argmax and (when asked) conv output of
+    nrs_conv2d_forward then (nrs_relu_forward then) nrs_maxpool_forward, bit
+    for bit (small integers, with ties the first maximum wins; and f32 data).
+    The integer case is also checked against the oracle's Conv2d forward, the
+    ReLU and its max pooling."""
     n, ci, co, h, wd, kh, kw, s, p, pk, ps = shape
     rng = np.random.default_rng(n * 100 + ci * 10 + co)
     if floats:
@@ -364,14 +372,19 @@ def test_conv2d_maxpool_forward_matches_the_two_ops(hip, shape, floats):
         x = int_matrix(rng, (n * ci * h * wd,), -2, 2)
         w = int_matrix(rng, (co * ci * kh * kw,), -2, 2)
         b = int_matrix(rng, (co,), -2, 2)
-    y_ref, pool_ref, am_ref, (oh, ow, ph, pw) = _pool_ref(hip, x, w, b, shape, floats)
+    y_ref, pool_ref, am_ref, (oh, ow, ph, pw) = _pool_ref(hip, x, w, b, shape, floats, relu)
+    if not floats:
+        y64, _, _ = orc.conv2d_forward(x, w, b, n, ci, co, h, wd, kh, kw, s, p)
+        a64 = np.where(y64 > 0, y64, 0).astype(np.float32) if relu else y64
+        po, ao = orc.maxpool_forward(a64, n, co, oh, ow, pk, ps)
+        assert np.array_equal(po, pool_ref) and np.array_equal(ao, am_ref)
     D = hip.DeviceBuffer.from_host
+    entry = "nrs_conv2d_relu_maxpool_forward" if relu else "nrs_conv2d_maxpool_forward"
     for with_out in (False, True):
         pooled, am = hip.DeviceBuffer(n * co * ph * pw), hip.DeviceBuffer(n * co * ph * pw, np.int32)
         y = hip.DeviceBuffer(n * co * oh * ow) if with_out else None
-        print(f"conv2d maxpool forward {shape} floats={floats} out={with_out}", flush=True)
-        hip.call("nrs_conv2d_maxpool_forward", pooled, am, y, D(x), D(w), D(b), n, ci, h, wd, co,
-                 kh, kw, s, p, pk, ps)
+        print(f"{entry} {shape} floats={floats} out={with_out}", flush=True)
+        hip.call(entry, pooled, am, y, D(x), D(w), D(b), n, ci, h, wd, co, kh, kw, s, p, pk, ps)
         assert np.array_equal(pooled.to_host(), pool_ref)
         assert np.array_equal(am.to_host(), am_ref)
         if with_out:
@@ -380,43 +393,92 @@ def test_conv2d_maxpool_forward_matches_the_two_ops(hip, shape, floats):
 
 @pytest.mark.parametrize("shape", POOL_SHAPES, ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("with_dx", [False, True], ids=["w_b", "x_w_b"])
-def test_maxpool_conv2d_backward_matches_the_two_ops(hip, orc, shape, with_dx):
+@pytest.mark.parametrize("relu", [False, True], ids=["pool", "relu_pool"])
+def test_maxpool_conv2d_backward_matches_the_two_ops(hip, orc, shape, with_dx, relu):
     """nrs_maxpool_conv2d_backward (weight and bias gradients, and the input
     gradient when asked) equals maxpool_backward into zeros followed by
     nrs_conv2d_backward, bit for bit, accumulating over old values; the
     weight-only form of cfg3 conv1 expands the pooled gradient while loading.
-    Also checked against the oracle's maxpool and conv2d backward on small
+    With relu, nrs_maxpool_relu_conv2d_backward against maxpool_backward,
+    then relu_backward on the conv output, then nrs_conv2d_backward. Also
+    checked against the oracle's maxpool and conv2d backward on small
     integers."""
     n, ci, co, h, wd, kh, kw, s, p, pk, ps = shape
     rng = np.random.default_rng(n * 7 + ci * 3 + co)
     x = int_matrix(rng, (n * ci * h * wd,), -2, 2)
     w = int_matrix(rng, (co * ci * kh * kw,), -2, 2)
     b = np.zeros(co, np.float32)
-    _, _, am, (oh, ow, ph, pw) = _pool_ref(hip, x, w, b, shape, False)
+    y, pooled, am, (oh, ow, ph, pw) = _pool_ref(hip, x, w, b, shape, False, relu)
     gp = int_matrix(rng, (n * co * ph * pw,), -3, 3)
     D = hip.DeviceBuffer.from_host
     old_x, old_w, old_b = (int_matrix(rng, (m,), -3, 3) for m in (x.size, w.size, co))
-    # the two ops
+    # the two (three) ops
     dam = hip.DeviceBuffer.from_host(am, np.int32)
     g = hip.DeviceBuffer.zeros(n * co * oh * ow)
     hip.call("nrs_maxpool_backward", g, D(gp), dam, n, co, oh, ow, pk, ps)
+    if relu:
+        gr = hip.DeviceBuffer(n * co * oh * ow)
+        hip.call("nrs_relu_backward", gr, g, D(y), n * co * oh * ow, 0.0)
+        g = gr
     rx, rw, rb = D(old_x), D(old_w), D(old_b)
     hip.call("nrs_conv2d_backward", rx if with_dx else None, rw, rb, g, D(x), D(w), n, ci, h, wd,
              co, kh, kw, s, p)
     fx, fw, fb = D(old_x), D(old_w), D(old_b)
-    print(f"maxpool conv2d backward {shape} dx={with_dx}", flush=True)
-    hip.call("nrs_maxpool_conv2d_backward", fx if with_dx else None, fw, fb, D(gp), dam, D(x),
-             D(w), n, ci, h, wd, co, kh, kw, s, p, pk, ps)
+    print(f"maxpool conv2d backward {shape} dx={with_dx} relu={relu}", flush=True)
+    if relu:
+        hip.call("nrs_maxpool_relu_conv2d_backward", fx if with_dx else None, fw, fb, D(gp), dam,
+                 D(pooled), D(x), D(w), n, ci, h, wd, co, kh, kw, s, p, pk, ps, 1.0)
+    else:
+        hip.call("nrs_maxpool_conv2d_backward", fx if with_dx else None, fw, fb, D(gp), dam, D(x),
+                 D(w), n, ci, h, wd, co, kh, kw, s, p, pk, ps)
     assert np.array_equal(fw.to_host(), rw.to_host())
     assert np.array_equal(fb.to_host(), rb.to_host())
     if with_dx:
         assert np.array_equal(fx.to_host(), rx.to_host())
-    # the oracle: maxpool backward into zeros, then Conv2d's backward
+    # the oracle: maxpool backward into zeros (gated by conv output > 0 with
+    # the ReLU), then Conv2d's backward
     g_ref = orc.maxpool_backward(gp, am, n * co * oh * ow)
+    if relu:
+        g_ref = np.where(y > 0, g_ref, 0).astype(np.float32)
     _, dw_ref, db_ref = orc.conv2d_backward(x, w, g_ref, n, ci, co, h, wd, kh, kw, s, p)
     assert np.array_equal(fw.to_host(), dw_ref.ravel() + old_w)
     assert np.array_equal(fb.to_host(), db_ref.ravel() + old_b)
     assert np.any(dw_ref != 0)  # the pooled gradient reached the weights
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 4, 8, 8, 3, 3, 1, 1), (3, 1, 32, 28, 28, 3, 3, 1, 1),
+                                   (3, 32, 64, 14, 14, 3, 3, 1, 1), (2, 6, 5, 9, 9, 3, 3, 1, 1),
+                                   (1, 8, 3, 7, 7, 3, 3, 2, 1), (2, 2, 3, 6, 6, 2, 2, 1, 2),
+                                   (1, 40, 70, 6, 7, 3, 3, 1, 1), (2, 16, 24, 11, 10, 3, 3, 2, 1)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("beta_p", [0.0, 0.5])
+@pytest.mark.parametrize("with_dx", [False, True], ids=["dw_db", "dx_dw_db"])
+def test_conv2d_backward_ex_param_beta(hip, orc, shape, beta_p, with_dx):
+    """nrs_conv2d_backward_ex: dweight and dbias = gradient + beta_params *
+    old on every weight-gradient path (chunk-pipelined, slab pair, few-taps,
+    small, slab, split-K GEMM); beta 0 over NaN shows that the old values
+    are not read. dinput takes beta_input 1 (it accumulates)."""
+    n, ci, co, h, w, kh, kw, s, p = shape
+    rng = np.random.default_rng(7 * n + ci + co + h)
+    x = int_matrix(rng, (n * ci * h * w,), -2, 2)
+    wt = int_matrix(rng, (co * ci * kh * kw,), -2, 2)
+    oh, ow = (h + 2 * p - kh) // s + 1, (w + 2 * p - kw) // s + 1
+    g = int_matrix(rng, (n * co * oh * ow,), -2, 2)
+    di_ref, dw_ref, db_ref = orc.conv2d_backward(x, wt, g, n, ci, co, h, w, kh, kw, s, p)
+    if beta_p:
+        ow0, ob0 = int_matrix(rng, (wt.size,), -3, 3), int_matrix(rng, (co,), -3, 3)
+    else:
+        ow0, ob0 = np.full(wt.size, np.nan, np.float32), np.full(co, np.nan, np.float32)
+    di0 = int_matrix(rng, (x.size,), -3, 3)
+    D = hip.DeviceBuffer.from_host
+    ddi, ddw, ddb = D(di0), D(ow0), D(ob0)
+    print(f"conv2d backward ex {shape} beta_params={beta_p} dx={with_dx}", flush=True)
+    hip.call("nrs_conv2d_backward_ex", ddi if with_dx else None, ddw, ddb, D(g), D(x), D(wt),
+             n, ci, h, w, co, kh, kw, s, p, 1.0, beta_p)
+    assert np.array_equal(ddw.to_host(), dw_ref.ravel() + (beta_p * ow0 if beta_p else 0))
+    assert np.array_equal(ddb.to_host(), db_ref.ravel() + (beta_p * ob0 if beta_p else 0))
+    if with_dx:
+        assert np.array_equal(ddi.to_host(), di_ref.ravel() + di0)
 
 
 @pytest.mark.parametrize("shape", [(2, 3, 4, 8, 8, 3, 3, 1, 1), (3, 1, 32, 28, 28, 3, 3, 1, 1),
