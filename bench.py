@@ -9,9 +9,10 @@ peak; conv2d fwd+bwd imgs/s.
   * value     = TFLOP/s over the K timed steps (2*M*N*K per step);
   * roofline  = the GEMM kernel's average duration from HIP events recorded
                 on the library stream around the timed steps;
-  * conv2d    = cfg3 (batch 128: conv1 1->32 3x3 p1, maxpool 2x2, conv2
-                32->64 3x3 p1, forward + backward incl. input grads and
-                split-K weight grads) in imgs/s, as the metric's second half;
+  * conv2d    = cfg3 (batch 128: conv1 1->32 3x3 p1, ReLU, maxpool 2x2,
+                conv2 32->64 3x3 p1, forward + backward incl. input grads and
+                split-K weight grads) in imgs/s, as the metric's second half,
+                timed from C++ through the operator surface (bench_host cnn);
   * cpu_baseline = the reference's CPU path (C restatement of
                 ops::simd::matmul_simd, AVX2 + all host threads) timed on a
                 bounded row sample of the same GEMM.
@@ -115,12 +116,15 @@ def bench_gemm(hip, n, steps, warmup):
 
 
 def bench_conv_cfg3(hip, steps, warmup, closures_only=False):
-    """cfg3 step: conv1 -> maxpool -> conv2, forward + backward: weight and
-    bias gradients of both layers, input gradient of conv2. conv1's input is
-    the image batch, which requires no gradient in the reference's training
-    step (examples/mnist_cuda_cnn.rs:261 sets requires_grad = false, and
-    src/cuda/nn/conv.rs:304 then skips the input gradient); that kernel is
-    timed on its own and reported beside the step."""
+    """cfg3 step: conv1 -> ReLU -> maxpool -> conv2 (the reference CNN's
+    maxpool2d(relu(conv2d(..))), examples/mnist_cuda_cnn.rs:125), forward +
+    backward: weight and bias gradients of both layers, input gradient of
+    conv2. conv1's input is the image batch, which requires no gradient in
+    the reference's training step (examples/mnist_cuda_cnn.rs:261 sets
+    requires_grad = false, and src/cuda/nn/conv.rs:304 then skips the input
+    gradient); that kernel is timed on its own and reported beside the step.
+    The step here issues the C ABI from Python; the same step through the
+    C++ operator surface is bench_host cnn (host_step)."""
     rng = np.random.default_rng(3)
     N, H, W = 128, 28, 28
     x = rng.uniform(0, 1, N * 1 * H * W).astype(np.float32)
@@ -140,31 +144,39 @@ def bench_conv_cfg3(hip, steps, warmup, closures_only=False):
     gw1, gw2 = hip.DeviceBuffer.zeros(w1.size), hip.DeviceBuffer.zeros(w2.size)
     gb1, gb2 = hip.DeviceBuffer.zeros(32), hip.DeviceBuffer.zeros(64)
 
-    # conv1 -> maxpool as one node each way: conv1's output only feeds the
-    # pooling, so the fused forward never writes it and the fused backward
-    # expands the pooled gradient while loading (nrs_conv2d_maxpool_forward /
-    # nrs_maxpool_conv2d_backward); the op-by-op sequence, with its zeroing
-    # launches, is step_unfused
+    a1 = hip.DeviceBuffer(N * 32 * 28 * 28)
+    ga1 = hip.DeviceBuffer.zeros(N * 32 * 28 * 28)
+
+    # conv1 -> ReLU -> maxpool as one node each way: conv1's output only
+    # feeds the pooling, so the fused forward never writes it and the fused
+    # backward expands the pooled gradient while loading, gated by the pooled
+    # value's sign (nrs_conv2d_relu_maxpool_forward /
+    # nrs_maxpool_relu_conv2d_backward). Gradients are written, not added
+    # (beta 0): a training step zeroes them first (zero_grad), and this is
+    # that zeroing and the first accumulation in one. The op-by-op sequence,
+    # with its zeroing launches, is step_unfused.
     def step():
-        hip.call("nrs_conv2d_maxpool_forward", p1.ptr, am.ptr, None, dx.ptr, dw1.ptr, db1.ptr,
-                 N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2)
+        hip.call("nrs_conv2d_relu_maxpool_forward", p1.ptr, am.ptr, None, dx.ptr, dw1.ptr,
+                 db1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2)
         hip.call("nrs_conv2d_forward", y2.ptr, p1.ptr, dw2.ptr, db2.ptr, N, 32, 14, 14, 64, 3, 3, 1, 1)
-        # backward: the pooled activation's gradient is written (beta 0: its
-        # zero_grad and first accumulate_into in one), the parameters' add up
-        hip.call("nrs_conv2d_backward_beta", gp1.ptr, gw2.ptr, gb2.ptr, dg2.ptr, p1.ptr, dw2.ptr,
-                 N, 32, 14, 14, 64, 3, 3, 1, 1, 0.0)
-        hip.call("nrs_maxpool_conv2d_backward", None, gw1.ptr, gb1.ptr, gp1.ptr, am.ptr, dx.ptr,
-                 dw1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2)
+        hip.call("nrs_conv2d_backward_ex", gp1.ptr, gw2.ptr, gb2.ptr, dg2.ptr, p1.ptr, dw2.ptr,
+                 N, 32, 14, 14, 64, 3, 3, 1, 1, 0.0, 0.0)
+        hip.call("nrs_maxpool_relu_conv2d_backward", None, gw1.ptr, gb1.ptr, gp1.ptr, am.ptr,
+                 p1.ptr, dx.ptr, dw1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2, 0.0)
 
     def step_unfused():
+        for buf in (gw1, gb1, gw2, gb2):
+            hip.call("nrs_memset_zero", buf.ptr, buf.nbytes)
         hip.call("nrs_conv2d_forward", y1.ptr, dx.ptr, dw1.ptr, db1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1)
-        hip.call("nrs_maxpool_forward", p1.ptr, am.ptr, y1.ptr, N, 32, 28, 28, 2, 2)
+        hip.call("nrs_relu_forward", a1.ptr, y1.ptr, a1.n)
+        hip.call("nrs_maxpool_forward", p1.ptr, am.ptr, a1.ptr, N, 32, 28, 28, 2, 2)
         hip.call("nrs_conv2d_forward", y2.ptr, p1.ptr, dw2.ptr, db2.ptr, N, 32, 14, 14, 64, 3, 3, 1, 1)
         hip.call("nrs_memset_zero", gp1.ptr, gp1.nbytes)
-        hip.call("nrs_memset_zero", gy1.ptr, gy1.nbytes)
+        hip.call("nrs_memset_zero", ga1.ptr, ga1.nbytes)
         hip.call("nrs_conv2d_backward", gp1.ptr, gw2.ptr, gb2.ptr, dg2.ptr, p1.ptr, dw2.ptr,
                  N, 32, 14, 14, 64, 3, 3, 1, 1)
-        hip.call("nrs_maxpool_backward", gy1.ptr, gp1.ptr, am.ptr, N, 32, 28, 28, 2, 2)
+        hip.call("nrs_maxpool_backward", ga1.ptr, gp1.ptr, am.ptr, N, 32, 28, 28, 2, 2)
+        hip.call("nrs_relu_backward", gy1.ptr, ga1.ptr, y1.ptr, gy1.n, 0.0)
         hip.call("nrs_conv2d_backward", None, gw1.ptr, gb1.ptr, gy1.ptr, dx.ptr, dw1.ptr,
                  N, 1, 28, 28, 32, 3, 3, 1, 1)
 
@@ -183,12 +195,12 @@ def bench_conv_cfg3(hip, steps, warmup, closures_only=False):
                  N, 1, 28, 28, 32, 3, 3, 1, 1)
 
     def conv1_pool_fwd():
-        hip.call("nrs_conv2d_maxpool_forward", p1.ptr, am.ptr, None, dx.ptr, dw1.ptr, db1.ptr,
-                 N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2)
+        hip.call("nrs_conv2d_relu_maxpool_forward", p1.ptr, am.ptr, None, dx.ptr, dw1.ptr,
+                 db1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2)
 
     def conv1_pool_bwd():
-        hip.call("nrs_maxpool_conv2d_backward", None, gw1.ptr, gb1.ptr, gp1.ptr, am.ptr, dx.ptr,
-                 dw1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2)
+        hip.call("nrs_maxpool_relu_conv2d_backward", None, gw1.ptr, gb1.ptr, gp1.ptr, am.ptr,
+                 p1.ptr, dx.ptr, dw1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2, 1.0)
 
     if closures_only:
         return {"conv_fwd_cfg3": conv_fwd, "conv_bwd_cfg3": conv_bwd,
@@ -284,8 +296,9 @@ def host_step(kind, steps, warmup):
     """Runs neuralrs_amd/bench_host (C++, no Python between launches) for
     `kind` ("mlp": the cfg2 step through the C ABI, eager and replayed as a
     HIP graph; "block": the cfg4 TransformerBlock forward + backward through
-    the C++ operator surface) in a child process and returns its JSON, or
-    None when the binary is missing or fails."""
+    the C++ operator surface; "cnn": the cfg3 step through the operator
+    surface) in a child process and returns its JSON, or None when the
+    binary is missing or fails."""
     import subprocess
     exe = os.path.join(ROOT, "neuralrs_amd", "bench_host")
     if not os.path.exists(exe):
@@ -541,20 +554,35 @@ def cpu_baseline_extra():
     OpenMP over images) on a bounded 16-image sample, in imgs/s, and cfg2's
     six MLP GEMMs on the restated CPU autograd matmul, in us per step."""
     import oracle
-    model = "unknown"
+    import subprocess
+    model, cpu_id = "unknown", {}
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
+        lscpu = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in lscpu.splitlines():
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "Model name":
+                model = v
+            elif k in ("CPU family", "Model", "Stepping", "Socket(s)", "Core(s) per socket",
+                       "Thread(s) per core", "CPU(s)"):
+                cpu_id[k] = v
+    except (OSError, subprocess.SubprocessError):
         pass
+    if model == "unknown":
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        model = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
     threads = oracle.max_threads()
     rng = np.random.default_rng(1)
     a = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
     b = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
-    out = {"host_cpu": model, "threads": threads}
+    out = {"host_cpu": model, "lscpu": cpu_id, "threads": threads,
+           "nproc": os.cpu_count()}
     for nt, key in ((0, "matmul_simd_512_gflops"), (1, "matmul_simd_512_gflops_1thread")):
         oracle.matmul_simd(a, b, nt)
         reps, t0 = 0, time.perf_counter()
@@ -584,6 +612,16 @@ def cpu_baseline_extra():
         reps += 1
     dt = (time.perf_counter() - t0) / reps
     out["conv_cfg3_imgs_per_s"] = round(n / dt, 1)
+    # the same sample on one thread
+    oracle.set_threads(1)
+    layers()
+    reps1, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 3.0:
+        layers()
+        reps1 += 1
+    dt1 = (time.perf_counter() - t0) / reps1
+    oracle.set_threads(threads)
+    out["conv_cfg3_imgs_per_s_1thread"] = round(n / dt1, 1)
     # cfg2's six MLP GEMMs on the reference's CPU autograd matmul (forward
     # and backward loops of autograd/graph/matmul.rs, single-threaded as
     # there), on the same shapes as the GPU step
@@ -612,7 +650,8 @@ def cpu_baseline_extra():
                               f"1 thread, {mreps} reps, {mdt * 1e3:.1f} ms each")
     out["conv_cfg3_sample"] = (f"{n} images of cfg3 (conv1 1->32 @28x28, conv2 32->64 @14x14, "
                                f"forward + backward with input, weight and bias grads), "
-                               f"{reps} reps, {dt * 1e3:.1f} ms each")
+                               f"{reps} reps, {dt * 1e3:.1f} ms each on {threads} threads; "
+                               f"{reps1} reps, {dt1 * 1e3:.1f} ms each on 1 thread")
     return out
 
 
@@ -753,16 +792,24 @@ def main():
     }
     if not args.no_conv:
         c = bench_conv_cfg3(hip, max(5, args.steps // 2), args.warmup)
+        hc = host_step("cnn", 50, 10)
         out["conv2d_fwd_bwd"] = {
-            "value": round(c["imgs_per_s"], 1), "unit": "imgs/s",
-            "ms_per_step": round(c["ms_per_step"], 4),
-            "ms_per_step_unfused": round(c["ms_per_step_unfused"], 4),
-            "config": "cfg3 batch 128 conv1 1->32, maxpool, conv2 32->64, fwd+bwd: weight and "
-                      "bias grads of both layers, input grad of conv2 (the image batch requires "
-                      "no grad, as in examples/mnist_cuda_cnn.rs:261); conv1 and the maxpool "
-                      "as one node each way (nrs_conv2d_maxpool_forward / "
-                      "nrs_maxpool_conv2d_backward), the two ops separately in "
-                      "ms_per_step_unfused",
+            "value": round(hc["imgs_per_s"] if hc else c["imgs_per_s"], 1), "unit": "imgs/s",
+            "timing": ("neuralrs_amd/bench_host cnn: the step through the C++ operator surface "
+                       "(nn::conv2d_maxpool with ReLU, nn::conv2d, backward_graph, zero_grad), "
+                       "HIP events on the stream" if hc else
+                       "C ABI calls from Python, wall clock (bench_host missing)"),
+            "step_us": round(hc["step_gpu_us"], 2) if hc else None,
+            "step_us_op_by_op": round(hc["unfused_step_gpu_us"], 2) if hc else None,
+            "c_abi_ms_per_step": round(c["ms_per_step"], 4),
+            "c_abi_ms_per_step_unfused": round(c["ms_per_step_unfused"], 4),
+            "config": "cfg3 batch 128 conv1 1->32 3x3 p1, ReLU, 2x2 maxpool, conv2 32->64 3x3 p1 "
+                      "(the reference CNN's maxpool2d(relu(conv2d(..))), "
+                      "examples/mnist_cuda_cnn.rs:125), fwd+bwd: weight and bias grads of both "
+                      "layers, input grad of conv2 (the image batch requires no grad, as in "
+                      "examples/mnist_cuda_cnn.rs:261); conv1, ReLU and the maxpool as one node "
+                      "each way, op by op in step_us_op_by_op; the conv_* legs time the two conv "
+                      "layers' own passes against their rooflines",
             "conv1_maxpool_fwd_us": round(c["conv1_pool_fwd_us"], 2),
             "maxpool_conv1_bwd_us": round(c["pool_conv1_bwd_us"], 2),
             "conv_fwd_us": round(c["fwd_us"], 2), "conv_bwd_us": round(c["bwd_us"], 2),

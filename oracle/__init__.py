@@ -76,6 +76,7 @@ def lib():
             "orc_gemm_f64_rowset": (None, [ctypes.c_int, f32p, f32p, f64p, f64p, I64, I64, I64,
                                            i64p, I64]),
             "orc_max_threads": (ctypes.c_int, []),
+            "orc_set_threads": (None, [ctypes.c_int]),
             "orc_transpose": (None, [f32p, f32p, I64, I64, I64]),
             "orc_transpose_backward": (None, [f32p, f32p, I64, I64, I64]),
             "orc_scale": (None, [f32p, f32p, ctypes.c_float, I64]),
@@ -432,3 +433,7 @@ def relu_backward(x, g, ga):
 
 def max_threads() -> int:
     return int(lib().orc_max_threads())
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))

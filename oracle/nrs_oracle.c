@@ -783,6 +783,15 @@ EXPORT void orc_relu_backward(const float *x, const float *g, float *ga, int64_t
     for (int64_t i = 0; i < n; ++i) ga[i] = ga[i] + (x[i] > 0.0f ? g[i] : 0.0f);
 }
 
+/* Threads of the OpenMP loops above (the CPU baseline's 1-thread figures). */
+EXPORT void orc_set_threads(int n) {
+#ifdef _OPENMP
+    omp_set_num_threads(n > 0 ? n : 1);
+#else
+    (void)n;
+#endif
+}
+
 EXPORT int orc_max_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();
