@@ -374,8 +374,8 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
         hip.call("nrs_attention_forward", fo, fst, fq, fk, fv, Bf, Hf, T, Dh, ldf, sc)
 
     def fused_bwd():
-        hip.call("nrs_attention_backward", fdq, fdk, fdv, fdo, fq, fk, fv, fst, Bf, Hf, T, Dh,
-                 ldf, sc, 0.0)
+        hip.call("nrs_attention_backward", fdq, fdk, fdv, fdo, fo, fq, fk, fv, fst, Bf, Hf, T,
+                 Dh, ldf, sc, 0.0)
 
     # the heads of the projections [32*128, 8*32] split into [8, 4096, 32]
     # (q, k, v) and the attention output merged back: one launch each, in

@@ -228,9 +228,12 @@ int nrs_bmm_backward(int layout, float *dA, float *dB, const float *G, const flo
  *   max_j u_j and sum_j 2^(u_j - max) with u = scale * log2(e) * q . k^T; the
  *   backward recomputes the probabilities from them (the S x S matrix is
  *   never stored).
- * The fused path takes seq <= 128 and d_head 16 or 32
- * (nrs_attention_supported); other shapes are refused with NRS_ERR_ARG and
- * the caller composes bmm / softmax / bmm instead.                          */
+ * The fused path takes d_head 16 or 32 and seq up to 16384
+ * (nrs_attention_supported): up to 128 one workgroup per (item, head) holds
+ * the whole sequence; past it the keys stream through in tiles of 128 with
+ * the softmax taken online, so no S x S matrix exists in any form (the
+ * stats are the final max and sum of each row). Other shapes are refused
+ * with NRS_ERR_ARG and the caller composes bmm / softmax / bmm instead.    */
 int nrs_attention_supported(int64_t batch, int64_t heads, int64_t seq, int64_t d_head, int64_t ld);
 int nrs_attention_forward(float *out, float *stats, const float *q, const float *k, const float *v,
                           int64_t batch, int64_t heads, int64_t seq, int64_t d_head, int64_t ld,
@@ -240,11 +243,15 @@ int nrs_attention_forward(float *out, float *stats, const float *q, const float 
  * stats: dq = dS . k, dk = dS^T . q, dv = P^T . dout with P recomputed and
  * dS = (P * (dP - rowsum(P * dP))) * scale, dP = dout . v^T; each gradient
  * = computed + beta * old (beta = 1 is accumulate_into). Same layouts as the
- * forward; dq, dk, dv must not overlap each other or the inputs.            */
-int nrs_attention_backward(float *dq, float *dk, float *dv, const float *dout, const float *q,
-                           const float *k, const float *v, const float *stats, int64_t batch,
-                           int64_t heads, int64_t seq, int64_t d_head, int64_t ld, float scale,
-                           float beta);
+ * forward; dq, dk, dv must not overlap each other or the inputs. out is the
+ * forward's output, required past seq 128 (rowsum(P * dP) = dout . out per
+ * row, so the key tiles need no other tiles' scores) and unused up to it.
+ * Past 128, each key tile's dq part goes to library scratch and a second
+ * launch adds the parts in key-tile order (deterministic).                 */
+int nrs_attention_backward(float *dq, float *dk, float *dv, const float *dout, const float *out,
+                           const float *q, const float *k, const float *v, const float *stats,
+                           int64_t batch, int64_t heads, int64_t seq, int64_t d_head, int64_t ld,
+                           float scale, float beta);
 
 /* ---------------------------------------------------------------- conv2d */
 /* The five primitive launches of src/cuda/nn/conv.rs:161-236, same index

@@ -58,7 +58,7 @@ SIGNATURES = {
     "nrs_bmm_backward": [ctypes.c_int, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F],
     "nrs_attention_supported": [_I, _I, _I, _I, _I],
     "nrs_attention_forward": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F],
-    "nrs_attention_backward": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F],
+    "nrs_attention_backward": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F],
     "nrs_im2col": [_P, _P] + [_I] * 8,
     "nrs_col2out": [_P, _P, _P, _I, _I, _I, _I],
     "nrs_out2mm": [_P, _P, _I, _I, _I, _I],

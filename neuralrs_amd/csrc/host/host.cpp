@@ -896,15 +896,17 @@ NodeRef fused_attention(const NodeRef& q, const NodeRef& k, const NodeRef& v, si
                                 vg.data.ptr(), batch, heads, seq, dh, ld, scale),
           "attention: launch failed");
     NodeRef node = make_output(q->shape, {q, k, v}, std::move(out));
-    node->backward_fn = [grad = node->gpu->grad, q, k, v, stats, len, batch, heads, seq, dh, ld,
-                         scale](const std::vector<float>&) {
+    Node* self = node.get();  // the output (read by the backward of long sequences)
+    node->backward_fn = [grad = node->gpu->grad, self, q, k, v, stats, len, batch, heads, seq, dh,
+                         ld, scale](const std::vector<float>&) {
         GpuBuffers& qg = gpu_of(q, "attention bwd: q not on GPU");
         GpuBuffers& kg = gpu_of(k, "attention bwd: k not on GPU");
         GpuBuffers& vg = gpu_of(v, "attention bwd: v not on GPU");
+        const float* o = self->gpu->data.ptr();
         if (qg.grad != kg.grad && kg.grad != vg.grad && qg.grad != vg.grad) {
             const float beta = joint_beta({qg.grad.get(), kg.grad.get(), vg.grad.get()});
             check(nrs_attention_backward(qg.grad->write_target(), kg.grad->write_target(),
-                                         vg.grad->write_target(), grad->ptr(), qg.data.ptr(),
+                                         vg.grad->write_target(), grad->ptr(), o, qg.data.ptr(),
                                          kg.data.ptr(), vg.data.ptr(), stats->ptr(), batch, heads,
                                          seq, dh, ld, scale, beta),
                   "attention bwd: launch");
@@ -912,7 +914,7 @@ NodeRef fused_attention(const NodeRef& q, const NodeRef& k, const NodeRef& v, si
         }
         // q, k or v are one node: the gradients go to temporaries, then add up
         DeviceBuffer tq(len, false), tk(len, false), tv(len, false);
-        check(nrs_attention_backward(tq.ptr(), tk.ptr(), tv.ptr(), grad->ptr(), qg.data.ptr(),
+        check(nrs_attention_backward(tq.ptr(), tk.ptr(), tv.ptr(), grad->ptr(), o, qg.data.ptr(),
                                      kg.data.ptr(), vg.data.ptr(), stats->ptr(), batch, heads, seq,
                                      dh, ld, scale, 0.0f),
               "attention bwd: launch");

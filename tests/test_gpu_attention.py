@@ -55,8 +55,8 @@ def run(hip, batch, heads, seq, d, ld, beta, seed):
     print(f"attention b{batch} h{heads} s{seq} d{d} ld{ld} beta{beta}", flush=True)
     hip.call("nrs_attention_forward", out, stats, dq_, dk_, dv_, batch, heads, seq, d, ld, scale)
     gq, gk, gv = (hip.DeviceBuffer.from_host(x) for x in old)
-    hip.call("nrs_attention_backward", gq, gk, gv, do_, dq_, dk_, dv_, stats, batch, heads, seq,
-             d, ld, scale, beta)
+    hip.call("nrs_attention_backward", gq, gk, gv, do_, out, dq_, dk_, dv_, stats, batch, heads,
+             seq, d, ld, scale, beta)
     o64, dq64, dk64, dv64 = ref_f64(*(heads_view(x, batch, heads, seq, d, ld) for x in (q, k, v, dout)),
                                     float(scale))
     L = max(seq, d)
@@ -83,6 +83,12 @@ def run(hip, batch, heads, seq, d, ld, beta, seed):
     (4, 1, 17, 32, 32),      # attention_batch on [batch, seq, d] (one head)
     (1, 1, 1, 16, 16),       # a single query and key
     (2, 2, 65, 32, 64),
+    # past 128: key tiles streamed with an online softmax, dQ parts summed
+    (2, 1, 129, 32, 40),     # one key past the first tile
+    (1, 2, 256, 16, 32),     # two whole tiles, d_head 16
+    (2, 2, 200, 32, 64),     # ragged second tile
+    (1, 1, 300, 32, 32),     # three tiles
+    (1, 4, 512, 32, 128),    # four tiles, four heads in place
 ], ids=lambda s: "b{}h{}s{}d{}ld{}".format(*s))
 @pytest.mark.parametrize("beta", [0.0, 1.0])
 def test_attention_fused_vs_f64(hip, shape, beta):
@@ -103,19 +109,22 @@ def test_attention_stats_are_softmax_max_and_sum(hip):
     assert np.abs(st[..., 1] - tot).max() <= 1e-5 * tot.max()
 
 
-def test_attention_matches_oracle_composition(hip, orc):
-    """cfg4 heads, the first two batch items: the oracle's CPU ops composed as
-    MultiHeadAttention runs them (slice_cols per head, transpose(k), bmm,
-    scale, softmax, bmm), forward and backward, at the reference's 1e-3."""
-    batch, heads, seq, d, ld = 2, 8, 128, 32, 256
+@pytest.mark.parametrize("shape", [(2, 8, 128, 32, 256), (1, 2, 320, 32, 64)],
+                         ids=["cfg4_heads", "seq320_tiled"])
+def test_attention_matches_oracle_composition(hip, orc, shape):
+    """cfg4 heads, the first two batch items (and a tiled sequence of 320):
+    the oracle's CPU ops composed as MultiHeadAttention runs them (slice_cols
+    per head, transpose(k), bmm, scale, softmax, bmm), forward and backward,
+    at the reference's 1e-3."""
+    batch, heads, seq, d, ld = shape
     st, (q, k, v, dout, scale) = run(hip, batch, heads, seq, d, ld, 0.0, seed=44)
     out = hip.DeviceBuffer(batch * seq * ld)
     stats = hip.DeviceBuffer(batch * heads * seq * 2)
     dq_, dk_, dv_, do_ = (hip.DeviceBuffer.from_host(x) for x in (q, k, v, dout))
     hip.call("nrs_attention_forward", out, stats, dq_, dk_, dv_, batch, heads, seq, d, ld, scale)
     gq, gk, gv = (hip.DeviceBuffer.zeros(batch * seq * ld) for _ in range(3))
-    hip.call("nrs_attention_backward", gq, gk, gv, do_, dq_, dk_, dv_, stats, batch, heads, seq,
-             d, ld, scale, 0.0)
+    hip.call("nrs_attention_backward", gq, gk, gv, do_, out, dq_, dk_, dv_, stats, batch, heads,
+             seq, d, ld, scale, 0.0)
     o, gqh, gkh, gvh = (x.to_host((batch * seq, ld)) for x in (out, gq, gk, gv))
     rows = batch * seq
     for h in range(heads):
@@ -143,8 +152,34 @@ def test_attention_unsupported_shapes_refused(hip):
     """Shapes outside the fused path are refused before any launch (the host
     layer composes bmm / softmax / bmm for those)."""
     assert hip.load().nrs_attention_supported(32, 8, 128, 32, 256) == 1
-    for shape in ((1, 1, 129, 32, 32), (1, 1, 8, 24, 24), (1, 2, 8, 32, 40), (1, 1, 8, 64, 64)):
+    assert hip.load().nrs_attention_supported(2, 8, 4096, 32, 256) == 1
+    for shape in ((1, 1, 16385, 32, 32), (1, 1, 8, 24, 24), (1, 2, 8, 32, 40), (1, 1, 8, 64, 64)):
         assert hip.load().nrs_attention_supported(*shape) == 0
         buf = hip.DeviceBuffer(4096)
         with pytest.raises(hip.NrsError, match="unsupported"):
             hip.call("nrs_attention_forward", buf, buf, buf, buf, buf, *shape, 1.0)
+
+
+def test_attention_tiled_backward_deterministic_and_needs_out(hip):
+    """Past 128 the dQ parts of the key tiles are added in a fixed order: two
+    backward calls give the same bits; without the forward output the call
+    is refused (its row term dout . out is what lets a key tile work alone)."""
+    batch, heads, seq, d, ld = 2, 2, 300, 32, 64
+    rng = np.random.default_rng(3)
+    q, k, v, dout = (hip.DeviceBuffer.from_host(rng.standard_normal((batch * seq, ld)).astype(np.float32))
+                     for _ in range(4))
+    out, stats = hip.DeviceBuffer(batch * seq * ld), hip.DeviceBuffer(batch * heads * seq * 2)
+    scale = np.float32(1.0 / np.sqrt(d))
+    hip.call("nrs_attention_forward", out, stats, q, k, v, batch, heads, seq, d, ld, scale)
+    res = []
+    for _ in range(2):
+        g = [hip.DeviceBuffer.zeros(batch * seq * ld) for _ in range(3)]
+        hip.call("nrs_attention_backward", *g, dout, out, q, k, v, stats, batch, heads, seq, d, ld,
+                 scale, 0.0)
+        res.append([x.to_host() for x in g])
+    for a, b in zip(*res):
+        assert np.array_equal(a, b)
+    g = [hip.DeviceBuffer.zeros(batch * seq * ld) for _ in range(3)]
+    with pytest.raises(hip.NrsError, match="forward output"):
+        hip.call("nrs_attention_backward", *g, dout, None, q, k, v, stats, batch, heads, seq, d,
+                 ld, scale, 0.0)
