@@ -327,7 +327,9 @@ __global__ __launch_bounds__(256) void conv_img_kernel(ImgArgs a) {
     }
 }
 
-constexpr int kImgLdsBytes = 160 * 1024;
+// LDS of one workgroup: at most 160 KiB (gfx950's whole LDS), and no more
+// than the device allows.
+size_t img_lds_budget() { return std::min<size_t>(160 * 1024, lds_limit()); }
 
 template <int PAD, int MB, int NSW, bool FLIP>
 int launch_img(const ImgArgs& a, int64_t N, size_t lds) {
@@ -335,7 +337,8 @@ int launch_img(const ImgArgs& a, int64_t N, size_t lds) {
     static bool attr_set = false;
     if (!attr_set) {
         NRS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, kImgLdsBytes));
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)img_lds_budget()));
         attr_set = true;
     }
     hipLaunchKernelGGL(fn, dim3((unsigned)N, (unsigned)((a.M + MB - 1) / MB)), dim3(256), lds,
@@ -380,7 +383,7 @@ int img_conv(const SlabConv& s) {
     const int wrow = s.C * 9 + 4;
     // (the epilogue's [MB][P] output tile reuses the image planes)
     const size_t lds = 4 * std::max((size_t)4 * qpitch + (size_t)MB * wrow, (size_t)MB * P);
-    if (lds > kImgLdsBytes) return kSlabUnsupported;
+    if (lds > img_lds_budget()) return kSlabUnsupported;
     ImgArgs a;
     a.x = s.x;
     a.w = s.w;

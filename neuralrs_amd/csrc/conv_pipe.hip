@@ -450,20 +450,27 @@ __global__ __launch_bounds__(256) void conv_pipe_kernel(PipeArgs a) {
     }
 }
 
-constexpr int kPipeLdsMax = 160 * 1024;
+// Dynamic LDS of a launch: two chunk buffers of the input-gradient blocks,
+// and with weight-gradient blocks their two image buffers and pixel-offset
+// table.
+size_t pipe_lds(bool has_w) {
+    return sizeof(float) * (size_t)(has_w ? std::max(2 * kPWBuf + 4 * kPGrow, 2 * kPDBuf) : 2 * kPDBuf);
+}
+
+// Whether the device gives one workgroup that much LDS.
+bool pipe_lds_fits(bool has_w) { return pipe_lds(has_w) <= lds_limit(); }
 
 template <bool FLIP, bool HAS_W>
 int launch_pipe(const PipeArgs& a) {
     auto fn = conv_pipe_kernel<FLIP, HAS_W>;
+    const size_t lds = pipe_lds(a.nw > 0);
     static bool attr_set = false;
     if (!attr_set) {
         NRS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, kPipeLdsMax));
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)pipe_lds(HAS_W)));
         attr_set = true;
     }
-    // W blocks: two image buffers and the pixel-offset table
-    const size_t lds = sizeof(float) * (size_t)(a.nw > 0 ? std::max(2 * kPWBuf + 4 * kPGrow, 2 * kPDBuf)
-                                                         : 2 * kPDBuf);
     hipLaunchKernelGGL(fn, dim3((unsigned)(a.nw + a.nd)), dim3(256), lds, stream(), a);
     NRS_LAUNCH_CHECK("conv2d (chunk-pipelined)");
     return NRS_OK;
@@ -482,7 +489,7 @@ int pipe_conv(const SlabConv& s) {
     if (!pipe_geometry(s.kh, s.kw, s.stride, s.pad_h, s.pad_w, s.H, s.W, s.OH, s.OW) ||
         s.C % kPCC != 0 || s.C <= 0 || s.M % kPMB != 0 || s.M <= 0 || s.N <= 0 ||
         s.N * (s.M / kPMB) > 0x7fffffff || s.N * (int64_t)std::max(s.C, s.M) * s.H * s.W > 0x1fffffff ||
-        ((uintptr_t)s.x & 7) != 0 || ((uintptr_t)s.out & 15) != 0)
+        ((uintptr_t)s.x & 7) != 0 || ((uintptr_t)s.out & 15) != 0 || !pipe_lds_fits(false))
         return kSlabUnsupported;
     PipeArgs a{};
     a.dimg = s.x;
@@ -504,7 +511,7 @@ int pipe_backward(const SlabConv* d, const SlabWgrad& w) {
     if (!pipe_geometry(w.kh, w.kw, w.stride, w.pad, w.pad, w.H, w.W, w.OH, w.OW) || !w.dw ||
         w.C % kPMB != 0 || w.C <= 0 || w.M % kPWM != 0 || w.M <= 0 || w.N <= 0 ||
         w.N * (int64_t)std::max(w.C, w.M) * w.H * w.W > 0x1fffffff || ((uintptr_t)w.x & 7) != 0 ||
-        ((uintptr_t)w.g & 15) != 0)
+        ((uintptr_t)w.g & 15) != 0 || !pipe_lds_fits(true))
         return kSlabUnsupported;
     if (d && (d->x != w.g || d->C != w.M || d->M != w.C || !d->flip || ((uintptr_t)d->out & 15) != 0))
         return kSlabUnsupported;

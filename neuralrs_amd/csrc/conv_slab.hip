@@ -419,7 +419,9 @@ __global__ __launch_bounds__(256) void pack_slab_weights_kernel(
     }
 }
 
-constexpr int kLdsBytes = 160 * 1024;
+// LDS of one workgroup: at most 160 KiB (gfx950's whole LDS), and no more
+// than the device allows.
+int64_t lds_budget() { return (int64_t)std::min<size_t>(160 * 1024, lds_limit()); }
 
 int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
@@ -431,7 +433,7 @@ struct SlabPlan {
 };
 
 template <int WM, int WN, int MSW, int NSW>
-SlabPlan plan_slab(const SlabConv& s, int64_t lds_cap = kLdsBytes) {
+SlabPlan plan_slab(const SlabConv& s, int64_t lds_cap) {
     using Cfg = SlabCfg<WM, WN, MSW, NSW>;
     SlabPlan pl;
     const int64_t P = (int64_t)s.OH * s.OW, taps = (int64_t)s.kh * s.kw;
@@ -459,7 +461,7 @@ SlabPlan plan_slab(const SlabConv& s, int64_t lds_cap = kLdsBytes) {
     while (CC > 16 && bytes(CC) > lds_cap) CC -= 16;
     const int64_t grid_x = s.N * pl.nb, grid_y = (s.M + Cfg::BM - 1) / Cfg::BM;
     // (the weight block's byte offsets must fit the buffer loads' 31 bits)
-    if (bytes(CC) > kLdsBytes || grid_x > INT32_MAX || grid_y > 65535 ||
+    if (bytes(CC) > lds_budget() || grid_x > INT32_MAX || grid_y > 65535 ||
         pl.slab_rows * pl.slab_w * (CC / 4) > INT32_MAX / 2 ||
         Cfg::BM * (taps * CC + 4) > INT32_MAX / 4)
         return SlabPlan{};
@@ -467,7 +469,7 @@ SlabPlan plan_slab(const SlabConv& s, int64_t lds_cap = kLdsBytes) {
     // the epilogue's per-wave tiles reuse the same LDS
     const int64_t tile = (int64_t)(Cfg::NT / 64) * (16 * MSW) * (16 * NSW + 4) * 4;
     pl.lds = (size_t)std::max<int64_t>(bytes(CC), tile);
-    if (pl.lds > kLdsBytes) return SlabPlan{};
+    if ((int64_t)pl.lds > lds_budget()) return SlabPlan{};
     return pl;
 }
 
@@ -525,12 +527,13 @@ int prepare_slab(const SlabConv& s, const SlabPlan& pl, SlabArgs& a, unsigned& g
     return NRS_OK;
 }
 
-// Raises a kernel's dynamic LDS limit to the whole 160 KB, once per process.
+// Raises a kernel's dynamic LDS limit to the LDS budget, once per process.
 template <typename F>
 int allow_full_lds(F fn, bool& done) {
     if (!done) {
         NRS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes));
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)lds_budget()));
         done = true;
     }
     return NRS_OK;
@@ -576,8 +579,8 @@ int launch_pair(const SlabConv& s, const SlabPlan& pl, const WgradPlan& wp) {
 // weight gradient's workgroups (one per CU) that keeps the input gradient to
 // one round of wide tiles instead of two rounds of narrow ones.
 int pick_slab(const SlabConv& s, SlabPlan& pl, bool chunked = false) {
-    constexpr size_t kHalf = kLdsBytes / 2;
-    const int64_t cap = chunked ? (int64_t)kHalf : kLdsBytes;
+    const size_t kHalf = (size_t)lds_budget() / 2;
+    const int64_t cap = chunked ? (int64_t)kHalf : lds_budget();
     const SlabPlan p64 = s.M >= 48 ? plan_slab<4, 1, 1, 7>(s, cap) : SlabPlan{};
     const SlabPlan p32 = s.M > 16 ? plan_slab<2, 2, 1, 4>(s, cap) : SlabPlan{};
     const SlabPlan p16 = plan_slab<1, 4, 1, 2>(s, cap);

@@ -74,7 +74,9 @@ __global__ __launch_bounds__(64 * kSumGroups) void wgrad_sum_kernel(
     }
 }
 
-constexpr int kLdsBytes = 160 * 1024;
+// LDS of one workgroup: at most 160 KiB (gfx950's whole LDS), and no more
+// than the device allows.
+int64_t lds_budget() { return (int64_t)std::min<size_t>(160 * 1024, lds_limit()); }
 
 }  // namespace
 
@@ -95,8 +97,8 @@ int plan_slab_wgrad(const SlabWgrad& s, WgradPlan& p) {
         return 4 * (kWgM * (KP + 4) + KP + kWgC * CS);
     };
     int64_t band_rows = s.OH, KP = 0, CS = 0, slab_rows = 0;
-    while (band_rows > 1 && lds_bytes(band_rows, KP, CS, slab_rows) > kLdsBytes) --band_rows;
-    if (lds_bytes(band_rows, KP, CS, slab_rows) > kLdsBytes) return kSlabUnsupported;
+    while (band_rows > 1 && lds_bytes(band_rows, KP, CS, slab_rows) > lds_budget()) --band_rows;
+    if (lds_bytes(band_rows, KP, CS, slab_rows) > lds_budget()) return kSlabUnsupported;
     const int64_t bands = (s.OH + band_rows - 1) / band_rows;
     const int64_t slices = s.N * bands;
     const int64_t cparts = (s.C + kWgC - 1) / kWgC, ntg = (taps + kTapw - 1) / kTapw;
@@ -169,7 +171,8 @@ int slab_wgrad(const SlabWgrad& s) {
     static bool attr_set[2] = {false, false};
     if (!attr_set[p.a.vec_g]) {
         NRS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes));
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)lds_budget()));
         attr_set[p.a.vec_g] = true;
     }
     hipLaunchKernelGGL(fn, dim3(p.gx, p.gy, p.gz), dim3(256), p.lds, stream(), p.a);

@@ -701,10 +701,22 @@ int nrs_linear_cross_entropy(float* logits, float* grad, const float* x, const f
     if (batch == 0) return NRS_OK;
     NRS_ARG_CHECK(logits && grad && target && (in_f == 0 || (x && w)),
                   "linear cross_entropy: null pointer");
+    // Both outputs are written while other workgroups still read x, w, the
+    // bias and the targets, so no output may share memory with an input or
+    // with the other output.
     const size_t out_bytes = sizeof(float) * (size_t)(batch * classes);
-    NRS_ARG_CHECK(!nrs::overlaps(logits, out_bytes, grad, out_bytes) &&
-                      !nrs::overlaps(grad, out_bytes, target, out_bytes),
-                  "linear cross_entropy: logits, grad and target must not overlap");
+    const size_t x_bytes = sizeof(float) * (size_t)(batch * in_f);
+    const size_t w_bytes = sizeof(float) * (size_t)(in_f * classes);
+    const size_t b_bytes = bias ? sizeof(float) * (size_t)classes : 0;
+    for (float* dst : {logits, grad}) {
+        NRS_ARG_CHECK(!nrs::overlaps(dst, out_bytes, x, x_bytes) &&
+                          !nrs::overlaps(dst, out_bytes, w, w_bytes) &&
+                          !nrs::overlaps(dst, out_bytes, bias, b_bytes) &&
+                          !nrs::overlaps(dst, out_bytes, target, out_bytes),
+                      "linear cross_entropy: logits and grad must not overlap x, w, bias or target");
+    }
+    NRS_ARG_CHECK(!nrs::overlaps(logits, out_bytes, grad, out_bytes),
+                  "linear cross_entropy: logits and grad must not overlap");
     nrs::GemmCall c;
     c.layout = NRS_NN;
     c.C = logits;
@@ -718,12 +730,7 @@ int nrs_linear_cross_entropy(float* logits, float* grad, const float* x, const f
     bool empty;
     const int rc = nrs::check_call(c, empty);
     if (rc != NRS_OK) return rc;
-    nrs::OperandRange seed_out{grad, out_bytes};
-    if (classes <= 16 && nrs::wsplit_eligible(c, false) &&
-        nrs::outputs_independent(&c, 1, nullptr) &&
-        !nrs::overlaps(grad, out_bytes, x, sizeof(float) * (size_t)(batch * in_f)) &&
-        !nrs::overlaps(grad, out_bytes, w, sizeof(float) * (size_t)(in_f * classes))) {
-        (void)seed_out;
+    if (classes <= 16 && nrs::wsplit_eligible(c, false)) {
         nrs::WsExtra e;
         e.ce_grad = grad;
         e.ce_target = target;

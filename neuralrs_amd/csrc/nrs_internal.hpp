@@ -43,6 +43,14 @@ int zero_fill(void* ptr, size_t bytes);
 // Number of compute units of the current device (queried once).
 int num_cus();
 
+// LDS bytes one workgroup may allocate dynamically on the current device:
+// the larger of its per-block and opt-in maxima, queried by nrs_init
+// (160 KiB on gfx950). Kernels whose dynamic LDS would exceed it are not
+// launched; their planners report the shape unsupported so that another
+// path takes the call. Static LDS needs no such check: the compiler refuses
+// a kernel whose static LDS exceeds the target's limit.
+size_t lds_limit();
+
 }  // namespace nrs
 
 #define NRS_REQUIRE_INIT()                                                           \

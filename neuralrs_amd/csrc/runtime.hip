@@ -2,6 +2,7 @@
 // errors and the library's lazily grown scratch. Replaces the reference's
 // process-global cudarc backend (src/cuda/backend.rs:10-42) and the
 // residency helpers of src/cuda/runtime.rs:39-124.
+#include <algorithm>
 #include <cstdarg>
 #include <cstring>
 #include <unordered_map>
@@ -21,6 +22,7 @@ constexpr int kSlots = 7;
 constexpr int kMaxDevices = 64;
 static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
 float* g_scratch_ptr[kMaxDevices] = {};
+size_t g_lds_limit[kMaxDevices] = {};
 
 struct State {
     bool init = false;
@@ -108,6 +110,9 @@ int num_cus() {
     return cus;
 }
 int device() { return g.device; }
+size_t lds_limit() {
+    return g.device >= 0 && g.device < kMaxDevices ? g_lds_limit[g.device] : 0;
+}
 bool initialized() { return g.init; }
 
 float* noalloc_scratch() {
@@ -180,6 +185,15 @@ int nrs_init(int device) {
         NRS_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(nrs::scratch)));
         NRS_ARG_CHECK(ptr != nullptr, "nrs_init: no device address for the scratch array");
         nrs::g_scratch_ptr[device] = static_cast<float*>(ptr);
+    }
+    if (!nrs::g_lds_limit[device]) {
+        int per_block = 0, opt_in = 0;
+        NRS_HIP_CHECK(hipDeviceGetAttribute(&per_block, hipDeviceAttributeMaxSharedMemoryPerBlock,
+                                            device));
+        if (hipDeviceGetAttribute(&opt_in, hipDeviceAttributeSharedMemPerBlockOptin, device) !=
+            hipSuccess)
+            opt_in = 0;
+        nrs::g_lds_limit[device] = (size_t)std::max(std::max(per_block, opt_in), 0);
     }
     g.device = device;
     g.init = true;

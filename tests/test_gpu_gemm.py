@@ -613,6 +613,18 @@ def test_linear_cross_entropy_errors(hip):
     buf = hip.DeviceBuffer(64)
     with pytest.raises(hip.NrsError):  # the seed would overwrite the logits
         hip.call("nrs_linear_cross_entropy", buf, buf, buf, buf, None, buf, 4, 2, 3)
+    # Each output against each input, one hazard per call, on the fused
+    # (3 classes) and the two-launch (40 classes) paths.
+    for classes in (3, 40):
+        names = ("logits", "grad", "x", "w", "bias", "target")
+        sizes = (4 * classes, 4 * classes, 4 * 2, 2 * classes, classes, 4 * classes)
+        for out_i in (0, 1):
+            for in_i in (2, 3, 4, 5):
+                bufs = [hip.DeviceBuffer(n) for n in sizes]
+                bufs[in_i] = bufs[out_i]
+                with pytest.raises(hip.NrsError, match="must not overlap"):
+                    hip.call("nrs_linear_cross_entropy", *bufs, 4, 2, classes)
+                print("refused", names[out_i], "over", names[in_i], classes)
     with pytest.raises(hip.NrsError):
         hip.call("nrs_linear_backward_relu", buf, buf, None, buf, buf, buf, None, 4, 2, 3,
                  0.0, 0.0, 0.0)
