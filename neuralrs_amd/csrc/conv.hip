@@ -1283,9 +1283,12 @@ int slab_dgrad(float* dinput, const float* grad, const float* weight, int64_t N,
             return rc;
         }
     } else {
-        // small 3x3 images: the gradient image resident in LDS, the weights
-        // flipped while they are staged (no packing launch)
-        int rc = pipe_conv(s);
+        // small 3x3 images: Winograd F(2x2, 3x3) over the flipped weights,
+        // else the gradient image resident in LDS, the weights flipped while
+        // they are staged (no packing launch)
+        int rc = wino_conv(s);
+        if (rc != kSlabUnsupported) return rc;
+        rc = pipe_conv(s);
         if (rc != kSlabUnsupported) return rc;
         rc = img_conv(s);
         if (rc != kSlabUnsupported) return rc;
@@ -1590,7 +1593,10 @@ int nrs_conv2d_forward(float* out, const float* input, const float* weight, cons
         s.OH = (int)d.out_h;
         s.OW = (int)d.out_w;
         if (c_out <= INT32_MAX && d.out_h <= INT32_MAX && d.out_w <= INT32_MAX) {
-            // small 3x3 images: the whole image resident in LDS
+            // small "same" 3x3 images: Winograd F(2x2, 3x3) on the matrix
+            // cores, else the whole image resident in LDS
+            rc = nrs::wino_conv(s);
+            if (rc != nrs::kSlabUnsupported) return rc;
             rc = nrs::pipe_conv(s);
             if (rc != nrs::kSlabUnsupported) return rc;
             rc = nrs::img_conv(s);

@@ -38,6 +38,12 @@ int slab_conv(const SlabConv& s);
 // (launching nothing) for other shapes.
 int img_conv(const SlabConv& s);
 
+// The same convolution by Winograd F(2x2, 3x3) (conv_wino.hip), for "same"
+// 3x3 stride-1 layers over images of at most 16x16 with an even width,
+// C % 8 == 0 and M % 32 == 0; kSlabUnsupported (launching nothing) for
+// other shapes.
+int wino_conv(const SlabConv& s);
+
 // The same convolution, chunk-pipelined (conv_pipe.hip), for "same" 3x3
 // stride-1 layers over images of at most 14x14 (even width >= 4, whole pixel
 // quads) with C % 16 == 0 and M % 32 == 0; kSlabUnsupported (launching

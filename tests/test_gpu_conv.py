@@ -56,6 +56,11 @@ CONV_SHAPES = [  # (n, c_in, c_out, h, w, kh, kw, stride, pad)
     (2, 96, 64, 10, 10, 3, 3, 1, 1),  # three output blocks each way, six forward chunks
     (3, 16, 64, 4, 4, 3, 3, 1, 1),    # forward only (16 input channels), one row tile per wave
     (1, 32, 64, 2, 8, 3, 3, 1, 1),    # two rows: most row tiles clamped
+    # Winograd F(2x2,3x3) forward ("same" 3x3, C % 16 == 0, M % 32 == 0, even width <= 16)
+    (2, 16, 32, 7, 8, 3, 3, 1, 1),    # odd height: the last tile row's second row clipped
+    (2, 32, 32, 16, 16, 3, 3, 1, 1),  # 8x8 tiles: every tile block full
+    (3, 16, 96, 9, 2, 3, 3, 1, 1),    # one tile per row, three output-channel groups
+    (2, 48, 32, 15, 14, 3, 3, 1, 1),  # three channel chunks, 56 tiles
 ]
 ids = ["x".join(map(str, s)) for s in CONV_SHAPES]
 
@@ -183,10 +188,13 @@ def test_conv2d_backward_without_input_grad(hip, orc):
     (2, 20, 32, 9, 7, 3, 3, 1, 1),    # ragged input-channel block
     (2, 16, 32, 12, 12, 3, 3, 1, 0),  # the flipped convolution pads by 2
     (2, 8, 16, 10, 10, 3, 3, 1, 2),   # ... and by 0
-], ids=["cfg3-conv2", "ragged", "pad0", "pad2"])
+    (2, 32, 16, 7, 8, 3, 3, 1, 1),    # flipped Winograd: odd height, 16 gradient channels
+    (2, 64, 24, 16, 16, 3, 3, 1, 1),  # flipped Winograd: 16x16, three 8-channel chunks
+], ids=["cfg3-conv2", "ragged", "pad0", "pad2", "wino-odd", "wino-16x16"])
 def test_conv2d_backward_input_grad_only(hip, orc, shape):
-    """dweight = dbias = NULL: the input gradient alone (the image-resident
-    flipped convolution for these shapes), accumulated into dinput."""
+    """dweight = dbias = NULL: the input gradient alone (a flipped
+    convolution of the output gradient: Winograd or image-resident for these
+    shapes), accumulated into dinput."""
     n, ci, co, h, w, kh, kw, s, p = shape
     rng = np.random.default_rng(80 + sum(shape))
     x = int_matrix(rng, (n * ci * h * w,), -3, 3)
@@ -272,6 +280,31 @@ def test_conv2d_cfg3_layers(hip, orc):
             assert rel_err(got, dw64, dwab) <= gemm_tol(K)
         for got in (gB.to_host(), dbr):
             assert rel_err(got, db64, dbab) <= gemm_tol(K)
+
+
+@pytest.mark.parametrize("shape", [(16, 32, 64, 14, 14), (2, 96, 64, 10, 10), (3, 48, 32, 15, 14),
+                                   (2, 16, 32, 16, 16)], ids=lambda s: "x".join(map(str, s)))
+def test_conv2d_winograd_forward_vs_f64(hip, orc, shape):
+    """The Winograd F(2x2,3x3) forward on general data: within the f32
+    accumulation bar gemm_tol(C*9) of the f64 direct sum, on the scale
+    sum |x||w| that bounds any summation order, times 8 for the transforms'
+    extra roundings (each transformed term is a short +-1 or 1/2 sum of
+    inputs and weights). The observed ratio is printed."""
+    n, ci, co, h, w = shape
+    rng = np.random.default_rng(sum(shape))
+    x = rng.standard_normal(n * ci * h * w).astype(np.float32)
+    wt = (rng.standard_normal(co * ci * 9) / np.sqrt(ci * 9)).astype(np.float32)
+    b = rng.standard_normal(co).astype(np.float32)
+    out = hip.DeviceBuffer(n * co * h * w)
+    hip.call("nrs_conv2d_forward", out.ptr, D(hip, x), D(hip, wt), D(hip, b), n, ci, h, w, co, 3, 3, 1, 1)
+    cols = orc.gpu_im2col(x, n, ci, h, w, 3, 3, 1, 1).astype(np.float64)
+    w64 = wt.reshape(co, -1).astype(np.float64)
+    y64 = (w64 @ cols + b[:, None]).reshape(co, n, h * w).transpose(1, 0, 2)
+    yab = ((np.abs(w64) @ np.abs(cols)) + np.abs(b)[:, None]).reshape(co, n, h * w).transpose(1, 0, 2)
+    got = out.to_host((n, co, h * w))
+    err = rel_err(got, y64, yab)
+    print(f"winograd rel err {err:.3g} (f32 bar {gemm_tol(ci * 9):.3g})")
+    assert err <= 8 * gemm_tol(ci * 9)
 
 
 # ------------------------------------------------------------ plumbing kernels
