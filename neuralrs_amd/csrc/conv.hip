@@ -211,22 +211,25 @@ __global__ __launch_bounds__(256) void conv_fwd_direct_kernel(
 // the weights are staged, so the input and weight round trips overlap. Same
 // sum order as conv_fwd_direct_kernel: taps in (ic, i, j) order from zero,
 // then + bias.
-constexpr int kQuadOc = 8;
+// Output channels per thread: 8 for the plain forward, 4 for the pooled one
+// (cfg3 conv1 + ReLU + pool: 5.9 -> 5.4 us, 2 channels 6.6 us; the plain
+// forward: 4.7 us at 8, 4.8 at 4, 5.8 at 2).
+constexpr int kQuadOcFwd = 8, kQuadOcPool = 4;
 // Threads per workgroup of the pixel-quad forward: one wave, so the grid
 // spreads evenly over the CUs (cfg3 conv1: 1568 workgroups, ~6 per CU; in
 // workgroups of 256 threads, 392 of them left 136 CUs with twice the work).
 constexpr int kQuadThreads = 64;
 
-template <int CIN>
+template <int CIN, int QOC>
 __global__ __launch_bounds__(kQuadThreads) void conv_fwd_quad_kernel(
     float* __restrict__ out, const float* __restrict__ input, const float* __restrict__ weight,
     const float* __restrict__ bias, int N, int H, int W, int c_out, FastDiv div_qimg,
     FastDiv div_qrow) {
     constexpr int ROWS = 3 * CIN, TAPS = 9 * CIN;
-    __shared__ __attribute__((aligned(16))) float wsh[kQuadOc][TAPS];
-    __shared__ float bsh[kQuadOc];
+    __shared__ __attribute__((aligned(16))) float wsh[QOC][TAPS];
+    __shared__ float bsh[QOC];
     const int tid = threadIdx.x;
-    const int P = H * W, oc0 = blockIdx.y * kQuadOc;
+    const int P = H * W, oc0 = blockIdx.y * QOC;
     const int64_t quads = (int64_t)N * (P >> 2);
     const int g = blockIdx.x * kQuadThreads + tid;
     const bool valid = g < quads;
@@ -249,7 +252,7 @@ __global__ __launch_bounds__(kQuadThreads) void conv_fwd_quad_kernel(
         for (int u = 0; u < 4; ++u) seg[r][1 + u] = mid[u];
     }
     // this block's weights (zero past c_out) and biases
-    constexpr int WN = kQuadOc * TAPS, WPT = (WN + kQuadThreads - 1) / kQuadThreads;
+    constexpr int WN = QOC * TAPS, WPT = (WN + kQuadThreads - 1) / kQuadThreads;
     const auto rw = buffer_rsrc(weight, (int64_t)c_out * TAPS * 4);
     const auto rb = buffer_rsrc(bias ? bias : weight, bias ? (int64_t)c_out * 4 : 0);
     float wv[WPT];
@@ -258,17 +261,17 @@ __global__ __launch_bounds__(kQuadThreads) void conv_fwd_quad_kernel(
         const int e = tid + kQuadThreads * k;
         wv[k] = buffer_load1(rw, e < WN ? (oc0 * TAPS + e) * 4 : kOutOfRange);
     }
-    const float bv = buffer_load1(rb, tid < kQuadOc ? (oc0 + tid) * 4 : kOutOfRange);
+    const float bv = buffer_load1(rb, tid < QOC ? (oc0 + tid) * 4 : kOutOfRange);
 #pragma unroll
     for (int k = 0; k < WPT; ++k)
         if (tid + kQuadThreads * k < WN) (&wsh[0][0])[tid + kQuadThreads * k] = wv[k];
-    if (tid < kQuadOc) bsh[tid] = bv;
+    if (tid < QOC) bsh[tid] = bv;
     __syncthreads();
     if (!valid) return;
     float* o = out + ((int64_t)n * c_out + oc0) * P + (int)oy * W + ox;
-    const int noc = min(kQuadOc, c_out - oc0);
+    const int noc = min(QOC, c_out - oc0);
 #pragma unroll
-    for (int oc = 0; oc < kQuadOc; ++oc) {
+    for (int oc = 0; oc < QOC; ++oc) {
         if (oc >= noc) break;
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -294,17 +297,17 @@ __global__ __launch_bounds__(kQuadThreads) void conv_fwd_quad_kernel(
 // and records the conv output's flat element index, as maxpool_forward does.
 // The conv output is written only when out is set; the pooled values and
 // indices leave as 64-bit stores.
-template <int CIN>
+template <int CIN, int QOC>
 __global__ __launch_bounds__(kQuadThreads) void conv_fwd_pool_quad_kernel(
     float* __restrict__ pooled, int32_t* __restrict__ argmax, float* __restrict__ out,
     const float* __restrict__ input, const float* __restrict__ weight,
     const float* __restrict__ bias, int N, int H, int W, int c_out, int relu, FastDiv div_bimg,
     FastDiv div_brow) {
     constexpr int ROWS = 4 * CIN, TAPS = 9 * CIN;
-    __shared__ __attribute__((aligned(16))) float wsh[kQuadOc][TAPS];
-    __shared__ float bsh[kQuadOc];
+    __shared__ __attribute__((aligned(16))) float wsh[QOC][TAPS];
+    __shared__ float bsh[QOC];
     const int tid = threadIdx.x;
-    const int P = H * W, PW = W >> 1, PP = (H >> 1) * PW, oc0 = blockIdx.y * kQuadOc;
+    const int P = H * W, PW = W >> 1, PP = (H >> 1) * PW, oc0 = blockIdx.y * QOC;
     const int64_t blocks = (int64_t)N * (H >> 1) * (W >> 2);
     const int g = blockIdx.x * kQuadThreads + tid;
     const bool valid = g < blocks;
@@ -326,7 +329,7 @@ __global__ __launch_bounds__(kQuadThreads) void conv_fwd_pool_quad_kernel(
 #pragma unroll
         for (int u = 0; u < 4; ++u) seg[r][1 + u] = mid[u];
     }
-    constexpr int WN = kQuadOc * TAPS, WPT = (WN + kQuadThreads - 1) / kQuadThreads;
+    constexpr int WN = QOC * TAPS, WPT = (WN + kQuadThreads - 1) / kQuadThreads;
     const auto rw = buffer_rsrc(weight, (int64_t)c_out * TAPS * 4);
     const auto rb = buffer_rsrc(bias ? bias : weight, bias ? (int64_t)c_out * 4 : 0);
     float wv[WPT];
@@ -335,16 +338,16 @@ __global__ __launch_bounds__(kQuadThreads) void conv_fwd_pool_quad_kernel(
         const int e = tid + kQuadThreads * k;
         wv[k] = buffer_load1(rw, e < WN ? (oc0 * TAPS + e) * 4 : kOutOfRange);
     }
-    const float bv = buffer_load1(rb, tid < kQuadOc ? (oc0 + tid) * 4 : kOutOfRange);
+    const float bv = buffer_load1(rb, tid < QOC ? (oc0 + tid) * 4 : kOutOfRange);
 #pragma unroll
     for (int k = 0; k < WPT; ++k)
         if (tid + kQuadThreads * k < WN) (&wsh[0][0])[tid + kQuadThreads * k] = wv[k];
-    if (tid < kQuadOc) bsh[tid] = bv;
+    if (tid < QOC) bsh[tid] = bv;
     __syncthreads();
     if (!valid) return;
-    const int noc = min(kQuadOc, c_out - oc0);
+    const int noc = min(QOC, c_out - oc0);
 #pragma unroll
-    for (int oc = 0; oc < kQuadOc; ++oc) {
+    for (int oc = 0; oc < QOC; ++oc) {
         if (oc >= noc) break;
         f32x4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -1373,11 +1376,12 @@ int conv_pool_forward(float* pooled, int32_t* argmax, float* out, const float* i
         a8(argmax) && N * c_in * in_h * in_w <= INT32_MAX / 4 &&
         N * std::max(c_in, c_out) * in_h * in_w <= INT32_MAX) {
         const int64_t blocks = N * (in_h / 2) * (in_w / 4);
-        auto fn = c_in == 1 ? nrs::conv_fwd_pool_quad_kernel<1>
-                            : (c_in == 2 ? nrs::conv_fwd_pool_quad_kernel<2>
-                                         : nrs::conv_fwd_pool_quad_kernel<3>);
+        constexpr int QOC = nrs::kQuadOcPool;
+        auto fn = c_in == 1 ? nrs::conv_fwd_pool_quad_kernel<1, QOC>
+                            : (c_in == 2 ? nrs::conv_fwd_pool_quad_kernel<2, QOC>
+                                         : nrs::conv_fwd_pool_quad_kernel<3, QOC>);
         hipLaunchKernelGGL(fn, dim3((unsigned)((blocks + nrs::kQuadThreads - 1) / nrs::kQuadThreads),
-                                    (unsigned)((c_out + nrs::kQuadOc - 1) / nrs::kQuadOc)),
+                                    (unsigned)((c_out + QOC - 1) / QOC)),
                            dim3(nrs::kQuadThreads), 0, nrs::stream(), pooled, argmax, out, input,
                            weight, bias, (int)N, (int)in_h, (int)in_w, (int)c_out, relu ? 1 : 0,
                            nrs::make_fastdiv((uint32_t)((in_h / 2) * (in_w / 4))),
@@ -1539,11 +1543,12 @@ int nrs_conv2d_forward(float* out, const float* input, const float* weight, cons
             N * c_in * in_h * in_w <= INT32_MAX / 4) {
             // "same" 3x3 over rows of whole quads: four pixels per thread
             const int64_t quads = N * P / 4;
-            auto fn = c_in == 1 ? nrs::conv_fwd_quad_kernel<1>
-                                : (c_in == 2 ? nrs::conv_fwd_quad_kernel<2>
-                                             : nrs::conv_fwd_quad_kernel<3>);
+            constexpr int QOC = nrs::kQuadOcFwd;
+            auto fn = c_in == 1 ? nrs::conv_fwd_quad_kernel<1, QOC>
+                                : (c_in == 2 ? nrs::conv_fwd_quad_kernel<2, QOC>
+                                             : nrs::conv_fwd_quad_kernel<3, QOC>);
             hipLaunchKernelGGL(fn, dim3((unsigned)((quads + nrs::kQuadThreads - 1) / nrs::kQuadThreads),
-                                        (unsigned)((c_out + nrs::kQuadOc - 1) / nrs::kQuadOc)),
+                                        (unsigned)((c_out + QOC - 1) / QOC)),
                                dim3(nrs::kQuadThreads), 0, nrs::stream(), out, input, weight, bias, (int)N,
                                (int)in_h, (int)in_w, (int)c_out,
                                nrs::make_fastdiv((uint32_t)(P / 4)),
