@@ -290,7 +290,7 @@ __global__ __launch_bounds__(kQuadThreads) void conv_fwd_quad_kernel(
 // Forward of a "same" 3x3 layer followed by 2x2 max pooling of stride 2: the
 // conv2d then MaxPool2d of a CNN (src/cuda/nn/conv.rs:244-277,
 // src/cuda/nn/maxpool.rs:18-46) in one pass. A thread owns a 4-wide, 2-tall
-// block of the conv output, i.e. two pooled outputs, for 8 output channels;
+// block of the conv output, i.e. two pooled outputs, for QOC output channels;
 // its input is 4 rows of 6 floats per input channel. Each conv value is
 // computed as conv_fwd_quad_kernel computes it (same products in the same
 // order, then + bias); each 2x2 window keeps the first maximum in scan order
