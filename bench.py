@@ -75,6 +75,12 @@ def event_ms(hip, fn, reps, warmup):
     return ev.elapsed_ms(e0, e1) / reps
 
 
+def leg_ms(hip, fn, reps, warmup, rounds=3):
+    """A short leg's GPU time in ms: the median of `rounds` event_ms batches
+    (one batch of a few-microsecond leg swings by a microsecond between runs)."""
+    return float(np.median([event_ms(hip, fn, reps, warmup) for _ in range(rounds)]))
+
+
 def roofline_us(flops, nbytes):
     """max(FLOP / FP32 MFMA peak, bytes / HBM bandwidth) in microseconds."""
     return max(flops / (PEAK_FP32_MFMA_TFLOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9)) * 1e6
@@ -219,9 +225,9 @@ def bench_conv_cfg3(hip, steps, warmup, closures_only=False):
 
     ms_unfused = wall_ms(step_unfused)
     ms = wall_ms(step)
-    fwd_ms = event_ms(hip, conv_fwd, steps, 3)
-    bwd_ms = event_ms(hip, conv_bwd, steps, 3)
-    dx1_ms = event_ms(hip, conv1_input_grad, steps, 3)
+    fwd_ms = leg_ms(hip, conv_fwd, steps, 3)
+    bwd_ms = leg_ms(hip, conv_bwd, steps, 3)
+    dx1_ms = leg_ms(hip, conv1_input_grad, steps, 3)
     # rooflines per layer (implicit-GEMM FLOPs; bytes = each tensor read or
     # written once): forward x, W, b, y; input grad g, W, dx; weight+bias
     # grad g, x, dW, db
@@ -238,8 +244,8 @@ def bench_conv_cfg3(hip, steps, warmup, closures_only=False):
             roof_b += dx_roof
         roof_b += roofline_us(fl, y_b + x_b + w_b + 4 * co)
     return {"ms_per_step": ms, "imgs_per_s": N / (ms / 1e3), "ms_per_step_unfused": ms_unfused,
-            "conv1_pool_fwd_us": event_ms(hip, conv1_pool_fwd, steps, 3) * 1e3,
-            "pool_conv1_bwd_us": event_ms(hip, conv1_pool_bwd, steps, 3) * 1e3,
+            "conv1_pool_fwd_us": leg_ms(hip, conv1_pool_fwd, steps, 3) * 1e3,
+            "pool_conv1_bwd_us": leg_ms(hip, conv1_pool_bwd, steps, 3) * 1e3,
             "fwd_us": fwd_ms * 1e3, "bwd_us": bwd_ms * 1e3,
             "fwd_roof_us": roof_f, "bwd_roof_us": roof_b,
             "conv1_input_grad_us": dx1_ms * 1e3, "conv1_input_grad_roof_us": roof_dx1}
@@ -410,16 +416,16 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
                     "attn_fused_bwd_cfg4": fused_bwd}
     else:
         fwd()
-        fwd_us = event_ms(hip, fwd, steps, warmup) * 1e3
-        bwd_us = event_ms(hip, bwd, steps, warmup) * 1e3
-        bmm_us = event_ms(hip, bmms_only, steps, warmup) * 1e3
-        bmm_acc_us = event_ms(hip, bmms_accumulate, steps, warmup) * 1e3
+        fwd_us = leg_ms(hip, fwd, steps, warmup) * 1e3
+        bwd_us = leg_ms(hip, bwd, steps, warmup) * 1e3
+        bmm_us = leg_ms(hip, bmms_only, steps, warmup) * 1e3
+        bmm_acc_us = leg_ms(hip, bmms_accumulate, steps, warmup) * 1e3
         fused_fwd()
-        ffwd_us = event_ms(hip, fused_fwd, steps, warmup) * 1e3
-        fbwd_us = event_ms(hip, fused_bwd, steps, warmup) * 1e3
-        heads_us = event_ms(hip, heads, steps, warmup) * 1e3
+        ffwd_us = leg_ms(hip, fused_fwd, steps, warmup) * 1e3
+        fbwd_us = leg_ms(hip, fused_bwd, steps, warmup) * 1e3
+        heads_us = leg_ms(hip, heads, steps, warmup) * 1e3
         heads_roof = roofline_us(0.0, 4 * 8.0 * Rh * Hh * Dh)  # each reads and writes 4 MB
-        ln_us = event_ms(hip, layernorm, steps, warmup) * 1e3
+        ln_us = leg_ms(hip, layernorm, steps, warmup) * 1e3
         # forward reads x, writes out and x_norm; backward reads grad and
         # x_norm, writes dinput (+ reads dinput, accumulating); the parameter
         # sums read grad and x_norm: 9 passes of 4 MB
