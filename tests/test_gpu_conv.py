@@ -545,3 +545,50 @@ def test_conv2d_backward_beta(hip, orc, shape, beta, with_w):
     if with_w:
         assert np.array_equal(ddw.to_host(), dw_ref.ravel() + ow0)
         assert np.array_equal(ddb.to_host(), db_ref.ravel() + ob0)
+
+
+def _wino_sweep_shapes():
+    """Seeded random shapes of the Winograd and chunk-pipelined 3x3 paths:
+    heights 1..16, even widths 2..16, 8..96 input channels (multiples of 8),
+    32..96 output channels (multiples of 32), 1..3 images."""
+    rng = np.random.default_rng(2026)
+    shapes = []
+    for _ in range(24):
+        h = int(rng.integers(1, 17))
+        w = int(rng.choice(np.arange(2, 17, 2)))
+        ci = int(rng.choice([8, 16, 24, 32, 48, 64, 96]))
+        co = int(rng.choice([32, 64, 96]))
+        n = int(rng.integers(1, 4))
+        shapes.append((n, ci, co, h, w))
+    return shapes
+
+
+@pytest.mark.parametrize("shape", _wino_sweep_shapes(), ids=lambda s: "x".join(map(str, s)))
+def test_conv2d_same3x3_sweep_exact_integers(hip, orc, shape):
+    """"Same" 3x3 layers at random eligible sizes (Winograd forward and input
+    gradient, chunk-pipelined backward where their blocks fit): forward, the
+    input gradient alone (beta 1 over old values), and the whole backward,
+    each exact against the oracle on small integers."""
+    n, ci, co, h, w = shape
+    rng = np.random.default_rng(7 * sum(shape))
+    x = int_matrix(rng, (n * ci * h * w,), -3, 3)
+    wt = int_matrix(rng, (co * ci * 9,), -3, 3)
+    b = int_matrix(rng, (co,), -3, 3)
+    ref, _, _ = orc.conv2d_forward(x, wt, b, n, ci, co, h, w, 3, 3, 1, 1)
+    out = hip.DeviceBuffer(n * co * h * w)
+    dx, dw, db = D(hip, x), D(hip, wt), D(hip, b)
+    hip.call("nrs_conv2d_forward", out.ptr, dx.ptr, dw.ptr, db.ptr, n, ci, h, w, co, 3, 3, 1, 1)
+    assert np.array_equal(out.to_host(), ref)
+    g = int_matrix(rng, (n * co * h * w,), -3, 3)
+    di_ref, dw_ref, db_ref = orc.conv2d_backward(x, wt, g, n, ci, co, h, w, 3, 3, 1, 1)
+    gi0 = int_matrix(rng, (x.size,))
+    gI = D(hip, gi0)
+    hip.call("nrs_conv2d_backward", gI.ptr, None, None, D(hip, g), dx.ptr, dw.ptr,
+             n, ci, h, w, co, 3, 3, 1, 1)
+    assert np.array_equal(gI.to_host(), gi0 + di_ref)
+    gI2, gW, gB = hip.DeviceBuffer.zeros(x.size), hip.DeviceBuffer.zeros(wt.size), hip.DeviceBuffer.zeros(co)
+    hip.call("nrs_conv2d_backward", gI2.ptr, gW.ptr, gB.ptr, D(hip, g), dx.ptr, dw.ptr,
+             n, ci, h, w, co, 3, 3, 1, 1)
+    assert np.array_equal(gI2.to_host(), di_ref)
+    assert np.array_equal(gW.to_host(), dw_ref)
+    assert np.array_equal(gB.to_host(), db_ref)
