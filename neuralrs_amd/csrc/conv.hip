@@ -494,7 +494,7 @@ template <int CIN>
 __global__ __launch_bounds__(256) void conv_dgrad_quad_kernel(
     float* __restrict__ dinput, const float* __restrict__ grad, const float* __restrict__ weight,
     int c_in, int H, int W, int c_out, int band, int bands, int pitch, int groups, int qpg,
-    FastDiv div_qrow, FastDiv div_slots, FastDiv div_pq) {
+    int lq, FastDiv div_slots, FastDiv div_pq) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int tid = threadIdx.x;
     const int n = blockIdx.x / bands, y0 = (blockIdx.x - n * bands) * band;
@@ -503,12 +503,13 @@ __global__ __launch_bounds__(256) void conv_dgrad_quad_kernel(
     float* gt = lds;                                       // [oc][rrows][pitch]
     float* wsh = lds + kQuadDgradOc * tile;                // [oc][CIN][9]
     float* red = wsh + kQuadDgradOc * CIN * 9;             // [groups][qpg][CIN][4]
-    // this thread's quad and channel group
-    const int grp = tid / qpg, q = tid - grp * qpg;
-    uint32_t yy, qx;
-    fast_divmod((uint32_t)q, div_qrow, yy, qx);
-    const bool live = grp < groups && (int)yy < rows;
-    const int x0 = 4 * (int)qx;
+    // this thread's quad and channel group: a row's quads sit in a run of
+    // 2^lq lanes (a power of two >= W/4; the run's extra lanes idle), so no
+    // row straddles two waves
+    const int grp = tid / qpg, q = tid - grp * qpg, nq = W >> 2;
+    const int yy = q >> lq, qx = q & ((1 << lq) - 1);
+    const bool live = grp < groups && yy < rows && qx < nq;
+    const int x0 = 4 * qx;
     const float* gimg = grad + (int64_t)n * c_out * HW;
     const auto rg = buffer_rsrc(gimg, (int64_t)c_out * HW * 4);
     const auto rw = buffer_rsrc(weight, (int64_t)c_out * c_in * 9 * 4);
@@ -563,9 +564,25 @@ __global__ __launch_bounds__(256) void conv_dgrad_quad_kernel(
 #pragma unroll
                 for (int i = 0; i < 3; ++i) {
                     // gradient row y + 1 - i = tile row (yy + 2 - i)
-                    const float* gr = gr0 + ((int)yy + 2 - i) * pitch;
+                    const float* gr = gr0 + (yy + 2 - i) * pitch;
                     const f32x4 mid = *reinterpret_cast<const f32x4*>(gr);
-                    const float gv[6] = {gr[-1], mid[0], mid[1], mid[2], mid[3], gr[4]};
+                    // the outer neighbours are the adjacent quads' edge values
+                    // (the next and previous lanes: consecutive lanes own
+                    // consecutive quads of a row), zero at the row's ends
+                    // where the tile's halo is zero; wave shifts by one lane
+                    // in place of two 32-bit LDS reads whose 4-float lane
+                    // stride hit each bank four times
+                    // (each element into a scalar first: a bit_cast of the
+                    // vector element expression read element 0 for both)
+                    const float m3 = mid[3], m0 = mid[0];
+                    const float left = __builtin_bit_cast(
+                        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, m3), 0x138, 0xf,
+                                                           0xf, false));
+                    const float right = __builtin_bit_cast(
+                        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, m0), 0x130, 0xf,
+                                                           0xf, false));
+                    const float gv[6] = {qx == 0 ? 0.0f : left, mid[0], mid[1], mid[2], mid[3],
+                                         qx == nq - 1 ? 0.0f : right};
 #pragma unroll
                     for (int j = 0; j < 3; ++j)
 #pragma unroll
@@ -589,7 +606,7 @@ __global__ __launch_bounds__(256) void conv_dgrad_quad_kernel(
     }
     __syncthreads();
     if (grp != 0 || !live) return;
-    float* drow = dinput + (int64_t)n * c_in * HW + (y0 + (int)yy) * W + x0;
+    float* drow = dinput + (int64_t)n * c_in * HW + (y0 + yy) * W + x0;
 #pragma unroll
     for (int c = 0; c < CIN; ++c) {
         if (c >= c_in) break;
@@ -1138,15 +1155,19 @@ int quad_dgrad(float* dinput, const float* grad, const float* weight, const Conv
         ((uintptr_t)grad & 15) || d.c_out * d.in_h * d.in_w > INT32_MAX / 4 ||
         d.c_in * d.in_h * d.in_w > INT32_MAX / 4)
         return kSlabUnsupported;
+    // a row's W/4 quads take a run of 2^lq lanes (the kernel's neighbour
+    // exchange shifts values between adjacent lanes of one wave)
     const int W4 = (int)d.in_w / 4;
+    int lq = 0;
+    while ((1 << lq) < W4) ++lq;
     // bands of rows so that about two workgroups per CU run, whose quads
     // fill at most 256 threads
     int64_t bands = std::max<int64_t>(1, std::min<int64_t>(d.in_h, (2 * num_cus() + d.N - 1) / d.N));
     int64_t band = (d.in_h + bands - 1) / bands;
-    band = std::max<int64_t>(1, std::min<int64_t>(band, 256 / W4));
+    band = std::max<int64_t>(1, std::min<int64_t>(band, 256 >> lq));
     bands = (d.in_h + band - 1) / band;
     if (d.N * bands > INT32_MAX) return kSlabUnsupported;
-    const int qpg = (int)(band * W4);  // quads per band
+    const int qpg = (int)(band << lq);  // quad slots per band
     int groups = 4;
     while (groups > 1 && groups * qpg > 256) groups /= 2;
     if (qpg > 256) return kSlabUnsupported;
@@ -1159,8 +1180,7 @@ int quad_dgrad(float* dinput, const float* grad, const float* weight, const Conv
     if (int rc = prescale_grad(dinput, d.N * d.c_in * d.in_h * d.in_w, beta)) return rc;
     hipLaunchKernelGGL(fn, dim3((unsigned)(d.N * bands)), dim3(256), lds, stream(), dinput, grad,
                        weight, (int)d.c_in, (int)d.in_h, (int)d.in_w, (int)d.c_out, (int)band,
-                       (int)bands, pitch, groups, qpg, make_fastdiv((uint32_t)W4),
-                       make_fastdiv((uint32_t)(rrows * (pitch / 4))),
+                       (int)bands, pitch, groups, qpg, lq, make_fastdiv((uint32_t)(rrows * (pitch / 4))),
                        make_fastdiv((uint32_t)(pitch / 4)));
     NRS_LAUNCH_CHECK("conv2d input gradient (pixel quads)");
     return NRS_OK;
