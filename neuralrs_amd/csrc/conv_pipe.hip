@@ -434,17 +434,33 @@ __device__ __forceinline__ void pipe_w_block(const PipeArgs& a, int bid, float* 
     }
 }
 
-// W blocks first (ids [0, nw)), then D blocks.
+// With W blocks (the backward), the blocks are ordered slice by slice: a
+// slice's W blocks, then the D blocks of its images. The output gradient of
+// a slice is read by all of them (the W blocks' gradient operand, the D
+// blocks' image), so when the grid is a multiple of 8 logical index L runs
+// on XCD L / (grid / 8): workgroup ids are dealt to the 8 XCDs round-robin
+// (id % 8), and consecutive logical blocks then share one XCD's L2.
 template <bool FLIP, bool HAS_W>
 __global__ __launch_bounds__(256) void conv_pipe_kernel(PipeArgs a) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int bid = blockIdx.x;
     if constexpr (HAS_W) {
-        if (bid < a.nw) {
-            pipe_w_block(a, bid, lds);
+        const int total = a.nw + a.nd;
+        const int L = (total & 7) == 0 ? (bid & 7) * (total >> 3) + (bid >> 3) : bid;
+        const int cblocks = a.wC / kPCC, wmblocks = a.wM / kPWM, dmblocks = a.dM / kPMB;
+        const int wper = cblocks * wmblocks, per = wper + (a.nd > 0 ? kPImgs * dmblocks : 0);
+        const int slice = L / per, r = L - slice * per;
+        if (r < wper) {
+            // pipe_w_block's decode: cblk fastest, then m-block, then slice
+            const int mblk = r / cblocks, cblk = r - mblk * cblocks;
+            pipe_w_block(a, (slice * wmblocks + mblk) * cblocks + cblk, lds);
             return;
         }
-        pipe_d_block<FLIP>(a, bid - a.nw, lds);
+        // the slice's images in order, m-blocks fastest (pipe_d_block's
+        // decode); the last slice of an odd batch has one image, and L stays
+        // below the grid, so r never reaches its missing image's blocks
+        const int rd = r - wper, img = slice * kPImgs + rd / dmblocks, mblk = rd % dmblocks;
+        pipe_d_block<FLIP>(a, img * dmblocks + mblk, lds);
     } else {
         pipe_d_block<FLIP>(a, bid, lds);
     }
