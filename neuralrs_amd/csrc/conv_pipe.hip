@@ -462,7 +462,9 @@ __global__ __launch_bounds__(256) void conv_pipe_kernel(PipeArgs a) {
         const int rd = r - wper, img = slice * kPImgs + rd / dmblocks, mblk = rd % dmblocks;
         pipe_d_block<FLIP>(a, img * dmblocks + mblk, lds);
     } else {
-        pipe_d_block<FLIP>(a, bid, lds);
+        // an image's m-blocks (consecutive ids) folded onto one XCD, as above
+        const int total = a.nd;
+        pipe_d_block<FLIP>(a, (total & 7) == 0 ? (bid & 7) * (total >> 3) + (bid >> 3) : bid, lds);
     }
 }
 

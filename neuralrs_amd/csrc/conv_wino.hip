@@ -116,7 +116,13 @@ __global__ __launch_bounds__(kWinoThreads) void conv_wino_kernel(WinoArgs a) {
     extern __shared__ __attribute__((aligned(16))) float lds[];  // kWinoStages x [image | filters]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n = blockIdx.x / a.mgroups, mg = blockIdx.x - n * a.mgroups;
+    // an image's output-channel groups are consecutive logical blocks, and
+    // when the grid is a multiple of 8 logical block L runs on XCD
+    // L / (grid / 8) (ids are dealt to the XCDs round-robin): the groups that
+    // read one image share an L2
+    const int grid = gridDim.x, bid = blockIdx.x;
+    const int L = (grid & 7) == 0 ? (bid & 7) * (grid >> 3) + (bid >> 3) : bid;
+    const int n = L / a.mgroups, mg = L - n * a.mgroups;
     const int mb = wave & 1, tb = wave >> 1;
     const int l16 = lane & 15, k = lane >> 4;
     const int HW = a.H * a.W, PW = a.PW, PS = a.PS, nch = a.C / kWinoCC;
