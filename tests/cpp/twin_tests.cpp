@@ -1079,6 +1079,50 @@ void cfg3_cnn_step() {
     }
 }
 
+// The conv2d_maxpool node without the ReLU (a pool over the raw conv
+// output), with the image's gradient asked for: against the oracle's Conv2d
+// and max pooling composed, and against the conv2d -> maxpool2d graph.
+void cuda_conv2d_maxpool_node() {
+    reseed(41);
+    const size_t N = 3, C = 2, H = 8, W = 12, M = 5, PH = 4, PW = 6;
+    const Vec x = normal(N * C * H * W, 1.0f), w = normal(M * C * 9, 0.3f), b = normal(M, 0.1f);
+    const Vec seed = normal(N * M * PH * PW, 1.0f);
+    Vec y(N * M * H * W), p(N * M * PH * PW);
+    std::vector<int32_t> am(p.size());
+    orc_conv2d_forward(x.data(), w.data(), b.data(), y.data(), N, C, M, H, W, 3, 3, 1, 1);
+    orc_maxpool_forward(y.data(), p.data(), am.data(), N, M, H, W, 2, 2);
+    Vec dy(y.size(), 0.0f), dx(x.size(), 0.0f), dw(w.size(), 0.0f), db(M, 0.0f);
+    orc_maxpool_backward(seed.data(), am.data(), dy.data(), seed.size());
+    orc_conv2d_backward(x.data(), w.data(), dy.data(), dx.data(), dw.data(), db.data(), N, C, M,
+                        H, W, 3, 3, 1, 1);
+    Vec first_out, first_dx, first_dw;
+    for (int fused = 0; fused < 2; ++fused) {
+        const char* tag = fused ? "conv2d_maxpool node" : "conv2d -> maxpool2d";
+        NodeRef gx = resident(x, {N, C, H, W});
+        NodeRef gw = resident(w, {M, C, 3, 3}), gb = resident(b, {M});
+        NodeRef out = fused ? hip::nn::conv2d_maxpool(gx, gw, gb, 1, 1, false, 2, 2)
+                            : hip::nn::maxpool2d(hip::nn::conv2d(gx, gw, gb, 1, 1), 2, 2);
+        if (out->shape != std::vector<size_t>{N, M, PH, PW}) throw Failure("conv2d_maxpool: shape");
+        const Vec gout = gpu::to_host(out);
+        close(gout, p, 1e-4f, std::string(tag) + " fwd");
+        gpu::set_grad(out, seed);
+        backward_graph(out);
+        const Vec gdx = gpu::read_grad(gx), gdw = gpu::read_grad(gw), gdb = gpu::read_grad(gb);
+        close(gdx, dx, 1e-4f, std::string(tag) + " input.grad");
+        close(gdw, dw, 1e-3f, std::string(tag) + " weight.grad");
+        close(gdb, db, 1e-3f, std::string(tag) + " bias.grad");
+        if (fused) {
+            close(gout, first_out, 1e-6f, "conv2d_maxpool node vs graph fwd");
+            close(gdx, first_dx, 1e-5f, "conv2d_maxpool node vs graph input.grad");
+            close(gdw, first_dw, 1e-5f, "conv2d_maxpool node vs graph weight.grad");
+        } else {
+            first_out = gout;
+            first_dx = gdx;
+            first_dw = gdw;
+        }
+    }
+}
+
 const Case kCases[] = {
     {"cuda_resident_matmul_backward", cuda_resident_matmul_backward},
     {"cuda_resident_linear_chain", cuda_resident_linear_chain},
@@ -1112,6 +1156,7 @@ const Case kCases[] = {
     {"cuda_maxpool_non_overlapping", cuda_maxpool_non_overlapping},
     {"cuda_maxpool_overlapping", cuda_maxpool_overlapping},
     {"cfg3_cnn_step", cfg3_cnn_step},
+    {"cuda_conv2d_maxpool_node", cuda_conv2d_maxpool_node},
 };
 
 int main(int argc, char** argv) {
