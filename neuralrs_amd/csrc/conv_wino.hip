@@ -294,10 +294,12 @@ __global__ __launch_bounds__(kWinoThreads) void conv_wino_kernel(WinoArgs a) {
         make_b(gn, 0, bc);
         interleave();
         __builtin_amdgcn_sched_barrier(0);
-        if (ch + 1 < nch) {
+        if (ch + 2 < nch) {
             // chunk ch+2 (set P) into the stage chunk ch-1 used (every wave
-            // finished reading it before the last barrier)
-            if (ch + 2 < nch) stage_store(raw[P], gn == kWinoStages - 1 ? 0 : gn + 1);
+            // finished reading it before the last barrier). Without a store
+            // there is nothing to wait for: the next chunk's stage was filled
+            // before the last barrier, and the chunk after it stores nothing.
+            stage_store(raw[P], gn == kWinoStages - 1 ? 0 : gn + 1);
             __syncthreads();
         }
     };
