@@ -1029,11 +1029,16 @@ __global__ __launch_bounds__(kBiasThreads) void bias_grad_kernel(float* __restri
 
 }  // namespace
 
-// dbias = beta * dbias when there is nothing to sum.
+// dst = beta * dst when there is nothing to sum (a gradient over an empty
+// batch); beta 0 writes zeros whatever dst held.
+int zero_or_scale(float* dst, int64_t n, float beta) {
+    if (!dst || n == 0 || beta == 1.0f) return NRS_OK;
+    if (beta == 0.0f) return zero_fill(dst, sizeof(float) * (size_t)n);
+    return nrs_scale(dst, dst, beta, n, 0.0f);
+}
+
 int zero_or_scale_bias(float* dbias, int64_t c_out, float beta) {
-    if (beta == 1.0f) return NRS_OK;
-    if (beta == 0.0f) return zero_fill(dbias, sizeof(float) * (size_t)c_out);
-    return nrs_scale(dbias, dbias, beta, c_out, 0.0f);
+    return zero_or_scale(dbias, c_out, beta);
 }
 
 int bias_grad_launch(float* dbias, const float* grad, int64_t N, int64_t c_out, int64_t P,
@@ -1445,7 +1450,12 @@ int pool_conv_backward(float* dinput, float* dweight, float* dbias, const float*
     const int64_t conv_elems = N * c_out * d.out_h * d.out_w;
     NRS_ARG_CHECK(conv_elems <= INT32_MAX,
                   "maxpool conv2d backward: conv output too large for int32 argmax");
-    if (c_out == 0 || N == 0 || (!dinput && !dweight && !dbias)) return NRS_OK;
+    if (c_out == 0 || (!dinput && !dweight && !dbias)) return NRS_OK;
+    if (N == 0) {
+        // no images: the parameter gradients keep beta_params of what they held
+        if ((rc = nrs::zero_or_scale(dweight, c_out * c_in * kh * kw, beta_params))) return rc;
+        return nrs::zero_or_scale(dbias, c_out, beta_params);
+    }
     NRS_ARG_CHECK(grad_pooled && argmax && input && weight, "maxpool conv2d backward: null pointer");
     if (!dinput && pool_k == 2 && pool_stride == 2 && c_in * kh * kw <= nrs::kDirectTaps &&
         c_out <= INT32_MAX) {
@@ -1684,6 +1694,12 @@ int nrs_conv2d_backward_ex(float* dinput, float* dweight, float* dbias, const fl
     if (rc) return rc;
     const int64_t col_h = c_in * kh * kw, P = d.out_h * d.out_w, width = N * P;
     if (c_out == 0) return NRS_OK;
+    if (N == 0) {
+        // no images (the output always has a pixel): dinput is empty and the
+        // parameter gradients keep beta_params of what they held
+        if ((rc = nrs::zero_or_scale(dweight, c_out * col_h, beta_params))) return rc;
+        return nrs::zero_or_scale(dbias, c_out, beta_params);
+    }
     NRS_ARG_CHECK(kh < 32768 && kw < 32768 && c_in * in_h * in_w <= INT32_MAX &&
                       c_out * d.out_h * d.out_w <= INT32_MAX && c_out * kh * kw <= INT32_MAX,
                   "conv2d: kernel or image too large");

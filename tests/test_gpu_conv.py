@@ -514,6 +514,48 @@ def test_conv2d_backward_ex_param_beta(hip, orc, shape, beta_p, with_dx):
         assert np.array_equal(ddi.to_host(), di_ref.ravel() + di0)
 
 
+@pytest.mark.parametrize("shape", [(1, 32, 28, 28, 3, 3, 1, 1), (32, 64, 14, 14, 3, 3, 1, 1),
+                                   (40, 70, 6, 7, 3, 3, 1, 1)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("beta_p", [0.0, 0.5, 1.0])
+def test_conv2d_backward_empty_batch(hip, shape, beta_p):
+    """No images: nrs_conv2d_backward_ex, nrs_maxpool_relu_conv2d_backward
+    and nrs_conv2d_relu_maxpool_forward return OK; the weight and bias
+    gradients become the empty sums plus beta_params * old (zeros over NaN
+    under beta 0), as nrs_linear_backward does with no rows."""
+    ci, co, h, w, kh, kw, s, p = shape
+    rng = np.random.default_rng(ci + co)
+    nw = co * ci * kh * kw
+    D = hip.DeviceBuffer.from_host
+    for entry in ("nrs_conv2d_backward_ex", "nrs_maxpool_relu_conv2d_backward"):
+        if beta_p:
+            ow0, ob0 = int_matrix(rng, (nw,), -3, 3), int_matrix(rng, (co,), -3, 3)
+        else:
+            ow0, ob0 = np.full(nw, np.nan, np.float32), np.full(co, np.nan, np.float32)
+        ddw, ddb = D(ow0), D(ob0)
+        print(f"{entry} N=0 {shape} beta_params={beta_p}", flush=True)
+        if entry == "nrs_conv2d_backward_ex":
+            hip.call(entry, None, ddw, ddb, None, None, None, 0, ci, h, w, co, kh, kw, s, p, 1.0,
+                     beta_p)
+        else:
+            hip.call(entry, None, ddw, ddb, None, None, None, None, None, 0, ci, h, w, co, kh, kw,
+                     s, p, 2, 2, beta_p)
+        assert np.array_equal(ddw.to_host(), beta_p * ow0 if beta_p else np.zeros(nw))
+        assert np.array_equal(ddb.to_host(), beta_p * ob0 if beta_p else np.zeros(co))
+    hip.call("nrs_conv2d_relu_maxpool_forward", None, None, None, None, None, None, 0, ci, h, w,
+             co, kh, kw, s, p, 2, 2)
+
+
+def test_attention_empty_batch(hip):
+    """No sequences: both attention entries return OK, on the short and the
+    long path, without reading their (null) operands."""
+    for seq in (64, 1024):
+        print(f"attention batch 0 seq {seq}", flush=True)
+        hip.call("nrs_attention_forward", None, None, None, None, None, 0, 4, seq, 32, 128,
+                 32 ** -0.5)
+        hip.call("nrs_attention_backward", None, None, None, None, None, None, None, None, None,
+                 0, 4, seq, 32, 128, 32 ** -0.5, 0.0)
+
+
 @pytest.mark.parametrize("shape", [(2, 3, 4, 8, 8, 3, 3, 1, 1), (3, 1, 32, 28, 28, 3, 3, 1, 1),
                                    (2, 32, 64, 14, 14, 3, 3, 1, 1), (2, 6, 5, 9, 9, 3, 3, 1, 1),
                                    (1, 8, 3, 7, 7, 3, 3, 2, 1), (2, 2, 3, 6, 6, 2, 2, 1, 2),
