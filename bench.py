@@ -255,13 +255,14 @@ def bench_mlp_cfg2(hip, steps, warmup, closures_only=False):
     """cfg2 training step: x[256,784] -> Linear(784,128) -> ReLU ->
     Linear(128,10) -> cross-entropy seed (softmax - onehot)/256 (the fused
     ce_backward of src/cuda/loss/cross_entropy.rs:39-58) -> backward (dW, db
-    of both layers, dh, dx), in four library calls of one launch each: bias
-    and ReLU in the first GEMM's epilogue, the seed in the second's
-    (nrs_linear_cross_entropy), layer 2's backward with the ReLU backward in
-    its input gradient's epilogue (nrs_linear_backward_relu, masked by the
-    activation: a > 0 exactly where the pre-activation is), layer 1's
-    backward (nrs_linear_backward). Issued from Python here; the same step
-    issued from C++ (eagerly and as a HIP graph) is host_step()."""
+    of both layers, dh, dx), in two library calls of one launch each:
+    nrs_mlp2_forward_seed (both layers forward, the seed, and the hidden
+    layer's gradient through the ReLU: all row-local) and nrs_mlp2_backward
+    (dW1, db1, dW2, db2 and dx as one short-GEMM launch). The four-call form
+    (nrs_gemm with bias and ReLU, nrs_linear_cross_entropy,
+    nrs_linear_backward_relu, nrs_linear_backward) is timed beside it. Issued
+    from Python here; the same steps issued from C++ (eagerly and as a HIP
+    graph) are host_step()."""
     rng = np.random.default_rng(2)
     B, I, Hd, O = 256, 784, 128, 10
     D = hip.DeviceBuffer.from_host
@@ -278,6 +279,11 @@ def bench_mlp_cfg2(hip, steps, warmup, closures_only=False):
     gb1, gb2 = hip.DeviceBuffer.zeros(Hd), hip.DeviceBuffer.zeros(O)
 
     def step():
+        hip.call("nrs_mlp2_forward_seed", a, z, gz, gh, x, w1, b1, w2, b2, onehot, B, I, Hd, O)
+        hip.call("nrs_mlp2_backward", gx, gw1, gb1, gw2, gb2, gh, gz, x, w1, a, B, I, Hd, O,
+                 0.0, 1.0)
+
+    def step_four_calls():
         hip.gemm(hip.NN, a, x, w1, B, Hd, I, 0.0, b1, hip.EPI_BIAS_COL | hip.EPI_RELU)
         hip.call("nrs_linear_cross_entropy", z, gz, a, w2, b2, onehot, B, Hd, O)
         hip.call("nrs_linear_backward_relu", gh, gw2, gb2, gz, a, w2, a, B, Hd, O, 0.0, 1.0, 1.0)
@@ -286,7 +292,8 @@ def bench_mlp_cfg2(hip, steps, warmup, closures_only=False):
     if closures_only:
         return {"mlp_step_cfg2": step}
     us = event_ms(hip, step, steps, warmup) * 1e3
-    return {"us_per_step": us, "gemm_roof_us": mlp_gemm_roof_us()}
+    us4 = event_ms(hip, step_four_calls, steps, warmup) * 1e3
+    return {"us_per_step": us, "us_per_step_four_calls": us4, "gemm_roof_us": mlp_gemm_roof_us()}
 
 
 def mlp_gemm_roof_us():
@@ -830,16 +837,18 @@ def main():
         m = bench_mlp_cfg2(hip, args.steps, 5)
         hm = host_step("mlp", 200, 20)
         out["mlp_cfg2"] = {"python_us_per_step": round(m["us_per_step"], 2),
+                           "python_us_per_step_four_calls": round(m["us_per_step_four_calls"], 2),
                            "gemm_roofline_us": round(m["gemm_roof_us"], 3),
-                           "library_calls": 4,
-                           "config": "cfg2 Linear 784->128 (+bias, ReLU epilogue), Linear 128->10 "
-                                     "(+bias, fused CE seed epilogue), batch 256, fwd+bwd incl. "
-                                     "dx and both bias grads (ReLU backward in layer 2's dx "
-                                     "epilogue)"}
+                           "library_calls": 2,
+                           "config": "cfg2 Linear 784->128 (+bias) -> ReLU -> Linear 128->10 "
+                                     "(+bias) -> CE seed -> hidden gradient through the ReLU "
+                                     "(nrs_mlp2_forward_seed, one launch), then dW1, db1, dW2, db2 "
+                                     "and dx (nrs_mlp2_backward, one launch); batch 256"}
         if hm:
             out["mlp_cfg2"].update({
                 "us_per_step": round(hm["eager_gpu_us"], 2),
                 "graph_us_per_step": round(hm["graph_gpu_us"], 2),
+                "us_per_step_four_calls": round(hm["four_call_gpu_us"], 2),
                 "gemm_roofline_frac": round(m["gemm_roof_us"] / hm["eager_gpu_us"], 4),
                 "timing": "C++ issue (neuralrs_amd/bench_host mlp), HIP events on the stream"})
         hb = host_step("block", 50, 10)

@@ -168,6 +168,35 @@ int nrs_linear_cross_entropy(float *logits, float *grad, const float *x, const f
                              const float *bias, const float *target, int64_t batch,
                              int64_t in_f, int64_t classes);
 
+/* The two-layer classifier of the reference's MNIST step
+ * (examples/mnist_cuda.rs:34-37: relu(add(matmul(x, w1), b1)), then
+ * add(matmul(h, w2), b2), then the fused cross-entropy seed of
+ * src/cuda/loss/cross_entropy.rs:39-58) through the gradient of its hidden
+ * layer, in one launch (everything here is row-local):
+ *   h  = relu(x . w1 + b1)               [batch, hidden]
+ *   z  = h . w2 + b2                     [batch, classes]  the logits
+ *   gz = (softmax(z) - target) / batch   [batch, classes]  ce_backward's seed
+ *   dh = (gz . w2^T) where h > 0         [batch, hidden]   relu_grad
+ *                                          (src/cuda/graph/relu.rs:23-28)
+ * hidden <= 256, classes <= 16; b1, b2 may be NULL. No output may overlap an
+ * input or another output.                                                   */
+int nrs_mlp2_forward_seed(float *h, float *z, float *gz, float *dh, const float *x,
+                          const float *w1, const float *b1, const float *w2, const float *b2,
+                          const float *target, int64_t batch, int64_t in_f, int64_t hidden,
+                          int64_t classes);
+/* Its parameter and input gradients in one launch (both layers' matmul
+ * backward closures, src/autograd/graph/matmul.rs:17-63 on the GPU path
+ * src/cuda/graph/matmul.rs:386-436, and the bias add's column sums):
+ *   dw1 = x^T . dh + beta_p * dw1      db1 = sum_rows(dh) + beta_p * db1
+ *   dw2 = h^T . gz + beta_p * dw2      db2 = sum_rows(gz) + beta_p * db2
+ *   dx  = dh . w1^T + beta_x * dx      (skipped when dx is NULL)
+ * the products nrs_linear_backward runs for each layer, with their bits.
+ * db1, db2 may be NULL.                                                      */
+int nrs_mlp2_backward(float *dx, float *dw1, float *db1, float *dw2, float *db2,
+                      const float *dh, const float *gz, const float *x, const float *w1,
+                      const float *h, int64_t batch, int64_t in_f, int64_t hidden,
+                      int64_t classes, float beta_x, float beta_p);
+
 /* mm_nt_splitk(a, b, rows, cols, inner) (src/cuda/graph/matmul.rs:354-379):
  * C = A[rows,inner] . B[cols,inner]^T + beta*C for skinny outputs with a huge
  * inner dimension. The inner dimension is split across workgroups; partial

@@ -52,6 +52,8 @@ SIGNATURES = {
     "nrs_linear_backward": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _F, _F],
     "nrs_linear_backward_relu": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _F, _F],
     "nrs_linear_cross_entropy": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
+    "nrs_mlp2_forward_seed": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I],
+    "nrs_mlp2_backward": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F],
     "nrs_gemm_nt_splitk": [_P, _P, _P, _I, _I, _I, _F],
     "nrs_gemm_nt_splitk_noalloc": [_P, _P, _P, _I, _I, _I, _F],
     "nrs_bmm": [ctypes.c_int, _P, _P, _P, _I, _I, _I, _I, _F],

@@ -384,15 +384,11 @@ int gemm_run(const GemmCall& c) {
     return NRS_OK;
 }
 
-namespace {
-
 bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
     const char* x = static_cast<const char*>(a);
     const char* y = static_cast<const char*>(b);
     return x < y + bbytes && y < x + abytes;
 }
-
-}  // namespace
 
 // True when no call's outputs (C, the row of sums) overlap another call's
 // outputs or operands (A, B, bias, and extra[j] of call j when given), so the

@@ -67,6 +67,10 @@ int gemm_run(const GemmCall& c);
 // qualify (see nrs_gemm_group), else gemm_run on each in order.
 int gemm_group_run(const GemmCall* calls, int count);
 
+// Whether byte ranges [a, a + abytes) and [b, b + bbytes) share memory (an
+// empty range overlaps nothing).
+bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes);
+
 // A further operand of a call (e.g. an epilogue's mask) for the overlap check.
 struct OperandRange {
     const void* p;

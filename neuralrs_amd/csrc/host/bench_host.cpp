@@ -5,8 +5,9 @@
 //          path a drop-in caller takes: nn::TransformerBlock::forward,
 //          set_grad, backward_graph, zero_grad of the parameters;
 //   mlp:   the cfg2 MLP training step (784 -> 128 -> ReLU -> 10, batch 256,
-//          fused cross-entropy gradient) issued through the C ABI, timed
-//          eagerly and as a replayed HIP graph of the same launches;
+//          fused cross-entropy gradient) issued through the C ABI in two
+//          calls, timed eagerly and as a replayed HIP graph of the same
+//          launches, and the four-call form of the same step eagerly;
 //   cnn:   the cfg3 step (batch 128: conv1 1->32 3x3 p1 -> ReLU -> 2x2 max
 //          pool -> conv2 32->64 3x3 p1, forward and backward, the image
 //          batch requiring no gradient) through the C++ operator surface, as
@@ -177,12 +178,24 @@ int bench_mlp(int steps, int warmup) {
     DeviceBuffer gw1(I * Hd, true), gw2(Hd * O, true), gb1(Hd, true), gb2(O, true);
     // the reference's step (Linear, ReLU, Linear, the fused cross-entropy
     // seed (softmax - onehot) / batch, then each layer's backward: dW and db
-    // accumulated, dx written) in four library calls: layer 1 with bias and
-    // ReLU in the product's epilogue; layer 2 with the seed in its epilogue;
-    // layer 2's backward with the ReLU backward applied to its input
-    // gradient (the mask is the ReLU output: a > 0 exactly where the
-    // pre-activation is); layer 1's backward. Each is one launch.
+    // accumulated, dx written) in two library calls of one launch each: the
+    // row-local part (both layers forward, the seed, the hidden layer's
+    // gradient through the ReLU) and the gradients that sum over the batch
+    // (dW1, db1, dW2, db2) with dx.
     auto step = [&] {
+        nrs_check(nrs_mlp2_forward_seed(a.ptr(), z.ptr(), gz.ptr(), gh.ptr(), x.ptr(), w1.ptr(),
+                                        b1.ptr(), w2.ptr(), b2.ptr(), onehot.ptr(), Bn, I, Hd, O),
+                  "mlp2 forward + seed");
+        nrs_check(nrs_mlp2_backward(gx.ptr(), gw1.ptr(), gb1.ptr(), gw2.ptr(), gb2.ptr(), gh.ptr(),
+                                    gz.ptr(), x.ptr(), w1.ptr(), a.ptr(), Bn, I, Hd, O, 0.0f, 1.0f),
+                  "mlp2 backward");
+    };
+    // the same step in four library calls: layer 1 with bias and ReLU in the
+    // product's epilogue; layer 2 with the seed in its epilogue; layer 2's
+    // backward with the ReLU backward applied to its input gradient (the mask
+    // is the ReLU output: a > 0 exactly where the pre-activation is); layer
+    // 1's backward. Each is one launch.
+    auto step4 = [&] {
         nrs_check(nrs_gemm(NRS_NN, a.ptr(), x.ptr(), w1.ptr(), Bn, Hd, I, 0.0f, b1.ptr(),
                            NRS_EPI_BIAS_COL | NRS_EPI_RELU), "l1+relu");
         nrs_check(nrs_linear_cross_entropy(z.ptr(), gz.ptr(), a.ptr(), w2.ptr(), b2.ptr(),
@@ -193,8 +206,9 @@ int bench_mlp(int steps, int warmup) {
         nrs_check(nrs_linear_backward(gx.ptr(), gw1.ptr(), gb1.ptr(), gh.ptr(), x.ptr(), w1.ptr(),
                                       Bn, I, Hd, 0.0f, 1.0f, 1.0f), "layer 1 bwd");
     };
-    double gpu_us = 0, wall_us = 0;
+    double gpu_us = 0, wall_us = 0, gpu4_us = 0, wall4_us = 0;
     time_steps(step, steps, warmup, gpu_us, wall_us);
+    time_steps(step4, steps, warmup, gpu4_us, wall4_us);
     // the same step captured once into a HIP graph and replayed (every
     // launch above is capture-safe once the split-K scratch has grown)
     hipStream_t cap;
@@ -215,9 +229,10 @@ int bench_mlp(int steps, int warmup) {
     hip_check(hipGraphDestroy(graph), "destroy");
     hip_check(hipStreamDestroy(cap), "destroy");
     std::printf("{\"workload\": \"cfg2 MLP step 784-128-10 batch 256 through the C ABI\", "
-                "\"calls\": 4, \"eager_gpu_us\": %.2f, \"eager_wall_us\": %.2f, "
-                "\"graph_gpu_us\": %.2f, \"graph_wall_us\": %.2f, \"steps\": %d}\n",
-                gpu_us, wall_us, g_gpu, g_wall, steps);
+                "\"calls\": 2, \"eager_gpu_us\": %.2f, \"eager_wall_us\": %.2f, "
+                "\"graph_gpu_us\": %.2f, \"graph_wall_us\": %.2f, "
+                "\"four_call_gpu_us\": %.2f, \"four_call_wall_us\": %.2f, \"steps\": %d}\n",
+                gpu_us, wall_us, g_gpu, g_wall, gpu4_us, wall4_us, steps);
     return 0;
 }
 

@@ -630,6 +630,166 @@ def test_linear_cross_entropy_errors(hip):
                  0.0, 0.0, 0.0)
 
 
+MLP2_SHAPES = [(256, 784, 128, 10),   # cfg2
+                (7, 50, 100, 3),       # ragged row block, hidden not a multiple of 64
+                (33, 17, 256, 16),     # four hidden column groups, the most classes
+                (5, 1, 64, 1),         # one input feature, one class
+                (64, 300, 192, 10)]    # three column groups, in_f not a multiple of 8
+
+
+@pytest.mark.parametrize("shape", MLP2_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_mlp2_forward_seed(hip, orc, shape):
+    """nrs_mlp2_forward_seed: h = relu(x . w1 + b1) and z = h . w2 + b2
+    exact on quarter-integer data (against numpy); gz with the bits of
+    nrs_cross_entropy_backward on those logits and within the CE test's bound
+    of the oracle's CrossEntropyLoss gradient; dh = gz . w2^T where h > 0
+    against float64 within the short-GEMM bound (K = classes)."""
+    batch, in_f, hidden, classes = shape
+    rng = np.random.default_rng(batch + in_f + hidden + classes)
+    q = np.float32(0.25)
+    x = int_matrix(rng, (batch, in_f), -2, 2) * q
+    w1 = int_matrix(rng, (in_f, hidden), -2, 2) * q
+    b1 = int_matrix(rng, (hidden,), -2, 2)
+    w2 = int_matrix(rng, (hidden, classes), -2, 2) * q
+    b2 = int_matrix(rng, (classes,), -2, 2)
+    t = np.zeros((batch, classes), np.float32)
+    t[np.arange(batch), rng.integers(0, classes, batch)] = 1.0
+    D = hip.DeviceBuffer.from_host
+    h, dh = hip.DeviceBuffer(batch * hidden), hip.DeviceBuffer(batch * hidden)
+    z, gz = hip.DeviceBuffer(batch * classes), hip.DeviceBuffer(batch * classes)
+    print(f"mlp2 forward {shape}", flush=True)
+    hip.call("nrs_mlp2_forward_seed", h, z, gz, dh, D(x), D(w1), D(b1), D(w2), D(b2), D(t),
+             batch, in_f, hidden, classes)
+    h_ref = np.maximum((x.astype(np.float64) @ w1 + b1), 0).astype(np.float32)
+    hh = h.to_host((batch, hidden))
+    assert np.array_equal(hh, h_ref)
+    zz = z.to_host((batch, classes))
+    assert np.array_equal(zz, (h_ref.astype(np.float64) @ w2 + b2).astype(np.float32))
+    seed = hip.DeviceBuffer(batch * classes)
+    hip.call("nrs_cross_entropy_backward", seed, z, D(t), batch, classes)
+    g = gz.to_host((batch, classes))
+    assert np.array_equal(g.ravel(), seed.to_host())
+    assert np.abs(g - orc.cross_entropy_grad(zz, t, classes).reshape(batch, classes)).max() <= \
+        2e-7 + 1e-6 / batch
+    g64 = g.astype(np.float64)
+    dh_ref = np.where(hh > 0, g64 @ w2.T.astype(np.float64), 0.0)
+    bound = gemm_tol(classes) * (np.abs(g64) @ np.abs(w2.T.astype(np.float64)) + 1e-30)
+    assert np.all(np.abs(dh.to_host((batch, hidden)) - dh_ref) <= bound)
+    assert np.all(dh.to_host((batch, hidden))[hh <= 0] == 0.0)
+
+
+@pytest.mark.parametrize("shape", MLP2_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("betas", [(0.0, 0.0), (1.0, 0.5)], ids=["write", "accumulate"])
+@pytest.mark.parametrize("with_dx", [True, False], ids=["dx", "no_dx"])
+def test_mlp2_backward_exact(hip, shape, betas, with_dx):
+    """nrs_mlp2_backward: dx = dh . w1^T, dw1 = x^T . dh, db1 = sum(dh),
+    dw2 = h^T . gz, db2 = sum(gz), exact on small integers against numpy and
+    bit for bit against nrs_linear_backward on each layer; beta_p 0 over NaN
+    shows the old parameter gradients are not read."""
+    batch, in_f, hidden, classes = shape
+    beta_x, beta_p = betas
+    rng = np.random.default_rng(3 * batch + in_f + hidden + classes)
+    x = int_matrix(rng, (batch, in_f), -2, 2)
+    w1 = int_matrix(rng, (in_f, hidden), -2, 2)
+    h = np.maximum(int_matrix(rng, (batch, hidden), -2, 2), 0)
+    dh = int_matrix(rng, (batch, hidden), -2, 2)
+    gz = int_matrix(rng, (batch, classes), -2, 2)
+    old = [int_matrix(rng, (n,), -3, 3) if beta_p else np.full(n, np.nan, np.float32)
+           for n in (in_f * hidden, hidden, hidden * classes, classes)]
+    dx0 = int_matrix(rng, (batch * in_f,), -3, 3)
+    D = hip.DeviceBuffer.from_host
+    outs = [D(dx0)] + [D(o) for o in old]
+    print(f"mlp2 backward {shape} betas={betas} dx={with_dx}", flush=True)
+    hip.call("nrs_mlp2_backward", outs[0] if with_dx else None, *outs[1:], D(dh), D(gz), D(x),
+             D(w1), D(h), batch, in_f, hidden, classes, beta_x, beta_p)
+    f64 = np.float64
+    keep = lambda o: beta_p * o if beta_p else 0
+    want = [(dh.astype(f64) @ w1.T.astype(f64)).ravel() + beta_x * dx0,
+            (x.T.astype(f64) @ dh).ravel() + keep(old[0]), dh.sum(0, dtype=f64) + keep(old[1]),
+            (h.T.astype(f64) @ gz).ravel() + keep(old[2]), gz.sum(0, dtype=f64) + keep(old[3])]
+    for i, (o, wv) in enumerate(zip(outs, want)):
+        if i == 0 and not with_dx:
+            assert np.array_equal(o.to_host(), dx0)
+        else:
+            assert np.array_equal(o.to_host(), wv.astype(np.float32)), i
+    # nrs_linear_backward on each layer gives the same bits
+    ref = [D(dx0)] + [D(o) for o in old]
+    hip.call("nrs_linear_backward", ref[0] if with_dx else None, ref[1], ref[2], D(dh), D(x),
+             D(w1), batch, in_f, hidden, beta_x, beta_p, beta_p)
+    hip.call("nrs_linear_backward", None, ref[3], ref[4], D(gz), D(h), None, batch, hidden,
+             classes, 0.0, beta_p, beta_p)
+    for o, r in zip(outs, ref):
+        assert np.array_equal(o.to_host(), r.to_host())
+
+
+def test_mlp2_composed_step_vs_four_calls(hip):
+    """The cfg2 step on normal data, two launches (nrs_mlp2_forward_seed,
+    nrs_mlp2_backward) against the four-call form (nrs_gemm with bias and
+    ReLU, nrs_linear_cross_entropy, nrs_linear_backward_relu,
+    nrs_linear_backward): h, dx, dw1, db1 within the short-GEMM bound of K
+    (the first products reduce in different orders), the rest likewise."""
+    B, I, Hd, O = 256, 784, 128, 10
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((B, I)).astype(np.float32)
+    w1 = (rng.standard_normal((I, Hd)) * np.sqrt(2.0 / I)).astype(np.float32)
+    w2 = (rng.standard_normal((Hd, O)) * np.sqrt(2.0 / Hd)).astype(np.float32)
+    b1 = (rng.standard_normal(Hd) * 0.1).astype(np.float32)
+    b2 = (rng.standard_normal(O) * 0.1).astype(np.float32)
+    t = np.zeros((B, O), np.float32)
+    t[np.arange(B), rng.integers(0, O, B)] = 1.0
+    D = hip.DeviceBuffer.from_host
+    dx_, dw1_, db1_, dw2_, db2_, dt = D(x), D(w1), D(b1), D(w2), D(b2), D(t)
+    # four calls
+    a, z, gz, gh = (hip.DeviceBuffer(n) for n in (B * Hd, B * O, B * O, B * Hd))
+    r_gx, r_gw1, r_gb1, r_gw2, r_gb2 = (hip.DeviceBuffer.zeros(n) for n in (B * I, I * Hd, Hd, Hd * O, O))
+    hip.gemm(hip.NN, a, dx_, dw1_, B, Hd, I, 0.0, db1_, hip.EPI_BIAS_COL | hip.EPI_RELU)
+    hip.call("nrs_linear_cross_entropy", z, gz, a, dw2_, db2_, dt, B, Hd, O)
+    hip.call("nrs_linear_backward_relu", gh, r_gw2, r_gb2, gz, a, dw2_, a, B, Hd, O, 0.0, 0.0, 0.0)
+    hip.call("nrs_linear_backward", r_gx, r_gw1, r_gb1, gh, dx_, dw1_, B, I, Hd, 0.0, 0.0, 0.0)
+    # two launches
+    h2, z2, gz2, dh2 = (hip.DeviceBuffer(n) for n in (B * Hd, B * O, B * O, B * Hd))
+    gx, gw1, gb1, gw2, gb2 = (hip.DeviceBuffer(n) for n in (B * I, I * Hd, Hd, Hd * O, O))
+    print("mlp2 composed step cfg2", flush=True)
+    hip.call("nrs_mlp2_forward_seed", h2, z2, gz2, dh2, dx_, dw1_, db1_, dw2_, db2_, dt, B, I, Hd, O)
+    hip.call("nrs_mlp2_backward", gx, gw1, gb1, gw2, gb2, dh2, gz2, dx_, dw1_, h2, B, I, Hd, O,
+             0.0, 0.0)
+    f64 = np.float64
+    h_ref = np.maximum(x.astype(f64) @ w1 + b1, 0)
+    habs = np.abs(x.astype(f64)) @ np.abs(w1) + np.abs(b1)
+    for got in (h2.to_host((B, Hd)), a.to_host((B, Hd))):
+        assert np.all(np.abs(got - h_ref) <= gemm_tol(I) * habs + 1e-30)
+    # downstream of h the two forms see slightly different h; compare each
+    # with the other within a bound scaled by the data
+    pairs = [(z2, z, 1e-5), (gz2, gz, 1e-6), (dh2, gh, 1e-6), (gx, r_gx, 1e-5),
+             (gw1, r_gw1, 1e-5), (gb1, r_gb1, 1e-5), (gw2, r_gw2, 1e-5), (gb2, r_gb2, 1e-5)]
+    for mine, theirs, tol in pairs:
+        m, r = mine.to_host(), theirs.to_host()
+        assert np.abs(m - r).max() <= tol * (np.abs(r).max() + 1e-30), (tol, np.abs(m - r).max())
+
+
+def test_mlp2_errors(hip):
+    buf = hip.DeviceBuffer(4096)
+    bad = [(8, 4, 257, 3), (8, 4, 16, 17), (8, 0, 16, 3), (-1, 4, 16, 3)]
+    for b, i, hd, o in bad:
+        with pytest.raises(hip.NrsError):
+            hip.call("nrs_mlp2_forward_seed", buf, buf, buf, buf, buf, buf, None, buf, None, buf,
+                     b, i, hd, o)
+    # each output over each input (and two outputs over each other)
+    B, I, Hd, O = 8, 4, 16, 3
+    sizes = (B * Hd, B * O, B * O, B * Hd, B * I, I * Hd, Hd, Hd * O, O, B * O)
+    for out_i in range(4):
+        for other in range(10):
+            if other == out_i:
+                continue
+            bufs = [hip.DeviceBuffer(n) for n in sizes]
+            bufs[other] = bufs[out_i]  # refused before any launch
+            with pytest.raises(hip.NrsError, match="overlap"):
+                hip.call("nrs_mlp2_forward_seed", *bufs, B, I, Hd, O)
+    # no rows: nothing launched
+    hip.call("nrs_mlp2_forward_seed", None, None, None, None, None, None, None, None, None, None,
+             0, I, Hd, O)
+
+
 @pytest.mark.parametrize("layout", [NN, TN])
 @pytest.mark.parametrize("shape", [(32, 8192, 2048), (17, 1024, 300), (1, 4096, 1000),
                                    (30, 8200, 1024), (32, 1152, 8200)],
