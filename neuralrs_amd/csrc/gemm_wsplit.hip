@@ -50,17 +50,13 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
 enum WsMode { WS_NN_AV = 0, WS_NN_AS, WS_NT_AV_BV, WS_NT_AV_BS, WS_NT_AS_BV, WS_NT_AS_BS, WS_TN,
               WS_MODES };
 
-// The S values of op(A) for row m and of op(B) for column n at k = k0 .. k0+S-1
-// (zero past K, M and N).
+// The S values of op(A) for row m at k = k0 .. k0+S-1 (zero past K and M).
 template <int MODE, int S>
-__device__ __forceinline__ void load_round(const WsProblem& p, __amdgpu_buffer_rsrc_t ra,
-                                           __amdgpu_buffer_rsrc_t rb, int m, int n, int k0,
-                                           float (&av)[S], float (&bv)[S]) {
+__device__ __forceinline__ void load_a(const WsProblem& p, __amdgpu_buffer_rsrc_t ra, int m, int k0,
+                                       float (&av)[S]) {
     constexpr bool a_kc = MODE != WS_TN;
     constexpr bool a_vec = MODE == WS_NN_AV || MODE == WS_NT_AV_BV || MODE == WS_NT_AV_BS;
-    constexpr bool b_kc = MODE >= WS_NT_AV_BV && MODE <= WS_NT_AS_BS;
-    constexpr bool b_vec = MODE == WS_NT_AV_BV || MODE == WS_NT_AS_BV;
-    const bool m_ok = m < p.M, n_ok = n < p.N;
+    const bool m_ok = m < p.M;
     if constexpr (a_vec) {
 #pragma unroll
         for (int v = 0; v < S / 4; ++v) {
@@ -78,6 +74,15 @@ __device__ __forceinline__ void load_round(const WsProblem& p, __amdgpu_buffer_r
             av[s] = buffer_load1(ra, (m_ok & (k < p.K)) ? (int)(off * 4) : kOutOfRange);
         }
     }
+}
+
+// The S values of op(B) for column n at k = k0 .. k0+S-1 (zero past K and N).
+template <int MODE, int S>
+__device__ __forceinline__ void load_b(const WsProblem& p, __amdgpu_buffer_rsrc_t rb, int n, int k0,
+                                       float (&bv)[S]) {
+    constexpr bool b_kc = MODE >= WS_NT_AV_BV && MODE <= WS_NT_AS_BS;
+    constexpr bool b_vec = MODE == WS_NT_AV_BV || MODE == WS_NT_AS_BV;
+    const bool n_ok = n < p.N;
     if constexpr (b_vec) {
 #pragma unroll
         for (int v = 0; v < S / 4; ++v) {
@@ -97,32 +102,48 @@ __device__ __forceinline__ void load_round(const WsProblem& p, __amdgpu_buffer_r
     }
 }
 
-// This wave's partial 16x16 block over its k values of every round. The lane
-// holding the row of sums (row M) feeds 1 for k < K in place of A.
-template <int W, int S, int MODE>
-__device__ __forceinline__ f32x4 ws_reduce(const WsProblem& p, int m0, int n0, int w, int c,
-                                           int g) {
+// This wave's partial 16x16 blocks (TM row blocks by TN column blocks from
+// (m0, n0)) over its k values of every round. Each block sees the same MFMA
+// sequence as a workgroup of one block would, so the grouping changes no
+// bits. The lane holding the row of sums (row M) feeds 1 for k < K in place
+// of A.
+template <int W, int S, int MODE, int TM, int TN>
+__device__ __forceinline__ void ws_reduce(const WsProblem& p, int m0, int n0, int w, int c, int g,
+                                          f32x4 (&acc)[TM][TN]) {
     const auto ra = buffer_rsrc(p.A, p.a_bytes), rb = buffer_rsrc(p.B, p.b_bytes);
-    const bool ones = p.sum_row != nullptr && m0 + c == p.M;
-    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    bool ones[TM];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) ones[tm] = p.sum_row != nullptr && m0 + 16 * tm + c == p.M;
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int k0 = w * 4 * S + g * S; k0 < p.K + w * 4 * S + g * S; k0 += W * 4 * S) {
-        float av[S], bv[S];
-        load_round<MODE, S>(p, ra, rb, m0 + c, n0 + c, k0, av, bv);
+        float av[TM][S], bv[TN][S];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) load_a<MODE, S>(p, ra, m0 + 16 * tm + c, k0, av[tm]);
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) load_b<MODE, S>(p, rb, n0 + 16 * tn + c, k0, bv[tn]);
         // every load of the round before the first MFMA (left alone, the
         // scheduler interleaves them to save registers: a round trip each)
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const float a = ones ? (k0 + s < p.K ? 1.0f : 0.0f) : av[s];
-            acc = mfma16(a, bv[s], acc);
-        }
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+                const float a = ones[tm] ? (k0 + s < p.K ? 1.0f : 0.0f) : av[tm][s];
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = mfma16(a, bv[tn][s], acc[tm][tn]);
+            }
     }
-    return acc;
 }
 
-template <int W, int S>
+// One workgroup per TM x TN group of 16x16 blocks of one problem's output
+// (TM = TN = 1 for the cross-entropy epilogue, whose rows are one block).
+template <int W, int S, int TM, int TN>
 __global__ __launch_bounds__(64 * W) void gemm_wsplit_kernel(WsArgs args) {
-    __shared__ float red[W * 16 * kWsPitch];
+    constexpr int NBLK = TM * TN;
+    __shared__ float red[W * NBLK * 16 * kWsPitch];
     __shared__ float row_stat[2][16];
     int q = 0;
 #pragma unroll
@@ -133,81 +154,106 @@ __global__ __launch_bounds__(64 * W) void gemm_wsplit_kernel(WsArgs args) {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tile = (int)blockIdx.x - p.first;
     const int tm = tile / p.tiles_n, tn = tile - tm * p.tiles_n;
-    const int m0 = 16 * tm, n0 = 16 * tn;
-    f32x4 acc;
+    const int m0 = 16 * TM * tm, n0 = 16 * TN * tn;
+    f32x4 acc[TM][TN];
     switch (p.mode) {
-        case WS_NN_AV: acc = ws_reduce<W, S, WS_NN_AV>(p, m0, n0, w, c, g); break;
-        case WS_NN_AS: acc = ws_reduce<W, S, WS_NN_AS>(p, m0, n0, w, c, g); break;
-        case WS_NT_AV_BV: acc = ws_reduce<W, S, WS_NT_AV_BV>(p, m0, n0, w, c, g); break;
-        case WS_NT_AV_BS: acc = ws_reduce<W, S, WS_NT_AV_BS>(p, m0, n0, w, c, g); break;
-        case WS_NT_AS_BV: acc = ws_reduce<W, S, WS_NT_AS_BV>(p, m0, n0, w, c, g); break;
-        case WS_NT_AS_BS: acc = ws_reduce<W, S, WS_NT_AS_BS>(p, m0, n0, w, c, g); break;
-        default: acc = ws_reduce<W, S, WS_TN>(p, m0, n0, w, c, g); break;
+        case WS_NN_AV: ws_reduce<W, S, WS_NN_AV, TM, TN>(p, m0, n0, w, c, g, acc); break;
+        case WS_NN_AS: ws_reduce<W, S, WS_NN_AS, TM, TN>(p, m0, n0, w, c, g, acc); break;
+        case WS_NT_AV_BV: ws_reduce<W, S, WS_NT_AV_BV, TM, TN>(p, m0, n0, w, c, g, acc); break;
+        case WS_NT_AV_BS: ws_reduce<W, S, WS_NT_AV_BS, TM, TN>(p, m0, n0, w, c, g, acc); break;
+        case WS_NT_AS_BV: ws_reduce<W, S, WS_NT_AS_BV, TM, TN>(p, m0, n0, w, c, g, acc); break;
+        case WS_NT_AS_BS: ws_reduce<W, S, WS_NT_AS_BS, TM, TN>(p, m0, n0, w, c, g, acc); break;
+        default: ws_reduce<W, S, WS_TN, TM, TN>(p, m0, n0, w, c, g, acc); break;
     }
-    // lane (c, g) holds rows 4g..4g+3 of column c of this wave's partial block
+    // lane (c, g) holds rows 4g..4g+3 of column c of each of this wave's
+    // partial blocks
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[(w * 16 + 4 * g + r) * kWsPitch + c] = acc[r];
+    for (int bm = 0; bm < TM; ++bm)
+#pragma unroll
+        for (int bn = 0; bn < TN; ++bn)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                red[((w * NBLK + bm * TN + bn) * 16 + 4 * g + r) * kWsPitch + c] = acc[bm][bn][r];
     __syncthreads();
-    const int i = (tid >> 4) & 15, j = tid & 15;
-    const int row = m0 + i, col = n0 + j;
-    float v = 0.0f;
-    if (tid < 256) {
+    if constexpr (NBLK == 1) {
+        if (p.epi & kWsCe) {
+            // the fused seed (softmax(logits) - target) / batch, with the
+            // reference kernel's arithmetic: the row max folded from class 0,
+            // the sum of expf(l - max) in class order, then expf(l - max) / sum
+            const int i = (tid >> 4) & 15, j = tid & 15;
+            const int row = m0 + i, col = n0 + j;
+            float v = 0.0f;
+            if (tid < 256) {
 #pragma unroll
-        for (int ww = 0; ww < W; ++ww) v += red[(ww * 16 + i) * kWsPitch + j];
-        if (p.epi & NRS_EPI_BIAS_COL) v += col < p.N ? p.bias[col] : 0.0f;
+                for (int ww = 0; ww < W; ++ww) v += red[(ww * 16 + i) * kWsPitch + j];
+                if (p.epi & NRS_EPI_BIAS_COL) v += col < p.N ? p.bias[col] : 0.0f;
+                if (p.epi & NRS_EPI_BIAS_ROW) v += row < p.M ? p.bias[row] : 0.0f;
+            }
+            __syncthreads();  // every wave is done reading its partial block
+            if (tid < 256) red[i * kWsPitch + j] = v;
+            __syncthreads();
+            if (tid < 16 && m0 + tid < p.M) {
+                const float* l = red + tid * kWsPitch;
+                float mx = l[0];
+                for (int cc = 1; cc < p.N; ++cc) mx = fmaxf(mx, l[cc]);
+                float sum = 0.0f;
+                for (int cc = 0; cc < p.N; ++cc) sum += expf(l[cc] - mx);
+                row_stat[0][tid] = mx;
+                row_stat[1][tid] = sum;
+            }
+            __syncthreads();
+            if (tid < 256 && row < p.M && col < p.N) {
+                const int64_t idx = (int64_t)row * p.ldc + col;
+                const float t = p.target[idx];
+                p.aux[idx] = (expf(v - row_stat[0][i]) / row_stat[1][i] - t) * p.inv_batch;
+                if (p.C) p.C[idx] = v;
+            }
+            return;
+        }
+    }
+    // one thread per output element: the W partials added in wave order
+    for (int e = tid; e < NBLK * 256; e += 64 * W) {
+        const int blk = e >> 8, i = (e >> 4) & 15, j = e & 15;
+        const int bm = blk / TN, bn = blk - bm * TN;
+        const int row = m0 + 16 * bm + i, col = n0 + 16 * bn + j;
+        if (col >= p.N) continue;
+        float v = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < W; ++ww) v += red[((ww * NBLK + blk) * 16 + i) * kWsPitch + j];
+        if (p.epi & NRS_EPI_BIAS_COL) v += p.bias[col];
         if (p.epi & NRS_EPI_BIAS_ROW) v += row < p.M ? p.bias[row] : 0.0f;
-    }
-    if (p.epi & kWsCe) {
-        // the fused seed (softmax(logits) - target) / batch, with the
-        // reference kernel's arithmetic: the row max folded from class 0,
-        // the sum of expf(l - max) in class order, then expf(l - max) / sum
-        __syncthreads();  // every wave is done reading its partial block
-        if (tid < 256) red[i * kWsPitch + j] = v;
-        __syncthreads();
-        if (tid < 16 && m0 + tid < p.M) {
-            const float* l = red + tid * kWsPitch;
-            float mx = l[0];
-            for (int cc = 1; cc < p.N; ++cc) mx = fmaxf(mx, l[cc]);
-            float sum = 0.0f;
-            for (int cc = 0; cc < p.N; ++cc) sum += expf(l[cc] - mx);
-            row_stat[0][tid] = mx;
-            row_stat[1][tid] = sum;
-        }
-        __syncthreads();
-        if (tid < 256 && row < p.M && col < p.N) {
+        if (row < p.M) {
+            if (p.epi & NRS_EPI_RELU) v = fmaxf(v, 0.0f);
             const int64_t idx = (int64_t)row * p.ldc + col;
-            const float t = p.target[idx];
-            p.aux[idx] = (expf(v - row_stat[0][i]) / row_stat[1][i] - t) * p.inv_batch;
-            if (p.C) p.C[idx] = v;
+            if ((p.epi & kWsMask) && !(p.mask[idx] > 0.0f)) v = 0.0f;
+            if (p.beta != 0.0f) v = v + p.beta * p.C[idx];
+            p.C[idx] = v;
+        } else if (row == p.M && p.sum_row != nullptr) {
+            if (p.sum_beta != 0.0f) v = v + p.sum_beta * p.sum_row[col];
+            p.sum_row[col] = v;
         }
-        return;
-    }
-    if (tid >= 256 || col >= p.N) return;
-    if (row < p.M) {
-        if (p.epi & NRS_EPI_RELU) v = fmaxf(v, 0.0f);
-        const int64_t idx = (int64_t)row * p.ldc + col;
-        if ((p.epi & kWsMask) && !(p.mask[idx] > 0.0f)) v = 0.0f;
-        if (p.beta != 0.0f) v = v + p.beta * p.C[idx];
-        p.C[idx] = v;
-    } else if (row == p.M && p.sum_row != nullptr) {
-        if (p.sum_beta != 0.0f) v = v + p.sum_beta * p.sum_row[col];
-        p.sum_row[col] = v;
     }
 }
 
 using WsKernel = void (*)(WsArgs);
 
 // (waves, k values per lane group per round) for a reduction of length K:
-// the smallest round that covers K, else 8 waves of 32 (several rounds).
+// the smallest round that covers K, else 8 waves of 32 (several rounds);
+// `group`: each workgroup takes 2 x 2 blocks.
+template <int TM, int TN>
 WsKernel ws_kernel_for(int64_t K, int& threads) {
     if (K <= 128) {
         threads = 256;
-        return gemm_wsplit_kernel<4, 8>;
+        return gemm_wsplit_kernel<4, 8, TM, TN>;
     }
     threads = 512;
-    if (K <= 256) return gemm_wsplit_kernel<8, 8>;
-    if (K <= 512) return gemm_wsplit_kernel<8, 16>;
-    return gemm_wsplit_kernel<8, 32>;
+    if (K <= 256) return gemm_wsplit_kernel<8, 8, TM, TN>;
+    if (K <= 512) return gemm_wsplit_kernel<8, 16, TM, TN>;
+    return gemm_wsplit_kernel<8, 32, TM, TN>;
+}
+
+WsKernel ws_kernel_for(int64_t K, bool group, int& threads) {
+    return group ? ws_kernel_for<2, 2>(K, threads) : ws_kernel_for<1, 1>(K, threads);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -278,16 +324,32 @@ int wsplit_run(const GemmCall* calls, int count, const WsExtra* extra) {
             p.inv_batch = 1.0f / (float)c.M;
             p.epi |= kWsCe;
         }
-        const int64_t mrows = c.M + (c.sum_row ? 1 : 0);
-        p.tiles_n = (int)((c.N + 15) / 16);
-        p.first = (int)total;
-        total += ((mrows + 15) / 16) * p.tiles_n;
         kmax = std::max<int64_t>(kmax, c.K);
+    }
+    // Outputs of many 16x16 blocks (more than two a CU) go 2 x 2 blocks a
+    // workgroup: a quarter of the workgroups, each reusing its loads of A
+    // and B twice, with every block's arithmetic unchanged. The
+    // cross-entropy epilogue keeps one block a workgroup.
+    int64_t blocks = 0;
+    bool ce = false;
+    for (int i = 0; i < count; ++i) {
+        const int64_t mrows = calls[i].M + (calls[i].sum_row ? 1 : 0);
+        blocks += ((mrows + 15) / 16) * ((calls[i].N + 15) / 16);
+        ce = ce || (a.prob[i].epi & kWsCe);
+    }
+    const bool group = !ce && blocks > 2 * (int64_t)num_cus();
+    const int bm = group ? 32 : 16, bn = group ? 32 : 16;
+    for (int i = 0; i < count; ++i) {
+        WsProblem& p = a.prob[i];
+        const int64_t mrows = calls[i].M + (calls[i].sum_row ? 1 : 0);
+        p.tiles_n = (int)((calls[i].N + bn - 1) / bn);
+        p.first = (int)total;
+        total += ((mrows + bm - 1) / bm) * p.tiles_n;
     }
     a.count = count;
     NRS_ARG_CHECK(total <= INT32_MAX, "short gemm: grid too large");
     int threads = 0;
-    WsKernel fn = ws_kernel_for(kmax, threads);
+    WsKernel fn = ws_kernel_for(kmax, group, threads);
     hipLaunchKernelGGL(fn, dim3((unsigned)total), dim3(threads), 0, stream(), a);
     NRS_LAUNCH_CHECK("short gemm");
     return NRS_OK;
