@@ -67,6 +67,12 @@ int gemm_run(const GemmCall& c);
 // qualify (see nrs_gemm_group), else gemm_run on each in order.
 int gemm_group_run(const GemmCall* calls, int count);
 
+// nrs_linear_backward (dx = grad . w^T masked where mask <= 0 when mask is
+// given, dw = x^T . grad, db = column sums of grad; each + beta * old).
+int linear_backward(float* dx, float* dw, float* db, const float* grad, const float* x,
+                    const float* w, const float* mask, int64_t batch, int64_t in_f, int64_t out_f,
+                    float beta_x, float beta_w, float beta_b);
+
 // Whether byte ranges [a, a + abytes) and [b, b + bbytes) share memory (an
 // empty range overlaps nothing).
 bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes);

@@ -414,6 +414,16 @@ int nrs_mlp2_backward(float* dx, float* dw1, float* db1, float* dw2, float* db2,
     NRS_ARG_CHECK(batch >= 0 && in_f >= 0 && hidden >= 0 && classes >= 0,
                   "mlp2 backward: negative size");
     NRS_ARG_CHECK(dw1 && dw2, "mlp2 backward: null weight gradient");
+    if (batch == 0 || in_f == 0 || hidden == 0 || classes == 0) {
+        // no rows (the sums are empty: beta_p * old), or a product with no
+        // output rows to carry its row of sums: each layer's
+        // nrs_linear_backward, which handles both
+        const int rc = nrs::linear_backward(dx, dw1, db1, dh, x, w1, nullptr, batch, in_f,
+                                            hidden, beta_x, beta_p, beta_p);
+        if (rc != NRS_OK) return rc;
+        return nrs::linear_backward(nullptr, dw2, db2, gz, h, nullptr, nullptr, batch, hidden,
+                                    classes, 0.0f, beta_p, beta_p);
+    }
     // dW1 = x^T . dh (+ db1 as its row of sums), dx = dh . w1^T,
     // dW2 = h^T . gz (+ db2): nrs_linear_backward's products for both layers
     nrs::GemmCall calls[3];

@@ -722,6 +722,32 @@ def test_mlp2_backward_exact(hip, shape, betas, with_dx):
         assert np.array_equal(o.to_host(), r.to_host())
 
 
+@pytest.mark.parametrize("shape", [(0, 12, 8, 3), (6, 0, 8, 3), (6, 12, 8, 3)],
+                         ids=["no_rows", "no_inputs", "small"])
+def test_mlp2_backward_degenerate(hip, shape):
+    """nrs_mlp2_backward without rows (every sum empty: the parameter
+    gradients become beta_p * old) or without input features (db1 still the
+    column sums of dh, with no dW1 rows to carry them), against numpy."""
+    batch, in_f, hidden, classes = shape
+    rng = np.random.default_rng(batch + in_f)
+    x = int_matrix(rng, (batch, in_f), -2, 2)
+    w1 = int_matrix(rng, (in_f, hidden), -2, 2)
+    h = np.maximum(int_matrix(rng, (batch, hidden), -2, 2), 0)
+    dh = int_matrix(rng, (batch, hidden), -2, 2)
+    gz = int_matrix(rng, (batch, classes), -2, 2)
+    old = [int_matrix(rng, (n,), -3, 3) for n in (in_f * hidden, hidden, hidden * classes, classes)]
+    D = hip.DeviceBuffer.from_host
+    outs = [D(o) for o in old]
+    print(f"mlp2 backward degenerate {shape}", flush=True)
+    hip.call("nrs_mlp2_backward", None, *outs, D(dh), D(gz), D(x), D(w1), D(h), batch, in_f,
+             hidden, classes, 0.0, 0.5)
+    f64 = np.float64
+    want = [(x.T.astype(f64) @ dh).ravel(), dh.sum(0, dtype=f64), (h.T.astype(f64) @ gz).ravel(),
+            gz.sum(0, dtype=f64)]
+    for o, wv, o0 in zip(outs, want, old):
+        assert np.array_equal(o.to_host(), (wv + 0.5 * o0).astype(np.float32))
+
+
 def test_mlp2_composed_step_vs_four_calls(hip):
     """The cfg2 step on normal data, two launches (nrs_mlp2_forward_seed,
     nrs_mlp2_backward) against the four-call form (nrs_gemm with bias and
