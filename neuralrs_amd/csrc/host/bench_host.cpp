@@ -147,11 +147,8 @@ int bench_cnn(int steps, int warmup) {
                            : hip::nn::maxpool2d(hip::graph::relu(hip::nn::conv2d(x, w1, b1, 1, 1)),
                                                 2, 2);
         NodeRef out = hip::nn::conv2d(p1, w2, b2, 1, 1);
-        // the upstream gradient: in the CNN the next layer's backward leaves
-        // it in out's gradient buffer, so the step installs the seed buffer
-        // as that gradient (a view of it) rather than timing a 6.4 MB copy
-        // that belongs to no conv layer
-        out->gpu->grad = std::make_shared<DeviceBuffer>(DeviceBuffer::view_of(seed));
+        nrs_check(nrs_memcpy_dtod(out->gpu->grad->write_target(), seed.ptr(), seed.len() * sizeof(float)),
+                  "seed");
         backward_graph(out);
         gpu::zero_grad(params);
     };
