@@ -17,12 +17,13 @@
 // within that time, so 64 workgroups run at batch 256. The reduction over
 // in_f is split over the 8 waves (ranges of kw rows of w1), each wave
 // requesting its next batch of rows before reducing the current one; the
-// partial rows meet in LDS and are added in a fixed order. The rest is small: w2 is staged in LDS, the logits
-// reduce their hidden dimension in 8 parts added in order, the seed is
-// ce_backward's arithmetic (src/cuda/loss/cross_entropy.rs:39-58: the row max
-// folded from class 0, the sum of expf(l - max) in class order), and dh is
-// relu_grad of src/cuda/graph/relu.rs:23-28 (the gradient where the
-// pre-activation, equivalently h, is > 0) applied to gz . w2^T.
+// partial rows meet in LDS and are added in a fixed order. The rest is
+// small: w2 is staged in LDS, the logits reduce their hidden dimension in 8
+// parts added in order, the seed is ce_backward's arithmetic
+// (src/cuda/loss/cross_entropy.rs:39-58: the row max folded from class 0,
+// the sum of expf(l - max) in class order), and dh is relu_grad of
+// src/cuda/graph/relu.rs:23-28 (the gradient where the pre-activation,
+// equivalently h, is > 0) applied to gz . w2^T.
 #include <algorithm>
 
 #include "buffer_ops.hpp"
