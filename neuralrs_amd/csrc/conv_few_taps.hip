@@ -59,8 +59,36 @@ void wgrad_few_taps_kernel(FewTapsArgs a) {
     const int n = blockIdx.x / a.chunks, chunk = blockIdx.x - n * a.chunks;
     const int t = lane & 15, kq = lane >> 4;
 
-    // gradient fragments first: [group][block], pixels 16*gi + 4*kq .. +3
-    // of channel 16*b + t (zero past P and M through the buffer bounds)
+    // the input image with a zero halo of `pad` (rows and columns), kStageX
+    // items per thread per round (a load at kOutOfRange returns zero, so the
+    // halo needs no select that would make each load wait for the previous).
+    // An image of one round is requested before the gradient, so the two
+    // round trips overlap (with the pooled gradient, expanding it waits for
+    // its loads).
+    const auto rimg =
+        buffer_rsrc(a.x + (int64_t)n * a.C * a.H * a.W, (int64_t)a.C * a.H * a.W * 4);
+    const int plane = a.Hp * a.Wp, xn = a.C * plane;
+    auto stage_load = [&](int e0, float (&v)[kStageX]) {
+#pragma unroll
+        for (int k = 0; k < kStageX; ++k) {
+            const int e = e0 + k * 256 + tid;
+            const int c = e / plane, r = e - c * plane, yy = r / a.Wp, xx = r - yy * a.Wp;
+            const int iy = yy - a.pad, ix = xx - a.pad;
+            const bool ok = (e < xn) & ((unsigned)iy < (unsigned)a.H) & ((unsigned)ix < (unsigned)a.W);
+            v[k] = buffer_load1(rimg, ok ? ((c * a.H + iy) * a.W + ix) * 4 : kOutOfRange);
+        }
+    };
+    auto stage_store = [&](int e0, const float (&v)[kStageX]) {
+#pragma unroll
+        for (int k = 0; k < kStageX; ++k)
+            if (e0 + k * 256 + tid < xn) xs[e0 + k * 256 + tid] = v[k];
+    };
+    const bool one_round = xn <= 256 * kStageX;
+    float v0[kStageX];
+    stage_load(0, v0);
+
+    // gradient fragments: [group][block], pixels 16*gi + 4*kq .. +3 of
+    // channel 16*b + t (zero past P and M through the buffer bounds)
     const int g0 = (chunk * 4 + wave) * GPW;
     f32x4v ga[GPW][NBLK];
     if constexpr (!UNPOOL) {
@@ -75,6 +103,7 @@ void wgrad_few_taps_kernel(FewTapsArgs a) {
                     buffer_load4(rg, ((p < a.P) & (oc < a.M)) ? (oc * a.P + p) * 4 : kOutOfRange);
             }
         }
+        stage_store(0, v0);  // waits for the image only: the older loads
     } else {
         // pixels p .. p+3 (one row: OW % 4 == 0) lie in pooled columns
         // x/2 and x/2 + 1 of pooled row y/2: two pooled values and two
@@ -109,6 +138,7 @@ void wgrad_few_taps_kernel(FewTapsArgs a) {
                 vv[q][b] = buffer_load2(rv, (ok & relu) ? (oc * PP + pw) * 4 : kOutOfRange);
             }
         }
+        stage_store(0, v0);  // waits for the image only: the older loads
 #pragma unroll
         for (int q = 0; q < GPW; ++q)
 #pragma unroll
@@ -128,29 +158,17 @@ void wgrad_few_taps_kernel(FewTapsArgs a) {
             }
     }
 
-    // the image with a zero halo of `pad` (rows and columns), kStageX items
-    // per thread per round: every load of a round is issued before its
-    // stores (a load at kOutOfRange returns zero, so the halo needs no
-    // select that would make each load wait for the previous)
-    const auto rimg =
-        buffer_rsrc(a.x + (int64_t)n * a.C * a.H * a.W, (int64_t)a.C * a.H * a.W * 4);
-    const int plane = a.Hp * a.Wp, xn = a.C * plane;
-    for (int e0 = 0; e0 < xn; e0 += 256 * kStageX) {
-        float v[kStageX];
-#pragma unroll
-        for (int k = 0; k < kStageX; ++k) {
-            const int e = e0 + k * 256 + tid;
-            const int c = e / plane, r = e - c * plane, yy = r / a.Wp, xx = r - yy * a.Wp;
-            const int iy = yy - a.pad, ix = xx - a.pad;
-            const bool ok = (e < xn) & ((unsigned)iy < (unsigned)a.H) & ((unsigned)ix < (unsigned)a.W);
-            v[k] = buffer_load1(rimg, ok ? ((c * a.H + iy) * a.W + ix) * 4 : kOutOfRange);
+    // the image's further rounds, every load of a round issued before its
+    // stores
+    if (!one_round) {
+        for (int e0 = 256 * kStageX; e0 < xn; e0 += 256 * kStageX) {
+            float v[kStageX];
+            stage_load(e0, v);
+            stage_store(e0, v);
+            // nothing outstanding at the loop edge: the compiler would
+            // otherwise wait for the gradient loads before the next round
+            __builtin_amdgcn_s_waitcnt(0);
         }
-#pragma unroll
-        for (int k = 0; k < kStageX; ++k)
-            if (e0 + k * 256 + tid < xn) xs[e0 + k * 256 + tid] = v[k];
-        // nothing outstanding at the loop edge: the compiler would otherwise
-        // wait for the gradient loads above before the first image load
-        __builtin_amdgcn_s_waitcnt(0);
     }
     // this lane's tap: offset in the staged image, or the bias column
     int toff = 0;
