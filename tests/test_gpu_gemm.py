@@ -793,6 +793,66 @@ def test_mlp2_composed_step_vs_four_calls(hip):
         assert np.abs(m - r).max() <= tol * (np.abs(r).max() + 1e-30), (tol, np.abs(m - r).max())
 
 
+def test_mlp2_step_vs_f64(hip, orc):
+    """The two-launch cfg2 step at full size on normal data against a float64
+    restatement of the step (Linear, ReLU, Linear, ce_backward's seed, both
+    backward closures), each output within the f32 GEMM bound of its own
+    reduction length times the float64 magnitude sum; the seed also within
+    the CE test's bound of the oracle's gradient of the float64 logits."""
+    B, I, Hd, O = 256, 784, 128, 10
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((B, I)).astype(np.float32)
+    w1 = (rng.standard_normal((I, Hd)) * np.sqrt(2.0 / I)).astype(np.float32)
+    w2 = (rng.standard_normal((Hd, O)) * np.sqrt(2.0 / Hd)).astype(np.float32)
+    b1 = (rng.standard_normal(Hd) * 0.1).astype(np.float32)
+    b2 = (rng.standard_normal(O) * 0.1).astype(np.float32)
+    t = np.zeros((B, O), np.float32)
+    t[np.arange(B), rng.integers(0, O, B)] = 1.0
+    D = hip.DeviceBuffer.from_host
+    h, z, gz, dh = (hip.DeviceBuffer(n) for n in (B * Hd, B * O, B * O, B * Hd))
+    gx, gw1, gb1, gw2, gb2 = (hip.DeviceBuffer(n) for n in (B * I, I * Hd, Hd, Hd * O, O))
+    print("mlp2 step vs f64 cfg2", flush=True)
+    hip.call("nrs_mlp2_forward_seed", h, z, gz, dh, D(x), D(w1), D(b1), D(w2), D(b2), D(t),
+             B, I, Hd, O)
+    hip.call("nrs_mlp2_backward", gx, gw1, gb1, gw2, gb2, dh, gz, D(x), D(w1), h, B, I, Hd, O,
+             0.0, 0.0)
+    f = np.float64
+    X, W1, W2 = x.astype(f), w1.astype(f), w2.astype(f)
+    pre = X @ W1 + b1
+    H64 = np.maximum(pre, 0)
+    Z64 = H64 @ W2 + b2
+    e = np.exp(Z64 - Z64.max(1, keepdims=True))
+    G64 = (e / e.sum(1, keepdims=True) - t) / B
+    DH64 = np.where(pre > 0, G64 @ W2.T, 0.0)
+
+    def within(got, want, bound):
+        assert np.all(np.abs(got - want) <= bound), np.max(np.abs(got - want) / (bound + 1e-300))
+
+    hh = h.to_host((B, Hd))
+    within(hh, H64, gemm_tol(I) * (np.abs(X) @ np.abs(W1) + np.abs(b1)))
+    within(z.to_host((B, O)), Z64, gemm_tol(I) * (np.abs(H64) @ np.abs(W2) + np.abs(b2)) * 4)
+    gzz = gz.to_host((B, O))
+    within(gzz, G64, 2e-6 / B + 1e-6 * np.abs(G64))
+    assert np.abs(gzz - orc.cross_entropy_grad(Z64.astype(np.float32), t, O).reshape(B, O)).max() \
+        <= 2e-7 + 1e-6 / B
+    # dh, and what the backward builds from the kernel's own gz and dh
+    # (pre-activations within rounding of zero may switch the mask: those
+    # elements are left out of dh's check)
+    clear = np.abs(pre) > 1e-4 * (np.abs(X) @ np.abs(W1) + np.abs(b1))
+    g64 = gzz.astype(f)
+    dhh = dh.to_host((B, Hd))
+    within(dhh[clear], np.where(hh > 0, g64 @ W2.T, 0.0)[clear],
+           (gemm_tol(O) * (np.abs(g64) @ np.abs(W2.T)))[clear] + 1e-30)
+    d64 = dhh.astype(f)
+    within(gx.to_host((B, I)), d64 @ W1.T, gemm_tol(Hd) * (np.abs(d64) @ np.abs(W1.T)) + 1e-30)
+    within(gw1.to_host((I, Hd)), X.T @ d64, gemm_tol(B) * (np.abs(X.T) @ np.abs(d64)) + 1e-30)
+    within(gb1.to_host(), d64.sum(0), gemm_tol(B) * np.abs(d64).sum(0) + 1e-30)
+    within(gw2.to_host((Hd, O)), hh.astype(f).T @ g64,
+           gemm_tol(B) * (np.abs(hh.astype(f).T) @ np.abs(g64)) + 1e-30)
+    within(gb2.to_host(), g64.sum(0), gemm_tol(B) * np.abs(g64).sum(0) + 1e-30)
+    assert np.count_nonzero(~clear) < 0.01 * clear.size  # ~0.1% at this cut
+
+
 def test_mlp2_errors(hip):
     buf = hip.DeviceBuffer(4096)
     bad = [(8, 4, 257, 3), (8, 4, 16, 17), (8, 0, 16, 3), (-1, 4, 16, 3)]
