@@ -178,8 +178,10 @@ int nrs_linear_cross_entropy(float *logits, float *grad, const float *x, const f
  *   gz = (softmax(z) - target) / batch   [batch, classes]  ce_backward's seed
  *   dh = (gz . w2^T) where h > 0         [batch, hidden]   relu_grad
  *                                          (src/cuda/graph/relu.rs:23-28)
- * hidden <= 256, classes <= 16; b1, b2 may be NULL. No output may overlap an
- * input or another output.                                                   */
+ * One launch for hidden <= 256, classes <= 16 and in_f <= 4096; any other
+ * shape gives the same quantities from three launches (layer 1 with bias and
+ * ReLU, nrs_linear_cross_entropy, the masked dh product). b1, b2 may be NULL.
+ * No output may overlap an input or another output.                          */
 int nrs_mlp2_forward_seed(float *h, float *z, float *gz, float *dh, const float *x,
                           const float *w1, const float *b1, const float *w2, const float *b2,
                           const float *target, int64_t batch, int64_t in_f, int64_t hidden,

@@ -40,6 +40,7 @@ constexpr int kHeadMaxHidden = 256;
 constexpr int kHeadMaxClasses = 16;
 constexpr int kHeadMaxIn = 4096;                // the block's x rows staged in LDS (64 KB)
 constexpr int kHeadSmallIn = 1024;
+constexpr int kHeadXPad = 64;                   // zeros after the staged x rows
 
 struct HeadArgs {
     const float* x;       // [B][I]
@@ -82,7 +83,7 @@ template <int HP, bool FAST, bool SMALLX>
 __global__ __launch_bounds__(kHeadThreads) void mlp_head_kernel(HeadArgs a) {
     constexpr int P = 256 / HP, LPR = HP / 4, RP = HP + 4, NPART = kHeadWaves * P;
     constexpr int NB = 8;  // w1 loads per batch (8 KB a wave); two batches in flight
-    extern __shared__ __attribute__((aligned(16))) float xs[];  // [4][I] x rows, then P zeros
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // [4][I] x rows, then kHeadXPad zeros
     __shared__ float red[NPART * kHeadRows * RP];  // partial rows of h, then logit parts
     __shared__ float w2s[HP * kHeadMaxClasses];
     __shared__ float hs[kHeadRows * HP];
@@ -159,7 +160,11 @@ __global__ __launch_bounds__(kHeadThreads) void mlp_head_kernel(HeadArgs a) {
     } else {
         for (int e = tid; e < xn; e += kHeadThreads) xs[e] = buffer_load1(rx, e * 4);
     }
-    if (tid < P) xs[xn + tid] = 0.0f;  // read (times a zero w1 value) past the last row
+    // past the last row: a batch may run up to KB - 1 rows past the wave's
+    // range (plus the parity q), whose w1 values read as zero; their x
+    // values must be finite (0 * NaN is NaN), so they read zeros
+    static_assert(KB + P <= kHeadXPad, "zero pad past the x rows");
+    if (tid < kHeadXPad) xs[xn + tid] = 0.0f;
     // w2 (read by the logits and dh) into registers; it goes to LDS after
     // the reduction, so no wait for it sits among the batches' loads
     constexpr int W2PT = HP * kHeadMaxClasses / kHeadThreads;
@@ -319,16 +324,10 @@ int nrs_mlp2_forward_seed(float* h, float* z, float* gz, float* dh, const float*
                           const float* target, int64_t batch, int64_t in_f, int64_t hidden,
                           int64_t classes) {
     NRS_REQUIRE_INIT();
-    NRS_ARG_CHECK(batch >= 0 && in_f >= 1 && in_f <= nrs::kHeadMaxIn && hidden >= 1 &&
-                      hidden <= nrs::kHeadMaxHidden && classes >= 1 &&
-                      classes <= nrs::kHeadMaxClasses,
-                  "mlp2 forward: unsupported shape (batch %lld, in %lld, hidden %lld, classes "
-                  "%lld): 1 <= in <= %d, hidden <= %d, classes <= %d",
-                  (long long)batch, (long long)in_f, (long long)hidden, (long long)classes,
-                  nrs::kHeadMaxIn, nrs::kHeadMaxHidden, nrs::kHeadMaxClasses);
+    NRS_ARG_CHECK(batch >= 0 && in_f >= 1 && hidden >= 1 && classes >= 1,
+                  "mlp2 forward: bad shape (batch %lld, in %lld, hidden %lld, classes %lld)",
+                  (long long)batch, (long long)in_f, (long long)hidden, (long long)classes);
     if (batch == 0) return NRS_OK;
-    NRS_ARG_CHECK(batch * in_f < (int64_t(1) << 29) && in_f * hidden < (int64_t(1) << 29),
-                  "mlp2 forward: operands too large for 32-bit offsets");
     NRS_ARG_CHECK(h && z && gz && dh && x && w1 && w2 && target, "mlp2 forward: null pointer");
     // the outputs are written while other workgroups still read the inputs
     const size_t hb = sizeof(float) * (size_t)(batch * hidden);
@@ -351,6 +350,30 @@ int nrs_mlp2_forward_seed(float* h, float* z, float* gz, float* dh, const float*
         for (int j = i + 1; j < 4; ++j)
             NRS_ARG_CHECK(!nrs::overlaps(outs[i].p, outs[i].n, outs[j].p, outs[j].n),
                           "mlp2 forward: outputs overlap");
+    }
+    const bool fused = in_f <= nrs::kHeadMaxIn && hidden <= nrs::kHeadMaxHidden &&
+                       classes <= nrs::kHeadMaxClasses && batch * in_f < (int64_t(1) << 29) &&
+                       in_f * hidden < (int64_t(1) << 29) && batch <= INT32_MAX;
+    if (!fused) {
+        // past the one-launch kernel's limits, the same quantities from three
+        // launches: layer 1 with its bias and ReLU in the GEMM epilogue,
+        // layer 2 with the seed (nrs_linear_cross_entropy), and dh = gz . w2^T
+        // masked where h > 0 in the product's epilogue
+        int rc = nrs_gemm(NRS_NN, h, x, w1, batch, hidden, in_f, 0.0f, b1,
+                          (b1 ? NRS_EPI_BIAS_COL : NRS_EPI_NONE) | NRS_EPI_RELU);
+        if (rc != NRS_OK) return rc;
+        rc = nrs_linear_cross_entropy(z, gz, h, w2, b2, target, batch, hidden, classes);
+        if (rc != NRS_OK) return rc;
+        nrs::GemmCall c;
+        c.layout = NRS_NT;
+        c.C = dh;
+        c.A = gz;
+        c.B = w2;
+        c.M = batch;
+        c.N = hidden;
+        c.K = classes;
+        c.mask = h;
+        return nrs::gemm_run(c);
     }
     nrs::HeadArgs a;
     a.x = x;
@@ -387,10 +410,10 @@ int nrs_mlp2_forward_seed(float* h, float* z, float* gz, float* dh, const float*
          {nrs::mlp_head_kernel<256, true, false>, nrs::mlp_head_kernel<256, true, true>}}};
     const int hi = hp == 64 ? 0 : (hp == 128 ? 1 : 2);
     const Fn fn = kFns[hi][fast ? 1 : 0][small ? 1 : 0];
-    // the block's x rows (+ 4 zeros) in dynamic LDS, beside the static LDS
-    // (at most ~54 KB): allowed up to the largest in_f once per kernel
-    const size_t lds = sizeof(float) * (size_t)(nrs::kHeadRows * in_f + 4);
-    constexpr size_t kMaxDyn = sizeof(float) * (nrs::kHeadRows * nrs::kHeadMaxIn + 4);
+    // the block's x rows and their zero pad in dynamic LDS, beside the static
+    // LDS (at most ~54 KB): allowed up to the largest in_f once per kernel
+    const size_t lds = sizeof(float) * (size_t)(nrs::kHeadRows * in_f + nrs::kHeadXPad);
+    constexpr size_t kMaxDyn = sizeof(float) * (nrs::kHeadRows * nrs::kHeadMaxIn + nrs::kHeadXPad);
     static bool attr_set[12] = {};
     const int fi = hi * 4 + (fast ? 2 : 0) + (small ? 1 : 0);
     if (!attr_set[fi]) {

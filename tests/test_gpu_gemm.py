@@ -634,7 +634,11 @@ MLP2_SHAPES = [(256, 784, 128, 10),   # cfg2
                 (7, 50, 100, 3),       # ragged row block, hidden not a multiple of 64
                 (33, 17, 256, 16),     # four hidden column groups, the most classes
                 (5, 1, 64, 1),         # one input feature, one class
-                (64, 300, 192, 10)]    # three column groups, in_f not a multiple of 8
+                (64, 300, 192, 10),    # three column groups, in_f not a multiple of 8
+                # past the one-launch kernel's limits: three launches
+                (8, 4100, 64, 3),      # in_f > 4096
+                (9, 30, 260, 5),       # hidden > 256
+                (7, 20, 32, 20)]       # classes > 16
 
 
 @pytest.mark.parametrize("shape", MLP2_SHAPES, ids=lambda s: "x".join(map(str, s)))
@@ -793,6 +797,39 @@ def test_mlp2_composed_step_vs_four_calls(hip):
         assert np.abs(m - r).max() <= tol * (np.abs(r).max() + 1e-30), (tol, np.abs(m - r).max())
 
 
+def test_mlp2_forward_after_nan_in_lds(hip):
+    """A wave's last batch of w1 rows may run past its range (those rows read
+    as zeros); their x operands must read the zero pad after the staged x
+    rows, not stale LDS. Calls on NaN inputs with a slightly larger in_f leave
+    NaN in LDS where a cfg2 call's overrun lands; the cfg2 call after them
+    must still be exact (quarter-integer data)."""
+    D = hip.DeviceBuffer.from_host
+    rng = np.random.default_rng(5)
+    for in_nan in (800, 820, 840):
+        B, Hd, O = 256, 128, 10
+        nan = D(np.full(B * in_nan, np.nan, np.float32))
+        w = D(np.full(in_nan * Hd, np.nan, np.float32))
+        outs = [hip.DeviceBuffer(n) for n in (B * Hd, B * O, B * O, B * Hd)]
+        hip.call("nrs_mlp2_forward_seed", *outs, nan, w, None, D(np.zeros(Hd * O, np.float32)),
+                 None, D(np.zeros(B * O, np.float32)), B, in_nan, Hd, O)
+    batch, in_f, hidden, classes = 256, 784, 128, 10
+    q = np.float32(0.25)
+    x = int_matrix(rng, (batch, in_f), -2, 2) * q
+    w1 = int_matrix(rng, (in_f, hidden), -2, 2) * q
+    b1 = int_matrix(rng, (hidden,), -2, 2)
+    w2 = int_matrix(rng, (hidden, classes), -2, 2) * q
+    t = np.zeros((batch, classes), np.float32)
+    t[np.arange(batch), 0] = 1.0
+    h = hip.DeviceBuffer(batch * hidden)
+    z, gz, dh = (hip.DeviceBuffer(n) for n in (batch * classes, batch * classes, batch * hidden))
+    print("mlp2 forward after NaN-filled LDS", flush=True)
+    hip.call("nrs_mlp2_forward_seed", h, z, gz, dh, D(x), D(w1), D(b1), D(w2), None, D(t), batch,
+             in_f, hidden, classes)
+    h_ref = np.maximum((x.astype(np.float64) @ w1 + b1), 0).astype(np.float32)
+    assert np.array_equal(h.to_host((batch, hidden)), h_ref)
+    assert np.isfinite(dh.to_host()).all() and np.isfinite(gz.to_host()).all()
+
+
 def test_mlp2_step_vs_f64(hip, orc):
     """The two-launch cfg2 step at full size on normal data against a float64
     restatement of the step (Linear, ReLU, Linear, ce_backward's seed, both
@@ -855,7 +892,7 @@ def test_mlp2_step_vs_f64(hip, orc):
 
 def test_mlp2_errors(hip):
     buf = hip.DeviceBuffer(4096)
-    bad = [(8, 4, 257, 3), (8, 4, 16, 17), (8, 0, 16, 3), (-1, 4, 16, 3)]
+    bad = [(8, 0, 16, 3), (-1, 4, 16, 3), (8, 4, 0, 3), (8, 4, 16, 0)]
     for b, i, hd, o in bad:
         with pytest.raises(hip.NrsError):
             hip.call("nrs_mlp2_forward_seed", buf, buf, buf, buf, buf, buf, None, buf, None, buf,
