@@ -3,7 +3,8 @@
 //   block: the cfg4 TransformerBlock (B32 S128 d256 h8 dff1024) forward and
 //          backward through the C++ operator surface (libnrs_host.so), the
 //          path a drop-in caller takes: nn::TransformerBlock::forward,
-//          set_grad, backward_graph, zero_grad of the parameters;
+//          the upstream gradient swapped in (runtime::swap_grad),
+//          backward_graph, zero_grad of the parameters;
 //   mlp:   the cfg2 MLP training step (784 -> 128 -> ReLU -> 10, batch 256,
 //          fused cross-entropy gradient) issued through the C ABI in two
 //          calls, timed eagerly and as a replayed HIP graph of the same
@@ -108,14 +109,15 @@ int bench_block(int steps, int warmup) {
                                  hip::nn::Linear(f1w, f1b), hip::nn::Linear(f2w, f2b), D, F};
     NodeRef x = resident(normal(B * S * D, 1.0f), {B, S, D});
     const std::vector<NodeRef> params{wq, wk, wv, wo, g1, b1, g2, b2, f1w, f1b, f2w, f2b};
-    // upstream gradient: a resident buffer copied into the output's gradient
-    // on the device (set_grad's host copy would synchronise every step)
+    // upstream gradient: a resident buffer swapped in as the output's
+    // gradient and back (set_grad's host copy would synchronise every step;
+    // in a network the layer above writes it there)
     DeviceBuffer seed = DeviceBuffer::from_host(normal(B * S * D, 1.0f));
     auto step = [&] {
         NodeRef out = tb.forward(x);
-        nrs_check(nrs_memcpy_dtod(out->gpu->grad->write_target(), seed.ptr(), seed.len() * sizeof(float)),
-                  "seed");
+        gpu::swap_grad(out, seed);
         backward_graph(out);
+        gpu::swap_grad(out, seed);
         gpu::zero_grad(params);
         x->gpu->grad->zero();
     };
@@ -147,9 +149,11 @@ int bench_cnn(int steps, int warmup) {
                            : hip::nn::maxpool2d(hip::graph::relu(hip::nn::conv2d(x, w1, b1, 1, 1)),
                                                 2, 2);
         NodeRef out = hip::nn::conv2d(p1, w2, b2, 1, 1);
-        nrs_check(nrs_memcpy_dtod(out->gpu->grad->write_target(), seed.ptr(), seed.len() * sizeof(float)),
-                  "seed");
+        // the upstream gradient swapped in as the output's gradient (no
+        // copy: in a network the layer above writes it there), then back
+        gpu::swap_grad(out, seed);
         backward_graph(out);
+        gpu::swap_grad(out, seed);
         gpu::zero_grad(params);
     };
     double f_gpu = 0, f_wall = 0, u_gpu = 0, u_wall = 0;

@@ -3,6 +3,7 @@
 // checks and panic messages, same output shape, same gradient flow.
 #include <algorithm>
 #include <memory>
+#include <utility>
 
 #include "neuralrs.hpp"
 
@@ -268,6 +269,12 @@ void set_grad(const NodeRef& node, const std::vector<float>& grad) {
     GpuBuffers& g = gpu_of(node, "set_grad: node not on GPU");
     if (grad.size() != g.data.len()) throw Panic("set_grad: gradient length mismatch");
     *g.grad = DeviceBuffer::from_host(grad);
+}
+
+void swap_grad(const NodeRef& node, DeviceBuffer& buf) {
+    GpuBuffers& g = gpu_of(node, "swap_grad: node not on GPU");
+    if (buf.len() != g.data.len()) throw Panic("swap_grad: gradient length mismatch");
+    std::swap(*g.grad, buf);
 }
 
 std::vector<float> read_grad(const NodeRef& node) {

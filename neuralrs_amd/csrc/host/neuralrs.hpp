@@ -149,6 +149,11 @@ void to_cuda(const NodeRef& node);
 std::vector<float> to_host(const NodeRef& node);
 // src/cuda/runtime.rs:87-93: replaces the gradient buffer with a copy of grad.
 void set_grad(const NodeRef& node, const std::vector<float>& grad);
+// set_grad's replacement of the gradient buffer for a gradient that is
+// already on the device: exchanges the node's gradient with `buf` (same
+// length), no copy. Backward closures hold the node's gradient object, so
+// they read what was swapped in; swapping back returns the buffer.
+void swap_grad(const NodeRef& node, DeviceBuffer& buf);
 // src/cuda/runtime.rs:96-103.
 std::vector<float> read_grad(const NodeRef& node);
 // src/cuda/runtime.rs:108-117.

@@ -1079,6 +1079,55 @@ void cfg3_cnn_step() {
     }
 }
 
+// runtime::swap_grad seeds a backward from a gradient already on the device:
+// the same bits as set_grad's host copy; swapping back returns the seed and
+// the node's own (zero) gradient; a buffer of another length panics.
+void swap_grad_seed() {
+    reseed(43);
+    const size_t N = 4, C = 3, H = 6, W = 6, M = 5;
+    const Vec x = normal(N * C * H * W, 1.0f), w = normal(M * C * 9, 0.3f), b = normal(M, 0.1f);
+    const Vec seed = normal(N * M * H * W, 1.0f);
+    auto same = [](const Vec& g, const Vec& c, const std::string& what) {
+        if (g.size() != c.size() || std::memcmp(g.data(), c.data(), g.size() * sizeof(float)))
+            throw Failure(what + ": bits differ");
+    };
+    Vec ref_dx, ref_dw, ref_db;
+    for (int swap = 0; swap < 2; ++swap) {
+        NodeRef gx = resident(x, {N, C, H, W}), gw = resident(w, {M, C, 3, 3});
+        NodeRef gb = resident(b, {M});
+        NodeRef out = hip::nn::conv2d(gx, gw, gb, 1, 1);
+        DeviceBuffer dseed = DeviceBuffer::from_host(seed);
+        if (swap)
+            gpu::swap_grad(out, dseed);
+        else
+            gpu::set_grad(out, seed);
+        backward_graph(out);
+        const Vec dx = gpu::read_grad(gx), dw = gpu::read_grad(gw), db = gpu::read_grad(gb);
+        if (!swap) {
+            ref_dx = dx;
+            ref_dw = dw;
+            ref_db = db;
+            continue;
+        }
+        same(dx, ref_dx, "swap_grad vs set_grad: input.grad");
+        same(dw, ref_dw, "swap_grad vs set_grad: weight.grad");
+        same(db, ref_db, "swap_grad vs set_grad: bias.grad");
+        gpu::swap_grad(out, dseed);
+        same(dseed.to_host(), seed, "swap_grad: the seed comes back");
+        same(gpu::read_grad(out), Vec(seed.size(), 0.0f),
+             "swap_grad: the node's own gradient comes back");
+        DeviceBuffer wrong(seed.size() - 1);
+        bool panicked = false;
+        try {
+            gpu::swap_grad(out, wrong);
+        } catch (const Panic& p) {
+            panicked = std::string(p.what()).find("swap_grad: gradient length mismatch") !=
+                       std::string::npos;
+        }
+        if (!panicked) throw Failure("swap_grad: no panic for a buffer of another length");
+    }
+}
+
 // The conv2d_maxpool node without the ReLU (a pool over the raw conv
 // output), with the image's gradient asked for: against the oracle's Conv2d
 // and max pooling composed, and against the conv2d -> maxpool2d graph.
@@ -1157,6 +1206,7 @@ const Case kCases[] = {
     {"cuda_maxpool_overlapping", cuda_maxpool_overlapping},
     {"cfg3_cnn_step", cfg3_cnn_step},
     {"cuda_conv2d_maxpool_node", cuda_conv2d_maxpool_node},
+    {"swap_grad_seed", swap_grad_seed},
 };
 
 int main(int argc, char** argv) {
