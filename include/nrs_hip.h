@@ -390,6 +390,34 @@ int nrs_maxpool_relu_conv2d_backward(float *dinput, float *dweight, float *dbias
                                      int64_t pad, int64_t pool_k, int64_t pool_stride,
                                      float beta_params);
 
+/* The backward of a conv layer over that pooled output, with the lower
+ * pair's parameter gradients: the reference CNN's
+ * conv2d(maxpool2d(relu(conv2d(x)))) (examples/mnist_cuda_cnn.rs:123-138)
+ * from the upper layer's output gradient down, when the lower layer's input
+ * needs no gradient (mnist_cuda_cnn.rs:261). Equals
+ *   nrs_conv2d_backward_ex(dpooled, dweight, dbias, grad, pooled, weight,
+ *       N, c_mid, ph, pw, c_out, kh, kw, stride, pad, 0, beta_params);
+ *   nrs_maxpool_relu_conv2d_backward(NULL, dweight_lo, dbias_lo, dpooled,
+ *       argmax, pooled, input_lo, weight_lo, N, c_in_lo, in_h, in_w, c_mid,
+ *       kh_lo, kw_lo, stride_lo, pad_lo, pool_k, pool_stride, beta_params);
+ * (ph x pw the pooled size): dpooled is written (not added); the four
+ * parameter gradients take beta_params. One launch plus one for both
+ * weight-gradient sums when the upper layer is "same" 3x3 stride 1 over
+ * pooled images of at most 14x14 (even width >= 4, whole pixel quads),
+ * c_mid % 32 == 0 and c_out % 64 == 0, and the lower layer is "same" 3x3
+ * stride 1 with 1 or 2 input channels under 2x2 stride-2 pooling of an even
+ * image; the lower weight gradient then sums over each window's argmax
+ * pixel in another order (the same values up to rounding; exact on
+ * small-integer data). Any other shape runs the two calls. weight_lo is
+ * read only by that path.                                                    */
+int nrs_conv2d_maxpool_relu_conv2d_backward(
+    float *dpooled, float *dweight, float *dbias, float *dweight_lo, float *dbias_lo,
+    const float *grad, const float *pooled, const float *weight, const int32_t *argmax,
+    const float *input_lo, const float *weight_lo, int64_t N, int64_t c_in_lo, int64_t in_h,
+    int64_t in_w, int64_t c_mid, int64_t kh_lo, int64_t kw_lo, int64_t stride_lo,
+    int64_t pad_lo, int64_t pool_k, int64_t pool_stride, int64_t c_out, int64_t kh, int64_t kw,
+    int64_t stride, int64_t pad, float beta_params);
+
 /* ------------------------------------------------------ gradient plumbing */
 /* accumulate (src/cuda/runtime.rs:13-19): acc[i] += src[i].                  */
 int nrs_accumulate(float *acc, const float *src, int64_t n);

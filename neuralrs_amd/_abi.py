@@ -74,6 +74,7 @@ SIGNATURES = {
     "nrs_maxpool_conv2d_backward": [_P, _P, _P, _P, _P, _P, _P] + [_I] * 11,
     "nrs_conv2d_relu_maxpool_forward": [_P, _P, _P, _P, _P, _P] + [_I] * 11,
     "nrs_maxpool_relu_conv2d_backward": [_P, _P, _P, _P, _P, _P, _P, _P] + [_I] * 11 + [_F],
+    "nrs_conv2d_maxpool_relu_conv2d_backward": [_P] * 11 + [_I] * 16 + [_F],
     "nrs_accumulate": [_P, _P, _I],
     "nrs_vadd": [_P, _P, _P, _I],
     "nrs_bias_add": [_P, _P, _P, _I, _I],

@@ -1551,6 +1551,92 @@ int nrs_maxpool_relu_conv2d_backward(float* dinput, float* dweight, float* dbias
                                    pool_stride, beta_params);
 }
 
+int nrs_conv2d_maxpool_relu_conv2d_backward(
+    float* dpooled, float* dweight, float* dbias, float* dweight_lo, float* dbias_lo,
+    const float* grad, const float* pooled, const float* weight, const int32_t* argmax,
+    const float* input_lo, const float* weight_lo, int64_t N, int64_t c_in_lo, int64_t in_h,
+    int64_t in_w, int64_t c_mid, int64_t kh_lo, int64_t kw_lo, int64_t stride_lo,
+    int64_t pad_lo, int64_t pool_k, int64_t pool_stride, int64_t c_out, int64_t kh, int64_t kw,
+    int64_t stride, int64_t pad, float beta_params) {
+    NRS_REQUIRE_INIT();
+    // the lower pair's geometry: conv output, then the pooled image (the
+    // upper layer's input)
+    nrs::ConvDims lo;
+    int rc = nrs::conv_dims(lo, N, c_in_lo, in_h, in_w, c_mid, kh_lo, kw_lo, stride_lo, pad_lo);
+    if (rc) return rc;
+    NRS_ARG_CHECK(pool_k >= 1 && pool_stride >= 1 && lo.out_h >= pool_k && lo.out_w >= pool_k,
+                  "conv2d maxpool relu conv2d backward: bad pooling window");
+    const int64_t ph = (lo.out_h - pool_k) / pool_stride + 1;
+    const int64_t pw = (lo.out_w - pool_k) / pool_stride + 1;
+    nrs::ConvDims up;
+    if ((rc = nrs::conv_dims(up, N, c_mid, ph, pw, c_out, kh, kw, stride, pad))) return rc;
+    NRS_ARG_CHECK(dpooled || N * c_mid * ph * pw == 0,
+                  "conv2d maxpool relu conv2d backward: null pooled gradient");
+    // one launch (and the two partial sums in one more): the upper layer on
+    // the chunk-pipelined kernel, the lower a "same" 3x3 stride-1 layer of 1
+    // or 2 input channels under 2x2 stride-2 pooling of an even image
+    const bool fused =
+        N >= 1 && dweight && dweight_lo && c_out >= 1 && c_mid >= 1 && kh_lo == 3 && kw_lo == 3 &&
+        stride_lo == 1 && pad_lo == 1 && c_in_lo >= 1 && c_in_lo <= 2 && pool_k == 2 &&
+        pool_stride == 2 && in_h % 2 == 0 && in_w % 2 == 0 && grad && pooled && weight && argmax &&
+        input_lo && c_mid <= INT32_MAX && c_out <= INT32_MAX && ph <= 16 && pw <= 16;
+    if (fused) {
+        nrs::SlabConv s;
+        s.x = grad;
+        s.w = weight;
+        s.out = dpooled;
+        s.N = N;
+        s.C = (int)c_out;
+        s.H = (int)up.out_h;
+        s.W = (int)up.out_w;
+        s.M = (int)c_mid;
+        s.kh = (int)kh;
+        s.kw = (int)kw;
+        s.stride = 1;
+        s.pad_h = (int)(kh - 1 - pad);
+        s.pad_w = (int)(kw - 1 - pad);
+        s.OH = (int)ph;
+        s.OW = (int)pw;
+        s.flip = true;
+        s.beta = 0.0f;
+        nrs::SlabWgrad w;
+        w.x = pooled;
+        w.g = grad;
+        w.dw = dweight;
+        w.db = dbias;
+        w.N = N;
+        w.C = (int)c_mid;
+        w.H = (int)ph;
+        w.W = (int)pw;
+        w.M = (int)c_out;
+        w.kh = (int)kh;
+        w.kw = (int)kw;
+        w.stride = (int)stride;
+        w.pad = (int)pad;
+        w.OH = (int)up.out_h;
+        w.OW = (int)up.out_w;
+        w.beta = beta_params;
+        nrs::PipeLower l;
+        l.am = argmax;
+        l.pooled = pooled;
+        l.x = input_lo;
+        l.dw = dweight_lo;
+        l.db = dbias_lo;
+        l.c_lo = (int)c_in_lo;
+        l.beta = beta_params;
+        if (stride == 1 && (rc = nrs::pipe_backward(&s, w, &l)) != nrs::kSlabUnsupported) return rc;
+    }
+    // any other shape: the two backward calls, the pooled gradient written
+    // by the first and read by the second
+    if ((rc = nrs_conv2d_backward_ex(dpooled, dweight, dbias, grad, pooled, weight, N, c_mid, ph,
+                                     pw, c_out, kh, kw, stride, pad, 0.0f, beta_params)))
+        return rc;
+    return nrs_maxpool_relu_conv2d_backward(nullptr, dweight_lo, dbias_lo, dpooled, argmax, pooled,
+                                            input_lo, weight_lo, N, c_in_lo, in_h, in_w, c_mid,
+                                            kh_lo, kw_lo, stride_lo, pad_lo, pool_k, pool_stride,
+                                            beta_params);
+}
+
 int nrs_conv2d_forward(float* out, const float* input, const float* weight, const float* bias,
                        int64_t N, int64_t c_in, int64_t in_h, int64_t in_w, int64_t c_out,
                        int64_t kh, int64_t kw, int64_t stride, int64_t pad) {

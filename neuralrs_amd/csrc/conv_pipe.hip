@@ -73,6 +73,20 @@ struct PipeArgs {
     float* part_b;       // or null
     int wC, wM, nw;      // input channels, output channels, W blocks
     int N, H, W, P;
+    // D blocks of an input gradient whose input is the 2x2 stride-2 max pool
+    // of relu(y), y a "same" 3x3 stride-1 convolution of lo_x (c_lo
+    // channels, 2H x 2W): each D block also writes that layer's weight and
+    // bias gradient over its image and channels, with the gradient it just
+    // computed as the pooled gradient (a pooled value's gradient reaches
+    // its window's argmax when the pooled value is > 0: relu_grad).
+    const int32_t* lo_am;     // [N][dM][H][W]: flat indices into [N][dM][2H][2W]
+    const float* lo_pooled;   // [N][dM][H][W]: the pooled values (this layer's input)
+    const float* lo_x;        // [N][c_lo][2H][2W]
+    float* lo_part_w;         // [N][dM][9][c_lo]: per-image partials
+    float* lo_part_b;         // [N][dM], or null
+    FastDiv lo_div_w2;        // 2W
+    FastDiv lo_div_plane;     // (2H + 2) * (2W + 2): a zero-padded plane
+    FastDiv lo_div_wp;        // 2W + 2
 };
 
 // Tap t of a 3x3 window as an offset in a staged plane.
@@ -149,7 +163,113 @@ struct WeightStage {
     }
 };
 
-template <bool FLIP>
+// The lower layer's weight and bias gradient over one image and the D
+// block's 32 channels (see PipeArgs), in two parts: issue() loads, per
+// thread, the argmax and pooled value of its pooled positions and its share
+// of the lower input image; finish() stages the image with a zero halo in
+// free LDS (xs) and reduces, given ot, the block's [32][P] gradient of the
+// pooled values. Thread t takes channel t / 8 and the positions
+// p = t % 8 + 8i in ascending order; a position's gradient goes to its
+// window's argmax pixel (y, x) and multiplies the nine input values around
+// it; the eight threads of a channel then add their sums in a fixed
+// butterfly order.
+template <int CLO>
+struct LowerWgrad {
+    static constexpr int kPos = (kPMaxSide * kPMaxSide + 7) / 8;  // positions per thread
+    static constexpr int kImgItems = (CLO * (2 * kPMaxSide + 2) * (2 * kPMaxSide + 2) + 255) / 256;
+    static_assert(CLO * (2 * kPMaxSide + 2) * (2 * kPMaxSide + 2) <= kPDBuf,
+                  "the padded lower input fits a chunk buffer");
+    float amv[kPos], pvv[kPos], xv[kImgItems];
+
+    __device__ __forceinline__ void issue(const PipeArgs& a, int img, int m0) {
+        const int tid = threadIdx.x, m = tid >> 3, part = tid & 7;
+        const int P = a.P, H2 = 2 * a.H, W2 = 2 * a.W, plane = (H2 + 2) * (W2 + 2);
+        // buffer bases uniform over the workgroup (a per-lane base would
+        // make the compiler loop over the distinct bases of each load); the
+        // lane's channel goes into the offset
+        const int64_t blk = ((int64_t)img * a.dM + m0) * P;
+        const auto ram =
+            buffer_rsrc(reinterpret_cast<const float*>(a.lo_am) + blk, (int64_t)kPMB * P * 4);
+        const auto rpv = buffer_rsrc(a.lo_pooled + blk, (int64_t)kPMB * P * 4);
+        const auto rx =
+            buffer_rsrc(a.lo_x + (int64_t)img * CLO * H2 * W2, (int64_t)CLO * H2 * W2 * 4);
+#pragma unroll
+        for (int i = 0; i < kPos; ++i) {
+            const int p = part + 8 * i;
+            amv[i] = buffer_load1(ram, p < P ? (m * P + p) * 4 : kOutOfRange);
+            pvv[i] = buffer_load1(rpv, p < P ? (m * P + p) * 4 : kOutOfRange);
+        }
+        // the image with its zero halo (a load at kOutOfRange returns zero)
+#pragma unroll
+        for (int k = 0; k < kImgItems; ++k) {
+            const int e = tid + 256 * k;
+            uint32_t c, r, yy, xx;
+            fast_divmod((uint32_t)e, a.lo_div_plane, c, r);
+            fast_divmod(r, a.lo_div_wp, yy, xx);
+            const int iy = (int)yy - 1, ix = (int)xx - 1;
+            const bool ok = (e < CLO * plane) & ((unsigned)iy < (unsigned)H2) &
+                            ((unsigned)ix < (unsigned)W2);
+            xv[k] = buffer_load1(rx, ok ? (((int)c * H2 + iy) * W2 + ix) * 4 : kOutOfRange);
+        }
+    }
+
+    __device__ __forceinline__ void finish(const PipeArgs& a, int img, int m0, const float* ot,
+                                           float* xs) const {
+        const int tid = threadIdx.x, m = tid >> 3, part = tid & 7;
+        const int P = a.P, H2 = 2 * a.H, W2 = 2 * a.W, Wp = W2 + 2, plane = (H2 + 2) * Wp;
+#pragma unroll
+        for (int k = 0; k < kImgItems; ++k) {
+            const int e = tid + 256 * k;
+            if (e < CLO * plane) xs[e] = xv[k];
+        }
+        __syncthreads();
+
+        const int64_t row = (int64_t)img * a.dM + m0 + m;
+        const int pix0 = (int)(row * H2 * W2);  // flat index of this channel's first pixel
+        float acc[CLO * 9];
+#pragma unroll
+        for (int k = 0; k < CLO * 9; ++k) acc[k] = 0.0f;
+        float bsum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kPos; ++i) {
+            const int p = part + 8 * i;
+            const bool live = p < P;
+            // the argmax as this channel's pixel, clamped into the image (the
+            // forward wrote it there; the clamp keeps the LDS reads in bounds)
+            const int loc = min(max(__builtin_bit_cast(int, amv[i]) - pix0, 0), H2 * W2 - 1);
+            uint32_t y, x;
+            fast_divmod((uint32_t)loc, a.lo_div_w2, y, x);
+            const float g = (live & (pvv[i] > 0.0f)) ? ot[m * P + (live ? p : 0)] : 0.0f;
+            bsum += g;
+            const float* xp = xs + (int)y * Wp + (int)x;
+#pragma unroll
+            for (int c = 0; c < CLO; ++c)
+#pragma unroll
+                for (int t = 0; t < 9; ++t)
+                    acc[c * 9 + t] += g * xp[c * plane + (t / 3) * Wp + t % 3];
+        }
+#pragma unroll
+        for (int sh = 1; sh < 8; sh <<= 1) {
+#pragma unroll
+            for (int k = 0; k < CLO * 9; ++k) acc[k] += __shfl_xor(acc[k], sh);
+            bsum += __shfl_xor(bsum, sh);
+        }
+        if (part == 0) {
+            // [img][m][tap][c], the layout of the slice-order partial sum
+#pragma unroll
+            for (int c = 0; c < CLO; ++c)
+#pragma unroll
+                for (int t = 0; t < 9; ++t) a.lo_part_w[(row * 9 + t) * CLO + c] = acc[c * 9 + t];
+            if (a.lo_part_b) a.lo_part_b[row] = bsum;
+        }
+    }
+};
+
+// (no lower layer)
+template <>
+struct LowerWgrad<0> {};
+
+template <bool FLIP, int CLO = 0>
 __device__ __forceinline__ void pipe_d_block(const PipeArgs& a, int bid, float* lds) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -241,6 +361,10 @@ __device__ __forceinline__ void pipe_d_block(const PipeArgs& a, int bid, float* 
         }
     }
 
+    // the lower layer's loads fly while the tile is stored
+    LowerWgrad<CLO> lower;
+    if constexpr (CLO > 0) lower.issue(a, img, m0);
+
     // epilogue: lane holds D[m = 4q + r][column l16] of each row tile. The
     // block's [32][P] output goes through the chunk buffer the last chunk did
     // not use (every wave finished reading it before the last barrier), so it
@@ -282,6 +406,10 @@ __device__ __forceinline__ void pipe_d_block(const PipeArgs& a, int bid, float* 
         if (a.beta != 0.0f) v = v + a.beta * old[u];
         *reinterpret_cast<f32x4*>(oimg + (int64_t)m * P + 4 * p4) = v;
     }
+    // the lower layer's gradients from the tile just stored (beta is 0 on
+    // this path, so the tile is the gradient as written); the other chunk
+    // buffer was last read by the last chunk, before the barrier above
+    if constexpr (CLO > 0) lower.finish(a, img, m0, ot, lds + ((nch + 1) & 1) * kPDBuf);
 }
 
 // ---- W blocks -------------------------------------------------------------
@@ -440,7 +568,7 @@ __device__ __forceinline__ void pipe_w_block(const PipeArgs& a, int bid, float* 
 // blocks' image), so when the grid is a multiple of 8 logical index L runs
 // on XCD L / (grid / 8): workgroup ids are dealt to the 8 XCDs round-robin
 // (id % 8), and consecutive logical blocks then share one XCD's L2.
-template <bool FLIP, bool HAS_W>
+template <bool FLIP, bool HAS_W, int CLO = 0>
 __global__ __launch_bounds__(256) void conv_pipe_kernel(PipeArgs a) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int bid = blockIdx.x;
@@ -460,7 +588,7 @@ __global__ __launch_bounds__(256) void conv_pipe_kernel(PipeArgs a) {
         // decode); the last slice of an odd batch has one image, and L stays
         // below the grid, so r never reaches its missing image's blocks
         const int rd = r - wper, img = slice * kPImgs + rd / dmblocks, mblk = rd % dmblocks;
-        pipe_d_block<FLIP>(a, img * dmblocks + mblk, lds);
+        pipe_d_block<FLIP, CLO>(a, img * dmblocks + mblk, lds);
     } else {
         // an image's m-blocks (consecutive ids) folded onto one XCD, as above
         const int total = a.nd;
@@ -478,9 +606,9 @@ size_t pipe_lds(bool has_w) {
 // Whether the device gives one workgroup that much LDS.
 bool pipe_lds_fits(bool has_w) { return pipe_lds(has_w) <= lds_limit(); }
 
-template <bool FLIP, bool HAS_W>
+template <bool FLIP, bool HAS_W, int CLO = 0>
 int launch_pipe(const PipeArgs& a) {
-    auto fn = conv_pipe_kernel<FLIP, HAS_W>;
+    auto fn = conv_pipe_kernel<FLIP, HAS_W, CLO>;
     const size_t lds = pipe_lds(a.nw > 0);
     static bool attr_set = false;
     if (!attr_set) {
@@ -525,7 +653,7 @@ int pipe_conv(const SlabConv& s) {
     return s.flip ? launch_pipe<true, false>(a) : launch_pipe<false, false>(a);
 }
 
-int pipe_backward(const SlabConv* d, const SlabWgrad& w) {
+int pipe_backward(const SlabConv* d, const SlabWgrad& w, const PipeLower* lo) {
     if (!pipe_geometry(w.kh, w.kw, w.stride, w.pad, w.pad, w.H, w.W, w.OH, w.OW) || !w.dw ||
         w.C % kPMB != 0 || w.C <= 0 || w.M % kPWM != 0 || w.M <= 0 || w.N <= 0 ||
         w.N * (int64_t)std::max(w.C, w.M) * w.H * w.W > 0x1fffffff || ((uintptr_t)w.x & 7) != 0 ||
@@ -533,13 +661,19 @@ int pipe_backward(const SlabConv* d, const SlabWgrad& w) {
         return kSlabUnsupported;
     if (d && (d->x != w.g || d->C != w.M || d->M != w.C || !d->flip || ((uintptr_t)d->out & 15) != 0))
         return kSlabUnsupported;
+    // the lower layer: its gradients come from d's result as written
+    // (beta 0), its argmax indices [N][C][2H][2W] within int32
+    if (lo && (!d || d->beta != 0.0f || lo->c_lo < 1 || lo->c_lo > 2 || !lo->dw || !lo->am ||
+               !lo->pooled || !lo->x || w.N * (int64_t)w.C * 4 * w.H * w.W > 0x7fffffff))
+        return kSlabUnsupported;
     const int P = w.H * w.W;
     const int64_t slices = (w.N + kPImgs - 1) / kPImgs;
     const int64_t nw = slices * (w.C / kPCC) * (w.M / kPWM);
     const int64_t nd = d ? w.N * (w.C / kPMB) : 0;
     if (nw + nd > 0x7fffffff) return kSlabUnsupported;
     const int64_t npw = (int64_t)w.M * 9 * w.C;
-    float* part = workspace(sizeof(float) * (size_t)(slices * (npw + w.M)), 3);
+    const int64_t nlo = lo ? w.N * (int64_t)w.C * (9 * lo->c_lo + 1) : 0;
+    float* part = workspace(sizeof(float) * (size_t)(slices * (npw + w.M) + nlo), 3);
     if (!part) return NRS_ERR_ALLOC;
     PipeArgs a{};
     if (d) {
@@ -562,9 +696,25 @@ int pipe_backward(const SlabConv* d, const SlabWgrad& w) {
     a.H = w.H;
     a.W = w.W;
     a.P = P;
-    int rc = launch_pipe<true, true>(a);
+    if (!lo) {
+        int rc = launch_pipe<true, true>(a);
+        if (rc) return rc;
+        return wgrad_partial_sum(w.dw, w.db, part, a.part_b, (int)slices, w.M, w.C, 9, w.beta);
+    }
+    a.lo_am = lo->am;
+    a.lo_pooled = lo->pooled;
+    a.lo_x = lo->x;
+    a.lo_part_w = part + slices * (npw + w.M);
+    a.lo_part_b = lo->db ? a.lo_part_w + w.N * (int64_t)w.C * 9 * lo->c_lo : nullptr;
+    a.lo_div_w2 = make_fastdiv((uint32_t)(2 * w.W));
+    a.lo_div_plane = make_fastdiv((uint32_t)((2 * w.H + 2) * (2 * w.W + 2)));
+    a.lo_div_wp = make_fastdiv((uint32_t)(2 * w.W + 2));
+    int rc = lo->c_lo == 1 ? launch_pipe<true, true, 1>(a) : launch_pipe<true, true, 2>(a);
     if (rc) return rc;
-    return wgrad_partial_sum(w.dw, w.db, part, a.part_b, (int)slices, w.M, w.C, 9, w.beta);
+    const WgradSumArgs up{w.dw, w.db, part, a.part_b, (int)slices, w.M, w.C, 9, w.beta};
+    const WgradSumArgs low{lo->dw, lo->db, a.lo_part_w, a.lo_part_b, (int)w.N, w.C, lo->c_lo, 9,
+                           lo->beta};
+    return wgrad_partial_sum_pair(up, low);
 }
 
 }  // namespace nrs

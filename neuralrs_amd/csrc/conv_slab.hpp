@@ -76,7 +76,21 @@ int slab_backward_pair(const SlabConv& d, const SlabWgrad& w);
 // is given, the input gradient d (a flipped convolution of w.g), then the
 // weight gradient's partial sum. Needs pipe_conv's geometry, C % 32 == 0 and
 // M % 64 == 0; returns kSlabUnsupported (launching nothing) otherwise.
-int pipe_backward(const SlabConv* d, const SlabWgrad& w);
+// With `lo`, d's input is the 2x2 stride-2 max pool of relu(y), y a "same"
+// 3x3 stride-1 layer with lo->c_lo (1 or 2) input channels, and the launch
+// also gives that layer's weight and bias gradient (lo->dw required), from
+// d's result as the pooled gradient; d->beta must be 0. Both partial sums
+// then run in one launch.
+struct PipeLower {
+    const int32_t* am = nullptr;      // the pool's argmax [N][d->M][H][W]
+    const float* pooled = nullptr;    // the pooled values (d's forward input)
+    const float* x = nullptr;         // the lower layer's input [N][c_lo][2H][2W]
+    float* dw = nullptr;              // [d->M][c_lo][3][3]
+    float* db = nullptr;              // [d->M] or null
+    int c_lo = 0;
+    float beta = 1.0f;                // as SlabWgrad::beta
+};
+int pipe_backward(const SlabConv* d, const SlabWgrad& w, const PipeLower* lo = nullptr);
 
 // Weight and bias gradient of a convolution with c_in*kh*kw <= 15 taps and at
 // most 64 output channels, on the matrix cores (conv_few_taps.hip): dw += and
@@ -107,5 +121,15 @@ int few_taps_wgrad(const FewTapsWgrad& s);
 // launch. beta 0 reads neither.
 int wgrad_partial_sum(float* dw, float* db, const float* part_w, const float* part_b, int slices,
                       int M, int C, int taps, float beta = 1.0f);
+// The arguments of one such sum, and two of them in one launch.
+struct WgradSumArgs {
+    float* dw;
+    float* db;
+    const float* part_w;
+    const float* part_b;
+    int slices, M, C, taps;
+    float beta;
+};
+int wgrad_partial_sum_pair(const WgradSumArgs& p0, const WgradSumArgs& p1);
 
 }  // namespace nrs

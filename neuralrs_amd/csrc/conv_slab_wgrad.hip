@@ -22,56 +22,70 @@ void conv_slab_wgrad_kernel(WgradArgs a) {
 // of that size costs one memory round trip.
 constexpr int kSumGroups = 16, kSumBatch = 32;
 
-__global__ __launch_bounds__(64 * kSumGroups) void wgrad_sum_kernel(
-    float* __restrict__ dw, float* __restrict__ db, const float* __restrict__ part_w,
-    const float* __restrict__ part_b, int slices, int M, int C, int taps, float beta) {
+// The 64 outputs from `base` on of one partial sum (every thread of the
+// workgroup takes part: the barriers are uniform).
+__device__ __forceinline__ void wgrad_sum_at(const WgradSumArgs& p, int base) {
     __shared__ float red[kSumGroups][64];
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    const int nw = dw ? M * taps * C : 0, total = nw + (db ? M : 0);
+    const int M = p.M, C = p.C, taps = p.taps, slices = p.slices;
+    const int nw = p.dw ? M * taps * C : 0, total = nw + (p.db ? M : 0);
     const int per = (slices + kSumGroups - 1) / kSumGroups;
     const int s0 = min(slices, ty * per), s1 = min(slices, s0 + per);
-    for (int base = blockIdx.x * 64; base < total; base += gridDim.x * 64) {
-        const int e = base + tx;
-        const bool is_w = e < nw;
-        const float* part = is_w ? part_w + e : part_b + (e - nw);
-        const int64_t stride = is_w ? nw : M;
-        float v = 0.0f;
-        if (e < total) {
-            for (int s = s0; s < s1; s += kSumBatch) {
-                float t[kSumBatch];
+    const int e = base + tx;
+    const bool is_w = e < nw;
+    const float* part = is_w ? p.part_w + e : p.part_b + (e - nw);
+    const int64_t stride = is_w ? nw : M;
+    float v = 0.0f;
+    if (e < total) {
+        for (int s = s0; s < s1; s += kSumBatch) {
+            float t[kSumBatch];
 #pragma unroll
-                for (int b = 0; b < kSumBatch; b += 8) {
-                    if (s + b < s1) {  // uniform over the wave (one slice group)
+            for (int b = 0; b < kSumBatch; b += 8) {
+                if (s + b < s1) {  // uniform over the wave (one slice group)
 #pragma unroll
-                        for (int u = b; u < b + 8; ++u)
-                            t[u] = part[(int64_t)min(s + u, s1 - 1) * stride];
-                    } else {
+                    for (int u = b; u < b + 8; ++u)
+                        t[u] = part[(int64_t)min(s + u, s1 - 1) * stride];
+                } else {
 #pragma unroll
-                        for (int u = b; u < b + 8; ++u) t[u] = 0.0f;
-                    }
+                    for (int u = b; u < b + 8; ++u) t[u] = 0.0f;
                 }
-#pragma unroll
-                for (int u = 0; u < kSumBatch; ++u) v += s + u < s1 ? t[u] : 0.0f;
             }
-        }
-        red[ty][tx] = v;
-        __syncthreads();
-        if (ty == 0 && e < total) {
-            float r = red[0][tx];
 #pragma unroll
-            for (int y = 1; y < kSumGroups; ++y) r += red[y][tx];
-            float* dst;
-            if (is_w) {
-                const int c = e % C, mt = e / C, tap = mt % taps, m = mt / taps;
-                dst = dw + ((int64_t)m * C + c) * taps + tap;
-            } else {
-                dst = db + (e - nw);
-            }
-            // beta 0 writes without reading the old gradient
-            *dst = beta != 0.0f ? r + beta * *dst : r;
+            for (int u = 0; u < kSumBatch; ++u) v += s + u < s1 ? t[u] : 0.0f;
         }
-        __syncthreads();
     }
+    red[ty][tx] = v;
+    __syncthreads();
+    if (ty == 0 && e < total) {
+        float r = red[0][tx];
+#pragma unroll
+        for (int y = 1; y < kSumGroups; ++y) r += red[y][tx];
+        float* dst;
+        if (is_w) {
+            const int c = e % C, mt = e / C, tap = mt % taps, m = mt / taps;
+            dst = p.dw + ((int64_t)m * C + c) * taps + tap;
+        } else {
+            dst = p.db + (e - nw);
+        }
+        // beta 0 writes without reading the old gradient
+        *dst = p.beta != 0.0f ? r + p.beta * *dst : r;
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(64 * kSumGroups) void wgrad_sum_kernel(WgradSumArgs p) {
+    wgrad_sum_at(p, blockIdx.x * 64);
+}
+
+// Two partial sums in one launch: blocks [0, blocks0) take p0, the rest p1.
+__global__ __launch_bounds__(64 * kSumGroups) void wgrad_sum_pair_kernel(WgradSumArgs p0,
+                                                                         WgradSumArgs p1,
+                                                                         int blocks0) {
+    const int b = blockIdx.x;
+    if (b < blocks0)
+        wgrad_sum_at(p0, b * 64);
+    else
+        wgrad_sum_at(p1, (b - blocks0) * 64);
 }
 
 // LDS of one workgroup: at most 160 KiB (gfx950's whole LDS), and no more
@@ -180,13 +194,29 @@ int slab_wgrad(const SlabWgrad& s) {
     return slab_wgrad_sum(s, p);
 }
 
+namespace {
+int64_t sum_blocks(const WgradSumArgs& p) {
+    const int64_t total = (p.dw ? (int64_t)p.M * p.taps * p.C : 0) + (p.db ? p.M : 0);
+    return (total + 63) / 64;
+}
+}  // namespace
+
 int wgrad_partial_sum(float* dw, float* db, const float* part_w, const float* part_b, int slices,
                       int M, int C, int taps, float beta) {
-    const int64_t total = (dw ? (int64_t)M * taps * C : 0) + (db ? M : 0);
-    if (total == 0) return NRS_OK;
-    hipLaunchKernelGGL(wgrad_sum_kernel, dim3((unsigned)((total + 63) / 64)),
-                       dim3(64 * kSumGroups), 0, stream(), dw, db, part_w, part_b, slices, M, C,
-                       taps, beta);
+    const WgradSumArgs p{dw, db, part_w, part_b, slices, M, C, taps, beta};
+    const int64_t blocks = sum_blocks(p);
+    if (blocks == 0) return NRS_OK;
+    hipLaunchKernelGGL(wgrad_sum_kernel, dim3((unsigned)blocks), dim3(64 * kSumGroups), 0,
+                       stream(), p);
+    NRS_LAUNCH_CHECK("conv2d weight gradient (sum)");
+    return NRS_OK;
+}
+
+int wgrad_partial_sum_pair(const WgradSumArgs& p0, const WgradSumArgs& p1) {
+    const int64_t b0 = sum_blocks(p0), b1 = sum_blocks(p1);
+    if (b0 + b1 == 0) return NRS_OK;
+    hipLaunchKernelGGL(wgrad_sum_pair_kernel, dim3((unsigned)(b0 + b1)), dim3(64 * kSumGroups), 0,
+                       stream(), p0, p1, (int)b0);
     NRS_LAUNCH_CHECK("conv2d weight gradient (sum)");
     return NRS_OK;
 }

@@ -9,6 +9,7 @@
 
 #include <cmath>
 #include <initializer_list>
+#include <unordered_map>
 #include <unordered_set>
 
 #include "nrs_hip.h"
@@ -158,7 +159,22 @@ void build_topo(const NodeRef& n, std::unordered_set<const Node*>& visited,
     topo.push_back(n);
 }
 
+// The backward pass being run on this thread: each node's consumers in its
+// graph, and the nodes whose closure a consumer's fused backward has run.
+struct BackwardPass {
+    std::unordered_map<const Node*, int> consumers;
+    std::unordered_set<const Node*> done;
+};
+thread_local BackwardPass* tl_pass = nullptr;
+
 }  // namespace
+
+// What the backward of a conv2d_maxpool node with a ReLU needs.
+struct ReluPoolConv {
+    NodeRef input, weight, bias;
+    std::shared_ptr<DeviceBuffer> argmax;
+    size_t n, c_in, in_h, in_w, c_out, kh, kw, stride, pad, pool_k, pool_stride;
+};
 
 // ------------------------------------------------------------ DeviceBuffer
 void note_pending_taken(DeviceBuffer* b) { taken_pending().push_back(b); }
@@ -244,7 +260,16 @@ void backward_graph(const NodeRef& root) {
     std::vector<NodeRef> topo;
     std::unordered_set<const Node*> visited;
     build_topo(root, visited, topo);
+    BackwardPass pass;
+    for (const NodeRef& n : topo)
+        for (const NodeRef& p : n->parents) ++pass.consumers[p.get()];
+    struct Restore {
+        BackwardPass* prev;
+        ~Restore() { tl_pass = prev; }
+    } restore{tl_pass};
+    tl_pass = &pass;
     for (auto it = topo.rbegin(); it != topo.rend(); ++it) {
+        if (pass.done.count(it->get())) continue;  // run by a consumer's fused backward
         const std::vector<float> grad = (*it)->grad;
         if ((*it)->backward_fn) (*it)->backward_fn(grad);
     }
@@ -563,6 +588,52 @@ void cross_entropy_backward(const NodeRef& pred, const NodeRef& target) {
 // ---------------------------------------------------------------------- nn
 namespace nn {
 
+namespace {
+
+// The backward of conv2d over a conv2d_maxpool node with a ReLU (the
+// reference CNN's conv2d(maxpool2d(relu(conv2d(x))))) together with that
+// node's, as one nrs_conv2d_maxpool_relu_conv2d_backward call: when this conv
+// is the pooled node's only consumer in the running pass, the pooled node's
+// gradient is still a pending zero (so this conv's input gradient is all of
+// it), the lower conv's input needs no gradient (conv.rs:304 skips it) and
+// the gradients written are distinct buffers. The pass then skips the pooled
+// node's closure. Returns false, having changed nothing, otherwise.
+bool fused_relu_pool_backward(const NodeRef& input, const NodeRef& weight, const NodeRef& bias,
+                              const DeviceBuffer& grad, size_t c_out, size_t kh, size_t kw,
+                              size_t stride, size_t pad) {
+    const ReluPoolConv* lo = input->relu_pool_conv.get();
+    if (!lo || !tl_pass || !input->requires_grad || lo->input->requires_grad) return false;
+    const auto it = tl_pass->consumers.find(input.get());
+    if (it == tl_pass->consumers.end() || it->second != 1) return false;
+    GpuBuffers& pg = gpu_of(input, "conv2d bwd: input not on GPU");
+    GpuBuffers& wg = gpu_of(weight, "conv2d bwd: weight not on GPU");
+    GpuBuffers& bg = gpu_of(bias, "conv2d bwd: bias not on GPU");
+    GpuBuffers& xg = gpu_of(lo->input, "conv2d bwd: input not on GPU");
+    GpuBuffers& lwg = gpu_of(lo->weight, "conv2d bwd: weight not on GPU");
+    GpuBuffers& lbg = gpu_of(lo->bias, "conv2d bwd: bias not on GPU");
+    if (!pg.grad->pending_zero()) return false;
+    DeviceBuffer* outs[5] = {pg.grad.get(), wg.grad.get(), bg.grad.get(), lwg.grad.get(),
+                             lbg.grad.get()};
+    for (int i = 0; i < 5; ++i)
+        for (int j = i + 1; j < 5; ++j)
+            if (outs[i] == outs[j]) return false;
+    // the four parameter gradients are written when all are pending zeros,
+    // else added (the pending ones cleared first), as each closure would
+    const float beta_p = joint_beta({outs[1], outs[2], outs[3], outs[4]});
+    check(nrs_conv2d_maxpool_relu_conv2d_backward(
+              pg.grad->write_target(), wg.grad->write_target(), bg.grad->write_target(),
+              lwg.grad->write_target(), lbg.grad->write_target(), grad.ptr(), pg.data.ptr(),
+              wg.data.ptr(), reinterpret_cast<const int32_t*>(lo->argmax->ptr()),
+              xg.data.ptr(), lwg.data.ptr(), lo->n, lo->c_in, lo->in_h, lo->in_w, lo->c_out,
+              lo->kh, lo->kw, lo->stride, lo->pad, lo->pool_k, lo->pool_stride, c_out, kh, kw,
+              stride, pad, beta_p),
+          "cuda conv2d bwd: launch failed");
+    tl_pass->done.insert(input.get());
+    return true;
+}
+
+}  // namespace
+
 NodeRef conv2d(const NodeRef& input, const NodeRef& weight, const NodeRef& bias, size_t stride,
                size_t pad) {
     GpuBuffers& ig = gpu_of(input, "cuda conv2d: input not on GPU");
@@ -586,6 +657,8 @@ NodeRef conv2d(const NodeRef& input, const NodeRef& weight, const NodeRef& bias,
     NodeRef node = make_output({n, c_out, out_h, out_w}, {input, weight, bias}, std::move(out));
     node->backward_fn = [grad = node->gpu->grad, input, weight, bias, n, c_in, in_h, in_w, c_out,
                          kh, kw, stride, pad](const std::vector<float>&) {
+        if (fused_relu_pool_backward(input, weight, bias, *grad, c_out, kh, kw, stride, pad))
+            return;
         GpuBuffers& ig = gpu_of(input, "conv2d bwd: input not on GPU");
         GpuBuffers& wg = gpu_of(weight, "conv2d bwd: weight not on GPU");
         GpuBuffers& bg = gpu_of(bias, "conv2d bwd: bias not on GPU");
@@ -663,6 +736,10 @@ NodeRef conv2d_maxpool(const NodeRef& input, const NodeRef& weight, const NodeRe
                                             c_out, kh, kw, stride, pad, pool_k, pool_stride),
           "cuda conv2d maxpool: launch failed");
     NodeRef node = make_output({n, c_out, ph, pw}, {input, weight, bias}, std::move(pooled));
+    if (relu)
+        node->relu_pool_conv = std::make_shared<const ReluPoolConv>(
+            ReluPoolConv{input, weight, bias, argmax, n, c_in, in_h, in_w, c_out, kh, kw, stride,
+                         pad, pool_k, pool_stride});
     Node* self = node.get();
     node->backward_fn = [grad = node->gpu->grad, self, input, weight, bias, argmax, relu, n, c_in,
                          in_h, in_w, c_out, kh, kw, stride, pad, pool_k,

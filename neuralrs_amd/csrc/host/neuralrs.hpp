@@ -119,6 +119,7 @@ struct GpuBuffers {
 
 struct Node;
 using NodeRef = std::shared_ptr<Node>;
+struct ReluPoolConv;
 
 // src/autograd/node.rs:38-47.
 struct Node {
@@ -129,6 +130,11 @@ struct Node {
     std::function<void(const std::vector<float>&)> backward_fn;
     bool requires_grad = true;
     std::unique_ptr<GpuBuffers> gpu;  // Option<GpuBuffers>
+    // Host-only, no counterpart in the reference: set by
+    // hip::nn::conv2d_maxpool with a ReLU. A conv2d over this node that is
+    // its only consumer in a backward pass runs both backwards in one call
+    // (same results) and the pass then skips this node's closure.
+    std::shared_ptr<const ReluPoolConv> relu_pool_conv;
 
     // Node::new (src/autograd/node.rs:61-74).
     static NodeRef create(std::vector<float> data, std::vector<size_t> shape);

@@ -1079,6 +1079,79 @@ void cfg3_cnn_step() {
     }
 }
 
+// The CNN's conv2d over a conv2d_maxpool node with a ReLU: when the conv is
+// the pooled node's only consumer and the image needs no gradient, the
+// backward pass runs both layers' backwards as one fused call. On small
+// integers every gradient equals, bit for bit, the pass that cannot fuse
+// (the image asking for its gradient) and the oracle's composition; with a
+// second consumer of the pooled node the pass does not fuse and still
+// matches the unfused pass.
+void cfg3_fused_backward_exact() {
+    reseed(47);
+    const size_t N = 3, H = 28, W = 28, C1 = 32, C2 = 64, PH = 14, PW = 14;
+    auto ints = [](size_t n, int lo, int hi) {
+        Vec v(n);
+        std::uniform_int_distribution<int> d(lo, hi);
+        for (float& e : v) e = (float)d(rng());
+        return v;
+    };
+    const Vec x = ints(N * H * W, -2, 2), w1 = ints(C1 * 9, -2, 2), b1 = ints(C1, -2, 2);
+    const Vec w2 = ints(C2 * C1 * 9, -2, 2), b2 = ints(C2, -2, 2), w3 = ints(C2 * C1 * 9, -2, 2);
+    const Vec seed = ints(N * C2 * PH * PW, -2, 2);
+    auto same = [](const Vec& g, const Vec& c, const std::string& what) {
+        if (g.size() != c.size() || std::memcmp(g.data(), c.data(), g.size() * sizeof(float)))
+            throw Failure(what + ": bits differ");
+    };
+    for (int two_consumers = 0; two_consumers < 2; ++two_consumers) {
+        Vec ref[5];
+        for (int x_grad = 0; x_grad < 2; ++x_grad) {  // x_grad: the pass cannot fuse
+            NodeRef gx = resident(x, {N, 1, H, W});
+            gx->requires_grad = x_grad != 0;
+            NodeRef gw1 = resident(w1, {C1, 1, 3, 3}), gb1 = resident(b1, {C1});
+            NodeRef gw2 = resident(w2, {C2, C1, 3, 3}), gb2 = resident(b2, {C2});
+            NodeRef pooled = hip::nn::conv2d_maxpool(gx, gw1, gb1, 1, 1, true, 2, 2);
+            NodeRef out = hip::nn::conv2d(pooled, gw2, gb2, 1, 1);
+            if (two_consumers) {
+                NodeRef gw3 = resident(w3, {C2, C1, 3, 3}), gb3 = resident(Vec(C2, 0.0f), {C2});
+                out = hip::graph::add(out, hip::nn::conv2d(pooled, gw3, gb3, 1, 1));
+            }
+            gpu::set_grad(out, seed);
+            backward_graph(out);
+            const Vec got[5] = {gpu::read_grad(pooled), gpu::read_grad(gw1), gpu::read_grad(gb1),
+                                gpu::read_grad(gw2), gpu::read_grad(gb2)};
+            const char* names[5] = {"pooled.grad", "conv1 weight.grad", "conv1 bias.grad",
+                                    "conv2 weight.grad", "conv2 bias.grad"};
+            for (int i = 0; i < 5; ++i) {
+                if (!x_grad)
+                    ref[i] = got[i];
+                else
+                    same(ref[i], got[i], std::string(two_consumers ? "two consumers: " : "") +
+                                             "fused vs unfused " + names[i]);
+            }
+        }
+        if (two_consumers) continue;
+        // the oracle's composition on the same integers
+        Vec y1(N * C1 * H * W), a1(y1.size()), p1(N * C1 * PH * PW);
+        std::vector<int32_t> am(p1.size());
+        orc_conv2d_forward(x.data(), w1.data(), b1.data(), y1.data(), N, 1, C1, H, W, 3, 3, 1, 1);
+        orc_relu_forward(y1.data(), a1.data(), y1.size());
+        orc_maxpool_forward(a1.data(), p1.data(), am.data(), N, C1, H, W, 2, 2);
+        Vec dp1(p1.size(), 0.0f), dw2(w2.size(), 0.0f), db2(C2, 0.0f), da1(a1.size(), 0.0f),
+            dy1(y1.size(), 0.0f), dx(x.size(), 0.0f), dw1(w1.size(), 0.0f), db1(C1, 0.0f);
+        orc_conv2d_backward(p1.data(), w2.data(), seed.data(), dp1.data(), dw2.data(), db2.data(),
+                            N, C1, C2, PH, PW, 3, 3, 1, 1);
+        orc_maxpool_backward(dp1.data(), am.data(), da1.data(), dp1.size());
+        orc_relu_backward(y1.data(), da1.data(), dy1.data(), y1.size());
+        orc_conv2d_backward(x.data(), w1.data(), dy1.data(), dx.data(), dw1.data(), db1.data(), N,
+                            1, C1, H, W, 3, 3, 1, 1);
+        same(ref[0], dp1, "fused vs oracle pooled.grad");
+        same(ref[1], dw1, "fused vs oracle conv1 weight.grad");
+        same(ref[2], db1, "fused vs oracle conv1 bias.grad");
+        same(ref[3], dw2, "fused vs oracle conv2 weight.grad");
+        same(ref[4], db2, "fused vs oracle conv2 bias.grad");
+    }
+}
+
 // runtime::swap_grad seeds a backward from a gradient already on the device:
 // the same bits as set_grad's host copy; swapping back returns the seed and
 // the node's own (zero) gradient; a buffer of another length panics.
@@ -1207,6 +1280,7 @@ const Case kCases[] = {
     {"cfg3_cnn_step", cfg3_cnn_step},
     {"cuda_conv2d_maxpool_node", cuda_conv2d_maxpool_node},
     {"swap_grad_seed", swap_grad_seed},
+    {"cfg3_fused_backward_exact", cfg3_fused_backward_exact},
 };
 
 int main(int argc, char** argv) {

@@ -479,6 +479,89 @@ def test_maxpool_conv2d_backward_matches_the_two_ops(hip, orc, shape, with_dx, r
     assert np.any(dw_ref != 0)  # the pooled gradient reached the weights
 
 
+FUSED_LOWER_SHAPES = [  # (n, c_lo, c_mid, c_out, h, w): lower "same" 3x3, 2x2 pool, upper "same" 3x3
+    (3, 1, 32, 64, 28, 28),   # cfg3's layers: one launch plus the sums
+    (2, 2, 32, 64, 12, 16),   # two lower input channels, pooled 6x8
+    (2, 1, 64, 64, 8, 8),     # two input-gradient blocks per image, pooled 4x4
+    (2, 3, 32, 64, 8, 8),     # three lower channels: the two calls
+    (2, 1, 16, 8, 10, 10),    # channel counts off the kernel's blocks: the two calls
+    (1, 1, 32, 64, 6, 6),     # pooled 3x3 (odd width): the two calls
+]
+
+
+@pytest.mark.parametrize("shape", FUSED_LOWER_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("floats", [False, True], ids=["ints", "floats"])
+@pytest.mark.parametrize("beta_p", [0.0, 1.0])
+def test_conv2d_maxpool_relu_conv2d_backward(hip, orc, shape, floats, beta_p):
+    """nrs_conv2d_maxpool_relu_conv2d_backward against its definition, the
+    upper layer's nrs_conv2d_backward_ex then nrs_maxpool_relu_conv2d_backward
+    without the lower input gradient: the pooled gradient and the upper
+    layer's weight and bias gradients bit for bit (the same kernels); the
+    lower layer's bit for bit on small integers (its sum runs over each
+    window's argmax pixel in another order) and within f32 rounding on
+    normal data; beta_params 0 over NaN and 1 over old values. The integer
+    case is also checked against the oracle's max pool, ReLU gate and
+    Conv2d backward."""
+    n, clo, cm, co, h, w = shape
+    rng = np.random.default_rng(n + 3 * clo + cm + co + h)
+    ph, pw = h // 2, w // 2
+    if floats:
+        x = rng.standard_normal(n * clo * h * w).astype(np.float32)
+        w1 = (rng.standard_normal(cm * clo * 9) * 0.3).astype(np.float32)
+        b1 = (rng.standard_normal(cm) * 0.1).astype(np.float32)
+        w2 = (rng.standard_normal(co * cm * 9) * 0.1).astype(np.float32)
+        g = rng.standard_normal(n * co * ph * pw).astype(np.float32)
+    else:
+        x = int_matrix(rng, (n * clo * h * w,), -2, 2)
+        w1 = int_matrix(rng, (cm * clo * 9,), -2, 2)
+        b1 = int_matrix(rng, (cm,), -2, 2)
+        w2 = int_matrix(rng, (co * cm * 9,), -2, 2)
+        g = int_matrix(rng, (n * co * ph * pw,), -2, 2)
+    D = hip.DeviceBuffer.from_host
+    pooled = hip.DeviceBuffer(n * cm * ph * pw)
+    am = hip.DeviceBuffer(n * cm * ph * pw, np.int32)
+    y = hip.DeviceBuffer(n * cm * h * w)
+    hip.call("nrs_conv2d_relu_maxpool_forward", pooled, am, y, D(x), D(w1), D(b1), n, clo, h, w,
+             cm, 3, 3, 1, 1, 2, 2)
+    if beta_p:
+        olds = [int_matrix(rng, (k,), -3, 3) for k in (w2.size, co, w1.size, cm)]
+    else:
+        olds = [np.full(k, np.nan, np.float32) for k in (w2.size, co, w1.size, cm)]
+    # the definition: the two calls
+    rp, rw2, rb2, rw1, rb1 = (hip.DeviceBuffer(n * cm * ph * pw),) + tuple(D(o) for o in olds)
+    hip.call("nrs_conv2d_backward_ex", rp, rw2, rb2, D(g), pooled, D(w2), n, cm, ph, pw, co, 3, 3,
+             1, 1, 0.0, beta_p)
+    hip.call("nrs_maxpool_relu_conv2d_backward", None, rw1, rb1, rp, am, pooled, D(x), D(w1), n,
+             clo, h, w, cm, 3, 3, 1, 1, 2, 2, beta_p)
+    fp = D(np.full(n * cm * ph * pw, np.nan, np.float32))
+    fw2, fb2, fw1, fb1 = (D(o) for o in olds)
+    print(f"conv2d maxpool relu conv2d backward {shape} floats={floats} beta={beta_p}", flush=True)
+    hip.call("nrs_conv2d_maxpool_relu_conv2d_backward", fp, fw2, fb2, fw1, fb1, D(g), pooled,
+             D(w2), am, D(x), D(w1), n, clo, h, w, cm, 3, 3, 1, 1, 2, 2, co, 3, 3, 1, 1, beta_p)
+    assert np.array_equal(fp.to_host(), rp.to_host())
+    assert np.array_equal(fw2.to_host(), rw2.to_host())
+    assert np.array_equal(fb2.to_host(), rb2.to_host())
+    got_w1, got_b1, ref_w1, ref_b1 = fw1.to_host(), fb1.to_host(), rw1.to_host(), rb1.to_host()
+    if floats:
+        # both sum the same products: within a few roundings of their scale
+        for got, ref in ((got_w1, ref_w1), (got_b1, ref_b1)):
+            scale = np.max(np.abs(ref)) + 1.0
+            assert np.max(np.abs(got - ref)) <= 1e-5 * scale
+    else:
+        assert np.array_equal(got_w1, ref_w1)
+        assert np.array_equal(got_b1, ref_b1)
+        # the oracle: pooled gradient to the argmax pixels, ReLU gate on the
+        # conv output, Conv2d backward
+        y_h = y.to_host()
+        gu = orc.maxpool_backward(rp.to_host(), am.to_host(), n * cm * h * w)
+        gu = np.where(y_h > 0, gu, 0).astype(np.float32)
+        _, dw_ref, db_ref = orc.conv2d_backward(x, w1, gu, n, clo, cm, h, w, 3, 3, 1, 1)
+        base_w, base_b = (olds[2], olds[3]) if beta_p else (0.0, 0.0)
+        assert np.array_equal(got_w1, dw_ref.ravel() + base_w)
+        assert np.array_equal(got_b1, db_ref.ravel() + base_b)
+        assert np.any(dw_ref != 0)
+
+
 @pytest.mark.parametrize("shape", [(2, 3, 4, 8, 8, 3, 3, 1, 1), (3, 1, 32, 28, 28, 3, 3, 1, 1),
                                    (3, 32, 64, 14, 14, 3, 3, 1, 1), (2, 6, 5, 9, 9, 3, 3, 1, 1),
                                    (1, 8, 3, 7, 7, 3, 3, 2, 1), (2, 2, 3, 6, 6, 2, 2, 1, 2),
