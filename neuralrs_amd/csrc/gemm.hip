@@ -591,11 +591,14 @@ int linear_backward(float* dx, float* dw, float* db, const float* grad, const fl
         db = nullptr;
     }
     // The row of sums rides the weight-gradient product when it costs no
-    // extra tile row (in_f not a multiple of 64) or the product is small;
-    // else (the cfg4 FFN's 256 x 1024 weight gradient: 80 tiles in place of
-    // 64) the column sums are a launch of their own after the group.
+    // extra tile row (in_f not a multiple of 64), the product is small, or
+    // the extra 64-row tile row is cheaper than the column-sum launches
+    // (two for more than 1024 rows, ~3 us each): at most 2^28 FLOP, e.g. the
+    // cfg4 FFN's 1024 x 256 weight gradient (68 tiles in place of 64). The
+    // 256 x 1024 one (80 tiles in place of 64, 2^29 FLOP more) sums after
+    // the group in a launch of its own.
     float* db_after = nullptr;
-    if (db && in_f % 64 == 0 && in_f * out_f > 65536) {
+    if (db && in_f % 64 == 0 && in_f * out_f > 65536 && 128 * out_f * batch > (int64_t)1 << 28) {
         db_after = db;
         db = nullptr;
     }
