@@ -156,19 +156,20 @@ def bench_conv_cfg3(hip, steps, warmup, closures_only=False):
     # conv1 -> ReLU -> maxpool as one node each way: conv1's output only
     # feeds the pooling, so the fused forward never writes it and the fused
     # backward expands the pooled gradient while loading, gated by the pooled
-    # value's sign (nrs_conv2d_relu_maxpool_forward /
-    # nrs_maxpool_relu_conv2d_backward). Gradients are written, not added
-    # (beta 0): a training step zeroes them first (zero_grad), and this is
-    # that zeroing and the first accumulation in one. The op-by-op sequence,
-    # with its zeroing launches, is step_unfused.
+    # value's sign (nrs_conv2d_relu_maxpool_forward), and conv2's backward
+    # gives conv1's weight and bias gradients in its own launch from the
+    # pooled gradient it computes (nrs_conv2d_maxpool_relu_conv2d_backward).
+    # Gradients are written, not added (beta 0): a training step zeroes them
+    # first (zero_grad), and this is that zeroing and the first accumulation
+    # in one. The op-by-op sequence, with its zeroing launches, is
+    # step_unfused.
     def step():
         hip.call("nrs_conv2d_relu_maxpool_forward", p1.ptr, am.ptr, None, dx.ptr, dw1.ptr,
                  db1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2)
         hip.call("nrs_conv2d_forward", y2.ptr, p1.ptr, dw2.ptr, db2.ptr, N, 32, 14, 14, 64, 3, 3, 1, 1)
-        hip.call("nrs_conv2d_backward_ex", gp1.ptr, gw2.ptr, gb2.ptr, dg2.ptr, p1.ptr, dw2.ptr,
-                 N, 32, 14, 14, 64, 3, 3, 1, 1, 0.0, 0.0)
-        hip.call("nrs_maxpool_relu_conv2d_backward", None, gw1.ptr, gb1.ptr, gp1.ptr, am.ptr,
-                 p1.ptr, dx.ptr, dw1.ptr, N, 1, 28, 28, 32, 3, 3, 1, 1, 2, 2, 0.0)
+        hip.call("nrs_conv2d_maxpool_relu_conv2d_backward", gp1.ptr, gw2.ptr, gb2.ptr, gw1.ptr,
+                 gb1.ptr, dg2.ptr, p1.ptr, dw2.ptr, am.ptr, dx.ptr, dw1.ptr, N, 1, 28, 28, 32,
+                 3, 3, 1, 1, 2, 2, 64, 3, 3, 1, 1, 0.0)
 
     def step_unfused():
         for buf in (gw1, gb1, gw2, gb2):
@@ -805,7 +806,7 @@ def main():
     }
     if not args.no_conv:
         c = bench_conv_cfg3(hip, max(5, args.steps // 2), args.warmup)
-        hc = host_step("cnn", 50, 10)
+        hc = host_step("cnn", 200, 20)
         out["conv2d_fwd_bwd"] = {
             "value": round(hc["imgs_per_s"] if hc else c["imgs_per_s"], 1), "unit": "imgs/s",
             "timing": ("neuralrs_amd/bench_host cnn: the step through the C++ operator surface "
@@ -821,7 +822,8 @@ def main():
                       "examples/mnist_cuda_cnn.rs:125), fwd+bwd: weight and bias grads of both "
                       "layers, input grad of conv2 (the image batch requires no grad, as in "
                       "examples/mnist_cuda_cnn.rs:261); conv1, ReLU and the maxpool as one node "
-                      "each way, op by op in step_us_op_by_op; the conv_* legs time the two conv "
+                      "each way, conv2's backward giving conv1's parameter gradients in its "
+                      "launch, op by op in step_us_op_by_op; the conv_* legs time the two conv "
                       "layers' own passes against their rooflines",
             "conv1_maxpool_fwd_us": round(c["conv1_pool_fwd_us"], 2),
             "maxpool_conv1_bwd_us": round(c["pool_conv1_bwd_us"], 2),
@@ -851,7 +853,7 @@ def main():
                 "us_per_step_four_calls": round(hm["four_call_gpu_us"], 2),
                 "gemm_roofline_frac": round(m["gemm_roof_us"] / hm["eager_gpu_us"], 4),
                 "timing": "C++ issue (neuralrs_amd/bench_host mlp), HIP events on the stream"})
-        hb = host_step("block", 50, 10)
+        hb = host_step("block", 200, 20)
         if hb:
             gemm_roof = hb["gemm_flop_per_step"] / (PEAK_FP32_MFMA_TFLOPS * 1e12) * 1e6
             out["transformer_block_cfg4"] = {
