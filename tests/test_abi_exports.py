@@ -34,3 +34,12 @@ def test_python_binding_covers_header():
     from neuralrs_amd import _abi
 
     assert set(declared("nrs_hip.h")) == set(_abi.SIGNATURES)
+
+
+def test_rust_binding_covers_header():
+    """The Rust extern block a maintainer copies from INTEGRATION.md lists
+    exactly the header's entry points."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    block = text[text.index('extern "C" {'):]
+    block = block[:block.index("\n}\n")]
+    assert set(re.findall(r"pub fn (nrs_\w+)\(", block)) == set(declared("nrs_hip.h"))
