@@ -86,6 +86,23 @@ def test_gemm_f64_tolerance(hip, orc, layout, shape):
     assert err <= gemm_tol(inner), (err, gemm_tol(inner))
 
 
+@pytest.mark.parametrize("layout", [NN, NT, TN])
+@pytest.mark.parametrize("shape", [(4096, 4096, 32), (4096, 4096, 288), (4096, 8192, 96),
+                                   (4096, 4096, 100)], ids=lambda s: "x".join(map(str, s)))
+def test_gemm_large_whole_tiles_exact(hip, layout, shape):
+    """Plain products over whole 256x256 tiles that fill the GPU (the
+    256x256 tile, with a K tail at K = 100), all three layouts: exact on
+    small integers, every element."""
+    rows, cols, inner = shape
+    rng = np.random.default_rng(rows + cols + inner + layout)
+    a, b = operands(layout, rows, cols, inner, lambda s: int_matrix(rng, s, -4, 4))
+    A, B = logical(layout, a, b)
+    print(f"gemm whole tiles {LNAME[layout]} {shape}", flush=True)
+    c = run_gemm(hip, layout, a, b, rows, cols, inner)
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    assert np.array_equal(c, ref.astype(np.float32)), f"{LNAME[layout]} {shape}"
+
+
 def test_gemm_cfg1_512_vs_cpu_simd(hip, orc):
     """cfg1: 512^3, U(-1,1) seed 0; the GPU and the reference's AVX2 path both
     sit within the f32 tolerance of f64, and within 2x that of each other."""
