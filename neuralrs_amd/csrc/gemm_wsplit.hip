@@ -37,7 +37,17 @@
 namespace nrs {
 namespace {
 
-constexpr int kWsPitch = 17;  // LDS pitch of a 16x16 partial block
+// Row of element e (mod 256) of a 16x16 block in the sums: a wave's 64
+// elements are rows r, r + 4, r + 8, r + 12 (r = bits 6-7 of e) by 16
+// columns, 16 banks apart at the pitch below, so the reads do not conflict;
+// each store still covers whole 64-byte row segments.
+__device__ __forceinline__ int ws_row(int e) { return ((e >> 4) & 3) * 4 + ((e >> 6) & 3); }
+
+// LDS pitch of a 16x16 partial block. A wave stores rows 4g + r, columns c
+// (g < 4, c < 16) at (4g + r) * pitch + c: with pitch = 4 (mod 16) the four
+// row groups start 16 banks apart, so the 64 lanes hit 64 banks (17 put
+// rows 4 apart and conflicted about 4-way).
+constexpr int kWsPitch = 20;
 
 __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -180,7 +190,7 @@ __global__ __launch_bounds__(64 * W) void gemm_wsplit_kernel(WsArgs args) {
             // the fused seed (softmax(logits) - target) / batch, with the
             // reference kernel's arithmetic: the row max folded from class 0,
             // the sum of expf(l - max) in class order, then expf(l - max) / sum
-            const int i = (tid >> 4) & 15, j = tid & 15;
+            const int i = ws_row(tid), j = tid & 15;
             const int row = m0 + i, col = n0 + j;
             float v = 0.0f;
             if (tid < 256) {
@@ -213,7 +223,7 @@ __global__ __launch_bounds__(64 * W) void gemm_wsplit_kernel(WsArgs args) {
     }
     // one thread per output element: the W partials added in wave order
     for (int e = tid; e < NBLK * 256; e += 64 * W) {
-        const int blk = e >> 8, i = (e >> 4) & 15, j = e & 15;
+        const int blk = e >> 8, i = ws_row(e), j = e & 15;
         const int bm = blk / TN, bn = blk - bm * TN;
         const int row = m0 + 16 * bm + i, col = n0 + 16 * bn + j;
         if (col >= p.N) continue;
