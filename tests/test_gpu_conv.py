@@ -481,6 +481,7 @@ def test_maxpool_conv2d_backward_matches_the_two_ops(hip, orc, shape, with_dx, r
 
 FUSED_LOWER_SHAPES = [  # (n, c_lo, c_mid, c_out, h, w): lower "same" 3x3, 2x2 pool, upper "same" 3x3
     (3, 1, 32, 64, 28, 28),   # cfg3's layers: one launch plus the sums
+    (128, 1, 32, 64, 28, 28),  # cfg3 at its full batch (integer sums stay below 2^24)
     (2, 2, 32, 64, 12, 16),   # two lower input channels, pooled 6x8
     (2, 1, 64, 64, 8, 8),     # two input-gradient blocks per image, pooled 4x4
     (2, 3, 32, 64, 8, 8),     # three lower channels: the two calls
