@@ -122,6 +122,25 @@ typedef struct nrs_gemm_desc {
 } nrs_gemm_desc;
 int nrs_gemm_group(const nrs_gemm_desc *descs, int count);
 
+/* The backward of count (1 to 3) products sharing their left operand,
+ * y_i = x . W_i: the Q, K and V projections of one input (src/cuda/nn/
+ * multihead.rs:64-66), each with the matmul closure of src/cuda/graph/
+ * matmul.rs:418-431 (replaces those closures run one after another).
+ * x [rows, inner], W_i [inner, cols], g_i = dL/dy_i [rows, cols]:
+ *   dx   = ((g_0 . W_0^T + beta_x * dx) + g_1 . W_1^T) + g_2 . W_2^T
+ *   dW_i = x^T . g_i + beta_w[i] * dW_i
+ * The input gradient adds the parts in index order: with index 0 the
+ * closure that would run first, the bits are those of the closures run in
+ * turn (each the nrs_gemm_group of its two products, the first adding to dx
+ * with beta_x, the others with 1). All products run in one grouped launch
+ * and the sums in a second. When an output overlaps another output or an
+ * operand, or the products are small enough for the short-GEMM kernel, the
+ * closures' sequence runs instead (same results). */
+int nrs_matmul_shared_lhs_backward(float *dx, float *const *dw, const float *const *g,
+                                   const float *x, const float *const *w, int count,
+                                   int64_t rows, int64_t inner, int64_t cols, float beta_x,
+                                   const float *beta_w);
+
 /* The backward of Linear::forward = add(matmul(x, W), bias) (src/cuda/nn/
  * linear.rs:22-25; the closures of src/cuda/graph/matmul.rs:418-431 and
  * src/cuda/graph/add.rs:91-100), grad [batch, out_f], x [batch, in_f],

@@ -49,6 +49,7 @@ SIGNATURES = {
     "nrs_sync": [],
     "nrs_gemm": [ctypes.c_int, _P, _P, _P, _I, _I, _I, _F, _P, ctypes.c_int],
     "nrs_gemm_group": [ctypes.POINTER(GemmDesc), ctypes.c_int],
+    "nrs_matmul_shared_lhs_backward": [_P, _P, _P, _P, _P, ctypes.c_int, _I, _I, _I, _F, _P],
     "nrs_linear_backward": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _F, _F],
     "nrs_linear_backward_relu": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _F, _F],
     "nrs_linear_cross_entropy": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
@@ -220,6 +221,18 @@ def gemm_group(calls):
         d.layout, d.C, d.A, d.B = layout, _ptr(C), _ptr(A), _ptr(B)
         d.rows, d.cols, d.inner, d.beta, d.bias, d.epilogue = rows, cols, inner, beta, _ptr(bias), epi
     call("nrs_gemm_group", descs, len(calls))
+
+
+def matmul_shared_lhs_backward(dx, dws, gs, x, ws, rows, inner, cols, beta_x=0.0,
+                               beta_w=None):
+    """dx and dW_i of y_i = x . W_i (i < len(ws) <= 3) in one call: dx adds
+    g_i . W_i^T in index order after beta_x * dx, dW_i = x^T . g_i +
+    beta_w[i] * dW_i."""
+    n = len(ws)
+    ptrs = lambda bufs: (ctypes.c_void_p * 3)(*[_ptr(b) for b in bufs])
+    betas = (ctypes.c_float * 3)(*(list(beta_w) if beta_w is not None else [0.0] * n))
+    call("nrs_matmul_shared_lhs_backward", _ptr(dx), ptrs(dws), ptrs(gs), _ptr(x), ptrs(ws), n,
+         rows, inner, cols, beta_x, betas)
 
 
 def gemm_nt_splitk(C, A, B, rows, cols, inner, beta=0.0):

@@ -435,14 +435,105 @@ namespace {
 // compiled for up to four waves per SIMD so that several problems'
 // workgroups share a CU.
 constexpr int kGroupBM = 64, kGroupBN = 64, kGroupBK = 32, kGroupThreads = 256;
-static_assert(kGroupMax == NRS_GEMM_GROUP_MAX, "group size of the kernel and the C ABI");
+static_assert(kGroupMax >= NRS_GEMM_GROUP_MAX, "group size of the kernel and the C ABI");
+static_assert(sizeof(GemmGroupArgs) <= 4096, "group kernel arguments");
+
+}  // namespace
+
+namespace {
+
+// The group kernel's plan: K slices per call, and the order the problems take
+// in the grid.
+struct GroupPlan {
+    Plan plans[kGroupMax];
+    int order[kGroupMax];
+    int live_n = 0;
+    size_t partial_floats = 0;  // split-K partials of every split call
+};
+
+// Plans each problem of a group: a problem of few tiles over a long K is
+// split so that it brings about one workgroup per CU (at least 8 k-tiles per
+// slice, 2 for a grid under 16 tiles), like a launch of its own would. The
+// plan of a call does not depend on the other calls of its group.
+void plan_group(const GemmCall* calls, int count, GroupPlan& gp) {
+    const int cus = num_cus();
+    const TileShape s{kGroupBM, kGroupBN, kGroupBK, kGroupThreads};
+    for (int i = 0; i < count; ++i) {
+        const GemmCall& c = calls[i];
+        if (c.M == 0 || c.N == 0) continue;
+        const int64_t tiles = cdiv(c.M + (c.sum_row ? 1 : 0), s.bm) * cdiv(c.N, s.bn);
+        int64_t slices = 1;
+        if (tiles * 2 <= cus && c.K >= 8 * s.bk) {
+            const int64_t want = std::min<int64_t>(256, cdiv(cus, tiles));
+            const int64_t max_by_k = std::max<int64_t>(1, c.K / ((tiles >= 16 ? 8 : 2) * s.bk));
+            slices = std::max<int64_t>(1, std::min(want, max_by_k));
+        }
+        const int64_t kps = cdiv(cdiv(c.K, slices), s.bk) * s.bk;
+        gp.plans[i] = Plan{T64x64, (int)std::max<int64_t>(1, cdiv(c.K, kps)), kps, 2};
+        if (gp.plans[i].slices > 1)
+            gp.partial_floats += (size_t)gp.plans[i].slices *
+                                 (size_t)((c.M + (c.sum_row ? 1 : 0)) * c.N);
+        // Workgroups are dispatched in grid order, so the problems whose
+        // workgroups run longest (most k-tiles each) go first: started last
+        // they would run on alone after the short ones drain (the FFN
+        // backward pair, dW over 32 k-tiles per workgroup behind dX's 1024
+        // tiles of 8, took 74 us that way against 60 us long-first).
+        int j = gp.live_n++;
+        for (; j > 0 && gp.plans[gp.order[j - 1]].k_per_slice < kps; --j)
+            gp.order[j] = gp.order[j - 1];
+        gp.order[j] = i;
+    }
+}
+
+// Launches the group kernel on a plan; split calls write their partials to
+// consecutive regions of `partials` (gp.partial_floats floats), in call
+// order. g receives the launched arguments (the caller reduces the splits).
+int launch_group(const GemmCall* calls, const GroupPlan& gp, float* partials, GemmGroupArgs& g,
+                 float** part_of_call = nullptr) {
+    const TileShape s{kGroupBM, kGroupBN, kGroupBK, kGroupThreads};
+    float* part_of[kGroupMax] = {};
+    float* ws = partials;
+    for (int oi = 0; oi < gp.live_n; ++oi) {
+        const int i = gp.order[oi];
+        if (gp.plans[i].slices <= 1) continue;
+        part_of[i] = ws;
+        ws += (size_t)gp.plans[i].slices *
+              (size_t)((calls[i].M + (calls[i].sum_row ? 1 : 0)) * calls[i].N);
+    }
+    int next = 0;
+    int64_t total_wgs = 0;
+    for (int oi = 0; oi < gp.live_n; ++oi) {
+        const int i = gp.order[oi];
+        const GemmCall& c = calls[i];
+        const Plan& pl = gp.plans[i];
+        const int64_t tiles = cdiv(c.M + (c.sum_row ? 1 : 0), s.bm) * cdiv(c.N, s.bn);
+        GemmArgs& p = g.prob[next];
+        const int rc = make_args(p, c, s, pl);
+        if (rc != NRS_OK) return rc;
+        total_wgs = (total_wgs + 7) / 8 * 8;
+        g.first[next] = (int)total_wgs;
+        g.layout[next] = c.layout;
+        g.slices[next] = pl.slices;
+        if (pl.slices > 1) p.partial = part_of[i];
+        total_wgs += tiles * pl.slices;
+        ++next;
+    }
+    g.count = next;
+    if (part_of_call)
+        for (int i = 0; i < kGroupMax; ++i) part_of_call[i] = part_of[i];
+    NRS_ARG_CHECK(total_wgs <= INT32_MAX, "gemm group: grid too large");
+    hipLaunchKernelGGL((gemm_group_kernel<kGroupBM, kGroupBN, kGroupBK, 2, 2, 4, 2>),
+                       dim3((unsigned)total_wgs), dim3(kGroupThreads), 0, stream(), g);
+    NRS_LAUNCH_CHECK("gemm group");
+    return NRS_OK;
+}
 
 }  // namespace
 
 int gemm_group_run(const GemmCall* calls, int count) {
     NRS_ARG_CHECK(count >= 0 && (count == 0 || calls != nullptr), "gemm group: bad count");
     // Checks first, so that an invalid call launches nothing.
-    bool grouped = count >= 2 && count <= kGroupMax;
+    bool grouped = count >= 2 && count <= NRS_GEMM_GROUP_MAX;
     bool short_group = grouped;  // every live call fits the short-GEMM kernel
     bool is_live[kGroupMax] = {};
     int live = 0;
@@ -479,73 +570,229 @@ int gemm_group_run(const GemmCall* calls, int count) {
         return NRS_OK;
     }
 
-    const int cus = num_cus();
-    const TileShape s{kGroupBM, kGroupBN, kGroupBK, kGroupThreads};
+    GroupPlan gp;
+    plan_group(calls, count, gp);
+    float* partials = nullptr;
+    if (gp.partial_floats > 0) {
+        partials = workspace(sizeof(float) * gp.partial_floats, 0);
+        if (!partials) return NRS_ERR_ALLOC;
+    }
     GemmGroupArgs g{};
-    size_t partial_floats = 0;
-    int next = 0;
-    int64_t total_wgs = 0;
-    // Plan each problem: a problem of few tiles over a long K is split so
-    // that it brings about one workgroup per CU (at least 8 k-tiles per
-    // slice, 2 for a grid under 16 tiles), like a launch of its own would.
-    Plan plans[kGroupMax];
-    int order[kGroupMax];
-    int live_n = 0;
-    for (int i = 0; i < count; ++i) {
-        const GemmCall& c = calls[i];
-        if (c.M == 0 || c.N == 0) continue;
-        const int64_t tiles = cdiv(c.M + (c.sum_row ? 1 : 0), s.bm) * cdiv(c.N, s.bn);
-        int64_t slices = 1;
-        if (tiles * 2 <= cus && c.K >= 8 * s.bk) {
-            const int64_t want = std::min<int64_t>(256, cdiv(cus, tiles));
-            const int64_t max_by_k = std::max<int64_t>(1, c.K / ((tiles >= 16 ? 8 : 2) * s.bk));
-            slices = std::max<int64_t>(1, std::min(want, max_by_k));
-        }
-        const int64_t kps = cdiv(cdiv(c.K, slices), s.bk) * s.bk;
-        plans[i] = Plan{T64x64, (int)std::max<int64_t>(1, cdiv(c.K, kps)), kps, 2};
-        // Workgroups are dispatched in grid order, so the problems whose
-        // workgroups run longest (most k-tiles each) go first: started last
-        // they would run on alone after the short ones drain (the FFN
-        // backward pair, dW over 32 k-tiles per workgroup behind dX's 1024
-        // tiles of 8, took 74 us that way against 60 us long-first).
-        int j = live_n++;
-        for (; j > 0 && plans[order[j - 1]].k_per_slice < kps; --j) order[j] = order[j - 1];
-        order[j] = i;
-    }
-    for (int oi = 0; oi < live_n; ++oi) {
-        const GemmCall& c = calls[order[oi]];
-        const Plan& pl = plans[order[oi]];
-        const int64_t tiles = cdiv(c.M + (c.sum_row ? 1 : 0), s.bm) * cdiv(c.N, s.bn);
-        GemmArgs& p = g.prob[next];
-        const int rc = make_args(p, c, s, pl);
-        if (rc != NRS_OK) return rc;
-        total_wgs = (total_wgs + 7) / 8 * 8;
-        g.first[next] = (int)total_wgs;
-        g.layout[next] = c.layout;
-        g.slices[next] = pl.slices;
-        total_wgs += tiles * pl.slices;
-        if (pl.slices > 1) partial_floats += (size_t)pl.slices * (size_t)(p.mrows * c.N);
-        ++next;
-    }
-    g.count = next;
-    NRS_ARG_CHECK(total_wgs <= INT32_MAX, "gemm group: grid too large");
-    if (partial_floats > 0) {
-        float* ws = workspace(sizeof(float) * partial_floats, 0);
-        if (!ws) return NRS_ERR_ALLOC;
-        for (int q = 0; q < g.count; ++q)
-            if (g.slices[q] > 1) {
-                g.prob[q].partial = ws;
-                ws += (size_t)g.slices[q] * (size_t)(g.prob[q].mrows * g.prob[q].N);
-            }
-    }
-    hipLaunchKernelGGL((gemm_group_kernel<kGroupBM, kGroupBN, kGroupBK, 2, 2, 4, 2>),
-                       dim3((unsigned)total_wgs), dim3(kGroupThreads), 0, stream(), g);
-    NRS_LAUNCH_CHECK("gemm group");
+    const int rc = launch_group(calls, gp, partials, g);
+    if (rc != NRS_OK) return rc;
     for (int q = 0; q < g.count; ++q)
         if (g.slices[q] > 1) {
             launch_reduce(g.prob[q], g.slices[q]);
             NRS_LAUNCH_CHECK("gemm group (split-K reduce)");
         }
+    return NRS_OK;
+}
+
+namespace {
+
+// The sums that finish a shared-operand backward, in one launch. Problem q
+// stores v = R_0 (+ beta * old) + R_1 + ... into dst, each part's R_j being
+// its one product or the sum of its split-K slices in slice order from 0;
+// with in_dst, dst already holds R_0 (+ beta * old) and every listed part is
+// added to it. These are the operations, in the same order, of the products'
+// epilogues and of splitk_reduce4_kernel when the products run one group
+// after another. A problem's workgroups are a contiguous block range, so the
+// problem index is uniform per workgroup.
+constexpr int kSumMax = 4;
+struct SumPart {
+    const float* src;
+    int slices;
+};
+struct SumProblem {
+    float* dst;
+    int64_t total4;  // float4s of dst (and of each slice)
+    float beta;
+    int nparts;
+    int in_dst;
+    SumPart part[3];
+};
+struct GroupSumArgs {
+    SumProblem prob[kSumMax];
+    int first[kSumMax];   // first workgroup of each problem, ascending
+    int blocks[kSumMax];  // its workgroups
+    int count;
+};
+
+__device__ __forceinline__ f32x4 sum_part(const SumPart& s, int64_t i, int64_t total4) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(s.src) + i;
+    if (s.slices == 1) return *src;
+    // eight slices' loads in flight, added in slice order
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    int k = 0;
+    for (; k + 8 <= s.slices; k += 8) {
+        f32x4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = src[(int64_t)(k + j) * total4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = acc + v[j];
+    }
+    for (; k < s.slices; ++k) acc = acc + src[(int64_t)k * total4];
+    return acc;
+}
+
+__global__ __launch_bounds__(256) void group_sum_kernel(GroupSumArgs a) {
+    const int b = blockIdx.x;
+    int q = 0;
+#pragma unroll
+    for (int j = 1; j < kSumMax; ++j)
+        if (j < a.count && b >= a.first[j]) q = j;
+    const SumProblem& p = a.prob[q];
+    const int64_t step = (int64_t)a.blocks[q] * 256;
+    for (int64_t i = (int64_t)(b - a.first[q]) * 256 + threadIdx.x; i < p.total4; i += step) {
+        f32x4* dst = reinterpret_cast<f32x4*>(p.dst) + i;
+        f32x4 v;
+        int j = 0;
+        if (p.in_dst) {
+            v = *dst;
+        } else {
+            v = sum_part(p.part[0], i, p.total4);
+            if (p.beta != 0.0f) v = v + p.beta * *dst;
+            j = 1;
+        }
+        for (; j < p.nparts; ++j) v = sum_part(p.part[j], i, p.total4) + v;
+        *dst = v;
+    }
+}
+
+}  // namespace
+
+int shared_lhs_backward(float* dx, float* const* dw, const float* const* g, const float* x,
+                        const float* const* w, int count, int64_t rows, int64_t inner,
+                        int64_t cols, float beta_x, const float* beta_w) {
+    NRS_ARG_CHECK(count >= 1 && count <= 3, "shared-lhs backward: %d products (1 to 3)", count);
+    NRS_ARG_CHECK(dw && g && w && beta_w, "shared-lhs backward: null array");
+    NRS_ARG_CHECK(rows >= 0 && inner >= 0 && cols >= 0, "shared-lhs backward: negative size");
+    // the pair of closure i: dx (+)= g_i . W_i^T, dW_i = x^T . g_i + beta_w[i] * dW_i
+    GemmCall pair[3][2];
+    for (int i = 0; i < count; ++i) {
+        GemmCall& d = pair[i][0];
+        d.layout = NRS_NT;
+        d.C = dx;
+        d.A = g[i];
+        d.B = w[i];
+        d.M = rows;
+        d.N = inner;
+        d.K = cols;
+        d.beta = i == 0 ? beta_x : 1.0f;
+        GemmCall& e = pair[i][1];
+        e.layout = NRS_TN;
+        e.C = dw[i];
+        e.A = x;
+        e.B = g[i];
+        e.M = inner;
+        e.N = cols;
+        e.K = rows;
+        e.beta = beta_w[i];
+        for (const GemmCall& c : pair[i]) {
+            bool empty;
+            const int rc = check_call(c, empty);
+            if (rc != NRS_OK) return rc;
+        }
+    }
+    // One group for all products when every pair would run the group kernel
+    // (not the short-GEMM kernel) and no output overlaps another output or an
+    // operand; otherwise the closures' sequence.
+    bool fused = count >= 2 && rows > 0 && inner > 0 && cols > 0 && (rows * inner) % 4 == 0 &&
+                 (inner * cols) % 4 == 0 && aligned16(dx);
+    for (int i = 0; i < count && fused; ++i)
+        for (const GemmCall& c : pair[i])
+            fused = fused && vec4_loads(c) && aligned16(c.C);
+    for (int i = 0; i < count && fused; ++i)
+        fused = !(wsplit_eligible(pair[i][0], true) && wsplit_eligible(pair[i][1], true));
+    if (fused) {
+        const OperandRange outs[4] = {{dx, sizeof(float) * (size_t)(rows * inner)},
+                                      {dw[0], sizeof(float) * (size_t)(inner * cols)},
+                                      {count > 1 ? dw[1] : nullptr, sizeof(float) * (size_t)(inner * cols)},
+                                      {count > 2 ? dw[2] : nullptr, sizeof(float) * (size_t)(inner * cols)}};
+        OperandRange ins[7] = {{x, sizeof(float) * (size_t)(rows * inner)}};
+        for (int i = 0; i < count; ++i) {
+            ins[1 + 2 * i] = {w[i], sizeof(float) * (size_t)(inner * cols)};
+            ins[2 + 2 * i] = {g[i], sizeof(float) * (size_t)(rows * cols)};
+        }
+        for (int a = 0; a <= count && fused; ++a) {
+            for (int b = 0; b < 1 + 2 * count; ++b)
+                fused = fused && !overlaps(outs[a].p, outs[a].bytes, ins[b].p, ins[b].bytes);
+            for (int b = a + 1; b <= count; ++b)
+                fused = fused && !overlaps(outs[a].p, outs[a].bytes, outs[b].p, outs[b].bytes);
+        }
+    }
+    if (!fused) {
+        for (int i = 0; i < count; ++i) {
+            const int rc = gemm_group_run(pair[i], 2);
+            if (rc != NRS_OK) return rc;
+        }
+        return NRS_OK;
+    }
+
+    // calls 0..count-1: the input-gradient products (the first into dx with
+    // beta_x when not split, the others with beta 0 into scratch when not
+    // split); count..2*count-1: the weight gradients
+    GemmCall calls[kGroupMax];
+    for (int i = 0; i < count; ++i) {
+        calls[i] = pair[i][0];
+        calls[i].beta = 0.0f;
+        calls[count + i] = pair[i][1];
+    }
+    GroupPlan gp;
+    plan_group(calls, 2 * count, gp);
+    const size_t dx_floats = (size_t)(rows * inner);
+    const bool first_in_dx = gp.plans[0].slices == 1;
+    if (first_in_dx) calls[0].beta = beta_x;
+    size_t direct = 0;
+    for (int i = first_in_dx ? 1 : 0; i < count; ++i)
+        direct += gp.plans[i].slices == 1 ? dx_floats : 0;
+    float* ws = workspace(sizeof(float) * (gp.partial_floats + direct), 0);
+    if (!ws) return NRS_ERR_ALLOC;
+    float* region = ws + gp.partial_floats;
+    float* direct_of[3] = {};
+    for (int i = first_in_dx ? 1 : 0; i < count; ++i)
+        if (gp.plans[i].slices == 1) {
+            direct_of[i] = region;
+            calls[i].C = region;
+            region += dx_floats;
+        }
+    GemmGroupArgs ga{};
+    float* part_of[kGroupMax] = {};
+    int rc = launch_group(calls, gp, ws, ga, part_of);
+    if (rc != NRS_OK) return rc;
+
+    GroupSumArgs sa{};
+    const int64_t cap = 8 * (int64_t)num_cus();
+    int blocks = 0;
+    auto add = [&](SumProblem p) {
+        const int q = sa.count++;
+        sa.prob[q] = p;
+        sa.first[q] = blocks;
+        sa.blocks[q] = (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(p.total4, 256), cap));
+        blocks += sa.blocks[q];
+    };
+    SumProblem px{};
+    px.dst = dx;
+    px.total4 = (int64_t)dx_floats / 4;
+    px.beta = beta_x;
+    px.in_dst = first_in_dx ? 1 : 0;
+    for (int i = first_in_dx ? 1 : 0; i < count; ++i)
+        px.part[px.nparts++] =
+            direct_of[i] ? SumPart{direct_of[i], 1} : SumPart{part_of[i], gp.plans[i].slices};
+    add(px);
+    for (int i = 0; i < count; ++i) {
+        const int c = count + i;
+        if (gp.plans[c].slices <= 1) continue;  // written with its beta by the group kernel
+        SumProblem pw{};
+        pw.dst = dw[i];
+        pw.total4 = inner * cols / 4;
+        pw.beta = beta_w[i];
+        pw.nparts = 1;
+        pw.part[0] = SumPart{part_of[c], gp.plans[c].slices};
+        add(pw);
+    }
+    hipLaunchKernelGGL(group_sum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream(), sa);
+    NRS_LAUNCH_CHECK("shared-lhs backward (sums)");
     return NRS_OK;
 }
 
@@ -674,6 +921,14 @@ int nrs_gemm_group(const nrs_gemm_desc* descs, int count) {
         c.epi = d.epilogue;
     }
     return nrs::gemm_group_run(calls, count);
+}
+
+int nrs_matmul_shared_lhs_backward(float* dx, float* const* dw, const float* const* g,
+                                   const float* x, const float* const* w, int count, int64_t rows,
+                                   int64_t inner, int64_t cols, float beta_x,
+                                   const float* beta_w) {
+    NRS_REQUIRE_INIT();
+    return nrs::shared_lhs_backward(dx, dw, g, x, w, count, rows, inner, cols, beta_x, beta_w);
 }
 
 int nrs_linear_backward(float* dx, float* dw, float* db, const float* grad, const float* x,

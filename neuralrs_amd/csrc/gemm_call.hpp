@@ -63,9 +63,15 @@ struct GemmCall {
 };
 
 int gemm_run(const GemmCall& c);
-// Up to kGroupMax dense calls in one launch of the group kernel when they
+// Up to NRS_GEMM_GROUP_MAX dense calls in one launch of the group kernel when they
 // qualify (see nrs_gemm_group), else gemm_run on each in order.
 int gemm_group_run(const GemmCall* calls, int count);
+
+// nrs_matmul_shared_lhs_backward: the backward of count <= 3 products
+// x . W_i, the input-gradient parts added in index order.
+int shared_lhs_backward(float* dx, float* const* dw, const float* const* g, const float* x,
+                        const float* const* w, int count, int64_t rows, int64_t inner,
+                        int64_t cols, float beta_x, const float* beta_w);
 
 // nrs_linear_backward (dx = grad . w^T masked where mask <= 0 when mask is
 // given, dw = x^T . grad, db = column sums of grad; each + beta * old).

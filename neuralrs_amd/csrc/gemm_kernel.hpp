@@ -735,7 +735,10 @@ void gemm_kernel(GemmArgs p) {
 // workgroups share the CUs, so one problem's load latency, barriers and
 // epilogue overlap another's MFMAs; one launch per GEMM leaves each CU a
 // single workgroup of small tiles whose waves all stall at the same points.
-constexpr int kGroupMax = 4;
+// Problems of one group launch: the C ABI's groups (NRS_GEMM_GROUP_MAX) and
+// the backward of three products sharing their left operand (three input-
+// gradient and three weight-gradient products).
+constexpr int kGroupMax = 6;
 struct GemmGroupArgs {
     GemmArgs prob[kGroupMax];
     int first[kGroupMax];   // first workgroup id of each problem, ascending

@@ -160,12 +160,18 @@ void build_topo(const NodeRef& n, std::unordered_set<const Node*>& visited,
 }
 
 // The backward pass being run on this thread: each node's consumers in its
-// graph, and the nodes whose closure a consumer's fused backward has run.
+// graph, how many of them have yet to run (a node's gradient is complete at
+// 0), its position in the topological order (closures run from the last
+// position down), and the nodes whose closure has run (on its own, or
+// within a fused backward).
 struct BackwardPass {
     std::unordered_map<const Node*, int> consumers;
+    std::unordered_map<const Node*, int> pending;
+    std::unordered_map<const Node*, size_t> pos;
     std::unordered_set<const Node*> done;
 };
 thread_local BackwardPass* tl_pass = nullptr;
+bool g_fused_backward = true;
 
 }  // namespace
 
@@ -261,17 +267,24 @@ void backward_graph(const NodeRef& root) {
     std::unordered_set<const Node*> visited;
     build_topo(root, visited, topo);
     BackwardPass pass;
-    for (const NodeRef& n : topo)
-        for (const NodeRef& p : n->parents) ++pass.consumers[p.get()];
+    for (size_t i = 0; i < topo.size(); ++i) {
+        pass.pos[topo[i].get()] = i;
+        for (const NodeRef& p : topo[i]->parents) ++pass.consumers[p.get()];
+    }
+    pass.pending = pass.consumers;
     struct Restore {
         BackwardPass* prev;
         ~Restore() { tl_pass = prev; }
     } restore{tl_pass};
     tl_pass = &pass;
     for (auto it = topo.rbegin(); it != topo.rend(); ++it) {
-        if (pass.done.count(it->get())) continue;  // run by a consumer's fused backward
-        const std::vector<float> grad = (*it)->grad;
-        if ((*it)->backward_fn) (*it)->backward_fn(grad);
+        // a node in `done` was run by a fused backward
+        if (!pass.done.count(it->get())) {
+            const std::vector<float> grad = (*it)->grad;
+            if ((*it)->backward_fn) (*it)->backward_fn(grad);
+            pass.done.insert(it->get());
+        }
+        for (const NodeRef& p : (*it)->parents) --pass.pending[p.get()];
     }
 }
 
@@ -295,6 +308,8 @@ void set_grad(const NodeRef& node, const std::vector<float>& grad) {
     if (grad.size() != g.data.len()) throw Panic("set_grad: gradient length mismatch");
     *g.grad = DeviceBuffer::from_host(grad);
 }
+
+void set_fused_backward(bool on) { g_fused_backward = on; }
 
 void swap_grad(const NodeRef& node, DeviceBuffer& buf) {
     GpuBuffers& g = gpu_of(node, "swap_grad: node not on GPU");
@@ -602,7 +617,9 @@ bool fused_relu_pool_backward(const NodeRef& input, const NodeRef& weight, const
                               const DeviceBuffer& grad, size_t c_out, size_t kh, size_t kw,
                               size_t stride, size_t pad) {
     const ReluPoolConv* lo = input->relu_pool_conv.get();
-    if (!lo || !tl_pass || !input->requires_grad || lo->input->requires_grad) return false;
+    if (!lo || !tl_pass || !g_fused_backward || !input->requires_grad ||
+        lo->input->requires_grad)
+        return false;
     const auto it = tl_pass->consumers.find(input.get());
     if (it == tl_pass->consumers.end() || it->second != 1) return false;
     GpuBuffers& pg = gpu_of(input, "conv2d bwd: input not on GPU");
@@ -871,9 +888,71 @@ NodeRef Linear::forward(const NodeRef& input) const {
 
 namespace {
 
+// The products of one matmul_shared_lhs call, for their joint backward.
+struct SharedLhs {
+    NodeRef x;
+    std::vector<NodeRef> ws;
+    std::vector<std::weak_ptr<Node>> outs;
+    size_t m, k, n;
+};
+
+// The matmul closures of every product of `s` (matmul.rs:418-431) as one
+// nrs_matmul_shared_lhs_backward call, when the running pass holds every
+// product, none has run yet and every product's gradient is complete (all
+// its consumers have run); the input-gradient parts are added in the order
+// the closures would run (the last topological position first), so the bits
+// are those of the closures. The pass then skips the other products'
+// closures. Returns false, having changed nothing, otherwise (and for shared
+// gradient buffers, e.g. a weight used twice).
+bool fused_shared_lhs_backward(const SharedLhs& s) {
+    const size_t count = s.outs.size();
+    if (!tl_pass || !g_fused_backward || count < 2 || count > 3) return false;
+    std::vector<NodeRef> outs;
+    for (const std::weak_ptr<Node>& wp : s.outs) {
+        NodeRef o = wp.lock();
+        if (!o || !o->gpu || tl_pass->done.count(o.get()) || !tl_pass->pos.count(o.get()))
+            return false;
+        const auto r = tl_pass->pending.find(o.get());
+        if (r != tl_pass->pending.end() && r->second != 0) return false;
+        outs.push_back(std::move(o));
+    }
+    GpuBuffers& xg = gpu_of(s.x, "cuda matmul bwd: lhs not on GPU");
+    std::vector<GpuBuffers*> wg;
+    for (const NodeRef& w : s.ws) wg.push_back(&gpu_of(w, "cuda matmul bwd: rhs not on GPU"));
+    for (size_t i = 0; i < count; ++i) {
+        if (wg[i]->grad == xg.grad) return false;
+        for (size_t j = i + 1; j < count; ++j)
+            if (wg[i]->grad == wg[j]->grad) return false;
+    }
+    size_t order[3] = {0, 1, 2};
+    std::sort(order, order + count, [&](size_t a, size_t b) {
+        return tl_pass->pos.at(outs[a].get()) > tl_pass->pos.at(outs[b].get());
+    });
+    float beta_x = 1.0f;
+    float* dx = xg.grad->acc_target(beta_x);
+    float* dw[3];
+    const float* g[3];
+    const float* w[3];
+    float beta_w[3];
+    for (size_t j = 0; j < count; ++j) {
+        const size_t i = order[j];
+        beta_w[j] = 1.0f;
+        dw[j] = wg[i]->grad->acc_target(beta_w[j]);
+        g[j] = outs[i]->gpu->grad->ptr();
+        w[j] = wg[i]->data.ptr();
+    }
+    check(nrs_matmul_shared_lhs_backward(dx, dw, g, xg.data.ptr(), w, (int)count, s.m, s.k, s.n,
+                                         beta_x, beta_w),
+          "cuda matmul bwd: launch failed");
+    for (const NodeRef& o : outs) tl_pass->done.insert(o.get());
+    return true;
+}
+
 // x . w for each of several weights, in one grouped launch: the Q, K and V
 // projections of one input (multihead.rs:64-66). Each result is a node of
-// its own with graph::matmul's checks, output and backward closure.
+// its own with graph::matmul's checks and output; their backward closures
+// run together when the pass allows (fused_shared_lhs_backward), else each
+// is graph::matmul's.
 std::vector<NodeRef> matmul_shared_lhs(const NodeRef& x, const std::vector<NodeRef>& ws) {
     GpuBuffers& xg = gpu_of(x, "cuda matmul: lhs not on GPU");
     if (x->shape.size() != 2) throw Panic("cuda matmul: operands must be 2-D");
@@ -892,11 +971,23 @@ std::vector<NodeRef> matmul_shared_lhs(const NodeRef& x, const std::vector<NodeR
     }
     check(nrs_gemm_group(d.data(), (int)d.size()), "cuda matmul: launch failed");
     std::vector<NodeRef> nodes;
+    for (size_t i = 0; i < ws.size(); ++i)
+        nodes.push_back(make_output({m, ws[i]->shape[1]}, {x, ws[i]}, std::move(outs[i])));
+    bool same_n = true;
+    for (const NodeRef& w : ws) same_n = same_n && w->shape[1] == ws[0]->shape[1];
+    std::shared_ptr<SharedLhs> group;
+    if (same_n && ws.size() >= 2 && ws.size() <= 3) {
+        group = std::make_shared<SharedLhs>(SharedLhs{x, ws, {}, m, k, ws[0]->shape[1]});
+        for (const NodeRef& node : nodes) group->outs.push_back(node);
+    }
     for (size_t i = 0; i < ws.size(); ++i) {
         const size_t n = ws[i]->shape[1];
-        NodeRef node = make_output({m, n}, {x, ws[i]}, std::move(outs[i]));
-        set_matmul_backward(node, x, ws[i], m, k, n);
-        nodes.push_back(std::move(node));
+        const NodeRef& w = ws[i];
+        nodes[i]->backward_fn = [grad = nodes[i]->gpu->grad, group, x, w, m, k,
+                                 n](const std::vector<float>&) {
+            if (group && fused_shared_lhs_backward(*group)) return;
+            matmul_backward_into(x, w, grad->ptr(), m, k, n, "cuda matmul bwd: launch failed");
+        };
     }
     return nodes;
 }

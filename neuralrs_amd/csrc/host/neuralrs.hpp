@@ -160,6 +160,11 @@ void set_grad(const NodeRef& node, const std::vector<float>& grad);
 // length), no copy. Backward closures hold the node's gradient object, so
 // they read what was swapped in; swapping back returns the buffer.
 void swap_grad(const NodeRef& node, DeviceBuffer& buf);
+// Whether backward_graph runs a closure together with its neighbours' where
+// that saves launches (a conv over a ReLU + max-pool node, the Q, K and V
+// projections' three matmul closures): the same results either way. On by
+// default; off runs every closure on its own.
+void set_fused_backward(bool on);
 // src/cuda/runtime.rs:96-103.
 std::vector<float> read_grad(const NodeRef& node);
 // src/cuda/runtime.rs:108-117.

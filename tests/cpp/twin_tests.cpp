@@ -1245,6 +1245,49 @@ void cuda_conv2d_maxpool_node() {
     }
 }
 
+// The Q, K and V projections' three matmul closures run as one
+// nrs_matmul_shared_lhs_backward call (fused) give the bits of the closures
+// run one by one (set_fused_backward(false)): the block's input gradient and
+// all four weight gradients, at cfg4's shape (one grouped launch) and at a
+// small shape (the short-GEMM kernel: the call runs the closures' sequence).
+// The fused pass is also checked against the oracle's composition by
+// cfg4_transformer_block.
+void mha_fused_projection_backward_exact() {
+    reseed(55);
+    const size_t shapes[2][4] = {{32, 128, 256, 8}, {2, 12, 32, 4}};  // batch, seq, d, heads
+    for (const auto& sh : shapes) {
+        const size_t B = sh[0], S = sh[1], D = sh[2], Hh = sh[3], n = B * S * D;
+        const Vec x = normal(n, 1.0f), seed = normal(n, 0.1f);
+        Vec wv[4];
+        for (Vec& w : wv) w = normal(D * D, 1.0f / std::sqrt((float)D));
+        Vec ref[5];
+        for (int fused = 1; fused >= 0; --fused) {
+            gpu::set_fused_backward(fused != 0);
+            NodeRef gx = resident(x, {B, S, D});
+            NodeRef w[4];
+            for (int i = 0; i < 4; ++i) w[i] = resident(wv[i], {D, D});
+            const hip::nn::MultiHeadAttention mha(w[0], w[1], w[2], w[3], D, Hh);
+            NodeRef out = mha.forward_batch(gx);
+            gpu::set_grad(out, seed);
+            backward_graph(out);
+            const Vec got[5] = {gpu::read_grad(gx), gpu::read_grad(w[0]), gpu::read_grad(w[1]),
+                                gpu::read_grad(w[2]), gpu::read_grad(w[3])};
+            const char* names[5] = {"x.grad", "w_q.grad", "w_k.grad", "w_v.grad", "w_o.grad"};
+            for (int i = 0; i < 5; ++i) {
+                if (fused) {
+                    ref[i] = got[i];
+                } else if (ref[i].size() != got[i].size() ||
+                           std::memcmp(ref[i].data(), got[i].data(), got[i].size() * sizeof(float))) {
+                    gpu::set_fused_backward(true);
+                    throw Failure(std::string("fused vs one by one (d ") + std::to_string(D) +
+                                  "): " + names[i] + " bits differ");
+                }
+            }
+        }
+        gpu::set_fused_backward(true);
+    }
+}
+
 const Case kCases[] = {
     {"cuda_resident_matmul_backward", cuda_resident_matmul_backward},
     {"cuda_resident_linear_chain", cuda_resident_linear_chain},
@@ -1281,6 +1324,7 @@ const Case kCases[] = {
     {"cuda_conv2d_maxpool_node", cuda_conv2d_maxpool_node},
     {"swap_grad_seed", swap_grad_seed},
     {"cfg3_fused_backward_exact", cfg3_fused_backward_exact},
+    {"mha_fused_projection_backward_exact", mha_fused_projection_backward_exact},
 };
 
 int main(int argc, char** argv) {

@@ -326,6 +326,67 @@ def test_linear_backward_optional_outputs_and_empty(hip):
         hip.call("nrs_linear_backward", None, None, ddb0, D(g), D(x), D(w), 64, 48, 32, 0.0, 0.0, 0.0)
 
 
+# (rows, inner, cols, count): cfg4's Q, K and V projections (one grouped
+# launch and the sums), input-gradient products split over K (few tiles, long
+# K), products small enough for the short-GEMM kernel (the closures run in
+# turn), two products, and one
+SHARED_LHS_SHAPES = [(4096, 256, 256, 3), (128, 64, 4096, 3), (64, 32, 48, 3),
+                     (1024, 128, 512, 2), (4096, 256, 256, 1)]
+
+
+@pytest.mark.parametrize("rows,inner,cols,count", SHARED_LHS_SHAPES)
+@pytest.mark.parametrize("beta_x", [0.0, 1.0])
+def test_matmul_shared_lhs_backward_matches_closures(hip, rows, inner, cols, count, beta_x):
+    """nrs_matmul_shared_lhs_backward gives the bits of the matmul closures
+    run in turn (src/cuda/graph/matmul.rs:418-431), each an nrs_gemm_group of
+    dx (+)= g_i . W_i^T and dW_i = x^T . g_i + beta_w[i] * dW_i, and the f64
+    result within the GEMM bar (U(-1, 1) data)."""
+    rng = np.random.default_rng(rows + inner + cols + count)
+    U = lambda s: rng.uniform(-1, 1, s).astype(np.float32)
+    x = U((rows, inner))
+    ws = [U((inner, cols)) for _ in range(count)]
+    gs = [U((rows, cols)) for _ in range(count)]
+    dx0, dw0 = U((rows, inner)), [U((inner, cols)) for _ in range(count)]
+    beta_w = [1.0, 0.0, 1.0][:count]
+    D = hip.DeviceBuffer.from_host
+    xd, wd, gd = D(x), [D(w) for w in ws], [D(g) for g in gs]
+    dx_a, dw_a = D(dx0), [D(w) for w in dw0]
+    dx_b, dw_b = D(dx0), [D(w) for w in dw0]
+    hip.matmul_shared_lhs_backward(dx_a, dw_a, gd, xd, wd, rows, inner, cols, beta_x, beta_w)
+    for i in range(count):
+        hip.gemm_group([(NT, dx_b, gd[i], wd[i], rows, inner, cols, beta_x if i == 0 else 1.0),
+                        (TN, dw_b[i], xd, gd[i], inner, cols, rows, beta_w[i])])
+    bits = lambda buf, shape: buf.to_host(shape).view(np.uint32)
+    assert np.array_equal(bits(dx_a, (rows, inner)), bits(dx_b, (rows, inner)))
+    for a, b in zip(dw_a, dw_b):
+        assert np.array_equal(bits(a, (inner, cols)), bits(b, (inner, cols)))
+    f = lambda a: a.astype(np.float64)
+    want_x = beta_x * f(dx0) + sum(f(g) @ f(w).T for g, w in zip(gs, ws))
+    ab_x = abs(beta_x) * np.abs(f(dx0)) + sum(np.abs(f(g)) @ np.abs(f(w)).T for g, w in zip(gs, ws))
+    assert rel_err(dx_a.to_host((rows, inner)), want_x, ab_x) <= gemm_tol(count * cols + 1)
+    for i in range(count):
+        want = f(x).T @ f(gs[i]) + beta_w[i] * f(dw0[i])
+        ab = np.abs(f(x)).T @ np.abs(f(gs[i])) + abs(beta_w[i]) * np.abs(f(dw0[i]))
+        assert rel_err(dw_a[i].to_host((inner, cols)), want, ab) <= gemm_tol(rows + 1)
+
+
+def test_matmul_shared_lhs_backward_shared_weight_runs_closures(hip):
+    """One weight used by two products (W_0 = W_1, so dW_0 = dW_1): the
+    weight-gradient outputs overlap, so the closures run in turn, the second
+    adding to the first one's dW."""
+    rng = np.random.default_rng(9)
+    rows, inner, cols = 1024, 128, 128
+    x, dx0 = int_matrix(rng, (rows, inner), -3, 3), int_matrix(rng, (rows, inner), -3, 3)
+    w = int_matrix(rng, (inner, cols), -3, 3)
+    g0, g1 = int_matrix(rng, (rows, cols), -3, 3), int_matrix(rng, (rows, cols), -3, 3)
+    D = hip.DeviceBuffer.from_host
+    dx, dw, wd = D(dx0), hip.DeviceBuffer.zeros(inner * cols), D(w)
+    hip.matmul_shared_lhs_backward(dx, [dw, dw], [D(g0), D(g1)], D(x), [wd, wd], rows, inner,
+                                   cols, 1.0, [0.0, 1.0])
+    assert np.array_equal(dw.to_host((inner, cols)), x.T @ g0 + x.T @ g1)
+    assert np.array_equal(dx.to_host((rows, inner)), dx0 + g0 @ w.T + g1 @ w.T)
+
+
 def test_gemm_group_errors(hip):
     dC = hip.DeviceBuffer(4)
     with pytest.raises(hip.NrsError):  # more calls than a group holds
