@@ -396,6 +396,18 @@ def test_gemm_group_errors(hip):
     hip.gemm_group([])  # nothing to do
 
 
+def test_matmul_shared_lhs_backward_errors(hip):
+    import ctypes
+    d = hip.DeviceBuffer(64)
+    arr = (ctypes.c_void_p * 3)(d.ptr, d.ptr, d.ptr)
+    betas = (ctypes.c_float * 3)()
+    with pytest.raises(hip.NrsError):  # more than three products
+        hip.call("nrs_matmul_shared_lhs_backward", d, arr, arr, d, arr, 4, 8, 8, 8, 0.0, betas)
+    with pytest.raises(hip.NrsError):  # a null weight gradient: nothing launches
+        hip.matmul_shared_lhs_backward(d, [None, d], [d, d], d, [d, d], 8, 8, 8)
+    hip.matmul_shared_lhs_backward(d, [d], [d], d, [d], 0, 8, 8)  # no rows: nothing to do
+
+
 # ------------------------------------------------------------------ split-K
 @pytest.mark.parametrize("shape", [(32, 9, 100352), (64, 288, 25088), (5, 7, 3000), (3, 2, 1)],
                          ids=lambda s: "x".join(map(str, s)))
