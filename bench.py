@@ -447,8 +447,10 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
 
     # the block's Linear GEMMs: X[4096,256] through 4 projections and the FFN,
     # launched as the operator surface launches them: the Q, K, V projections
-    # of one input as one grouped launch, each layer's input and weight
-    # gradients (dX = dY.W^T, dW = X^T.dY) as one grouped launch
+    # of one input as one grouped launch and their backward as one pass
+    # (nrs_matmul_shared_lhs_backward: six products in one grouped launch and
+    # the sums), each other layer's input and weight gradients (dX = dY.W^T,
+    # dW = X^T.dY) as one grouped launch
     R, dm, ff = 32 * 128, 256, 1024
     X = D(rng.standard_normal(R * dm).astype(np.float32))
     H = D(rng.standard_normal(R * ff).astype(np.float32))
@@ -468,9 +470,9 @@ def bench_attention_cfg4(hip, steps, warmup, closures_only=False):
         hip.gemm(hip.NN, Yp[3], X, Wp[3], R, dm, dm)                              # output proj
         hip.gemm(hip.NN, Yf, X, W1, R, ff, dm)
         hip.gemm(hip.NN, Yd, H, W2, R, dm, ff)
-        for i in range(4):
-            hip.gemm_group([(hip.NT, gXd, Yp[i], Wp[i], R, dm, dm),
-                            (hip.TN, gWp[i], X, Yp[i], dm, dm, R)])
+        hip.matmul_shared_lhs_backward(gXd, gWp[:3], Yp[:3], X, Wp[:3], R, dm, dm)
+        hip.gemm_group([(hip.NT, gXd, Yp[3], Wp[3], R, dm, dm),
+                        (hip.TN, gWp[3], X, Yp[3], dm, dm, R)])
         hip.gemm_group([(hip.NT, gXd, Yf, W1, R, dm, ff), (hip.TN, gW1, X, Yf, dm, ff, R)])
         hip.gemm_group([(hip.NT, gXf, Yd, W2, R, ff, dm), (hip.TN, gW2, H, Yd, ff, dm, R)])
 
